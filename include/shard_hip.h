@@ -1,0 +1,224 @@
+/*
+ * shard_hip.h — C ABI of libshard_hip.so, the MI355X (gfx950) kernels of the
+ * compressed-KV attention path.
+ *
+ * Conventions (every entry point):
+ *   - plain device pointers (HBM), element counts and strides; no torch types;
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream); all work
+ *     is enqueued on it, nothing synchronizes the host;
+ *   - fp16 tensors are passed as uint16_t* (IEEE binary16 bit patterns);
+ *   - return 0 on success, a negative SHARD_ERR_* code otherwise; nothing is
+ *     allocated inside: scratch memory comes in through `workspace`, sized by
+ *     the matching *_workspace() query;
+ *   - entry points are stateless and re-entrant (no mutable globals).
+ *
+ * Each declaration names the reference code (bhengubv/shard, src/shard/...)
+ * whose role it takes over.
+ */
+#ifndef SHARD_HIP_H
+#define SHARD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SHARD_OK 0
+#define SHARD_ERR_ARG (-1)       /* null pointer, negative or zero size */
+#define SHARD_ERR_SHAPE (-2)     /* shape the kernels do not support */
+#define SHARD_ERR_HIP (-3)       /* a HIP launch or runtime call failed */
+#define SHARD_ERR_WORKSPACE (-4) /* workspace missing or too small */
+
+/* Library version string, e.g. "shard_hip 0.1.0 gfx950". */
+const char* shard_version(void);
+
+/* Human-readable text of the last HIP error seen on this thread ("" if none). */
+const char* shard_last_error(void);
+
+/* sizeof(shard_decode_args) as compiled into the library (ABI check for bindings). */
+size_t shard_decode_args_size(void);
+
+/* ------------------------------------------------------------------------
+ * Prefill compression: keys
+ * ------------------------------------------------------------------------ */
+
+/* PCA projection GEMM on MFMA: C[m, n] (fp32) = A[m, k] (fp16) . Bt[n, k]^T (fp16).
+ * A row-major with row stride lda (elements), Bt row-major (n rows of k),
+ * C row-major with row stride ldc.  k % 16 == 0, n % 32 == 0, n <= 256.
+ * Replaces the projection GEMM of _compress_k, cache.py:392
+ * ((flat - mean) @ (basis_q * scale)). */
+int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_t lda,
+                      const uint16_t* bt, int32_t n, float* c, int64_t ldc,
+                      void* stream);
+
+/* Prefill K preparation fused with the projection input: reads post-RoPE keys
+ * k (B, n_kv, T, hd) fp16, undoes RoPE at positions start+t with fp32 phases
+ * fl(pos * inv_freq[i]) (rope.py:13-24), subtracts mean[n_kv*hd] (fp32) and
+ * writes the fp16 row-major matrix out[(b*n_comp + t), n_kv*hd] for tokens
+ * t in [0, n_comp).  Replaces undo_rope + permute/reshape + (flat - mean) of
+ * cache.py:370-376 (as the fp16 GEMM operand). */
+int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
+                    int32_t hd, int32_t start, int32_t n_comp,
+                    const float* inv_freq, const float* mean, uint16_t* out,
+                    void* stream);
+
+/* Integer chain of the key coefficients, bit-exact with the reference:
+ *   per column c with bits[c] > 0: lo = min, rng = max(max - lo, 1e-6),
+ *     code = clamp(rint(clamp((x - lo) / rng, 0, 1) * L), 0, L), L = 2^bits - 1,
+ *     y = code / L * rng + lo;  columns with bits[c] == 0 give y = 0
+ *     (quantize_group / dequantize_group values, rope.py:95-161);
+ *   cs = max(max |y|, 1e-6) / 7;  q = clamp(rint(y / cs), -7, 7)
+ *     (cache.py:416-419);
+ *   packed[i] = ((q[2i] + 8) & 15) | ((q[2i+1] + 8) & 15) << 4 over the
+ *     row-major (n_rows, keep) matrix, zero-padded if odd
+ *     (int4_pack, triton_kernels.py:648-682).
+ * proj: (n_rows, keep) fp32 row-major.  Outputs: packed ((n_rows*keep+1)/2),
+ * coeff_scale (keep, fp32), lo/rng (keep, fp32, nullable), codes
+ * ((n_rows, keep) uint8 group codes, nullable). */
+size_t shard_int4_quant_pack_workspace(int64_t n_rows, int32_t keep);
+int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep,
+                          const int32_t* bits, uint8_t* packed, float* coeff_scale,
+                          float* lo, float* rng, uint8_t* codes,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Prefill compression: values
+ * ------------------------------------------------------------------------ */
+
+/* Normalized fast Walsh-Hadamard transform over the last dim d (power of two,
+ * 2..1024) of `rows` fp32 rows; bit-exact with hadamard(), cache.py:10-19
+ * (butterflies h = 1, 2, 4, ... then one IEEE division by fp32(sqrt(d))).
+ * y may alias x. */
+int shard_fwht(const float* x, float* y, int64_t rows, int32_t d, void* stream);
+
+/* V encoder front half (vq_encode, cache.py:41-46 after hadamard, cache.py:402):
+ * v fp16 (bh, seq, hd) -> v_rot = hadamard(fp32(v)); ch = max(max_t |v_rot|, 1e-8)
+ * per (bh, channel); x = v_rot / ch written as fp32 (bh*seq*hd/g, g) subvectors;
+ * ch also written as fp16 (bh, hd).  Uses workspace for the fp32 channel max. */
+size_t shard_vq_prepare_workspace(int64_t bh, int32_t hd);
+int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
+                     int64_t v_bh_stride, float* x_out, float* ch_f32,
+                     uint16_t* ch_f16, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Nearest-centroid assignment: idx[i] = argmin_k sum_j (x[i,j] - c[k,j])^2 with
+ * the squared differences summed in fp32 in j order without FMA, first index
+ * on ties.  d <= 8, k <= 1024.  Replaces vq_assign, triton_kernels.py:689-746
+ * (whose CPU fallback is cdist(...).argmin, triton_kernels.py:733-734). */
+int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids,
+                    int32_t k, int32_t* idx, void* stream);
+
+/* One k-means update (cache.py:28-38) given assignments idx: new_c[k] = mean of
+ * the rows assigned to k (empty clusters keep c[k]); also writes
+ * max |new_c - c| to *max_delta (device fp32).  Sums are accumulated per
+ * centroid in increasing row order, so the result is deterministic.
+ * workspace: shard_kmeans_update_workspace(n, k) bytes. */
+size_t shard_kmeans_update_workspace(int64_t n, int32_t k);
+int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx,
+                        const float* centroids, int32_t k, float* new_centroids,
+                        float* max_delta, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decode stream (8-bit Lloyd-Max, per token)
+ * ------------------------------------------------------------------------ */
+
+/* Per-token quantizer, bit-exact with _stream_append's _unit (cache.py:207-213)
+ * + quantize_per_token (streaming.py:59-72, qjl off):
+ *   t = fp32(x); n = max(||t||, 1e-8) with torch-CPU's 8-lane summation order;
+ *   r = hadamard(t / n * signs); idx = bucketize(r, codebook) clamped, then the
+ *   nearer of (idx-1, idx) by |cb - r| in fp32 (ties to idx); norm = fp16(n).
+ * x: (rows, hd) fp16 contiguous, hd in {64, 128, 256}; codebook sorted, n_codes <= 256. */
+int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd,
+                       const float* signs, const float* codebook, int32_t n_codes,
+                       uint8_t* idx, uint16_t* norm, void* stream);
+
+/* Stream dequantizer, bit-exact with _dequant_stream / dequantize_per_token
+ * (cache.py:275-278, streaming.py:74-79, qjl off):
+ *   y = fp16(fp16(hadamard(codebook[idx]) * signs) * norm)
+ * idx (rows, hd) uint8, norm (rows) fp16 -> y (rows, hd) fp16; hd = 128. */
+int shard_stream_dequant(const uint8_t* idx, const uint16_t* norm, int64_t rows, int32_t hd,
+                         const float* signs, const float* codebook, uint16_t* y,
+                         void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused decode attention over the compressed cache
+ * ------------------------------------------------------------------------ */
+
+/* Arguments of one decode-attention call (one layer, one query token per row).
+ * Layouts (B = batch, H = n_q_heads, G = n_kv_heads, D = head_dim = 128):
+ *   q            (B, H, D) fp16, post-RoPE at position pos_q
+ *   inv_freq     (D/2) fp32
+ *   k_coeffs     (B*n_comp, rank/2) packed int4 (row-major, low nibble first)
+ *   k_coeff_scale (rank) fp16;  k_basis (G*D, rank) fp16;  k_mean (G*D) fp16
+ *   v_idx        (B, G, n_comp, D/4) uint8;  v_codebook (256, 4) fp16
+ *   v_ch         (B, G, D) fp16
+ *   sink_k/v     (B, G, n_sink, D) fp16;  win_k/v (B, G, n_win, D) fp16
+ *   dec_k/v      (B, G, dec_stride, D) fp16, first n_dec tokens valid
+ *   s_kidx/s_vidx (>= n_stream, B, G, D) uint8; s_knorm/s_vnorm (>= n_stream, B, G) fp16
+ *   s_signs      (D) fp32;  s_codebook (256) fp32
+ *   mask         additive fp32, row b at mask + b*mask_stride, indexed in the
+ *                reference's concatenation order [sink, comp, win, dec, stream]
+ *                (nullable)
+ *   out          (B, H, D) fp16
+ * rank must be a multiple of 32 (<= 192); pad coefficients and basis with
+ * zeros otherwise.  The softmax and all sums run in fp32.
+ * Replaces fused_attention_compressed (attention.py:270-343) with its
+ * compressed_scores (18-81) and _v_weighted_sum_compressed (83-121), and the
+ * flash-mixing of fused_attention_compressed_full (183-267). */
+typedef struct shard_decode_args {
+  int32_t batch, n_q_heads, n_kv_heads, head_dim;
+  int32_t rank, n_comp, compress_start, pos_q;
+  const uint16_t* q;
+  const float* inv_freq;
+  const uint8_t* k_coeffs;
+  const uint16_t* k_coeff_scale;
+  const uint16_t* k_basis;
+  const uint16_t* k_mean;
+  const uint8_t* v_idx;
+  const uint16_t* v_codebook;
+  const uint16_t* v_ch;
+  const uint16_t* sink_k;
+  const uint16_t* sink_v;
+  int32_t n_sink;
+  const uint16_t* win_k;
+  const uint16_t* win_v;
+  int32_t n_win;
+  const uint16_t* dec_k;
+  const uint16_t* dec_v;
+  int32_t n_dec, dec_stride;
+  const uint8_t* s_kidx;
+  const uint8_t* s_vidx;
+  const uint16_t* s_knorm;
+  const uint16_t* s_vnorm;
+  const float* s_signs;
+  const float* s_codebook;
+  int32_t n_stream, _pad0;
+  const float* mask;
+  int64_t mask_stride;
+  uint16_t* out;
+  int32_t n_splits; /* 0 = choose automatically */
+  int32_t _pad1;
+} shard_decode_args;
+
+size_t shard_decode_attn_workspace(const shard_decode_args* args);
+int shard_decode_attn(const shard_decode_args* args, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Full fp16 reconstruction of the compressed segment for unfused consumers,
+ * _ensure_dequant (cache.py:87-124), using the compressed-segment fields of
+ * `args` (q, out and the fp16 segments are ignored):
+ *   K: fp16(fp16(sum_r fp16(nib*cs) * basis) + mean), then RoPE re-applied at
+ *      positions compress_start + t with fp32 phases fl(pos*theta), fp16 out;
+ *   V: fp16(hadamard(cb[idx] * ch)) (hadamard in fp32, bit-exact).
+ * k_out / v_out: (B, G, n_comp, D) fp16 contiguous. */
+int shard_kv_reconstruct(const shard_decode_args* args, uint16_t* k_out,
+                         uint16_t* v_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHARD_HIP_H */

@@ -1,0 +1,5 @@
+"""Drop-in import name of the reference package: ``from shard import Cache, ...``
+resolves to the MI355X implementation in shard_amd."""
+from shard_amd import Cache, enable_llama_fused_attention, fused_attention_compressed
+
+__all__ = ["Cache", "enable_llama_fused_attention", "fused_attention_compressed"]

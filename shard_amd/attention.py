@@ -1,0 +1,138 @@
+"""Fused compressed-KV decode attention and the Llama integration.
+
+fused_attention_compressed (attention.py:270-343 of the reference) computes
+softmax(q.K^T/sqrt(d)).V over [sink, compressed, window, decode, stream]
+without materializing the compressed K or V: one HIP split kernel rebuilds
+no-RoPE keys on chip from int4 PCA coefficients, scores them with the
+relative-delta RoPE identity
+
+    pair_i(D) = (a_i c_i + b_i d_i) cos(theta_i D) + (b_i c_i - a_i d_i) sin(theta_i D)
+
+(q_n = [a, b] = undo-RoPE(q, pos_q), k_n = [c, d], D = pos_t - pos_q), and
+accumulates the VQ values in Hadamard-rotated space; a combine kernel merges
+the splits with the fp16 segments and the 8-bit stream and applies one
+inverse Hadamard.
+"""
+import torch
+
+from . import ops
+
+_workspaces = {}
+
+
+def _workspace(device, nbytes):
+    key = (device.type, device.index)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
+    """q_rope (B, n_q, 1, hd) post-RoPE; returns (B, n_q, 1, hd) in q's dtype,
+    or None when the layer is not compressed (attention.py:270-274)."""
+    gc = getattr(layer, "_gpu_compressed", None)
+    if gc is None:
+        return None
+    B, n_q, s, hd = q_rope.shape
+    if s != 1:
+        return None
+    q = q_rope.reshape(B, n_q, hd)
+    if q.dtype != torch.float16:
+        q = q.to(torch.float16)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    c = layer._cache_ref
+    inv = gc["inv_freq_dev"]
+    if inv_freq is not None and inv_freq is not getattr(c, "_rope_inv_freq", None):
+        inv = inv_freq.to(q.device, torch.float32).contiguous()
+    stream_n = gc.get("stream_n", 0) // B if gc.get("stream_n", 0) else 0
+    dec = (gc["decode_k"], gc["decode_v"]) if "decode_k" in gc else None
+    mask = None
+    if attn_mask is not None:
+        mask = attn_mask.reshape(B, -1)[:, -(gc["sink_k"].shape[2] + gc["n_compress"] +
+                                          gc["win_k"].shape[2] + stream_n +
+                                          (dec[0].shape[2] if dec else 0)):]
+    call = ops.make_decode_args(q, gc, pos_q, inv, mask=mask,
+                                n_splits=getattr(c, "_n_splits", 0),
+                                stream_n=stream_n, decode_kv=dec)
+    ws = _workspace(q.device, ops.decode_workspace_bytes(call))
+    out = ops.decode_attn(call, ws)
+    return out.view(B, n_q, 1, hd).to(q_rope.dtype)
+
+
+def fused_attention_compressed_full(q_rope, layer, pos_q, inv_freq, attn_mask=None):
+    """The reference's opt-in single-pass variant (attention.py:183-267).  The HIP
+    kernel is already single-pass over every segment, so both entry points run it."""
+    return fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask)
+
+
+def enable_llama_fused_attention(model=None):
+    """Patch LlamaAttention.forward process-wide so decode steps (q_len == 1) on a
+    compressed shard Cache layer go through the fused HIP kernel; everything else
+    calls the original forward (attention.py:345-414).  Returns False when the
+    transformers Llama module is unavailable."""
+    from .cache import Cache
+    try:
+        from transformers.models.llama.modeling_llama import LlamaAttention, apply_rotary_pos_emb
+    except ImportError:
+        return False
+    if getattr(LlamaAttention.forward, "_shard_amd_patched", False):
+        return True
+    original = LlamaAttention.forward
+
+    def forward(self, hidden_states, position_embeddings=None, attention_mask=None,
+                past_key_values=None, cache_position=None, **kwargs):
+        is_shard = isinstance(past_key_values, Cache)
+        layer = past_key_values.layers[self.layer_idx] if is_shard else None
+        fuse = (is_shard and layer is not None
+                and getattr(layer, "_gpu_compressed", None) is not None
+                and hidden_states.shape[1] == 1
+                and past_key_values._rope_inv_freq is not None)
+        if not fuse:
+            if cache_position is not None:
+                kwargs["cache_position"] = cache_position
+            return original(self, hidden_states, position_embeddings, attention_mask,
+                            past_key_values, **kwargs)
+        input_shape = hidden_states.shape[:-1]
+        hidden_shape = (*input_shape, -1, self.head_dim)
+        q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        past_key_values._fused_decode_update = True
+        try:
+            past_key_values.update(k, v, self.layer_idx,
+                                   {"sin": sin, "cos": cos, "cache_position": cache_position})
+        finally:
+            past_key_values._fused_decode_update = False
+        pos_q = int(cache_position[-1].item()) if cache_position is not None \
+            else past_key_values.get_seq_length() - 1
+        out = None
+        if getattr(past_key_values, "_full_fused", False):
+            past_key_values._full_fused_attempts = getattr(past_key_values, "_full_fused_attempts", 0) + 1
+            try:
+                out = fused_attention_compressed_full(q, layer, pos_q, past_key_values._rope_inv_freq,
+                                                      attention_mask)
+                if out is not None:
+                    past_key_values._full_fused_hits = getattr(past_key_values, "_full_fused_hits", 0) + 1
+            except Exception as exc:  # counted, then the default fused path runs
+                past_key_values._full_fused_errors = getattr(past_key_values, "_full_fused_errors", 0) + 1
+                past_key_values._last_full_fused_error = repr(exc)
+                out = None
+        if out is None:
+            out = fused_attention_compressed(q, layer, pos_q, past_key_values._rope_inv_freq,
+                                             attention_mask)
+        if out is None:
+            if cache_position is not None:
+                kwargs["cache_position"] = cache_position
+            return original(self, hidden_states, position_embeddings, attention_mask,
+                            past_key_values, **kwargs)
+        out = out.transpose(1, 2).contiguous().view(*input_shape, -1)
+        return self.o_proj(out), None
+
+    forward._shard_amd_patched = True
+    LlamaAttention.forward = forward
+    return True

@@ -1,0 +1,492 @@
+"""shard.Cache on MI355X: a transformers Cache whose layers compress their KV.
+
+API and state machine follow the reference's cache.py (Cache: 295-539,
+CacheLayer: 64-292):
+  prefill (q_len > 1)     fp16 K/V kept as-is (cache.py:142-147)
+  first decode step       Cache.compress() of every layer (cache.py:149-151, 338-460):
+                          K -> undo RoPE -> PCA (svd_lowrank) -> DP bits -> int8
+                          basis -> projection (MFMA) -> group quant -> int4 (HIP);
+                          V -> Hadamard -> k-means VQ (HIP assign + update);
+                          sink (4) and window (64) tokens stay fp16.
+  decode tokens           8-bit Lloyd-Max stream (_streaming=True, HIP quantizer)
+                          or fp16 decode_k/decode_v (cache.py:156-181)
+  fused decode attention  attention.fused_attention_compressed (HIP kernel)
+  unfused consumers       layer.keys / layer.values rebuild fp16 K/V on the GPU
+                          (_ensure_dequant, cache.py:87-124; HIP reconstruct)
+All device work runs in HIP kernels of libshard_hip.so; CPU tensors are rejected.
+"""
+import torch
+from transformers.cache_utils import Cache as HFCache, CacheLayerMixin
+
+from . import host, ops
+
+
+def _nb(t):
+    return t.nelement() * t.element_size()
+
+
+class CacheLayer(CacheLayerMixin):
+    """One layer's cache (cache.py:64-292)."""
+
+    is_sliding = False
+    is_compileable = False
+
+    def __init__(self, layer_idx):
+        self.layer_idx = layer_idx
+        self._keys = None
+        self._values = None
+        self._prefilled = False
+        self._seq_len = 0
+        self._cache_ref = None
+        self._needs_decompress = False
+        self._gpu_compressed = None
+        self.is_initialized = False
+
+    # -- lazy per-layer materialization (cache.py:74-136) -------------------
+    def _lazy_evict(self):
+        c = self._cache_ref
+        if c is None or not c._lazy_per_layer:
+            return
+        last = c._last_accessed_layer
+        if last != -1 and last != self.layer_idx:
+            prev = c.layers[last]
+            if getattr(prev, "_gpu_compressed", None) is not None:
+                prev._keys = None
+                prev._values = None
+                prev._needs_decompress = True
+        c._last_accessed_layer = self.layer_idx
+
+    def _ensure_dequant(self):
+        if not self._needs_decompress:
+            return
+        gc = self._gpu_compressed
+        if gc is None:
+            return
+        B = gc["batch"]
+        k_mid, v_mid = ops.kv_reconstruct(gc, B)
+        parts_k = [gc["sink_k"], k_mid, gc["win_k"]]
+        parts_v = [gc["sink_v"], v_mid, gc["win_v"]]
+        sk, sv = self._dequant_stream(gc, B)
+        if sk is not None:
+            parts_k.append(sk)
+            parts_v.append(sv)
+        if "decode_k" in gc:
+            parts_k.append(gc["decode_k"])
+            parts_v.append(gc["decode_v"])
+        self._keys = torch.cat(parts_k, dim=2)
+        self._values = torch.cat(parts_v, dim=2)
+        self._needs_decompress = False
+
+    @property
+    def keys(self):
+        self._lazy_evict()
+        self._ensure_dequant()
+        return self._keys
+
+    @keys.setter
+    def keys(self, v):
+        self._keys = v
+
+    @property
+    def values(self):
+        self._lazy_evict()
+        self._ensure_dequant()
+        return self._values
+
+    @values.setter
+    def values(self, v):
+        self._values = v
+
+    # -- update (cache.py:138-191) -----------------------------------------
+    def update(self, key_states, value_states, *args, **kwargs):
+        seq_new = key_states.shape[2]
+        c = self._cache_ref
+        self.is_initialized = True
+        if seq_new > 1 and not self._prefilled:
+            self._prefilled = True
+            self._seq_len = seq_new
+            self._keys = key_states
+            self._values = value_states
+            return key_states, value_states
+
+        if self.layer_idx == 0 and c is not None and not c._compressed:
+            c.compress()
+
+        self._lazy_evict()
+        gc = self._gpu_compressed
+
+        if gc is not None and c._streaming:
+            for t in range(seq_new):
+                self._stream_append(key_states[:, :, t:t + 1, :], value_states[:, :, t:t + 1, :])
+            self._seq_len += seq_new
+            self._needs_decompress = True
+            if getattr(c, "_fused_decode_update", False):
+                return key_states, value_states
+            self._ensure_dequant()
+            return self._keys, self._values
+
+        if gc is not None:
+            if "decode_k" in gc:
+                gc["decode_k"] = torch.cat([gc["decode_k"], key_states], dim=2)
+                gc["decode_v"] = torch.cat([gc["decode_v"], value_states], dim=2)
+            else:
+                gc["decode_k"] = key_states.contiguous()
+                gc["decode_v"] = value_states.contiguous()
+            self._seq_len += seq_new
+            self._needs_decompress = True
+            if getattr(c, "_fused_decode_update", False):
+                return key_states, value_states
+            self._ensure_dequant()
+            return self._keys, self._values
+
+        self._ensure_dequant()
+        self._seq_len += seq_new
+        if self._keys is not None:
+            self._keys = torch.cat([self._keys, key_states], dim=2)
+            self._values = torch.cat([self._values, value_states], dim=2)
+        else:
+            self._keys = key_states
+            self._values = value_states
+        return self._keys, self._values
+
+    # -- decode stream (cache.py:193-279) ----------------------------------
+    def _stream_append(self, k, v):
+        """Quantize one decode token (B, G, 1, D) of K and V into the 8-bit
+        stream buffers (growable, doubling, as cache.py:220-230)."""
+        gc = self._gpu_compressed
+        c = self._cache_ref
+        if c._stream_bits != 8 or c._stream_qjl:
+            raise NotImplementedError("the HIP stream quantizer implements 8-bit codes without QJL")
+        B, G, _, D = k.shape
+        dev = k.device
+        if "signs" not in gc:
+            gc["signs"] = host.stream_signs(self.layer_idx, D).to(dev)
+            gc["stream_codebook"] = host.lloyd_max_codebook(D, 8).to(dev)
+        s = gc.get("stream_n", 0) // B
+        needed = s + 1
+
+        def _ensure(key, shape, dtype):
+            buf_key = f"{key}_buf"
+            buf = gc.get(buf_key)
+            if buf is not None and buf.shape[0] >= needed:
+                return buf
+            cap = max(needed, 16 if buf is None else buf.shape[0] * 2)
+            new = torch.empty((cap, *shape), device=dev, dtype=dtype)
+            if buf is not None:
+                new[:buf.shape[0]].copy_(buf)
+            gc[buf_key] = new
+            return new
+
+        kib = _ensure("k_idx", (B, G, D), torch.uint8)
+        vib = _ensure("v_idx", (B, G, D), torch.uint8)
+        knb = _ensure("k_norm", (B, G), torch.float16)
+        vnb = _ensure("v_norm", (B, G), torch.float16)
+        kx = k.reshape(B, G, D)
+        vx = v.reshape(B, G, D)
+        if not kx.is_contiguous():
+            kx = kx.contiguous()
+        if not vx.is_contiguous():
+            vx = vx.contiguous()
+        ops.stream_quant_into(kx, gc["signs"], gc["stream_codebook"], kib[s], knb[s])
+        ops.stream_quant_into(vx, gc["signs"], gc["stream_codebook"], vib[s], vnb[s])
+        gc["stream_n"] = gc.get("stream_n", 0) + B
+
+    def _dequant_stream(self, gc, B, nkv=None, hd=None):
+        n = gc.get("stream_n", 0)
+        if n == 0 or "k_idx_buf" not in gc:
+            return None, None
+        s = n // B
+        sk = ops.stream_dequant(gc["k_idx_buf"][:s], gc["k_norm_buf"][:s], gc["signs"],
+                                gc["stream_codebook"])
+        sv = ops.stream_dequant(gc["v_idx_buf"][:s], gc["v_norm_buf"][:s], gc["signs"],
+                                gc["stream_codebook"])
+        return sk.permute(1, 2, 0, 3).contiguous(), sv.permute(1, 2, 0, 3).contiguous()
+
+    # -- HF Cache API glue (cache.py:281-292; TF 5.x additions) ----------------
+    def get_seq_length(self):
+        return self._seq_len
+
+    def get_max_length(self):
+        return -1
+
+    def get_max_cache_shape(self):
+        return None
+
+    def get_mask_sizes(self, query_length, *args, **kwargs):
+        return self._seq_len + query_length, 0
+
+    def lazy_initialization(self, *args, **kwargs):
+        pass
+
+    def reorder_cache(self, beam_idx):
+        if self._needs_decompress:
+            _ = self.keys
+        if self._keys is not None:
+            self._keys = self._keys.index_select(0, beam_idx.to(self._keys.device))
+        if self._values is not None:
+            self._values = self._values.index_select(0, beam_idx.to(self._values.device))
+
+
+class Cache(HFCache):
+    """KV cache compression (cache.py:295-539).
+    Prefill: per-layer PCA on K (RoPE removed, int4 coefficients + int8 basis)
+    + Hadamard + k-means VQ on V; sink (4) + window (64) kept fp16.
+    Decode: optional 8-bit Lloyd-Max per-token stream (``_streaming``)."""
+
+    def __init__(self, head_dim=128, num_layers=32, n_kv_heads=8, device="cuda",
+                 k_target_cr=20.0, max_rank_k=192,
+                 v_vq_group_size=4, v_vq_codebook_size=256,
+                 sink_tokens=4, residual_window=64, rope_inv_freq=None):
+        self.head_dim = head_dim
+        self._num_layers = num_layers
+        self._n_kv_heads = n_kv_heads
+        self._per_layer_dim = n_kv_heads * head_dim
+        self._k_target_cr = k_target_cr
+        self._max_rank_k = max_rank_k
+        self._v_vq_group_size = v_vq_group_size
+        self._v_vq_codebook_size = v_vq_codebook_size
+        self._sink_tokens = sink_tokens
+        self._residual_window = residual_window
+        self._rope_inv_freq = rope_inv_freq
+        self._device = device
+        self._streaming = False
+        self._stream_bits = 8
+        self._stream_qjl = False
+        self._lazy_per_layer = True
+        self._full_fused = False
+        self._last_accessed_layer = -1
+        self._compressed = False
+        self._compressed_layers = {}
+        self._fused_decode_update = False
+        # decode-attention knobs of the HIP kernel (0 = automatic split count)
+        self._n_splits = 0
+        self._basis_override = None  # {layer_idx: (1024, rank) fp32} to pin the PCA basis
+        super().__init__(layers=[CacheLayer(i) for i in range(num_layers)])
+        for l in self.layers:
+            l._cache_ref = self
+
+    @classmethod
+    def from_model(cls, model, k_target_cr=16.0, **kwargs):
+        cfg = model.config
+        hd = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        return cls(head_dim=hd, num_layers=cfg.num_hidden_layers,
+                   n_kv_heads=getattr(cfg, "num_key_value_heads", cfg.num_attention_heads),
+                   device=str(next(model.parameters()).device),
+                   k_target_cr=k_target_cr,
+                   rope_inv_freq=host.get_rope_inv_freq(model), **kwargs)
+
+    # -- compression (cache.py:338-460) -----------------------------------
+    def compress(self):
+        if self._compressed:
+            return
+        k0 = self.layers[0]._keys
+        if k0 is None:
+            return
+        B, _, seq, _ = k0.shape
+        sink, win = self._sink_tokens, self._residual_window
+        if seq <= sink + win + 4:
+            return
+        if not k0.is_cuda:
+            raise ops.ShardHipUnavailable("shard_amd.Cache compresses on the GPU only")
+        for li in range(self._num_layers):
+            layer = self.layers[li]
+            if layer._keys is None:
+                continue
+            layer._gpu_compressed = compress_layer(self, layer._keys, layer._values, li)
+            layer._keys = None
+            layer._values = None
+            layer._needs_decompress = True
+        self._compressed = True
+
+    # -- memory accounting (cache.py:462-539) ------------------------------
+    def memory_bytes(self):
+        total = 0
+        has_gc = False
+        for l in self.layers:
+            gc = l._gpu_compressed
+            if gc is None:
+                continue
+            has_gc = True
+            seen = set()
+            for k, v in gc.items():
+                if torch.is_tensor(v) and v.data_ptr() not in seen and not k.endswith("_buf"):
+                    seen.add(v.data_ptr())
+                    total += _nb(v)
+            if "k_idx_buf" in gc:
+                s = gc.get("stream_n", 0) // max(gc.get("batch", 1), 1)
+                bpv = self._stream_bits / 8.0
+                for k in ("k_idx_buf", "v_idx_buf"):
+                    total += int(gc[k][:s].nelement() * bpv)
+                for k in ("k_norm_buf", "v_norm_buf"):
+                    total += _nb(gc[k][:s])
+        if has_gc:
+            return total
+        return sum(_nb(l._keys) + _nb(l._values) for l in self.layers if l._keys is not None)
+
+    def clean_memory_bytes(self):
+        """Storage-only compressed KV size (same fields as cache.py:499-516)."""
+        total = 0
+        has_gc = False
+        for l in self.layers:
+            gc = l._gpu_compressed
+            if gc is None:
+                continue
+            has_gc = True
+            total += sum(_nb(gc[k]) for k in
+                         ("k_coeffs", "k_coeff_scale", "k_basis_q", "k_basis_scale", "k_mean",
+                          "v_packed", "sink_k", "sink_v", "win_k", "win_v"))
+            total += _nb(gc["v_qdata"]["ch_maxabs"])
+            total += _nb(gc["v_qdata"]["centroids"])
+        if has_gc:
+            return total
+        return sum(_nb(l._keys) + _nb(l._values) for l in self.layers if l._keys is not None)
+
+    def fp16_equivalent_bytes(self):
+        gc = self.layers[0]._gpu_compressed
+        if gc is not None:
+            seq = gc["n_compress"] + self._sink_tokens + self._residual_window + gc.get("stream_n", 0)
+        elif self.layers[0]._keys is not None:
+            seq = self.layers[0]._keys.shape[2]
+        else:
+            return 0
+        return seq * self._n_kv_heads * self.head_dim * 4 * self._num_layers
+
+    def compress_ratio(self):
+        return self.fp16_equivalent_bytes() / max(self.memory_bytes(), 1)
+
+    def clean_compress_ratio(self):
+        gc = self.layers[0]._gpu_compressed
+        if gc is not None:
+            seq = gc["n_compress"] + self._sink_tokens + self._residual_window
+            fp16_bytes = seq * self._n_kv_heads * self.head_dim * 4 * self._num_layers
+            return fp16_bytes / max(self.clean_memory_bytes(), 1)
+        return self.compress_ratio()
+
+
+def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li: int,
+                   basis=None) -> dict:
+    """Compress one layer's prefill K/V (B, G, T, D) fp16 into the device format.
+
+    _compress_k (cache.py:368-396), _compress_v (398-404), _build_gpu_format
+    (406-454).  The projection runs on the MFMA GEMM, the integer chain, the
+    Hadamard/normalization, the k-means assignment and update in HIP kernels.
+    """
+    B, G, seq, D = k_full.shape
+    dev = k_full.device
+    sink, win = cache._sink_tokens, cache._residual_window
+    start, end = sink, seq - win
+    n_comp = end - start
+    inv_freq = cache._rope_inv_freq
+    torch.manual_seed(42 + li)
+
+    # ---- K: undo RoPE (fp32), PCA basis, DP bits, int8 basis
+    k_mid = k_full[:, :, start:end, :].float()
+    if inv_freq is not None:
+        pos = torch.arange(start, end, device=dev)
+        k_mid = host.undo_rope(k_mid, pos, inv_freq.to(dev))
+    p_dim = G * D
+    flat = k_mid.permute(0, 2, 1, 3).reshape(B * n_comp, p_dim)
+    del k_mid
+    n = flat.shape[0]
+    mean = flat.mean(dim=0)
+    rank = min(cache._max_rank_k, p_dim, n - 1)
+    centered = flat - mean
+    del flat
+    if basis is None and cache._basis_override is not None:
+        basis = cache._basis_override.get(li)
+    if basis is None:
+        _, S, V = torch.svd_lowrank(centered, q=rank, niter=24)
+        basis = V[:, :rank]
+        eig = (S[:rank].float() ** 2) / n
+    else:
+        basis = basis.to(dev, torch.float32)[:, :rank]
+        eig = (centered @ basis).pow(2).mean(dim=0)
+    budget = max(64, int(p_dim * 16 / cache._k_target_cr))
+    alloc = host.dp_bit_allocation(eig, budget)
+    keep = sum(1 for b in alloc if b > 0)
+    if keep & 1:
+        keep -= 1
+    if keep > 0:
+        basis = basis[:, :keep].contiguous()
+        alloc = alloc[:keep]
+    col_max = basis.abs().max(dim=0).values.clamp(min=1e-6)
+    scale = col_max / 127.0
+    basis_q = (basis / scale).round().clamp(-127, 127).to(torch.int8)
+    basis_deq = basis_q.float() * scale.float()                  # (p_dim, keep)
+
+    # ---- projection on MFMA (fp16 operands, fp32 accumulate); columns padded to 32
+    keep32 = ((keep + 31) // 32) * 32
+    bt = torch.zeros(keep32, p_dim, dtype=torch.float16, device=dev)
+    bt[:keep] = basis_deq.t().half()
+    proj = ops.pca_project(centered.half(), bt)[:, :keep].contiguous()
+    del centered
+    bits = torch.tensor(alloc, dtype=torch.int32, device=dev)
+    chain = ops.int4_quant_pack(proj, bits)
+    del proj
+
+    # ---- V: Hadamard -> channel max -> 4-dim subvectors -> k-means (256)
+    x, ch32, ch16 = ops.vq_prepare(v_full[:, :, start:end, :].reshape(B * G, n_comp, D),
+                                   cache._v_vq_group_size)
+    centroids, idx = ops.kmeans(x, cache._v_vq_codebook_size, n_iter=30, seed=42)
+    del x
+    ng = D // cache._v_vq_group_size
+    v_idx = idx.to(torch.uint8)
+    v_indices = v_idx.view(B, G, n_comp, ng)
+
+    k_scale_h = scale.half()
+    k_basis_f16 = (basis_q.to(torch.float16) * k_scale_h.to(torch.float16)).contiguous()
+    cs16 = chain["coeff_scale"].half()
+    gc = {
+        "k_coeffs": chain["packed"],
+        "k_coeff_scale": cs16,
+        "k_coeffs_shape": (B * n_comp, keep),
+        "k_basis_q": basis_q,
+        "k_basis_scale": k_scale_h,
+        "k_basis_f16": k_basis_f16,
+        "k_mean": mean.half(),
+        "k_mean_f16": mean.half().contiguous(),
+        "k_alloc": alloc,
+        "v_qdata": {"centroids": centroids.half(), "packed": v_idx, "ch_maxabs": ch16,
+                    "shape": (B * G, n_comp, D), "group_size": cache._v_vq_group_size,
+                    "bits": 8, "n_orig": v_idx.numel()},
+        "v_packed": v_idx,
+        "v_indices": v_indices,
+        "v_centroids_f16": centroids.half().contiguous(),
+        "v_ch_f16": ch16.view(B, G, D),
+        "sink_k": k_full[:, :, :sink, :].contiguous(),
+        "sink_v": v_full[:, :, :sink, :].contiguous(),
+        "win_k": k_full[:, :, end:, :].contiguous(),
+        "win_v": v_full[:, :, end:, :].contiguous(),
+        "n_compress": n_comp, "batch": B, "compress_start": start,
+        "n_kv": G, "head_dim": D, "rank": keep,
+    }
+    if B == 1:
+        gc["v_indices_u8"] = v_indices.view(G, n_comp, ng)
+    finalize_format(gc, inv_freq, dev)
+    return gc
+
+
+def finalize_format(gc: dict, inv_freq, dev):
+    """Derived device tensors of the decode kernel: rank padded to a multiple of
+    32 (zero nibbles / zero basis columns), inverse frequencies on the device."""
+    n_total, keep = gc["k_coeffs_shape"]
+    rank_pad = ((keep + 31) // 32) * 32
+    gc["rank_pad"] = rank_pad
+    if rank_pad == keep:
+        gc["k_coeffs_pad"] = gc["k_coeffs"]
+        gc["k_basis_pad"] = gc["k_basis_f16"]
+        gc["k_coeff_scale_pad"] = gc["k_coeff_scale"]
+    else:
+        packed = gc["k_coeffs"][: n_total * keep // 2].view(n_total, keep // 2)
+        pad = torch.full((n_total, rank_pad // 2), 0x88, dtype=torch.uint8, device=dev)
+        pad[:, : keep // 2] = packed
+        gc["k_coeffs_pad"] = pad.reshape(-1)
+        bp = torch.zeros(gc["k_basis_f16"].shape[0], rank_pad, dtype=torch.float16, device=dev)
+        bp[:, :keep] = gc["k_basis_f16"]
+        gc["k_basis_pad"] = bp
+        cp = torch.zeros(rank_pad, dtype=torch.float16, device=dev)
+        cp[:keep] = gc["k_coeff_scale"]
+        gc["k_coeff_scale_pad"] = cp
+    if inv_freq is None:
+        inv_freq = torch.zeros(gc["head_dim"] // 2)
+    gc["inv_freq_dev"] = inv_freq.to(dev, torch.float32).contiguous()

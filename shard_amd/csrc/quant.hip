@@ -1,0 +1,647 @@
+// Bit-exact integer chains of the compressed-KV path on gfx950:
+//   * key coefficient group quantization -> dequantization -> int4 -> packing
+//   * per-token 8-bit Lloyd-Max stream quantizer
+//   * Walsh-Hadamard transform, VQ front half, nearest-centroid assignment,
+//     deterministic k-means centroid update
+// This file is compiled with -ffp-contract=off and uses explicitly rounded
+// fp32 operations so every value follows the reference's per-op rounding.
+#include "common.h"
+
+namespace shard {
+
+// ---------------------------------------------------------------------------
+// int4 chain (rope.py:95-161 values, cache.py:416-420, triton_kernels.py:648-682)
+// ---------------------------------------------------------------------------
+
+// Dequantized group value of one coefficient (quantize_group then
+// dequantize_group): y = code/L*rng + lo, code = clamp(rint(clamp((x-lo)/rng,0,1)*L),0,L).
+__device__ __forceinline__ float group_deq(float x, int bits, float lo, float rng,
+                                           uint8_t* code_out) {
+  if (bits <= 0) {
+    *code_out = 0;
+    return 0.f;
+  }
+  const float L = (float)((1 << bits) - 1);
+  float v = div_rn(sub_rn(x, lo), rng);
+  v = fminf(fmaxf(v, 0.f), 1.f);
+  v = mul_rn(v, L);
+  float code = rintf(v);  // round half to even, as torch.round
+  code = fminf(fmaxf(code, 0.f), L);
+  *code_out = (uint8_t)(int)code;
+  return add_rn(mul_rn(div_rn(code, L), rng), lo);
+}
+
+__global__ void k_int4_init(uint32_t* ws, int keep) {
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < keep) {
+    ws[c] = 0xFFFFFFFFu;     // running min (ordered key)
+    ws[keep + c] = 0u;       // running max (ordered key)
+    ws[2 * keep + c] = 0u;   // running max |y| (bits of a non-negative float)
+  }
+}
+
+// Column min/max over a slab of rows; one thread per column.
+__global__ void k_int4_minmax(const float* __restrict__ proj, int64_t n, int keep,
+                              int rows_per_block, uint32_t* ws) {
+  int c = threadIdx.x;
+  if (c >= keep) return;
+  int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
+  float mn = INFINITY, mx = -INFINITY;
+  for (int64_t r = r0; r < r1; ++r) {
+    float x = proj[r * keep + c];
+    mn = fminf(mn, x);
+    mx = fmaxf(mx, x);
+  }
+  if (r0 < r1) {
+    atomicMin(&ws[c], f2ord(mn));
+    atomicMax(&ws[keep + c], f2ord(mx));
+  }
+}
+
+__device__ __forceinline__ void col_lo_rng(const uint32_t* ws, int keep, int c,
+                                           float* lo, float* rng) {
+  float l = ord2f(ws[c]);
+  float h = ord2f(ws[keep + c]);
+  *lo = l;
+  *rng = fmaxf(sub_rn(h, l), 1e-6f);
+}
+
+// Column max |y| of the dequantized values; optionally writes the group codes.
+__global__ void k_int4_absmax(const float* __restrict__ proj, int64_t n, int keep,
+                              int rows_per_block, const int32_t* __restrict__ bits,
+                              uint32_t* ws, uint8_t* __restrict__ codes) {
+  int c = threadIdx.x;
+  if (c >= keep) return;
+  int b = bits[c];
+  float lo, rng;
+  col_lo_rng(ws, keep, c, &lo, &rng);
+  int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
+  float amax = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    uint8_t code;
+    float y = group_deq(proj[r * keep + c], b, lo, rng, &code);
+    amax = fmaxf(amax, fabsf(y));
+    if (codes) codes[r * keep + c] = code;
+  }
+  if (r0 < r1) atomicMax(&ws[2 * keep + c], __float_as_uint(amax));
+}
+
+__device__ __forceinline__ int q4_of(const float* __restrict__ proj, int64_t e, int keep,
+                                     const int32_t* __restrict__ bits, const uint32_t* ws) {
+  int c = (int)(e % keep);
+  float lo, rng;
+  col_lo_rng(ws, keep, c, &lo, &rng);
+  uint8_t code;
+  float y = group_deq(proj[e], bits[c], lo, rng, &code);
+  float cs = div_rn(fmaxf(__uint_as_float(ws[2 * keep + c]), 1e-6f), 7.0f);
+  float q = rintf(div_rn(y, cs));
+  q = fminf(fmaxf(q, -7.f), 7.f);
+  return (int)q;
+}
+
+__global__ void k_int4_pack(const float* __restrict__ proj, int64_t n, int keep,
+                            const int32_t* __restrict__ bits, const uint32_t* ws,
+                            uint8_t* __restrict__ packed, float* coeff_scale,
+                            float* lo_out, float* rng_out) {
+  int64_t total = n * keep;
+  int64_t nbytes = (total + 1) / 2;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < keep) {
+    float lo, rng;
+    col_lo_rng(ws, keep, (int)i, &lo, &rng);
+    coeff_scale[i] = div_rn(fmaxf(__uint_as_float(ws[2 * keep + i]), 1e-6f), 7.0f);
+    if (lo_out) lo_out[i] = bits[i] > 0 ? lo : 0.f;
+    if (rng_out) rng_out[i] = bits[i] > 0 ? rng : 0.f;
+  }
+  if (i >= nbytes) return;
+  int64_t e0 = 2 * i, e1 = 2 * i + 1;
+  int q0 = q4_of(proj, e0, keep, bits, ws);
+  int q1 = e1 < total ? q4_of(proj, e1, keep, bits, ws) : -8;  // pad nibble -> 0
+  packed[i] = (uint8_t)(((q0 + 8) & 15) | (((q1 + 8) & 15) << 4));
+}
+
+// ---------------------------------------------------------------------------
+// Walsh-Hadamard within a wave: lane l holds elements l + 64*k, k < E.
+// Stage h pairs element e with e^h: lower index gets a+b, upper a-b
+// (cache.py:14-18), stages in increasing h, then one IEEE division.
+// ---------------------------------------------------------------------------
+template <int E>
+__device__ __forceinline__ void wave_fwht(float (&x)[E], int d) {
+  const int l = (int)lane_id();
+  for (int h = 1; h < d; h <<= 1) {
+    if (h < 64) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        float p = __shfl_xor(x[k], h, 64);
+        x[k] = (l & h) ? sub_rn(p, x[k]) : add_rn(x[k], p);
+      }
+    } else {
+      const int hk = h >> 6;
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        if ((k & hk) == 0) {
+          float a = x[k], b = x[k | hk];
+          x[k] = add_rn(a, b);
+          x[k | hk] = sub_rn(a, b);
+        }
+      }
+    }
+  }
+  // torch divides an fp32 tensor by the Python float sqrt(d): fp32(double sqrt)
+  const float s = (float)sqrt((double)d);
+#pragma unroll
+  for (int k = 0; k < E; ++k) x[k] = div_rn(x[k], s);
+}
+
+template <int E>
+__global__ void k_fwht_rows(const float* __restrict__ x, float* __restrict__ y, int64_t rows) {
+  const int d = 64 * E;
+  const int l = (int)lane_id();
+  int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t r = wave; r < rows; r += nwaves) {
+    float v[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = x[r * d + l + 64 * k];
+    wave_fwht<E>(v, d);
+#pragma unroll
+    for (int k = 0; k < E; ++k) y[r * d + l + 64 * k] = v[k];
+  }
+}
+
+// Small d (< 64): one thread per row, same butterflies.
+__global__ void k_fwht_small(const float* __restrict__ x, float* __restrict__ y, int64_t rows,
+                             int d) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float v[32];
+  for (int i = 0; i < d; ++i) v[i] = x[r * d + i];
+  for (int h = 1; h < d; h <<= 1)
+    for (int i = 0; i < d; ++i)
+      if ((i & h) == 0) {
+        float a = v[i], b = v[i + h];
+        v[i] = add_rn(a, b);
+        v[i + h] = sub_rn(a, b);
+      }
+  const float s = (float)sqrt((double)d);
+  for (int i = 0; i < d; ++i) y[r * d + i] = div_rn(v[i], s);
+}
+
+// ---------------------------------------------------------------------------
+// VQ front half: hadamard(fp32(v)) -> channel abs max -> normalized subvectors
+// ---------------------------------------------------------------------------
+template <int E>
+__global__ void k_vq_rot(const uint16_t* __restrict__ v, int64_t bh, int64_t seq,
+                         int64_t bh_stride, float* __restrict__ xo,
+                         uint32_t* __restrict__ chmax) {
+  const int d = 64 * E;
+  const int l = (int)lane_id();
+  int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  int64_t rows = bh * seq;
+  // per-lane running channel max for the current bh (flushed when bh changes)
+  int64_t cur = -1;
+  float m[E];
+  for (int64_t r = wave; r < rows; r += nwaves) {
+    int64_t b = r / seq, t = r - b * seq;
+    if (b != cur) {
+      if (cur >= 0)
+#pragma unroll
+        for (int k = 0; k < E; ++k) atomicMax(&chmax[cur * d + l + 64 * k], __float_as_uint(m[k]));
+      cur = b;
+#pragma unroll
+      for (int k = 0; k < E; ++k) m[k] = 0.f;
+    }
+    float x[E];
+    const uint16_t* src = v + b * bh_stride + t * d;
+#pragma unroll
+    for (int k = 0; k < E; ++k) x[k] = h2f(src[l + 64 * k]);
+    wave_fwht<E>(x, d);
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      xo[r * d + l + 64 * k] = x[k];
+      m[k] = fmaxf(m[k], fabsf(x[k]));
+    }
+  }
+  if (cur >= 0)
+#pragma unroll
+    for (int k = 0; k < E; ++k) atomicMax(&chmax[cur * d + l + 64 * k], __float_as_uint(m[k]));
+}
+
+__global__ void k_vq_norm(float* __restrict__ xo, int64_t bh, int64_t seq, int d,
+                          const uint32_t* __restrict__ chmax, float* ch_f32,
+                          uint16_t* ch_f16) {
+  int64_t total = bh * seq * d;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int64_t c = i % d;
+    int64_t b = i / (seq * d);
+    float ch = fmaxf(__uint_as_float(chmax[b * d + c]), 1e-8f);
+    xo[i] = div_rn(xo[i], ch);
+    if (i - b * seq * d < d) {  // first token of this bh writes the channel scale
+      if (ch_f32) ch_f32[b * d + c] = ch;
+      if (ch_f16) ch_f16[b * d + c] = f2h(ch);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Nearest centroid (triton_kernels.py:689-746 formula; first index on ties)
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ void k_vq_assign(const float* __restrict__ x, int64_t n,
+                            const float* __restrict__ c, int k, int32_t* __restrict__ idx) {
+  extern __shared__ float cs[];
+  for (int i = threadIdx.x; i < k * D; i += blockDim.x) cs[i] = c[i];
+  __syncthreads();
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+    float xv[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) xv[j] = x[r * D + j];
+    float best = INFINITY;
+    int arg = 0;
+    for (int q = 0; q < k; ++q) {
+      float dist = 0.f;
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        float df = sub_rn(xv[j], cs[q * D + j]);
+        dist = add_rn(dist, mul_rn(df, df));
+      }
+      if (dist < best) {
+        best = dist;
+        arg = q;
+      }
+    }
+    idx[r] = arg;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic k-means update: stable counting sort by centroid, then each
+// (centroid, dim) sums its rows in increasing row order (torch CPU index_add_
+// order), divides by the count, and keeps empty centroids.
+// ---------------------------------------------------------------------------
+constexpr int KM_BLOCK = 256;
+
+__global__ void k_km_hist(const int32_t* __restrict__ idx, int64_t n, int k,
+                          int32_t* __restrict__ blk_hist) {
+  __shared__ int32_t h[1024];
+  for (int i = threadIdx.x; i < k; i += blockDim.x) h[i] = 0;
+  __syncthreads();
+  int64_t r = (int64_t)blockIdx.x * KM_BLOCK + threadIdx.x;
+  if (r < n) atomicAdd(&h[idx[r]], 1);
+  __syncthreads();
+  for (int i = threadIdx.x; i < k; i += blockDim.x) blk_hist[(int64_t)blockIdx.x * k + i] = h[i];
+}
+
+// For each centroid: exclusive scan over blocks (in place) and total count.
+__global__ void k_km_scan_blocks(int32_t* __restrict__ blk_hist, int64_t nblk, int k,
+                                 int32_t* __restrict__ count) {
+  int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= k) return;
+  int32_t run = 0;
+  for (int64_t b = 0; b < nblk; ++b) {
+    int32_t v = blk_hist[b * k + q];
+    blk_hist[b * k + q] = run;
+    run += v;
+  }
+  count[q] = run;
+}
+
+__global__ void k_km_offsets(const int32_t* __restrict__ count, int k, int32_t* __restrict__ off) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    int32_t run = 0;
+    for (int q = 0; q < k; ++q) {
+      off[q] = run;
+      run += count[q];
+    }
+  }
+}
+
+__global__ void k_km_scatter(const int32_t* __restrict__ idx, int64_t n, int k,
+                             const int32_t* __restrict__ blk_off, const int32_t* __restrict__ off,
+                             int32_t* __restrict__ perm) {
+  __shared__ int32_t s[KM_BLOCK];
+  int64_t r = (int64_t)blockIdx.x * KM_BLOCK + threadIdx.x;
+  int my = r < n ? idx[r] : -1;
+  s[threadIdx.x] = my;
+  __syncthreads();
+  if (r >= n) return;
+  int rank = 0;
+  for (int j = 0; j < (int)threadIdx.x; ++j) rank += (s[j] == my);
+  perm[off[my] + blk_off[(int64_t)blockIdx.x * k + my] + rank] = (int32_t)r;
+}
+
+template <int D>
+__global__ void k_km_sum(const float* __restrict__ x, const int32_t* __restrict__ perm,
+                         const int32_t* __restrict__ count, const int32_t* __restrict__ off,
+                         const float* __restrict__ c, int k, float* __restrict__ newc,
+                         uint32_t* __restrict__ maxd) {
+  // one wave per centroid; 64 rows are loaded in parallel, then added in
+  // increasing row order (every lane keeps the same running sums)
+  const int l = (int)lane_id();
+  int q = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+  if (q >= k) return;
+  int32_t cnt = count[q], o = off[q];
+  float acc[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) acc[j] = 0.f;
+  for (int32_t base = 0; base < cnt; base += 64) {
+    int n_here = cnt - base < 64 ? cnt - base : 64;
+    float xv[D];
+    if (l < n_here) {
+      int64_t row = perm[o + base + l];
+#pragma unroll
+      for (int j = 0; j < D; ++j) xv[j] = x[row * D + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < D; ++j) xv[j] = 0.f;
+    }
+    for (int i = 0; i < n_here; ++i)
+#pragma unroll
+      for (int j = 0; j < D; ++j) acc[j] = add_rn(acc[j], __shfl(xv[j], i, 64));
+  }
+  if (l < D) {
+    float a = acc[0];
+#pragma unroll
+    for (int j = 1; j < D; ++j) a = (l == j) ? acc[j] : a;
+    int t = q * D + l;
+    float old = c[t];
+    float nv = cnt > 0 ? div_rn(a, (float)cnt) : old;
+    newc[t] = nv;
+    atomicMax(maxd, __float_as_uint(fabsf(sub_rn(nv, old))));
+  }
+}
+
+__global__ void k_km_zero(uint32_t* p) { *p = 0u; }
+
+__global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Per-token 8-bit Lloyd-Max stream quantizer (cache.py:207-215, streaming.py:59-72)
+// one wave per row, E = hd/64 elements per lane.
+// ---------------------------------------------------------------------------
+template <int E>
+__global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
+                               const float* __restrict__ signs, const float* __restrict__ cb_g,
+                               int n_codes, uint8_t* __restrict__ idx,
+                               uint16_t* __restrict__ norm) {
+  constexpr int D = 64 * E;
+  __shared__ float cb[256];
+  for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
+  __syncthreads();
+  const int l = (int)lane_id();
+  const int w = threadIdx.x >> 6;
+  int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + w;
+  if (r >= rows) return;  // no block-level barrier below this point
+  float t[E], sq[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    t[k] = h2f(x[r * D + l + 64 * k]);
+    sq[k] = mul_rn(t[k], t[k]);  // exact: fp16-derived values square exactly in fp32
+  }
+  // torch CPU fp32 norm: accumulator j (< 8) sums elements j, j+8, j+16, ... in
+  // increasing order; the 8 accumulators are then added left to right.
+  float acc = 0.f;
+#pragma unroll
+  for (int m = 0; m < D / 8; ++m) {
+    float v = __shfl(sq[(8 * m) >> 6], (l + 8 * m) & 63, 64);
+    acc = add_rn(acc, v);  // meaningful in lanes 0..7 (lane j holds accumulator j)
+  }
+  float tot = __shfl(acc, 0, 64);
+#pragma unroll
+  for (int j = 1; j < 8; ++j) tot = add_rn(tot, __shfl(acc, j, 64));
+  float n = fmaxf(sqrtf(tot), 1e-8f);
+#pragma unroll
+  for (int k = 0; k < E; ++k) t[k] = mul_rn(div_rn(t[k], n), signs[l + 64 * k]);
+  wave_fwht<E>(t, D);
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    float v = t[k];
+    int lo = 0, hi = n_codes;  // first i with v <= cb[i] (torch.bucketize, right=False)
+    while (lo < hi) {
+      int mid = (lo + hi) >> 1;
+      if (cb[mid] < v) lo = mid + 1; else hi = mid;
+    }
+    int i = lo < n_codes - 1 ? lo : n_codes - 1;
+    int left = i > 0 ? i - 1 : 0;
+    float dl = fabsf(sub_rn(cb[left], v));
+    float di = fabsf(sub_rn(cb[i], v));
+    idx[r * D + l + 64 * k] = (uint8_t)(dl < di ? left : i);
+  }
+  if (l == 0) norm[r] = f2h(n);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill K preparation: undo RoPE (fp32), subtract mean, fp16 GEMM operand.
+// ---------------------------------------------------------------------------
+__global__ void k_k_prepare(const uint16_t* __restrict__ k, int batch, int n_kv, int seq, int hd,
+                            int start, int n_comp, const float* __restrict__ inv_freq,
+                            const float* __restrict__ mean, uint16_t* __restrict__ out) {
+  const int D = n_kv * hd;
+  const int hd2 = hd >> 1;
+  int64_t total = (int64_t)batch * n_comp * n_kv * hd2;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    int i = (int)(e % hd2);
+    int64_t r = e / hd2;
+    int g = (int)(r % n_kv);
+    int64_t bt = r / n_kv;
+    int t = (int)(bt % n_comp);
+    int b = (int)(bt / n_comp);
+    int pos = start + t;
+    float ph = mul_rn((float)pos, inv_freq[i]);
+    float sn, cs;
+    sincosf(ph, &sn, &cs);
+    const uint16_t* src = k + (((int64_t)b * n_kv + g) * seq + pos) * hd;
+    float lo = h2f(src[i]), hi = h2f(src[i + hd2]);
+    // undo_rope: k*cos - rotate_half(k)*sin, rotate_half = [-hi, lo]
+    float ulo = add_rn(mul_rn(lo, cs), mul_rn(hi, sn));
+    float uhi = sub_rn(mul_rn(hi, cs), mul_rn(lo, sn));
+    int64_t row = (int64_t)b * n_comp + t;
+    int col = g * hd + i;
+    out[row * D + col] = f2h(sub_rn(ulo, mean[col]));
+    out[row * D + col + hd2] = f2h(sub_rn(uhi, mean[col + hd2]));
+  }
+}
+
+}  // namespace shard
+
+using namespace shard;
+
+extern "C" {
+
+size_t shard_int4_quant_pack_workspace(int64_t n_rows, int32_t keep) {
+  (void)n_rows;
+  return (size_t)3 * (keep > 0 ? keep : 0) * sizeof(uint32_t);
+}
+
+int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const int32_t* bits,
+                          uint8_t* packed, float* coeff_scale, float* lo, float* rng,
+                          uint8_t* codes, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (!proj || !bits || !packed || !coeff_scale || n_rows <= 0 || keep <= 0) return SHARD_ERR_ARG;
+  if (keep > 1024) return SHARD_ERR_SHAPE;
+  if (!workspace || workspace_bytes < shard_int4_quant_pack_workspace(n_rows, keep))
+    return SHARD_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* ws = (uint32_t*)workspace;
+  const int rpb = 128;
+  int64_t nblk = (n_rows + rpb - 1) / rpb;
+  int tpb = ((keep + 63) / 64) * 64;
+  hipLaunchKernelGGL(k_int4_init, dim3((keep + 255) / 256), dim3(256), 0, s, ws, keep);
+  hipLaunchKernelGGL(k_int4_minmax, dim3((unsigned)nblk), dim3(tpb), 0, s, proj, n_rows, keep, rpb, ws);
+  hipLaunchKernelGGL(k_int4_absmax, dim3((unsigned)nblk), dim3(tpb), 0, s, proj, n_rows, keep, rpb,
+                     bits, ws, codes);
+  int64_t nbytes = (n_rows * keep + 1) / 2;
+  int64_t nthreads = nbytes > keep ? nbytes : keep;
+  hipLaunchKernelGGL(k_int4_pack, dim3((unsigned)((nthreads + 255) / 256)), dim3(256), 0, s, proj,
+                     n_rows, keep, bits, ws, packed, coeff_scale, lo, rng);
+  SHARD_LAUNCH_CHECK("shard_int4_quant_pack");
+  return SHARD_OK;
+}
+
+int shard_fwht(const float* x, float* y, int64_t rows, int32_t d, void* stream) {
+  if (!x || !y || rows <= 0 || d < 2) return SHARD_ERR_ARG;
+  if (d & (d - 1)) return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  if (d < 64) {
+    if (d > 32) return SHARD_ERR_SHAPE;
+    hipLaunchKernelGGL(k_fwht_small, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, x, y,
+                       rows, d);
+  } else {
+    int64_t waves = rows;
+    int blocks = grid_cap((waves + 3) / 4, 4096);
+    switch (d) {
+      case 64: hipLaunchKernelGGL(k_fwht_rows<1>, dim3(blocks), dim3(256), 0, s, x, y, rows); break;
+      case 128: hipLaunchKernelGGL(k_fwht_rows<2>, dim3(blocks), dim3(256), 0, s, x, y, rows); break;
+      case 256: hipLaunchKernelGGL(k_fwht_rows<4>, dim3(blocks), dim3(256), 0, s, x, y, rows); break;
+      case 512: hipLaunchKernelGGL(k_fwht_rows<8>, dim3(blocks), dim3(256), 0, s, x, y, rows); break;
+      case 1024: hipLaunchKernelGGL(k_fwht_rows<16>, dim3(blocks), dim3(256), 0, s, x, y, rows); break;
+      default: return SHARD_ERR_SHAPE;
+    }
+  }
+  SHARD_LAUNCH_CHECK("shard_fwht");
+  return SHARD_OK;
+}
+
+size_t shard_vq_prepare_workspace(int64_t bh, int32_t hd) {
+  return (size_t)(bh > 0 ? bh : 0) * (hd > 0 ? hd : 0) * sizeof(uint32_t);
+}
+
+int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int64_t v_bh_stride,
+                     float* x_out, float* ch_f32, uint16_t* ch_f16, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (!v || !x_out || bh <= 0 || seq <= 0) return SHARD_ERR_ARG;
+  if (hd != 64 && hd != 128 && hd != 256) return SHARD_ERR_SHAPE;
+  if (!workspace || workspace_bytes < shard_vq_prepare_workspace(bh, hd)) return SHARD_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* chmax = (uint32_t*)workspace;
+  const int64_t nch = bh * hd;
+  hipLaunchKernelGGL(k_fill_u32, dim3(grid_cap((nch + 255) / 256, 4096)), dim3(256), 0, s, chmax,
+                     nch, 0u);
+  int64_t rows = bh * seq;
+  int blocks = grid_cap((rows + 3) / 4, 8192);
+  switch (hd) {
+    case 64: hipLaunchKernelGGL(k_vq_rot<1>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
+    case 128: hipLaunchKernelGGL(k_vq_rot<2>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
+    default: hipLaunchKernelGGL(k_vq_rot<4>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
+  }
+  int64_t total = rows * hd;
+  hipLaunchKernelGGL(k_vq_norm, dim3(grid_cap((total + 255) / 256, 16384)), dim3(256), 0, s, x_out,
+                     bh, seq, hd, chmax, ch_f32, ch_f16);
+  SHARD_LAUNCH_CHECK("shard_vq_prepare");
+  return SHARD_OK;
+}
+
+int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids, int32_t k,
+                    int32_t* idx, void* stream) {
+  if (!x || !centroids || !idx || n <= 0 || k <= 0 || d <= 0) return SHARD_ERR_ARG;
+  if (k > 1024 || d > 8) return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  int blocks = grid_cap((n + 255) / 256, 8192);
+  size_t lds = (size_t)k * d * sizeof(float);
+  switch (d) {
+    case 1: hipLaunchKernelGGL(k_vq_assign<1>, dim3(blocks), dim3(256), lds, s, x, n, centroids, k, idx); break;
+    case 2: hipLaunchKernelGGL(k_vq_assign<2>, dim3(blocks), dim3(256), lds, s, x, n, centroids, k, idx); break;
+    case 4: hipLaunchKernelGGL(k_vq_assign<4>, dim3(blocks), dim3(256), lds, s, x, n, centroids, k, idx); break;
+    case 8: hipLaunchKernelGGL(k_vq_assign<8>, dim3(blocks), dim3(256), lds, s, x, n, centroids, k, idx); break;
+    default: return SHARD_ERR_SHAPE;
+  }
+  SHARD_LAUNCH_CHECK("shard_vq_assign");
+  return SHARD_OK;
+}
+
+size_t shard_kmeans_update_workspace(int64_t n, int32_t k) {
+  if (n <= 0 || k <= 0) return 0;
+  int64_t nblk = (n + KM_BLOCK - 1) / KM_BLOCK;
+  return (size_t)(nblk * k + 2 * (int64_t)k + n) * sizeof(int32_t);
+}
+
+int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx,
+                        const float* centroids, int32_t k, float* new_centroids,
+                        float* max_delta, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (!x || !idx || !centroids || !new_centroids || !max_delta || n <= 0 || k <= 0)
+    return SHARD_ERR_ARG;
+  if (k > 1024 || (d != 1 && d != 2 && d != 4 && d != 8)) return SHARD_ERR_SHAPE;
+  if (!workspace || workspace_bytes < shard_kmeans_update_workspace(n, k)) return SHARD_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  int64_t nblk = (n + KM_BLOCK - 1) / KM_BLOCK;
+  int32_t* blk = (int32_t*)workspace;
+  int32_t* count = blk + nblk * k;
+  int32_t* off = count + k;
+  int32_t* perm = off + k;
+  hipLaunchKernelGGL(k_km_hist, dim3((unsigned)nblk), dim3(KM_BLOCK), 0, s, idx, n, k, blk);
+  hipLaunchKernelGGL(k_km_scan_blocks, dim3((k + 255) / 256), dim3(256), 0, s, blk, nblk, k, count);
+  hipLaunchKernelGGL(k_km_offsets, dim3(1), dim3(64), 0, s, count, k, off);
+  hipLaunchKernelGGL(k_km_scatter, dim3((unsigned)nblk), dim3(KM_BLOCK), 0, s, idx, n, k, blk, off, perm);
+  hipLaunchKernelGGL(k_km_zero, dim3(1), dim3(1), 0, s, (uint32_t*)max_delta);
+  unsigned kb = (unsigned)((k + 3) / 4);
+  switch (d) {
+    case 1: hipLaunchKernelGGL(k_km_sum<1>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
+    case 2: hipLaunchKernelGGL(k_km_sum<2>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
+    case 4: hipLaunchKernelGGL(k_km_sum<4>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
+    default: hipLaunchKernelGGL(k_km_sum<8>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
+  }
+  SHARD_LAUNCH_CHECK("shard_kmeans_update");
+  return SHARD_OK;
+}
+
+int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,
+                       const float* codebook, int32_t n_codes, uint8_t* idx, uint16_t* norm,
+                       void* stream) {
+  if (!x || !signs || !codebook || !idx || !norm || rows <= 0 || n_codes <= 0) return SHARD_ERR_ARG;
+  if (n_codes > 256) return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  unsigned blocks = (unsigned)((rows + 3) / 4);
+  switch (hd) {
+    case 64: hipLaunchKernelGGL(k_stream_quant<1>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm); break;
+    case 128: hipLaunchKernelGGL(k_stream_quant<2>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm); break;
+    case 256: hipLaunchKernelGGL(k_stream_quant<4>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm); break;
+    default: return SHARD_ERR_SHAPE;
+  }
+  SHARD_LAUNCH_CHECK("shard_stream_quant");
+  return SHARD_OK;
+}
+
+int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq, int32_t hd,
+                    int32_t start, int32_t n_comp, const float* inv_freq, const float* mean,
+                    uint16_t* out, void* stream) {
+  if (!k || !inv_freq || !mean || !out || batch <= 0 || n_kv <= 0 || n_comp <= 0) return SHARD_ERR_ARG;
+  if ((hd & 1) || start < 0 || start + n_comp > seq) return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  int64_t total = (int64_t)batch * n_comp * n_kv * (hd / 2);
+  hipLaunchKernelGGL(k_k_prepare, dim3(grid_cap((total + 255) / 256, 32768)), dim3(256), 0, s, k,
+                     batch, n_kv, seq, hd, start, n_comp, inv_freq, mean, out);
+  SHARD_LAUNCH_CHECK("shard_k_prepare");
+  return SHARD_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+// Full fp16 reconstruction of the compressed cache for unfused consumers
+// (_ensure_dequant, cache.py:87-124) and the stream dequantizer
+// (_dequant_stream, cache.py:243-279).  Off the decode hot path: used on the
+// first decode step (compression happens inside it), for q_len > 1 extends and
+// for callers that read layer.keys / layer.values.
+#include "common.h"
+
+namespace shard {
+
+constexpr int kRcTok = 32;   // tokens per block
+constexpr int kRcHD = 128;
+
+// K: block = (b, 32-token tile, kv head g); 256 threads = 32 tokens x 8 lanes,
+// each lane owns 8 RoPE pairs (16 dims) of its token.  The head's basis rows
+// and the tile's coefficients are staged in LDS.
+__global__ __launch_bounds__(256)
+void k_reconstruct_k(const uint8_t* __restrict__ coef, const uint16_t* __restrict__ cs,
+                     const uint16_t* __restrict__ basis, const uint16_t* __restrict__ mean,
+                     const float* __restrict__ inv_freq, int B, int G, int rank, int n_comp,
+                     int cstart, uint16_t* __restrict__ k_out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* cf = (uint16_t*)smem;                  // [kRcTok][rank] fp16(nib*cs)
+  uint16_t* bb = cf + kRcTok * rank;               // [kRcHD][rank] basis rows of head g
+  const int tid = threadIdx.x;
+  const int g = blockIdx.y, b = blockIdx.z;
+  const int t0 = blockIdx.x * kRcTok;
+  const int row_bytes = rank / 2;
+  for (int i = tid; i < kRcTok * rank; i += 256) {
+    const int tt = i / rank, r = i - tt * rank;
+    const int t = t0 + tt;
+    uint16_t v = 0;
+    if (t < n_comp) {
+      const uint8_t byte = coef[((int64_t)b * n_comp + t) * row_bytes + (r >> 1)];
+      const int nib = (r & 1) ? (byte >> 4) : (byte & 15);
+      // fp16(nib - 8) * fp16(cs) rounded to fp16, as the reference's fp16 multiply
+      v = f2h((float)(nib - 8) * h2f(cs[r]));
+    }
+    cf[i] = v;
+  }
+  for (int i = tid; i < kRcHD * rank; i += 256)
+    bb[i] = basis[(int64_t)g * kRcHD * rank + i];
+  __syncthreads();
+  const int tt = tid >> 3, part = tid & 7;
+  const int t = t0 + tt;
+  if (t >= n_comp) return;
+  const uint16_t* cr = cf + tt * rank;
+  const int pos = cstart + t;
+#pragma unroll 1
+  for (int u = 0; u < 8; ++u) {
+    const int i = part * 8 + u;  // pair index 0..63
+    float c = 0.f, d = 0.f;
+    const uint16_t* b0 = bb + i * rank;
+    const uint16_t* b1 = bb + (i + 64) * rank;
+    for (int r = 0; r < rank; ++r) {
+      const float cv = h2f(cr[r]);
+      c += cv * h2f(b0[r]);
+      d += cv * h2f(b1[r]);
+    }
+    // recon = fp16(coeffs @ basis^T) + mean, both fp16
+    const float cm = h2f(f2h(h2f(f2h(c)) + h2f(mean[g * kRcHD + i])));
+    const float dm = h2f(f2h(h2f(f2h(d)) + h2f(mean[g * kRcHD + i + 64])));
+    // reapply_rope: k*cos + rotate_half(k)*sin with fp32 phase fl(pos*theta)
+    float sn, csn;
+    sincosf(__fmul_rn((float)pos, inv_freq[i]), &sn, &csn);
+    uint16_t* o = k_out + (((int64_t)b * G + g) * n_comp + t) * kRcHD;
+    o[i] = f2h(__fsub_rn(__fmul_rn(cm, csn), __fmul_rn(dm, sn)));
+    o[i + 64] = f2h(__fadd_rn(__fmul_rn(dm, csn), __fmul_rn(cm, sn)));
+  }
+}
+
+// Butterflies over 128 values held as (lane, lane + 64), bit-exact with hadamard().
+__device__ __forceinline__ void rc_fwht128(float& x0, float& x1) {
+  const int l = (int)lane_id();
+#pragma unroll
+  for (int h = 1; h < 64; h <<= 1) {
+    const float p0 = __shfl_xor(x0, h, 64), p1 = __shfl_xor(x1, h, 64);
+    x0 = (l & h) ? __fsub_rn(p0, x0) : __fadd_rn(x0, p0);
+    x1 = (l & h) ? __fsub_rn(p1, x1) : __fadd_rn(x1, p1);
+  }
+  const float a = x0, c = x1;
+  x0 = __fadd_rn(a, c);
+  x1 = __fsub_rn(a, c);
+  const float s = (float)sqrt(128.0);
+  x0 = __fdiv_rn(x0, s);
+  x1 = __fdiv_rn(x1, s);
+}
+
+// V: one wave per (b, g, t): fp16(hadamard(cb[idx] * ch)), fp32 math.
+__global__ void k_reconstruct_v(const uint8_t* __restrict__ vidx, const uint16_t* __restrict__ vcb,
+                                const uint16_t* __restrict__ vch, int64_t rows, int G, int n_comp,
+                                uint16_t* __restrict__ v_out) {
+  const int l = (int)lane_id();
+  int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t r = wave; r < rows; r += nw) {  // r = (b*G + g)*n_comp + t
+    const int64_t bg = r / n_comp;
+    const uint8_t* ix = vidx + r * 32;
+    const uint16_t* ch = vch + bg * kRcHD;
+    const int d0 = l, d1 = l + 64;
+    float x0 = __fmul_rn(h2f(vcb[4 * ix[d0 >> 2] + (d0 & 3)]), h2f(ch[d0]));
+    float x1 = __fmul_rn(h2f(vcb[4 * ix[d1 >> 2] + (d1 & 3)]), h2f(ch[d1]));
+    rc_fwht128(x0, x1);
+    v_out[r * kRcHD + d0] = f2h(x0);
+    v_out[r * kRcHD + d1] = f2h(x1);
+  }
+}
+
+// Stream rows: fp16(fp16(hadamard(cb[idx]) * signs) * norm).
+__global__ void k_stream_dequant(const uint8_t* __restrict__ idx, const uint16_t* __restrict__ norm,
+                                 int64_t rows, const float* __restrict__ signs,
+                                 const float* __restrict__ cb, uint16_t* __restrict__ y) {
+  const int l = (int)lane_id();
+  int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t r = wave; r < rows; r += nw) {
+    float x0 = cb[idx[r * kRcHD + l]], x1 = cb[idx[r * kRcHD + l + 64]];
+    rc_fwht128(x0, x1);
+    const float n = h2f(norm[r]);
+    y[r * kRcHD + l] = f2h(h2f(f2h(__fmul_rn(x0, signs[l]))) * n);
+    y[r * kRcHD + l + 64] = f2h(h2f(f2h(__fmul_rn(x1, signs[l + 64]))) * n);
+  }
+}
+
+}  // namespace shard
+
+using namespace shard;
+
+extern "C" {
+
+int shard_kv_reconstruct(const shard_decode_args* a, uint16_t* k_out, uint16_t* v_out,
+                         void* stream) {
+  if (!a || !a->k_coeffs || !a->k_coeff_scale || !a->k_basis || !a->k_mean || !a->v_idx ||
+      !a->v_codebook || !a->v_ch || !a->inv_freq || !k_out || !v_out)
+    return SHARD_ERR_ARG;
+  if (a->batch <= 0 || a->n_comp <= 0 || a->n_kv_heads <= 0) return SHARD_ERR_ARG;
+  if (a->head_dim != kRcHD || a->rank <= 0 || (a->rank & 1) || a->rank > 192) return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t lds = (size_t)(kRcTok + kRcHD) * a->rank * sizeof(uint16_t);  // <= 60 KB at rank 192
+  dim3 grid((unsigned)((a->n_comp + kRcTok - 1) / kRcTok), (unsigned)a->n_kv_heads,
+            (unsigned)a->batch);
+  hipLaunchKernelGGL(k_reconstruct_k, grid, dim3(256), lds, s, a->k_coeffs, a->k_coeff_scale,
+                     a->k_basis, a->k_mean, a->inv_freq, a->batch, a->n_kv_heads, a->rank,
+                     a->n_comp, a->compress_start, k_out);
+  const int64_t rows = (int64_t)a->batch * a->n_kv_heads * a->n_comp;
+  hipLaunchKernelGGL(k_reconstruct_v, dim3(grid_cap((rows + 3) / 4, 16384)), dim3(256), 0, s,
+                     a->v_idx, a->v_codebook, a->v_ch, rows, a->n_kv_heads, a->n_comp, v_out);
+  SHARD_LAUNCH_CHECK("shard_kv_reconstruct");
+  return SHARD_OK;
+}
+
+int shard_stream_dequant(const uint8_t* idx, const uint16_t* norm, int64_t rows, int32_t hd,
+                         const float* signs, const float* codebook, uint16_t* y, void* stream) {
+  if (!idx || !norm || !signs || !codebook || !y || rows <= 0) return SHARD_ERR_ARG;
+  if (hd != kRcHD) return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_stream_dequant, dim3(grid_cap((rows + 3) / 4, 16384)), dim3(256), 0, s, idx,
+                     norm, rows, signs, codebook, y);
+  SHARD_LAUNCH_CHECK("shard_stream_dequant");
+  return SHARD_OK;
+}
+
+}  // extern "C"

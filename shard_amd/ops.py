@@ -1,0 +1,340 @@
+"""torch-tensor wrappers over the libshard_hip C ABI.
+
+Every wrapper checks shapes/dtypes/devices on the host before calling into the
+library (the kernels assume what is checked here), passes raw device pointers
+and the current HIP stream, and raises ShardHipError on a non-zero status.
+Tensors must live on a ROCm device; there is no CPU path.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import DecodeArgs, ShardHipError, ShardHipUnavailable  # noqa: F401
+
+
+def _require_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ShardHipUnavailable(
+                "shard_amd kernels run on the GPU only (got a tensor on %s)" % t.device)
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _contig(t, dtype, name):
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# prefill compression: keys
+# ---------------------------------------------------------------------------
+def pca_project(a: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
+    """C = A @ Bt^T on MFMA; A (m, k) fp16, Bt (n, k) fp16 -> (m, n) fp32."""
+    _require_gpu(a, bt)
+    lib = _lib.load()
+    a = _contig(a, torch.float16, "a")
+    bt = _contig(bt, torch.float16, "bt")
+    m, k = a.shape
+    n, k2 = bt.shape
+    if k != k2:
+        raise ValueError("pca_project: inner dims differ")
+    c = torch.empty(m, n, dtype=torch.float32, device=a.device)
+    _lib.check("shard_pca_project", lib.shard_pca_project(
+        _p(a), m, k, k, _p(bt), n, _p(c), n, _stream(a)))
+    return c
+
+
+def k_prepare(k: torch.Tensor, start: int, n_comp: int, inv_freq: torch.Tensor,
+              mean: torch.Tensor) -> torch.Tensor:
+    """undo-RoPE + mean subtraction of keys (B, G, T, D) fp16 -> (B*n_comp, G*D) fp16."""
+    _require_gpu(k, inv_freq, mean)
+    lib = _lib.load()
+    k = _contig(k, torch.float16, "k")
+    B, G, T, D = k.shape
+    inv_freq = _contig(inv_freq.to(k.device), torch.float32, "inv_freq")
+    mean = _contig(mean, torch.float32, "mean")
+    out = torch.empty(B * n_comp, G * D, dtype=torch.float16, device=k.device)
+    _lib.check("shard_k_prepare", lib.shard_k_prepare(
+        _p(k), B, G, T, D, start, n_comp, _p(inv_freq), _p(mean), _p(out), _stream(k)))
+    return out
+
+
+def int4_quant_pack(proj: torch.Tensor, bits: torch.Tensor, want_codes: bool = False):
+    """Group quant -> dequant -> int4 -> packed (bit-exact chain).
+
+    proj (n, keep) fp32; bits (keep,) int32.  Returns dict(packed, coeff_scale,
+    lo, rng[, codes])."""
+    _require_gpu(proj, bits)
+    lib = _lib.load()
+    proj = _contig(proj, torch.float32, "proj")
+    bits = _contig(bits.to(device=proj.device, dtype=torch.int32), torch.int32, "bits")
+    n, keep = proj.shape
+    if bits.numel() != keep:
+        raise ValueError("int4_quant_pack: bits length != keep")
+    dev = proj.device
+    packed = torch.empty((n * keep + 1) // 2, dtype=torch.uint8, device=dev)
+    cs = torch.empty(keep, dtype=torch.float32, device=dev)
+    lo = torch.empty(keep, dtype=torch.float32, device=dev)
+    rng = torch.empty(keep, dtype=torch.float32, device=dev)
+    codes = torch.empty(n, keep, dtype=torch.uint8, device=dev) if want_codes else None
+    ws = _workspace(lib.shard_int4_quant_pack_workspace(n, keep), dev)
+    _lib.check("shard_int4_quant_pack", lib.shard_int4_quant_pack(
+        _p(proj), n, keep, _p(bits), _p(packed), _p(cs), _p(lo), _p(rng), _p(codes),
+        _p(ws), ws.numel(), _stream(proj)))
+    out = {"packed": packed, "coeff_scale": cs, "lo": lo, "rng": rng}
+    if want_codes:
+        out["codes"] = codes
+    return out
+
+
+# ---------------------------------------------------------------------------
+# prefill compression: values
+# ---------------------------------------------------------------------------
+def fwht(x: torch.Tensor) -> torch.Tensor:
+    """Normalized Walsh-Hadamard transform over the last dim (fp32, bit-exact)."""
+    _require_gpu(x)
+    lib = _lib.load()
+    x = _contig(x, torch.float32, "x")
+    d = x.shape[-1]
+    y = torch.empty_like(x)
+    _lib.check("shard_fwht", lib.shard_fwht(_p(x), _p(y), x.numel() // d, d, _stream(x)))
+    return y
+
+
+def vq_prepare(v: torch.Tensor, group_size: int = 4):
+    """hadamard(fp32(v)) -> per-(bh, channel) abs max -> normalized subvectors.
+
+    v: (B, G, T, D) fp16 or a (bh, seq, D) view whose last two dims are
+    contiguous.  Returns (x (bh*seq*D/gs, gs) fp32, ch fp32 (bh, D), ch fp16)."""
+    _require_gpu(v)
+    lib = _lib.load()
+    if v.dtype != torch.float16:
+        raise TypeError("vq_prepare: v must be fp16")
+    D = v.shape[-1]
+    seq = v.shape[-2]
+    v3 = v.reshape(-1, seq, D) if v.dim() != 3 else v
+    if v3.stride(-1) != 1 or v3.stride(-2) != D:
+        v3 = v3.contiguous()
+    bh = v3.shape[0]
+    dev = v.device
+    x = torch.empty(bh * seq * D // group_size, group_size, dtype=torch.float32, device=dev)
+    ch32 = torch.empty(bh, D, dtype=torch.float32, device=dev)
+    ch16 = torch.empty(bh, D, dtype=torch.float16, device=dev)
+    ws = _workspace(lib.shard_vq_prepare_workspace(bh, D), dev)
+    _lib.check("shard_vq_prepare", lib.shard_vq_prepare(
+        _p(v3), bh, seq, D, v3.stride(0), _p(x), _p(ch32), _p(ch16), _p(ws), ws.numel(),
+        _stream(v)))
+    return x, ch32, ch16
+
+
+def vq_assign(x: torch.Tensor, centroids: torch.Tensor) -> torch.Tensor:
+    """argmin_k ||x - c_k||^2 (direct fp32 form, first index on ties) -> int32."""
+    _require_gpu(x, centroids)
+    lib = _lib.load()
+    x = _contig(x, torch.float32, "x")
+    c = _contig(centroids, torch.float32, "centroids")
+    n, d = x.shape
+    idx = torch.empty(n, dtype=torch.int32, device=x.device)
+    _lib.check("shard_vq_assign", lib.shard_vq_assign(
+        _p(x), n, d, _p(c), c.shape[0], _p(idx), _stream(x)))
+    return idx
+
+
+def kmeans_update(x: torch.Tensor, idx: torch.Tensor, centroids: torch.Tensor, ws=None):
+    """One deterministic k-means update; returns (new_centroids, max_delta (1,) fp32)."""
+    _require_gpu(x, idx, centroids)
+    lib = _lib.load()
+    x = _contig(x, torch.float32, "x")
+    idx = _contig(idx, torch.int32, "idx")
+    c = _contig(centroids, torch.float32, "centroids")
+    n, d = x.shape
+    k = c.shape[0]
+    newc = torch.empty_like(c)
+    maxd = torch.empty(1, dtype=torch.float32, device=x.device)
+    need = lib.shard_kmeans_update_workspace(n, k)
+    if ws is None or ws.numel() < need:
+        ws = _workspace(need, x.device)
+    _lib.check("shard_kmeans_update", lib.shard_kmeans_update(
+        _p(x), n, d, _p(idx), _p(c), k, _p(newc), _p(maxd), _p(ws), ws.numel(), _stream(x)))
+    return newc, maxd
+
+
+def kmeans(data: torch.Tensor, k: int, n_iter: int = 30, seed: int = 42):
+    """k-means of cache.py:21-39 on the GPU: CPU-generator randperm init, then
+    assign (shard_vq_assign) + deterministic update per iteration; stops like the
+    reference (max |delta| < 1e-4 once it >= 5) and returns the last assignment
+    (made against the pre-update centroids) with the final centroids."""
+    n, d = data.shape
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    perm = torch.randperm(n, generator=g)[:k].to(data.device)
+    centroids = data[perm].clone()
+    lib = _lib.load()
+    ws = _workspace(lib.shard_kmeans_update_workspace(n, centroids.shape[0]), data.device)
+    idx = None
+    deltas = []
+    for it in range(n_iter):
+        idx = vq_assign(data, centroids)
+        new, maxd = kmeans_update(data, idx, centroids, ws)
+        deltas.append(maxd)
+        # one host sync per iteration, as the reference's .item() (cache.py:36)
+        if it >= 5 and maxd.item() < 1e-4:
+            centroids = new
+            break
+        centroids = new
+    return centroids, idx
+
+
+# ---------------------------------------------------------------------------
+# decode stream
+# ---------------------------------------------------------------------------
+def stream_quant(x: torch.Tensor, signs: torch.Tensor, codebook: torch.Tensor):
+    """Per-token Lloyd-Max quantizer; x (..., D) fp16 -> (idx u8 (..., D), norm fp16 (...))."""
+    _require_gpu(x, signs, codebook)
+    lib = _lib.load()
+    x = _contig(x, torch.float16, "x")
+    D = x.shape[-1]
+    rows = x.numel() // D
+    idx = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    norm = torch.empty(x.shape[:-1], dtype=torch.float16, device=x.device)
+    stream_quant_into(x, signs, codebook, idx, norm)
+    return idx, norm
+
+
+def stream_quant_into(x, signs, codebook, idx_out, norm_out):
+    lib = _lib.load()
+    D = x.shape[-1]
+    rows = x.numel() // D
+    _lib.check("shard_stream_quant", lib.shard_stream_quant(
+        _p(x), rows, D, _p(signs), _p(codebook), codebook.numel(), _p(idx_out), _p(norm_out),
+        _stream(x)))
+
+
+def stream_dequant(idx: torch.Tensor, norm: torch.Tensor, signs: torch.Tensor,
+                   codebook: torch.Tensor) -> torch.Tensor:
+    """fp16(fp16(H(cb[idx]) * signs) * norm) for (..., D) codes."""
+    _require_gpu(idx, norm, signs, codebook)
+    lib = _lib.load()
+    idx = _contig(idx, torch.uint8, "idx")
+    norm = _contig(norm, torch.float16, "norm")
+    D = idx.shape[-1]
+    y = torch.empty(idx.shape, dtype=torch.float16, device=idx.device)
+    _lib.check("shard_stream_dequant", lib.shard_stream_dequant(
+        _p(idx), _p(norm), idx.numel() // D, D, _p(signs), _p(codebook), _p(y), _stream(idx)))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# decode attention
+# ---------------------------------------------------------------------------
+class DecodeCall:
+    """Holds the ctypes argument block and the tensors it points to."""
+
+    def __init__(self, args: DecodeArgs, keep_alive: list):
+        self.args = args
+        self.keep = keep_alive
+
+
+def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
+                     stream_n=0, decode_kv=None) -> DecodeCall:
+    """Build shard_decode_args for one layer.
+
+    q (B, H, D) fp16 (post-RoPE); ``fmt`` is the layer's device format dict
+    (see cache.CompressedLayerFormat); decode_kv = (dec_k, dec_v) fp16
+    (B, G, S, D) or None."""
+    _require_gpu(q)
+    B, H, D = q.shape
+    if tuple(fmt["v_centroids_f16"].shape) != (256, 4):
+        raise ValueError("decode kernel needs a (256, 4) VQ codebook")
+    if q.dtype != torch.float16 or not q.is_contiguous():
+        raise TypeError("q must be contiguous fp16 (B, H, D)")
+    keep = [q]
+    a = DecodeArgs()
+    a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim = B, H, fmt["n_kv"], D
+    a.rank, a.n_comp = fmt["rank_pad"], fmt["n_compress"]
+    a.compress_start, a.pos_q = fmt["compress_start"], int(pos_q)
+    inv_freq = fmt["inv_freq_dev"] if inv_freq is None else inv_freq
+    for name, t in (("q", q), ("inv_freq", inv_freq), ("k_coeffs", fmt["k_coeffs_pad"]),
+                    ("k_coeff_scale", fmt["k_coeff_scale_pad"]), ("k_basis", fmt["k_basis_pad"]),
+                    ("k_mean", fmt["k_mean_f16"]), ("v_idx", fmt["v_indices"]),
+                    ("v_codebook", fmt["v_centroids_f16"]), ("v_ch", fmt["v_ch_f16"]),
+                    ("sink_k", fmt["sink_k"]), ("sink_v", fmt["sink_v"]),
+                    ("win_k", fmt["win_k"]), ("win_v", fmt["win_v"])):
+        setattr(a, name, t.data_ptr())
+        keep.append(t)
+    a.n_sink = fmt["sink_k"].shape[2]
+    a.n_win = fmt["win_k"].shape[2]
+    if decode_kv is not None:
+        dk, dv = decode_kv
+        a.dec_k, a.dec_v = dk.data_ptr(), dv.data_ptr()
+        a.n_dec, a.dec_stride = dk.shape[2], dk.shape[2]
+        keep += [dk, dv]
+    if stream_n > 0:
+        for name, key in (("s_kidx", "k_idx_buf"), ("s_vidx", "v_idx_buf"),
+                          ("s_knorm", "k_norm_buf"), ("s_vnorm", "v_norm_buf"),
+                          ("s_signs", "signs"), ("s_codebook", "stream_codebook")):
+            setattr(a, name, fmt[key].data_ptr())
+            keep.append(fmt[key])
+        a.n_stream = stream_n
+    if mask is not None:
+        m = mask.reshape(B, -1)
+        n_total = (a.n_sink + a.n_comp + a.n_win + a.n_dec + a.n_stream)
+        if m.shape[1] < n_total:
+            raise ValueError(f"attention mask covers {m.shape[1]} keys, the cache holds {n_total}")
+        if m.dtype != torch.float32:
+            m = m.float()
+        if m.stride(-1) != 1:
+            m = m.contiguous()
+        a.mask, a.mask_stride = m.data_ptr(), m.stride(0)
+        keep.append(m)
+    if out is None:
+        out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
+    a.out = out.data_ptr()
+    keep.append(out)
+    a.n_splits = int(n_splits)
+    return DecodeCall(a, keep)
+
+
+def decode_attn(call: DecodeCall, ws: torch.Tensor = None) -> torch.Tensor:
+    lib = _lib.load()
+    q = call.keep[0]
+    need = lib.shard_decode_attn_workspace(ctypes.byref(call.args))
+    if ws is None or ws.numel() < need:
+        ws = _workspace(need, q.device)
+    _lib.check("shard_decode_attn", lib.shard_decode_attn(
+        ctypes.byref(call.args), _p(ws), ws.numel(), _stream(q)))
+    return call.keep[-1]
+
+
+def decode_workspace_bytes(call: DecodeCall) -> int:
+    return int(_lib.load().shard_decode_attn_workspace(ctypes.byref(call.args)))
+
+
+def kv_reconstruct(fmt, batch: int):
+    """Full fp16 K (RoPE re-applied) and V of the compressed segment: (B, G, n, D)."""
+    lib = _lib.load()
+    dev = fmt["k_coeffs"].device
+    B, G, n, D = batch, fmt["n_kv"], fmt["n_compress"], fmt["head_dim"]
+    q_dummy = torch.empty(B, G * 4, D, dtype=torch.float16, device=dev)
+    call = make_decode_args(q_dummy, fmt, 0, None)
+    call.args.k_coeffs = fmt["k_coeffs"].data_ptr()
+    call.args.k_coeff_scale = fmt["k_coeff_scale"].data_ptr()
+    call.args.k_basis = fmt["k_basis_f16"].data_ptr()
+    call.args.rank = fmt["rank"]
+    k_out = torch.empty(B, G, n, D, dtype=torch.float16, device=dev)
+    v_out = torch.empty(B, G, n, D, dtype=torch.float16, device=dev)
+    _lib.check("shard_kv_reconstruct", lib.shard_kv_reconstruct(
+        ctypes.byref(call.args), _p(k_out), _p(v_out), _stream(k_out)))
+    return k_out, v_out

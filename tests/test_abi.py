@@ -1,0 +1,54 @@
+"""The C ABI: libshard_hip.so loads on the CPU host and exports every entry
+point include/shard_hip.h declares, with the struct layout the binding uses.
+No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    src = open(os.path.join(ROOT, "include", "shard_hip.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"\b(shard_[a-z0-9_]+)\s*\(", src)
+    return sorted(set(names))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for must in ("shard_decode_attn", "shard_stream_quant", "shard_pca_project",
+                 "shard_int4_quant_pack", "shard_fwht", "shard_vq_assign", "shard_kv_reconstruct"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from shard_amd import _lib
+    lib = _lib.load()
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(raw, name), f"{name} declared in shard_hip.h but not exported"
+    bound = {n for n, _, _ in _lib.SIGNATURES}
+    assert set(declared_functions()) <= bound, "binding misses a declared entry point"
+    assert lib.shard_version().startswith(b"shard_hip")
+    assert lib.shard_decode_args_size() == ctypes.sizeof(_lib.DecodeArgs)
+
+
+def test_argument_errors_without_gpu_work():
+    """Bad arguments are rejected on the host before any launch."""
+    from shard_amd import _lib
+    lib = _lib.load()
+    assert lib.shard_fwht(None, None, 10, 128, None) == -1
+    assert lib.shard_pca_project(None, 1, 16, 16, None, 32, None, 32, None) == -1
+    assert lib.shard_decode_attn(None, None, 0, None) == -1
+    args = _lib.DecodeArgs()
+    assert lib.shard_decode_attn_workspace(ctypes.byref(args)) == 0
+
+
+def test_cpu_tensor_is_rejected_loudly():
+    import torch
+    from shard_amd import ops
+    with pytest.raises(ops.ShardHipUnavailable):
+        ops.fwht(torch.zeros(4, 128))

@@ -1,0 +1,128 @@
+"""GPU parity of the fused decode-attention kernel.
+
+Bar (from the north star): max-abs-err <= 2e-3 and cosine >= 0.9999 against the
+fp64 evaluation of the reference's math over the same stored representation
+(oracle/exact.py).  Inputs are built on the CPU (seeded) and uploaded, so the
+kernel and the oracle see identical bits."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import exact, ref
+from tests.helpers import compare, random_layer, to_device
+
+pytestmark = pytest.mark.gpu
+
+TOL_ABS = 2e-3
+TOL_COS = 0.9999
+
+
+def _run(cuda, gc, inv, q, pos_q, mask=None, n_splits=0, nkv=8):
+    from shard_amd import ops
+    d = to_device(gc, cuda, inv, nkv=nkv)
+    B = gc["batch"]
+    stream_n = gc.get("stream_n", 0) // B
+    dec = (d["decode_k"], d["decode_v"]) if "decode_k" in d else None
+    m = None if mask is None else torch.from_numpy(mask).to(cuda)
+    call = ops.make_decode_args(q.to(cuda).reshape(B, -1, 128), d, pos_q, None, mask=m,
+                                n_splits=n_splits, stream_n=stream_n, decode_kv=dec)
+    out = ops.decode_attn(call)
+    torch.cuda.synchronize()
+    return out.cpu().float().numpy().reshape(B, -1, 1, 128)
+
+
+CASES = [
+    # (B, nkv, rank, n_comp, sink, win, n_stream, n_dec)
+    (1, 8, 192, 1980, 4, 64, 0, 0),      # config-1 shape (T = 2048)
+    (1, 8, 192, 8124, 4, 64, 0, 0),      # config-2 shape (T = 8192)
+    (1, 8, 192, 1980, 4, 64, 37, 0),     # with an 8-bit stream
+    (1, 8, 128, 517, 4, 64, 0, 5),       # fp16 decode tokens, rank 128, ragged tile
+    (2, 8, 192, 300, 4, 64, 3, 0),       # batch 2
+    (1, 2, 64, 33, 2, 3, 1, 0),          # tiny, 2 kv heads
+    (1, 8, 96, 1, 4, 64, 0, 0),          # a single compressed token
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
+def test_decode_matches_exact_oracle(cuda, case):
+    B, nkv, rank, n_comp, sink, win, n_stream, n_dec = case
+    gc, inv = random_layer(B=B, nkv=nkv, rank=rank, n_comp=n_comp, sink=sink, win=win,
+                           n_stream=n_stream, n_dec=n_dec, seed=n_comp + rank)
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(B, 4 * nkv, 1, 128, generator=g).half()
+    pos_q = sink + n_comp + win + n_dec + n_stream - 1
+    want = exact.decode_attention(q.numpy(), gc, nkv, pos_q, inv.numpy())
+    got = _run(cuda, gc, inv, q, pos_q, nkv=nkv)
+    err, cos = compare(got, want)
+    print(f"case={case} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= TOL_ABS and cos >= TOL_COS
+
+
+def test_decode_rank_padding_and_splits(cuda):
+    """rank 100 (padded to 128 on the device) and several explicit split counts."""
+    gc, inv = random_layer(rank=100, n_comp=1000, seed=5)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(2)).half()
+    pos_q = 4 + 1000 + 64 - 1
+    want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    for ns in (8, 16, 64, 200):
+        got = _run(cuda, gc, inv, q, pos_q, n_splits=ns)
+        err, cos = compare(got, want)
+        assert err <= TOL_ABS and cos >= TOL_COS, (ns, err, cos)
+
+
+def test_decode_additive_mask(cuda):
+    gc, inv = random_layer(n_comp=700, n_stream=4, seed=8)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(3)).half()
+    T = 4 + 700 + 64 + 4
+    mask = np.zeros((1, T), np.float32)
+    rng = np.random.default_rng(0)
+    mask[0, rng.choice(T, 50, replace=False)] = -65504.0   # HF fp16 masked entries
+    mask[0, rng.choice(T, 50, replace=False)] = 0.5
+    want = exact.decode_attention(q.numpy(), gc, 8, T - 1, inv.numpy(), attn_mask=mask)
+    got = _run(cuda, gc, inv, q, T - 1, mask=mask)
+    err, cos = compare(got, want)
+    assert err <= TOL_ABS and cos >= TOL_COS
+
+
+def test_decode_vs_reference_golden(cuda, golden):
+    """The reference's own CPU output on its stub cache (fp16 intermediates)."""
+    from tests.test_oracle import _gc_from_fixture
+    f = golden("fused_attn.npz")
+    gc, nkv = _gc_from_fixture(f)
+    gc["v_idx_full"] = gc["v_idx_full"].reshape(1, nkv, gc["n_compress"], 32)
+    inv = torch.from_numpy(f["inv_freq"])
+    got = _run(cuda, gc, inv, torch.from_numpy(f["q_rope"]), int(f["pos_q"]), nkv=nkv)
+    want64 = exact.decode_attention(f["q_rope"], gc, nkv, int(f["pos_q"]), f["inv_freq"])
+    err, cos = compare(got, want64)
+    assert err <= TOL_ABS and cos >= TOL_COS
+    err_ref, cos_ref = compare(got, f["out"])
+    print(f"vs reference fp16 path: max_abs={err_ref:.3e} cos={cos_ref:.7f}")
+    assert err_ref <= 5e-3 and cos_ref >= 0.9999
+
+
+def test_decode_compressed_real_synthetic(cuda):
+    """Config-1 synthetic K/V compressed by the CPU oracle (PCA + DP bits + int4 +
+    k-means VQ), then decoded on the GPU."""
+    from shard_amd import bench_data
+    k, v = bench_data.make_kv(2048, seed=0)
+    inv = bench_data.inv_freq()
+    basis = bench_data.random_orthonormal_basis(rank=192, seed=0)
+    gc = ref.compress_layer(k, v, 0, inv, basis=basis)
+    q = bench_data.make_q(seed=0)
+    want = exact.decode_attention(q.numpy(), gc, 8, 2048, inv.numpy())
+    got = _run(cuda, gc, inv, q, 2048)
+    err, cos = compare(got, want)
+    print(f"synthetic T=2048: max_abs={err:.3e} cos={cos:.7f}")
+    assert err <= TOL_ABS and cos >= TOL_COS
+
+
+def test_kv_reconstruct(cuda):
+    """Unfused fp16 reconstruction (_ensure_dequant): V bit-exact, K within fp16 rounding."""
+    from shard_amd import ops
+    gc, inv = random_layer(B=2, rank=160, n_comp=300, seed=12)
+    d = to_device(gc, cuda, inv)
+    k_got, v_got = ops.kv_reconstruct(d, 2)
+    k_want, v_want = ref.reconstruct_kv(gc, 8, 128, inv)
+    assert np.array_equal(v_got.cpu().numpy().view(np.uint16), v_want.numpy().view(np.uint16))
+    kg, kw = k_got.cpu().float(), k_want.float()
+    assert float(((kg - kw).abs() / (kw.abs() + 1e-2)).max()) < 4e-3

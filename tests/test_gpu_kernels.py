@@ -1,0 +1,151 @@
+"""GPU parity of the integer/byte kernels against the CPU oracle (bit-exact),
+and of the MFMA projection GEMM against an fp64 product of the same fp16 inputs."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from shard_amd import ops
+    return ops
+
+
+@pytest.mark.parametrize("n,alloc", [
+    (5000, [4] * 64 + [2] * 64 + [8] * 64),
+    (777, [6] * 64 + [0] * 64 + [2] * 32),
+    (33, [8] * 10 + [4] * 6),
+    (1, [2] * 32),
+])
+def test_int4_quant_pack_bitexact(cuda, n, alloc):
+    ops = _ops()
+    keep = len(alloc)
+    rng = np.random.default_rng(n)
+    proj = (rng.standard_normal((n, keep)) * np.exp(-np.arange(keep) / 60.0)).astype(np.float32)
+    if n > 2:
+        proj[rng.integers(0, n, 3), rng.integers(0, keep, 3)] = 0.0
+    want = ref.k_code_chain(proj, alloc)
+    got = ops.int4_quant_pack(torch.from_numpy(proj).to(cuda),
+                              torch.tensor(alloc, dtype=torch.int32), want_codes=True)
+    assert np.array_equal(got["packed"].cpu().numpy(), want["packed"])
+    assert np.array_equal(got["coeff_scale"].cpu().numpy(), want["coeff_scale"])
+    assert np.array_equal(got["codes"].cpu().numpy(), want["codes"])
+    nz = np.array(alloc) > 0
+    assert np.array_equal(got["lo"].cpu().numpy()[nz], want["lo"][nz])
+    assert np.array_equal(got["rng"].cpu().numpy()[nz], want["rng"][nz])
+
+
+@pytest.mark.parametrize("rows", [1, 16, 4099])
+def test_stream_quant_bitexact(cuda, rows):
+    ops = _ops()
+    g = torch.Generator().manual_seed(rows)
+    x = (torch.randn(rows, 128, generator=g) * torch.rand(rows, 1, generator=g) * 6).half()
+    if rows > 3:
+        x[1] = 0          # norm clamp path
+        x[2, :5] = 60000  # large values
+    cb = ref.lloyd_max_codebook(128, 8)
+    signs = ref.stream_signs(11, 128)
+    want_idx, want_n = ref.quantize_stream_token(x.numpy(), signs, cb)
+    idx, nrm = ops.stream_quant(x.to(cuda), torch.from_numpy(signs).to(cuda),
+                                torch.from_numpy(cb).to(cuda))
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    assert np.array_equal(nrm.cpu().numpy().view(np.uint16), want_n.view(np.uint16))
+    y = ops.stream_dequant(idx, nrm, torch.from_numpy(signs).to(cuda), torch.from_numpy(cb).to(cuda))
+    want_y = ref.dequantize_stream_token(want_idx, want_n, signs, cb)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), want_y.view(np.uint16))
+
+
+@pytest.mark.parametrize("d", [16, 64, 128, 256])
+def test_fwht_bitexact(cuda, d):
+    ops = _ops()
+    x = torch.randn(1001, d) * 3
+    got = ops.fwht(x.to(cuda)).cpu().numpy()
+    assert np.array_equal(got, ref.hadamard_np(x.numpy()))
+    assert np.array_equal(got, ref.hadamard(x).numpy())
+
+
+def test_vq_prepare_bitexact(cuda):
+    ops = _ops()
+    g = torch.Generator().manual_seed(3)
+    B, G, T, D, start, end = 2, 8, 300, 128, 4, 236
+    v = torch.randn(B, G, T, D, generator=g).half()
+    v[:, :, :, 7] *= 8
+    vm = v[:, :, start:end, :].float().reshape(B * G, end - start, D)
+    rot = ref.hadamard(vm)
+    ch = rot.abs().amax(dim=1).clamp(min=1e-8)
+    want = (rot / ch.unsqueeze(1)).reshape(-1, 4)
+    x, ch32, ch16 = ops.vq_prepare(v.to(cuda)[:, :, start:end, :].reshape(B * G, end - start, D))
+    assert np.array_equal(ch32.cpu().numpy(), ch.numpy())
+    assert np.array_equal(ch16.cpu().numpy().view(np.uint16), ch.half().numpy().view(np.uint16))
+    assert np.array_equal(x.cpu().numpy(), want.numpy())
+
+
+def test_vq_assign_bitexact(cuda):
+    ops = _ops()
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(300001, 4, generator=g)
+    c = torch.randn(256, 4, generator=g)
+    got = ops.vq_assign(x.to(cuda), c.to(cuda)).cpu().numpy()
+    want = ref.vq_assign_direct(x.numpy(), c.numpy())
+    assert np.array_equal(got, want)
+    mism = int((got != ref.vq_assign_cdist(x, c).numpy()).sum())
+    assert mism == 0, f"{mism} rows differ from torch.cdist argmin"
+
+
+def test_kmeans_update_bitexact(cuda):
+    ops = _ops()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(70000, 4, generator=g)
+    c = x[torch.randperm(70000, generator=g)[:256]].clone()
+    c[17] = 100.0  # an empty cluster keeps its centroid
+    idx = torch.from_numpy(ref.vq_assign_direct(x.numpy(), c.numpy()))
+    new = torch.zeros_like(c)
+    cnt = torch.zeros(256)
+    new.index_add_(0, idx, x)
+    cnt.index_add_(0, idx, torch.ones(70000))
+    nz = cnt > 0
+    new[nz] /= cnt[nz].unsqueeze(1)
+    new[~nz] = c[~nz]
+    got, maxd = ops.kmeans_update(x.to(cuda), idx.to(torch.int32).to(cuda), c.to(cuda))
+    assert np.array_equal(got.cpu().numpy(), new.numpy())
+    assert maxd.item() == (new - c).abs().max().item()
+
+
+def test_kmeans_matches_reference_golden(cuda, golden):
+    ops = _ops()
+    gld = golden("kmeans.npz")
+    cent, idx = ops.kmeans(torch.from_numpy(gld["data"]).to(cuda), int(gld["k"]), int(gld["n_iter"]),
+                           int(gld["seed"]))
+    assert np.array_equal(cent.cpu().numpy(), gld["centroids"])
+    assert np.array_equal(idx.cpu().numpy().astype(np.int64), gld["idx"])
+
+
+@pytest.mark.parametrize("m,k,n", [(1000, 1024, 192), (4099, 1024, 64), (257, 512, 256), (31, 64, 32)])
+def test_pca_project_mfma(cuda, m, k, n):
+    ops = _ops()
+    g = torch.Generator().manual_seed(m)
+    a = torch.randn(m, k, generator=g).half()
+    bt = (torch.randn(n, k, generator=g) * 0.05).half()
+    got = ops.pca_project(a.to(cuda), bt.to(cuda)).cpu().double()
+    want = a.double() @ bt.double().T
+    scale = (a.double().abs() @ bt.double().abs().T)
+    assert float(((got - want).abs() / scale).max()) < 1e-5
+
+
+def test_k_prepare(cuda):
+    ops = _ops()
+    g = torch.Generator().manual_seed(2)
+    B, G, T, D, start, n_comp = 2, 8, 200, 128, 4, 132
+    k = torch.randn(B, G, T, D, generator=g).half()
+    inv = ref.default_inv_freq(500000.0, D)
+    pos = torch.arange(start, start + n_comp)
+    un = ref.undo_rope(k[:, :, start:start + n_comp].float(), pos, inv)
+    flat = un.permute(0, 2, 1, 3).reshape(B * n_comp, G * D)
+    mean = flat.mean(0)
+    want = (flat - mean).half().float()
+    got = ops.k_prepare(k.to(cuda), start, n_comp, inv.to(cuda), mean.to(cuda)).cpu().float()
+    # sin/cos may differ by an ulp from torch's CPU ones: allow one fp16 ulp
+    assert float((got - want).abs().max()) <= 2e-3 * float(want.abs().max())

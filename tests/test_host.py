@@ -1,0 +1,128 @@
+"""Host logic of shard_amd on the CPU: tables, HF Cache glue, the Llama patch
+and its fallbacks (forced from the host, no kernel launched)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref
+
+
+def test_dp_allocation_matches_oracle():
+    from shard_amd import host
+    rng = np.random.default_rng(0)
+    for trial in range(20):
+        d = int(rng.integers(2, 400))
+        var = np.sort(rng.exponential(1.0, d))[::-1].astype(np.float32) * rng.uniform(0.1, 100)
+        budget = int(rng.integers(16, 4096))
+        assert host.dp_bit_allocation(torch.from_numpy(var.copy()), budget) == \
+            ref.dp_bit_allocation(torch.from_numpy(var.copy()), budget)
+
+
+def test_lloyd_max_and_signs(golden):
+    from shard_amd import host
+    assert np.array_equal(host.lloyd_max_codebook(128, 8).numpy(), golden("lloyd_max.npz")["codebook"])
+    for layer in (0, 1, 31):
+        assert np.array_equal(host.stream_signs(layer, 128).numpy(), ref.stream_signs(layer, 128))
+
+
+def test_cache_constructs_and_prefill_glue():
+    import shard
+    from shard_amd import Cache
+    assert shard.Cache is Cache
+    c = Cache(num_layers=2)
+    assert len(c.layers) == 2 and c.get_seq_length() == 0
+    k = torch.randn(1, 8, 100, 128).half()
+    v = torch.randn(1, 8, 100, 128).half()
+    kk, vv = c.update(k, v, 0)
+    assert kk is k and vv is v
+    assert c.get_seq_length(0) == 100
+    assert c.layers[0].get_mask_sizes(1) == (101, 0)
+    assert c.layers[0].get_max_length() == -1
+    assert c.memory_bytes() == 2 * k.numel() * 2
+    assert c.fp16_equivalent_bytes() == 100 * 8 * 128 * 4 * 2
+
+
+def test_compress_on_cpu_fails_loudly():
+    from shard_amd import Cache, ops
+    c = Cache(num_layers=1)
+    c.update(torch.randn(1, 8, 200, 128).half(), torch.randn(1, 8, 200, 128).half(), 0)
+    with pytest.raises(ops.ShardHipUnavailable):
+        c.update(torch.randn(1, 8, 1, 128).half(), torch.randn(1, 8, 1, 128).half(), 0)
+
+
+def test_short_prompt_skips_compression():
+    from shard_amd import Cache
+    c = Cache(num_layers=1)
+    c.update(torch.randn(1, 8, 60, 128), torch.randn(1, 8, 60, 128), 0)
+    k, v = c.update(torch.randn(1, 8, 1, 128), torch.randn(1, 8, 1, 128), 0)
+    assert k.shape[2] == 61 and c.layers[0]._gpu_compressed is None
+
+
+def _tiny_llama():
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                      max_position_embeddings=256, rope_theta=500000.0)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).eval()
+
+
+def test_llama_patch_falls_back_on_uncompressed_layers():
+    """Patched forward == original forward when no layer is compressed
+    (attention.py:359-368 routing), with both a DynamicCache and a shard Cache."""
+    from transformers import DynamicCache
+    from shard_amd import Cache, enable_llama_fused_attention
+    from shard_amd.host import get_rope_inv_freq
+    model = _tiny_llama()
+    ids = torch.randint(0, 64, (1, 20))
+    with torch.no_grad():
+        base = model(ids, past_key_values=DynamicCache(), use_cache=True).logits
+    assert enable_llama_fused_attention(model) is True
+    assert enable_llama_fused_attention(model) is True   # idempotent
+    with torch.no_grad():
+        patched = model(ids, past_key_values=DynamicCache(), use_cache=True).logits
+        c = Cache.from_model(model)
+        sh = model(ids, past_key_values=c, use_cache=True).logits
+    assert torch.equal(base, patched)
+    assert torch.allclose(base, sh)
+    assert torch.equal(get_rope_inv_freq(model), model.model.rotary_emb.inv_freq.float())
+    assert c.get_seq_length() == 20
+
+
+def test_full_fused_error_is_counted_then_default_path_runs(monkeypatch):
+    """A failing opt-in full-fused call is counted and the default path runs
+    (attention.py:386-403); forced from the host with stub layers."""
+    from shard_amd import attention
+    calls = []
+
+    def boom(*a, **k):
+        raise RuntimeError("forced")
+
+    def ok(q, layer, pos_q, inv, mask):
+        calls.append(pos_q)
+        return torch.zeros_like(q)
+
+    monkeypatch.setattr(attention, "fused_attention_compressed_full", boom)
+    monkeypatch.setattr(attention, "fused_attention_compressed", ok)
+    from shard_amd import Cache, enable_llama_fused_attention
+    model = _tiny_llama()
+    enable_llama_fused_attention(model)
+    c = Cache.from_model(model)
+    c._full_fused = True
+    for l in c.layers:
+        l._gpu_compressed = {"stub": True}
+        l._prefilled = True
+        l._seq_len = 10
+    c._compressed = True
+    c._streaming = False
+
+    def upd(self, k, v, *a, **kw):
+        self._seq_len += 1
+        return k, v
+    monkeypatch.setattr(type(c.layers[0]), "update", upd)
+    ids = torch.randint(0, 64, (1, 1))
+    with torch.no_grad():
+        model(ids, past_key_values=c, use_cache=True)
+    assert c._full_fused_attempts == 2 and c._full_fused_errors == 2
+    assert "forced" in c._last_full_fused_error
+    assert calls == [10, 10]

@@ -1,0 +1,279 @@
+"""Pins the CPU oracle (oracle/) against closed forms, library routines,
+brute force and the golden vectors of tests/golden (reference outputs)."""
+import itertools
+import math
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+from oracle import exact, ref
+
+
+# --------------------------------------------------------------------------
+# Hadamard: Sylvester closed form, involution, torch/numpy agreement
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("d", [2, 4, 8, 16, 32, 64, 128])
+def test_hadamard_matches_sylvester(d):
+    rng = np.random.default_rng(d)
+    x = rng.standard_normal((5, d)).astype(np.float32)
+    H = scipy.linalg.hadamard(d).astype(np.float64) / math.sqrt(d)
+    want = x.astype(np.float64) @ H.T
+    got = ref.hadamard(torch.from_numpy(x)).numpy()
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6 * math.sqrt(d))
+    np.testing.assert_allclose(exact.fwht64(x), want, rtol=0, atol=1e-12)
+
+
+def test_hadamard_involution_and_np_bitexact():
+    x = torch.randn(300, 128)
+    y = ref.hadamard(x)
+    np.testing.assert_allclose(ref.hadamard(y).numpy(), x.numpy(), atol=5e-6)
+    assert np.array_equal(ref.hadamard_np(x.numpy()), y.numpy())
+
+
+def test_sqrt_divisor_is_correctly_rounded():
+    # fp32(double sqrt(d)) equals the correctly rounded fp32 sqrt for the dims used
+    for d in (64, 128, 256):
+        assert np.float32(math.sqrt(d)) == np.sqrt(np.float32(d))
+
+
+# --------------------------------------------------------------------------
+# RoPE: rotation closed form, undo o reapply = id
+# --------------------------------------------------------------------------
+def test_rope_rotation_closed_form():
+    hd = 128
+    inv = ref.default_inv_freq(500000.0, hd)
+    pos = torch.arange(0, 50)
+    x = torch.randn(1, 2, 50, hd, dtype=torch.float64).float()
+    y = ref.reapply_rope(x, pos, inv)
+    ph = (pos.float()[:, None] * inv[None, :]).double()
+    c, s = ph.cos(), ph.sin()
+    x1, x2 = x[..., :64].double(), x[..., 64:].double()
+    want = torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
+    np.testing.assert_allclose(y.numpy(), want.numpy(), atol=2e-6)
+    back = ref.undo_rope(y, pos, inv)
+    np.testing.assert_allclose(back.numpy(), x.numpy(), atol=5e-6)
+
+
+# --------------------------------------------------------------------------
+# DP bit allocation: exhaustive enumeration
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("seed", range(6))
+def test_dp_allocation_is_optimal(seed):
+    rng = np.random.default_rng(seed)
+    ng = int(rng.integers(1, 4))
+    d = 64 * ng - int(rng.integers(0, 20))
+    var = np.sort(rng.exponential(1.0, d))[::-1].astype(np.float32) * 10
+    budget = int(rng.integers(64, 64 * 8 * ng))
+    alloc = ref.dp_bit_allocation(torch.from_numpy(var.copy()), budget)
+    sizes = [min(64, d - 64 * g) for g in range(ng)]
+    gv = [float(torch.from_numpy(var[64 * g: 64 * g + sizes[g]].copy()).sum()) for g in range(ng)]
+    units = budget // 16 + 1
+
+    def err(bits):
+        return sum(gv[g] * 4.0 if b == 0 else gv[g] / (3.0 * (1 << (2 * b))) for g, b in enumerate(bits))
+
+    def cost(bits):
+        return sum(0 if b == 0 else (sizes[g] * b + 15) // 16 for g, b in enumerate(bits))
+
+    best = min(err(bits) for bits in itertools.product([0, 2, 4, 6, 8], repeat=ng)
+               if cost(bits) <= units)
+    got_bits = [alloc[64 * g] for g in range(ng)]
+    assert all(alloc[64 * g + i] == got_bits[g] for g in range(ng) for i in range(sizes[g]))
+    assert cost(got_bits) <= units
+    assert err(got_bits) == pytest.approx(best, rel=1e-12)
+
+
+# --------------------------------------------------------------------------
+# Group quantizer + int4 chain: error bounds, ranges, packing relation
+# --------------------------------------------------------------------------
+def test_group_quant_error_bound():
+    rng = np.random.default_rng(0)
+    proj = (rng.standard_normal((777, 10)) * rng.uniform(0.1, 5, 10)).astype(np.float32)
+    alloc = [8, 8, 6, 6, 4, 4, 2, 2, 0, 0]
+    codes, lo, rng_ = ref.group_quant(proj, alloc)
+    deq = ref.group_dequant(codes, lo, rng_, alloc)
+    for c, b in enumerate(alloc):
+        if b == 0:
+            assert np.all(deq[:, c] == 0)
+            continue
+        L = (1 << b) - 1
+        assert codes[:, c].max() <= L
+        assert lo[c] == proj[:, c].min()
+        assert codes[np.argmin(proj[:, c]), c] == 0 and codes[np.argmax(proj[:, c]), c] == L
+        step = rng_[c] / L
+        assert np.max(np.abs(deq[:, c] - proj[:, c])) <= step / 2 * (1 + 1e-4) + 1e-6
+
+
+def test_int4_chain_pack_relation_and_roundtrip():
+    rng = np.random.default_rng(1)
+    y = (rng.standard_normal((301, 12)) * rng.uniform(0.1, 3, 12)).astype(np.float32)
+    q, cs = ref.int4_quantize(y)
+    assert q.min() >= -7 and q.max() <= 7
+    for c in range(y.shape[1]):
+        assert np.abs(q[:, c]).max() == 7
+        ok = np.abs(y[:, c] / cs[c]) <= 7
+        assert np.all(np.abs(q[ok, c] * cs[c] - y[ok, c]) <= cs[c] / 2 * (1 + 1e-5))
+    packed = ref.int4_pack(q)
+    flat = (q.astype(np.int16) + 8).astype(np.uint8).reshape(-1)   # kernel_test.py:140-143
+    if flat.size % 2:
+        flat = np.concatenate([flat, np.zeros(1, np.uint8)])
+    assert np.array_equal(packed, flat[0::2] | (flat[1::2] << 4))
+    assert np.array_equal(ref.int4_unpack(packed, *q.shape), q)
+
+
+# --------------------------------------------------------------------------
+# Lloyd-Max codebook and the stream quantizer
+# --------------------------------------------------------------------------
+def test_lloyd_max_matches_reference_golden(golden):
+    g = golden("lloyd_max.npz")
+    cb = ref.lloyd_max_codebook(128, 8)
+    assert cb.dtype == np.float32 and np.array_equal(cb, g["codebook"])
+
+
+def test_lloyd_max_is_near_fixed_point():
+    cb = ref.lloyd_max_codebook(128, 8).astype(np.float64)
+    assert np.all(np.diff(cb) > 0)
+    np.testing.assert_allclose(cb, -cb[::-1], atol=1e-7)          # symmetric
+    # centroid condition E[X | cell] for N(0, 1/128) holds to ~1e-3 relative
+    from scipy.stats import norm
+    s = 1 / math.sqrt(128)
+    b = np.concatenate([[-np.inf], (cb[1:] + cb[:-1]) / 2, [np.inf]]) / s
+    m = norm.cdf(b[1:]) - norm.cdf(b[:-1])
+    cond = (norm.pdf(b[:-1]) - norm.pdf(b[1:])) * s / m
+    assert np.max(np.abs(cond - cb)[16:-16]) < 2e-3 * s
+
+
+def test_norm_order_matches_torch():
+    x = (torch.randn(20000, 128) * 4).half().float()
+    assert np.array_equal(ref.norm_fp32_8lane(x.numpy()), x.norm(dim=-1).numpy())
+
+
+def test_stream_quant_is_nearest_code():
+    cb = ref.lloyd_max_codebook(128, 8)
+    signs = ref.stream_signs(3, 128)
+    x = (torch.randn(2000, 128) * 2).half().numpy()
+    idx, nrm = ref.quantize_stream_token(x, signs, cb)
+    t = x.astype(np.float64)
+    n = np.maximum(np.sqrt((t * t).sum(-1)), 1e-8)
+    import scipy.linalg as sl
+    H = sl.hadamard(128) / math.sqrt(128)
+    r = ((t / n[:, None]) * signs) @ H.T
+    d = np.abs(r[..., None] - cb.astype(np.float64)[None, None, :])
+    best = d.argmin(-1)
+    srt = np.sort(d, axis=-1)
+    clear = (srt[..., 1] - srt[..., 0]) > 1e-6
+    assert np.array_equal(idx[clear], best[clear])
+    np.testing.assert_allclose(nrm.astype(np.float64), n, rtol=1e-3)
+    # dequantized tokens reproduce the inputs (tails beyond the last level clip)
+    y = ref.dequantize_stream_token(idx, nrm, signs, cb).astype(np.float64)
+    cos = (y * t).sum(-1) / (np.linalg.norm(y, axis=-1) * n)
+    assert cos.mean() > 0.9999 and cos.min() > 0.99
+
+
+# --------------------------------------------------------------------------
+# VQ assignment and k-means
+# --------------------------------------------------------------------------
+def test_vq_assign_direct_matches_cdist_and_fp64():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(20000, 4, generator=g)
+    c = torch.randn(256, 4, generator=g)
+    direct = ref.vq_assign_direct(x.numpy(), c.numpy())
+    cd = ref.vq_assign_cdist(x, c).numpy()
+    d64 = ((x.double()[:, None, :] - c.double()[None]) ** 2).sum(-1).argmin(1).numpy()
+    assert np.array_equal(direct, cd)
+    assert np.array_equal(direct, d64)
+
+
+def test_kmeans_matches_reference_golden(golden):
+    g = golden("kmeans.npz")
+    cent, idx = ref.kmeans(torch.from_numpy(g["data"]), int(g["k"]), int(g["n_iter"]), int(g["seed"]))
+    assert np.array_equal(cent.numpy(), g["centroids"])
+    assert np.array_equal(idx.numpy(), g["idx"])
+
+
+def test_kmeans_direct_assign_equals_cdist_assign(golden):
+    g = golden("kmeans.npz")
+    data = torch.from_numpy(g["data"])
+    direct = lambda x, c: torch.from_numpy(ref.vq_assign_direct(x.numpy(), c.numpy()))
+    c1, i1 = ref.kmeans(data, 16, 30, 42, assign=direct)
+    assert np.array_equal(c1.numpy(), g["centroids"]) and np.array_equal(i1.numpy(), g["idx"])
+
+
+# --------------------------------------------------------------------------
+# Attention: relative-delta identity and the reference's fused path
+# --------------------------------------------------------------------------
+def _gc_from_fixture(f):
+    rank, n_comp, start = int(f["rank"]), int(f["n_comp"]), int(f["start"])
+    nkv = f["sink_k"].shape[1]
+    basis_q = torch.from_numpy(f["k_basis_q"])
+    bs = torch.from_numpy(f["k_basis_scale"])
+    idx = torch.from_numpy(f["v_idx"])
+    gc = {
+        "k_coeffs": torch.from_numpy(f["k_coeffs"]), "k_coeffs_shape": (n_comp, rank),
+        "k_coeff_scale": torch.from_numpy(f["k_coeff_scale"]),
+        "k_basis_q": basis_q, "k_basis_scale": bs,
+        "k_basis_f16": (basis_q.to(torch.float16) * bs.to(torch.float16)).contiguous(),
+        "k_mean": torch.from_numpy(f["k_mean"]), "k_mean_f16": torch.from_numpy(f["k_mean"]),
+        "v_qdata": {"centroids": torch.from_numpy(f["centroids"]), "idx": idx,
+                    "ch_maxabs": torch.from_numpy(f["ch"]), "shape": (nkv, n_comp, 128),
+                    "group_size": 4},
+        "v_idx_full": idx.view(1, nkv, n_comp, 32),
+        "v_centroids_f16": torch.from_numpy(f["centroids"]),
+        "v_ch_f16": torch.from_numpy(f["ch"]).view(1, nkv, 128),
+        "sink_k": torch.from_numpy(f["sink_k"]), "sink_v": torch.from_numpy(f["sink_v"]),
+        "win_k": torch.from_numpy(f["win_k"]), "win_v": torch.from_numpy(f["win_v"]),
+        "n_compress": n_comp, "batch": 1, "compress_start": start,
+        "signs": f["signs"], "stream_codebook": ref.lloyd_max_codebook(128, 8),
+        "stream_n": f["s_kidx"].shape[0],
+        "k_idx_buf": f["s_kidx"], "v_idx_buf": f["s_vidx"],
+        "k_norm_buf": f["s_knorm"], "v_norm_buf": f["s_vnorm"],
+    }
+    return gc, nkv
+
+
+def test_reference_fused_path_matches_golden(golden):
+    f = golden("fused_attn.npz")
+    gc, nkv = _gc_from_fixture(f)
+    out = ref.fused_attention_compressed(torch.from_numpy(f["q_rope"]), gc, nkv, int(f["pos_q"]),
+                                         torch.from_numpy(f["inv_freq"]))
+    np.testing.assert_allclose(out.float().numpy(), f["out"].astype(np.float32), atol=2e-3, rtol=0)
+
+
+def test_exact_oracle_close_to_reference_fused_path(golden):
+    f = golden("fused_attn.npz")
+    gc, nkv = _gc_from_fixture(f)
+    out = exact.decode_attention(f["q_rope"], gc, nkv, int(f["pos_q"]), f["inv_freq"])
+    g = f["out"].astype(np.float64)
+    assert np.max(np.abs(out - g)) < 5e-3          # the reference's fp16 intermediates
+    cos = (out * g).sum() / (np.linalg.norm(out) * np.linalg.norm(g))
+    assert cos > 0.9999
+
+
+def test_relative_delta_identity_against_reapplied_rope(golden):
+    """exact.decode_attention's compressed scores equal q_rope . RoPE(k_n, pos_t)
+    computed by brute force (reconstruct, reapply RoPE, dot)."""
+    f = golden("fused_attn.npz")
+    gc, nkv = _gc_from_fixture(f)
+    q = f["q_rope"].astype(np.float64)
+    pos_q = int(f["pos_q"])
+    inv = f["inv_freq"]
+    _, parts = exact.decode_attention(q, gc, nkv, pos_q, inv, return_parts=True)
+    kn = exact.keys_norope(gc, nkv, 128)                      # (1, nkv, n, 128)
+    n = gc["n_compress"]
+    pos = np.arange(gc["compress_start"], gc["compress_start"] + n)
+    ph = (pos[:, None] * inv[None, :].astype(np.float64))
+    c, s = np.cos(ph), np.sin(ph)
+    k1, k2 = kn[..., :64], kn[..., 64:]
+    krope = np.concatenate([k1 * c - k2 * s, k2 * c + k1 * s], -1)
+    krope = np.repeat(krope, 4, axis=1)
+    qph = pos_q * inv.astype(np.float64)
+    brute = np.einsum("bhd,bhkd->bhk", q[:, :, 0], krope) / math.sqrt(128)
+    got = parts["scores"][..., 4:4 + n]
+    np.testing.assert_allclose(got, brute, atol=1e-4)
+    # a wrong sign of the sin term would break the identity
+    bad = np.concatenate([k1 * c + k2 * s, k2 * c - k1 * s], -1)
+    bad = np.einsum("bhd,bhkd->bhk", q[:, :, 0], np.repeat(bad, 4, axis=1)) / math.sqrt(128)
+    assert np.max(np.abs(bad - got)) > 1e-2
+    del qph
