@@ -70,7 +70,12 @@ def build_layer(T, dev, seed=0, n_stream=0):
     return fmt, k, v
 
 
-def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0):
+def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, graph_len=100):
+    """Per-call time of shard_decode_attn, rotating over n_copies of the layer.
+
+    The calls are captured in a HIP graph (graph_len calls per graph, each call
+    on the next copy) and the graph is replayed, so the host's per-launch cost
+    is not part of the measurement.  Returns (us rotated, us hot, us eager)."""
     from shard_amd import ops
     copies = [fmt] + [clone_format(fmt) for _ in range(n_copies - 1)]
     calls = [ops.make_decode_args(q, c, pos_q, None, n_splits=n_splits, stream_n=stream_n)
@@ -81,40 +86,80 @@ def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0):
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    # eager launches from Python (host-bound at these kernel sizes)
     e0.record(st)
-    for i in range(steps):
+    for i in range(min(steps, 200)):
         ops.decode_attn(calls[i % n_copies], ws)
     e1.record(st)
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / steps
-    # hot: the same copy every launch (cache-resident)
-    e0.record(st)
-    for i in range(steps):
-        ops.decode_attn(calls[0], ws)
-    e1.record(st)
-    torch.cuda.synchronize()
-    us_hot = e0.elapsed_time(e1) * 1000.0 / steps
-    return us, us_hot, calls[0].keep[-1]
+    us_eager = e0.elapsed_time(e1) * 1000.0 / min(steps, 200)
+
+    def graph_of(idx_fn):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(graph_len):       # one eager pass on the capture stream
+                ops.decode_attn(calls[idx_fn(i)], ws)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(graph_len):
+                ops.decode_attn(calls[idx_fn(i)], ws)
+        torch.cuda.synchronize()
+        return g
+
+    reps = max(1, steps // graph_len)
+    res = []
+    for idx_fn in (lambda i: i % n_copies, lambda i: 0):
+        g = graph_of(idx_fn)
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(reps):
+            g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        res.append(e0.elapsed_time(e1) * 1000.0 / (reps * graph_len))
+        del g
+    return res[0], res[1], us_eager
 
 
-def time_sdpa(k, v, q, steps, warmup, dev):
-    """fp16 uncompressed decode attention on the same K/V (torch SDPA, GQA)."""
+def time_sdpa(k, v, q, steps, warmup, dev, graph_len=50):
+    """fp16 uncompressed decode attention on the same K/V (torch SDPA with GQA),
+    rotating over copies and replayed from a HIP graph like the compressed call."""
     import torch.nn.functional as F
     T = k.shape[2]
     n_copies = max(1, math.ceil(512e6 / (2 * k.numel() * 2)))
     ks = [k.to(dev) for _ in range(n_copies)]
     vs = [v.to(dev) for _ in range(n_copies)]
     qq = q.to(dev)
-    for i in range(warmup):
-        F.scaled_dot_product_attention(qq, ks[i % n_copies], vs[i % n_copies], enable_gqa=True)
+
+    def call(i):
+        return F.scaled_dot_product_attention(qq, ks[i % n_copies], vs[i % n_copies], enable_gqa=True)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(max(warmup, graph_len)):
+            call(i)
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(graph_len):
+            call(i)
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // graph_len)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(steps):
-        F.scaled_dot_product_attention(qq, ks[i % n_copies], vs[i % n_copies], enable_gqa=True)
+    for _ in range(reps):
+        g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / steps, 2 * T * 8 * 128 * 2
+    return e0.elapsed_time(e1) * 1000.0 / (reps * graph_len), 2 * T * 8 * 128 * 2
 
 
 def cpu_baseline(fmt, q, pos_q, inv, budget_s=15.0):
@@ -174,8 +219,10 @@ def main():
         q = bench_data.make_q().to(dev).view(1, 32, 128)
         nbytes = algorithmic_bytes(n, rank)
         n_copies = max(2, math.ceil(2 * 256e6 / nbytes))
-        us, us_hot, _ = time_decode(fmt, q, T, args.steps, args.warmup, n_copies, args.n_splits)
+        us, us_hot, us_eager = time_decode(fmt, q, T, args.steps, args.warmup, n_copies,
+                                           args.n_splits)
         res = {"T": T, "n_comp": n, "rank": fmt["rank"], "us": us, "us_hot": us_hot,
+               "us_eager": us_eager,
                "bytes": nbytes, "flops": algorithmic_flops(n, rank), "copies": n_copies}
         if with_baselines:
             res["sdpa_us"], res["sdpa_bytes"] = time_sdpa(k, v, q.view(1, 32, 1, 128),
@@ -206,6 +253,7 @@ def main():
                    "rotated_copies": r8["copies"]},
         "achieved_hbm_gbs": round(gbs, 1),
         "us_hot": round(r8["us_hot"], 3),
+        "us_eager_python_launch": round(r8["us_eager"], 3),
         "fp16_sdpa_us": round(r8["sdpa_us"], 3),
         "speedup_vs_fp16_sdpa": round(r8["sdpa_us"] / us, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
@@ -217,6 +265,7 @@ def main():
     if r32 is not None:
         g32 = r32["bytes"] / (r32["us"] * 1e-6) / 1e9
         out["at_32k"] = {"us": round(r32["us"], 3), "us_hot": round(r32["us_hot"], 3),
+                         "us_eager_python_launch": round(r32["us_eager"], 3),
                          "achieved_hbm_gbs": round(g32, 1), "frac": round(g32 / HBM_PEAK_GBS, 4),
                          "n_comp": r32["n_comp"], "rank": r32["rank"]}
     if not args.no_cpu:

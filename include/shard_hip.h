@@ -130,10 +130,13 @@ int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx
  *   t = fp32(x); n = max(||t||, 1e-8) with torch-CPU's 8-lane summation order;
  *   r = hadamard(t / n * signs); idx = bucketize(r, codebook) clamped, then the
  *   nearer of (idx-1, idx) by |cb - r| in fp32 (ties to idx); norm = fp16(n).
+ * Optional `deq` (nullable, (rows, hd) fp16) receives the token as the
+ * reference dequantizes it, fp16(fp16(hadamard(cb[idx]) * signs) * norm)
+ * (cache.py:275-278, streaming.py:74-79), bit-exact.
  * x: (rows, hd) fp16 contiguous, hd in {64, 128, 256}; codebook sorted, n_codes <= 256. */
 int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd,
                        const float* signs, const float* codebook, int32_t n_codes,
-                       uint8_t* idx, uint16_t* norm, void* stream);
+                       uint8_t* idx, uint16_t* norm, uint16_t* deq, void* stream);
 
 /* Stream dequantizer, bit-exact with _dequant_stream / dequantize_per_token
  * (cache.py:275-278, streaming.py:74-79, qjl off):
@@ -157,8 +160,9 @@ int shard_stream_dequant(const uint8_t* idx, const uint16_t* norm, int64_t rows,
  *   v_ch         (B, G, D) fp16
  *   sink_k/v     (B, G, n_sink, D) fp16;  win_k/v (B, G, n_win, D) fp16
  *   dec_k/v      (B, G, dec_stride, D) fp16, first n_dec tokens valid
- *   s_kidx/s_vidx (>= n_stream, B, G, D) uint8; s_knorm/s_vnorm (>= n_stream, B, G) fp16
- *   s_signs      (D) fp32;  s_codebook (256) fp32
+ *   s_k/s_v      (>= n_stream, B, G, D) fp16: the 8-bit stream tokens as the
+ *                reference dequantizes them (cache.py:275-278), written by
+ *                shard_stream_quant's `deq` output when each token is appended
  *   mask         additive fp32, row b at mask + b*mask_stride, indexed in the
  *                reference's concatenation order [sink, comp, win, dec, stream]
  *                (nullable)
@@ -177,6 +181,7 @@ typedef struct shard_decode_args {
   const uint16_t* k_coeff_scale;
   const uint16_t* k_basis;
   const uint16_t* k_mean;
+  const void* prep;          /* shard_decode_prepare output of this layer */
   const uint8_t* v_idx;
   const uint16_t* v_codebook;
   const uint16_t* v_ch;
@@ -189,12 +194,8 @@ typedef struct shard_decode_args {
   const uint16_t* dec_k;
   const uint16_t* dec_v;
   int32_t n_dec, dec_stride;
-  const uint8_t* s_kidx;
-  const uint8_t* s_vidx;
-  const uint16_t* s_knorm;
-  const uint16_t* s_vnorm;
-  const float* s_signs;
-  const float* s_codebook;
+  const uint16_t* s_k;
+  const uint16_t* s_v;
   int32_t n_stream, _pad0;
   const float* mask;
   int64_t mask_stride;
@@ -202,6 +203,18 @@ typedef struct shard_decode_args {
   int32_t n_splits; /* 0 = choose automatically */
   int32_t _pad1;
 } shard_decode_args;
+
+/* Per-layer constant operands of shard_decode_attn, computed once after a
+ * layer is compressed (they depend only on its basis, scales, mean and RoPE
+ * frequencies): the MFMA operand image of fp16(k_basis * k_coeff_scale) with
+ * the mean folded in, and the in-tile RoPE rotation tables.  `out` holds
+ * shard_decode_prepare_bytes(n_kv_heads, rank) bytes and is passed to
+ * shard_decode_attn as args->prep.  rank % 32 == 0, rank <= 192. */
+size_t shard_decode_prepare_bytes(int32_t n_kv_heads, int32_t rank);
+int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
+                         const uint16_t* k_mean, const float* inv_freq, int32_t n_kv_heads,
+                         int32_t head_dim, int32_t rank, void* out, size_t out_bytes,
+                         void* stream);
 
 size_t shard_decode_attn_workspace(const shard_decode_args* args);
 int shard_decode_attn(const shard_decode_args* args, void* workspace,

@@ -33,13 +33,13 @@ class DecodeArgs(ctypes.Structure):
         ("batch", c_int32), ("n_q_heads", c_int32), ("n_kv_heads", c_int32), ("head_dim", c_int32),
         ("rank", c_int32), ("n_comp", c_int32), ("compress_start", c_int32), ("pos_q", c_int32),
         ("q", c_void_p), ("inv_freq", c_void_p), ("k_coeffs", c_void_p), ("k_coeff_scale", c_void_p),
-        ("k_basis", c_void_p), ("k_mean", c_void_p), ("v_idx", c_void_p), ("v_codebook", c_void_p),
+        ("k_basis", c_void_p), ("k_mean", c_void_p), ("prep", c_void_p), ("v_idx", c_void_p),
+        ("v_codebook", c_void_p),
         ("v_ch", c_void_p),
         ("sink_k", c_void_p), ("sink_v", c_void_p), ("n_sink", c_int32),
         ("win_k", c_void_p), ("win_v", c_void_p), ("n_win", c_int32),
         ("dec_k", c_void_p), ("dec_v", c_void_p), ("n_dec", c_int32), ("dec_stride", c_int32),
-        ("s_kidx", c_void_p), ("s_vidx", c_void_p), ("s_knorm", c_void_p), ("s_vnorm", c_void_p),
-        ("s_signs", c_void_p), ("s_codebook", c_void_p), ("n_stream", c_int32), ("_pad0", c_int32),
+        ("s_k", c_void_p), ("s_v", c_void_p), ("n_stream", c_int32), ("_pad0", c_int32),
         ("mask", c_void_p), ("mask_stride", c_int64),
         ("out", c_void_p), ("n_splits", c_int32), ("_pad1", c_int32),
     ]
@@ -60,7 +60,9 @@ SIGNATURES = [
     ("shard_vq_assign", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     ("shard_kmeans_update_workspace", c_size_t, [c_int64, c_int32]),
     ("shard_kmeans_update", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
-    ("shard_stream_quant", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
+    ("shard_stream_quant", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("shard_decode_prepare_bytes", c_size_t, [c_int32, c_int32]),
+    ("shard_decode_prepare", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
     ("shard_decode_attn_workspace", c_size_t, [ctypes.POINTER(DecodeArgs)]),
     ("shard_decode_attn", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
     ("shard_kv_reconstruct", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_void_p, c_void_p]),

@@ -27,7 +27,7 @@ PER_FILE = {
     "quant.hip": ["-ffp-contract=off"],
     "decode_attn.hip": [],
     "pca.hip": [],
-    "reconstruct.hip": [],
+    "reconstruct.hip": ["-ffp-contract=off"],
     "abi.hip": [],
 }
 

@@ -181,14 +181,18 @@ class CacheLayer(CacheLayerMixin):
         vib = _ensure("v_idx", (B, G, D), torch.uint8)
         knb = _ensure("k_norm", (B, G), torch.float16)
         vnb = _ensure("v_norm", (B, G), torch.float16)
+        # fp16 tokens as the reference dequantizes them (cache.py:275-278), written
+        # once at append time and read by the decode kernel (runtime scratch)
+        kdb = _ensure("k_deq", (B, G, D), torch.float16)
+        vdb = _ensure("v_deq", (B, G, D), torch.float16)
         kx = k.reshape(B, G, D)
         vx = v.reshape(B, G, D)
         if not kx.is_contiguous():
             kx = kx.contiguous()
         if not vx.is_contiguous():
             vx = vx.contiguous()
-        ops.stream_quant_into(kx, gc["signs"], gc["stream_codebook"], kib[s], knb[s])
-        ops.stream_quant_into(vx, gc["signs"], gc["stream_codebook"], vib[s], vnb[s])
+        ops.stream_quant_into(kx, gc["signs"], gc["stream_codebook"], kib[s], knb[s], kdb[s])
+        ops.stream_quant_into(vx, gc["signs"], gc["stream_codebook"], vib[s], vnb[s], vdb[s])
         gc["stream_n"] = gc.get("stream_n", 0) + B
 
     def _dequant_stream(self, gc, B, nkv=None, hd=None):
@@ -196,10 +200,8 @@ class CacheLayer(CacheLayerMixin):
         if n == 0 or "k_idx_buf" not in gc:
             return None, None
         s = n // B
-        sk = ops.stream_dequant(gc["k_idx_buf"][:s], gc["k_norm_buf"][:s], gc["signs"],
-                                gc["stream_codebook"])
-        sv = ops.stream_dequant(gc["v_idx_buf"][:s], gc["v_norm_buf"][:s], gc["signs"],
-                                gc["stream_codebook"])
+        sk = gc["k_deq_buf"][:s]
+        sv = gc["v_deq_buf"][:s]
         return sk.permute(1, 2, 0, 3).contiguous(), sv.permute(1, 2, 0, 3).contiguous()
 
     # -- HF Cache API glue (cache.py:281-292; TF 5.x additions) ----------------
@@ -317,7 +319,7 @@ class Cache(HFCache):
                 bpv = self._stream_bits / 8.0
                 for k in ("k_idx_buf", "v_idx_buf"):
                     total += int(gc[k][:s].nelement() * bpv)
-                for k in ("k_norm_buf", "v_norm_buf"):
+                for k in ("k_norm_buf", "v_norm_buf", "k_deq_buf", "v_deq_buf"):
                     total += _nb(gc[k][:s])
         if has_gc:
             return total
@@ -490,3 +492,4 @@ def finalize_format(gc: dict, inv_freq, dev):
     if inv_freq is None:
         inv_freq = torch.zeros(gc["head_dim"] // 2)
     gc["inv_freq_dev"] = inv_freq.to(dev, torch.float32).contiguous()
+    gc["decode_prep"] = ops.decode_prepare(gc)

@@ -46,6 +46,20 @@ __device__ __forceinline__ float ord2f(uint32_t u) {
   return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
 }
 
+// x * s for s = +-1 as a sign-bit flip: exact, and keeps the sign of zero
+// (-1 * +0 = -0), which a multiply lowered to fma(x, s, +0) would lose.
+__device__ __forceinline__ float mul_sign(float x, float s) {
+  return __uint_as_float(__float_as_uint(x) ^ (__float_as_uint(s) & 0x80000000u));
+}
+
+// fp16(x) of an fp32 value that must be rounded exactly once from this very
+// register: the empty asm keeps the compiler from folding the producing
+// multiply into a mixed-precision fma with a +0 addend (which turns -0 into +0).
+__device__ __forceinline__ uint16_t f2h_opaque(float x) {
+  asm volatile("" : "+v"(x));
+  return f2h(x);
+}
+
 // IEEE fp32 ops with explicit rounding (no contraction into FMA).
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 __device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }

@@ -1,6 +1,6 @@
 // Fused decode attention over Shard's compressed KV cache, written for gfx950.
 //
-// Work split (one launch + one combine launch per layer-step):
+// Work split (one split launch + one combine launch per layer-step):
 //   split kernel   grid = (n_splits * n_kv/NB, B); a 256-thread workgroup owns
 //                  NB kv heads x a chunk of compressed tokens.  Wave w owns the
 //                  16 RoPE pairs [16w, 16w+16) of each of its NB heads, so the
@@ -9,11 +9,13 @@
 //     1. no-RoPE keys are rebuilt on chip with MFMA 32x32x16 f16:
 //          K_n[rows, tok] = Basis'[rows, r] . coef[r, tok] + mean
 //        Basis' = fp16(basis_f16 * coeff_scale) lives in VGPRs for the whole
-//        kernel; coef are the packed nibbles (128-bit loads) turned into exact
-//        fp16 integers n-8 with a magic-number trick.  Keys never reach HBM.
-//     2. each (c, d) pair is rotated by phi = fl32(fl32(pos_t - pos_q) * theta_i)
-//        (the relative-delta RoPE identity, attention.py:3-6) and dotted with
+//        kernel; coef are the packed nibbles (128-bit loads, prefetched one
+//        tile ahead) turned into exact fp16 integers n-8 with a magic-number
+//        trick; the accumulators start from the mean (LDS).  Keys never reach HBM.
+//     2. each (c, d) pair is rotated by phi = (pos_t - pos_q) * theta_i (the
+//        relative-delta RoPE identity, attention.py:3-6) and dotted with
 //        q_n = undo-RoPE(q, pos_q) by a second MFMA (rows = query heads).
+//        sin/cos(phi) advance by one fixed rotation per 32-token tile.
 //     3. the 4 waves' partial scores are summed in LDS, online softmax (fp32,
 //        base-2), and the VQ values sum_t p_t * cb[idx_t] (rotated space) are
 //        accumulated with the fp32 codebook in LDS.
@@ -21,17 +23,18 @@
 //        accumulator go to the workspace.
 //   combine kernel grid = (n_kv, B): merges the splits, applies ch and ONE
 //                  inverse Hadamard to the VQ accumulator, adds the fp16 sink /
-//                  window / decode segments and the 8-bit stream (dequantized
-//                  bit-exactly like cache.py:243-279), normalizes, writes fp16.
+//                  window / decode tokens and the dequantized 8-bit stream
+//                  tokens, normalizes, writes fp16.
 #include "common.h"
 
 namespace shard {
 
 constexpr int kThreads = 256;
-constexpr int kTile = 32;      // tokens per MFMA tile
-constexpr int kHD = 128;       // head_dim
-constexpr int kGQA = 4;        // query heads per kv head
+constexpr int kTile = 32;         // tokens per MFMA tile
+constexpr int kHD = 128;          // head_dim
+constexpr int kGQA = 4;           // query heads per kv head
 constexpr int kMaxExtra = 2048;   // sink + window + decode + stream tokens per call
+constexpr int kMaxSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct SplitParams {
@@ -39,9 +42,8 @@ struct SplitParams {
   const uint16_t* q;
   const float* inv_freq;
   const uint8_t* coef;
-  const uint16_t* cs;
-  const uint16_t* basis;
-  const uint16_t* mean;
+  const uint4* op;          // per-layer A operands (k_decode_prepare)
+  const float2* rope;       // per-layer rotation tables (k_decode_prepare)
   const uint8_t* vidx;
   const uint16_t* vcb;
   const float* mask;
@@ -54,12 +56,21 @@ struct SplitParams {
 
 // 8 packed nibbles (n0 in bits 0-3 ... n7 in bits 28-31) -> 8 exact fp16 values
 // n-8 in element order (n0, n4, n1, n5, n2, n6, n3, n7).
+// (x & m) | (y & ~m) in one VALU op; the compiler would emit and + or for
+// literal masks (a three-operand op takes one literal at most).
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(x), "v"(y));
+  return r;
+}
+
 __device__ __forceinline__ half8 nib8_to_half8(uint32_t x) {
   const uint32_t x8 = x >> 8;
-  const uint32_t v0 = (x & 0x000F000Fu) | 0x64006400u;   // 1024 + n0 | 1024 + n4
-  const uint32_t v1 = (x & 0x00F000F0u) | 0x64006400u;   // 1024 + 16 n1 | 1024 + 16 n5
-  const uint32_t v2 = (x8 & 0x000F000Fu) | 0x64006400u;  // 1024 + n2 | 1024 + n6
-  const uint32_t v3 = (x8 & 0x00F000F0u) | 0x64006400u;  // 1024 + 16 n3 | 1024 + 16 n7
+  const uint32_t m0 = 0x000F000Fu, m1 = 0x00F000F0u, magic = 0x64006400u;
+  const uint32_t v0 = bfi(m0, x, magic);    // 1024 + n0 | 1024 + n4
+  const uint32_t v1 = bfi(m1, x, magic);    // 1024 + 16 n1 | 1024 + 16 n5
+  const uint32_t v2 = bfi(m0, x8, magic);   // 1024 + n2 | 1024 + n6
+  const uint32_t v3 = bfi(m1, x8, magic);   // 1024 + 16 n3 | 1024 + 16 n7
   const half2v k1032 = {(half_t)1032.f, (half_t)1032.f};
   const half2v k16 = {(half_t)0.0625f, (half_t)0.0625f};
   const half2v k72 = {(half_t)72.f, (half_t)72.f};
@@ -73,7 +84,8 @@ __device__ __forceinline__ half8 nib8_to_half8(uint32_t x) {
   return r;
 }
 
-__device__ __forceinline__ int nib_perm(int e) { return ((e & 1) << 2) | (e >> 1); }
+// element e of a converted dword holds nibble nib_perm(e)
+__device__ __forceinline__ constexpr int nib_perm(int e) { return ((e & 1) << 2) | (e >> 1); }
 
 // Wave-local row rho (0..31) of the MFMA tile -> head dim: rows 0..15 are the
 // first components c of pairs 16P+rho, rows 16..31 the second components d.
@@ -81,17 +93,88 @@ __device__ __forceinline__ int row_dim(int P, int rho) {
   return rho < 16 ? 16 * P + rho : 64 + 16 * P + (rho - 16);
 }
 
+template <int KS>
+__device__ __forceinline__ void load_coef(const uint8_t* rowp, bool valid, uint32_t (&cw)[KS]) {
+  if (valid) {
+    if constexpr (KS % 4 == 0) {
+#pragma unroll
+      for (int s = 0; s < KS; s += 4) {
+        const uint4 v = *(const uint4*)(rowp + 4 * s);
+        cw[s] = v.x; cw[s + 1] = v.y; cw[s + 2] = v.z; cw[s + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; s += 2) {
+        const uint2 v = *(const uint2*)(rowp + 4 * s);
+        cw[s] = v.x; cw[s + 1] = v.y;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) cw[s] = 0x88888888u;  // nibble 8 -> coefficient 0
+  }
+}
+
+// Per-layer constant operands (shard_decode_prepare), in HBM after compression:
+//   op   uint4 [G][4 P][KS+1][64 lanes]: the MFMA A operand of wave P of head g,
+//        k-steps 0..KS-1 = fp16(basis * coeff_scale) in the nibble order of the
+//        coefficient dwords, k-step KS = the fp16 mean in element 0 of the lanes
+//        of the first half (paired with a constant 1 operand), so the key
+//        accumulators start at zero;
+//   rope float2 [32][64] = (cos, sin)(col * theta_i) for the token column inside
+//        a tile, then float2 [64] = (cos, sin)(32 * theta_i), the per-tile step.
+__global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint16_t* __restrict__ cs,
+                                 const uint16_t* __restrict__ mean, const float* __restrict__ inv_freq,
+                                 int G, int rank, uint4* __restrict__ op, float2* __restrict__ rope) {
+  const int KS = rank / 16;
+  const int64_t n_op = (int64_t)G * 4 * (KS + 1) * 64;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_op + 32 * 64 + 64; i += stride) {
+    if (i < n_op) {
+      const int lane = (int)(i % 64);
+      const int s = (int)((i / 64) % (KS + 1));
+      const int P = (int)((i / (64 * (KS + 1))) % 4);
+      const int g = (int)(i / (64 * (KS + 1) * 4));
+      const int col = lane & 31, hh = lane >> 5;
+      const int row = g * kHD + row_dim(P, col);
+      half8 v;
+      if (s < KS) {
+        const int r0 = 8 * (KS * hh + s);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = r0 + nib_perm(e);
+          v[e] = (half_t)(h2f(basis[(int64_t)row * rank + r]) * h2f(cs[r]));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (half_t)0.f;
+        if (hh == 0) v[0] = __builtin_bit_cast(half_t, mean[row]);
+      }
+      op[i] = __builtin_bit_cast(uint4, v);
+    } else {
+      const int k = (int)(i - n_op);
+      float sn, cn;
+      if (k < 32 * 64) sincosf((float)(k / 64) * inv_freq[k % 64], &sn, &cn);
+      else sincosf((float)kTile * inv_freq[k - 32 * 64], &sn, &cn);
+      rope[k] = make_float2(cn, sn);
+    }
+  }
+}
+
 template <int KS, int NB>
 __global__ __launch_bounds__(kThreads, 1)
 void k_decode_split(const SplitParams p) {
   constexpr int NQ = kGQA * NB;          // query heads of this workgroup
   constexpr int TS = 8 / NB;             // token subsets of the V stage
+  constexpr int VT = kTile / TS;         // tokens per V-stage thread per tile
   constexpr int SPT = (NQ * kTile + kThreads - 1) / kThreads;
 
   __shared__ __align__(16) float sp[4][NQ][kTile];   // per-wave partial scores
-  __shared__ __align__(16) float pp[kTile][NQ];      // softmax numerators of the tile
+  __shared__ __align__(16) half_t pp16[NQ][kTile];   // softmax numerators of the tile (fp16)
   __shared__ __align__(16) float alpha_s[NQ];        // rescale factors of the tile
-  __shared__ __align__(16) float4 cbl[256];          // VQ codebook in fp32
+  __shared__ __align__(16) uint2 cbl[256];           // VQ codebook (4 x fp16 per entry)
+  __shared__ __align__(16) float2 phq[64];           // (cos, sin)(pos_q * theta_i)
+  __shared__ __align__(16) float2 phb[64];           // (cos, sin)(delta of the chunk start)
   __shared__ __align__(16) float red[kThreads][16];  // end-of-chunk reduction
 
   const int tid = threadIdx.x;
@@ -113,47 +196,55 @@ void k_decode_split(const SplitParams p) {
   int t_end = t_begin + p.chunk;
   if (t_end > p.n_comp) t_end = p.n_comp;
 
-  for (int i = tid; i < 256; i += kThreads) {
-    const uint16_t* c4 = p.vcb + 4 * i;
-    cbl[i] = make_float4(h2f(c4[0]), h2f(c4[1]), h2f(c4[2]), h2f(c4[3]));
-  }
+  // ---- first tile's loads go out before the setup work.  Token indices are
+  // clamped to the chunk (no divergent loads); rows past the chunk end get
+  // -inf scores and zero weights.
+  const int64_t coef_row_bytes = p.rank / 2;
+  const int rowb = KS * 4;  // bytes per lane-half of a coefficient row
+  const uint8_t* coef_b = p.coef + (int64_t)b * p.n_comp * coef_row_bytes + rowb * hh;
+  const int vG = tid & 31;
+  const int vts = (tid >> 5) % TS;
+  const int vj = (tid >> 5) / TS;
+  const int vg = hg * NB + vj;
+  const uint8_t* vidx_b = p.vidx + (((int64_t)b * p.G + vg) * p.n_comp) * 32 + vG;
+  const int t_last = t_end > t_begin ? t_end - 1 : t_begin;
+  auto load_tile = [&](int t0, uint32_t (&cw_)[KS], uint32_t (&vc_)[VT]) {
+    const int tc = min(t0 + col, t_last);
+    load_coef<KS>(coef_b + (int64_t)tc * coef_row_bytes, true, cw_);
+#pragma unroll
+    for (int m = 0; m < VT; ++m) vc_[m] = vidx_b[(int64_t)min(t0 + VT * vts + m, t_last) * 32];
+  };
+  uint32_t cwA[KS], vcA[VT], cwB[KS], vcB[VT];
+  if (t_begin < t_end) load_tile(t_begin, cwA, vcA);
 
-  // ---- lane constants: pairs, theta, basis A-operand, mean C-init, q_n A-operand
+  // ---- per-layer constant operands: coalesced 16-byte loads
+  half8 Ab[NB][KS + 1];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const uint4* opp = p.op + ((int64_t)((hg * NB + j) * 4 + P) * (KS + 1)) * 64 + lane;
+#pragma unroll
+    for (int s = 0; s <= KS; ++s) Ab[j][s] = __builtin_bit_cast(half8, opp[s * 64]);
+  }
   int pr[8];
-  float th[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) pr[i] = 16 * P + 8 * (i >> 2) + 4 * hh + (i & 3);
+  float2 rc[8], rs[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    pr[i] = 16 * P + 8 * (i >> 2) + 4 * hh + (i & 3);
-    th[i] = p.inv_freq[pr[i]];
+    rc[i] = p.rope[col * 64 + pr[i]];      // (cos, sin)(col * theta)
+    rs[i] = p.rope[32 * 64 + pr[i]];       // (cos, sin)(32 * theta)
   }
 
-  half8 Ab[NB][KS];
-  float16v meanC[NB];
-  {
-    const int rho = col;
-    const int dim = row_dim(P, rho);
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int g = hg * NB + j;
-      const uint16_t* brow = p.basis + (int64_t)(g * kHD + dim) * p.rank;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int r0 = 8 * (KS * hh + s);
-        half8 v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int r = r0 + nib_perm(e);
-          v[e] = (half_t)(h2f(brow[r]) * h2f(p.cs[r]));
-        }
-        Ab[j][s] = v;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int rho_i = 8 * (i >> 2) + 4 * hh + (i & 3);
-        meanC[j][i] = h2f(p.mean[g * kHD + row_dim(P, rho_i)]);
-      }
-    }
+  for (int i = tid; i < 256; i += kThreads) cbl[i] = *(const uint2*)(p.vcb + 4 * i);
+  if (tid < 128) {
+    const int i = tid & 63;
+    const float th = p.inv_freq[i];
+    const float x = tid < 64 ? (float)p.pos_q * th : (float)(p.cstart + t_begin - p.pos_q) * th;
+    float sn, cn;
+    sincosf(x, &sn, &cn);
+    (tid < 64 ? phq : phb)[i] = make_float2(cn, sn);
   }
+  __syncthreads();
 
   // q_n = undo-RoPE(q_rope, pos_q): a = q_lo cos + q_hi sin, b = q_hi cos - q_lo sin
   half8 Aq[NB][2];
@@ -163,15 +254,21 @@ void k_decode_split(const SplitParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) { a_[i] = 0.f; b_[i] = 0.f; }
     if (qr < NQ) {
-      const int qh = hg * NQ + qr;
-      const uint16_t* qv = p.q + ((int64_t)b * p.H + qh) * kHD;
+      const uint16_t* qv = p.q + ((int64_t)b * p.H + hg * NQ + qr) * kHD;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float sn, cs;
-        sincosf((float)p.pos_q * th[i], &sn, &cs);
-        const float lo = h2f(qv[pr[i]]), hi = h2f(qv[pr[i] + 64]);
-        a_[i] = lo * cs + hi * sn;
-        b_[i] = hi * cs - lo * sn;
+      for (int jj = 0; jj < 2; ++jj) {
+        const int d0 = 16 * P + 8 * jj + 4 * hh;
+        const uint2 lo4 = *(const uint2*)(qv + d0), hi4 = *(const uint2*)(qv + d0 + 64);
+        const half2v l0 = __builtin_bit_cast(half2v, lo4.x), l1 = __builtin_bit_cast(half2v, lo4.y);
+        const half2v h0 = __builtin_bit_cast(half2v, hi4.x), h1 = __builtin_bit_cast(half2v, hi4.y);
+        const float lo[4] = {(float)l0[0], (float)l0[1], (float)l1[0], (float)l1[1]};
+        const float hi[4] = {(float)h0[0], (float)h0[1], (float)h1[0], (float)h1[1]};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float2 cq = phq[pr[4 * jj + m]];
+          a_[4 * jj + m] = lo[m] * cq.x + hi[m] * cq.y;
+          b_[4 * jj + m] = hi[m] * cq.x - lo[m] * cq.y;
+        }
       }
     }
 #pragma unroll
@@ -185,88 +282,68 @@ void k_decode_split(const SplitParams p) {
     }
   }
 
+  // ---- relative phase of this lane's token at the first tile:
+  // phi = delta(chunk start) * theta + col * theta; advanced by 32 theta per tile
+  float ph_c[8], ph_s[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float2 bb = phb[pr[i]];
+    ph_c[i] = bb.x * rc[i].x - bb.y * rc[i].y;
+    ph_s[i] = bb.y * rc[i].x + bb.x * rc[i].y;
+  }
+  half8 one8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) one8[e] = (half_t)0.f;
+  one8[0] = (half_t)(hh == 0 ? 1.f : 0.f);
+
   // ---- softmax-stage state (thread owns entries e = tid + 256*k)
   float m_run[SPT], l_part[SPT];
 #pragma unroll
   for (int k = 0; k < SPT; ++k) { m_run[k] = -INFINITY; l_part[k] = 0.f; }
   const float sc = kLog2e * rsqrtf((float)kHD);
 
-  // ---- V-stage mapping: tid = (j*TS + ts)*32 + G
-  const int vG = tid & 31;
-  const int vts = (tid >> 5) % TS;
-  const int vj = (tid >> 5) / TS;
-  const int vg = hg * NB + vj;
   float vacc[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int e = 0; e < 4; ++e) vacc[a][e] = 0.f;
 
-  const int rowb = KS * 4;  // bytes per lane-half of a coefficient row
-  const int64_t coef_row_bytes = p.rank / 2;
-  __syncthreads();
-
-  for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
-    const int t = t0 + col;
-    const bool tv = t < t_end;
-
-    // V-stage index prefetch (latency hidden by the key MFMAs)
-    uint8_t vcode[kTile / TS];
-#pragma unroll
-    for (int m = 0; m < kTile / TS; ++m) {
-      const int tt = t0 + vts + TS * m;
-      vcode[m] = tt < t_end ? p.vidx[(((int64_t)b * p.G + vg) * p.n_comp + tt) * 32 + vG] : 0;
-    }
-
-    // coefficient dwords of this lane: row (b, t), dwords [KS*hh, KS*hh+KS)
-    uint32_t cw[KS];
-    if (tv) {
-      const uint8_t* rowp = p.coef + ((int64_t)b * p.n_comp + t) * coef_row_bytes + rowb * hh;
-      if constexpr (KS % 4 == 0) {
-#pragma unroll
-        for (int s = 0; s < KS; s += 4) {
-          uint4 v = *(const uint4*)(rowp + 4 * s);
-          cw[s] = v.x; cw[s + 1] = v.y; cw[s + 2] = v.z; cw[s + 3] = v.w;
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < KS; s += 2) {
-          uint2 v = *(const uint2*)(rowp + 4 * s);
-          cw[s] = v.x; cw[s + 1] = v.y;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) cw[s] = 0x88888888u;  // nibble 8 -> 0
-    }
-
-    // 1. no-RoPE keys of NB heads for 32 tokens (rows x tokens, fp32)
+  auto tile = [&](const int t0, const uint32_t (&cw)[KS], const uint32_t (&vc)[VT]) {
+    // 1. no-RoPE keys of NB heads for 32 tokens (rows x tokens, fp32):
+    //    mean (k-step KS, times a constant 1) + basis . coefficients
     float16v acc[NB];
+    const float16v zero16 = {};
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[j][KS], one8, zero16, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const half8 bo = nib8_to_half8(cw[s]);
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[j][s], bo, s == 0 ? meanC[j] : acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[j][s], bo, acc[j], 0, 0, 0);
     }
 
     // 2. rotate pairs by phi(t, i), then dot with q_n on MFMA
-    float sn[8], cs[8];
-    const float delta = (float)(p.cstart + t - p.pos_q);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sincosf(delta * th[i], &sn[i], &cs[i]);
-    float16v sacc = {};
+    float16v sacc = zero16;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       half8 b0, b1;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float c = acc[j][i], d = acc[j][i + 8];
-        b0[i] = (half_t)(c * cs[i] - d * sn[i]);
-        b1[i] = (half_t)(d * cs[i] + c * sn[i]);
+        b0[i] = (half_t)(c * ph_c[i] - d * ph_s[i]);
+        b1[i] = (half_t)(d * ph_c[i] + c * ph_s[i]);
       }
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[j][0], b0, sacc, 0, 0, 0);
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[j][1], b1, sacc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float c = ph_c[i] * rs[i].x - ph_s[i] * rs[i].y;
+      const float s = ph_s[i] * rs[i].x + ph_c[i] * rs[i].y;
+      ph_c[i] = c;
+      ph_s[i] = s;
     }
     // rows of sacc: 8*(i/4) + 4*hh + (i%4) = query head; column = token col
 #pragma unroll
@@ -297,13 +374,14 @@ void k_decode_split(const SplitParams p) {
         const float pv = (s == -INFINITY) ? 0.f : exp2f(s - m_new);
         l_part[k] = l_part[k] * al + pv;
         m_run[k] = m_new;
-        pp[tt][qr] = pv;
+        pp16[qr][tt] = (half_t)pv;
         if (tt == 0) alpha_s[qr] = al;
       }
     }
     __syncthreads();
 
-    // 3b. VQ values: vacc[q][e] = alpha*vacc + sum_t p[q,t] * cb[idx[t,G]][e]
+    // 3b. VQ values (dot2 over token pairs, fp32 accumulation):
+    //     vacc[q][e] = alpha * vacc + sum_t p[q,t] * cb[idx[t,G]][e]
     {
       const float4 al4 = *(const float4*)&alpha_s[4 * vj];
       const float alv[4] = {al4.x, al4.y, al4.z, al4.w};
@@ -311,20 +389,38 @@ void k_decode_split(const SplitParams p) {
       for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int e = 0; e < 4; ++e) vacc[a][e] *= alv[a];
+      uint32_t pq[4][VT / 2];
 #pragma unroll
-      for (int m = 0; m < kTile / TS; ++m) {
-        const int tt = vts + TS * m;
-        const float4 c4 = cbl[vcode[m]];
-        const float4 p4 = *(const float4*)&pp[tt][4 * vj];
-        const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+      for (int a = 0; a < 4; ++a) {
+        const uint32_t* src = (const uint32_t*)&pp16[4 * vj + a][VT * vts];
+#pragma unroll
+        for (int u = 0; u < VT / 2; ++u) pq[a][u] = src[u];
+      }
+#pragma unroll
+      for (int u = 0; u < VT / 2; ++u) {
+        const uint2 ca = cbl[vc[2 * u]], cb = cbl[vc[2 * u + 1]];
+        half2v c2[4];
+        c2[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x05040100u));
+        c2[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x07060302u));
+        c2[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x05040100u));
+        c2[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x07060302u));
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-          vacc[a][0] += pv[a] * c4.x;
-          vacc[a][1] += pv[a] * c4.y;
-          vacc[a][2] += pv[a] * c4.z;
-          vacc[a][3] += pv[a] * c4.w;
+          const half2v p2 = __builtin_bit_cast(half2v, pq[a][u]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vacc[a][e] = __builtin_amdgcn_fdot2(p2, c2[e], vacc[a][e], false);
         }
       }
+    }
+  };
+
+  for (int t0 = t_begin; t0 < t_end; t0 += 2 * kTile) {
+    // ping-pong buffers: the next tile's loads are in flight during this tile
+    load_tile(t0 + kTile, cwB, vcB);
+    tile(t0, cwA, vcA);
+    if (t0 + kTile < t_end) {
+      load_tile(t0 + 2 * kTile, cwA, vcA);
+      tile(t0 + kTile, cwB, vcB);
     }
   }
 
@@ -365,7 +461,7 @@ void k_decode_split(const SplitParams p) {
 }
 
 // --------------------------------------------------------------------------
-// Combine: merge splits, fp16 segments and the 8-bit stream; one inverse FWHT.
+// Combine: merge splits, fp16 segments and the stream; one inverse FWHT.
 // --------------------------------------------------------------------------
 struct CombineParams {
   int32_t B, H, G, n_comp, n_splits;
@@ -377,10 +473,7 @@ struct CombineParams {
   int32_t n_win;
   const uint16_t *dec_k, *dec_v;
   int32_t n_dec, dec_stride;
-  const uint8_t *s_kidx, *s_vidx;
-  const uint16_t *s_knorm, *s_vnorm;
-  const float* s_signs;
-  const float* s_cb;
+  const uint16_t *s_k, *s_v;
   int32_t n_stream;
   const float* mask;
   int64_t mask_stride;
@@ -390,134 +483,135 @@ struct CombineParams {
   uint16_t* out;
 };
 
-// Butterflies over 128 values held as (lane, lane + 64); same pairing and
-// per-op rounding as hadamard() (cache.py:10-19).
-__device__ __forceinline__ void fwht128(float& x0, float& x1) {
+// Butterflies over 128 values held as (2l, 2l+1) in lane l (Sylvester order).
+__device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
   const int l = (int)lane_id();
-#pragma unroll
-  for (int h = 1; h < 64; h <<= 1) {
-    const float p0 = __shfl_xor(x0, h, 64), p1 = __shfl_xor(x1, h, 64);
-    x0 = (l & h) ? __fsub_rn(p0, x0) : __fadd_rn(x0, p0);
-    x1 = (l & h) ? __fsub_rn(p1, x1) : __fadd_rn(x1, p1);
+  {
+    const float a = x0, c = x1;
+    x0 = a + c;
+    x1 = a - c;
   }
-  const float a = x0, c = x1;
-  x0 = __fadd_rn(a, c);
-  x1 = __fsub_rn(a, c);
-  const float s = (float)sqrt(128.0);
-  x0 = __fdiv_rn(x0, s);
-  x1 = __fdiv_rn(x1, s);
-}
-
-// Stream token (K or V) as the reference dequantizes it (qjl off):
-// fp16(fp16(hadamard(cb[idx]) * signs) * norm), returned in fp32.
-__device__ __forceinline__ void stream_token(const uint8_t* idx, uint16_t norm_bits,
-                                             const float* cb, const float* signs, float& y0,
-                                             float& y1) {
-  const int l = (int)lane_id();
-  float x0 = cb[idx[l]], x1 = cb[idx[l + 64]];
-  fwht128(x0, x1);
-  const float n = h2f(norm_bits);
-  y0 = h2f(f2h(h2f(f2h(__fmul_rn(x0, signs[l]))) * n));
-  y1 = h2f(f2h(h2f(f2h(__fmul_rn(x1, signs[l + 64]))) * n));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  for (int hl = 1; hl < 64; hl <<= 1) {  // element stride 2*hl = lane stride hl
+    const float p0 = __shfl_xor(x0, hl, 64), p1 = __shfl_xor(x1, hl, 64);
+    x0 = (l & hl) ? p0 - x0 : x0 + p0;
+    x1 = (l & hl) ? p1 - x1 : x1 + p1;
+  }
+  const float s = 0.08838834764831845f;  // 1/sqrt(128)
+  x0 *= s;
+  x1 *= s;
 }
+
+// Row x of the extra tokens (sink, window, decode, stream) of kv head g, row b.
+__device__ __forceinline__ const uint16_t* extra_row(const CombineParams& p, int b, int g, int x,
+                                                     bool v, int* mask_pos) {
+  if (x < p.n_sink) {
+    *mask_pos = x;
+    return (v ? p.sink_v : p.sink_k) + (((int64_t)b * p.G + g) * p.n_sink + x) * kHD;
+  }
+  x -= p.n_sink;
+  if (x < p.n_win) {
+    *mask_pos = p.n_sink + p.n_comp + x;
+    return (v ? p.win_v : p.win_k) + (((int64_t)b * p.G + g) * p.n_win + x) * kHD;
+  }
+  x -= p.n_win;
+  if (x < p.n_dec) {
+    *mask_pos = p.n_sink + p.n_comp + p.n_win + x;
+    return (v ? p.dec_v : p.dec_k) + (((int64_t)b * p.G + g) * p.dec_stride + x) * kHD;
+  }
+  x -= p.n_dec;
+  *mask_pos = p.n_sink + p.n_comp + p.n_win + p.n_dec + x;
+  return (v ? p.s_v : p.s_k) + (((int64_t)x * p.B + b) * p.G + g) * kHD;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
-
-// Fetch extra token x (order: sink, window, decode, stream) of kv head g, row b.
-__device__ __forceinline__ void extra_kv(const CombineParams& p, int b, int g, int x, bool want_v,
-                                         const float* cb, const float* signs, float& y0,
-                                         float& y1, int& mask_pos) {
-  const int l = (int)lane_id();
-  const uint16_t* src = nullptr;
-  if (x < p.n_sink) {
-    src = (want_v ? p.sink_v : p.sink_k) + (((int64_t)b * p.G + g) * p.n_sink + x) * kHD;
-    mask_pos = x;
-  } else if ((x -= p.n_sink) < p.n_win) {
-    src = (want_v ? p.win_v : p.win_k) + (((int64_t)b * p.G + g) * p.n_win + x) * kHD;
-    mask_pos = p.n_sink + p.n_comp + x;
-  } else if ((x -= p.n_win) < p.n_dec) {
-    src = (want_v ? p.dec_v : p.dec_k) + (((int64_t)b * p.G + g) * p.dec_stride + x) * kHD;
-    mask_pos = p.n_sink + p.n_comp + p.n_win + x;
-  } else {
-    x -= p.n_dec;
-    mask_pos = p.n_sink + p.n_comp + p.n_win + p.n_dec + x;
-    const int64_t row = ((int64_t)x * p.B + b) * p.G + g;
-    stream_token((want_v ? p.s_vidx : p.s_kidx) + row * kHD,
-                 (want_v ? p.s_vnorm : p.s_knorm)[row], cb, signs, y0, y1);
-    return;
-  }
-  y0 = h2f(src[l]);
-  y1 = h2f(src[l + 64]);
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
 }
 
 __global__ __launch_bounds__(kThreads, 1)
 void k_decode_combine(const CombineParams p) {
-  __shared__ float sx[kGQA][kMaxExtra];
-  __shared__ float wsp[kGQA][1024];
-  __shared__ float cb[256];
-  __shared__ float sg[kHD];
+  __shared__ __align__(16) float qs[kGQA][kHD];
+  __shared__ __align__(16) float sx[kMaxExtra][kGQA];
+  __shared__ __align__(16) float wsp[kGQA][kMaxSplits];
+  __shared__ __align__(16) float red[4][kGQA][kHD];
   __shared__ float Ms[kGQA], Ls[kGQA];
-  __shared__ float red[4][kGQA][kHD];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = blockIdx.x, b = blockIdx.y;
   const int n_x = p.n_sink + p.n_win + p.n_dec + p.n_stream;
-  if (p.n_stream > 0) {
-    for (int i = tid; i < 256; i += kThreads) cb[i] = p.s_cb[i];
-    for (int i = tid; i < kHD; i += kThreads) sg[i] = p.s_signs[i];
-  }
+  for (int i = tid; i < kGQA * kHD; i += kThreads)
+    qs[i / kHD][i % kHD] = h2f(p.q[((int64_t)b * p.H + g * kGQA + i / kHD) * kHD + i % kHD]);
   __syncthreads();
 
-  const float inv_sqrt = 1.0f / sqrtf((float)kHD);
-  float q0[kGQA], q1[kGQA];
-#pragma unroll
-  for (int a = 0; a < kGQA; ++a) {
-    const uint16_t* qv = p.q + ((int64_t)b * p.H + g * kGQA + a) * kHD;
-    q0[a] = h2f(qv[lane]);
-    q1[a] = h2f(qv[lane + 64]);
-  }
-
-  // extra-token scores (natural log units, as the reference's fp32 scores)
-  for (int x = w; x < n_x; x += 4) {
-    float k0, k1;
+  // extra-token scores: 4 threads per token, 32 dims each, two shuffles
+  const float inv_sqrt = 0.08838834764831845f;  // 1/sqrt(128)
+  for (int x0 = 0; x0 < n_x; x0 += kThreads / 4) {
+    const int x = x0 + tid / 4, qd = tid & 3;
+    float d[kGQA] = {0.f, 0.f, 0.f, 0.f};
     int mpos = 0;
-    extra_kv(p, b, g, x, false, cb, sg, k0, k1, mpos);
-    const float madd = p.mask ? p.mask[(int64_t)b * p.mask_stride + mpos] : 0.f;
+    if (x < n_x) {
+      const uint4* kr = (const uint4*)(extra_row(p, b, g, x, false, &mpos) + 32 * qd);
+      uint4 kv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kv[c] = kr[c];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const half8 h = __builtin_bit_cast(half8, kv[c]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float kf = (float)h[e];
+#pragma unroll
+          for (int a = 0; a < kGQA; ++a) d[a] += qs[a][32 * qd + 8 * c + e] * kf;
+        }
+      }
+    }
 #pragma unroll
     for (int a = 0; a < kGQA; ++a) {
-      const float s = wave_sum(q0[a] * k0 + q1[a] * k1) * inv_sqrt + madd;
-      if (lane == 0) sx[a][x] = s;
+      d[a] += __shfl_xor(d[a], 1, 64);
+      d[a] += __shfl_xor(d[a], 2, 64);
+    }
+    if (x < n_x && qd == 0) {
+      const float madd = p.mask ? p.mask[(int64_t)b * p.mask_stride + mpos] : 0.f;
+      *(float4*)&sx[x][0] = make_float4(d[0] * inv_sqrt + madd, d[1] * inv_sqrt + madd,
+                                        d[2] * inv_sqrt + madd, d[3] * inv_sqrt + madd);
     }
   }
   __syncthreads();
 
-  // per query head (wave w = head a): global max, weights, total sum
+  // per query head (wave w = head a): global max, split weights, total sum
   {
     const int a = w;
     const int64_t base = ((int64_t)b * p.H + g * kGQA + a) * p.n_splits;
+    float msp[kMaxSplits / 64];
     float m = -INFINITY;
-    for (int s = lane; s < p.n_splits; s += 64) m = fmaxf(m, p.ws_m[base + s] / kLog2e);
-    for (int x = lane; x < n_x; x += 64) m = fmaxf(m, sx[a][x]);
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / 64; ++k) {
+      const int s = lane + 64 * k;
+      msp[k] = s < p.n_splits ? p.ws_m[base + s] : -INFINITY;
+      m = fmaxf(m, msp[k] * (1.0f / kLog2e));
+    }
+    for (int x = lane; x < n_x; x += 64) m = fmaxf(m, sx[x][a]);
     m = wave_max(m);
     float l = 0.f;
-    for (int s = lane; s < p.n_splits; s += 64) {
-      const float ms = p.ws_m[base + s];
-      const float wv = (ms == -INFINITY) ? 0.f : exp2f(ms - m * kLog2e);
-      wsp[a][s] = wv;
-      l += wv * p.ws_l[base + s];
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / 64; ++k) {
+      const int s = lane + 64 * k;
+      if (s < p.n_splits) {
+        const float wv = (msp[k] == -INFINITY) ? 0.f : exp2f(msp[k] - m * kLog2e);
+        wsp[a][s] = wv;
+        l += wv * p.ws_l[base + s];
+      }
     }
     for (int x = lane; x < n_x; x += 64) {
-      const float e = expf(sx[a][x] - m);
-      sx[a][x] = e;
+      const float e = expf(sx[x][a] - m);
+      sx[x][a] = e;
       l += e;
     }
     l = wave_sum(l);
@@ -525,54 +619,79 @@ void k_decode_combine(const CombineParams p) {
   }
   __syncthreads();
 
-  // compressed part: sum_s w_s acc_s, times ch, one inverse Hadamard
+  // compressed part: sum_s w_s acc_s (dims 2l, 2l+1), times ch, one inverse FWHT
   float f0, f1;
   {
     const int a = w;
-    const int64_t base = ((int64_t)b * p.H + g * kGQA + a) * p.n_splits;
+    const float* ac = p.ws_acc + ((int64_t)b * p.H + g * kGQA + a) * p.n_splits * kHD + 2 * lane;
     float s0 = 0.f, s1 = 0.f;
-    for (int s = 0; s < p.n_splits; ++s) {
-      const float wv = wsp[a][s];
-      const float* ac = p.ws_acc + (base + s) * kHD;
-      s0 += wv * ac[lane];
-      s1 += wv * ac[lane + 64];
+    int s = 0;
+    for (; s + 16 <= p.n_splits; s += 16) {
+      float2 v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = *(const float2*)(ac + (int64_t)(s + u) * kHD);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        s0 += wsp[a][s + u] * v[u].x;
+        s1 += wsp[a][s + u] * v[u].y;
+      }
     }
-    const uint16_t* ch = p.vch + ((int64_t)b * p.G + g) * kHD;
-    f0 = s0 * h2f(ch[lane]);
-    f1 = s1 * h2f(ch[lane + 64]);
-    fwht128(f0, f1);
+    for (; s < p.n_splits; ++s) {
+      const float2 v = *(const float2*)(ac + (int64_t)s * kHD);
+      s0 += wsp[a][s] * v.x;
+      s1 += wsp[a][s] * v.y;
+    }
+    const uint32_t ch2 = *(const uint32_t*)(p.vch + ((int64_t)b * p.G + g) * kHD + 2 * lane);
+    const half2v chh = __builtin_bit_cast(half2v, ch2);
+    f0 = s0 * (float)chh[0];
+    f1 = s1 * (float)chh[1];
+    fwht128_pairs(f0, f1);
   }
 
-  // fp16 segments and stream values
+  // fp16 segments and stream values: thread (token subset w, dims 2l, 2l+1)
   float ax0[kGQA], ax1[kGQA];
 #pragma unroll
   for (int a = 0; a < kGQA; ++a) { ax0[a] = 0.f; ax1[a] = 0.f; }
-  for (int x = w; x < n_x; x += 4) {
-    float v0, v1;
-    int mpos;
-    extra_kv(p, b, g, x, true, cb, sg, v0, v1, mpos);
+  for (int xb = w; xb < n_x; xb += 4 * 8) {
+    uint32_t vv[8];
 #pragma unroll
-    for (int a = 0; a < kGQA; ++a) {
-      const float e = sx[a][x];
-      ax0[a] += e * v0;
-      ax1[a] += e * v1;
+    for (int u = 0; u < 8; ++u) {
+      const int x = xb + 4 * u;
+      int mpos;
+      vv[u] = x < n_x ? *(const uint32_t*)(extra_row(p, b, g, x, true, &mpos) + 2 * lane) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int x = xb + 4 * u;
+      if (x < n_x) {
+        const half2v h = __builtin_bit_cast(half2v, vv[u]);
+        const float4 e4 = *(const float4*)&sx[x][0];
+        const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int a = 0; a < kGQA; ++a) {
+          ax0[a] += ev[a] * (float)h[0];
+          ax1[a] += ev[a] * (float)h[1];
+        }
+      }
     }
   }
 #pragma unroll
-  for (int a = 0; a < kGQA; ++a) {
-    red[w][a][lane] = ax0[a];
-    red[w][a][lane + 64] = ax1[a];
-  }
+  for (int a = 0; a < kGQA; ++a) *(float2*)&red[w][a][2 * lane] = make_float2(ax0[a], ax1[a]);
   __syncthreads();
   {
     const int a = w;
-    const float t0 = red[0][a][lane] + red[1][a][lane] + red[2][a][lane] + red[3][a][lane];
-    const float t1 = red[0][a][lane + 64] + red[1][a][lane + 64] + red[2][a][lane + 64] +
-                     red[3][a][lane + 64];
+    float t0 = 0.f, t1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float2 r2 = *(const float2*)&red[u][a][2 * lane];
+      t0 += r2.x;
+      t1 += r2.y;
+    }
     const float inv_l = 1.0f / Ls[a];
-    uint16_t* o = p.out + ((int64_t)b * p.H + g * kGQA + a) * kHD;
-    o[lane] = f2h((f0 + t0) * inv_l);
-    o[lane + 64] = f2h((f1 + t1) * inv_l);
+    half2v o;
+    o[0] = (half_t)((f0 + t0) * inv_l);
+    o[1] = (half_t)((f1 + t1) * inv_l);
+    *(half2v*)(p.out + ((int64_t)b * p.H + g * kGQA + a) * kHD + 2 * lane) = o;
   }
 }
 
@@ -584,23 +703,49 @@ inline int choose_splits(const shard_decode_args* a, int NB) {
   if (want > max_useful) want = max_useful;
   if (want < 1) want = 1;
   want = ((want + 7) / 8) * 8;
-  if (want > 1024) want = 1024;
+  if (want > kMaxSplits) want = kMaxSplits;
   return want;
 }
 
 constexpr int kNB = 2;
 
 template <int KS>
-int launch_split(const SplitParams& sp, dim3 grid, hipStream_t s) {
+void launch_split(const SplitParams& sp, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((k_decode_split<KS, kNB>), grid, dim3(kThreads), 0, s, sp);
-  return 0;
 }
 
 }  // namespace shard
 
 using namespace shard;
 
+static size_t shard_decode_prepare_op_bytes(int32_t G, int32_t rank) {
+  return (size_t)G * 4 * (rank / 16 + 1) * 64 * sizeof(uint4);
+}
+
 extern "C" {
+
+size_t shard_decode_prepare_bytes(int32_t n_kv_heads, int32_t rank) {
+  if (n_kv_heads <= 0 || rank <= 0 || rank % 32 != 0) return 0;
+  return shard_decode_prepare_op_bytes(n_kv_heads, rank) + (32 * 64 + 64) * sizeof(float2);
+}
+
+int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
+                         const uint16_t* k_mean, const float* inv_freq, int32_t n_kv_heads,
+                         int32_t head_dim, int32_t rank, void* out, size_t out_bytes,
+                         void* stream) {
+  if (!k_basis || !k_coeff_scale || !k_mean || !inv_freq || !out || n_kv_heads <= 0)
+    return SHARD_ERR_ARG;
+  if (head_dim != kHD || rank <= 0 || rank % 32 != 0 || rank > 192) return SHARD_ERR_SHAPE;
+  if (out_bytes < shard_decode_prepare_bytes(n_kv_heads, rank)) return SHARD_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  uint4* op = (uint4*)out;
+  float2* rope = (float2*)((char*)out + shard_decode_prepare_op_bytes(n_kv_heads, rank));
+  const int64_t total = (int64_t)n_kv_heads * 4 * (rank / 16 + 1) * 64 + 32 * 64 + 64;
+  hipLaunchKernelGGL(k_decode_prepare, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     k_basis, k_coeff_scale, k_mean, inv_freq, n_kv_heads, rank, op, rope);
+  SHARD_LAUNCH_CHECK("shard_decode_prepare");
+  return SHARD_OK;
+}
 
 size_t shard_decode_attn_workspace(const shard_decode_args* a) {
   if (!a || a->batch <= 0 || a->n_q_heads <= 0) return 0;
@@ -610,22 +755,21 @@ size_t shard_decode_attn_workspace(const shard_decode_args* a) {
 
 int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t workspace_bytes,
                       void* stream) {
-  if (!a || !a->q || !a->inv_freq || !a->k_coeffs || !a->k_coeff_scale || !a->k_basis ||
-      !a->k_mean || !a->v_idx || !a->v_codebook || !a->v_ch || !a->out)
+  if (!a || !a->q || !a->inv_freq || !a->k_coeffs || !a->prep || !a->v_idx || !a->v_codebook ||
+      !a->v_ch || !a->out)
     return SHARD_ERR_ARG;
   if (a->batch <= 0 || a->n_comp <= 0) return SHARD_ERR_ARG;
   if (a->head_dim != kHD || a->n_q_heads != kGQA * a->n_kv_heads || a->n_kv_heads % kNB != 0)
     return SHARD_ERR_SHAPE;
   if (a->rank <= 0 || a->rank % 32 != 0 || a->rank > 192) return SHARD_ERR_SHAPE;
+  if (a->n_sink < 0 || a->n_win < 0 || a->n_dec < 0 || a->n_stream < 0) return SHARD_ERR_ARG;
   const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
   if (n_x > kMaxExtra) return SHARD_ERR_SHAPE;
   if ((a->n_sink && (!a->sink_k || !a->sink_v)) || (a->n_win && (!a->win_k || !a->win_v)) ||
-      (a->n_dec && (!a->dec_k || !a->dec_v)) ||
-      (a->n_stream && (!a->s_kidx || !a->s_vidx || !a->s_knorm || !a->s_vnorm || !a->s_signs ||
-                       !a->s_codebook)))
+      (a->n_dec && (!a->dec_k || !a->dec_v || a->dec_stride < a->n_dec)) ||
+      (a->n_stream && (!a->s_k || !a->s_v)))
     return SHARD_ERR_ARG;
   const int ns = choose_splits(a, kNB);
-  if (ns > 1024) return SHARD_ERR_SHAPE;
   if (!workspace || workspace_bytes < shard_decode_attn_workspace(a)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
 
@@ -638,8 +782,10 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   int chunk = (a->n_comp + ns - 1) / ns;
   chunk = ((chunk + kTile - 1) / kTile) * kTile;
   sp.chunk = chunk;
-  sp.q = a->q; sp.inv_freq = a->inv_freq; sp.coef = a->k_coeffs; sp.cs = a->k_coeff_scale;
-  sp.basis = a->k_basis; sp.mean = a->k_mean; sp.vidx = a->v_idx; sp.vcb = a->v_codebook;
+  sp.q = a->q; sp.inv_freq = a->inv_freq; sp.coef = a->k_coeffs;
+  sp.op = (const uint4*)a->prep;
+  sp.rope = (const float2*)((const char*)a->prep + shard_decode_prepare_op_bytes(a->n_kv_heads, a->rank));
+  sp.vidx = a->v_idx; sp.vcb = a->v_codebook;
   sp.mask = a->mask; sp.mask_stride = a->mask_stride; sp.n_sink = a->n_sink;
   sp.ws_m = ws; sp.ws_l = ws + nm; sp.ws_acc = ws + 2 * nm;
 
@@ -661,8 +807,7 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   cp.sink_k = a->sink_k; cp.sink_v = a->sink_v; cp.n_sink = a->n_sink;
   cp.win_k = a->win_k; cp.win_v = a->win_v; cp.n_win = a->n_win;
   cp.dec_k = a->dec_k; cp.dec_v = a->dec_v; cp.n_dec = a->n_dec; cp.dec_stride = a->dec_stride;
-  cp.s_kidx = a->s_kidx; cp.s_vidx = a->s_vidx; cp.s_knorm = a->s_knorm; cp.s_vnorm = a->s_vnorm;
-  cp.s_signs = a->s_signs; cp.s_cb = a->s_codebook; cp.n_stream = a->n_stream;
+  cp.s_k = a->s_k; cp.s_v = a->s_v; cp.n_stream = a->n_stream;
   cp.mask = a->mask; cp.mask_stride = a->mask_stride;
   cp.ws_m = sp.ws_m; cp.ws_l = sp.ws_l; cp.ws_acc = sp.ws_acc; cp.out = a->out;
   hipLaunchKernelGGL(k_decode_combine, dim3((unsigned)a->n_kv_heads, (unsigned)a->batch),

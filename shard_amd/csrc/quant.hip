@@ -391,7 +391,7 @@ template <int E>
 __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
                                const float* __restrict__ signs, const float* __restrict__ cb_g,
                                int n_codes, uint8_t* __restrict__ idx,
-                               uint16_t* __restrict__ norm) {
+                               uint16_t* __restrict__ norm, uint16_t* __restrict__ deq) {
   constexpr int D = 64 * E;
   __shared__ float cb[256];
   for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
@@ -419,7 +419,7 @@ __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
   for (int j = 1; j < 8; ++j) tot = add_rn(tot, __shfl(acc, j, 64));
   float n = fmaxf(sqrtf(tot), 1e-8f);
 #pragma unroll
-  for (int k = 0; k < E; ++k) t[k] = mul_rn(div_rn(t[k], n), signs[l + 64 * k]);
+  for (int k = 0; k < E; ++k) t[k] = mul_sign(div_rn(t[k], n), signs[l + 64 * k]);
   wave_fwht<E>(t, D);
 #pragma unroll
   for (int k = 0; k < E; ++k) {
@@ -433,9 +433,20 @@ __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
     int left = i > 0 ? i - 1 : 0;
     float dl = fabsf(sub_rn(cb[left], v));
     float di = fabsf(sub_rn(cb[i], v));
-    idx[r * D + l + 64 * k] = (uint8_t)(dl < di ? left : i);
+    const int code = dl < di ? left : i;
+    idx[r * D + l + 64 * k] = (uint8_t)code;
+    t[k] = cb[code];
   }
-  if (l == 0) norm[r] = f2h(n);
+  const uint16_t nh = f2h(n);
+  if (l == 0) norm[r] = nh;
+  if (deq) {
+    // reference dequant: fp16(fp16(hadamard(cb[idx]) * signs) * fp16 norm)
+    wave_fwht<E>(t, D);
+    const float nf = h2f(nh);
+#pragma unroll
+    for (int k = 0; k < E; ++k)
+      deq[r * D + l + 64 * k] = f2h_opaque(h2f(f2h(mul_sign(t[k], signs[l + 64 * k]))) * nf);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -616,15 +627,15 @@ int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx
 
 int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,
                        const float* codebook, int32_t n_codes, uint8_t* idx, uint16_t* norm,
-                       void* stream) {
+                       uint16_t* deq, void* stream) {
   if (!x || !signs || !codebook || !idx || !norm || rows <= 0 || n_codes <= 0) return SHARD_ERR_ARG;
   if (n_codes > 256) return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   unsigned blocks = (unsigned)((rows + 3) / 4);
   switch (hd) {
-    case 64: hipLaunchKernelGGL(k_stream_quant<1>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm); break;
-    case 128: hipLaunchKernelGGL(k_stream_quant<2>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm); break;
-    case 256: hipLaunchKernelGGL(k_stream_quant<4>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm); break;
+    case 64: hipLaunchKernelGGL(k_stream_quant<1>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, deq); break;
+    case 128: hipLaunchKernelGGL(k_stream_quant<2>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, deq); break;
+    case 256: hipLaunchKernelGGL(k_stream_quant<4>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, deq); break;
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_stream_quant");

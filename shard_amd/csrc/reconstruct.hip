@@ -100,8 +100,8 @@ __global__ void k_reconstruct_v(const uint8_t* __restrict__ vidx, const uint16_t
     float x0 = __fmul_rn(h2f(vcb[4 * ix[d0 >> 2] + (d0 & 3)]), h2f(ch[d0]));
     float x1 = __fmul_rn(h2f(vcb[4 * ix[d1 >> 2] + (d1 & 3)]), h2f(ch[d1]));
     rc_fwht128(x0, x1);
-    v_out[r * kRcHD + d0] = f2h(x0);
-    v_out[r * kRcHD + d1] = f2h(x1);
+    v_out[r * kRcHD + d0] = f2h_opaque(x0);
+    v_out[r * kRcHD + d1] = f2h_opaque(x1);
   }
 }
 
@@ -116,8 +116,10 @@ __global__ void k_stream_dequant(const uint8_t* __restrict__ idx, const uint16_t
     float x0 = cb[idx[r * kRcHD + l]], x1 = cb[idx[r * kRcHD + l + 64]];
     rc_fwht128(x0, x1);
     const float n = h2f(norm[r]);
-    y[r * kRcHD + l] = f2h(h2f(f2h(__fmul_rn(x0, signs[l]))) * n);
-    y[r * kRcHD + l + 64] = f2h(h2f(f2h(__fmul_rn(x1, signs[l + 64]))) * n);
+    // fp16(fp16(x * sign) * norm): the sign flip is exact, the product of two
+    // fp16 values is exact in fp32, so each line rounds exactly twice like torch
+    y[r * kRcHD + l] = f2h_opaque(h2f(f2h(mul_sign(x0, signs[l]))) * n);
+    y[r * kRcHD + l + 64] = f2h_opaque(h2f(f2h(mul_sign(x1, signs[l + 64]))) * n);
   }
 }
 

@@ -77,10 +77,10 @@ def int4_quant_pack(proj: torch.Tensor, bits: torch.Tensor, want_codes: bool = F
 
     proj (n, keep) fp32; bits (keep,) int32.  Returns dict(packed, coeff_scale,
     lo, rng[, codes])."""
-    _require_gpu(proj, bits)
+    _require_gpu(proj)
     lib = _lib.load()
     proj = _contig(proj, torch.float32, "proj")
-    bits = _contig(bits.to(device=proj.device, dtype=torch.int32), torch.int32, "bits")
+    bits = torch.as_tensor(bits, dtype=torch.int32).to(proj.device).contiguous()
     n, keep = proj.shape
     if bits.numel() != keep:
         raise ValueError("int4_quant_pack: bits length != keep")
@@ -200,26 +200,26 @@ def kmeans(data: torch.Tensor, k: int, n_iter: int = 30, seed: int = 42):
 # ---------------------------------------------------------------------------
 # decode stream
 # ---------------------------------------------------------------------------
-def stream_quant(x: torch.Tensor, signs: torch.Tensor, codebook: torch.Tensor):
-    """Per-token Lloyd-Max quantizer; x (..., D) fp16 -> (idx u8 (..., D), norm fp16 (...))."""
+def stream_quant(x: torch.Tensor, signs: torch.Tensor, codebook: torch.Tensor,
+                 with_deq: bool = False):
+    """Per-token Lloyd-Max quantizer; x (..., D) fp16 -> (idx u8 (..., D), norm fp16 (...)
+    [, deq fp16 (..., D) = the token as the reference dequantizes it])."""
     _require_gpu(x, signs, codebook)
-    lib = _lib.load()
     x = _contig(x, torch.float16, "x")
-    D = x.shape[-1]
-    rows = x.numel() // D
     idx = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     norm = torch.empty(x.shape[:-1], dtype=torch.float16, device=x.device)
-    stream_quant_into(x, signs, codebook, idx, norm)
-    return idx, norm
+    deq = torch.empty(x.shape, dtype=torch.float16, device=x.device) if with_deq else None
+    stream_quant_into(x, signs, codebook, idx, norm, deq)
+    return (idx, norm, deq) if with_deq else (idx, norm)
 
 
-def stream_quant_into(x, signs, codebook, idx_out, norm_out):
+def stream_quant_into(x, signs, codebook, idx_out, norm_out, deq_out=None):
     lib = _lib.load()
     D = x.shape[-1]
     rows = x.numel() // D
     _lib.check("shard_stream_quant", lib.shard_stream_quant(
         _p(x), rows, D, _p(signs), _p(codebook), codebook.numel(), _p(idx_out), _p(norm_out),
-        _stream(x)))
+        _p(deq_out), _stream(x)))
 
 
 def stream_dequant(idx: torch.Tensor, norm: torch.Tensor, signs: torch.Tensor,
@@ -247,6 +247,20 @@ class DecodeCall:
         self.keep = keep_alive
 
 
+def decode_prepare(fmt) -> torch.Tensor:
+    """Per-layer constant operands of the decode kernel (uint8 buffer on the device)."""
+    lib = _lib.load()
+    basis, cs, mean = fmt["k_basis_pad"], fmt["k_coeff_scale_pad"], fmt["k_mean_f16"]
+    _require_gpu(basis, cs, mean)
+    G, rank = fmt["n_kv"], fmt["rank_pad"]
+    inv = fmt["inv_freq_dev"]
+    buf = torch.empty(lib.shard_decode_prepare_bytes(G, rank), dtype=torch.uint8, device=basis.device)
+    _lib.check("shard_decode_prepare", lib.shard_decode_prepare(
+        _p(basis), _p(cs), _p(mean), _p(inv), G, fmt["head_dim"], rank, _p(buf), buf.numel(),
+        _stream(basis)))
+    return buf
+
+
 def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
                      stream_n=0, decode_kv=None) -> DecodeCall:
     """Build shard_decode_args for one layer.
@@ -268,7 +282,8 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
     inv_freq = fmt["inv_freq_dev"] if inv_freq is None else inv_freq
     for name, t in (("q", q), ("inv_freq", inv_freq), ("k_coeffs", fmt["k_coeffs_pad"]),
                     ("k_coeff_scale", fmt["k_coeff_scale_pad"]), ("k_basis", fmt["k_basis_pad"]),
-                    ("k_mean", fmt["k_mean_f16"]), ("v_idx", fmt["v_indices"]),
+                    ("k_mean", fmt["k_mean_f16"]), ("prep", fmt["decode_prep"]),
+                    ("v_idx", fmt["v_indices"]),
                     ("v_codebook", fmt["v_centroids_f16"]), ("v_ch", fmt["v_ch_f16"]),
                     ("sink_k", fmt["sink_k"]), ("sink_v", fmt["sink_v"]),
                     ("win_k", fmt["win_k"]), ("win_v", fmt["win_v"])):
@@ -282,11 +297,8 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
         a.n_dec, a.dec_stride = dk.shape[2], dk.shape[2]
         keep += [dk, dv]
     if stream_n > 0:
-        for name, key in (("s_kidx", "k_idx_buf"), ("s_vidx", "v_idx_buf"),
-                          ("s_knorm", "k_norm_buf"), ("s_vnorm", "v_norm_buf"),
-                          ("s_signs", "signs"), ("s_codebook", "stream_codebook")):
-            setattr(a, name, fmt[key].data_ptr())
-            keep.append(fmt[key])
+        a.s_k, a.s_v = fmt["k_deq_buf"].data_ptr(), fmt["v_deq_buf"].data_ptr()
+        keep += [fmt["k_deq_buf"], fmt["v_deq_buf"]]
         a.n_stream = stream_n
     if mask is not None:
         m = mask.reshape(B, -1)

@@ -78,13 +78,18 @@ def to_device(gc, device, inv_freq, nkv=8, hd=128):
         d["decode_k"] = t(gc["decode_k"]).contiguous()
         d["decode_v"] = t(gc["decode_v"]).contiguous()
     if gc.get("stream_n", 0):
+        kdeq = ref.dequantize_stream_token(gc["k_idx_buf"], gc["k_norm_buf"], gc["signs"],
+                                           gc["stream_codebook"])
+        vdeq = ref.dequantize_stream_token(gc["v_idx_buf"], gc["v_norm_buf"], gc["signs"],
+                                           gc["stream_codebook"])
         d.update({"signs": t(np.asarray(gc["signs"], np.float32)),
                   "stream_codebook": t(np.asarray(gc["stream_codebook"], np.float32)),
                   "stream_n": gc["stream_n"],
                   "k_idx_buf": t(gc["k_idx_buf"]).contiguous(),
                   "v_idx_buf": t(gc["v_idx_buf"]).contiguous(),
                   "k_norm_buf": t(gc["k_norm_buf"]).contiguous(),
-                  "v_norm_buf": t(gc["v_norm_buf"]).contiguous()})
+                  "v_norm_buf": t(gc["v_norm_buf"]).contiguous(),
+                  "k_deq_buf": t(kdeq).contiguous(), "v_deq_buf": t(vdeq).contiguous()})
     finalize_format(d, torch.as_tensor(inv_freq), device)
     return d
 

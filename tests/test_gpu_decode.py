@@ -124,5 +124,9 @@ def test_kv_reconstruct(cuda):
     k_got, v_got = ops.kv_reconstruct(d, 2)
     k_want, v_want = ref.reconstruct_kv(gc, 8, 128, inv)
     assert np.array_equal(v_got.cpu().numpy().view(np.uint16), v_want.numpy().view(np.uint16))
+    # the fp16 rounding of the rebuilt key depends on the fp32 accumulation order,
+    # so a key may differ by an ulp of its pre-RoPE value (|k| < 2: ulp <= 2^-10)
     kg, kw = k_got.cpu().float(), k_want.float()
-    assert float(((kg - kw).abs() / (kw.abs() + 1e-2)).max()) < 4e-3
+    diff = (kg - kw).abs()
+    assert float(diff.max()) <= 2 * 2.0 ** -10
+    assert float((diff > 0).float().mean()) < 0.02
