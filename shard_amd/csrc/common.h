@@ -66,6 +66,87 @@ __device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, 
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
+// ---- cross-lane exchange without the LDS crossbar.
+// DPP moves inside rows of 16 lanes; v_permlane16_swap / v_permlane32_swap
+// (gfx950) across rows and halves.  A ds_bpermute costs an LDS round trip
+// (~100+ cycles) per step of a reduction chain; these are VALU operations.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i inside groups of 8
+constexpr int kDppMirror = 0x140;      // lane i <- 15 - i inside rows of 16
+constexpr int kDppRor4 = 0x124;        // row rotate right by 4
+constexpr int kDppRor8 = 0x128;        // row rotate right by 8
+constexpr int kDppRor12 = 0x12C;       // row rotate right by 12
+
+// (value of row r^1, value of half h^1) pairs: returns both swap results; for
+// a commutative reduction their combination is the same on every lane.
+__device__ __forceinline__ void perm16_swap(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void perm32_swap(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+// Reductions whose result every lane of the group holds: over each row of 16,
+// each half (32 lanes) and the whole wave.
+template <class Op>
+__device__ __forceinline__ float row16_reduce(float v, Op op) {
+  v = op(v, dpp_mov<kDppXor1>(v));
+  v = op(v, dpp_mov<kDppXor2>(v));
+  v = op(v, dpp_mov<kDppHalfMirror>(v));
+  return op(v, dpp_mov<kDppMirror>(v));
+}
+template <class Op>
+__device__ __forceinline__ float half32_reduce(float v, Op op) {
+  v = row16_reduce(v, op);
+  float a, b;
+  perm16_swap(v, a, b);
+  return op(a, b);
+}
+template <class Op>
+__device__ __forceinline__ float wave64_reduce(float v, Op op) {
+  v = half32_reduce(v, op);
+  float a, b;
+  perm32_swap(v, a, b);
+  return op(a, b);
+}
+struct OpMax { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpAdd { __device__ float operator()(float a, float b) const { return a + b; } };
+
+// The value of lane (l ^ HL), HL a power of two below 64.
+template <int HL>
+__device__ __forceinline__ float xor_lane(float v) {
+  const int l = (int)(threadIdx.x & 63u);
+  if constexpr (HL == 1) {
+    return dpp_mov<kDppXor1>(v);
+  } else if constexpr (HL == 2) {
+    return dpp_mov<kDppXor2>(v);
+  } else if constexpr (HL == 4) {
+    // rotate right by 4 brings lane i-4, by 12 brings lane i+4 (mod 16)
+    const float lo = dpp_mov<kDppRor4>(v), hi = dpp_mov<kDppRor12>(v);
+    return (l & 4) ? lo : hi;
+  } else if constexpr (HL == 8) {
+    return dpp_mov<kDppRor8>(v);
+  } else if constexpr (HL == 16) {
+    float a, b;
+    perm16_swap(v, a, b);  // a: rows (0,0,2,2), b: rows (1,1,3,3)
+    return (l & 16) ? a : b;
+  } else {
+    static_assert(HL == 32, "xor_lane: HL must be a power of two below 64");
+    float a, b;
+    perm32_swap(v, a, b);  // a: halves (0,0), b: halves (1,1)
+    return (l & 32) ? a : b;
+  }
+}
+
 inline int grid_cap(int64_t blocks, int cap = 65535 * 8) {
   return (int)(blocks < cap ? blocks : cap);
 }

@@ -21,7 +21,7 @@
 //        accumulated with the fp32 codebook in LDS.
 //     4. per (query head, split): running max m, sum l and the 128-dim
 //        accumulator go to the workspace.
-//   combine kernel grid = (n_kv, B): merges the splits, applies ch and ONE
+//   combine kernel grid = (n_q, B): merges the splits, applies ch and ONE
 //                  inverse Hadamard to the VQ accumulator, adds the fp16 sink /
 //                  window / decode tokens and the dequantized 8-bit stream
 //                  tokens, normalizes, writes fp16.
@@ -37,8 +37,21 @@ constexpr int kMaxExtra = 2048;   // sink + window + decode + stream tokens per 
 constexpr int kMaxSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
 
+// The fp16 segments around the compressed span, in attention-mask order:
+// sink [0, n_sink), window, decode tokens, then the 8-bit stream (dequantized
+// to fp16 rows as tokens arrive).
+struct ExtraSegs {
+  const uint16_t *sink_k, *sink_v;
+  const uint16_t *win_k, *win_v;
+  const uint16_t *dec_k, *dec_v;
+  const uint16_t *s_k, *s_v;
+  int32_t n_sink, n_win, n_dec, dec_stride, n_stream, n_x;
+};
+
 struct SplitParams {
   int32_t B, H, G, rank, n_comp, cstart, pos_q, n_splits, chunk;
+  int32_t nsp;   // partial rows per (batch row, query head): n_splits (+1 with extra tokens)
+  ExtraSegs xs;  // processed by the last split of each head before its compressed tiles
   const uint16_t* q;
   const float* inv_freq;
   const uint8_t* coef;
@@ -161,8 +174,143 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
   }
 }
 
+// Row x of the extra tokens (sink, window, decode, stream) of kv head g in
+// batch row b, and its column in the attention mask (the compressed span sits
+// between the sink and the window).
+__device__ __forceinline__ const uint16_t* extra_row(const ExtraSegs& s, int B, int G, int n_comp,
+                                                     int b, int g, int x, bool v, int* mpos) {
+  const int e1 = s.n_sink, e2 = e1 + s.n_win, e3 = e2 + s.n_dec;
+  const int64_t bg = (int64_t)b * G + g;
+  const uint16_t* base;
+  int64_t row;
+  if (x < e1) {
+    base = v ? s.sink_v : s.sink_k;
+    row = bg * s.n_sink + x;
+  } else if (x < e2) {
+    base = v ? s.win_v : s.win_k;
+    row = bg * s.n_win + (x - e1);
+  } else if (x < e3) {
+    base = v ? s.dec_v : s.dec_k;
+    row = bg * s.dec_stride + (x - e2);
+  } else {
+    base = v ? s.s_v : s.s_k;
+    row = ((int64_t)(x - e3) * B + b) * G + g;
+  }
+  *mpos = x < e1 ? x : x + n_comp;
+  return base + row * kHD;
+}
+
+constexpr int kXTok = 128;  // extra tokens per pass (32 per wave)
+
+// Extra tokens (sink, window, decode, stream; fp16 rows) of kv head g, run by
+// the last split workgroup of the head before its compressed tiles.  Per pass
+// of 128 tokens: scores on MFMA (rows = the kGQA query heads, k = head dims,
+// columns = the wave's 32 tokens), online softmax per head (wave h owns head
+// h), values accumulated lane-per-dim pair.  Writes partial row n_splits of
+// each query head, in the plain (not rotated) basis.
+__device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const int g, const int b) {
+  __shared__ __align__(16) float xsc[kGQA][kXTok];     // scores of the pass (base 2)
+  __shared__ __align__(16) float xpw[kXTok][kGQA];     // softmax numerators, [token][head]
+  __shared__ __align__(16) float2 xred[4][kGQA][64];   // per-wave value sums
+  __shared__ float xal[kGQA];                          // rescale of the running sums
+
+  const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_x = p.xs.n_x;
+  const float sc = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
+
+  half8 Aq[8];
+  {
+    const uint16_t* qv = p.q + ((int64_t)b * p.H + g * kGQA + min(col, kGQA - 1)) * kHD + 8 * hh;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const uint4 v4 = *(const uint4*)(qv + 16 * st);
+      Aq[st] = __builtin_bit_cast(half8, col < kGQA ? v4 : make_uint4(0u, 0u, 0u, 0u));
+    }
+  }
+  float m_run = -INFINITY, l_run = 0.f;  // softmax state of head w
+  float2 acc[kGQA];
+#pragma unroll
+  for (int h = 0; h < kGQA; ++h) acc[h] = make_float2(0.f, 0.f);
+
+  for (int x0 = 0; x0 < n_x; x0 += kXTok) {
+    const int xt = min(x0 + 32 * w + col, n_x - 1);  // clamped: rows past n_x are masked
+    int mpos;
+    const uint16_t* krow = extra_row(p.xs, p.B, p.G, p.n_comp, b, g, xt, false, &mpos);
+    const uint16_t* vrow = extra_row(p.xs, p.B, p.G, p.n_comp, b, g, xt, true, &mpos);
+    half8 Bk[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) Bk[st] = __builtin_bit_cast(half8, *(const uint4*)(krow + 16 * st + 8 * hh));
+    const float madd = p.mask ? p.mask[(int64_t)b * p.mask_stride + mpos] * kLog2e : 0.f;
+    uint32_t vx[32];
+    const uint64_t vb = (uint64_t)vrow;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
+      vx[t] = *(const uint32_t*)((const uint16_t*)(((uint64_t)hi << 32) | lo) + 2 * lane);
+    }
+    float16v sacc = {};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[st], Bk[st], sacc, 0, 0, 0);
+    if (hh == 0) {
+      const bool valid = x0 + 32 * w + col < n_x;
+#pragma unroll
+      for (int i = 0; i < kGQA; ++i) xsc[i][32 * w + col] = valid ? sacc[i] * sc + madd : -INFINITY;
+    }
+    __syncthreads();
+    {  // wave w: online softmax of head w over the pass
+      const float s0 = xsc[w][lane], s1 = xsc[w][lane + 64];
+      const float m_new = fmaxf(m_run, wave64_reduce(fmaxf(s0, s1), OpMax()));
+      const float al = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+      const float p0 = s0 == -INFINITY ? 0.f : exp2f(s0 - m_new);
+      const float p1 = s1 == -INFINITY ? 0.f : exp2f(s1 - m_new);
+      l_run = l_run * al + wave64_reduce(p0 + p1, OpAdd());
+      m_run = m_new;
+      xpw[lane][w] = p0;
+      xpw[lane + 64][w] = p1;
+      if (lane == 0) xal[w] = al;
+    }
+    __syncthreads();
+    const float4 al4 = *(const float4*)xal;
+    acc[0].x *= al4.x; acc[0].y *= al4.x;
+    acc[1].x *= al4.y; acc[1].y *= al4.y;
+    acc[2].x *= al4.z; acc[2].y *= al4.z;
+    acc[3].x *= al4.w; acc[3].y *= al4.w;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      const float4 pw = *(const float4*)&xpw[32 * w + t][0];
+      const half2v hv = __builtin_bit_cast(half2v, vx[t]);
+      const float v0 = (float)hv[0], v1 = (float)hv[1];
+      acc[0].x += pw.x * v0; acc[0].y += pw.x * v1;
+      acc[1].x += pw.y * v0; acc[1].y += pw.y * v1;
+      acc[2].x += pw.z * v0; acc[2].y += pw.z * v1;
+      acc[3].x += pw.w * v0; acc[3].y += pw.w * v1;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < kGQA; ++h) xred[w][h][lane] = acc[h];
+  __syncthreads();
+  {
+    const int h = w;
+    float2 t = xred[0][h][lane];
+#pragma unroll
+    for (int u = 1; u < 4; ++u) {
+      const float2 a = xred[u][h][lane];
+      t.x += a.x;
+      t.y += a.y;
+    }
+    const int64_t widx = ((int64_t)b * p.H + g * kGQA + h) * p.nsp + p.n_splits;
+    *(float2*)(p.ws_acc + widx * kHD + 2 * lane) = t;
+    if (lane == 0) {
+      p.ws_m[widx] = m_run;
+      p.ws_l[widx] = l_run;
+    }
+  }
+}
+
 template <int KS, int NB>
-__global__ __launch_bounds__(kThreads, 1)
+__global__ __launch_bounds__(kThreads, NB == 1 ? 2 : 1)
 void k_decode_split(const SplitParams p) {
   constexpr int NQ = kGQA * NB;          // query heads of this workgroup
   constexpr int TS = 8 / NB;             // token subsets of the V stage
@@ -179,19 +327,42 @@ void k_decode_split(const SplitParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int P = tid >> 6;                // wave = pair slice
+  const int P = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = pair slice (SGPR)
   const int col = lane & 31;
   const int hh = lane >> 5;
 
-  // ---- XCD-aware block -> (head group, split): all head groups of one split
-  // land on the same XCD (block ids congruent mod 8) so the coefficient rows
-  // of that split are fetched once into that XCD's L2.
+  // ---- block -> (head group, split).  Consecutive blocks are consecutive head
+  // groups of one split; the dispatcher deals blocks to the 8 XCDs in turn, so
+  // with 8 head groups every XCD serves one head group and its L2 holds that
+  // head's basis operands.
   const int HG = p.G / NB;
   const int bid = blockIdx.x;
-  const int slot = bid >> 3;
-  const int hg = slot % HG;
-  const int split = (slot / HG) * 8 + (bid & 7);
+  const int hg = bid % HG;
+  const int split = bid / HG;
   const int b = blockIdx.y;
+  // The last split of each head runs the extra tokens first (its compressed
+  // chunk is shorter by their cost), so their cold loads overlap the other
+  // workgroups' set-up instead of trailing the kernel.
+  if (split == p.n_splits - 1 && p.xs.n_x > 0) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) decode_extras_tail(p, hg * NB + j, b);
+  }
+
+  // ---- loads that feed LDS and the q operand go out first: the first barrier
+  // waits for these only, not for the tile and basis loads behind them.
+  const uint2 cb_v = *(const uint2*)(p.vcb + 4 * tid);   // 256 codebook entries, one per thread
+  const float th_v = tid < 128 ? p.inv_freq[tid & 63] : 0.f;
+  uint2 q_lo[2], q_hi[2];
+  {
+    const int qr = col;
+    const uint16_t* qv = p.q + ((int64_t)b * p.H + hg * NQ + min(qr, NQ - 1)) * kHD;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int d0 = 16 * P + 8 * jj + 4 * hh;
+      q_lo[jj] = *(const uint2*)(qv + d0);
+      q_hi[jj] = *(const uint2*)(qv + d0 + 64);
+    }
+  }
   const int t_begin = split * p.chunk;
   int t_end = t_begin + p.chunk;
   if (t_end > p.n_comp) t_end = p.n_comp;
@@ -235,14 +406,12 @@ void k_decode_split(const SplitParams p) {
     rs[i] = p.rope[32 * 64 + pr[i]];       // (cos, sin)(32 * theta)
   }
 
-  for (int i = tid; i < 256; i += kThreads) cbl[i] = *(const uint2*)(p.vcb + 4 * i);
+  cbl[tid] = cb_v;
   if (tid < 128) {
-    const int i = tid & 63;
-    const float th = p.inv_freq[i];
-    const float x = tid < 64 ? (float)p.pos_q * th : (float)(p.cstart + t_begin - p.pos_q) * th;
+    const float x = tid < 64 ? (float)p.pos_q * th_v : (float)(p.cstart + t_begin - p.pos_q) * th_v;
     float sn, cn;
     sincosf(x, &sn, &cn);
-    (tid < 64 ? phq : phb)[i] = make_float2(cn, sn);
+    (tid < 64 ? phq : phb)[tid & 63] = make_float2(cn, sn);
   }
   __syncthreads();
 
@@ -254,11 +423,9 @@ void k_decode_split(const SplitParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) { a_[i] = 0.f; b_[i] = 0.f; }
     if (qr < NQ) {
-      const uint16_t* qv = p.q + ((int64_t)b * p.H + hg * NQ + qr) * kHD;
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const int d0 = 16 * P + 8 * jj + 4 * hh;
-        const uint2 lo4 = *(const uint2*)(qv + d0), hi4 = *(const uint2*)(qv + d0 + 64);
+        const uint2 lo4 = q_lo[jj], hi4 = q_hi[jj];
         const half2v l0 = __builtin_bit_cast(half2v, lo4.x), l1 = __builtin_bit_cast(half2v, lo4.y);
         const half2v h0 = __builtin_bit_cast(half2v, hi4.x), h1 = __builtin_bit_cast(half2v, hi4.y);
         const float lo[4] = {(float)l0[0], (float)l0[1], (float)l1[0], (float)l1[1]};
@@ -366,9 +533,7 @@ void k_decode_split(const SplitParams p) {
           s *= sc;
           if (p.mask) s += p.mask[(int64_t)b * p.mask_stride + p.n_sink + tok] * kLog2e;
         }
-        float tmax = s;
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
+        const float tmax = half32_reduce(s, OpMax());
         const float m_new = fmaxf(m_run[k], tmax);
         const float al = (m_new == -INFINITY) ? 1.f : exp2f(m_run[k] - m_new);
         const float pv = (s == -INFINITY) ? 0.f : exp2f(s - m_new);
@@ -428,13 +593,11 @@ void k_decode_split(const SplitParams p) {
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
     const int e = tid + kThreads * k;
-    float l = l_part[k];
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+    const float l = half32_reduce(l_part[k], OpAdd());
     if (e < NQ * kTile && (e & 31) == 0) {
       const int qr = e >> 5;
       const int qh = hg * NQ + qr;
-      const int64_t widx = ((int64_t)b * p.H + qh) * p.n_splits + split;
+      const int64_t widx = ((int64_t)b * p.H + qh) * p.nsp + split;
       p.ws_m[widx] = m_run[k];
       p.ws_l[widx] = l;
     }
@@ -454,34 +617,31 @@ void k_decode_split(const SplitParams p) {
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       const int qh = hg * NQ + 4 * vj + a;
-      float* dst = p.ws_acc + (((int64_t)b * p.H + qh) * p.n_splits + split) * kHD + 4 * vG;
+      float* dst = p.ws_acc + (((int64_t)b * p.H + qh) * p.nsp + split) * kHD + 4 * vG;
       *(float4*)dst = make_float4(sum[4 * a], sum[4 * a + 1], sum[4 * a + 2], sum[4 * a + 3]);
     }
   }
 }
 
 // --------------------------------------------------------------------------
-// Combine: merge splits, fp16 segments and the stream; one inverse FWHT.
+// Combine: merge the partials of one query head, one inverse FWHT.
 // --------------------------------------------------------------------------
 struct CombineParams {
-  int32_t B, H, G, n_comp, n_splits;
-  const uint16_t* q;
+  int32_t B, H, G, n_splits, nsp;
   const uint16_t* vch;
-  const uint16_t *sink_k, *sink_v;
-  int32_t n_sink;
-  const uint16_t *win_k, *win_v;
-  int32_t n_win;
-  const uint16_t *dec_k, *dec_v;
-  int32_t n_dec, dec_stride;
-  const uint16_t *s_k, *s_v;
-  int32_t n_stream;
-  const float* mask;
-  int64_t mask_stride;
   const float* ws_m;
   const float* ws_l;
   const float* ws_acc;
   uint16_t* out;
 };
+
+// One butterfly stage at element stride 2*HL = lane stride HL.
+template <int HL>
+__device__ __forceinline__ void fwht_lane_stage(float& x0, float& x1, int l) {
+  const float p0 = xor_lane<HL>(x0), p1 = xor_lane<HL>(x1);
+  x0 = (l & HL) ? p0 - x0 : x0 + p0;
+  x1 = (l & HL) ? p1 - x1 : x1 + p1;
+}
 
 // Butterflies over 128 values held as (2l, 2l+1) in lane l (Sylvester order).
 __device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
@@ -491,223 +651,142 @@ __device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
     x0 = a + c;
     x1 = a - c;
   }
-#pragma unroll
-  for (int hl = 1; hl < 64; hl <<= 1) {  // element stride 2*hl = lane stride hl
-    const float p0 = __shfl_xor(x0, hl, 64), p1 = __shfl_xor(x1, hl, 64);
-    x0 = (l & hl) ? p0 - x0 : x0 + p0;
-    x1 = (l & hl) ? p1 - x1 : x1 + p1;
-  }
+  fwht_lane_stage<1>(x0, x1, l);
+  fwht_lane_stage<2>(x0, x1, l);
+  fwht_lane_stage<4>(x0, x1, l);
+  fwht_lane_stage<8>(x0, x1, l);
+  fwht_lane_stage<16>(x0, x1, l);
+  fwht_lane_stage<32>(x0, x1, l);
   const float s = 0.08838834764831845f;  // 1/sqrt(128)
   x0 *= s;
   x1 *= s;
 }
 
-// Row x of the extra tokens (sink, window, decode, stream) of kv head g, row b.
-__device__ __forceinline__ const uint16_t* extra_row(const CombineParams& p, int b, int g, int x,
-                                                     bool v, int* mask_pos) {
-  if (x < p.n_sink) {
-    *mask_pos = x;
-    return (v ? p.sink_v : p.sink_k) + (((int64_t)b * p.G + g) * p.n_sink + x) * kHD;
-  }
-  x -= p.n_sink;
-  if (x < p.n_win) {
-    *mask_pos = p.n_sink + p.n_comp + x;
-    return (v ? p.win_v : p.win_k) + (((int64_t)b * p.G + g) * p.n_win + x) * kHD;
-  }
-  x -= p.n_win;
-  if (x < p.n_dec) {
-    *mask_pos = p.n_sink + p.n_comp + p.n_win + x;
-    return (v ? p.dec_v : p.dec_k) + (((int64_t)b * p.G + g) * p.dec_stride + x) * kHD;
-  }
-  x -= p.n_dec;
-  *mask_pos = p.n_sink + p.n_comp + p.n_win + p.n_dec + x;
-  return (v ? p.s_v : p.s_k) + (((int64_t)x * p.B + b) * p.G + g) * kHD;
-}
+constexpr int kCombPF = 16;  // partials per wave held in registers
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__global__ __launch_bounds__(kThreads, 1)
+// One workgroup per (query head, batch row); wave w merges a quarter of the
+// partial rows.  Rows [0, n_splits) hold VQ values in the rotated basis (summed,
+// scaled by ch and rotated back once), rows [n_splits, nsp) the extra tokens in
+// the plain basis.  Every load is issued at entry; one barrier publishes the
+// wave maxima, the next the partial sums.
+__global__ __launch_bounds__(kThreads)
 void k_decode_combine(const CombineParams p) {
-  __shared__ __align__(16) float qs[kGQA][kHD];
-  __shared__ __align__(16) float sx[kMaxExtra][kGQA];
-  __shared__ __align__(16) float wsp[kGQA][kMaxSplits];
-  __shared__ __align__(16) float red[4][kGQA][kHD];
-  __shared__ float Ms[kGQA], Ls[kGQA];
+  __shared__ __align__(16) float2 rrot[4][64];   // per-wave rotated-basis sums
+  __shared__ __align__(16) float2 rpl[4][64];    // per-wave plain-basis sums
+  __shared__ float wmax[4], wsum[4];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = blockIdx.x, b = blockIdx.y;
-  const int n_x = p.n_sink + p.n_win + p.n_dec + p.n_stream;
-  for (int i = tid; i < kGQA * kHD; i += kThreads)
-    qs[i / kHD][i % kHD] = h2f(p.q[((int64_t)b * p.H + g * kGQA + i / kHD) * kHD + i % kHD]);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qh = blockIdx.x, b = blockIdx.y, g = qh / kGQA;
+  const int64_t hrow = (int64_t)b * p.H + qh;
+  const int nsp = p.nsp, ns = p.n_splits;
+  const int per = (nsp + 3) / 4;
+  const int s_lo = min(nsp, w * per);
+  const int s_hi = min(nsp, s_lo + per);
+  const float* mrow = p.ws_m + hrow * nsp;
+  const float* lrow = p.ws_l + hrow * nsp;
+  const float* arow = p.ws_acc + hrow * nsp * kHD + 2 * lane;
+
+  const uint32_t ch2 = *(const uint32_t*)(p.vch + ((int64_t)b * p.G + g) * kHD + 2 * lane);
+  float2 av[kCombPF];
+#pragma unroll
+  for (int u = 0; u < kCombPF; ++u)
+    av[u] = s_lo + u < s_hi ? *(const float2*)(arow + (int64_t)(s_lo + u) * kHD) : make_float2(0.f, 0.f);
+  float m0 = -INFINITY, l0 = 0.f;
+  if (s_lo + lane < s_hi) { m0 = mrow[s_lo + lane]; l0 = lrow[s_lo + lane]; }
+  float mw = m0;
+  for (int s = s_lo + 64 + lane; s < s_hi; s += 64) mw = fmaxf(mw, mrow[s]);
+  mw = wave64_reduce(mw, OpMax());
+  if (lane == 0) wmax[w] = mw;
   __syncthreads();
 
-  // extra-token scores: 4 threads per token, 32 dims each, two shuffles
-  const float inv_sqrt = 0.08838834764831845f;  // 1/sqrt(128)
-  for (int x0 = 0; x0 < n_x; x0 += kThreads / 4) {
-    const int x = x0 + tid / 4, qd = tid & 3;
-    float d[kGQA] = {0.f, 0.f, 0.f, 0.f};
-    int mpos = 0;
-    if (x < n_x) {
-      const uint4* kr = (const uint4*)(extra_row(p, b, g, x, false, &mpos) + 32 * qd);
-      uint4 kv[4];
+  float M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  if (M == -INFINITY) M = 0.f;  // everything masked: all weights are zero
+
+  const float wt0 = m0 == -INFINITY ? 0.f : exp2f(m0 - M);
+  float L = wt0 * l0;
+  for (int s = s_lo + 64 + lane; s < s_hi; s += 64) {
+    const float m = mrow[s];
+    if (m != -INFINITY) L += exp2f(m - M) * lrow[s];
+  }
+  float2 Sr = make_float2(0.f, 0.f), Sp = make_float2(0.f, 0.f);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kv[c] = kr[c];
+  for (int u = 0; u < kCombPF; ++u) {
+    const float wg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt0), u));
+    const bool rot = s_lo + u < ns;
+    const float wr = rot ? wg : 0.f, wp = rot ? 0.f : wg;
+    Sr.x += wr * av[u].x; Sr.y += wr * av[u].y;
+    Sp.x += wp * av[u].x; Sp.y += wp * av[u].y;
+  }
+  for (int s0 = s_lo + kCombPF; s0 < s_hi; s0 += kCombPF) {
+    float2 bv[kCombPF];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const half8 h = __builtin_bit_cast(half8, kv[c]);
+    for (int u = 0; u < kCombPF; ++u)
+      bv[u] = s0 + u < s_hi ? *(const float2*)(arow + (int64_t)(s0 + u) * kHD) : make_float2(0.f, 0.f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kf = (float)h[e];
-#pragma unroll
-          for (int a = 0; a < kGQA; ++a) d[a] += qs[a][32 * qd + 8 * c + e] * kf;
-        }
+    for (int u = 0; u < kCombPF; ++u) {
+      const int s = s0 + u;
+      if (s < s_hi) {
+        const float m = mrow[s];
+        const float wg = m == -INFINITY ? 0.f : exp2f(m - M);
+        const float wr = s < ns ? wg : 0.f, wp = s < ns ? 0.f : wg;
+        Sr.x += wr * bv[u].x; Sr.y += wr * bv[u].y;
+        Sp.x += wp * bv[u].x; Sp.y += wp * bv[u].y;
       }
-    }
-#pragma unroll
-    for (int a = 0; a < kGQA; ++a) {
-      d[a] += __shfl_xor(d[a], 1, 64);
-      d[a] += __shfl_xor(d[a], 2, 64);
-    }
-    if (x < n_x && qd == 0) {
-      const float madd = p.mask ? p.mask[(int64_t)b * p.mask_stride + mpos] : 0.f;
-      *(float4*)&sx[x][0] = make_float4(d[0] * inv_sqrt + madd, d[1] * inv_sqrt + madd,
-                                        d[2] * inv_sqrt + madd, d[3] * inv_sqrt + madd);
     }
   }
+  rrot[w][lane] = Sr;
+  rpl[w][lane] = Sp;
+  L = wave64_reduce(L, OpAdd());
+  if (lane == 0) wsum[w] = L;
   __syncthreads();
 
-  // per query head (wave w = head a): global max, split weights, total sum
-  {
-    const int a = w;
-    const int64_t base = ((int64_t)b * p.H + g * kGQA + a) * p.n_splits;
-    float msp[kMaxSplits / 64];
-    float m = -INFINITY;
+  // wave 0: ch, one inverse FWHT, the plain-basis part, normalization
+  if (w == 0) {
+    float2 t = rrot[0][lane], xs = rpl[0][lane];
 #pragma unroll
-    for (int k = 0; k < kMaxSplits / 64; ++k) {
-      const int s = lane + 64 * k;
-      msp[k] = s < p.n_splits ? p.ws_m[base + s] : -INFINITY;
-      m = fmaxf(m, msp[k] * (1.0f / kLog2e));
+    for (int u = 1; u < 4; ++u) {
+      const float2 a = rrot[u][lane], c = rpl[u][lane];
+      t.x += a.x; t.y += a.y;
+      xs.x += c.x; xs.y += c.y;
     }
-    for (int x = lane; x < n_x; x += 64) m = fmaxf(m, sx[x][a]);
-    m = wave_max(m);
-    float l = 0.f;
-#pragma unroll
-    for (int k = 0; k < kMaxSplits / 64; ++k) {
-      const int s = lane + 64 * k;
-      if (s < p.n_splits) {
-        const float wv = (msp[k] == -INFINITY) ? 0.f : exp2f(msp[k] - m * kLog2e);
-        wsp[a][s] = wv;
-        l += wv * p.ws_l[base + s];
-      }
-    }
-    for (int x = lane; x < n_x; x += 64) {
-      const float e = expf(sx[x][a] - m);
-      sx[x][a] = e;
-      l += e;
-    }
-    l = wave_sum(l);
-    if (lane == 0) { Ms[a] = m; Ls[a] = l; }
-  }
-  __syncthreads();
-
-  // compressed part: sum_s w_s acc_s (dims 2l, 2l+1), times ch, one inverse FWHT
-  float f0, f1;
-  {
-    const int a = w;
-    const float* ac = p.ws_acc + ((int64_t)b * p.H + g * kGQA + a) * p.n_splits * kHD + 2 * lane;
-    float s0 = 0.f, s1 = 0.f;
-    int s = 0;
-    for (; s + 16 <= p.n_splits; s += 16) {
-      float2 v[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = *(const float2*)(ac + (int64_t)(s + u) * kHD);
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        s0 += wsp[a][s + u] * v[u].x;
-        s1 += wsp[a][s + u] * v[u].y;
-      }
-    }
-    for (; s < p.n_splits; ++s) {
-      const float2 v = *(const float2*)(ac + (int64_t)s * kHD);
-      s0 += wsp[a][s] * v.x;
-      s1 += wsp[a][s] * v.y;
-    }
-    const uint32_t ch2 = *(const uint32_t*)(p.vch + ((int64_t)b * p.G + g) * kHD + 2 * lane);
     const half2v chh = __builtin_bit_cast(half2v, ch2);
-    f0 = s0 * (float)chh[0];
-    f1 = s1 * (float)chh[1];
+    float f0 = t.x * (float)chh[0], f1 = t.y * (float)chh[1];
     fwht128_pairs(f0, f1);
-  }
-
-  // fp16 segments and stream values: thread (token subset w, dims 2l, 2l+1)
-  float ax0[kGQA], ax1[kGQA];
-#pragma unroll
-  for (int a = 0; a < kGQA; ++a) { ax0[a] = 0.f; ax1[a] = 0.f; }
-  for (int xb = w; xb < n_x; xb += 4 * 8) {
-    uint32_t vv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int x = xb + 4 * u;
-      int mpos;
-      vv[u] = x < n_x ? *(const uint32_t*)(extra_row(p, b, g, x, true, &mpos) + 2 * lane) : 0u;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int x = xb + 4 * u;
-      if (x < n_x) {
-        const half2v h = __builtin_bit_cast(half2v, vv[u]);
-        const float4 e4 = *(const float4*)&sx[x][0];
-        const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
-#pragma unroll
-        for (int a = 0; a < kGQA; ++a) {
-          ax0[a] += ev[a] * (float)h[0];
-          ax1[a] += ev[a] * (float)h[1];
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int a = 0; a < kGQA; ++a) *(float2*)&red[w][a][2 * lane] = make_float2(ax0[a], ax1[a]);
-  __syncthreads();
-  {
-    const int a = w;
-    float t0 = 0.f, t1 = 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float2 r2 = *(const float2*)&red[u][a][2 * lane];
-      t0 += r2.x;
-      t1 += r2.y;
-    }
-    const float inv_l = 1.0f / Ls[a];
+    const float inv_l = 1.0f / (wsum[0] + wsum[1] + wsum[2] + wsum[3]);
     half2v o;
-    o[0] = (half_t)((f0 + t0) * inv_l);
-    o[1] = (half_t)((f1 + t1) * inv_l);
-    *(half2v*)(p.out + ((int64_t)b * p.H + g * kGQA + a) * kHD + 2 * lane) = o;
+    o[0] = (half_t)((f0 + xs.x) * inv_l);
+    o[1] = (half_t)((f1 + xs.y) * inv_l);
+    *(half2v*)(p.out + hrow * kHD + 2 * lane) = o;
   }
 }
+
+#ifndef SHARD_DECODE_NB
+#define SHARD_DECODE_NB 1
+#endif
+// kv heads per split workgroup.  One head keeps the kernel at 2 waves per SIMD
+// (a single wave per SIMD issues an MFMA only every 32 cycles and a VALU op
+// every ~8), two heads halve the int4 unpacking per head at 1 wave per SIMD.
+constexpr int kNB = SHARD_DECODE_NB;
+constexpr int kSplitWavesPerSimd = kNB == 1 ? 2 : 1;
 
 inline int choose_splits(const shard_decode_args* a, int NB) {
-  if (a->n_splits > 0) return ((a->n_splits + 7) / 8) * 8;
-  const int HG = a->n_kv_heads / NB;
-  int want = (256 + HG * a->batch - 1) / (HG * a->batch);
-  int max_useful = (a->n_comp + kTile - 1) / kTile;
+  const int max_useful = (a->n_comp + kTile - 1) / kTile;
+  int want;
+  if (a->n_splits > 0) {
+    want = a->n_splits;
+  } else {
+    const int HG = a->n_kv_heads / NB;
+    const int target = 256 * kSplitWavesPerSimd;  // workgroups that fill 256 CUs
+    want = target / (HG * a->batch);
+  }
   if (want > max_useful) want = max_useful;
   if (want < 1) want = 1;
-  want = ((want + 7) / 8) * 8;
   if (want > kMaxSplits) want = kMaxSplits;
   return want;
 }
 
-constexpr int kNB = 2;
+
 
 template <int KS>
 void launch_split(const SplitParams& sp, dim3 grid, hipStream_t s) {
@@ -748,9 +827,10 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
 }
 
 size_t shard_decode_attn_workspace(const shard_decode_args* a) {
-  if (!a || a->batch <= 0 || a->n_q_heads <= 0) return 0;
-  const int ns = choose_splits(a, kNB);
-  return (size_t)a->batch * a->n_q_heads * ns * (kHD + 2) * sizeof(float);
+  if (!a || a->batch <= 0 || a->n_q_heads <= 0 || a->n_comp <= 0) return 0;
+  const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
+  const int nsp = choose_splits(a, kNB) + (n_x > 0 ? 1 : 0);
+  return (size_t)a->batch * a->n_q_heads * nsp * (kHD + 2) * sizeof(float);
 }
 
 int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t workspace_bytes,
@@ -770,18 +850,30 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
       (a->n_stream && (!a->s_k || !a->s_v)))
     return SHARD_ERR_ARG;
   const int ns = choose_splits(a, kNB);
+  const int nsp = ns + (n_x > 0 ? 1 : 0);
   if (!workspace || workspace_bytes < shard_decode_attn_workspace(a)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
 
   float* ws = (float*)workspace;
-  const int64_t nm = (int64_t)a->batch * a->n_q_heads * ns;
+  const int64_t nm = (int64_t)a->batch * a->n_q_heads * nsp;
   SplitParams sp;
   sp.B = a->batch; sp.H = a->n_q_heads; sp.G = a->n_kv_heads; sp.rank = a->rank;
   sp.n_comp = a->n_comp; sp.cstart = a->compress_start; sp.pos_q = a->pos_q;
   sp.n_splits = ns;
-  int chunk = (a->n_comp + ns - 1) / ns;
-  chunk = ((chunk + kTile - 1) / kTile) * kTile;
-  sp.chunk = chunk;
+  // Compressed tiles per split, in whole 32-token tiles.  The last split of
+  // each head also runs the extra tokens (an extra token costs about half a
+  // compressed one), so the tiles are spread over the splits as if there were
+  // n_x / 64 more of them and the last split takes what remains.
+  const int n_tiles = (a->n_comp + kTile - 1) / kTile;
+  const int x_cost = (n_x + 63) / 64;
+  sp.chunk = ((n_tiles + x_cost + ns - 1) / ns) * kTile;
+  sp.nsp = nsp;
+  sp.xs.sink_k = a->sink_k; sp.xs.sink_v = a->sink_v;
+  sp.xs.win_k = a->win_k; sp.xs.win_v = a->win_v;
+  sp.xs.dec_k = a->dec_k; sp.xs.dec_v = a->dec_v;
+  sp.xs.s_k = a->s_k; sp.xs.s_v = a->s_v;
+  sp.xs.n_sink = a->n_sink; sp.xs.n_win = a->n_win; sp.xs.n_dec = a->n_dec;
+  sp.xs.dec_stride = a->dec_stride; sp.xs.n_stream = a->n_stream; sp.xs.n_x = n_x;
   sp.q = a->q; sp.inv_freq = a->inv_freq; sp.coef = a->k_coeffs;
   sp.op = (const uint4*)a->prep;
   sp.rope = (const float2*)((const char*)a->prep + shard_decode_prepare_op_bytes(a->n_kv_heads, a->rank));
@@ -802,15 +894,10 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   SHARD_LAUNCH_CHECK("shard_decode_attn split");
 
   CombineParams cp;
-  cp.B = a->batch; cp.H = a->n_q_heads; cp.G = a->n_kv_heads; cp.n_comp = a->n_comp;
-  cp.n_splits = ns; cp.q = a->q; cp.vch = a->v_ch;
-  cp.sink_k = a->sink_k; cp.sink_v = a->sink_v; cp.n_sink = a->n_sink;
-  cp.win_k = a->win_k; cp.win_v = a->win_v; cp.n_win = a->n_win;
-  cp.dec_k = a->dec_k; cp.dec_v = a->dec_v; cp.n_dec = a->n_dec; cp.dec_stride = a->dec_stride;
-  cp.s_k = a->s_k; cp.s_v = a->s_v; cp.n_stream = a->n_stream;
-  cp.mask = a->mask; cp.mask_stride = a->mask_stride;
+  cp.B = a->batch; cp.H = a->n_q_heads; cp.G = a->n_kv_heads;
+  cp.n_splits = ns; cp.nsp = nsp; cp.vch = a->v_ch;
   cp.ws_m = sp.ws_m; cp.ws_l = sp.ws_l; cp.ws_acc = sp.ws_acc; cp.out = a->out;
-  hipLaunchKernelGGL(k_decode_combine, dim3((unsigned)a->n_kv_heads, (unsigned)a->batch),
+  hipLaunchKernelGGL(k_decode_combine, dim3((unsigned)a->n_q_heads, (unsigned)a->batch),
                      dim3(kThreads), 0, s, cp);
   SHARD_LAUNCH_CHECK("shard_decode_attn combine");
   return SHARD_OK;
