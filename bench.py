@@ -52,21 +52,23 @@ def clone_format(fmt):
     return out
 
 
-def build_layer(T, dev, seed=0, n_stream=0):
+def build_layer(T, dev, seed=0, n_stream=0, with_layer=False):
     from shard_amd import Cache, bench_data
     from shard_amd.cache import compress_layer
     k, v = bench_data.make_kv(T, seed=seed)
     cache = Cache(num_layers=1, rope_inv_freq=bench_data.inv_freq())
     fmt = compress_layer(cache, k.to(dev), v.to(dev), 0)
+    layer = cache.layers[0]
+    layer._gpu_compressed = fmt
+    cache._compressed = True
     if n_stream:
-        layer = cache.layers[0]
-        layer._gpu_compressed = fmt
-        cache._compressed = True
         cache._streaming = True
         ks, vs = bench_data.make_stream_tokens(n_stream, seed=seed)
         for i in range(n_stream):
             layer._stream_append(ks[i].to(dev), vs[i].to(dev))
     torch.cuda.synchronize()
+    if with_layer:
+        return fmt, k, v, layer
     return fmt, k, v
 
 
@@ -80,7 +82,7 @@ def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, 
     copies = [fmt] + [clone_format(fmt) for _ in range(n_copies - 1)]
     calls = [ops.make_decode_args(q, c, pos_q, None, n_splits=n_splits, stream_n=stream_n)
              for c in copies]
-    ws = torch.empty(ops.decode_workspace_bytes(calls[0]), dtype=torch.uint8, device=q.device)
+    ws = ops.decode_workspace(calls[0])
     for i in range(warmup):
         ops.decode_attn(calls[i % n_copies], ws)
     torch.cuda.synchronize()
@@ -192,6 +194,172 @@ def cpu_baseline(fmt, q, pos_q, inv, budget_s=15.0):
                       f"{n}-token compressed context, median"}
 
 
+def read_traffic(T):
+    """HBM bytes per decode call measured with rocprofv3 PMC (FETCH_SIZE +
+    WRITE_SIZE of both kernels, copy-calibrated), from the committed summary
+    profiles/decode_traffic.md (a line `traffic_bytes_per_call T=<T>: <bytes>`)."""
+    path = os.path.join(ROOT, "profiles", "decode_traffic.md")
+    try:
+        import re
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_call T=(\d+):\s*(\d+)", line)
+                if m and int(m.group(1)) == T:
+                    return int(m.group(2))
+    except OSError:
+        pass
+    return None
+
+
+def calibrate_copy(dev, mib=256, reps=10):
+    """A plain device copy of known size, for calibrating the PMC byte counters
+    (run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"calibrate_copy": {"bytes_read_per_call": src.numel() * 4,
+                               "bytes_written_per_call": dst.numel() * 4, "calls": reps}}
+
+
+def stream_curve(dev, T=32768, n_stream=512, reps=10):
+    """32K compressed context, append a 512-token 8-bit
+    stream one token at a time (K and V through the Lloyd-Max quantizer) and
+    time the decode call at every stream length."""
+    from shard_amd import ops, bench_data
+    fmt, k, v, layer = build_layer(T, dev, with_layer=True)
+    layer._cache_ref._streaming = True
+    q = bench_data.make_q().to(dev).view(1, 32, 128)
+    ks, vs = bench_data.make_stream_tokens(n_stream)
+    ks, vs = ks.to(dev), vs.to(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ws = None
+    us_decode, us_append = [], []
+    for s in range(n_stream):
+        e0.record()
+        layer._stream_append(ks[s], vs[s])
+        e1.record()
+        torch.cuda.synchronize()
+        us_append.append(e0.elapsed_time(e1) * 1000.0)
+        call = ops.make_decode_args(q, fmt, T + s, None, stream_n=s + 1)
+        if ws is None or ws.numel() < ops.decode_workspace_bytes(call):
+            ws = torch.zeros(2 * ops.decode_workspace_bytes(call), dtype=torch.uint8, device=dev)
+        ops.decode_attn(call, ws)
+        e0.record()
+        for _ in range(reps):
+            ops.decode_attn(call, ws)
+        e1.record()
+        torch.cuda.synchronize()
+        us_decode.append(e0.elapsed_time(e1) * 1000.0 / reps)
+    pts = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512]
+    import statistics
+    slope = (statistics.mean(us_decode[-32:]) - statistics.mean(us_decode[:32])) / (n_stream - 32)
+    return {"metric": "decode attn us/layer-step vs 8-bit stream length (BASELINE config 3)",
+            "unit": "us/layer-step", "n_comp": fmt["n_compress"], "context": T,
+            "points": [[p, round(us_decode[p - 1], 3)] for p in pts if p <= n_stream],
+            "median_us": round(statistics.median(us_decode), 3),
+            "min_us": round(min(us_decode), 3), "max_us": round(max(us_decode), 3),
+            "slope_ns_per_stream_token": round(slope * 1000.0, 2),
+            "append_us_median": round(statistics.median(us_append), 3),
+            "timing": f"HIP events around {reps} eager calls per stream length"}
+
+
+def prefill(dev, layers=32, batch=4, T=8192):
+    """compression kernels over `layers` x batch x T tokens of
+    synthetic K (low-rank Gaussian, RoPE'd) and V.  Per layer: undo-RoPE into
+    the fp16 GEMM operand, MFMA projection onto a fixed random-orthonormal
+    1024x192 basis, per-column int4 quantization + packing, FWHT + channel
+    normalization of V, nearest-centroid assignment to a seeded codebook."""
+    from shard_amd import ops, bench_data
+    G, D, R = 8, 128, 192
+    basis = bench_data.random_orthonormal_basis(G * D, R).to(dev)
+    bt = basis.t().contiguous().half()                            # (R, G*D)
+    bits = torch.full((R,), 4, dtype=torch.int32, device=dev)
+    invf = bench_data.inv_freq().to(dev)
+    mean = torch.zeros(G * D, dtype=torch.float32, device=dev)
+    data, mix = [], None
+    for li in range(layers):
+        k, v, mix = bench_data.make_kv_device(T, batch, li, dev, mix=mix)
+        data.append((k, v))
+    x0, _, _ = ops.vq_prepare(data[0][1].reshape(batch * G, T, D))
+    gsel = torch.Generator(device=dev).manual_seed(42)
+    codebook = x0[torch.randperm(x0.shape[0], generator=gsel, device=dev)[:256]].contiguous()
+    del x0
+
+    def layer_pass(k, v, ev=None):
+        kp = ops.k_prepare(k, 0, T, invf, mean)
+        if ev is not None:
+            ev[0].record()
+        proj = ops.pca_project(kp, bt)
+        if ev is not None:
+            ev[1].record()
+        chain = ops.int4_quant_pack(proj, bits)
+        x, _, _ = ops.vq_prepare(v.reshape(batch * G, T, D))
+        idx = ops.vq_assign(x, codebook)
+        return chain, idx
+
+    layer_pass(*data[0])                                           # warm-up
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(layers)]
+    e0.record()
+    for li in range(layers):
+        layer_pass(*data[li], evs[li])
+    e1.record()
+    torch.cuda.synchronize()
+    total_s = e0.elapsed_time(e1) / 1000.0
+    gemm_s = sum(a.elapsed_time(b) for a, b in evs) / 1000.0
+    flops = 2.0 * batch * T * G * D * R * layers
+    return {"metric": "prefill compression tokens/s (BASELINE config 4)", "unit": "tokens/s",
+            "value": round(batch * T / total_s, 1),
+            "config": {"layers": layers, "batch": batch, "tokens": T, "rank": R,
+                       "data": "synthetic, generated on device"},
+            "ms_total": round(total_s * 1000.0, 3),
+            "projection": {"ms": round(gemm_s * 1000.0, 3),
+                           "tflops": round(flops / gemm_s / 1e12, 2),
+                           "mfma_util_fp16": round(flops / gemm_s / 2.5e15, 4)}}
+
+
+def _to(x, dev):
+    if torch.is_tensor(x):
+        return x.to(dev)
+    if isinstance(x, dict):
+        return {k: _to(v, dev) for k, v in x.items()}
+    return x
+
+
+def save_layer(dev, T, path):
+    """Compress the benchmark layer once and store it (the PMC runs load it, so
+    the profiled process runs no SVD)."""
+    fmt, _, _ = build_layer(T, dev)
+    torch.save(_to(fmt, "cpu"), path)
+    return {"saved_layer": path, "context": T}
+
+
+def pmc_workload(dev, T, calls=200, layer_path=None):
+    """Eager decode calls rotating over cold copies of the layer: the workload
+    profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (no graph replay)."""
+    from shard_amd import ops, bench_data
+    if layer_path:
+        fmt = _to(torch.load(layer_path, weights_only=True), dev)
+    else:
+        fmt, _, _ = build_layer(T, dev)
+    q = bench_data.make_q().to(dev).view(1, 32, 128)
+    n_copies = max(2, math.ceil(2 * 256e6 / algorithmic_bytes(fmt["n_compress"], fmt["rank_pad"])))
+    copies = [fmt] + [clone_format(fmt) for _ in range(n_copies - 1)]
+    cl = [ops.make_decode_args(q, c, T, None) for c in copies]
+    ws = ops.decode_workspace(cl[0])
+    for i in range(calls):
+        ops.decode_attn(cl[i % n_copies], ws)
+    torch.cuda.synchronize()
+    return {"pmc_workload": {"context": T, "calls": calls, "copies": n_copies,
+                             "algorithmic_bytes_per_call": algorithmic_bytes(fmt["n_compress"],
+                                                                             fmt["rank_pad"])}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,6 +370,17 @@ def main():
     ap.add_argument("--no-32k", dest="also_32k", action="store_false")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--n-splits", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run a 256 MiB device copy (PMC byte-counter calibration) and exit")
+    ap.add_argument("--stream-curve", action="store_true",
+                    help="BASELINE config 3: decode time vs 8-bit stream length at 32K")
+    ap.add_argument("--prefill", action="store_true",
+                    help="BASELINE config 4: prefill compression kernels, tokens/s")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="eager decode calls over cold layer copies at --ctx (for rocprofv3 --pmc)")
+    ap.add_argument("--save-layer", default=None,
+                    help="compress the --ctx layer, save it to this path and exit")
+    ap.add_argument("--layer", default=None, help="--pmc-workload: load the layer saved here")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the compressed-KV decode path "
@@ -212,6 +391,21 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     from shard_amd import bench_data
+    if args.calibrate_copy:
+        print(json.dumps(calibrate_copy(dev)), flush=True)
+        return
+    if args.stream_curve:
+        print(json.dumps(stream_curve(dev)), flush=True)
+        return
+    if args.prefill:
+        print(json.dumps(prefill(dev)), flush=True)
+        return
+    if args.save_layer:
+        print(json.dumps(save_layer(dev, args.ctx, args.save_layer)), flush=True)
+        return
+    if args.pmc_workload:
+        print(json.dumps(pmc_workload(dev, args.ctx, layer_path=args.layer)), flush=True)
+        return
 
     def measure(T, with_baselines):
         fmt, k, v = build_layer(T, dev)
@@ -258,7 +452,7 @@ def main():
         "speedup_vs_fp16_sdpa": round(r8["sdpa_us"] / us, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": read_traffic(args.ctx),
                      "kernel": "shard_decode_attn (k_decode_split + k_decode_combine), per call",
                      "mfma_frac_fp16": round(r8["flops"] / (us * 1e-6) / 2.5e15, 4)},
     }

@@ -55,6 +55,31 @@ def make_kv(T: int, batch: int = 1, seed: int = 0, n_kv: int = N_KV, hd: int = H
     return k.half().contiguous(), v.half().contiguous()
 
 
+def make_kv_device(T: int, batch: int, seed: int, device, n_kv: int = N_KV, hd: int = HD,
+                   mix=None):
+    """make_kv's distributions generated on the device (for the many-layer
+    prefill benchmark): returns (k_rope fp16, v fp16, mix) with shapes
+    (batch, n_kv, T, hd).  `mix` (the scaled component matrix, D x D) can be
+    passed back in to skip its QR; it is built from ``seed`` on the CPU."""
+    D = n_kv * hd
+    if mix is None:
+        g = torch.Generator().manual_seed(seed)
+        W, _ = torch.linalg.qr(torch.randn(D, D, generator=g))
+        tau = 384.0 / math.log(100.0)
+        sigma = torch.exp(-torch.arange(D, dtype=torch.float32) / tau)
+        M = sigma[:, None] * W.T
+        mix = (M * (1.0 / M.pow(2).sum(0).sqrt())).to(device)
+    gd = torch.Generator(device=device).manual_seed(seed + 7)
+    z = torch.randn(batch * T, D, generator=gd, device=device)
+    kn = (z @ mix).view(batch, T, n_kv, hd).permute(0, 2, 1, 3)
+    k = apply_rope(kn, torch.arange(T, device=device), inv_freq(hd).to(device))
+    v = torch.randn(batch * T, D, generator=gd, device=device)
+    outl = torch.randperm(D, generator=gd, device=device)[:2]
+    v[:, outl] *= 8.0
+    v = v.view(batch, T, n_kv, hd).permute(0, 2, 1, 3)
+    return k.half().contiguous(), v.half().contiguous(), mix
+
+
 def make_q(batch: int = 1, seed: int = 0, n_q: int = N_Q, hd: int = HD):
     g = torch.Generator().manual_seed(seed + 1)
     return torch.randn(batch, n_q, 1, hd, generator=g).half()

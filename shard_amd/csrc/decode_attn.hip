@@ -36,6 +36,10 @@ constexpr int kGQA = 4;           // query heads per kv head
 constexpr int kMaxExtra = 2048;   // sink + window + decode + stream tokens per call
 constexpr int kMaxSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
+#ifndef SHARD_SPLIT_PER_XCD
+#define SHARD_SPLIT_PER_XCD 1
+#endif
+constexpr bool kSplitPerXcd = SHARD_SPLIT_PER_XCD;
 
 // The fp16 segments around the compressed span, in attention-mask order:
 // sink [0, n_sink), window, decode tokens, then the 8-bit stream (dequantized
@@ -331,14 +335,22 @@ void k_decode_split(const SplitParams p) {
   const int col = lane & 31;
   const int hh = lane >> 5;
 
-  // ---- block -> (head group, split).  Consecutive blocks are consecutive head
-  // groups of one split; the dispatcher deals blocks to the 8 XCDs in turn, so
-  // with 8 head groups every XCD serves one head group and its L2 holds that
-  // head's basis operands.
+  // ---- block -> (head group, split).  The dispatcher deals blocks to the 8
+  // XCDs in turn (block id mod 8).  With n_splits % 8 == 0 all head groups of
+  // one split get block ids congruent mod 8, so they share one XCD and its L2
+  // fetches the split's coefficient rows (read by every head) once; otherwise
+  // consecutive blocks are consecutive head groups of one split.
   const int HG = p.G / NB;
   const int bid = blockIdx.x;
-  const int hg = bid % HG;
-  const int split = bid / HG;
+  int hg, split;
+  if (kSplitPerXcd && (p.n_splits & 7) == 0) {
+    const int slot = bid >> 3;
+    hg = slot % HG;
+    split = (slot / HG) * 8 + (bid & 7);
+  } else {
+    hg = bid % HG;
+    split = bid / HG;
+  }
   const int b = blockIdx.y;
   // The last split of each head runs the extra tokens first (its compressed
   // chunk is shorter by their cost), so their cold loads overlap the other

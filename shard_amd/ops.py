@@ -319,12 +319,19 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
     return DecodeCall(a, keep)
 
 
+def decode_workspace(call: DecodeCall) -> torch.Tensor:
+    """A decode workspace for ``call`` (zero-filled; reusable by later calls,
+    one call at a time per buffer)."""
+    need = decode_workspace_bytes(call)
+    return torch.zeros(max(need, 16), dtype=torch.uint8, device=call.keep[0].device)
+
+
 def decode_attn(call: DecodeCall, ws: torch.Tensor = None) -> torch.Tensor:
     lib = _lib.load()
     q = call.keep[0]
     need = lib.shard_decode_attn_workspace(ctypes.byref(call.args))
     if ws is None or ws.numel() < need:
-        ws = _workspace(need, q.device)
+        ws = decode_workspace(call)
     _lib.check("shard_decode_attn", lib.shard_decode_attn(
         ctypes.byref(call.args), _p(ws), ws.numel(), _stream(q)))
     return call.keep[-1]
