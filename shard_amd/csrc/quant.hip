@@ -127,25 +127,34 @@ __global__ void k_int4_pack(const float* __restrict__ proj, int64_t n, int keep,
 // Stage h pairs element e with e^h: lower index gets a+b, upper a-b
 // (cache.py:14-18), stages in increasing h, then one IEEE division.
 // ---------------------------------------------------------------------------
+// One butterfly stage across lanes l and l ^ H (element stride H).
+template <int H, int E>
+__device__ __forceinline__ void fwht_lane_stage(float (&x)[E], int l) {
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    const float p = xor_lane<H>(x[k]);
+    x[k] = (l & H) ? sub_rn(p, x[k]) : add_rn(x[k], p);
+  }
+}
+
 template <int E>
 __device__ __forceinline__ void wave_fwht(float (&x)[E], int d) {
+  // d == 64 * E: element i = lane + 64 k; strides 1..32 cross lanes, 64.. cross registers
   const int l = (int)lane_id();
-  for (int h = 1; h < d; h <<= 1) {
-    if (h < 64) {
+  fwht_lane_stage<1>(x, l);
+  fwht_lane_stage<2>(x, l);
+  fwht_lane_stage<4>(x, l);
+  fwht_lane_stage<8>(x, l);
+  fwht_lane_stage<16>(x, l);
+  fwht_lane_stage<32>(x, l);
 #pragma unroll
-      for (int k = 0; k < E; ++k) {
-        float p = __shfl_xor(x[k], h, 64);
-        x[k] = (l & h) ? sub_rn(p, x[k]) : add_rn(x[k], p);
-      }
-    } else {
-      const int hk = h >> 6;
+  for (int hk = 1; hk < E; hk <<= 1) {
 #pragma unroll
-      for (int k = 0; k < E; ++k) {
-        if ((k & hk) == 0) {
-          float a = x[k], b = x[k | hk];
-          x[k] = add_rn(a, b);
-          x[k | hk] = sub_rn(a, b);
-        }
+    for (int k = 0; k < E; ++k) {
+      if ((k & hk) == 0) {
+        const float a = x[k], b = x[k | hk];
+        x[k] = add_rn(a, b);
+        x[k | hk] = sub_rn(a, b);
       }
     }
   }
@@ -198,13 +207,17 @@ __global__ void k_vq_rot(const uint16_t* __restrict__ v, int64_t bh, int64_t seq
                          uint32_t* __restrict__ chmax) {
   const int d = 64 * E;
   const int l = (int)lane_id();
-  int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  int64_t rows = bh * seq;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int64_t rows = bh * seq;
+  // each wave owns a contiguous run of rows, so bh changes at most a few times
+  const int64_t rpw = (rows + nwaves - 1) / nwaves;
+  const int64_t r_begin = wave * rpw;
+  const int64_t r_end = r_begin + rpw < rows ? r_begin + rpw : rows;
   // per-lane running channel max for the current bh (flushed when bh changes)
   int64_t cur = -1;
   float m[E];
-  for (int64_t r = wave; r < rows; r += nwaves) {
+  for (int64_t r = r_begin; r < r_end; ++r) {
     int64_t b = r / seq, t = r - b * seq;
     if (b != cur) {
       if (cur >= 0)
@@ -297,18 +310,34 @@ __global__ void k_km_hist(const int32_t* __restrict__ idx, int64_t n, int k,
   for (int i = threadIdx.x; i < k; i += blockDim.x) blk_hist[(int64_t)blockIdx.x * k + i] = h[i];
 }
 
-// For each centroid: exclusive scan over blocks (in place) and total count.
-__global__ void k_km_scan_blocks(int32_t* __restrict__ blk_hist, int64_t nblk, int k,
-                                 int32_t* __restrict__ count) {
-  int q = blockIdx.x * blockDim.x + threadIdx.x;
-  if (q >= k) return;
-  int32_t run = 0;
-  for (int64_t b = 0; b < nblk; ++b) {
-    int32_t v = blk_hist[b * k + q];
+// For each centroid (one workgroup): exclusive scan of its per-block counts
+// over the blocks (in place) and its total count.  Thread t owns a contiguous
+// run of blocks; run totals are scanned in LDS.
+__global__ __launch_bounds__(256) void k_km_scan_blocks(int32_t* __restrict__ blk_hist, int64_t nblk,
+                                                        int k, int32_t* __restrict__ count) {
+  __shared__ int32_t part[256];
+  const int q = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t per = (nblk + 255) / 256;
+  const int64_t b0 = (int64_t)t * per;
+  const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
+  int32_t sum = 0;
+  for (int64_t b = b0; b < b1; ++b) sum += blk_hist[b * k + q];
+  part[t] = sum;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {  // inclusive Hillis-Steele scan
+    const int32_t v = t >= o ? part[t - o] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int32_t run = t > 0 ? part[t - 1] : 0;
+  for (int64_t b = b0; b < b1; ++b) {
+    const int32_t v = blk_hist[b * k + q];
     blk_hist[b * k + q] = run;
     run += v;
   }
-  count[q] = run;
+  if (t == 255) count[q] = part[255];
 }
 
 __global__ void k_km_offsets(const int32_t* __restrict__ count, int k, int32_t* __restrict__ off) {
@@ -335,43 +364,58 @@ __global__ void k_km_scatter(const int32_t* __restrict__ idx, int64_t n, int k,
   perm[off[my] + blk_off[(int64_t)blockIdx.x * k + my] + rank] = (int32_t)r;
 }
 
+// One workgroup per centroid.  Its rows (perm[off .. off+cnt), increasing row
+// order) are gathered 256 at a time into LDS, dim-major, double-buffered; lanes
+// 0..D-1 of wave 0 then add them in order, one running sum per dim, while the
+// other threads gather the next chunk.
 template <int D>
-__global__ void k_km_sum(const float* __restrict__ x, const int32_t* __restrict__ perm,
-                         const int32_t* __restrict__ count, const int32_t* __restrict__ off,
-                         const float* __restrict__ c, int k, float* __restrict__ newc,
-                         uint32_t* __restrict__ maxd) {
-  // one wave per centroid; 64 rows are loaded in parallel, then added in
-  // increasing row order (every lane keeps the same running sums)
-  const int l = (int)lane_id();
-  int q = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-  if (q >= k) return;
-  int32_t cnt = count[q], o = off[q];
-  float acc[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j) acc[j] = 0.f;
-  for (int32_t base = 0; base < cnt; base += 64) {
-    int n_here = cnt - base < 64 ? cnt - base : 64;
-    float xv[D];
-    if (l < n_here) {
-      int64_t row = perm[o + base + l];
+__global__ __launch_bounds__(256) void k_km_sum(const float* __restrict__ x, const int32_t* __restrict__ perm,
+                                                const int32_t* __restrict__ count,
+                                                const int32_t* __restrict__ off,
+                                                const float* __restrict__ c, int k,
+                                                float* __restrict__ newc, uint32_t* __restrict__ maxd) {
+  __shared__ __align__(16) float buf[2][D][256];
+  const int q = blockIdx.x;
+  const int t = threadIdx.x;
+  const int32_t cnt = count[q], o = off[q];
+  float xv[D];
+  auto gather = [&](int32_t base) {
+    if (base + t < cnt) {
+      const int64_t row = perm[o + base + t];
 #pragma unroll
       for (int j = 0; j < D; ++j) xv[j] = x[row * D + j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < D; ++j) xv[j] = 0.f;
     }
-    for (int i = 0; i < n_here; ++i)
+  };
+  gather(0);
+  float acc = 0.f;
+  int cur = 0;
+  for (int32_t base = 0; base < cnt; base += 256) {
+    if (base + t < cnt) {
 #pragma unroll
-      for (int j = 0; j < D; ++j) acc[j] = add_rn(acc[j], __shfl(xv[j], i, 64));
+      for (int j = 0; j < D; ++j) buf[cur][j][t] = xv[j];
+    }
+    __syncthreads();
+    gather(base + 256);
+    if (t < D) {
+      const int n_here = cnt - base < 256 ? cnt - base : 256;
+      const float* col = buf[cur][t];
+      int i = 0;
+      for (; i + 4 <= n_here; i += 4) {
+        const float4 v = *(const float4*)(col + i);
+        acc = add_rn(acc, v.x);
+        acc = add_rn(acc, v.y);
+        acc = add_rn(acc, v.z);
+        acc = add_rn(acc, v.w);
+      }
+      for (; i < n_here; ++i) acc = add_rn(acc, col[i]);
+    }
+    cur ^= 1;
   }
-  if (l < D) {
-    float a = acc[0];
-#pragma unroll
-    for (int j = 1; j < D; ++j) a = (l == j) ? acc[j] : a;
-    int t = q * D + l;
-    float old = c[t];
-    float nv = cnt > 0 ? div_rn(a, (float)cnt) : old;
-    newc[t] = nv;
+  if (t < D) {
+    const int idx = q * D + t;
+    const float old = c[idx];
+    const float nv = cnt > 0 ? div_rn(acc, (float)cnt) : old;
+    newc[idx] = nv;
     atomicMax(maxd, __float_as_uint(fabsf(sub_rn(nv, old))));
   }
 }
@@ -558,7 +602,7 @@ int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int
   hipLaunchKernelGGL(k_fill_u32, dim3(grid_cap((nch + 255) / 256, 4096)), dim3(256), 0, s, chmax,
                      nch, 0u);
   int64_t rows = bh * seq;
-  int blocks = grid_cap((rows + 3) / 4, 8192);
+  int blocks = grid_cap((rows + 63) / 64, 2048);  // 16 rows per wave or more
   switch (hd) {
     case 64: hipLaunchKernelGGL(k_vq_rot<1>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
     case 128: hipLaunchKernelGGL(k_vq_rot<2>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
@@ -610,11 +654,11 @@ int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx
   int32_t* off = count + k;
   int32_t* perm = off + k;
   hipLaunchKernelGGL(k_km_hist, dim3((unsigned)nblk), dim3(KM_BLOCK), 0, s, idx, n, k, blk);
-  hipLaunchKernelGGL(k_km_scan_blocks, dim3((k + 255) / 256), dim3(256), 0, s, blk, nblk, k, count);
+  hipLaunchKernelGGL(k_km_scan_blocks, dim3((unsigned)k), dim3(256), 0, s, blk, nblk, k, count);
   hipLaunchKernelGGL(k_km_offsets, dim3(1), dim3(64), 0, s, count, k, off);
   hipLaunchKernelGGL(k_km_scatter, dim3((unsigned)nblk), dim3(KM_BLOCK), 0, s, idx, n, k, blk, off, perm);
   hipLaunchKernelGGL(k_km_zero, dim3(1), dim3(1), 0, s, (uint32_t*)max_delta);
-  unsigned kb = (unsigned)((k + 3) / 4);
+  const unsigned kb = (unsigned)k;
   switch (d) {
     case 1: hipLaunchKernelGGL(k_km_sum<1>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
     case 2: hipLaunchKernelGGL(k_km_sum<2>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
