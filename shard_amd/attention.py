@@ -134,5 +134,6 @@ def enable_llama_fused_attention(model=None):
         return self.o_proj(out), None
 
     forward._shard_amd_patched = True
+    forward.__wrapped__ = original
     LlamaAttention.forward = forward
     return True
