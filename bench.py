@@ -360,6 +360,112 @@ def pmc_workload(dev, T, calls=200, layer_path=None):
                                                                              fmt["rank_pad"])}}
 
 
+def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
+    """random-init Llama-3.1-8B architecture (fp16) with the
+    shard Cache (8-bit stream on, fused decode attention) against the fp16
+    DynamicCache on the same GPU, as benchmarks/benchmark.py:614-726 measures it:
+    prefill, one-time compression and greedy decode timed separately;
+    tokens/s = batch x new_tokens / decode seconds."""
+    from transformers import LlamaConfig, LlamaForCausalLM, DynamicCache
+    from shard_amd import Cache, enable_llama_fused_attention
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336,
+                      num_hidden_layers=layers, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, max_position_embeddings=131072, rope_theta=500000.0)
+    def progress(msg):
+        print(f"[e2e] {msg}", file=sys.stderr, flush=True)
+
+    torch.manual_seed(seed)
+    t_init = time.perf_counter()
+    with torch.device(dev):
+        model = LlamaForCausalLM(cfg).to(torch.float16).eval()
+    enable_llama_fused_attention(model)
+    progress(f"model built in {time.perf_counter() - t_init:.1f} s")
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, cfg.vocab_size, (batch, prompt), generator=g).to(dev)
+
+    def sync_time():
+        torch.cuda.synchronize()
+        return time.perf_counter()
+
+    def compress_with_progress(cache):
+        # Cache.compress, one layer at a time with a progress line per layer
+        from shard_amd.cache import compress_layer
+        for li, layer in enumerate(cache.layers):
+            layer._gpu_compressed = compress_layer(cache, layer._keys, layer._values, li)
+            layer._keys = None
+            layer._values = None
+            layer._needs_decompress = True
+            torch.cuda.synchronize()
+            progress(f"compressed layer {li}")
+        cache._compressed = True
+
+    def decode(cache, first, n):
+        nxt, toks = first, []
+        t0 = sync_time()
+        with torch.no_grad():
+            for _ in range(n):
+                out = model(nxt, past_key_values=cache, use_cache=True)
+                nxt = out.logits[:, -1:].argmax(-1)
+                toks.append(nxt)
+        t1 = sync_time()
+        return t1 - t0, torch.cat(toks, 1)
+
+    with torch.no_grad():                      # warm-up on a short prompt (kernels, allocator)
+        wc = Cache.from_model(model)
+        wc._streaming = True
+        model(ids[:, :512], past_key_values=wc, use_cache=True, logits_to_keep=1)
+        progress("warm-up prefill")
+        decode(wc, ids[:, :1], 2)
+        progress("warm-up decode (includes compression)")
+        del wc
+        model(ids[:, :512], past_key_values=DynamicCache(), use_cache=True, logits_to_keep=1)
+    torch.cuda.empty_cache()
+    progress("warm-up done")
+    res = {}
+    for kind in ("fp16", "shard"):
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        if kind == "fp16":
+            cache = DynamicCache()
+        else:
+            cache = Cache.from_model(model)
+            cache._streaming = True
+        t0 = sync_time()
+        with torch.no_grad():
+            out = model(ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        first = out.logits[:, -1:].argmax(-1)
+        del out
+        t1 = sync_time()
+        r = {"prefill_s": round(t1 - t0, 3), "peak_prefill_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2)}
+        progress(f"{kind}: prefill {r['prefill_s']} s")
+        if kind == "shard":
+            compress_with_progress(cache)
+            t2 = sync_time()
+            r["compress_s"] = round(t2 - t1, 3)
+            r["peak_compress_gb"] = round(torch.cuda.max_memory_allocated() / 1e9, 2)
+            r["clean_compress_ratio"] = round(cache.clean_compress_ratio(), 2)
+        torch.cuda.reset_peak_memory_stats()
+        dt, toks = decode(cache, first, new_tokens)
+        r["decode_s"] = round(dt, 3)
+        r["tokens_per_s"] = round(batch * new_tokens / dt, 1)
+        r["ms_per_step"] = round(dt / new_tokens * 1000.0, 3)
+        r["peak_decode_gb"] = round(torch.cuda.max_memory_allocated() / 1e9, 2)
+        r["tokens"] = toks.cpu()
+        progress(f"{kind}: decode {r['decode_s']} s, {r['tokens_per_s']} tokens/s")
+        res[kind] = r
+        del cache
+    match = (res["fp16"]["tokens"] == res["shard"]["tokens"]).float().mean().item()
+    for r in res.values():
+        r.pop("tokens")
+    return {"metric": "e2e decode tokens/s, shard cache vs fp16 cache (BASELINE config 5)",
+            "unit": "tokens/s", "value": res["shard"]["tokens_per_s"],
+            "vs_fp16_cache": round(res["shard"]["tokens_per_s"] / res["fp16"]["tokens_per_s"], 3),
+            "config": {"model": "Llama-3.1-8B architecture, random init, fp16", "layers": layers,
+                       "batch": batch, "prompt": prompt, "new_tokens": new_tokens,
+                       "data": "random token ids (seeded)"},
+            "shard": res["shard"], "fp16": res["fp16"], "greedy_token_match_rate": round(match, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -378,6 +484,12 @@ def main():
                     help="BASELINE config 4: prefill compression kernels, tokens/s")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="eager decode calls over cold layer copies at --ctx (for rocprofv3 --pmc)")
+    ap.add_argument("--e2e", action="store_true",
+                    help="BASELINE config 5: random Llama-3.1-8B, shard cache vs fp16 cache")
+    ap.add_argument("--e2e-batch", type=int, default=16)
+    ap.add_argument("--e2e-prompt", type=int, default=16384)
+    ap.add_argument("--e2e-new", type=int, default=128)
+    ap.add_argument("--e2e-layers", type=int, default=32)
     ap.add_argument("--save-layer", default=None,
                     help="compress the --ctx layer, save it to this path and exit")
     ap.add_argument("--layer", default=None, help="--pmc-workload: load the layer saved here")
@@ -399,6 +511,10 @@ def main():
         return
     if args.prefill:
         print(json.dumps(prefill(dev)), flush=True)
+        return
+    if args.e2e:
+        print(json.dumps(e2e(dev, args.e2e_batch, args.e2e_prompt, args.e2e_new,
+                             args.e2e_layers)), flush=True)
         return
     if args.save_layer:
         print(json.dumps(save_layer(dev, args.ctx, args.save_layer)), flush=True)

@@ -4,7 +4,7 @@ API and state machine follow the reference's cache.py (Cache: 295-539,
 CacheLayer: 64-292):
   prefill (q_len > 1)     fp16 K/V kept as-is (cache.py:142-147)
   first decode step       Cache.compress() of every layer (cache.py:149-151, 338-460):
-                          K -> undo RoPE -> PCA (svd_lowrank) -> DP bits -> int8
+                          K -> undo RoPE -> PCA (covariance eigh) -> DP bits -> int8
                           basis -> projection (MFMA) -> group quant -> int4 (HIP);
                           V -> Hadamard -> k-means VQ (HIP assign + update);
                           sink (4) and window (64) tokens stay fp16.
@@ -344,14 +344,19 @@ class Cache(HFCache):
         return sum(_nb(l._keys) + _nb(l._values) for l in self.layers if l._keys is not None)
 
     def fp16_equivalent_bytes(self):
+        # the reference counts one batch row (cache.py:518-528); all rows here,
+        # so that the ratios stay meaningful for batch > 1 (stream_n counts
+        # tokens x batch rows)
         gc = self.layers[0]._gpu_compressed
         if gc is not None:
-            seq = gc["n_compress"] + self._sink_tokens + self._residual_window + gc.get("stream_n", 0)
+            batch = gc.get("batch", 1)
+            seq = (gc["n_compress"] + self._sink_tokens + self._residual_window
+                   + gc.get("stream_n", 0) // max(batch, 1))
         elif self.layers[0]._keys is not None:
-            seq = self.layers[0]._keys.shape[2]
+            batch, seq = self.layers[0]._keys.shape[0], self.layers[0]._keys.shape[2]
         else:
             return 0
-        return seq * self._n_kv_heads * self.head_dim * 4 * self._num_layers
+        return batch * seq * self._n_kv_heads * self.head_dim * 4 * self._num_layers
 
     def compress_ratio(self):
         return self.fp16_equivalent_bytes() / max(self.memory_bytes(), 1)
@@ -360,9 +365,25 @@ class Cache(HFCache):
         gc = self.layers[0]._gpu_compressed
         if gc is not None:
             seq = gc["n_compress"] + self._sink_tokens + self._residual_window
-            fp16_bytes = seq * self._n_kv_heads * self.head_dim * 4 * self._num_layers
+            fp16_bytes = (gc.get("batch", 1) * seq * self._n_kv_heads * self.head_dim * 4
+                          * self._num_layers)   # all batch rows (the reference counts one)
             return fp16_bytes / max(self.clean_memory_bytes(), 1)
         return self.compress_ratio()
+
+
+def pca_basis(centered: torch.Tensor, rank: int):
+    """Top-`rank` principal directions of the centered rows and their variances
+    (S^2 / n), the quantities _compress_k takes from svd_lowrank(q=rank,
+    niter=24) (cache.py:376-378).  The reference's randomized subspace iteration
+    converges to this subspace; here it is computed exactly and
+    deterministically: the fp32 covariance X^T X / n on the GPU (one GEMM), then
+    a float64 symmetric eigendecomposition of the (p, p) matrix on the host."""
+    n = centered.shape[0]
+    cov = (centered.t() @ centered) / n
+    evals, evecs = torch.linalg.eigh(cov.double().cpu())
+    evals = evals.flip(0)[:rank].clamp(min=0.0)
+    evecs = evecs.flip(1)[:, :rank]
+    return evecs.float().to(centered.device), evals.float().to(centered.device)
 
 
 def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li: int,
@@ -397,9 +418,7 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     if basis is None and cache._basis_override is not None:
         basis = cache._basis_override.get(li)
     if basis is None:
-        _, S, V = torch.svd_lowrank(centered, q=rank, niter=24)
-        basis = V[:, :rank]
-        eig = (S[:rank].float() ** 2) / n
+        basis, eig = pca_basis(centered, rank)
     else:
         basis = basis.to(dev, torch.float32)[:, :rank]
         eig = (centered @ basis).pow(2).mean(dim=0)

@@ -172,14 +172,32 @@ def kmeans_update(x: torch.Tensor, idx: torch.Tensor, centroids: torch.Tensor, w
     return newc, maxd
 
 
+_init_rows = {}
+
+
+def _kmeans_init_rows(n: int, k: int, seed: int) -> torch.Tensor:
+    """First k entries of randperm(n) from a CPU generator seeded with `seed`.
+    Every layer of a cache draws with the same seed (cache.py:21-26), so the
+    rows repeat for equal n; a full CPU randperm of tens of millions of rows
+    takes seconds, so it is drawn once per (n, k, seed)."""
+    key = (int(n), int(k), int(seed))
+    rows = _init_rows.get(key)
+    if rows is None:
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        rows = torch.randperm(n, generator=g)[:k].clone()
+        if len(_init_rows) > 64:
+            _init_rows.clear()
+        _init_rows[key] = rows
+    return rows
+
+
 def kmeans(data: torch.Tensor, k: int, n_iter: int = 30, seed: int = 42):
     """k-means of cache.py:21-39 on the GPU: CPU-generator randperm init, then
     assign (shard_vq_assign) + deterministic update per iteration; stops like the
     reference (max |delta| < 1e-4 once it >= 5) and returns the last assignment
     (made against the pre-update centroids) with the final centroids."""
     n, d = data.shape
-    g = torch.Generator(device="cpu").manual_seed(seed)
-    perm = torch.randperm(n, generator=g)[:k].to(data.device)
+    perm = _kmeans_init_rows(n, k, seed).to(data.device)
     centroids = data[perm].clone()
     lib = _lib.load()
     ws = _workspace(lib.shard_kmeans_update_workspace(n, centroids.shape[0]), data.device)
