@@ -141,10 +141,32 @@ int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd,
 /* Stream dequantizer, bit-exact with _dequant_stream / dequantize_per_token
  * (cache.py:275-278, streaming.py:74-79, qjl off):
  *   y = fp16(fp16(hadamard(codebook[idx]) * signs) * norm)
- * idx (rows, hd) uint8, norm (rows) fp16 -> y (rows, hd) fp16; hd = 128. */
+ * idx (rows, hd) uint8, norm (rows) fp16 -> y (rows, hd) fp16; hd in {64, 128, 256}. */
 int shard_stream_dequant(const uint8_t* idx, const uint16_t* norm, int64_t rows, int32_t hd,
                          const float* signs, const float* codebook, uint16_t* y,
                          void* stream);
+
+/* shard_stream_quant with the 1-bit QJL residual (quantize_per_token with
+ * qjl=True, streaming.py:67-70; stored by cache.py:234-240):
+ *   res = r - codebook[idx] (fp32); qsign (rows, hd) uint8 = res >= 0;
+ *   qscale (rows) fp16 = fp16(mean |res|), the sum in torch CPU's order for a
+ *   contiguous fp32 row (element i into accumulator (i/8) % 4, lane i % 8, in
+ *   increasing i; accumulators then lanes added in order), divided by hd;
+ *   `deq` includes the residual: fp16(fp16(hadamard(codebook[idx] + (2 qsign - 1)
+ *   qscale) * signs) * norm) (streaming.py:74-79, cache.py:275-278).
+ * qsign and qscale are both null (exactly shard_stream_quant) or both set. */
+int shard_stream_quant_qjl(const uint16_t* x, int64_t rows, int32_t hd,
+                           const float* signs, const float* codebook, int32_t n_codes,
+                           uint8_t* idx, uint16_t* norm, uint8_t* qsign, uint16_t* qscale,
+                           uint16_t* deq, void* stream);
+
+/* shard_stream_dequant with the QJL residual term (streaming.py:76-77):
+ * codebook[idx] + (2 qsign - 1) * qscale before the inverse Hadamard.
+ * qsign (rows, hd) uint8 and qscale (rows) fp16 both null or both set. */
+int shard_stream_dequant_qjl(const uint8_t* idx, const uint16_t* norm, const uint8_t* qsign,
+                             const uint16_t* qscale, int64_t rows, int32_t hd,
+                             const float* signs, const float* codebook, uint16_t* y,
+                             void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused decode attention over the compressed cache

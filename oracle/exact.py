@@ -12,7 +12,7 @@ intermediates.  Stored values enter exactly as the reference holds them:
                  phi = fl32(fl32(pos_t - pos_q) * theta_i)   (attention.py:3-6, 27-31, 75-81)
   compressed V   FWHT(cb[idx] * ch)                     (attention.py:83-121)
   fp16 segments  sink / window / decode K,V as stored   (attention.py:280-342)
-  stream         H(cb_LM[idx]) * signs * norm_f16       (streaming.py:74-79, exact)
+  stream         H(cb_LM[idx] (+ QJL)) * signs * norm_f16 (streaming.py:74-79, exact)
   softmax        over [sink, comp, win, decode, stream] (+ additive mask)
 
 Pinned by: the relative-delta identity against brute-force
@@ -78,12 +78,18 @@ def stream_kv(gc, B, nkv, hd):
     cb = np.asarray(gc["stream_codebook"], F64)
     signs = np.asarray(gc["signs"], F64)
 
-    def deq(idx, norm):
-        u = fwht64(cb[np.asarray(idx).astype(np.int64)]) * signs
-        return u * np.asarray(norm, np.float16).astype(F64)[..., None]
+    qjl = "k_qsign_buf" in gc
 
-    k = deq(gc["k_idx_buf"][:s], gc["k_norm_buf"][:s])    # (s, B, nkv, hd)
-    v = deq(gc["v_idx_buf"][:s], gc["v_norm_buf"][:s])
+    def deq(p):
+        rot = cb[np.asarray(gc[p + "_idx_buf"][:s]).astype(np.int64)]
+        if qjl:   # streaming.py:77-78: + (2 sign - 1) * scale in the rotated domain
+            sgn = np.asarray(gc[p + "_qsign_buf"][:s]).astype(F64) * 2 - 1
+            rot = rot + sgn * np.asarray(gc[p + "_qscale_buf"][:s], np.float16).astype(F64)[..., None]
+        u = fwht64(rot) * signs
+        return u * np.asarray(gc[p + "_norm_buf"][:s], np.float16).astype(F64)[..., None]
+
+    k = deq("k")    # (s, B, nkv, hd)
+    v = deq("v")
     return k.transpose(1, 2, 0, 3), v.transpose(1, 2, 0, 3)
 
 

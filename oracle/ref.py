@@ -6,17 +6,24 @@ order and dtypes as the reference's non-Triton fallbacks, so fp16 cast points
 are kept; the integer chains are written in numpy with every fp32 rounding
 explicit (no fused multiply-add anywhere in numpy elementwise code).
 
-How each function is pinned (checked in ``tests/test_oracle_*.py``):
+Test infrastructure only: tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it as the checker; the product never imports it.
+
+How each function is pinned (checked in ``tests/test_oracle.py``):
   hadamard            closed form: Sylvester matrix H/sqrt(d) on small d; H.H = I.
   rope helpers        rotation-matrix closed form; undo(reapply(x)) = x.
   dp_bit_allocation   exhaustive enumeration of bit vectors on tiny inputs.
   group_quant/dequant bit formulas; codes equal brute-force nearest level.
   int4_chain/pack     bit formula; the reference's own kernel_test.py:133-146
                       relation (pack == flat[0::2] | flat[1::2] << 4).
-  lloyd_max_codebook  golden vector written by importing the reference
-                      (tests/golden/make_golden.py) + Lloyd fixed-point residual.
+  lloyd_max_codebook  golden vectors written by importing the reference
+                      (tests/golden/make_golden.py) at 3..8 bits + Lloyd
+                      fixed-point residual; Max's (1960) table at 1 and 2 bits.
   stream quantize     torch.norm (library) for the norm order; brute-force
                       nearest codebook entry in fp64 away from ties.
+  QJL residual        torch.mean (library) for mean_fp32_4x8's order; sign
+                      against fp64; the per-token error identity
+                      |r - cb - s m|^2 = |r - cb|^2 - d m^2 for the dequant term.
   vq_assign           torch.cdist(...).argmin (the reference's own fallback,
                       triton_kernels.py:733-734) and fp64 brute force.
   kmeans              golden vectors from the reference import.
@@ -310,10 +317,33 @@ def norm_fp32_8lane(t: np.ndarray) -> np.ndarray:
     return np.sqrt(tot).astype(F32)
 
 
-def quantize_stream_token(x_f16: np.ndarray, signs: np.ndarray, codebook: np.ndarray):
-    """cache.py:207-215 (_unit) + streaming.py:59-72 (quantize_per_token, qjl off).
+def mean_fp32_4x8(a: np.ndarray) -> np.ndarray:
+    """torch CPU fp32 mean over a contiguous last dim (a multiple of 32): element
+    i goes to accumulator (i // 8) % 4, lane i % 8, in increasing i; the four
+    accumulators are added in order per lane, then the 8 lanes in order; then one
+    division by the length.  (Pinned against torch's mean in the tests.)"""
+    a = np.asarray(a, dtype=F32)
+    d = a.shape[-1]
+    acc = np.zeros(a.shape[:-1] + (4, 8), F32)
+    for i in range(d):
+        k, j = (i // 8) % 4, i % 8
+        acc[..., k, j] = (acc[..., k, j] + a[..., i]).astype(F32)
+    v = acc[..., 0, :].copy()
+    for k in range(1, 4):
+        v = (v + acc[..., k, :]).astype(F32)
+    tot = v[..., 0].copy()
+    for j in range(1, 8):
+        tot = (tot + v[..., j]).astype(F32)
+    return (tot / F32(d)).astype(F32)
 
-    x_f16: (..., hd) float16.  Returns (idx uint8 (..., hd), norm float16 (...)).
+
+def quantize_stream_token(x_f16: np.ndarray, signs: np.ndarray, codebook: np.ndarray,
+                          qjl: bool = False):
+    """cache.py:207-215 (_unit) + streaming.py:59-72 (quantize_per_token).
+
+    x_f16: (..., hd) float16.  Returns (idx uint8 (..., hd), norm float16 (...))
+    and, with qjl, also (qsign uint8 (..., hd), qscale float16 (...)): the sign
+    of the residual r - cb[idx] and fp16(mean |r - cb[idx]|) (streaming.py:67-70).
     """
     t = np.asarray(x_f16, dtype=np.float16).astype(F32)
     n = np.maximum(norm_fp32_8lane(t), F32(1e-8))
@@ -326,13 +356,24 @@ def quantize_stream_token(x_f16: np.ndarray, signs: np.ndarray, codebook: np.nda
     dl = np.abs((cb[left] - r).astype(F32))
     di = np.abs((cb[idx] - r).astype(F32))
     idx = np.where(dl < di, left, idx).astype(np.uint8)
+    if qjl:
+        res = (r - cb[idx.astype(np.int64)]).astype(F32)
+        qsign = (res >= 0).astype(np.uint8)
+        qscale = mean_fp32_4x8(np.abs(res)).astype(np.float16)
+        return idx, n.astype(np.float16), qsign, qscale
     return idx, n.astype(np.float16)
 
 
-def dequantize_stream_token(idx: np.ndarray, norm_f16: np.ndarray, signs, codebook):
-    """streaming.py:74-79 + cache.py:275-278: fp16(fp16(H(cb[idx])*signs)*norm)."""
+def dequantize_stream_token(idx: np.ndarray, norm_f16: np.ndarray, signs, codebook,
+                            qsign=None, qscale=None):
+    """streaming.py:74-79 + cache.py:275-278: fp16(fp16(H(cb[idx] (+ QJL term))
+    * signs) * norm); the QJL term is (2 qsign - 1) * fp32(qscale)."""
     cb = np.asarray(codebook, F32)
     rot = cb[np.asarray(idx).astype(np.int64)]
+    if qsign is not None:
+        term = ((np.asarray(qsign).astype(F32) * F32(2) - F32(1))
+                * np.asarray(qscale, np.float16).astype(F32)[..., None]).astype(F32)
+        rot = (rot + term).astype(F32)
     u = (hadamard_np(rot) * np.asarray(signs, F32)).astype(np.float16)
     return (u.astype(F32) * np.asarray(norm_f16, np.float16).astype(F32)[..., None]).astype(np.float16)
 
@@ -548,14 +589,22 @@ def v_weighted_sum_compressed(weights_mid, gc, B, nkv, n_comp, hd):
 
 
 def stream_dequant(gc, B, nkv, hd):
-    """cache.py:243-279 (qjl off): (B, nkv, S, hd) fp16 K and V, or (None, None)."""
+    """cache.py:243-279: (B, nkv, S, hd) fp16 K and V, or (None, None); with the
+    QJL term when the layer holds sign/scale buffers (cache.py:263-273)."""
     s = gc.get("stream_n", 0) // B if gc.get("stream_n", 0) else 0
     if s == 0:
         return None, None
     cb = gc["stream_codebook"]
     signs = gc["signs"]
-    k = dequantize_stream_token(gc["k_idx_buf"][:s], gc["k_norm_buf"][:s], signs, cb)
-    v = dequantize_stream_token(gc["v_idx_buf"][:s], gc["v_norm_buf"][:s], signs, cb)
+    qjl = "k_qsign_buf" in gc
+
+    def _q(key):
+        return gc[key][:s] if qjl else None
+
+    k = dequantize_stream_token(gc["k_idx_buf"][:s], gc["k_norm_buf"][:s], signs, cb,
+                                _q("k_qsign_buf"), _q("k_qscale_buf"))
+    v = dequantize_stream_token(gc["v_idx_buf"][:s], gc["v_norm_buf"][:s], signs, cb,
+                                _q("v_qsign_buf"), _q("v_qscale_buf"))
     sk = torch.from_numpy(np.ascontiguousarray(np.transpose(k, (1, 2, 0, 3))))
     sv = torch.from_numpy(np.ascontiguousarray(np.transpose(v, (1, 2, 0, 3))))
     return sk, sv

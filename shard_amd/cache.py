@@ -155,13 +155,16 @@ class CacheLayer(CacheLayerMixin):
         stream buffers (growable, doubling, as cache.py:220-230)."""
         gc = self._gpu_compressed
         c = self._cache_ref
-        if c._stream_bits != 8 or c._stream_qjl:
-            raise NotImplementedError("the HIP stream quantizer implements 8-bit codes without QJL")
+        bits, qjl = int(c._stream_bits), bool(c._stream_qjl)
+        if not 1 <= bits <= 8:
+            raise ValueError(f"_stream_bits must be in 1..8 (uint8 codes), got {bits}")
         B, G, _, D = k.shape
         dev = k.device
         if "signs" not in gc:
             gc["signs"] = host.stream_signs(self.layer_idx, D).to(dev)
-            gc["stream_codebook"] = host.lloyd_max_codebook(D, 8).to(dev)
+        if gc.get("stream_bits") != bits:
+            gc["stream_codebook"] = host.lloyd_max_codebook(D, bits).to(dev)
+            gc["stream_bits"] = bits
         s = gc.get("stream_n", 0) // B
         needed = s + 1
 
@@ -185,14 +188,22 @@ class CacheLayer(CacheLayerMixin):
         # once at append time and read by the decode kernel (runtime scratch)
         kdb = _ensure("k_deq", (B, G, D), torch.float16)
         vdb = _ensure("v_deq", (B, G, D), torch.float16)
+        kqs = vqs = kqc = vqc = None
+        if qjl:  # 1-bit residual signs and per-token scale (cache.py:234-240)
+            kqs = _ensure("k_qsign", (B, G, D), torch.uint8)[s]
+            vqs = _ensure("v_qsign", (B, G, D), torch.uint8)[s]
+            kqc = _ensure("k_qscale", (B, G), torch.float16)[s]
+            vqc = _ensure("v_qscale", (B, G), torch.float16)[s]
         kx = k.reshape(B, G, D)
         vx = v.reshape(B, G, D)
         if not kx.is_contiguous():
             kx = kx.contiguous()
         if not vx.is_contiguous():
             vx = vx.contiguous()
-        ops.stream_quant_into(kx, gc["signs"], gc["stream_codebook"], kib[s], knb[s], kdb[s])
-        ops.stream_quant_into(vx, gc["signs"], gc["stream_codebook"], vib[s], vnb[s], vdb[s])
+        ops.stream_quant_into(kx, gc["signs"], gc["stream_codebook"], kib[s], knb[s], kdb[s],
+                              kqs, kqc)
+        ops.stream_quant_into(vx, gc["signs"], gc["stream_codebook"], vib[s], vnb[s], vdb[s],
+                              vqs, vqc)
         gc["stream_n"] = gc.get("stream_n", 0) + B
 
     def _dequant_stream(self, gc, B, nkv=None, hd=None):
@@ -321,6 +332,11 @@ class Cache(HFCache):
                     total += int(gc[k][:s].nelement() * bpv)
                 for k in ("k_norm_buf", "v_norm_buf", "k_deq_buf", "v_deq_buf"):
                     total += _nb(gc[k][:s])
+                if "k_qsign_buf" in gc:  # QJL: 1 bit per element + fp16 scale per token
+                    for k in ("k_qsign_buf", "v_qsign_buf"):
+                        total += gc[k][:s].nelement() // 8
+                    for k in ("k_qscale_buf", "v_qscale_buf"):
+                        total += _nb(gc[k][:s])
         if has_gc:
             return total
         return sum(_nb(l._keys) + _nb(l._values) for l in self.layers if l._keys is not None)

@@ -147,6 +147,44 @@ __device__ __forceinline__ float xor_lane(float v) {
   }
 }
 
+// ---- fast Walsh-Hadamard transform of one row held by a wave.
+// One butterfly stage across lanes l and l ^ H (element stride H).
+template <int H, int E>
+__device__ __forceinline__ void fwht_lane_stage(float (&x)[E], int l) {
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    const float p = xor_lane<H>(x[k]);
+    x[k] = (l & H) ? sub_rn(p, x[k]) : add_rn(x[k], p);
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void wave_fwht(float (&x)[E], int d) {
+  // d == 64 * E: element i = lane + 64 k; strides 1..32 cross lanes, 64.. cross registers
+  const int l = (int)lane_id();
+  fwht_lane_stage<1>(x, l);
+  fwht_lane_stage<2>(x, l);
+  fwht_lane_stage<4>(x, l);
+  fwht_lane_stage<8>(x, l);
+  fwht_lane_stage<16>(x, l);
+  fwht_lane_stage<32>(x, l);
+#pragma unroll
+  for (int hk = 1; hk < E; hk <<= 1) {
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      if ((k & hk) == 0) {
+        const float a = x[k], b = x[k | hk];
+        x[k] = add_rn(a, b);
+        x[k | hk] = sub_rn(a, b);
+      }
+    }
+  }
+  // torch divides an fp32 tensor by the Python float sqrt(d): fp32(double sqrt)
+  const float s = (float)sqrt((double)d);
+#pragma unroll
+  for (int k = 0; k < E; ++k) x[k] = div_rn(x[k], s);
+}
+
 inline int grid_cap(int64_t blocks, int cap = 65535 * 8) {
   return (int)(blocks < cap ? blocks : cap);
 }

@@ -127,43 +127,6 @@ __global__ void k_int4_pack(const float* __restrict__ proj, int64_t n, int keep,
 // Stage h pairs element e with e^h: lower index gets a+b, upper a-b
 // (cache.py:14-18), stages in increasing h, then one IEEE division.
 // ---------------------------------------------------------------------------
-// One butterfly stage across lanes l and l ^ H (element stride H).
-template <int H, int E>
-__device__ __forceinline__ void fwht_lane_stage(float (&x)[E], int l) {
-#pragma unroll
-  for (int k = 0; k < E; ++k) {
-    const float p = xor_lane<H>(x[k]);
-    x[k] = (l & H) ? sub_rn(p, x[k]) : add_rn(x[k], p);
-  }
-}
-
-template <int E>
-__device__ __forceinline__ void wave_fwht(float (&x)[E], int d) {
-  // d == 64 * E: element i = lane + 64 k; strides 1..32 cross lanes, 64.. cross registers
-  const int l = (int)lane_id();
-  fwht_lane_stage<1>(x, l);
-  fwht_lane_stage<2>(x, l);
-  fwht_lane_stage<4>(x, l);
-  fwht_lane_stage<8>(x, l);
-  fwht_lane_stage<16>(x, l);
-  fwht_lane_stage<32>(x, l);
-#pragma unroll
-  for (int hk = 1; hk < E; hk <<= 1) {
-#pragma unroll
-    for (int k = 0; k < E; ++k) {
-      if ((k & hk) == 0) {
-        const float a = x[k], b = x[k | hk];
-        x[k] = add_rn(a, b);
-        x[k | hk] = sub_rn(a, b);
-      }
-    }
-  }
-  // torch divides an fp32 tensor by the Python float sqrt(d): fp32(double sqrt)
-  const float s = (float)sqrt((double)d);
-#pragma unroll
-  for (int k = 0; k < E; ++k) x[k] = div_rn(x[k], s);
-}
-
 template <int E>
 __global__ void k_fwht_rows(const float* __restrict__ x, float* __restrict__ y, int64_t rows) {
   const int d = 64 * E;
@@ -435,7 +398,8 @@ template <int E>
 __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
                                const float* __restrict__ signs, const float* __restrict__ cb_g,
                                int n_codes, uint8_t* __restrict__ idx,
-                               uint16_t* __restrict__ norm, uint16_t* __restrict__ deq) {
+                               uint16_t* __restrict__ norm, uint8_t* __restrict__ qsign,
+                               uint16_t* __restrict__ qscale, uint16_t* __restrict__ deq) {
   constexpr int D = 64 * E;
   __shared__ float cb[256];
   for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
@@ -444,7 +408,7 @@ __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
   const int w = threadIdx.x >> 6;
   int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + w;
   if (r >= rows) return;  // no block-level barrier below this point
-  float t[E], sq[E];
+  float t[E], sq[E], res[E];
 #pragma unroll
   for (int k = 0; k < E; ++k) {
     t[k] = h2f(x[r * D + l + 64 * k]);
@@ -479,12 +443,45 @@ __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
     float di = fabsf(sub_rn(cb[i], v));
     const int code = dl < di ? left : i;
     idx[r * D + l + 64 * k] = (uint8_t)code;
+    res[k] = sub_rn(v, cb[code]);  // QJL residual (streaming.py:69)
     t[k] = cb[code];
   }
   const uint16_t nh = f2h(n);
   if (l == 0) norm[r] = nh;
+  if (qsign) {
+    // QJL: sign bit of the residual per element, fp16 mean |residual| per row
+    // (streaming.py:68-70), the mean in torch CPU's order for a contiguous
+    // fp32 row: element i goes to accumulator (i / 8) % 4, lane i % 8, in
+    // increasing i; the 4 accumulators are added in order per lane, then the
+    // 8 lanes in order; then one division by the row length.
+    float ares[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      qsign[r * D + l + 64 * k] = res[k] >= 0.f ? 1 : 0;
+      ares[k] = fabsf(res[k]);
+    }
+    float acc = 0.f;  // lane L < 32 holds accumulator (L / 8, L % 8): elements L + 32 m
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      const float v = __shfl(ares[(32 * m) >> 6], (l + 32 * m) & 63, 64);
+      acc = add_rn(acc, v);
+    }
+    float tot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float vj = __shfl(acc, j, 64);
+#pragma unroll
+      for (int a = 1; a < 4; ++a) vj = add_rn(vj, __shfl(acc, j + 8 * a, 64));
+      tot = j == 0 ? vj : add_rn(tot, vj);
+    }
+    const uint16_t sh = f2h(div_rn(tot, (float)D));
+    if (l == 0) qscale[r] = sh;
+    const float sf = h2f(sh);
+#pragma unroll
+    for (int k = 0; k < E; ++k) t[k] = add_rn(t[k], res[k] >= 0.f ? sf : -sf);
+  }
   if (deq) {
-    // reference dequant: fp16(fp16(hadamard(cb[idx]) * signs) * fp16 norm)
+    // reference dequant: fp16(fp16(hadamard(cb[idx] (+ qjl)) * signs) * fp16 norm)
     wave_fwht<E>(t, D);
     const float nf = h2f(nh);
 #pragma unroll
@@ -669,21 +666,29 @@ int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx
   return SHARD_OK;
 }
 
-int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,
-                       const float* codebook, int32_t n_codes, uint8_t* idx, uint16_t* norm,
-                       uint16_t* deq, void* stream) {
+int shard_stream_quant_qjl(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,
+                           const float* codebook, int32_t n_codes, uint8_t* idx, uint16_t* norm,
+                           uint8_t* qsign, uint16_t* qscale, uint16_t* deq, void* stream) {
   if (!x || !signs || !codebook || !idx || !norm || rows <= 0 || n_codes <= 0) return SHARD_ERR_ARG;
+  if ((qsign == nullptr) != (qscale == nullptr)) return SHARD_ERR_ARG;
   if (n_codes > 256) return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   unsigned blocks = (unsigned)((rows + 3) / 4);
   switch (hd) {
-    case 64: hipLaunchKernelGGL(k_stream_quant<1>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, deq); break;
-    case 128: hipLaunchKernelGGL(k_stream_quant<2>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, deq); break;
-    case 256: hipLaunchKernelGGL(k_stream_quant<4>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, deq); break;
+    case 64: hipLaunchKernelGGL(k_stream_quant<1>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, qsign, qscale, deq); break;
+    case 128: hipLaunchKernelGGL(k_stream_quant<2>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, qsign, qscale, deq); break;
+    case 256: hipLaunchKernelGGL(k_stream_quant<4>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, qsign, qscale, deq); break;
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_stream_quant");
   return SHARD_OK;
+}
+
+int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,
+                       const float* codebook, int32_t n_codes, uint8_t* idx, uint16_t* norm,
+                       uint16_t* deq, void* stream) {
+  return shard_stream_quant_qjl(x, rows, hd, signs, codebook, n_codes, idx, norm, nullptr, nullptr,
+                                deq, stream);
 }
 
 int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq, int32_t hd,

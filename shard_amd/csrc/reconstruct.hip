@@ -68,23 +68,6 @@ void k_reconstruct_k(const uint8_t* __restrict__ coef, const uint16_t* __restric
   }
 }
 
-// Butterflies over 128 values held as (lane, lane + 64), bit-exact with hadamard().
-__device__ __forceinline__ void rc_fwht128(float& x0, float& x1) {
-  const int l = (int)lane_id();
-#pragma unroll
-  for (int h = 1; h < 64; h <<= 1) {
-    const float p0 = __shfl_xor(x0, h, 64), p1 = __shfl_xor(x1, h, 64);
-    x0 = (l & h) ? __fsub_rn(p0, x0) : __fadd_rn(x0, p0);
-    x1 = (l & h) ? __fsub_rn(p1, x1) : __fadd_rn(x1, p1);
-  }
-  const float a = x0, c = x1;
-  x0 = __fadd_rn(a, c);
-  x1 = __fsub_rn(a, c);
-  const float s = (float)sqrt(128.0);
-  x0 = __fdiv_rn(x0, s);
-  x1 = __fdiv_rn(x1, s);
-}
-
 // V: one wave per (b, g, t): fp16(hadamard(cb[idx] * ch)), fp32 math.
 __global__ void k_reconstruct_v(const uint8_t* __restrict__ vidx, const uint16_t* __restrict__ vcb,
                                 const uint16_t* __restrict__ vch, int64_t rows, int G, int n_comp,
@@ -97,29 +80,42 @@ __global__ void k_reconstruct_v(const uint8_t* __restrict__ vidx, const uint16_t
     const uint8_t* ix = vidx + r * 32;
     const uint16_t* ch = vch + bg * kRcHD;
     const int d0 = l, d1 = l + 64;
-    float x0 = __fmul_rn(h2f(vcb[4 * ix[d0 >> 2] + (d0 & 3)]), h2f(ch[d0]));
-    float x1 = __fmul_rn(h2f(vcb[4 * ix[d1 >> 2] + (d1 & 3)]), h2f(ch[d1]));
-    rc_fwht128(x0, x1);
-    v_out[r * kRcHD + d0] = f2h_opaque(x0);
-    v_out[r * kRcHD + d1] = f2h_opaque(x1);
+    float x[2] = {__fmul_rn(h2f(vcb[4 * ix[d0 >> 2] + (d0 & 3)]), h2f(ch[d0])),
+                  __fmul_rn(h2f(vcb[4 * ix[d1 >> 2] + (d1 & 3)]), h2f(ch[d1]))};
+    wave_fwht<2>(x, kRcHD);
+    v_out[r * kRcHD + d0] = f2h_opaque(x[0]);
+    v_out[r * kRcHD + d1] = f2h_opaque(x[1]);
   }
 }
 
-// Stream rows: fp16(fp16(hadamard(cb[idx]) * signs) * norm).
+// Stream rows: fp16(fp16(hadamard(cb[idx] (+ QJL term)) * signs) * norm), one
+// wave per row of D = 64 E elements (element i = lane + 64 k).
+template <int E>
 __global__ void k_stream_dequant(const uint8_t* __restrict__ idx, const uint16_t* __restrict__ norm,
-                                 int64_t rows, const float* __restrict__ signs,
-                                 const float* __restrict__ cb, uint16_t* __restrict__ y) {
+                                 const uint8_t* __restrict__ qsign,
+                                 const uint16_t* __restrict__ qscale, int64_t rows,
+                                 const float* __restrict__ signs, const float* __restrict__ cb,
+                                 uint16_t* __restrict__ y) {
+  constexpr int D = 64 * E;
   const int l = (int)lane_id();
   int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
   for (int64_t r = wave; r < rows; r += nw) {
-    float x0 = cb[idx[r * kRcHD + l]], x1 = cb[idx[r * kRcHD + l + 64]];
-    rc_fwht128(x0, x1);
+    float x[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) x[k] = cb[idx[r * D + l + 64 * k]];
+    if (qsign) {  // QJL: cb[idx] + (2 s - 1) * scale (streaming.py:76-77)
+      const float sc = h2f(qscale[r]);
+#pragma unroll
+      for (int k = 0; k < E; ++k) x[k] = __fadd_rn(x[k], qsign[r * D + l + 64 * k] ? sc : -sc);
+    }
+    wave_fwht<E>(x, D);
     const float n = h2f(norm[r]);
     // fp16(fp16(x * sign) * norm): the sign flip is exact, the product of two
     // fp16 values is exact in fp32, so each line rounds exactly twice like torch
-    y[r * kRcHD + l] = f2h_opaque(h2f(f2h(mul_sign(x0, signs[l]))) * n);
-    y[r * kRcHD + l + 64] = f2h_opaque(h2f(f2h(mul_sign(x1, signs[l + 64]))) * n);
+#pragma unroll
+    for (int k = 0; k < E; ++k)
+      y[r * D + l + 64 * k] = f2h_opaque(h2f(f2h(mul_sign(x[k], signs[l + 64 * k]))) * n);
   }
 }
 
@@ -150,15 +146,26 @@ int shard_kv_reconstruct(const shard_decode_args* a, uint16_t* k_out, uint16_t* 
   return SHARD_OK;
 }
 
-int shard_stream_dequant(const uint8_t* idx, const uint16_t* norm, int64_t rows, int32_t hd,
-                         const float* signs, const float* codebook, uint16_t* y, void* stream) {
+int shard_stream_dequant_qjl(const uint8_t* idx, const uint16_t* norm, const uint8_t* qsign,
+                             const uint16_t* qscale, int64_t rows, int32_t hd, const float* signs,
+                             const float* codebook, uint16_t* y, void* stream) {
   if (!idx || !norm || !signs || !codebook || !y || rows <= 0) return SHARD_ERR_ARG;
-  if (hd != kRcHD) return SHARD_ERR_SHAPE;
+  if ((qsign == nullptr) != (qscale == nullptr)) return SHARD_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_stream_dequant, dim3(grid_cap((rows + 3) / 4, 16384)), dim3(256), 0, s, idx,
-                     norm, rows, signs, codebook, y);
+  const dim3 grid(grid_cap((rows + 3) / 4, 16384)), block(256);
+  switch (hd) {
+    case 64: hipLaunchKernelGGL(k_stream_dequant<1>, grid, block, 0, s, idx, norm, qsign, qscale, rows, signs, codebook, y); break;
+    case 128: hipLaunchKernelGGL(k_stream_dequant<2>, grid, block, 0, s, idx, norm, qsign, qscale, rows, signs, codebook, y); break;
+    case 256: hipLaunchKernelGGL(k_stream_dequant<4>, grid, block, 0, s, idx, norm, qsign, qscale, rows, signs, codebook, y); break;
+    default: return SHARD_ERR_SHAPE;
+  }
   SHARD_LAUNCH_CHECK("shard_stream_dequant");
   return SHARD_OK;
+}
+
+int shard_stream_dequant(const uint8_t* idx, const uint16_t* norm, int64_t rows, int32_t hd,
+                         const float* signs, const float* codebook, uint16_t* y, void* stream) {
+  return shard_stream_dequant_qjl(idx, norm, nullptr, nullptr, rows, hd, signs, codebook, y, stream);
 }
 
 }  // extern "C"

@@ -219,38 +219,48 @@ def kmeans(data: torch.Tensor, k: int, n_iter: int = 30, seed: int = 42):
 # decode stream
 # ---------------------------------------------------------------------------
 def stream_quant(x: torch.Tensor, signs: torch.Tensor, codebook: torch.Tensor,
-                 with_deq: bool = False):
+                 with_deq: bool = False, qjl: bool = False):
     """Per-token Lloyd-Max quantizer; x (..., D) fp16 -> (idx u8 (..., D), norm fp16 (...)
-    [, deq fp16 (..., D) = the token as the reference dequantizes it])."""
+    [, qsign u8 (..., D), qscale fp16 (...) with qjl] [, deq fp16 (..., D) = the token
+    as the reference dequantizes it])."""
     _require_gpu(x, signs, codebook)
     x = _contig(x, torch.float16, "x")
     idx = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     norm = torch.empty(x.shape[:-1], dtype=torch.float16, device=x.device)
+    qs = torch.empty(x.shape, dtype=torch.uint8, device=x.device) if qjl else None
+    qsc = torch.empty(x.shape[:-1], dtype=torch.float16, device=x.device) if qjl else None
     deq = torch.empty(x.shape, dtype=torch.float16, device=x.device) if with_deq else None
-    stream_quant_into(x, signs, codebook, idx, norm, deq)
-    return (idx, norm, deq) if with_deq else (idx, norm)
+    stream_quant_into(x, signs, codebook, idx, norm, deq, qs, qsc)
+    out = (idx, norm) + ((qs, qsc) if qjl else ())
+    return out + (deq,) if with_deq else out
 
 
-def stream_quant_into(x, signs, codebook, idx_out, norm_out, deq_out=None):
+def stream_quant_into(x, signs, codebook, idx_out, norm_out, deq_out=None, qsign_out=None,
+                      qscale_out=None):
     lib = _lib.load()
     D = x.shape[-1]
     rows = x.numel() // D
-    _lib.check("shard_stream_quant", lib.shard_stream_quant(
+    _lib.check("shard_stream_quant", lib.shard_stream_quant_qjl(
         _p(x), rows, D, _p(signs), _p(codebook), codebook.numel(), _p(idx_out), _p(norm_out),
-        _p(deq_out), _stream(x)))
+        _p(qsign_out), _p(qscale_out), _p(deq_out), _stream(x)))
 
 
 def stream_dequant(idx: torch.Tensor, norm: torch.Tensor, signs: torch.Tensor,
-                   codebook: torch.Tensor) -> torch.Tensor:
-    """fp16(fp16(H(cb[idx]) * signs) * norm) for (..., D) codes."""
+                   codebook: torch.Tensor, qsign: torch.Tensor = None,
+                   qscale: torch.Tensor = None) -> torch.Tensor:
+    """fp16(fp16(H(cb[idx] (+ (2 qsign - 1) qscale)) * signs) * norm) for (..., D) codes."""
     _require_gpu(idx, norm, signs, codebook)
     lib = _lib.load()
     idx = _contig(idx, torch.uint8, "idx")
     norm = _contig(norm, torch.float16, "norm")
+    if qsign is not None:
+        qsign = _contig(qsign, torch.uint8, "qsign")
+        qscale = _contig(qscale, torch.float16, "qscale")
     D = idx.shape[-1]
     y = torch.empty(idx.shape, dtype=torch.float16, device=idx.device)
-    _lib.check("shard_stream_dequant", lib.shard_stream_dequant(
-        _p(idx), _p(norm), idx.numel() // D, D, _p(signs), _p(codebook), _p(y), _stream(idx)))
+    _lib.check("shard_stream_dequant", lib.shard_stream_dequant_qjl(
+        _p(idx), _p(norm), _p(qsign), _p(qscale), idx.numel() // D, D, _p(signs),
+        _p(codebook), _p(y), _stream(idx)))
     return y
 
 

@@ -4,6 +4,9 @@ invariant or library routine pins are recorded here:
 
   lloyd_max.npz      lloyd_max_codebook(128, 8)  (streaming.py:35-51) — the
                      100th, non-converged Lloyd iterate
+  lloyd_max_bits.npz lloyd_max_codebook(128, b) for b = 3..7, the widths that
+                     do not converge within 100 iterations either (1 and 2
+                     bits converge and are pinned by Max's table instead)
   kmeans.npz         kmeans(data, 16, 30, seed 42) on 600 x 4 fp32 rows
                      (cache.py:21-39): pre-update indices, CPU randperm init
   fused_attn.npz     fused_attention_compressed on a hand-built stub cache
@@ -12,7 +15,8 @@ invariant or library routine pins are recorded here:
                      fp16 cast points.  Same stub technique as the reference's
                      own benchmarks/kernel_test.py:178-259.
 
-Usage:  python tests/golden/make_golden.py /root/reference
+Usage:  python tests/golden/make_golden.py /root/reference [fixture ...]
+        (no fixture names: write all of them)
 The fixtures hold inputs and outputs only (arrays), no reference source.
 """
 import os
@@ -25,22 +29,32 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def main(ref_root):
+def main(ref_root, only=()):
     sys.path.insert(0, os.path.join(ref_root, "src"))
     from shard.streaming import lloyd_max_codebook, quantize_per_token  # noqa: F401
     from shard import cache as rcache
     from shard.attention import fused_attention_compressed
 
-    # 1. Lloyd-Max codebook
-    cb = lloyd_max_codebook(128, 8).numpy().astype(np.float32)
-    np.savez(os.path.join(HERE, "lloyd_max.npz"), codebook=cb, d=128, bits=8)
+    want = lambda name: not only or name in only
+
+    # 1. Lloyd-Max codebooks
+    if want("lloyd_max.npz"):
+        cb = lloyd_max_codebook(128, 8).numpy().astype(np.float32)
+        np.savez(os.path.join(HERE, "lloyd_max.npz"), codebook=cb, d=128, bits=8)
+    if want("lloyd_max_bits.npz"):
+        books = {f"cb{b}": lloyd_max_codebook(128, b).numpy().astype(np.float32)
+                 for b in range(3, 8)}
+        np.savez(os.path.join(HERE, "lloyd_max_bits.npz"), d=128, **books)
 
     # 2. k-means on small data
-    g = torch.Generator().manual_seed(123)
-    data = torch.randn(600, 4, generator=g)
-    cent, idx = rcache.kmeans(data, 16, n_iter=30, seed=42)
-    np.savez(os.path.join(HERE, "kmeans.npz"), data=data.numpy(), centroids=cent.numpy(),
-             idx=idx.numpy().astype(np.int64), k=16, n_iter=30, seed=42)
+    if want("kmeans.npz"):
+        g = torch.Generator().manual_seed(123)
+        data = torch.randn(600, 4, generator=g)
+        cent, idx = rcache.kmeans(data, 16, n_iter=30, seed=42)
+        np.savez(os.path.join(HERE, "kmeans.npz"), data=data.numpy(), centroids=cent.numpy(),
+                 idx=idx.numpy().astype(np.int64), k=16, n_iter=30, seed=42)
+    if not want("fused_attn.npz"):
+        return
 
     # 3. fused attention on a stub cache layer (B=1, 8 q heads, 2 kv heads, hd 128)
     g = torch.Generator().manual_seed(7)
@@ -100,4 +114,4 @@ def main(ref_root):
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference", tuple(sys.argv[2:]))

@@ -8,7 +8,7 @@ from oracle import ref
 
 
 def random_layer(B=1, nkv=8, hd=128, rank=192, n_comp=512, sink=4, win=64, n_stream=0,
-                 n_dec=0, seed=0, inv_freq=None, basis_amp=0.05):
+                 n_dec=0, seed=0, inv_freq=None, basis_amp=0.05, stream_bits=8, qjl=False):
     """A random compressed layer in the oracle's gc format (CPU tensors)."""
     g = torch.Generator().manual_seed(seed)
     if inv_freq is None:
@@ -42,14 +42,17 @@ def random_layer(B=1, nkv=8, hd=128, rank=192, n_comp=512, sink=4, win=64, n_str
         gc["decode_k"] = torch.randn(B, nkv, n_dec, hd, generator=g).half()
         gc["decode_v"] = torch.randn(B, nkv, n_dec, hd, generator=g).half()
     if n_stream:
-        cb = ref.lloyd_max_codebook(hd, 8)
+        cb = ref.lloyd_max_codebook(hd, stream_bits)
         signs = ref.stream_signs(5, hd)
         xk = (torch.randn(n_stream, B, nkv, hd, generator=g) * 1.5).half().numpy()
         xv = torch.randn(n_stream, B, nkv, hd, generator=g).half().numpy()
-        kidx, knorm = ref.quantize_stream_token(xk, signs, cb)
-        vidx, vnorm = ref.quantize_stream_token(xv, signs, cb)
+        kq = ref.quantize_stream_token(xk, signs, cb, qjl=qjl)
+        vq = ref.quantize_stream_token(xv, signs, cb, qjl=qjl)
         gc.update({"signs": signs, "stream_codebook": cb, "stream_n": n_stream * B,
-                   "k_idx_buf": kidx, "v_idx_buf": vidx, "k_norm_buf": knorm, "v_norm_buf": vnorm})
+                   "k_idx_buf": kq[0], "v_idx_buf": vq[0], "k_norm_buf": kq[1], "v_norm_buf": vq[1]})
+        if qjl:
+            gc.update({"k_qsign_buf": kq[2], "v_qsign_buf": vq[2],
+                       "k_qscale_buf": kq[3], "v_qscale_buf": vq[3]})
     return gc, inv_freq
 
 
@@ -78,10 +81,11 @@ def to_device(gc, device, inv_freq, nkv=8, hd=128):
         d["decode_k"] = t(gc["decode_k"]).contiguous()
         d["decode_v"] = t(gc["decode_v"]).contiguous()
     if gc.get("stream_n", 0):
+        q = (lambda k: gc.get(k))
         kdeq = ref.dequantize_stream_token(gc["k_idx_buf"], gc["k_norm_buf"], gc["signs"],
-                                           gc["stream_codebook"])
+                                           gc["stream_codebook"], q("k_qsign_buf"), q("k_qscale_buf"))
         vdeq = ref.dequantize_stream_token(gc["v_idx_buf"], gc["v_norm_buf"], gc["signs"],
-                                           gc["stream_codebook"])
+                                           gc["stream_codebook"], q("v_qsign_buf"), q("v_qscale_buf"))
         d.update({"signs": t(np.asarray(gc["signs"], np.float32)),
                   "stream_codebook": t(np.asarray(gc["stream_codebook"], np.float32)),
                   "stream_n": gc["stream_n"],

@@ -58,6 +58,21 @@ def test_decode_matches_exact_oracle(cuda, case):
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
+@pytest.mark.parametrize("bits,qjl", [(4, True), (2, False), (8, True)])
+def test_decode_with_qjl_and_narrow_stream(cuda, bits, qjl):
+    """Stream tokens quantized with 2/4-bit codes and the QJL residual
+    (cache.py:234-240, 263-273): the oracle adds (2 sign - 1) * scale in the
+    rotated domain before the inverse Hadamard."""
+    gc, inv = random_layer(B=2, n_comp=400, n_stream=23, seed=bits, stream_bits=bits, qjl=qjl)
+    q = torch.randn(2, 32, 1, 128, generator=torch.Generator().manual_seed(4)).half()
+    pos_q = 4 + 400 + 64 + 23 - 1
+    want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    got = _run(cuda, gc, inv, q, pos_q)
+    err, cos = compare(got, want)
+    print(f"bits={bits} qjl={qjl} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= TOL_ABS and cos >= TOL_COS
+
+
 def test_decode_rank_padding_and_splits(cuda):
     """rank 100 (padded to 128 on the device) and several explicit split counts."""
     gc, inv = random_layer(rank=100, n_comp=1000, seed=5)

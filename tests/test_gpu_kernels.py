@@ -68,6 +68,43 @@ def test_stream_quant_bitexact(cuda, rows):
     assert np.array_equal(got_d.view(np.uint16)[fin], want_y.view(np.uint16)[fin])
 
 
+def _bits_eq(got, want):
+    gb, wb = np.asarray(got).view(np.uint16), np.asarray(want).view(np.uint16)
+    bad = np.argwhere(gb != wb)
+    assert bad.size == 0, f"{len(bad)} mismatches, first {bad[:5].tolist()}"
+
+
+@pytest.mark.parametrize("bits,qjl,hd", [
+    (8, True, 128), (4, False, 128), (4, True, 128), (3, True, 128), (2, True, 128),
+    (1, True, 128), (2, True, 64), (8, True, 256), (5, False, 256),
+])
+def test_stream_quant_widths_qjl_bitexact(cuda, bits, qjl, hd):
+    """Lloyd-Max codes of 1..8 bits and the QJL residual (streaming.py:59-79):
+    codes, norms, residual signs and fp16 scales, and both dequantizations."""
+    ops = _ops()
+    rows = 1031
+    g = torch.Generator().manual_seed(bits * 1000 + hd)
+    x = (torch.randn(rows, hd, generator=g) * torch.rand(rows, 1, generator=g) * 6).half()
+    x[1] = 0
+    cb = ref.lloyd_max_codebook(hd, bits)
+    signs = ref.stream_signs(bits, hd)
+    want = ref.quantize_stream_token(x.numpy(), signs, cb, qjl=qjl)
+    sd, cd = torch.from_numpy(signs).to(cuda), torch.from_numpy(cb).to(cuda)
+    got = ops.stream_quant(x.to(cuda), sd, cd, with_deq=True, qjl=qjl)
+    got = [t.cpu().numpy() for t in got]
+    assert np.array_equal(got[0], want[0])
+    _bits_eq(got[1], want[1])
+    if qjl:
+        assert np.array_equal(got[2], want[2])
+        _bits_eq(got[3], want[3])
+    want_y = ref.dequantize_stream_token(want[0], want[1], signs, cb,
+                                         *(want[2:4] if qjl else (None, None)))
+    _bits_eq(got[-1], want_y)
+    y = ops.stream_dequant(*(torch.from_numpy(a).to(cuda) for a in want[:2]), sd, cd,
+                           *((torch.from_numpy(a).to(cuda) for a in want[2:4]) if qjl else ()))
+    _bits_eq(y.cpu().numpy(), want_y)
+
+
 @pytest.mark.parametrize("d", [16, 64, 128, 256])
 def test_fwht_bitexact(cuda, d):
     ops = _ops()

@@ -172,6 +172,73 @@ def test_stream_quant_is_nearest_code():
     assert cos.mean() > 0.9999 and cos.min() > 0.99
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_mean_order_matches_torch(d):
+    """The QJL scale is torch's CPU fp32 mean of |residual| (streaming.py:70)."""
+    g = torch.Generator().manual_seed(d)
+    x = torch.rand(20000, d, generator=g) * torch.exp(torch.randn(20000, 1, generator=g) * 3)
+    x[:50] = torch.rand(50, d, generator=g) * 1e-3 + torch.arange(d) * 1e3   # wide spread
+    assert np.array_equal(ref.mean_fp32_4x8(x.numpy()), x.mean(-1).numpy())
+
+
+# Max (1960), Table 1: optimum output levels of the N(0, 1) quantizer (4 digits).
+# The 1- and 2-bit iterations converge (break before 100 steps) to these.
+_MAX_LEVELS = {1: [0.7979], 2: [0.4528, 1.510]}
+
+
+@pytest.mark.parametrize("bits", [1, 2])
+def test_lloyd_max_converged_widths_match_max_table(bits):
+    cb = ref.lloyd_max_codebook(128, bits).astype(np.float64) * math.sqrt(128)
+    half = np.array(_MAX_LEVELS[bits])
+    np.testing.assert_allclose(cb, np.concatenate([-half[::-1], half]), atol=6e-4)
+    if bits == 1:
+        assert abs(cb[1] - math.sqrt(2 / math.pi)) < 1e-6      # E|X| closed form
+
+
+@pytest.mark.parametrize("bits", [3, 4, 5, 6, 7])
+def test_lloyd_max_widths_match_reference_golden(golden, bits):
+    """Widths whose iteration stops at the 100-step cap: the reference's own output."""
+    assert np.array_equal(ref.lloyd_max_codebook(128, bits), golden("lloyd_max_bits.npz")[f"cb{bits}"])
+
+
+def _rotated64(x, signs):
+    import scipy.linalg as sl
+    t = x.astype(np.float64)
+    n = np.maximum(np.sqrt((t * t).sum(-1)), 1e-8)
+    H = sl.hadamard(x.shape[-1]) / math.sqrt(x.shape[-1])
+    return ((t / n[:, None]) * signs) @ H.T, n
+
+
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_stream_qjl_oracle(bits):
+    """QJL fields (streaming.py:67-70, 77-78) against an fp64 restatement, and the
+    exact per-token error identity ||r - cb - s m||^2 = ||r - cb||^2 - d m^2 for
+    m = mean |r - cb| that makes the 1-bit term a strict improvement."""
+    cb = ref.lloyd_max_codebook(128, bits)
+    signs = ref.stream_signs(4, 128)
+    x = (torch.randn(1500, 128, generator=torch.Generator().manual_seed(bits)) * 2).half().numpy()
+    idx, nrm = ref.quantize_stream_token(x, signs, cb)
+    idx2, nrm2, qs, qsc = ref.quantize_stream_token(x, signs, cb, qjl=True)
+    assert np.array_equal(idx, idx2) and np.array_equal(nrm, nrm2)
+    assert qs.dtype == np.uint8 and qsc.dtype == np.float16 and qsc.shape == nrm.shape
+    r, n = _rotated64(x, signs)
+    res = r - cb.astype(np.float64)[idx.astype(np.int64)]
+    clear = np.abs(res) > 1e-6
+    assert np.array_equal(qs[clear], (res >= 0)[clear])
+    m = np.abs(res).mean(-1)
+    np.testing.assert_allclose(qsc.astype(np.float64), m, rtol=1.2e-3)
+    # the oracle's dequantization adds +-scale: output-domain error drops by ~d m^2 n^2
+    y0 = ref.dequantize_stream_token(idx, nrm, signs, cb).astype(np.float64)
+    y1 = ref.dequantize_stream_token(idx, nrm, signs, cb, qs, qsc).astype(np.float64)
+    t = x.astype(np.float64)
+    e0 = ((y0 - t) ** 2).sum(-1)
+    e1 = ((y1 - t) ** 2).sum(-1)
+    pred = e0 - 128 * (qsc.astype(np.float64) * n) ** 2
+    fp16_noise = 128 * (np.abs(t).max(-1) * 2.0 ** -10) ** 2
+    assert np.all(np.abs(e1 - pred) <= 0.02 * e0 + 4 * fp16_noise)
+    assert e1.mean() < e0.mean() * (0.9 if bits <= 4 else 1.0)
+
+
 # --------------------------------------------------------------------------
 # VQ assignment and k-means
 # --------------------------------------------------------------------------
