@@ -1,30 +1,34 @@
 // Fused decode attention over Shard's compressed KV cache, written for gfx950.
 //
 // Work split (one split launch + one combine launch per layer-step):
-//   split kernel   grid = (n_splits * n_kv/NB, B); a 256-thread workgroup owns
-//                  NB kv heads x a chunk of compressed tokens.  Wave w owns the
-//                  16 RoPE pairs [16w, 16w+16) of each of its NB heads, so the
-//                  sin/cos of a (token, pair) is computed once per wave and the
-//                  int4 coefficient tile is unpacked once for NB heads.
+//   split kernel   grid = (n_splits * n_kv, B); a 512-thread workgroup (one per
+//                  CU) owns one kv head x a chunk of compressed tokens, which it
+//                  walks 64 tokens at a time: waves 0-3 take the first 32-token
+//                  tile, waves 4-7 the second.  Wave w owns the 16 RoPE pairs
+//                  [16 (w%4), 16 (w%4) + 16) of the head, so the sin/cos of a
+//                  (token, pair) is computed once.
 //     1. no-RoPE keys are rebuilt on chip with MFMA 32x32x16 f16:
 //          K_n[rows, tok] = Basis'[rows, r] . coef[r, tok] + mean
 //        Basis' = fp16(basis_f16 * coeff_scale) lives in VGPRs for the whole
 //        kernel; coef are the packed nibbles (128-bit loads, prefetched one
-//        tile ahead) turned into exact fp16 integers n-8 with a magic-number
-//        trick; the accumulators start from the mean (LDS).  Keys never reach HBM.
+//        iteration ahead) turned into exact fp16 integers n-8 with a
+//        magic-number trick; the mean is one more k-step (times a constant 1).
+//        Keys never reach HBM.
 //     2. each (c, d) pair is rotated by phi = (pos_t - pos_q) * theta_i (the
 //        relative-delta RoPE identity, attention.py:3-6) and dotted with
 //        q_n = undo-RoPE(q, pos_q) by a second MFMA (rows = query heads).
-//        sin/cos(phi) advance by one fixed rotation per 32-token tile.
-//     3. the 4 waves' partial scores are summed in LDS, online softmax (fp32,
-//        base-2), and the VQ values sum_t p_t * cb[idx_t] (rotated space) are
-//        accumulated with the fp32 codebook in LDS.
+//        sin/cos(phi) advance by one fixed rotation per iteration.
+//     3. the 4 pair slices' partial scores are summed in LDS, online softmax
+//        (fp32, base 2), and the VQ values sum_t p_t * cb[idx_t] (rotated
+//        space) are accumulated with the codebook in LDS.
 //     4. per (query head, split): running max m, sum l and the 128-dim
 //        accumulator go to the workspace.
-//   combine kernel grid = (n_q, B): merges the splits, applies ch and ONE
-//                  inverse Hadamard to the VQ accumulator, adds the fp16 sink /
-//                  window / decode tokens and the dequantized 8-bit stream
-//                  tokens, normalizes, writes fp16.
+//     The last split of each head first runs the extra tokens (fp16 sink,
+//     window and decode tokens, the dequantized stream) into one more partial
+//     row per query head.
+//   combine kernel grid = (n_q, B): merges the partial rows, applies ch and ONE
+//                  inverse Hadamard to the VQ part, adds the plain-basis part of
+//                  the extra tokens, normalizes, writes fp16.
 #include "common.h"
 
 namespace shard {
@@ -53,7 +57,10 @@ struct ExtraSegs {
 };
 
 struct SplitParams {
-  int32_t B, H, G, rank, n_comp, cstart, pos_q, n_splits, chunk;
+  int32_t B, H, G, rank, n_comp, cstart, pos_q, n_splits;
+  // Token ranges: splits [0, n_first) cover `chunk` tokens each, the others
+  // `chunk2` (two_class: the first and the second workgroup of each CU).
+  int32_t chunk, chunk2, n_first, two_class;
   int32_t nsp;   // partial rows per (batch row, query head): n_splits (+1 with extra tokens)
   ExtraSegs xs;  // processed by the last split of each head before its compressed tiles
   const uint16_t* q;
@@ -71,8 +78,6 @@ struct SplitParams {
   float* ws_acc;
 };
 
-// 8 packed nibbles (n0 in bits 0-3 ... n7 in bits 28-31) -> 8 exact fp16 values
-// n-8 in element order (n0, n4, n1, n5, n2, n6, n3, n7).
 // (x & m) | (y & ~m) in one VALU op; the compiler would emit and + or for
 // literal masks (a three-operand op takes one literal at most).
 __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
@@ -81,24 +86,23 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
   return r;
 }
 
-__device__ __forceinline__ half8 nib8_to_half8(uint32_t x) {
+// 8 packed nibbles (n0 in bits 0-3 ... n7 in bits 28-31) -> 8 fp16 values in
+// element order (n0, n4, n1, n5, n2, n6, n3, n7).  A nibble dropped into the
+// mantissa of 1024.0 (0x6400) reads as 1024 + n from bits 0-3 of a half and
+// as 1024 + 16 n from bits 4-7.  Elements 0, 1, 4, 5 (even nibbles) become the
+// exact integers n - 8 with one packed subtraction per pair; elements 2, 3, 6,
+// 7 (odd nibbles) stay 1024 + 16 n.  The basis operand carries 16 x the even
+// ranks' entries, and the mean k-step the constant that the odd ranks' 1152
+// offset leaves (k_decode_prepare), so the MFMA yields 16 K.  Seven VALU ops.
+__device__ __forceinline__ half8 nib8_to_mfma(uint32_t x) {
   const uint32_t x8 = x >> 8;
   const uint32_t m0 = 0x000F000Fu, m1 = 0x00F000F0u, magic = 0x64006400u;
-  const uint32_t v0 = bfi(m0, x, magic);    // 1024 + n0 | 1024 + n4
-  const uint32_t v1 = bfi(m1, x, magic);    // 1024 + 16 n1 | 1024 + 16 n5
-  const uint32_t v2 = bfi(m0, x8, magic);   // 1024 + n2 | 1024 + n6
-  const uint32_t v3 = bfi(m1, x8, magic);   // 1024 + 16 n3 | 1024 + 16 n7
   const half2v k1032 = {(half_t)1032.f, (half_t)1032.f};
-  const half2v k16 = {(half_t)0.0625f, (half_t)0.0625f};
-  const half2v k72 = {(half_t)72.f, (half_t)72.f};
-  half2v h0 = __builtin_bit_cast(half2v, v0) - k1032;
-  half2v h1 = __builtin_bit_cast(half2v, v1) * k16 - k72;
-  half2v h2 = __builtin_bit_cast(half2v, v2) - k1032;
-  half2v h3 = __builtin_bit_cast(half2v, v3) * k16 - k72;
-  half8 r;
-  r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-  r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-  return r;
+  const half2v e0 = __builtin_bit_cast(half2v, bfi(m0, x, magic)) - k1032;
+  const half2v e2 = __builtin_bit_cast(half2v, bfi(m0, x8, magic)) - k1032;
+  const uint4 r = make_uint4(__builtin_bit_cast(uint32_t, e0), bfi(m1, x, magic),
+                             __builtin_bit_cast(uint32_t, e2), bfi(m1, x8, magic));
+  return __builtin_bit_cast(half8, r);
 }
 
 // element e of a converted dword holds nibble nib_perm(e)
@@ -134,10 +138,15 @@ __device__ __forceinline__ void load_coef(const uint8_t* rowp, bool valid, uint3
 
 // Per-layer constant operands (shard_decode_prepare), in HBM after compression:
 //   op   uint4 [G][4 P][KS+1][64 lanes]: the MFMA A operand of wave P of head g,
-//        k-steps 0..KS-1 = fp16(basis * coeff_scale) in the nibble order of the
-//        coefficient dwords, k-step KS = the fp16 mean in element 0 of the lanes
-//        of the first half (paired with a constant 1 operand), so the key
-//        accumulators start at zero;
+//        k-steps 0..KS-1 = A'(r) = fp16(basis * coeff_scale) in the nibble order
+//        of the coefficient dwords, times 16 for even ranks r (see
+//        nib8_to_mfma); k-step KS = C = 16 mean - 1152 sum_{r odd} A'(r) as
+//        16 fp16 parts (paired with a constant-1 operand), which cancels the
+//        odd ranks' 1024 + 16 n encoding:
+//          16 sum_r A'(r)(n_r - 8) + 16 mean = C + sum_{r even} 16 A'(r)(n_r - 8)
+//                                              + sum_{r odd} A'(r)(1024 + 16 n_r)
+//        The parts hold |C| up to about 9.8e5 (greedy split, 15 x 65504 + rest),
+//        far above real keys (|C| is a few thousand).
 //   rope float2 [32][64] = (cos, sin)(col * theta_i) for the token column inside
 //        a tile, then float2 [64] = (cos, sin)(32 * theta_i), the per-tile step.
 __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint16_t* __restrict__ cs,
@@ -160,12 +169,20 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = r0 + nib_perm(e);
-          v[e] = (half_t)(h2f(basis[(int64_t)row * rank + r]) * h2f(cs[r]));
+          const half_t a = (half_t)(h2f(basis[(int64_t)row * rank + r]) * h2f(cs[r]));
+          v[e] = (e & 2) ? a : (half_t)(16.f * (float)a);  // elements 2, 3, 6, 7: odd ranks
         }
       } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (half_t)0.f;
-        if (hh == 0) v[0] = __builtin_bit_cast(half_t, mean[row]);
+        double c = 16.0 * (double)h2f(mean[row]);
+        for (int r = 1; r < rank; r += 2)
+          c -= 1152.0 * (double)(float)(half_t)(h2f(basis[(int64_t)row * rank + r]) * h2f(cs[r]));
+        // greedy split into 16 fp16 parts (8 per lane half), largest first
+        for (int part = 0; part < 16; ++part) {
+          const double cl = c > 65504.0 ? 65504.0 : (c < -65504.0 ? -65504.0 : c);
+          const half_t h = (half_t)(float)cl;
+          if (part >> 3 == hh) v[part & 7] = h;
+          c -= (double)(float)h;
+        }
       }
       op[i] = __builtin_bit_cast(uint4, v);
     } else {
@@ -204,19 +221,42 @@ __device__ __forceinline__ const uint16_t* extra_row(const ExtraSegs& s, int B, 
   return base + row * kHD;
 }
 
-constexpr int kXTok = 128;  // extra tokens per pass (32 per wave)
+#ifndef SHARD_DECODE_TG
+#define SHARD_DECODE_TG 1
+#endif
+#ifndef SHARD_SPLIT_BIAS
+#define SHARD_SPLIT_BIAS 1
+#endif
+// With two workgroups per CU, the first-dispatched one runs a tile in about
+// 1.15 us and the second in about 2.05 us while both are resident, and the
+// second finishes its set-up about 1.3 tiles later (measured on MI355X at 8K
+// and 32K).  Equal finishing times then give the first one
+//   ta = 0.47 + 0.64 N  tiles  of every N = ta + tb.
+// SHARD_SPLIT_BIAS=0 keeps even chunks.
+constexpr bool kSplitBias = SHARD_SPLIT_BIAS;
+// 32-token tiles a split workgroup processes side by side, one per group of 4
+// waves.  Two tiles (512 threads, one workgroup per CU, 2 waves per SIMD in
+// lockstep) rather than two 256-thread workgroups per CU: the older of two
+// co-resident workgroups gets issue priority and the younger then finishes
+// alone at 1 wave per SIMD, a tail that costs up to a quarter of the kernel.
+constexpr int kTG = SHARD_DECODE_TG;
+static_assert(kTG == 1 || kTG == 2, "SHARD_DECODE_TG must be 1 or 2");
 
 // Extra tokens (sink, window, decode, stream; fp16 rows) of kv head g, run by
-// the last split workgroup of the head before its compressed tiles.  Per pass
-// of 128 tokens: scores on MFMA (rows = the kGQA query heads, k = head dims,
-// columns = the wave's 32 tokens), online softmax per head (wave h owns head
-// h), values accumulated lane-per-dim pair.  Writes partial row n_splits of
-// each query head, in the plain (not rotated) basis.
+// the last split workgroup of the head before its compressed tiles, with NW
+// waves.  Per pass of 32 NW tokens: scores on MFMA (rows = the kGQA query
+// heads, k = head dims, columns = the wave's 32 tokens), online softmax per
+// head (wave h < kGQA owns head h), values accumulated lane-per-dim pair.
+// Writes partial row n_splits of each query head, in the plain (not rotated)
+// basis.
+template <int NW>
 __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const int g, const int b) {
-  __shared__ __align__(16) float xsc[kGQA][kXTok];     // scores of the pass (base 2)
-  __shared__ __align__(16) float xpw[kXTok][kGQA];     // softmax numerators, [token][head]
-  __shared__ __align__(16) float2 xred[4][kGQA][64];   // per-wave value sums
-  __shared__ float xal[kGQA];                          // rescale of the running sums
+  constexpr int XT = 32 * NW;  // tokens per pass
+  constexpr int XV = XT / 64;  // softmax values per lane
+  __shared__ __align__(16) float xsc[kGQA][XT];       // scores of the pass (base 2)
+  __shared__ __align__(16) float xpw[XT][kGQA];       // softmax numerators, [token][head]
+  __shared__ __align__(16) float2 xred[NW][kGQA][64]; // per-wave value sums
+  __shared__ float xal[kGQA];                         // rescale of the running sums
 
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -232,12 +272,12 @@ __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const i
       Aq[st] = __builtin_bit_cast(half8, col < kGQA ? v4 : make_uint4(0u, 0u, 0u, 0u));
     }
   }
-  float m_run = -INFINITY, l_run = 0.f;  // softmax state of head w
+  float m_run = -INFINITY, l_run = 0.f;  // softmax state of head w (w < kGQA)
   float2 acc[kGQA];
 #pragma unroll
   for (int h = 0; h < kGQA; ++h) acc[h] = make_float2(0.f, 0.f);
 
-  for (int x0 = 0; x0 < n_x; x0 += kXTok) {
+  for (int x0 = 0; x0 < n_x; x0 += XT) {
     const int xt = min(x0 + 32 * w + col, n_x - 1);  // clamped: rows past n_x are masked
     int mpos;
     const uint16_t* krow = extra_row(p.xs, p.B, p.G, p.n_comp, b, g, xt, false, &mpos);
@@ -263,16 +303,25 @@ __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const i
       for (int i = 0; i < kGQA; ++i) xsc[i][32 * w + col] = valid ? sacc[i] * sc + madd : -INFINITY;
     }
     __syncthreads();
-    {  // wave w: online softmax of head w over the pass
-      const float s0 = xsc[w][lane], s1 = xsc[w][lane + 64];
-      const float m_new = fmaxf(m_run, wave64_reduce(fmaxf(s0, s1), OpMax()));
+    if (w < kGQA) {  // wave w: online softmax of head w over the pass
+      float s[XV];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < XV; ++k) {
+        s[k] = xsc[w][lane + 64 * k];
+        mx = fmaxf(mx, s[k]);
+      }
+      const float m_new = fmaxf(m_run, wave64_reduce(mx, OpMax()));
       const float al = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
-      const float p0 = s0 == -INFINITY ? 0.f : exp2f(s0 - m_new);
-      const float p1 = s1 == -INFINITY ? 0.f : exp2f(s1 - m_new);
-      l_run = l_run * al + wave64_reduce(p0 + p1, OpAdd());
+      float ps = 0.f;
+#pragma unroll
+      for (int k = 0; k < XV; ++k) {
+        const float pk = s[k] == -INFINITY ? 0.f : exp2f(s[k] - m_new);
+        ps += pk;
+        xpw[lane + 64 * k][w] = pk;
+      }
+      l_run = l_run * al + wave64_reduce(ps, OpAdd());
       m_run = m_new;
-      xpw[lane][w] = p0;
-      xpw[lane + 64][w] = p1;
       if (lane == 0) xal[w] = al;
     }
     __syncthreads();
@@ -295,11 +344,11 @@ __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const i
 #pragma unroll
   for (int h = 0; h < kGQA; ++h) xred[w][h][lane] = acc[h];
   __syncthreads();
-  {
+  if (w < kGQA) {
     const int h = w;
     float2 t = xred[0][h][lane];
 #pragma unroll
-    for (int u = 1; u < 4; ++u) {
+    for (int u = 1; u < NW; ++u) {
       const float2 a = xred[u][h][lane];
       t.x += a.x;
       t.y += a.y;
@@ -313,61 +362,80 @@ __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const i
   }
 }
 
-template <int KS, int NB>
-__global__ __launch_bounds__(kThreads, NB == 1 ? 2 : 1)
+template <int KS, int TG>
+__global__ __launch_bounds__(256 * TG, TG == 1 ? 2 : 1)
 void k_decode_split(const SplitParams p) {
-  constexpr int NQ = kGQA * NB;          // query heads of this workgroup
-  constexpr int TS = 8 / NB;             // token subsets of the V stage
-  constexpr int VT = kTile / TS;         // tokens per V-stage thread per tile
-  constexpr int SPT = (NQ * kTile + kThreads - 1) / kThreads;
+  constexpr int NT = 256 * TG;    // threads
+  constexpr int TT = kTile * TG;  // tokens per iteration: one tile per group of 4 waves
+  constexpr int NQ = kGQA;        // query heads of the workgroup's kv head
+  constexpr int VT = 4;           // V-stage tokens per thread per iteration
+  constexpr int TS = TT / VT;     // V-stage token subsets
+  static_assert(TS * 32 == NT, "V stage: 32 dim groups x TS token subsets");
+  static_assert(NQ * TT <= NT, "softmax: at most one entry per thread");
 
-  __shared__ __align__(16) float sp[4][NQ][kTile];   // per-wave partial scores
-  __shared__ __align__(16) half_t pp16[NQ][kTile];   // softmax numerators of the tile (fp16)
-  __shared__ __align__(16) float alpha_s[NQ];        // rescale factors of the tile
-  __shared__ __align__(16) uint2 cbl[256];           // VQ codebook (4 x fp16 per entry)
-  __shared__ __align__(16) float2 phq[64];           // (cos, sin)(pos_q * theta_i)
-  __shared__ __align__(16) float2 phb[64];           // (cos, sin)(delta of the chunk start)
-  __shared__ __align__(16) float red[kThreads][16];  // end-of-chunk reduction
+  __shared__ __align__(16) float sp[TG][4][NQ][kTile];  // per-wave partial scores
+  __shared__ __align__(16) half_t pp16[NQ][TT];         // softmax numerators (fp16)
+  __shared__ __align__(16) float alpha_s[NQ];           // rescale factors of the iteration
+  __shared__ __align__(16) uint2 cbl[256];              // VQ codebook (4 x fp16 per entry)
+  __shared__ __align__(16) float2 phq[64];              // (cos, sin)(pos_q * theta_i)
+  __shared__ __align__(16) float2 phb[64];              // (cos, sin)(delta of the chunk start)
+  __shared__ __align__(16) float2 phs[64];              // (cos, sin)(TT * theta_i)
+  __shared__ __align__(16) float red[NT][17];           // end-of-chunk reduction
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int P = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = pair slice (SGPR)
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int P = wv & 3;     // pair slice of the wave (16 RoPE pairs)
+  const int grp = wv >> 2;  // tile of the iteration the wave works on
   const int col = lane & 31;
   const int hh = lane >> 5;
 
-  // ---- block -> (head group, split).  The dispatcher deals blocks to the 8
-  // XCDs in turn (block id mod 8).  With n_splits % 8 == 0 all head groups of
-  // one split get block ids congruent mod 8, so they share one XCD and its L2
+  // ---- block -> (kv head, split).  The dispatcher deals blocks to the 8
+  // XCDs in turn (block id mod 8).  With n_splits % 8 == 0 all heads of one
+  // split get block ids congruent mod 8, so they share one XCD and its L2
   // fetches the split's coefficient rows (read by every head) once; otherwise
-  // consecutive blocks are consecutive head groups of one split.
-  const int HG = p.G / NB;
+  // consecutive blocks are consecutive heads of one split.
+  //
+  // two_class (exactly two workgroups per CU): the dispatcher fills one slot
+  // of every CU with the first 256 workgroups and the second slot with the
+  // next 256.  The older workgroup of a CU gets issue priority, so splits
+  // [0, n_first) go to the first class with longer chunks and the second class
+  // gets shorter ones; both then finish together.  Each class holds half the
+  // splits of every (batch row, kv head).
+  const int HG = p.G;
   const int bid = blockIdx.x;
-  int hg, split;
-  if (kSplitPerXcd && (p.n_splits & 7) == 0) {
-    const int slot = bid >> 3;
+  int hg, split, b;
+  if (p.two_class) {
+    const int L = blockIdx.y * gridDim.x + bid;  // dispatch order
+    const int c = L >> 8, j = L & 255;
+    const int slot = j >> 3;
     hg = slot % HG;
-    split = (slot / HG) * 8 + (bid & 7);
+    const int q = (slot / HG) * 8 + (j & 7);
+    b = q / p.n_first;
+    split = c * p.n_first + q % p.n_first;
   } else {
-    hg = bid % HG;
-    split = bid / HG;
+    if (kSplitPerXcd && (p.n_splits & 7) == 0) {
+      const int slot = bid >> 3;
+      hg = slot % HG;
+      split = (slot / HG) * 8 + (bid & 7);
+    } else {
+      hg = bid % HG;
+      split = bid / HG;
+    }
+    b = blockIdx.y;
   }
-  const int b = blockIdx.y;
   // The last split of each head runs the extra tokens first (its compressed
   // chunk is shorter by their cost), so their cold loads overlap the other
   // workgroups' set-up instead of trailing the kernel.
-  if (split == p.n_splits - 1 && p.xs.n_x > 0) {
-#pragma unroll
-    for (int j = 0; j < NB; ++j) decode_extras_tail(p, hg * NB + j, b);
-  }
+  if (split == p.n_splits - 1 && p.xs.n_x > 0) decode_extras_tail<4 * TG>(p, hg, b);
 
   // ---- loads that feed LDS and the q operand go out first: the first barrier
   // waits for these only, not for the tile and basis loads behind them.
-  const uint2 cb_v = *(const uint2*)(p.vcb + 4 * tid);   // 256 codebook entries, one per thread
-  const float th_v = tid < 128 ? p.inv_freq[tid & 63] : 0.f;
+  const uint2 cb_v = tid < 256 ? *(const uint2*)(p.vcb + 4 * tid) : make_uint2(0u, 0u);
+  const float th_v = tid < 192 ? p.inv_freq[tid & 63] : 0.f;
   uint2 q_lo[2], q_hi[2];
   {
-    const int qr = col;
-    const uint16_t* qv = p.q + ((int64_t)b * p.H + hg * NQ + min(qr, NQ - 1)) * kHD;
+    const uint16_t* qv = p.q + ((int64_t)b * p.H + hg * NQ + min(col, NQ - 1)) * kHD;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int d0 = 16 * P + 8 * jj + 4 * hh;
@@ -375,24 +443,23 @@ void k_decode_split(const SplitParams p) {
       q_hi[jj] = *(const uint2*)(qv + d0 + 64);
     }
   }
-  const int t_begin = split * p.chunk;
-  int t_end = t_begin + p.chunk;
+  const int t_begin = split < p.n_first ? split * p.chunk
+                                         : p.n_first * p.chunk + (split - p.n_first) * p.chunk2;
+  int t_end = t_begin + (split < p.n_first ? p.chunk : p.chunk2);
   if (t_end > p.n_comp) t_end = p.n_comp;
 
-  // ---- first tile's loads go out before the setup work.  Token indices are
-  // clamped to the chunk (no divergent loads); rows past the chunk end get
+  // ---- first iteration's loads go out before the setup work.  Token indices
+  // are clamped to the chunk (no divergent loads); rows past the chunk end get
   // -inf scores and zero weights.
   const int64_t coef_row_bytes = p.rank / 2;
   const int rowb = KS * 4;  // bytes per lane-half of a coefficient row
   const uint8_t* coef_b = p.coef + (int64_t)b * p.n_comp * coef_row_bytes + rowb * hh;
   const int vG = tid & 31;
-  const int vts = (tid >> 5) % TS;
-  const int vj = (tid >> 5) / TS;
-  const int vg = hg * NB + vj;
-  const uint8_t* vidx_b = p.vidx + (((int64_t)b * p.G + vg) * p.n_comp) * 32 + vG;
+  const int vts = tid >> 5;
+  const uint8_t* vidx_b = p.vidx + (((int64_t)b * p.G + hg) * p.n_comp) * 32 + vG;
   const int t_last = t_end > t_begin ? t_end - 1 : t_begin;
   auto load_tile = [&](int t0, uint32_t (&cw_)[KS], uint32_t (&vc_)[VT]) {
-    const int tc = min(t0 + col, t_last);
+    const int tc = min(t0 + kTile * grp + col, t_last);
     load_coef<KS>(coef_b + (int64_t)tc * coef_row_bytes, true, cw_);
 #pragma unroll
     for (int m = 0; m < VT; ++m) vc_[m] = vidx_b[(int64_t)min(t0 + VT * vts + m, t_last) * 32];
@@ -401,40 +468,41 @@ void k_decode_split(const SplitParams p) {
   if (t_begin < t_end) load_tile(t_begin, cwA, vcA);
 
   // ---- per-layer constant operands: coalesced 16-byte loads
-  half8 Ab[NB][KS + 1];
+  half8 Ab[KS + 1];
+  {
+    const uint4* opp = p.op + ((int64_t)(hg * 4 + P) * (KS + 1)) * 64 + lane;
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const uint4* opp = p.op + ((int64_t)((hg * NB + j) * 4 + P) * (KS + 1)) * 64 + lane;
-#pragma unroll
-    for (int s = 0; s <= KS; ++s) Ab[j][s] = __builtin_bit_cast(half8, opp[s * 64]);
+    for (int s = 0; s <= KS; ++s) Ab[s] = __builtin_bit_cast(half8, opp[s * 64]);
   }
   int pr[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) pr[i] = 16 * P + 8 * (i >> 2) + 4 * hh + (i & 3);
-  float2 rc[8], rs[8];
+  float2 rc[8], r32[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    rc[i] = p.rope[col * 64 + pr[i]];      // (cos, sin)(col * theta)
-    rs[i] = p.rope[32 * 64 + pr[i]];       // (cos, sin)(32 * theta)
+    rc[i] = p.rope[col * 64 + pr[i]];  // (cos, sin)(col * theta)
+    r32[i] = p.rope[32 * 64 + pr[i]];  // (cos, sin)(32 * theta)
   }
 
-  cbl[tid] = cb_v;
-  if (tid < 128) {
-    const float x = tid < 64 ? (float)p.pos_q * th_v : (float)(p.cstart + t_begin - p.pos_q) * th_v;
+  if (tid < 256) cbl[tid] = cb_v;
+  if (tid < 192) {
+    const int k = tid >> 6;  // 0: q position, 1: chunk start delta, 2: iteration step
+    const float x = k == 0 ? (float)p.pos_q * th_v
+                  : k == 1 ? (float)(p.cstart + t_begin - p.pos_q) * th_v
+                           : (float)TT * th_v;
     float sn, cn;
     sincosf(x, &sn, &cn);
-    (tid < 64 ? phq : phb)[tid & 63] = make_float2(cn, sn);
+    (k == 0 ? phq : k == 1 ? phb : phs)[tid & 63] = make_float2(cn, sn);
   }
   __syncthreads();
 
   // q_n = undo-RoPE(q_rope, pos_q): a = q_lo cos + q_hi sin, b = q_hi cos - q_lo sin
-  half8 Aq[NB][2];
+  half8 Aq[2];
   {
-    const int qr = col;  // MFMA row = query head within the workgroup
     float a_[8], b_[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) { a_[i] = 0.f; b_[i] = 0.f; }
-    if (qr < NQ) {
+    if (col < NQ) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         const uint2 lo4 = q_lo[jj], hi4 = q_hi[jj];
@@ -451,34 +519,37 @@ void k_decode_split(const SplitParams p) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const bool mine = (qr >> 2) == j && qr < NQ;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        Aq[j][0][e] = (half_t)(mine ? a_[e] : 0.f);
-        Aq[j][1][e] = (half_t)(mine ? b_[e] : 0.f);
-      }
+    for (int e = 0; e < 8; ++e) {
+      Aq[0][e] = (half_t)a_[e];
+      Aq[1][e] = (half_t)b_[e];
     }
   }
 
-  // ---- relative phase of this lane's token at the first tile:
-  // phi = delta(chunk start) * theta + col * theta; advanced by 32 theta per tile
+  // ---- relative phase of this lane's token at the first iteration:
+  // phi = delta(chunk start) * theta + (32 grp + col) * theta; advanced by
+  // TT * theta per iteration
   float ph_c[8], ph_s[8];
+  float2 rstep[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float2 bb = phb[pr[i]];
-    ph_c[i] = bb.x * rc[i].x - bb.y * rc[i].y;
-    ph_s[i] = bb.y * rc[i].x + bb.x * rc[i].y;
+    float c = bb.x * rc[i].x - bb.y * rc[i].y;
+    float s = bb.y * rc[i].x + bb.x * rc[i].y;
+    if (grp) {
+      const float c2 = c * r32[i].x - s * r32[i].y;
+      s = s * r32[i].x + c * r32[i].y;
+      c = c2;
+    }
+    ph_c[i] = c * 0.0625f;  // the rebuilt keys come out 16x: fold 1/16 in (exact)
+    ph_s[i] = s * 0.0625f;
+    rstep[i] = phs[pr[i]];
   }
-  half8 one8;
+  half8 one8;  // the B operand of the mean k-step: 1 in all 16 k-elements
 #pragma unroll
-  for (int e = 0; e < 8; ++e) one8[e] = (half_t)0.f;
-  one8[0] = (half_t)(hh == 0 ? 1.f : 0.f);
+  for (int e = 0; e < 8; ++e) one8[e] = (half_t)1.f;
 
-  // ---- softmax-stage state (thread owns entries e = tid + 256*k)
-  float m_run[SPT], l_part[SPT];
-#pragma unroll
-  for (int k = 0; k < SPT; ++k) { m_run[k] = -INFINITY; l_part[k] = 0.f; }
+  // ---- softmax-stage state: thread tid < NQ * TT owns (head tid / TT, token tid % TT)
+  float m_run = -INFINITY, l_part = 0.f;
   const float sc = kLog2e * rsqrtf((float)kHD);
 
   float vacc[4][4];
@@ -488,39 +559,30 @@ void k_decode_split(const SplitParams p) {
     for (int e = 0; e < 4; ++e) vacc[a][e] = 0.f;
 
   auto tile = [&](const int t0, const uint32_t (&cw)[KS], const uint32_t (&vc)[VT]) {
-    // 1. no-RoPE keys of NB heads for 32 tokens (rows x tokens, fp32):
-    //    mean (k-step KS, times a constant 1) + basis . coefficients
-    float16v acc[NB];
+    // 1. 16 x the no-RoPE keys of the wave's 32 rows for the group's 32 tokens
+    //    (fp32): constant (k-step KS, times 1) + basis . coefficients
     const float16v zero16 = {};
+    float16v acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[KS], one8, zero16, 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[j][KS], one8, zero16, 0, 0, 0);
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const half8 bo = nib8_to_half8(cw[s]);
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[j][s], bo, acc[j], 0, 0, 0);
-    }
+    for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[s], nib8_to_mfma(cw[s]), acc, 0, 0, 0);
 
     // 2. rotate pairs by phi(t, i), then dot with q_n on MFMA
-    float16v sacc = zero16;
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
+    float16v sacc;
+    {
       half8 b0, b1;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float c = acc[j][i], d = acc[j][i + 8];
+        const float c = acc[i], d = acc[i + 8];
         b0[i] = (half_t)(c * ph_c[i] - d * ph_s[i]);
         b1[i] = (half_t)(d * ph_c[i] + c * ph_s[i]);
       }
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[j][0], b0, sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[j][1], b1, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[0], b0, zero16, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[1], b1, sacc, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float c = ph_c[i] * rs[i].x - ph_s[i] * rs[i].y;
-      const float s = ph_s[i] * rs[i].x + ph_c[i] * rs[i].y;
+      const float c = ph_c[i] * rstep[i].x - ph_s[i] * rstep[i].y;
+      const float s = ph_s[i] * rstep[i].x + ph_c[i] * rstep[i].y;
       ph_c[i] = c;
       ph_s[i] = s;
     }
@@ -528,39 +590,37 @@ void k_decode_split(const SplitParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int row = 8 * (i >> 2) + 4 * hh + (i & 3);
-      if (row < NQ) sp[P][row][col] = sacc[i];
+      if (row < NQ) sp[grp][P][row][col] = sacc[i];
     }
     __syncthreads();
 
-    // 3a. online softmax over the tile (base 2, scores scaled by log2e/sqrt(D))
-#pragma unroll
-    for (int k = 0; k < SPT; ++k) {
-      const int e = tid + kThreads * k;
-      if (e < NQ * kTile) {
-        const int qr = e >> 5, tt = e & 31;
-        const int tok = t0 + tt;
-        float s = -INFINITY;
-        if (tok < t_end) {
-          s = sp[0][qr][tt] + sp[1][qr][tt] + sp[2][qr][tt] + sp[3][qr][tt];
-          s *= sc;
-          if (p.mask) s += p.mask[(int64_t)b * p.mask_stride + p.n_sink + tok] * kLog2e;
-        }
-        const float tmax = half32_reduce(s, OpMax());
-        const float m_new = fmaxf(m_run[k], tmax);
-        const float al = (m_new == -INFINITY) ? 1.f : exp2f(m_run[k] - m_new);
-        const float pv = (s == -INFINITY) ? 0.f : exp2f(s - m_new);
-        l_part[k] = l_part[k] * al + pv;
-        m_run[k] = m_new;
-        pp16[qr][tt] = (half_t)pv;
-        if (tt == 0) alpha_s[qr] = al;
+    // 3a. online softmax over the iteration's TT tokens (base 2, scores scaled
+    //     by log2e/sqrt(D)); a head's tokens fill one wave (TT = 64) or half
+    if (tid < NQ * TT) {
+      const int qr = tid / TT, tt = tid % TT;
+      const int tok = t0 + tt;
+      float s = -INFINITY;
+      if (tok < t_end) {
+        const int gg = tt >> 5, c = tt & 31;
+        s = sp[gg][0][qr][c] + sp[gg][1][qr][c] + sp[gg][2][qr][c] + sp[gg][3][qr][c];
+        s *= sc;
+        if (p.mask) s += p.mask[(int64_t)b * p.mask_stride + p.n_sink + tok] * kLog2e;
       }
+      const float tmax = TT == 64 ? wave64_reduce(s, OpMax()) : half32_reduce(s, OpMax());
+      const float m_new = fmaxf(m_run, tmax);
+      const float al = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+      const float pv = (s == -INFINITY) ? 0.f : exp2f(s - m_new);
+      l_part = l_part * al + pv;
+      m_run = m_new;
+      pp16[qr][tt] = (half_t)pv;
+      if (tt == 0) alpha_s[qr] = al;
     }
     __syncthreads();
 
     // 3b. VQ values (dot2 over token pairs, fp32 accumulation):
     //     vacc[q][e] = alpha * vacc + sum_t p[q,t] * cb[idx[t,G]][e]
     {
-      const float4 al4 = *(const float4*)&alpha_s[4 * vj];
+      const float4 al4 = *(const float4*)&alpha_s[0];
       const float alv[4] = {al4.x, al4.y, al4.z, al4.w};
 #pragma unroll
       for (int a = 0; a < 4; ++a)
@@ -569,7 +629,7 @@ void k_decode_split(const SplitParams p) {
       uint32_t pq[4][VT / 2];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const uint32_t* src = (const uint32_t*)&pp16[4 * vj + a][VT * vts];
+        const uint32_t* src = (const uint32_t*)&pp16[a][VT * vts];
 #pragma unroll
         for (int u = 0; u < VT / 2; ++u) pq[a][u] = src[u];
       }
@@ -591,26 +651,22 @@ void k_decode_split(const SplitParams p) {
     }
   };
 
-  for (int t0 = t_begin; t0 < t_end; t0 += 2 * kTile) {
-    // ping-pong buffers: the next tile's loads are in flight during this tile
-    load_tile(t0 + kTile, cwB, vcB);
+  for (int t0 = t_begin; t0 < t_end; t0 += 2 * TT) {
+    // ping-pong buffers: the next iteration's loads are in flight during this one
+    load_tile(t0 + TT, cwB, vcB);
     tile(t0, cwA, vcA);
-    if (t0 + kTile < t_end) {
-      load_tile(t0 + 2 * kTile, cwA, vcA);
-      tile(t0 + kTile, cwB, vcB);
+    if (t0 + TT < t_end) {
+      load_tile(t0 + 2 * TT, cwA, vcA);
+      tile(t0 + TT, cwB, vcB);
     }
   }
 
   // ---- chunk epilogue: (m, l) per query head and the reduced accumulators
-#pragma unroll
-  for (int k = 0; k < SPT; ++k) {
-    const int e = tid + kThreads * k;
-    const float l = half32_reduce(l_part[k], OpAdd());
-    if (e < NQ * kTile && (e & 31) == 0) {
-      const int qr = e >> 5;
-      const int qh = hg * NQ + qr;
-      const int64_t widx = ((int64_t)b * p.H + qh) * p.nsp + split;
-      p.ws_m[widx] = m_run[k];
+  if (tid < NQ * TT) {
+    const float l = TT == 64 ? wave64_reduce(l_part, OpAdd()) : half32_reduce(l_part, OpAdd());
+    if (tid % TT == 0) {
+      const int64_t widx = ((int64_t)b * p.H + hg * NQ + tid / TT) * p.nsp + split;
+      p.ws_m[widx] = m_run;
       p.ws_l[widx] = l;
     }
   }
@@ -619,19 +675,13 @@ void k_decode_split(const SplitParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) red[tid][4 * a + e] = vacc[a][e];
   __syncthreads();
-  if (vts == 0) {
-    float sum[16];
+  // thread (vG, i): value i = 4 a + e of dim group vG, summed over the TS subsets
+  for (int i = tid >> 5; i < 16; i += NT / 32) {
+    float s = red[vG][i];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sum[i] = red[tid][i];
-    for (int u = 1; u < TS; ++u)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sum[i] += red[tid + 32 * u][i];
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int qh = hg * NQ + 4 * vj + a;
-      float* dst = p.ws_acc + (((int64_t)b * p.H + qh) * p.nsp + split) * kHD + 4 * vG;
-      *(float4*)dst = make_float4(sum[4 * a], sum[4 * a + 1], sum[4 * a + 2], sum[4 * a + 3]);
-    }
+    for (int u = 1; u < TS; ++u) s += red[32 * u + vG][i];
+    const int qh = hg * NQ + (i >> 2);
+    p.ws_acc[(((int64_t)b * p.H + qh) * p.nsp + split) * kHD + 4 * vG + (i & 3)] = s;
   }
 }
 
@@ -773,24 +823,14 @@ void k_decode_combine(const CombineParams p) {
   }
 }
 
-#ifndef SHARD_DECODE_NB
-#define SHARD_DECODE_NB 1
-#endif
-// kv heads per split workgroup.  One head keeps the kernel at 2 waves per SIMD
-// (a single wave per SIMD issues an MFMA only every 32 cycles and a VALU op
-// every ~8), two heads halve the int4 unpacking per head at 1 wave per SIMD.
-constexpr int kNB = SHARD_DECODE_NB;
-constexpr int kSplitWavesPerSimd = kNB == 1 ? 2 : 1;
-
-inline int choose_splits(const shard_decode_args* a, int NB) {
+inline int choose_splits(const shard_decode_args* a) {
   const int max_useful = (a->n_comp + kTile - 1) / kTile;
   int want;
   if (a->n_splits > 0) {
     want = a->n_splits;
   } else {
-    const int HG = a->n_kv_heads / NB;
-    const int target = 256 * kSplitWavesPerSimd;  // workgroups that fill 256 CUs
-    want = target / (HG * a->batch);
+    const int target = kTG == 1 ? 512 : 256;  // workgroups that fill 256 CUs
+    want = target / (a->n_kv_heads * a->batch);
   }
   if (want > max_useful) want = max_useful;
   if (want < 1) want = 1;
@@ -798,11 +838,9 @@ inline int choose_splits(const shard_decode_args* a, int NB) {
   return want;
 }
 
-
-
 template <int KS>
 void launch_split(const SplitParams& sp, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((k_decode_split<KS, kNB>), grid, dim3(kThreads), 0, s, sp);
+  hipLaunchKernelGGL((k_decode_split<KS, kTG>), grid, dim3(256 * kTG), 0, s, sp);
 }
 
 }  // namespace shard
@@ -841,7 +879,7 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
 size_t shard_decode_attn_workspace(const shard_decode_args* a) {
   if (!a || a->batch <= 0 || a->n_q_heads <= 0 || a->n_comp <= 0) return 0;
   const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
-  const int nsp = choose_splits(a, kNB) + (n_x > 0 ? 1 : 0);
+  const int nsp = choose_splits(a) + (n_x > 0 ? 1 : 0);
   return (size_t)a->batch * a->n_q_heads * nsp * (kHD + 2) * sizeof(float);
 }
 
@@ -851,7 +889,7 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
       !a->v_ch || !a->out)
     return SHARD_ERR_ARG;
   if (a->batch <= 0 || a->n_comp <= 0) return SHARD_ERR_ARG;
-  if (a->head_dim != kHD || a->n_q_heads != kGQA * a->n_kv_heads || a->n_kv_heads % kNB != 0)
+  if (a->head_dim != kHD || a->n_q_heads != kGQA * a->n_kv_heads)
     return SHARD_ERR_SHAPE;
   if (a->rank <= 0 || a->rank % 32 != 0 || a->rank > 192) return SHARD_ERR_SHAPE;
   if (a->n_sink < 0 || a->n_win < 0 || a->n_dec < 0 || a->n_stream < 0) return SHARD_ERR_ARG;
@@ -861,7 +899,7 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
       (a->n_dec && (!a->dec_k || !a->dec_v || a->dec_stride < a->n_dec)) ||
       (a->n_stream && (!a->s_k || !a->s_v)))
     return SHARD_ERR_ARG;
-  const int ns = choose_splits(a, kNB);
+  const int ns = choose_splits(a);
   const int nsp = ns + (n_x > 0 ? 1 : 0);
   if (!workspace || workspace_bytes < shard_decode_attn_workspace(a)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
@@ -878,7 +916,26 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   // n_x / 64 more of them and the last split takes what remains.
   const int n_tiles = (a->n_comp + kTile - 1) / kTile;
   const int x_cost = (n_x + 63) / 64;
-  sp.chunk = ((n_tiles + x_cost + ns - 1) / ns) * kTile;
+  const int cap = n_tiles + x_cost;
+  const int chunk_tiles = (cap + ns - 1) / ns;
+  sp.chunk = ((chunk_tiles + kTG - 1) / kTG) * kTG * kTile;
+  sp.chunk2 = sp.chunk;
+  sp.n_first = ns;
+  sp.two_class = 0;
+  const int half = ns / 2;
+  if (kTG == 1 && kSplitBias && (int64_t)ns * a->n_kv_heads * a->batch == 512 &&
+      ns % 2 == 0 && 32 % a->n_kv_heads == 0 && n_tiles >= 2 * ns) {
+    // first class: ta tiles per split, second class: tb (the last split also
+    // runs the extra tokens, counted as x_cost tiles)
+    const int ta = (97 * half + 64 * cap) / (100 * half);  // round(0.47 + 0.64 cap / half)
+    const int tb = (cap - half * ta + half - 1) / half;
+    if (ta >= 1 && tb >= 1) {
+      sp.chunk = ta * kTile;
+      sp.chunk2 = tb * kTile;
+      sp.n_first = half;
+      sp.two_class = 1;
+    }
+  }
   sp.nsp = nsp;
   sp.xs.sink_k = a->sink_k; sp.xs.sink_v = a->sink_v;
   sp.xs.win_k = a->win_k; sp.xs.win_v = a->win_v;
@@ -893,7 +950,7 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   sp.mask = a->mask; sp.mask_stride = a->mask_stride; sp.n_sink = a->n_sink;
   sp.ws_m = ws; sp.ws_l = ws + nm; sp.ws_acc = ws + 2 * nm;
 
-  dim3 grid((unsigned)(ns * (a->n_kv_heads / kNB)), (unsigned)a->batch);
+  dim3 grid((unsigned)(ns * a->n_kv_heads), (unsigned)a->batch);
   switch (a->rank / 16) {
     case 2: launch_split<2>(sp, grid, s); break;
     case 4: launch_split<4>(sp, grid, s); break;
