@@ -365,7 +365,11 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
     shard Cache (8-bit stream on, fused decode attention) against the fp16
     DynamicCache on the same GPU, as benchmarks/benchmark.py:614-726 measures it:
     prefill, one-time compression and greedy decode timed separately;
-    tokens/s = batch x new_tokens / decode seconds."""
+    tokens/s = batch x new_tokens / decode seconds.  The shard run decodes the
+    fp16 run's greedy tokens (teacher forcing, same work per step) and reports
+    per-step top-1 agreement and logit cosine against the fp16 logits: with
+    random weights the keys are not low-rank and near-uniform logits flip
+    under any perturbation, so free-running token agreement says little."""
     from transformers import LlamaConfig, LlamaForCausalLM, DynamicCache
     from shard_amd import Cache, enable_llama_fused_attention
     cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336,
@@ -399,16 +403,31 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
             progress(f"compressed layer {li}")
         cache._compressed = True
 
-    def decode(cache, first, n):
-        nxt, toks = first, []
+    def decode(cache, first, n, forced=None, ref_logits=None):
+        """Greedy decode of n tokens; with `forced` (batch, n) the inputs after
+        `first` are those tokens, and each step's logits are compared with
+        ref_logits[step] (top-1 agreement, cosine) or kept (ref_logits None)."""
+        nxt, toks, logits, agree, cos = first, [], [], [], []
         t0 = sync_time()
         with torch.no_grad():
-            for _ in range(n):
-                out = model(nxt, past_key_values=cache, use_cache=True)
-                nxt = out.logits[:, -1:].argmax(-1)
-                toks.append(nxt)
+            for i in range(n):
+                lg = model(nxt, past_key_values=cache, use_cache=True).logits[:, -1]
+                tok = lg.argmax(-1, keepdim=True)
+                toks.append(tok)
+                if forced is None:
+                    logits.append(lg.half())
+                    nxt = tok
+                else:
+                    ref = ref_logits[i].float()
+                    agree.append((tok[:, 0] == ref.argmax(-1)).float().mean())
+                    cos.append(torch.nn.functional.cosine_similarity(lg.float(), ref, dim=-1).mean())
+                    nxt = forced[:, i:i + 1]
         t1 = sync_time()
-        return t1 - t0, torch.cat(toks, 1)
+        stats = None
+        if forced is not None:
+            stats = {"teacher_forced_top1_agreement": round(torch.stack(agree).mean().item(), 4),
+                     "teacher_forced_logit_cosine": round(torch.stack(cos).mean().item(), 5)}
+        return t1 - t0, torch.cat(toks, 1), logits, stats
 
     with torch.no_grad():                      # warm-up on a short prompt (kernels, allocator)
         wc = Cache.from_model(model)
@@ -422,6 +441,7 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
     torch.cuda.empty_cache()
     progress("warm-up done")
     res = {}
+    fp16_toks = fp16_logits = None
     for kind in ("fp16", "shard"):
         torch.cuda.empty_cache()
         torch.cuda.reset_peak_memory_stats()
@@ -445,25 +465,34 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
             r["peak_compress_gb"] = round(torch.cuda.max_memory_allocated() / 1e9, 2)
             r["clean_compress_ratio"] = round(cache.clean_compress_ratio(), 2)
         torch.cuda.reset_peak_memory_stats()
-        dt, toks = decode(cache, first, new_tokens)
+        if kind == "fp16":
+            dt, toks, fp16_logits, _ = decode(cache, first, new_tokens)
+            fp16_toks = toks
+        else:
+            dt, toks, _, stats = decode(cache, first, new_tokens, forced=fp16_toks, ref_logits=fp16_logits)
+            r.update(stats)
         r["decode_s"] = round(dt, 3)
         r["tokens_per_s"] = round(batch * new_tokens / dt, 1)
         r["ms_per_step"] = round(dt / new_tokens * 1000.0, 3)
-        r["peak_decode_gb"] = round(torch.cuda.max_memory_allocated() / 1e9, 2)
-        r["tokens"] = toks.cpu()
+        # the fp16 run's kept logits (alive during both decodes) are not part of
+        # either cache's footprint
+        kept = sum(x.numel() * x.element_size() for x in fp16_logits) / 1e9
+        r["peak_decode_gb"] = round(torch.cuda.max_memory_allocated() / 1e9 - kept, 2)
         progress(f"{kind}: decode {r['decode_s']} s, {r['tokens_per_s']} tokens/s")
         res[kind] = r
         del cache
-    match = (res["fp16"]["tokens"] == res["shard"]["tokens"]).float().mean().item()
-    for r in res.values():
-        r.pop("tokens")
     return {"metric": "e2e decode tokens/s, shard cache vs fp16 cache (BASELINE config 5)",
             "unit": "tokens/s", "value": res["shard"]["tokens_per_s"],
             "vs_fp16_cache": round(res["shard"]["tokens_per_s"] / res["fp16"]["tokens_per_s"], 3),
             "config": {"model": "Llama-3.1-8B architecture, random init, fp16", "layers": layers,
                        "batch": batch, "prompt": prompt, "new_tokens": new_tokens,
                        "data": "random token ids (seeded)"},
-            "shard": res["shard"], "fp16": res["fp16"], "greedy_token_match_rate": round(match, 4)}
+            "shard": res["shard"], "fp16": res["fp16"],
+            "note": ("teacher-forced agreement with the fp16 cache is low by construction with "
+                     "random weights: keys are full-rank (the rank-limited PCA keeps a fraction of "
+                     "their energy), V is Gaussian (2 bits per value after VQ) and attention "
+                     "outputs dominate the residual stream; kernel parity is established against "
+                     "the CPU oracle and fused vs unfused decode agree (tests/test_gpu_*.py)")}
 
 
 def main():
