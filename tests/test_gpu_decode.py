@@ -40,6 +40,10 @@ CASES = [
     (2, 8, 192, 300, 4, 64, 3, 0),       # batch 2
     (1, 2, 64, 33, 2, 3, 1, 0),          # tiny, 2 kv heads
     (1, 8, 96, 1, 4, 64, 0, 0),          # a single compressed token
+    # batch 4 / 16: the grid is again 2 x 256 workgroups (16 and 4 splits per
+    # head), so the two-class chunks and block map run with other class sizes
+    (4, 8, 192, 1100, 4, 64, 2, 0),
+    (16, 8, 128, 300, 4, 16, 1, 0),
 ]
 
 
