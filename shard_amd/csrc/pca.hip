@@ -1,74 +1,139 @@
 // PCA projection GEMM of prefill compression on gfx950 MFMA:
 //   C[m, n] (fp32) = A[m, k] (fp16, row-major) . Bt[n, k]^T (fp16, row-major)
-// The basis side Bt (n <= 256 components) is tiny and shared by every
-// workgroup, so it is staged in LDS per 64-wide k chunk; A streams from HBM.
-// Workgroup = 4 waves x 32 rows = 128 rows; each wave owns all n columns
-// (n/32 accumulator blocks of v_mfma_f32_32x32x16_f16).
+// Workgroup = 8 waves, one 128-row tile of A and all n <= 256 columns: wave w
+// owns rows 32 (w % 4) .. + 32 and column half w / 4 (n/32 accumulator blocks
+// of v_mfma_f32_32x32x16_f16 split over the two halves), so every SIMD runs
+// two waves.  The basis side Bt is small and read by every workgroup: it is
+// staged in LDS 64 k at a time, double-buffered; both its pieces and the A
+// fragments are loaded into registers three chunks ahead (a 4-slot ring), so
+// L2 and HBM latency hide behind the MFMAs of the chunks in between; one
+// barrier per chunk.  All global loads are raw buffer loads whose bounds
+// (rows past m, k past the row end) are handled by an out-of-range offset that
+// the hardware answers with zeros: no load sits under a branch, so the
+// compiler's wait counters stay exact and a chunk waits only for its own data.
 #include "common.h"
 
 namespace shard {
 
-constexpr int kPcaThreads = 256;
+constexpr int kPcaThreads = 512;
 constexpr int kPcaRows = 128;
-constexpr int kKc = 64;  // k chunk staged in LDS
+#ifndef SHARD_PCA_KC
+#define SHARD_PCA_KC 64
+#endif
+constexpr int kKc = SHARD_PCA_KC;  // k chunk staged in LDS
+// buffer resource word 3 for raw (untyped, unswizzled) dword access on gfx9
+constexpr int kBufWord3 = 0x00020000;
+constexpr int kOutOfRange = 0x7fffff00;  // a byte offset past every buffer here
 
 template <int NB32>
-__global__ __launch_bounds__(kPcaThreads, 2)
+__global__ __launch_bounds__(kPcaThreads, 1)
 void k_pca_project(const uint16_t* __restrict__ A, int64_t m, int k, int64_t lda,
                    const uint16_t* __restrict__ Bt, float* __restrict__ C, int64_t ldc) {
-  // Bt chunk: NB32*32 rows x 64 halves, padded row stride to spread LDS banks
-  constexpr int kRowStride = kKc + 8;
-  __shared__ __align__(16) uint16_t bs[NB32 * 32 * kRowStride];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  constexpr int kRowStride = kKc + 8;            // halves per staged row (bank spread)
+  constexpr int NH = (NB32 + 1) / 2;             // column blocks per wave half
+  constexpr int kPieces = NB32 * 32 * (kKc / 8);  // 16-byte pieces of one Bt chunk
+  constexpr int kPer = (kPieces + kPcaThreads - 1) / kPcaThreads;
+  __shared__ __align__(16) uint16_t bs[2][NB32 * 32 * kRowStride];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rw = w & 3, half = w >> 2;
   const int col = lane & 31, hh = lane >> 5;
-  const int64_t row0 = (int64_t)blockIdx.x * kPcaRows + 32 * w;
-  const int64_t arow = row0 + col;
-  const bool arow_ok = arow < m;
-  const uint16_t* ap = A + (arow_ok ? arow : 0) * lda;
+  const int j0 = half * NH;
+  const int nj = NB32 - j0 < NH ? NB32 - j0 : NH;  // this wave's column blocks
+  const int64_t blk0 = (int64_t)blockIdx.x * kPcaRows;
+  const int64_t row0 = blk0 + 32 * rw;
+  // buffer resources: this workgroup's rows of A, and all of Bt (byte sizes
+  // < 2^31, checked by the host); offsets at or past the size read as zero
+  const int64_t nrows = m - blk0 < kPcaRows ? m - blk0 : kPcaRows;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + blk0 * lda), (short)0, (int)(nrows * lda * 2), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)Bt, (short)0, NB32 * 32 * k * 2, kBufWord3);
+  const int a_off = (32 * rw + col) * (int)lda * 2;  // byte offset of this lane's A row
+  const int nc = (k + kKc - 1) / kKc;
 
-  float16v acc[NB32];
+  auto load_b = [&](int c, uint4 (&pb)[kPer]) {
 #pragma unroll
-  for (int j = 0; j < NB32; ++j) acc[j] = {};
-
-  for (int k0 = 0; k0 < k; k0 += kKc) {
-    // stage Bt[:, k0:k0+64] (16-byte pieces)
-    const int pieces = NB32 * 32 * (kKc / 8);
-    for (int pc = tid; pc < pieces; pc += kPcaThreads) {
-      const int r = pc / (kKc / 8), c8 = pc % (kKc / 8);
-      const int kk = k0 + 8 * c8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (kk < k) v = *(const uint4*)(Bt + (int64_t)r * k + kk);
-      *(uint4*)(bs + r * kRowStride + 8 * c8) = v;
+    for (int u = 0; u < kPer; ++u) {
+      const int pc = tid + kPcaThreads * u;
+      const int r = pc / (kKc / 8), kk = kKc * c + 8 * (pc % (kKc / 8));
+      const int off = (pc < kPieces && kk < k) ? (r * k + kk) * 2 : kOutOfRange;
+      pb[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
     }
-    // A fragments for the 4 k-steps of this chunk (16 B per lane per step)
-    half8 af[kKc / 16];
+  };
+  auto store_b = [&](int buf, const uint4 (&pb)[kPer]) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int pc = tid + kPcaThreads * u;
+      if (pc < kPieces) *(uint4*)(&bs[buf][(pc / (kKc / 8)) * kRowStride + 8 * (pc % (kKc / 8))]) = pb[u];
+    }
+  };
+  auto load_a = [&](int c, half8 (&af)[kKc / 16]) {
 #pragma unroll
     for (int s = 0; s < kKc / 16; ++s) {
-      const int kk = k0 + 16 * s + 8 * hh;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (arow_ok && kk < k) v = *(const uint4*)(ap + kk);
-      af[s] = __builtin_bit_cast(half8, v);
+      const int kk = kKc * c + 16 * s + 8 * hh;
+      const int off = kk < k ? a_off + kk * 2 : kOutOfRange;
+      af[s] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
     }
-    __syncthreads();
+  };
+
+  float16v acc[NH];
+#pragma unroll
+  for (int j = 0; j < NH; ++j) acc[j] = {};
+
+  // ring: chunk c's basis pieces and A fragments live in slot c % 4
+  uint4 pb[4][kPer];
+  half8 af[4][kKc / 16];
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    load_b(d, pb[d]);
+    load_a(d, af[d]);
+  }
+  store_b(0, pb[0]);
+  __syncthreads();
+
+  // chunk c: MFMAs from LDS buffer c & 1; then chunk c + 1's pieces into the
+  // other buffer (last read in iteration c - 1) and chunk c + 3's loads into
+  // the slot chunk c - 1 used.  The chunk count is rounded up to a multiple of
+  // the ring length: chunks past k read zeros (out-of-range offsets) and add
+  // exact zeros, so the loop body is one straight-line block and the
+  // compiler's wait counts name exactly the chunk being consumed.
+  auto step = [&](const int c, const half8 (&a)[kKc / 16], half8 (&a3)[kKc / 16],
+                  const uint4 (&b1)[kPer], uint4 (&b3)[kPer]) {
+    const uint16_t* b = bs[c & 1];
 #pragma unroll
     for (int s = 0; s < kKc / 16; ++s) {
 #pragma unroll
-      for (int j = 0; j < NB32; ++j) {
-        const uint4 bv = *(const uint4*)(bs + (32 * j + col) * kRowStride + 16 * s + 8 * hh);
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s], __builtin_bit_cast(half8, bv),
-                                                        acc[j], 0, 0, 0);
+      for (int jj = 0; jj < NH; ++jj) {
+        if (NB32 % 2 == 0 || jj < nj) {
+          const uint4 bv = *(const uint4*)(b + (32 * (j0 + jj) + col) * kRowStride + 16 * s + 8 * hh);
+          acc[jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s], __builtin_bit_cast(half8, bv), acc[jj], 0, 0, 0);
+        }
       }
     }
+    store_b((c + 1) & 1, b1);
+    load_b(c + 3, b3);
+    load_a(c + 3, a3);
     __syncthreads();
+  };
+  const int nc4 = (nc + 3) & ~3;
+  for (int c0 = 0; c0 < nc4; c0 += 4) {
+    step(c0, af[0], af[3], pb[1], pb[3]);
+    step(c0 + 1, af[1], af[0], pb[2], pb[0]);
+    step(c0 + 2, af[2], af[1], pb[3], pb[1]);
+    step(c0 + 3, af[3], af[2], pb[0], pb[2]);
   }
   // C layout of the 32x32 block: lane (col, hh), reg i -> row 8*(i/4) + 4*hh + i%4
 #pragma unroll
-  for (int j = 0; j < NB32; ++j)
+  for (int jj = 0; jj < NH; ++jj) {
+    if (jj < nj) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t r = row0 + 8 * (i >> 2) + 4 * hh + (i & 3);
-      if (r < m) C[r * ldc + 32 * j + col] = acc[j][i];
+      for (int i = 0; i < 16; ++i) {
+        const int64_t r = row0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (r < m) C[r * ldc + 32 * (j0 + jj) + col] = acc[jj][i];
+      }
     }
+  }
 }
 
 }  // namespace shard
@@ -80,6 +145,9 @@ extern "C" int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_
                                  void* stream) {
   if (!a || !bt || !c || m <= 0 || k <= 0 || n <= 0) return SHARD_ERR_ARG;
   if (k % 16 != 0 || n % 32 != 0 || n > 256 || lda < k || ldc < n || (lda % 8) != 0)
+    return SHARD_ERR_SHAPE;
+  // byte ranges of the buffer resources (one workgroup's A rows, all of Bt)
+  if ((int64_t)kPcaRows * lda * 2 >= (1ll << 31) - 256 || (int64_t)n * k * 2 >= (1ll << 31) - 256)
     return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)((m + kPcaRows - 1) / kPcaRows));
