@@ -256,6 +256,239 @@ __global__ void k_vq_assign(const float* __restrict__ x, int64_t n,
 }
 
 // ---------------------------------------------------------------------------
+// Nearest centroid of 4-dim rows among k = 32 NB centroids (NB <= 8): the
+// same result as k_vq_assign, found in two stages.
+//  1. Screen on MFMA.  key(c) = bias + |c|^2 - 2 x.c (= |x - c|^2 - |x|^2 +
+//     bias) for 32 rows x 32 centroids per pair of v_mfma_f32_32x32x16_bf16
+//     (32 k slots): x and t = -2c are split into three bf16 parts each and
+//     x.t ~ xh.th + xm.th + xh.tm + xl.th + xm.tm + xh.tl; |c|^2 takes three
+//     slots and the row's bias bf16(1.03125 S) one.  S = max|c|^2 + 2 sum_j
+//     |x_j| max|c_j| bounds ||c|^2 - 2 x.c|, so every key is a positive float
+//     and orders like its bits as an unsigned integer.  The low 4 mantissa
+//     bits of every key are replaced by the centroid's register index within
+//     its 32-centroid block, and each lane keeps the two smallest keys of
+//     every block (v_min_u32, v_med3_u32: 3 VALU ops per row and centroid).
+//  2. Certify.  Every key is within 1.13e-5 S of the exact bias + |c|^2 -
+//     2 x.c: dropped split products 4.01 2^-24 |x_j t_j| (2.4e-7 S), |c|^2 in
+//     fp32 and its parts (4.5e-7 S), fp32 accumulation of the 28 terms
+//     (< 27 2^-23 of their absolute sum <= 2.1 S: 6.8e-6 S, a worst case) and
+//     the code (15 ulp of a key < 2.1 S: 3.8e-6 S).  The reference's direct
+//     fp32 distance is within 6.01 2^-24 (relative) of |x - c|^2 (six
+//     roundings of non-negative terms), so a centroid whose key exceeds
+//     thr = min key + 2^-15 (S + |x|^2) (more than the 2 E + 12.1 2^-24
+//     (|x|^2 + S) needed) can neither be the reference's argmin nor tie with
+//     it.  If the second smallest key exceeds thr the smallest key's centroid
+//     is the answer.  Otherwise the lane evaluates the reference's direct
+//     distance for the tracked keys under thr (rescanning a block whose
+//     second key is under thr, as it may hold a third), and for rows or
+//     centroids that are non-finite or outside [2^-60, 2^64] in scale (where
+//     the relative bounds could fail) for every centroid, keeping the
+//     smallest distance and, among equal ones, the smallest index, as the
+//     sequential strict-< scan does (an index-0 answer when no distance is
+//     finite).
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// the reference's distance: fp32 sum of squared differences in dim order
+__device__ __forceinline__ float vq_dist4(const float (&xv)[4], const float4 cv) {
+  const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
+  float dist = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float df = sub_rn(xv[j], cc[j]);
+    dist = add_rn(dist, mul_rn(df, df));
+  }
+  return dist;
+}
+
+__device__ __forceinline__ uint32_t umin(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a < b ? b : a; }
+// median of three unsigned values in one VALU op (no builtin exists for the
+// integer form, and the compiler rewrites the min/max expression of it)
+__device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// x = h + m + l in bf16 parts, |x - h - m - l| <= 2^-24 |x| (both
+// differences are exact in fp32)
+__device__ __forceinline__ void split3(float v, __bf16& h, __bf16& m, __bf16& l) {
+  h = (__bf16)v;
+  const float r = v - (float)h;
+  m = (__bf16)r;
+  l = (__bf16)(r - (float)m);
+}
+
+// (256, 2): at most 256 registers per lane, so the MFMA results land in VGPRs
+template <int NB>
+__global__ __launch_bounds__(256, 2)
+void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __restrict__ c,
+                      int32_t* __restrict__ idx) {
+  constexpr int K = 32 * NB;
+  __shared__ float4 cs[K];
+  __shared__ bf16x8 atab[NB][2][64];  // the A operands again, for the rare rescans
+  const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
+  for (int i = tid; i < K; i += 256) cs[i] = ((const float4*)c)[i];
+  __syncthreads();
+
+  // A operands of block b: lane (centroid 32 b + col, half hh) holds k slots
+  // 8 hh .. 8 hh + 7 of each MFMA: first [th, tm] (hh 0) | [th, tl] (hh 1),
+  // second [th, tm] (hh 0) | [|c|^2 in three parts, 1, 0, 0, 0, 0] (hh 1)
+  bf16x8 a1[NB], a2[NB];
+  float cnmax = 0.f, cm[4] = {0.f, 0.f, 0.f, 0.f};
+  bool bad = false;
+  const __bf16 one = (__bf16)1.f, nil = (__bf16)0.f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float4 cv = cs[32 * b + col];
+    const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
+    __bf16 th[4], tm[4], tl[4];
+    float cn = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      split3(-2.f * cc[j], th[j], tm[j], tl[j]);
+      cn = cn + cc[j] * cc[j];
+      cm[j] = fmaxf(cm[j], fabsf(cc[j]));
+      bad |= !(fabsf(cc[j]) <= 0x1p60f);
+    }
+    __bf16 n0, n1, n2;
+    split3(cn, n0, n1, n2);
+    cnmax = fmaxf(cnmax, cn);
+    const bf16x8 htm = {th[0], th[1], th[2], th[3], tm[0], tm[1], tm[2], tm[3]};
+    a1[b] = hh == 0 ? htm : bf16x8{th[0], th[1], th[2], th[3], tl[0], tl[1], tl[2], tl[3]};
+    a2[b] = hh == 0 ? htm : bf16x8{n0, n1, n2, one, nil, nil, nil, nil};
+    if (tid < 64) {  // every wave builds the same operands; wave 0 stores them
+      atab[b][0][lane] = a1[b];
+      atab[b][1][lane] = a2[b];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    cnmax = fmaxf(cnmax, __shfl_xor(cnmax, o));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cm[j] = fmaxf(cm[j], __shfl_xor(cm[j], o));
+  }
+  bad = __ballot(bad) != 0;  // wave-uniform
+
+  const int64_t ngroups = (n + 31) / 32;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const float16v zero = {};
+  for (int64_t g = ((int64_t)blockIdx.x * blockDim.x + tid) >> 6; g < ngroups; g += nwaves) {
+    const int64_t row = g * 32 + col;
+    const bool valid = row < n;
+    const float4 x4 = ((const float4*)x)[valid ? row : 0];
+    const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+    // B operands: lane (row col, half hh): first [xh, xh] (hh 0) | [xm, xh]
+    // (hh 1), second [xl, xm] (hh 0) | [1, 1, 1, bias, 0, 0, 0, 0] (hh 1)
+    __bf16 xh[4], xm[4], xl[4];
+    float S = 0.f, xx = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      split3(xv[j], xh[j], xm[j], xl[j]);
+      S = S + fabsf(xv[j]) * cm[j];
+      xx = xx + xv[j] * xv[j];
+    }
+    S = cnmax + 2.f * S;
+    const bool in_range = !bad && S >= 0x1p-60f && S <= 0x1p64f && xx <= 0x1p64f;
+    const bf16x8 b1 = hh == 0 ? bf16x8{xh[0], xh[1], xh[2], xh[3], xh[0], xh[1], xh[2], xh[3]}
+                              : bf16x8{xm[0], xm[1], xm[2], xm[3], xh[0], xh[1], xh[2], xh[3]};
+    const bf16x8 b2 = hh == 0 ? bf16x8{xl[0], xl[1], xl[2], xl[3], xm[0], xm[1], xm[2], xm[3]}
+                              : bf16x8{one, one, one, (__bf16)(1.03125f * S), nil, nil, nil, nil};
+    auto keys = [&](int b) {
+      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          a2[b], b2, __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[b], b1, zero, 0, 0, 0), 0, 0, 0);
+    };
+    // 1. the two smallest coded keys of each block; C reg i of block b is
+    //    centroid 32 b + 8 (i / 4) + 4 hh + i % 4, code i
+    uint32_t m1[NB], m2[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float16v acc = keys(b);
+      uint32_t e[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) e[i] = (__float_as_uint(acc[i]) & ~15u) | (uint32_t)i;
+      m1[b] = umin(e[0], e[1]);
+      m2[b] = umax(e[0], e[1]);
+#pragma unroll
+      for (int i = 2; i < 16; ++i) {
+        m2[b] = umed3(m1[b], m2[b], e[i]);
+        m1[b] = umin(m1[b], e[i]);
+      }
+    }
+    // smallest key of the lane, its block, and the lane's second smallest key
+    // (the second smallest block minimum or a second key of any block)
+    uint32_t T1 = m1[0], S1 = 0xFFFFFFFFu, T2 = m2[0];
+    int blk = 0;
+#pragma unroll
+    for (int b = 1; b < NB; ++b) {
+      S1 = umed3(T1, S1, m1[b]);
+      blk = m1[b] < T1 ? b : blk;
+      T1 = umin(T1, m1[b]);
+      T2 = umin(T2, m2[b]);
+    }
+    T2 = umin(T2, S1);
+    // the other half of the lane pair holds the row's other 16 centroids of each block
+    const uint32_t oT1 = __shfl_xor(T1, 32), oT2 = __shfl_xor(T2, 32);
+    const int oblk = __shfl_xor(blk, 32);
+    const bool other = oT1 < T1;
+    const uint32_t R2 = umin(umax(T1, oT1), umin(T2, oT2));
+    const uint32_t R1 = umin(T1, oT1);
+    const int ci = (int)(R1 & 15u);
+    int best = 32 * (other ? oblk : blk) + 8 * (ci >> 2) + 4 * (other ? hh ^ 1 : hh) + (ci & 3);
+    // 2. certify, or decide by the reference's distances
+    const float thr = __uint_as_float(R1) + 0x1p-15f * (S + xx);
+    const bool amb = valid && !(in_range && __uint_as_float(R2) > thr);
+    if (__ballot(amb) != 0) {
+      const bool all = amb && !in_range;
+      const uint32_t lim = amb && in_range ? __float_as_uint(thr) : 0u;  // keys are > 0
+      float bd = INFINITY;
+      int bi = 0;
+      auto consider = [&](int j) {
+        const float d = vq_dist4(xv, cs[j]);
+        if (d < bd || (d == bd && j < bi && d < INFINITY)) {
+          bd = d;
+          bi = j;
+        }
+      };
+      auto centroid = [&](int b, int i) { return 32 * b + 8 * (i >> 2) + 4 * hh + (i & 3); };
+      if (__ballot(all) != 0) {
+#pragma unroll 1
+        for (int j = 0; j < 16 * NB; ++j)
+          if (all) consider(centroid(j >> 4, j & 15));
+      }
+      uint32_t more = 0;  // blocks whose second key is under thr may hold a third
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (m1[b] <= lim) consider(centroid(b, (int)(m1[b] & 15u)));
+        if (m2[b] <= lim) {
+          consider(centroid(b, (int)(m2[b] & 15u)));
+          more |= 1u << b;
+        }
+      }
+#pragma unroll 1
+      for (int b = 0; b < NB; ++b) {
+        const bool mb = (more >> b) & 1u;
+        if (__ballot(mb) != 0) {
+          const float16v acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              atab[b][1][lane], b2,
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(atab[b][0][lane], b1, zero, 0, 0, 0), 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (mb && __float_as_uint(acc[i]) <= lim) consider(centroid(b, i));
+        }
+      }
+      const float od = __shfl_xor(bd, 32);
+      const int oi = __shfl_xor(bi, 32);
+      if (od < bd || (od == bd && oi < bi && od < INFINITY)) bi = oi;
+      if (amb) best = bi;
+    }
+    if (hh == 0 && valid) idx[row] = best;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Deterministic k-means update: stable counting sort by centroid, then each
 // (centroid, dim) sums its rows in increasing row order (torch CPU index_add_
 // order), divides by the count, and keeps empty centroids.
@@ -617,6 +850,23 @@ int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids
   if (!x || !centroids || !idx || n <= 0 || k <= 0 || d <= 0) return SHARD_ERR_ARG;
   if (k > 1024 || d > 8) return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+  if (d == 4 && k % 32 == 0 && k <= 256 && ((uintptr_t)x & 15) == 0 &&
+      ((uintptr_t)centroids & 15) == 0) {
+    const int64_t groups = (n + 31) / 32;  // 32 rows per wave
+    const dim3 grid(grid_cap((groups + 3) / 4, 2048)), block(256);
+    switch (k / 32) {
+      case 1: hipLaunchKernelGGL(k_vq_assign_mfma<1>, grid, block, 0, s, x, n, centroids, idx); break;
+      case 2: hipLaunchKernelGGL(k_vq_assign_mfma<2>, grid, block, 0, s, x, n, centroids, idx); break;
+      case 3: hipLaunchKernelGGL(k_vq_assign_mfma<3>, grid, block, 0, s, x, n, centroids, idx); break;
+      case 4: hipLaunchKernelGGL(k_vq_assign_mfma<4>, grid, block, 0, s, x, n, centroids, idx); break;
+      case 5: hipLaunchKernelGGL(k_vq_assign_mfma<5>, grid, block, 0, s, x, n, centroids, idx); break;
+      case 6: hipLaunchKernelGGL(k_vq_assign_mfma<6>, grid, block, 0, s, x, n, centroids, idx); break;
+      case 7: hipLaunchKernelGGL(k_vq_assign_mfma<7>, grid, block, 0, s, x, n, centroids, idx); break;
+      default: hipLaunchKernelGGL(k_vq_assign_mfma<8>, grid, block, 0, s, x, n, centroids, idx); break;
+    }
+    SHARD_LAUNCH_CHECK("shard_vq_assign");
+    return SHARD_OK;
+  }
   int blocks = grid_cap((n + 255) / 256, 8192);
   size_t lds = (size_t)k * d * sizeof(float);
   switch (d) {

@@ -142,6 +142,65 @@ def test_vq_assign_bitexact(cuda):
     assert mism == 0, f"{mism} rows differ from torch.cdist argmin"
 
 
+def _vq_hard_rows(c, g):
+    """Rows that stress the MFMA screen's certification: midpoints of centroid
+    pairs (near and exact fp32 ties), rows on and near centroids, zero rows,
+    rows far outside the screen's scale range, and non-finite rows."""
+    k = c.shape[0]
+    a = torch.randint(0, k, (6000,), generator=g)
+    b = torch.randint(0, k, (6000,), generator=g)
+    mid = 0.5 * (c[a] + c[b])
+    nan, inf = float("nan"), float("inf")
+    special = torch.tensor([[nan, 0, 0, 0], [inf, 0, 0, 0], [-inf, 1, 2, 3], [1e30, 0, 0, 0],
+                            [0, 0, 0, 0], [1e-40, 0, 0, 0], [-0.0, 0, 0, 0]])
+    return torch.cat([torch.randn(9000, 4, generator=g), mid,
+                      mid + 1e-7 * torch.randn(6000, 4, generator=g),
+                      c[a] + 1e-6 * torch.randn(6000, 4, generator=g), c[a[:500]],
+                      torch.zeros(100, 4), 1e20 * torch.randn(500, 4, generator=g),
+                      1e-25 * torch.randn(500, 4, generator=g), special])
+
+
+@pytest.mark.parametrize("k", [32, 96, 160, 256])
+def test_vq_assign_hard_rows_bitexact(cuda, k):
+    """The MFMA-screened assignment (d = 4, k = 32 NB) against the sequential
+    direct-distance oracle on rows built to defeat the screen, with duplicate
+    and zero centroids (exact ties: first index wins)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(1000 + k)
+    c = torch.randn(k, 4, generator=g)
+    c[3] = c[5]
+    c[7] = 0.0
+    c[k - 1] = c[0] * (1 + 2 ** -20)
+    x = _vq_hard_rows(c, g)
+    x = x[torch.randperm(x.shape[0], generator=g)][: x.shape[0] - 13]  # ragged tail
+    got = ops.vq_assign(x.to(cuda), c.to(cuda)).cpu().numpy()
+    with np.errstate(all="ignore"):
+        want = ref.vq_assign_direct(x.numpy(), c.numpy())
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} rows differ, first {bad[:5]}: got {got[bad[:5]]} want {want[bad[:5]]}"
+
+
+@pytest.mark.parametrize("case", ["nan_centroid", "tiny_centroids", "huge_centroids"])
+def test_vq_assign_out_of_range_centroids_bitexact(cuda, case):
+    """Centroid sets the screen must not certify (non-finite, or far outside its
+    scale range): every row falls back to the reference's distances."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(77)
+    c = torch.randn(256, 4, generator=g)
+    if case == "nan_centroid":
+        c[9] = float("nan")
+        c[10, 2] = float("inf")
+    elif case == "tiny_centroids":
+        c = c * 1e-30
+    else:
+        c = c * 1e25
+    x = torch.randn(4099, 4, generator=g) * (1e-30 if case == "tiny_centroids" else 1.0)
+    got = ops.vq_assign(x.to(cuda), c.to(cuda)).cpu().numpy()
+    with np.errstate(all="ignore"):
+        want = ref.vq_assign_direct(x.numpy(), c.numpy())
+    assert np.array_equal(got, want)
+
+
 def test_kmeans_update_bitexact(cuda):
     ops = _ops()
     g = torch.Generator().manual_seed(4)
