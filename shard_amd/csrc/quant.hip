@@ -31,95 +31,159 @@ __device__ __forceinline__ float group_deq(float x, int bits, float lo, float rn
   return add_rn(mul_rn(div_rn(code, L), rng), lo);
 }
 
-__global__ void k_int4_init(uint32_t* ws, int keep) {
-  int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c < keep) {
-    ws[c] = 0xFFFFFFFFu;     // running min (ordered key)
-    ws[keep + c] = 0u;       // running max (ordered key)
-    ws[2 * keep + c] = 0u;   // running max |y| (bits of a non-negative float)
-  }
-}
+// The column reductions write one partial per (block, column) and a wave per
+// column folds the partials: no global atomics (every block would otherwise
+// hit the same keep addresses).  Column passes use blocks of (column, row
+// group) threads; thread (c, g) takes rows r0 + g, r0 + g + RG, ...
+constexpr int kI4Blocks = 256;  // partial slots per column
 
-// Column min/max over a slab of rows; one thread per column.
-__global__ void k_int4_minmax(const float* __restrict__ proj, int64_t n, int keep,
-                              int rows_per_block, uint32_t* ws) {
-  int c = threadIdx.x;
-  if (c >= keep) return;
-  int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-  int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
+__device__ __forceinline__ uint32_t u32min(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t u32max(uint32_t a, uint32_t b) { return a < b ? b : a; }
+
+// Column min/max (order-preserving keys) of one slab of rows.
+__global__ __launch_bounds__(1024) void k_int4_minmax(const float* __restrict__ proj, int64_t n,
+                                                      int keep, int64_t rows_per_block,
+                                                      uint32_t* __restrict__ pmin,
+                                                      uint32_t* __restrict__ pmax) {
+  __shared__ float smn[1024], smx[1024];
+  const int c = threadIdx.x, rg = threadIdx.y, RG = blockDim.y, w = blockDim.x;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
   float mn = INFINITY, mx = -INFINITY;
-  for (int64_t r = r0; r < r1; ++r) {
-    float x = proj[r * keep + c];
-    mn = fminf(mn, x);
-    mx = fmaxf(mx, x);
+  if (c < keep) {
+    int64_t r = r0 + rg;
+    for (; r + 3 * RG < r1; r += 4 * RG) {  // four rows in flight
+      const float x0 = proj[r * keep + c], x1 = proj[(r + RG) * keep + c];
+      const float x2 = proj[(r + 2 * RG) * keep + c], x3 = proj[(r + 3 * RG) * keep + c];
+      mn = fminf(fminf(fminf(mn, x0), fminf(x1, x2)), x3);
+      mx = fmaxf(fmaxf(fmaxf(mx, x0), fmaxf(x1, x2)), x3);
+    }
+    for (; r < r1; r += RG) {
+      const float x = proj[r * keep + c];
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
+    }
   }
-  if (r0 < r1) {
-    atomicMin(&ws[c], f2ord(mn));
-    atomicMax(&ws[keep + c], f2ord(mx));
+  smn[rg * w + c] = mn;
+  smx[rg * w + c] = mx;
+  __syncthreads();
+  if (rg == 0 && c < keep) {
+    for (int q = 1; q < RG; ++q) {
+      mn = fminf(mn, smn[q * w + c]);
+      mx = fmaxf(mx, smx[q * w + c]);
+    }
+    pmin[(int64_t)blockIdx.x * keep + c] = f2ord(mn);
+    pmax[(int64_t)blockIdx.x * keep + c] = f2ord(mx);
   }
 }
 
-__device__ __forceinline__ void col_lo_rng(const uint32_t* ws, int keep, int c,
-                                           float* lo, float* rng) {
-  float l = ord2f(ws[c]);
-  float h = ord2f(ws[keep + c]);
-  *lo = l;
-  *rng = fmaxf(sub_rn(h, l), 1e-6f);
+// One wave per column: fold the block partials; lo = min, rng = max(max - lo, 1e-6).
+__global__ void k_int4_fold_minmax(const uint32_t* __restrict__ pmin,
+                                   const uint32_t* __restrict__ pmax, int nblk, int keep,
+                                   float* __restrict__ lo, float* __restrict__ rng) {
+  const int c = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6), l = (int)lane_id();
+  if (c >= keep) return;  // whole waves
+  uint32_t a = 0xFFFFFFFFu, b = 0u;
+  for (int q = l; q < nblk; q += 64) {
+    a = u32min(a, pmin[(int64_t)q * keep + c]);
+    b = u32max(b, pmax[(int64_t)q * keep + c]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a = u32min(a, __shfl_xor(a, o));
+    b = u32max(b, __shfl_xor(b, o));
+  }
+  if (l == 0) {
+    const float lv = ord2f(a);
+    lo[c] = lv;
+    rng[c] = fmaxf(sub_rn(ord2f(b), lv), 1e-6f);
+  }
 }
 
-// Column max |y| of the dequantized values; optionally writes the group codes.
-__global__ void k_int4_absmax(const float* __restrict__ proj, int64_t n, int keep,
-                              int rows_per_block, const int32_t* __restrict__ bits,
-                              uint32_t* ws, uint8_t* __restrict__ codes) {
-  int c = threadIdx.x;
-  if (c >= keep) return;
-  int b = bits[c];
-  float lo, rng;
-  col_lo_rng(ws, keep, c, &lo, &rng);
-  int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-  int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
+// Column max |y| of the dequantized values of one slab; optionally the group codes.
+__global__ __launch_bounds__(1024) void k_int4_absmax(const float* __restrict__ proj, int64_t n,
+                                                      int keep, int64_t rows_per_block,
+                                                      const int32_t* __restrict__ bits,
+                                                      const float* __restrict__ lo,
+                                                      const float* __restrict__ rng,
+                                                      uint32_t* __restrict__ pamax,
+                                                      uint8_t* __restrict__ codes) {
+  __shared__ float sam[1024];
+  const int c = threadIdx.x, rg = threadIdx.y, RG = blockDim.y, w = blockDim.x;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
   float amax = 0.f;
-  for (int64_t r = r0; r < r1; ++r) {
+  if (c < keep) {
+    const int b = bits[c];
+    const float l = lo[c], rn = rng[c];
+    int64_t r = r0 + rg;
+    for (; r + RG < r1; r += 2 * RG) {
+      const float x0 = proj[r * keep + c], x1 = proj[(r + RG) * keep + c];
+      uint8_t k0, k1;
+      const float y0 = group_deq(x0, b, l, rn, &k0), y1 = group_deq(x1, b, l, rn, &k1);
+      amax = fmaxf(amax, fmaxf(fabsf(y0), fabsf(y1)));
+      if (codes) {
+        codes[r * keep + c] = k0;
+        codes[(r + RG) * keep + c] = k1;
+      }
+    }
+    for (; r < r1; r += RG) {
+      uint8_t k0;
+      const float y = group_deq(proj[r * keep + c], b, l, rn, &k0);
+      amax = fmaxf(amax, fabsf(y));
+      if (codes) codes[r * keep + c] = k0;
+    }
+  }
+  sam[rg * w + c] = amax;
+  __syncthreads();
+  if (rg == 0 && c < keep) {
+    for (int q = 1; q < RG; ++q) amax = fmaxf(amax, sam[q * w + c]);
+    pamax[(int64_t)blockIdx.x * keep + c] = __float_as_uint(amax);  // >= 0: bits order as values
+  }
+}
+
+// One wave per column: cs = max(max |y|, 1e-6) / 7 and the per-column outputs.
+__global__ void k_int4_fold_absmax(const uint32_t* __restrict__ pamax, int nblk, int keep,
+                                   const int32_t* __restrict__ bits, const float* __restrict__ lo,
+                                   const float* __restrict__ rng, float* __restrict__ cs,
+                                   float* coeff_scale, float* lo_out, float* rng_out) {
+  const int c = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6), l = (int)lane_id();
+  if (c >= keep) return;  // whole waves
+  uint32_t a = 0u;
+  for (int q = l; q < nblk; q += 64) a = u32max(a, pamax[(int64_t)q * keep + c]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) a = u32max(a, __shfl_xor(a, o));
+  if (l == 0) {
+    const float v = div_rn(fmaxf(__uint_as_float(a), 1e-6f), 7.0f);
+    cs[c] = v;
+    coeff_scale[c] = v;
+    if (lo_out) lo_out[c] = bits[c] > 0 ? lo[c] : 0.f;
+    if (rng_out) rng_out[c] = bits[c] > 0 ? rng[c] : 0.f;
+  }
+}
+
+// Byte i packs elements 2i and 2i + 1 of the row-major matrix; IT is 32-bit
+// when the element count allows, so the column of an element is a 32-bit mod.
+template <typename IT>
+__global__ void k_int4_pack(const float* __restrict__ proj, IT total, int keep,
+                            const int32_t* __restrict__ bits, const float* __restrict__ lo,
+                            const float* __restrict__ rng, const float* __restrict__ cs,
+                            uint8_t* __restrict__ packed) {
+  const IT nbytes = (total + 1) / 2;
+  auto q4 = [&](IT e, int c) {
     uint8_t code;
-    float y = group_deq(proj[r * keep + c], b, lo, rng, &code);
-    amax = fmaxf(amax, fabsf(y));
-    if (codes) codes[r * keep + c] = code;
+    const float y = group_deq(proj[e], bits[c], lo[c], rng[c], &code);
+    const float q = fminf(fmaxf(rintf(div_rn(y, cs[c])), -7.f), 7.f);
+    return (int)q;
+  };
+  const IT stride = (IT)gridDim.x * blockDim.x;
+  for (IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x; i < nbytes; i += stride) {
+    const IT e0 = 2 * i;
+    const int c0 = (int)(e0 % (IT)keep);
+    const int q0 = q4(e0, c0);
+    const int q1 = e0 + 1 < total ? q4(e0 + 1, c0 + 1 == keep ? 0 : c0 + 1) : -8;  // pad nibble -> 0
+    packed[i] = (uint8_t)(((q0 + 8) & 15) | (((q1 + 8) & 15) << 4));
   }
-  if (r0 < r1) atomicMax(&ws[2 * keep + c], __float_as_uint(amax));
-}
-
-__device__ __forceinline__ int q4_of(const float* __restrict__ proj, int64_t e, int keep,
-                                     const int32_t* __restrict__ bits, const uint32_t* ws) {
-  int c = (int)(e % keep);
-  float lo, rng;
-  col_lo_rng(ws, keep, c, &lo, &rng);
-  uint8_t code;
-  float y = group_deq(proj[e], bits[c], lo, rng, &code);
-  float cs = div_rn(fmaxf(__uint_as_float(ws[2 * keep + c]), 1e-6f), 7.0f);
-  float q = rintf(div_rn(y, cs));
-  q = fminf(fmaxf(q, -7.f), 7.f);
-  return (int)q;
-}
-
-__global__ void k_int4_pack(const float* __restrict__ proj, int64_t n, int keep,
-                            const int32_t* __restrict__ bits, const uint32_t* ws,
-                            uint8_t* __restrict__ packed, float* coeff_scale,
-                            float* lo_out, float* rng_out) {
-  int64_t total = n * keep;
-  int64_t nbytes = (total + 1) / 2;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < keep) {
-    float lo, rng;
-    col_lo_rng(ws, keep, (int)i, &lo, &rng);
-    coeff_scale[i] = div_rn(fmaxf(__uint_as_float(ws[2 * keep + i]), 1e-6f), 7.0f);
-    if (lo_out) lo_out[i] = bits[i] > 0 ? lo : 0.f;
-    if (rng_out) rng_out[i] = bits[i] > 0 ? rng : 0.f;
-  }
-  if (i >= nbytes) return;
-  int64_t e0 = 2 * i, e1 = 2 * i + 1;
-  int q0 = q4_of(proj, e0, keep, bits, ws);
-  int q1 = e1 < total ? q4_of(proj, e1, keep, bits, ws) : -8;  // pad nibble -> 0
-  packed[i] = (uint8_t)(((q0 + 8) & 15) | (((q1 + 8) & 15) << 4));
 }
 
 // ---------------------------------------------------------------------------
@@ -206,19 +270,35 @@ __global__ void k_vq_rot(const uint16_t* __restrict__ v, int64_t bh, int64_t seq
     for (int k = 0; k < E; ++k) atomicMax(&chmax[cur * d + l + 64 * k], __float_as_uint(m[k]));
 }
 
-__global__ void k_vq_norm(float* __restrict__ xo, int64_t bh, int64_t seq, int d,
-                          const uint32_t* __restrict__ chmax, float* ch_f32,
-                          uint16_t* ch_f16) {
-  int64_t total = bh * seq * d;
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    int64_t c = i % d;
-    int64_t b = i / (seq * d);
-    float ch = fmaxf(__uint_as_float(chmax[b * d + c]), 1e-8f);
-    xo[i] = div_rn(xo[i], ch);
-    if (i - b * seq * d < d) {  // first token of this bh writes the channel scale
-      if (ch_f32) ch_f32[b * d + c] = ch;
-      if (ch_f16) ch_f16[b * d + c] = f2h(ch);
+// x /= channel max over each (b, channel) slab of seq rows x d (d a power of
+// two, at most 256), float4 at a time; the first workgroup of a slab writes
+// the channel scales
+__global__ __launch_bounds__(256) void k_vq_norm(float* __restrict__ xo, int64_t bh, int64_t seq,
+                                                 int d, const uint32_t* __restrict__ chmax,
+                                                 float* ch_f32, uint16_t* ch_f16) {
+  __shared__ float chs[256];
+  const int tid = threadIdx.x;
+  const int64_t n4 = seq * d / 4;
+  for (int64_t b = blockIdx.y; b < bh; b += gridDim.y) {
+    __syncthreads();
+    for (int c = tid; c < d; c += 256) {
+      const float ch = fmaxf(__uint_as_float(chmax[b * d + c]), 1e-8f);
+      chs[c] = ch;
+      if (blockIdx.x == 0) {
+        if (ch_f32) ch_f32[b * d + c] = ch;
+        if (ch_f16) ch_f16[b * d + c] = f2h(ch);
+      }
+    }
+    __syncthreads();
+    float4* slab = (float4*)(xo + b * seq * d);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < n4; i += (int64_t)gridDim.x * 256) {
+      const int c = (int)((i * 4) & (d - 1));
+      float4 v = slab[i];
+      v.x = div_rn(v.x, chs[c]);
+      v.y = div_rn(v.y, chs[c + 1]);
+      v.z = div_rn(v.z, chs[c + 2]);
+      v.w = div_rn(v.w, chs[c + 3]);
+      slab[i] = v;
     }
   }
 }
@@ -726,33 +806,36 @@ __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
 // ---------------------------------------------------------------------------
 // Prefill K preparation: undo RoPE (fp32), subtract mean, fp16 GEMM operand.
 // ---------------------------------------------------------------------------
-__global__ void k_k_prepare(const uint16_t* __restrict__ k, int batch, int n_kv, int seq, int hd,
-                            int start, int n_comp, const float* __restrict__ inv_freq,
-                            const float* __restrict__ mean, uint16_t* __restrict__ out) {
-  const int D = n_kv * hd;
-  const int hd2 = hd >> 1;
-  int64_t total = (int64_t)batch * n_comp * n_kv * hd2;
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-    int i = (int)(e % hd2);
-    int64_t r = e / hd2;
-    int g = (int)(r % n_kv);
-    int64_t bt = r / n_kv;
-    int t = (int)(bt % n_comp);
-    int b = (int)(bt / n_comp);
-    int pos = start + t;
-    float ph = mul_rn((float)pos, inv_freq[i]);
+// One workgroup per token t of the window: the token's hd/2 RoPE phases are
+// computed once (shared by every batch row and kv head), then thread (i, y)
+// undoes pair i of the (b, g) rows y, y + blockDim.y, ...
+__global__ __launch_bounds__(256) void k_k_prepare(const uint16_t* __restrict__ k, int batch,
+                                                   int n_kv, int seq, int hd, int start, int n_comp,
+                                                   const float* __restrict__ inv_freq,
+                                                   const float* __restrict__ mean,
+                                                   uint16_t* __restrict__ out) {
+  __shared__ float2 ph[256];  // (cos, sin) of the token's phases, hd / 2 <= 256
+  const int hd2 = hd >> 1, D = n_kv * hd;
+  const int t = blockIdx.x, pos = start + t;
+  const int flat = threadIdx.y * blockDim.x + threadIdx.x;
+  for (int i = flat; i < hd2; i += blockDim.x * blockDim.y) {
     float sn, cs;
-    sincosf(ph, &sn, &cs);
+    sincosf(mul_rn((float)pos, inv_freq[i]), &sn, &cs);
+    ph[i] = make_float2(cs, sn);
+  }
+  __syncthreads();
+  const int i = threadIdx.x;  // blockDim.x == hd / 2
+  const float cs = ph[i].x, sn = ph[i].y;
+  for (int bg = threadIdx.y; bg < batch * n_kv; bg += blockDim.y) {
+    const int b = bg / n_kv, g = bg - b * n_kv;
     const uint16_t* src = k + (((int64_t)b * n_kv + g) * seq + pos) * hd;
-    float lo = h2f(src[i]), hi = h2f(src[i + hd2]);
+    const float lo = h2f(src[i]), hi = h2f(src[i + hd2]);
     // undo_rope: k*cos - rotate_half(k)*sin, rotate_half = [-hi, lo]
-    float ulo = add_rn(mul_rn(lo, cs), mul_rn(hi, sn));
-    float uhi = sub_rn(mul_rn(hi, cs), mul_rn(lo, sn));
-    int64_t row = (int64_t)b * n_comp + t;
-    int col = g * hd + i;
-    out[row * D + col] = f2h(sub_rn(ulo, mean[col]));
-    out[row * D + col + hd2] = f2h(sub_rn(uhi, mean[col + hd2]));
+    const float ulo = add_rn(mul_rn(lo, cs), mul_rn(hi, sn));
+    const float uhi = sub_rn(mul_rn(hi, cs), mul_rn(lo, sn));
+    uint16_t* o = out + ((int64_t)b * n_comp + t) * D + g * hd;
+    o[i] = f2h(sub_rn(ulo, mean[g * hd + i]));
+    o[i + hd2] = f2h(sub_rn(uhi, mean[g * hd + i + hd2]));
   }
 }
 
@@ -764,7 +847,8 @@ extern "C" {
 
 size_t shard_int4_quant_pack_workspace(int64_t n_rows, int32_t keep) {
   (void)n_rows;
-  return (size_t)3 * (keep > 0 ? keep : 0) * sizeof(uint32_t);
+  // pmin, pmax, pamax partials (kI4Blocks x keep) + lo, rng, cs (keep)
+  return (size_t)(3 * kI4Blocks + 3) * (keep > 0 ? keep : 0) * sizeof(uint32_t);
 }
 
 int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const int32_t* bits,
@@ -776,18 +860,33 @@ int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const
   if (!workspace || workspace_bytes < shard_int4_quant_pack_workspace(n_rows, keep))
     return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
-  uint32_t* ws = (uint32_t*)workspace;
-  const int rpb = 128;
-  int64_t nblk = (n_rows + rpb - 1) / rpb;
-  int tpb = ((keep + 63) / 64) * 64;
-  hipLaunchKernelGGL(k_int4_init, dim3((keep + 255) / 256), dim3(256), 0, s, ws, keep);
-  hipLaunchKernelGGL(k_int4_minmax, dim3((unsigned)nblk), dim3(tpb), 0, s, proj, n_rows, keep, rpb, ws);
-  hipLaunchKernelGGL(k_int4_absmax, dim3((unsigned)nblk), dim3(tpb), 0, s, proj, n_rows, keep, rpb,
-                     bits, ws, codes);
-  int64_t nbytes = (n_rows * keep + 1) / 2;
-  int64_t nthreads = nbytes > keep ? nbytes : keep;
-  hipLaunchKernelGGL(k_int4_pack, dim3((unsigned)((nthreads + 255) / 256)), dim3(256), 0, s, proj,
-                     n_rows, keep, bits, ws, packed, coeff_scale, lo, rng);
+  uint32_t* pmin = (uint32_t*)workspace;
+  uint32_t* pmax = pmin + (size_t)kI4Blocks * keep;
+  uint32_t* pamax = pmax + (size_t)kI4Blocks * keep;
+  float* clo = (float*)(pamax + (size_t)kI4Blocks * keep);
+  float* crng = clo + keep;
+  float* ccs = crng + keep;
+  const int tpb = ((keep + 63) / 64) * 64;
+  const int rg = 1024 / tpb < 4 ? 1024 / tpb : 4;
+  const int64_t nblk = n_rows / rg < kI4Blocks ? (n_rows + rg - 1) / rg : kI4Blocks;
+  const int64_t rpb = (n_rows + nblk - 1) / nblk;
+  const dim3 cgrid((unsigned)nblk), cblock(tpb, rg);
+  const dim3 fgrid((unsigned)((keep + 3) / 4)), fblock(256);  // a wave per column
+  hipLaunchKernelGGL(k_int4_minmax, cgrid, cblock, 0, s, proj, n_rows, keep, rpb, pmin, pmax);
+  hipLaunchKernelGGL(k_int4_fold_minmax, fgrid, fblock, 0, s, pmin, pmax, (int)nblk, keep, clo, crng);
+  hipLaunchKernelGGL(k_int4_absmax, cgrid, cblock, 0, s, proj, n_rows, keep, rpb, bits, clo, crng,
+                     pamax, codes);
+  hipLaunchKernelGGL(k_int4_fold_absmax, fgrid, fblock, 0, s, pamax, (int)nblk, keep, bits, clo,
+                     crng, ccs, coeff_scale, lo, rng);
+  const int64_t total = n_rows * keep;
+  const int64_t nbytes = (total + 1) / 2;
+  const dim3 pgrid(grid_cap((nbytes + 255) / 256, 8192));
+  if (total < (1ll << 31))
+    hipLaunchKernelGGL(k_int4_pack<uint32_t>, pgrid, dim3(256), 0, s, proj, (uint32_t)total, keep,
+                       bits, clo, crng, ccs, packed);
+  else
+    hipLaunchKernelGGL(k_int4_pack<uint64_t>, pgrid, dim3(256), 0, s, proj, (uint64_t)total, keep,
+                       bits, clo, crng, ccs, packed);
   SHARD_LAUNCH_CHECK("shard_int4_quant_pack");
   return SHARD_OK;
 }
@@ -838,9 +937,10 @@ int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int
     case 128: hipLaunchKernelGGL(k_vq_rot<2>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
     default: hipLaunchKernelGGL(k_vq_rot<4>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
   }
-  int64_t total = rows * hd;
-  hipLaunchKernelGGL(k_vq_norm, dim3(grid_cap((total + 255) / 256, 16384)), dim3(256), 0, s, x_out,
-                     bh, seq, hd, chmax, ch_f32, ch_f16);
+  // about four float4 per thread, all heads in flight at once
+  const int64_t per_slab = (seq * hd / 4 + 1023) / 1024;
+  const dim3 ngrid((unsigned)(per_slab < 1024 ? per_slab : 1024), (unsigned)(bh < 65535 ? bh : 65535));
+  hipLaunchKernelGGL(k_vq_norm, ngrid, dim3(256), 0, s, x_out, bh, seq, hd, chmax, ch_f32, ch_f16);
   SHARD_LAUNCH_CHECK("shard_vq_prepare");
   return SHARD_OK;
 }
@@ -945,11 +1045,12 @@ int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
                     int32_t start, int32_t n_comp, const float* inv_freq, const float* mean,
                     uint16_t* out, void* stream) {
   if (!k || !inv_freq || !mean || !out || batch <= 0 || n_kv <= 0 || n_comp <= 0) return SHARD_ERR_ARG;
-  if ((hd & 1) || start < 0 || start + n_comp > seq) return SHARD_ERR_SHAPE;
+  if ((hd & 1) || hd > 512 || start < 0 || start + n_comp > seq) return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  int64_t total = (int64_t)batch * n_comp * n_kv * (hd / 2);
-  hipLaunchKernelGGL(k_k_prepare, dim3(grid_cap((total + 255) / 256, 32768)), dim3(256), 0, s, k,
-                     batch, n_kv, seq, hd, start, n_comp, inv_freq, mean, out);
+  const int hd2 = hd / 2;
+  const dim3 block(hd2, hd2 >= 256 ? 1 : 256 / hd2);
+  hipLaunchKernelGGL(k_k_prepare, dim3((unsigned)n_comp), block, 0, s, k, batch, n_kv, seq, hd,
+                     start, n_comp, inv_freq, mean, out);
   SHARD_LAUNCH_CHECK("shard_k_prepare");
   return SHARD_OK;
 }
