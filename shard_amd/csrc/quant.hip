@@ -390,6 +390,11 @@ __device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
   asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
 }
+__device__ __forceinline__ uint32_t umin3(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_min3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 // x = h + m + l in bf16 parts, |x - h - m - l| <= 2^-24 |x| (both
 // differences are exact in fp32)
@@ -481,21 +486,28 @@ void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __res
           a2[b], b2, __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[b], b1, zero, 0, 0, 0), 0, 0, 0);
     };
     // 1. the two smallest coded keys of each block; C reg i of block b is
-    //    centroid 32 b + 8 (i / 4) + 4 hh + i % 4, code i
+    //    centroid 32 b + 8 (i / 4) + 4 hh + i % 4, code i.  Keys enter in
+    //    pairs (a, b): the new second smallest of {m1 <= m2, a, b} is
+    //    min(m2, med3(m1, a, b)) and the new smallest min3(m1, a, b), three
+    //    compare ops per two keys.  The next block's MFMAs are issued before
+    //    this block's keys are consumed.
     uint32_t m1[NB], m2[NB];
+    float16v acc = keys(0);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float16v acc = keys(b);
+      float16v nxt;
+      if (b + 1 < NB) nxt = keys(b + 1);
       uint32_t e[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) e[i] = (__float_as_uint(acc[i]) & ~15u) | (uint32_t)i;
       m1[b] = umin(e[0], e[1]);
       m2[b] = umax(e[0], e[1]);
 #pragma unroll
-      for (int i = 2; i < 16; ++i) {
-        m2[b] = umed3(m1[b], m2[b], e[i]);
-        m1[b] = umin(m1[b], e[i]);
+      for (int i = 2; i < 16; i += 2) {
+        m2[b] = umin(m2[b], umed3(m1[b], e[i], e[i + 1]));
+        m1[b] = umin3(m1[b], e[i], e[i + 1]);
       }
+      if (b + 1 < NB) acc = nxt;
     }
     // smallest key of the lane, its block, and the lane's second smallest key
     // (the second smallest block minimum or a second key of any block)
