@@ -72,7 +72,8 @@ int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
  *   cs = max(max |y|, 1e-6) / 7;  q = clamp(rint(y / cs), -7, 7)
  *     (cache.py:416-419);
  *   packed[i] = ((q[2i] + 8) & 15) | ((q[2i+1] + 8) & 15) << 4 over the
- *     row-major (n_rows, keep) matrix, zero-padded if odd
+ *     row-major (n_rows, keep) matrix; an odd count is padded with a zero
+ *     value (high nibble 8)
  *     (int4_pack, triton_kernels.py:648-682).
  * proj: (n_rows, keep) fp32 row-major.  Outputs: packed ((n_rows*keep+1)/2),
  * coeff_scale (keep, fp32), lo/rng (keep, fp32, nullable), codes

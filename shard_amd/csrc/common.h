@@ -148,13 +148,23 @@ __device__ __forceinline__ float xor_lane(float v) {
 }
 
 // ---- fast Walsh-Hadamard transform of one row held by a wave.
-// One butterfly stage across lanes l and l ^ H (element stride H).
+// One butterfly stage across lanes l and l ^ H (element stride H): the lower
+// lane of a pair gets x + p, the upper p - x.  Both are fma(s, ., .) with
+// s = +-1: s * x is exact, so the fma rounds once, exactly as the add or
+// subtract (signs of zeros included), and no select is needed.
 template <int H, int E>
 __device__ __forceinline__ void fwht_lane_stage(float (&x)[E], int l) {
+  const float s = (l & H) ? -1.f : 1.f;
 #pragma unroll
   for (int k = 0; k < E; ++k) {
-    const float p = xor_lane<H>(x[k]);
-    x[k] = (l & H) ? sub_rn(p, x[k]) : add_rn(x[k], p);
+    if constexpr (H == 16 || H == 32) {
+      float a, b;  // the pair's lower-lane and upper-lane values, in both lanes
+      if constexpr (H == 16) perm16_swap(x[k], a, b);
+      else perm32_swap(x[k], a, b);
+      x[k] = __builtin_fmaf(s, b, a);
+    } else {
+      x[k] = __builtin_fmaf(s, x[k], xor_lane<H>(x[k]));
+    }
   }
 }
 

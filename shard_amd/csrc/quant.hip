@@ -100,7 +100,7 @@ __global__ void k_int4_fold_minmax(const uint32_t* __restrict__ pmin,
   }
 }
 
-// Column max |y| of the dequantized values of one slab; optionally the group codes.
+// Column max |y| of the dequantized values of one slab, and the group codes.
 __global__ __launch_bounds__(1024) void k_int4_absmax(const float* __restrict__ proj, int64_t n,
                                                       int keep, int64_t rows_per_block,
                                                       const int32_t* __restrict__ bits,
@@ -122,16 +122,14 @@ __global__ __launch_bounds__(1024) void k_int4_absmax(const float* __restrict__ 
       uint8_t k0, k1;
       const float y0 = group_deq(x0, b, l, rn, &k0), y1 = group_deq(x1, b, l, rn, &k1);
       amax = fmaxf(amax, fmaxf(fabsf(y0), fabsf(y1)));
-      if (codes) {
-        codes[r * keep + c] = k0;
-        codes[(r + RG) * keep + c] = k1;
-      }
+      codes[r * keep + c] = k0;
+      codes[(r + RG) * keep + c] = k1;
     }
     for (; r < r1; r += RG) {
       uint8_t k0;
       const float y = group_deq(proj[r * keep + c], b, l, rn, &k0);
       amax = fmaxf(amax, fabsf(y));
-      if (codes) codes[r * keep + c] = k0;
+      codes[r * keep + c] = k0;
     }
   }
   sam[rg * w + c] = amax;
@@ -142,10 +140,12 @@ __global__ __launch_bounds__(1024) void k_int4_absmax(const float* __restrict__ 
   }
 }
 
-// One wave per column: cs = max(max |y|, 1e-6) / 7 and the per-column outputs.
+// One wave per column: cs = max(max |y|, 1e-6) / 7, the per-column outputs,
+// and the column's int4 value of every group code (y and q depend on the
+// element only through its code): qtab[c][code] = clamp(rint(y(code) / cs), -7, 7).
 __global__ void k_int4_fold_absmax(const uint32_t* __restrict__ pamax, int nblk, int keep,
                                    const int32_t* __restrict__ bits, const float* __restrict__ lo,
-                                   const float* __restrict__ rng, float* __restrict__ cs,
+                                   const float* __restrict__ rng, int8_t* __restrict__ qtab,
                                    float* coeff_scale, float* lo_out, float* rng_out) {
   const int c = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6), l = (int)lane_id();
   if (c >= keep) return;  // whole waves
@@ -153,36 +153,59 @@ __global__ void k_int4_fold_absmax(const uint32_t* __restrict__ pamax, int nblk,
   for (int q = l; q < nblk; q += 64) a = u32max(a, pamax[(int64_t)q * keep + c]);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) a = u32max(a, __shfl_xor(a, o));
+  const float cs = div_rn(fmaxf(__uint_as_float(a), 1e-6f), 7.0f);
+  const int b = bits[c];
+  const float lv = lo[c], rv = rng[c];
+  for (int code = l; code < 256; code += 64) {
+    float y = 0.f;  // columns without bits have y = 0 (code 0)
+    if (b > 0 && code < (1 << b)) {
+      const float L = (float)((1 << b) - 1);
+      y = add_rn(mul_rn(div_rn((float)code, L), rv), lv);
+    }
+    qtab[c * 256 + code] = (int8_t)fminf(fmaxf(rintf(div_rn(y, cs)), -7.f), 7.f);
+  }
   if (l == 0) {
-    const float v = div_rn(fmaxf(__uint_as_float(a), 1e-6f), 7.0f);
-    cs[c] = v;
-    coeff_scale[c] = v;
-    if (lo_out) lo_out[c] = bits[c] > 0 ? lo[c] : 0.f;
-    if (rng_out) rng_out[c] = bits[c] > 0 ? rng[c] : 0.f;
+    coeff_scale[c] = cs;
+    if (lo_out) lo_out[c] = b > 0 ? lv : 0.f;
+    if (rng_out) rng_out[c] = b > 0 ? rv : 0.f;
   }
 }
 
-// Byte i packs elements 2i and 2i + 1 of the row-major matrix; IT is 32-bit
-// when the element count allows, so the column of an element is a 32-bit mod.
+// Byte i packs elements 2i and 2i + 1 of the row-major matrix from their group
+// codes; a thread takes 8 elements (4 bytes).  IT is 32-bit when the element
+// count allows, so the column of an element is a 32-bit mod.
 template <typename IT>
-__global__ void k_int4_pack(const float* __restrict__ proj, IT total, int keep,
-                            const int32_t* __restrict__ bits, const float* __restrict__ lo,
-                            const float* __restrict__ rng, const float* __restrict__ cs,
-                            uint8_t* __restrict__ packed) {
+__global__ void k_int4_pack(const uint8_t* __restrict__ codes, IT total, int keep,
+                            const int8_t* __restrict__ qtab, uint8_t* __restrict__ packed) {
   const IT nbytes = (total + 1) / 2;
-  auto q4 = [&](IT e, int c) {
-    uint8_t code;
-    const float y = group_deq(proj[e], bits[c], lo[c], rng[c], &code);
-    const float q = fminf(fmaxf(rintf(div_rn(y, cs[c])), -7.f), 7.f);
-    return (int)q;
-  };
+  const IT nquads = (nbytes + 3) / 4;
   const IT stride = (IT)gridDim.x * blockDim.x;
-  for (IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x; i < nbytes; i += stride) {
-    const IT e0 = 2 * i;
-    const int c0 = (int)(e0 % (IT)keep);
-    const int q0 = q4(e0, c0);
-    const int q1 = e0 + 1 < total ? q4(e0 + 1, c0 + 1 == keep ? 0 : c0 + 1) : -8;  // pad nibble -> 0
-    packed[i] = (uint8_t)(((q0 + 8) & 15) | (((q1 + 8) & 15) << 4));
+  for (IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x; i < nquads; i += stride) {
+    const IT e0 = 8 * i;
+    int c = (int)(e0 % (IT)keep);
+    uint32_t word = 0;
+    if (e0 + 8 <= total && ((uintptr_t)(codes + e0) & 7) == 0) {
+      const uint2 cw = *(const uint2*)(codes + e0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t code = ((j < 4 ? cw.x : cw.y) >> (8 * (j & 3))) & 255u;
+        word |= (uint32_t)((qtab[c * 256 + code] + 8) & 15) << (4 * j);
+        c = c + 1 == keep ? 0 : c + 1;
+      }
+    } else {
+      for (int j = 0; j < 8; ++j) {
+        // an odd count pairs the last element with a zero value (nibble 8), as
+        // the reference appends a 0 before packing (triton_kernels.py:668-670)
+        const int q = e0 + j < total ? qtab[c * 256 + codes[e0 + j]] : 0;
+        word |= (uint32_t)((q + 8) & 15) << (4 * j);
+        c = c + 1 == keep ? 0 : c + 1;
+      }
+    }
+    if (4 * i + 4 <= nbytes && ((uintptr_t)(packed + 4 * i) & 3) == 0) {
+      *(uint32_t*)(packed + 4 * i) = word;
+    } else {
+      for (int j = 0; 4 * i + j < nbytes; ++j) packed[4 * i + j] = (uint8_t)(word >> (8 * j));
+    }
   }
 }
 
@@ -228,67 +251,95 @@ __global__ void k_fwht_small(const float* __restrict__ x, float* __restrict__ y,
 // ---------------------------------------------------------------------------
 // VQ front half: hadamard(fp32(v)) -> channel abs max -> normalized subvectors
 // ---------------------------------------------------------------------------
+// Workgroup (x, b) rotates rows [x R, (x + 1) R) of head b (R = ceil(seq /
+// gridDim.x), at most kVqSlots workgroups per head) and writes its channel
+// maxima of |x| as one partial; a fold kernel takes the max over the partials.
+constexpr int kVqSlots = 64;
+
 template <int E>
-__global__ void k_vq_rot(const uint16_t* __restrict__ v, int64_t bh, int64_t seq,
-                         int64_t bh_stride, float* __restrict__ xo,
-                         uint32_t* __restrict__ chmax) {
-  const int d = 64 * E;
+__global__ __launch_bounds__(256) void k_vq_rot(const uint16_t* __restrict__ v, int64_t bh,
+                                                int64_t seq, int64_t bh_stride,
+                                                float* __restrict__ xo,
+                                                float* __restrict__ part) {
+  constexpr int d = 64 * E;
+  constexpr int RS = 4;  // rows per step: all their loads are issued before any FWHT
+  __shared__ float red[4][d];
   const int l = (int)lane_id();
-  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  const int64_t rows = bh * seq;
-  // each wave owns a contiguous run of rows, so bh changes at most a few times
-  const int64_t rpw = (rows + nwaves - 1) / nwaves;
-  const int64_t r_begin = wave * rpw;
-  const int64_t r_end = r_begin + rpw < rows ? r_begin + rpw : rows;
-  // per-lane running channel max for the current bh (flushed when bh changes)
-  int64_t cur = -1;
-  float m[E];
-  for (int64_t r = r_begin; r < r_end; ++r) {
-    int64_t b = r / seq, t = r - b * seq;
-    if (b != cur) {
-      if (cur >= 0)
+  const int w = (int)(threadIdx.x >> 6);
+  const int64_t R = (seq + gridDim.x - 1) / gridDim.x;
+  const int64_t per_wave = (R + 3) / 4;
+  for (int64_t b = blockIdx.y; b < bh; b += gridDim.y) {
+    const int64_t t_blk = (int64_t)blockIdx.x * R;
+    const int64_t t_blk_end = t_blk + R < seq ? t_blk + R : seq;
+    const int64_t t0 = t_blk + w * per_wave;
+    const int64_t t1 = t0 + per_wave < t_blk_end ? t0 + per_wave : t_blk_end;
+    const uint16_t* src = v + b * bh_stride;
+    float* dst = xo + b * seq * d;
+    float m[E];
 #pragma unroll
-        for (int k = 0; k < E; ++k) atomicMax(&chmax[cur * d + l + 64 * k], __float_as_uint(m[k]));
-      cur = b;
+    for (int k = 0; k < E; ++k) m[k] = 0.f;
+    for (int64_t t = t0; t < t1; t += RS) {
+      float x[RS][E];
 #pragma unroll
-      for (int k = 0; k < E; ++k) m[k] = 0.f;
+      for (int q = 0; q < RS; ++q)
+#pragma unroll
+        for (int k = 0; k < E; ++k) x[q][k] = t + q < t1 ? h2f(src[(t + q) * d + l + 64 * k]) : 0.f;
+#pragma unroll
+      for (int q = 0; q < RS; ++q) {
+        if (t + q >= t1) break;  // wave-uniform
+        wave_fwht<E>(x[q], d);
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+          dst[(t + q) * d + l + 64 * k] = x[q][k];
+          m[k] = fmaxf(m[k], fabsf(x[q][k]));
+        }
+      }
     }
-    float x[E];
-    const uint16_t* src = v + b * bh_stride + t * d;
+    __syncthreads();  // red is reused across heads
 #pragma unroll
-    for (int k = 0; k < E; ++k) x[k] = h2f(src[l + 64 * k]);
-    wave_fwht<E>(x, d);
-#pragma unroll
-    for (int k = 0; k < E; ++k) {
-      xo[r * d + l + 64 * k] = x[k];
-      m[k] = fmaxf(m[k], fabsf(x[k]));
-    }
+    for (int k = 0; k < E; ++k) red[w][l + 64 * k] = m[k];
+    __syncthreads();
+    for (int c = threadIdx.x; c < d; c += 256)
+      part[(b * kVqSlots + blockIdx.x) * d + c] =
+          fmaxf(fmaxf(red[0][c], red[1][c]), fmaxf(red[2][c], red[3][c]));
   }
-  if (cur >= 0)
-#pragma unroll
-    for (int k = 0; k < E; ++k) atomicMax(&chmax[cur * d + l + 64 * k], __float_as_uint(m[k]));
 }
 
-// x /= channel max over each (b, channel) slab of seq rows x d (d a power of
-// two, at most 256), float4 at a time; the first workgroup of a slab writes
-// the channel scales
+// Channel scales of head blockIdx.x: max over the head's partials (thread
+// (c, j) takes slots j, j + 256 / d, ... of channel c), clamped to 1e-8; also
+// the fp32 / fp16 copies the caller asked for.
+__global__ __launch_bounds__(256) void k_vq_fold(const float* __restrict__ part, int64_t bh, int d,
+                                                 int nslots, float* __restrict__ ch, float* ch_f32,
+                                                 uint16_t* ch_f16) {
+  __shared__ float red[256];
+  const int tid = threadIdx.x, c = tid & (d - 1), j0 = tid / d, nj = 256 / d;
+  for (int64_t b = blockIdx.x; b < bh; b += gridDim.x) {
+    float m = 0.f;
+#pragma unroll 8
+    for (int x = j0; x < nslots; x += nj) m = fmaxf(m, part[(b * kVqSlots + x) * d + c]);
+    __syncthreads();
+    red[tid] = m;
+    __syncthreads();
+    if (tid < d) {
+      for (int j = 1; j < nj; ++j) m = fmaxf(m, red[j * d + tid]);
+      const float v = fmaxf(m, 1e-8f);
+      ch[b * d + tid] = v;
+      if (ch_f32) ch_f32[b * d + tid] = v;
+      if (ch_f16) ch_f16[b * d + tid] = f2h(v);
+    }
+  }
+}
+
+// x /= channel scale over each (b, channel) slab of seq rows x d (d a power
+// of two, at most 256), float4 at a time
 __global__ __launch_bounds__(256) void k_vq_norm(float* __restrict__ xo, int64_t bh, int64_t seq,
-                                                 int d, const uint32_t* __restrict__ chmax,
-                                                 float* ch_f32, uint16_t* ch_f16) {
+                                                 int d, const float* __restrict__ ch) {
   __shared__ float chs[256];
   const int tid = threadIdx.x;
   const int64_t n4 = seq * d / 4;
   for (int64_t b = blockIdx.y; b < bh; b += gridDim.y) {
     __syncthreads();
-    for (int c = tid; c < d; c += 256) {
-      const float ch = fmaxf(__uint_as_float(chmax[b * d + c]), 1e-8f);
-      chs[c] = ch;
-      if (blockIdx.x == 0) {
-        if (ch_f32) ch_f32[b * d + c] = ch;
-        if (ch_f16) ch_f16[b * d + c] = f2h(ch);
-      }
-    }
+    for (int c = tid; c < d; c += 256) chs[c] = ch[b * d + c];
     __syncthreads();
     float4* slab = (float4*)(xo + b * seq * d);
     for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < n4; i += (int64_t)gridDim.x * 256) {
@@ -710,11 +761,6 @@ __global__ __launch_bounds__(256) void k_km_sum(const float* __restrict__ x, con
 
 __global__ void k_km_zero(uint32_t* p) { *p = 0u; }
 
-__global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
-}
-
 // ---------------------------------------------------------------------------
 // Per-token 8-bit Lloyd-Max stream quantizer (cache.py:207-215, streaming.py:59-72)
 // one wave per row, E = hd/64 elements per lane.
@@ -858,9 +904,11 @@ using namespace shard;
 extern "C" {
 
 size_t shard_int4_quant_pack_workspace(int64_t n_rows, int32_t keep) {
-  (void)n_rows;
-  // pmin, pmax, pamax partials (kI4Blocks x keep) + lo, rng, cs (keep)
-  return (size_t)(3 * kI4Blocks + 3) * (keep > 0 ? keep : 0) * sizeof(uint32_t);
+  if (n_rows <= 0 || keep <= 0) return 0;
+  // pmin, pmax, pamax partials (kI4Blocks x keep), lo, rng (keep), the int4
+  // table (keep x 256 bytes) and the group codes (n_rows x keep bytes)
+  return (size_t)(3 * kI4Blocks + 2) * keep * sizeof(uint32_t) + (size_t)keep * 256 +
+         (size_t)n_rows * keep;
 }
 
 int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const int32_t* bits,
@@ -877,7 +925,8 @@ int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const
   uint32_t* pamax = pmax + (size_t)kI4Blocks * keep;
   float* clo = (float*)(pamax + (size_t)kI4Blocks * keep);
   float* crng = clo + keep;
-  float* ccs = crng + keep;
+  int8_t* qtab = (int8_t*)(crng + keep);
+  uint8_t* ccodes = codes ? codes : (uint8_t*)(qtab + (size_t)keep * 256);
   const int tpb = ((keep + 63) / 64) * 64;
   const int rg = 1024 / tpb < 4 ? 1024 / tpb : 4;
   const int64_t nblk = n_rows / rg < kI4Blocks ? (n_rows + rg - 1) / rg : kI4Blocks;
@@ -887,18 +936,18 @@ int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const
   hipLaunchKernelGGL(k_int4_minmax, cgrid, cblock, 0, s, proj, n_rows, keep, rpb, pmin, pmax);
   hipLaunchKernelGGL(k_int4_fold_minmax, fgrid, fblock, 0, s, pmin, pmax, (int)nblk, keep, clo, crng);
   hipLaunchKernelGGL(k_int4_absmax, cgrid, cblock, 0, s, proj, n_rows, keep, rpb, bits, clo, crng,
-                     pamax, codes);
+                     pamax, ccodes);
   hipLaunchKernelGGL(k_int4_fold_absmax, fgrid, fblock, 0, s, pamax, (int)nblk, keep, bits, clo,
-                     crng, ccs, coeff_scale, lo, rng);
+                     crng, qtab, coeff_scale, lo, rng);
   const int64_t total = n_rows * keep;
-  const int64_t nbytes = (total + 1) / 2;
-  const dim3 pgrid(grid_cap((nbytes + 255) / 256, 8192));
+  const int64_t nquads = ((total + 1) / 2 + 3) / 4;
+  const dim3 pgrid(grid_cap((nquads + 255) / 256, 8192));
   if (total < (1ll << 31))
-    hipLaunchKernelGGL(k_int4_pack<uint32_t>, pgrid, dim3(256), 0, s, proj, (uint32_t)total, keep,
-                       bits, clo, crng, ccs, packed);
+    hipLaunchKernelGGL(k_int4_pack<uint32_t>, pgrid, dim3(256), 0, s, ccodes, (uint32_t)total, keep,
+                       qtab, packed);
   else
-    hipLaunchKernelGGL(k_int4_pack<uint64_t>, pgrid, dim3(256), 0, s, proj, (uint64_t)total, keep,
-                       bits, clo, crng, ccs, packed);
+    hipLaunchKernelGGL(k_int4_pack<uint64_t>, pgrid, dim3(256), 0, s, ccodes, (uint64_t)total, keep,
+                       qtab, packed);
   SHARD_LAUNCH_CHECK("shard_int4_quant_pack");
   return SHARD_OK;
 }
@@ -928,7 +977,8 @@ int shard_fwht(const float* x, float* y, int64_t rows, int32_t d, void* stream) 
 }
 
 size_t shard_vq_prepare_workspace(int64_t bh, int32_t hd) {
-  return (size_t)(bh > 0 ? bh : 0) * (hd > 0 ? hd : 0) * sizeof(uint32_t);
+  // kVqSlots channel-max partials per head, then the folded channel scales
+  return (size_t)(kVqSlots + 1) * (bh > 0 ? bh : 0) * (hd > 0 ? hd : 0) * sizeof(float);
 }
 
 int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int64_t v_bh_stride,
@@ -938,21 +988,22 @@ int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int
   if (hd != 64 && hd != 128 && hd != 256) return SHARD_ERR_SHAPE;
   if (!workspace || workspace_bytes < shard_vq_prepare_workspace(bh, hd)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
-  uint32_t* chmax = (uint32_t*)workspace;
-  const int64_t nch = bh * hd;
-  hipLaunchKernelGGL(k_fill_u32, dim3(grid_cap((nch + 255) / 256, 4096)), dim3(256), 0, s, chmax,
-                     nch, 0u);
-  int64_t rows = bh * seq;
-  int blocks = grid_cap((rows + 63) / 64, 2048);  // 16 rows per wave or more
+  float* part = (float*)workspace;
+  float* ch = part + (size_t)kVqSlots * bh * hd;
+  // workgroups per head: up to kVqSlots, at least 16 rows per wave
+  const int64_t nx = (seq + 63) / 64 < kVqSlots ? (seq + 63) / 64 : kVqSlots;
+  const dim3 rgrid((unsigned)nx, (unsigned)(bh < 65535 ? bh : 65535));
   switch (hd) {
-    case 64: hipLaunchKernelGGL(k_vq_rot<1>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
-    case 128: hipLaunchKernelGGL(k_vq_rot<2>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
-    default: hipLaunchKernelGGL(k_vq_rot<4>, dim3(blocks), dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, chmax); break;
+    case 64: hipLaunchKernelGGL(k_vq_rot<1>, rgrid, dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, part); break;
+    case 128: hipLaunchKernelGGL(k_vq_rot<2>, rgrid, dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, part); break;
+    default: hipLaunchKernelGGL(k_vq_rot<4>, rgrid, dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, part); break;
   }
+  hipLaunchKernelGGL(k_vq_fold, dim3((unsigned)(bh < 65535 ? bh : 65535)), dim3(256), 0, s, part,
+                     bh, hd, (int)nx, ch, ch_f32, ch_f16);
   // about four float4 per thread, all heads in flight at once
   const int64_t per_slab = (seq * hd / 4 + 1023) / 1024;
   const dim3 ngrid((unsigned)(per_slab < 1024 ? per_slab : 1024), (unsigned)(bh < 65535 ? bh : 65535));
-  hipLaunchKernelGGL(k_vq_norm, ngrid, dim3(256), 0, s, x_out, bh, seq, hd, chmax, ch_f32, ch_f16);
+  hipLaunchKernelGGL(k_vq_norm, ngrid, dim3(256), 0, s, x_out, bh, seq, hd, ch);
   SHARD_LAUNCH_CHECK("shard_vq_prepare");
   return SHARD_OK;
 }
