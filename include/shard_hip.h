@@ -58,7 +58,8 @@ int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_t lda,
  * fl(pos * inv_freq[i]) (rope.py:13-24), subtracts mean[n_kv*hd] (fp32) and
  * writes the fp16 row-major matrix out[(b*n_comp + t), n_kv*hd] for tokens
  * t in [0, n_comp).  Replaces undo_rope + permute/reshape + (flat - mean) of
- * cache.py:370-376 (as the fp16 GEMM operand). */
+ * cache.py:370-376 (as the fp16 GEMM operand).  hd is a multiple of 8 and at
+ * most 512; k and out are 8-byte aligned (rows move as 4-half vectors). */
 int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
                     int32_t hd, int32_t start, int32_t n_comp,
                     const float* inv_freq, const float* mean, uint16_t* out,
@@ -97,7 +98,9 @@ int shard_fwht(const float* x, float* y, int64_t rows, int32_t d, void* stream);
 /* V encoder front half (vq_encode, cache.py:41-46 after hadamard, cache.py:402):
  * v fp16 (bh, seq, hd) -> v_rot = hadamard(fp32(v)); ch = max(max_t |v_rot|, 1e-8)
  * per (bh, channel); x = v_rot / ch written as fp32 (bh*seq*hd/g, g) subvectors;
- * ch also written as fp16 (bh, hd).  Uses workspace for the fp32 channel max. */
+ * ch also written as fp16 (bh, hd).  Uses workspace for the fp32 channel max.
+ * v must be aligned to hd/32 bytes with v_bh_stride a multiple of hd/64, and
+ * x_out to hd/16 bytes (rows move as hd/64-element vectors). */
 size_t shard_vq_prepare_workspace(int64_t bh, int32_t hd);
 int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
                      int64_t v_bh_stride, float* x_out, float* ch_f32,

@@ -195,6 +195,37 @@ __device__ __forceinline__ void wave_fwht(float (&x)[E], int d) {
   for (int k = 0; k < E; ++k) x[k] = div_rn(x[k], s);
 }
 
+// The same transform with a contiguous layout: lane l holds elements
+// E l .. E l + E - 1 (so a row loads and stores as E-element vectors).  Stages
+// still run in increasing stride h and pair the same elements: strides h < E
+// inside the lane, then strides h >= E across lanes l and l ^ (h / E).
+template <int E, bool SCALE = true>
+__device__ __forceinline__ void wave_fwht_contig(float (&x)[E], int d) {
+  const int l = (int)lane_id();
+#pragma unroll
+  for (int h = 1; h < E; h <<= 1) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      if ((j & h) == 0) {
+        const float a = x[j], b = x[j | h];
+        x[j] = add_rn(a, b);
+        x[j | h] = sub_rn(a, b);
+      }
+    }
+  }
+  fwht_lane_stage<1>(x, l);
+  fwht_lane_stage<2>(x, l);
+  fwht_lane_stage<4>(x, l);
+  fwht_lane_stage<8>(x, l);
+  fwht_lane_stage<16>(x, l);
+  fwht_lane_stage<32>(x, l);
+  if constexpr (SCALE) {  // SCALE = false leaves the final division to the caller
+    const float s = (float)sqrt((double)d);
+#pragma unroll
+    for (int k = 0; k < E; ++k) x[k] = div_rn(x[k], s);
+  }
+}
+
 inline int grid_cap(int64_t blocks, int cap = 65535 * 8) {
   return (int)(blocks < cap ? blocks : cap);
 }

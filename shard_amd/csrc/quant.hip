@@ -252,15 +252,21 @@ __global__ void k_fwht_small(const float* __restrict__ x, float* __restrict__ y,
 // VQ front half: hadamard(fp32(v)) -> channel abs max -> normalized subvectors
 // ---------------------------------------------------------------------------
 // Workgroup (x, b) rotates rows [x R, (x + 1) R) of head b (R = ceil(seq /
-// gridDim.x), at most kVqSlots workgroups per head) and writes its channel
-// maxima of |x| as one partial; a fold kernel takes the max over the partials.
+// gridDim.x), at most kVqSlots workgroups per head).  Two passes over V:
+//   NORM = false: FWHT only, writing the workgroup's channel maxima of |x|
+//                 as one partial (a fold kernel takes the max over partials);
+//   NORM = true:  FWHT again (the same values) divided by the folded channel
+//                 scale, stored as x.
+// Recomputing the FWHT moves less data than storing x and normalizing it in
+// place (2 B read per element instead of 4 B written + 4 B read + 4 B written).
 constexpr int kVqSlots = 64;
 
-template <int E>
+template <int E, bool NORM>
 __global__ __launch_bounds__(256) void k_vq_rot(const uint16_t* __restrict__ v, int64_t bh,
                                                 int64_t seq, int64_t bh_stride,
-                                                float* __restrict__ xo,
-                                                float* __restrict__ part) {
+                                                float* __restrict__ part,
+                                                const float* __restrict__ ch,
+                                                float* __restrict__ xo) {
   constexpr int d = 64 * E;
   constexpr int RS = 4;  // rows per step: all their loads are issued before any FWHT
   __shared__ float red[4][d];
@@ -275,33 +281,64 @@ __global__ __launch_bounds__(256) void k_vq_rot(const uint16_t* __restrict__ v, 
     const int64_t t1 = t0 + per_wave < t_blk_end ? t0 + per_wave : t_blk_end;
     const uint16_t* src = v + b * bh_stride;
     float* dst = xo + b * seq * d;
-    float m[E];
+    // lane l holds channels E l .. E l + E - 1 (contiguous-layout FWHT)
+    float m[E], cs[E];
 #pragma unroll
-    for (int k = 0; k < E; ++k) m[k] = 0.f;
+    for (int k = 0; k < E; ++k) {
+      m[k] = 0.f;
+      if constexpr (NORM) cs[k] = ch[b * d + E * l + k];
+    }
     for (int64_t t = t0; t < t1; t += RS) {
       float x[RS][E];
 #pragma unroll
-      for (int q = 0; q < RS; ++q)
-#pragma unroll
-        for (int k = 0; k < E; ++k) x[q][k] = t + q < t1 ? h2f(src[(t + q) * d + l + 64 * k]) : 0.f;
+      for (int q = 0; q < RS; ++q) {
+        const uint16_t* p = src + (t + q) * d + E * l;
+        if constexpr (E == 1) {
+          x[q][0] = t + q < t1 ? h2f(p[0]) : 0.f;
+        } else if constexpr (E == 2) {
+          const uint32_t u = t + q < t1 ? *(const uint32_t*)p : 0u;
+          x[q][0] = h2f((uint16_t)u);
+          x[q][1] = h2f((uint16_t)(u >> 16));
+        } else {
+          const uint2 u = t + q < t1 ? *(const uint2*)p : make_uint2(0u, 0u);
+          x[q][0] = h2f((uint16_t)u.x);
+          x[q][1] = h2f((uint16_t)(u.x >> 16));
+          x[q][2] = h2f((uint16_t)u.y);
+          x[q][3] = h2f((uint16_t)(u.y >> 16));
+        }
+      }
 #pragma unroll
       for (int q = 0; q < RS; ++q) {
         if (t + q >= t1) break;  // wave-uniform
-        wave_fwht<E>(x[q], d);
+        // the statistics pass keeps max |y| of the unscaled transform: dividing
+        // by sqrt(d) rounds monotonically, so max |RN(y / s)| = RN(max |y| / s)
+        wave_fwht_contig<E, NORM>(x[q], d);
+        if constexpr (NORM) {
+          float* o = dst + (t + q) * d + E * l;
+          if constexpr (E == 1) {
+            o[0] = div_rn(x[q][0], cs[0]);
+          } else if constexpr (E == 2) {
+            *(float2*)o = make_float2(div_rn(x[q][0], cs[0]), div_rn(x[q][1], cs[1]));
+          } else {
+            *(float4*)o = make_float4(div_rn(x[q][0], cs[0]), div_rn(x[q][1], cs[1]),
+                                      div_rn(x[q][2], cs[2]), div_rn(x[q][3], cs[3]));
+          }
+        } else {
 #pragma unroll
-        for (int k = 0; k < E; ++k) {
-          dst[(t + q) * d + l + 64 * k] = x[q][k];
-          m[k] = fmaxf(m[k], fabsf(x[q][k]));
+          for (int k = 0; k < E; ++k) m[k] = fmaxf(m[k], fabsf(x[q][k]));
         }
       }
     }
-    __syncthreads();  // red is reused across heads
+    if constexpr (!NORM) {
+      __syncthreads();  // red is reused across heads
 #pragma unroll
-    for (int k = 0; k < E; ++k) red[w][l + 64 * k] = m[k];
-    __syncthreads();
-    for (int c = threadIdx.x; c < d; c += 256)
-      part[(b * kVqSlots + blockIdx.x) * d + c] =
-          fmaxf(fmaxf(red[0][c], red[1][c]), fmaxf(red[2][c], red[3][c]));
+      for (int k = 0; k < E; ++k) red[w][E * l + k] = m[k];
+      __syncthreads();
+      const float sd = (float)sqrt((double)d);
+      for (int c = threadIdx.x; c < d; c += 256)
+        part[(b * kVqSlots + blockIdx.x) * d + c] =
+            div_rn(fmaxf(fmaxf(red[0][c], red[1][c]), fmaxf(red[2][c], red[3][c])), sd);
+    }
   }
 }
 
@@ -326,30 +363,6 @@ __global__ __launch_bounds__(256) void k_vq_fold(const float* __restrict__ part,
       ch[b * d + tid] = v;
       if (ch_f32) ch_f32[b * d + tid] = v;
       if (ch_f16) ch_f16[b * d + tid] = f2h(v);
-    }
-  }
-}
-
-// x /= channel scale over each (b, channel) slab of seq rows x d (d a power
-// of two, at most 256), float4 at a time
-__global__ __launch_bounds__(256) void k_vq_norm(float* __restrict__ xo, int64_t bh, int64_t seq,
-                                                 int d, const float* __restrict__ ch) {
-  __shared__ float chs[256];
-  const int tid = threadIdx.x;
-  const int64_t n4 = seq * d / 4;
-  for (int64_t b = blockIdx.y; b < bh; b += gridDim.y) {
-    __syncthreads();
-    for (int c = tid; c < d; c += 256) chs[c] = ch[b * d + c];
-    __syncthreads();
-    float4* slab = (float4*)(xo + b * seq * d);
-    for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < n4; i += (int64_t)gridDim.x * 256) {
-      const int c = (int)((i * 4) & (d - 1));
-      float4 v = slab[i];
-      v.x = div_rn(v.x, chs[c]);
-      v.y = div_rn(v.y, chs[c + 1]);
-      v.z = div_rn(v.z, chs[c + 2]);
-      v.w = div_rn(v.w, chs[c + 3]);
-      slab[i] = v;
     }
   }
 }
@@ -865,8 +878,9 @@ __global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
 // Prefill K preparation: undo RoPE (fp32), subtract mean, fp16 GEMM operand.
 // ---------------------------------------------------------------------------
 // One workgroup per token t of the window: the token's hd/2 RoPE phases are
-// computed once (shared by every batch row and kv head), then thread (i, y)
-// undoes pair i of the (b, g) rows y, y + blockDim.y, ...
+// computed once (shared by every batch row and kv head), then thread (i4, y)
+// undoes pairs 4 i4 .. 4 i4 + 3 of the (b, g) rows y, y + blockDim.y, ...
+// (8-byte loads and stores; hd a multiple of 8).
 __global__ __launch_bounds__(256) void k_k_prepare(const uint16_t* __restrict__ k, int batch,
                                                    int n_kv, int seq, int hd, int start, int n_comp,
                                                    const float* __restrict__ inv_freq,
@@ -882,19 +896,35 @@ __global__ __launch_bounds__(256) void k_k_prepare(const uint16_t* __restrict__ 
     ph[i] = make_float2(cs, sn);
   }
   __syncthreads();
-  const int i = threadIdx.x;  // blockDim.x == hd / 2
-  const float cs = ph[i].x, sn = ph[i].y;
+  const int i0 = 4 * threadIdx.x;  // blockDim.x == hd / 8
+  float2 p[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = ph[i0 + j];
   for (int bg = threadIdx.y; bg < batch * n_kv; bg += blockDim.y) {
     const int b = bg / n_kv, g = bg - b * n_kv;
     const uint16_t* src = k + (((int64_t)b * n_kv + g) * seq + pos) * hd;
-    const float lo = h2f(src[i]), hi = h2f(src[i + hd2]);
-    // undo_rope: k*cos - rotate_half(k)*sin, rotate_half = [-hi, lo]
-    const float ulo = add_rn(mul_rn(lo, cs), mul_rn(hi, sn));
-    const float uhi = sub_rn(mul_rn(hi, cs), mul_rn(lo, sn));
+    const uint2 lo4 = *(const uint2*)(src + i0), hi4 = *(const uint2*)(src + hd2 + i0);
+    const uint16_t lo[4] = {(uint16_t)lo4.x, (uint16_t)(lo4.x >> 16), (uint16_t)lo4.y,
+                            (uint16_t)(lo4.y >> 16)};
+    const uint16_t hi[4] = {(uint16_t)hi4.x, (uint16_t)(hi4.x >> 16), (uint16_t)hi4.y,
+                            (uint16_t)(hi4.y >> 16)};
+    const float* mn = mean + g * hd;
+    uint16_t olo[4], ohi[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float l = h2f(lo[j]), h = h2f(hi[j]);
+      // undo_rope: k*cos - rotate_half(k)*sin, rotate_half = [-hi, lo]
+      const float ulo = add_rn(mul_rn(l, p[j].x), mul_rn(h, p[j].y));
+      const float uhi = sub_rn(mul_rn(h, p[j].x), mul_rn(l, p[j].y));
+      olo[j] = f2h(sub_rn(ulo, mn[i0 + j]));
+      ohi[j] = f2h(sub_rn(uhi, mn[hd2 + i0 + j]));
+    }
     uint16_t* o = out + ((int64_t)b * n_comp + t) * D + g * hd;
-    o[i] = f2h(sub_rn(ulo, mean[g * hd + i]));
-    o[i + hd2] = f2h(sub_rn(uhi, mean[g * hd + i + hd2]));
+    *(uint2*)(o + i0) = make_uint2(olo[0] | ((uint32_t)olo[1] << 16), olo[2] | ((uint32_t)olo[3] << 16));
+    *(uint2*)(o + hd2 + i0) =
+        make_uint2(ohi[0] | ((uint32_t)ohi[1] << 16), ohi[2] | ((uint32_t)ohi[3] << 16));
   }
+}
 }
 
 }  // namespace shard
@@ -986,24 +1016,30 @@ int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int
                      size_t workspace_bytes, void* stream) {
   if (!v || !x_out || bh <= 0 || seq <= 0) return SHARD_ERR_ARG;
   if (hd != 64 && hd != 128 && hd != 256) return SHARD_ERR_SHAPE;
+  // rows load as hd/64-half vectors and store as hd/64-float vectors
+  const int E = hd / 64;
+  if (((uintptr_t)v & (2 * E - 1)) || (v_bh_stride % E) || ((uintptr_t)x_out & (4 * E - 1)))
+    return SHARD_ERR_SHAPE;
   if (!workspace || workspace_bytes < shard_vq_prepare_workspace(bh, hd)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   float* part = (float*)workspace;
   float* ch = part + (size_t)kVqSlots * bh * hd;
   // workgroups per head: up to kVqSlots, at least 16 rows per wave
   const int64_t nx = (seq + 63) / 64 < kVqSlots ? (seq + 63) / 64 : kVqSlots;
-  const dim3 rgrid((unsigned)nx, (unsigned)(bh < 65535 ? bh : 65535));
+  const dim3 rgrid((unsigned)nx, (unsigned)(bh < 65535 ? bh : 65535)), rblock(256);
+  const dim3 fgrid((unsigned)(bh < 65535 ? bh : 65535)), fblock(256);
+#define SHARD_VQ_PASSES(E)                                                                      \
+  hipLaunchKernelGGL((k_vq_rot<E, false>), rgrid, rblock, 0, s, v, bh, seq, v_bh_stride, part,  \
+                     (const float*)nullptr, (float*)nullptr);                                  \
+  hipLaunchKernelGGL(k_vq_fold, fgrid, fblock, 0, s, part, bh, hd, (int)nx, ch, ch_f32, ch_f16); \
+  hipLaunchKernelGGL((k_vq_rot<E, true>), rgrid, rblock, 0, s, v, bh, seq, v_bh_stride,         \
+                     (float*)nullptr, (const float*)ch, x_out)
   switch (hd) {
-    case 64: hipLaunchKernelGGL(k_vq_rot<1>, rgrid, dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, part); break;
-    case 128: hipLaunchKernelGGL(k_vq_rot<2>, rgrid, dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, part); break;
-    default: hipLaunchKernelGGL(k_vq_rot<4>, rgrid, dim3(256), 0, s, v, bh, seq, v_bh_stride, x_out, part); break;
+    case 64: SHARD_VQ_PASSES(1); break;
+    case 128: SHARD_VQ_PASSES(2); break;
+    default: SHARD_VQ_PASSES(4); break;
   }
-  hipLaunchKernelGGL(k_vq_fold, dim3((unsigned)(bh < 65535 ? bh : 65535)), dim3(256), 0, s, part,
-                     bh, hd, (int)nx, ch, ch_f32, ch_f16);
-  // about four float4 per thread, all heads in flight at once
-  const int64_t per_slab = (seq * hd / 4 + 1023) / 1024;
-  const dim3 ngrid((unsigned)(per_slab < 1024 ? per_slab : 1024), (unsigned)(bh < 65535 ? bh : 65535));
-  hipLaunchKernelGGL(k_vq_norm, ngrid, dim3(256), 0, s, x_out, bh, seq, hd, ch);
+#undef SHARD_VQ_PASSES
   SHARD_LAUNCH_CHECK("shard_vq_prepare");
   return SHARD_OK;
 }
@@ -1108,10 +1144,11 @@ int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
                     int32_t start, int32_t n_comp, const float* inv_freq, const float* mean,
                     uint16_t* out, void* stream) {
   if (!k || !inv_freq || !mean || !out || batch <= 0 || n_kv <= 0 || n_comp <= 0) return SHARD_ERR_ARG;
-  if ((hd & 1) || hd > 512 || start < 0 || start + n_comp > seq) return SHARD_ERR_SHAPE;
+  if ((hd & 7) || hd > 512 || start < 0 || start + n_comp > seq) return SHARD_ERR_SHAPE;
+  if (((uintptr_t)k & 7) || ((uintptr_t)out & 7)) return SHARD_ERR_SHAPE;  // 8-byte vectors
   hipStream_t s = (hipStream_t)stream;
-  const int hd2 = hd / 2;
-  const dim3 block(hd2, hd2 >= 256 ? 1 : 256 / hd2);
+  const int hd8 = hd / 8;
+  const dim3 block(hd8, 256 / hd8 < 1 ? 1 : 256 / hd8);
   hipLaunchKernelGGL(k_k_prepare, dim3((unsigned)n_comp), block, 0, s, k, batch, n_kv, seq, hd,
                      start, n_comp, inv_freq, mean, out);
   SHARD_LAUNCH_CHECK("shard_k_prepare");
