@@ -925,7 +925,6 @@ __global__ __launch_bounds__(256) void k_k_prepare(const uint16_t* __restrict__ 
         make_uint2(ohi[0] | ((uint32_t)ohi[1] << 16), ohi[2] | ((uint32_t)ohi[3] << 16));
   }
 }
-}
 
 }  // namespace shard
 
