@@ -724,7 +724,7 @@ __device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
   x1 *= s;
 }
 
-constexpr int kCombPF = 16;  // partials per wave held in registers
+constexpr int kCombPF = 24;  // partials per wave held in registers: 4 waves cover 96 rows in one round trip
 
 // One workgroup per (query head, batch row); wave w merges a quarter of the
 // partial rows.  Rows [0, n_splits) hold VQ values in the rotated basis (summed,
