@@ -228,6 +228,10 @@ typedef struct shard_decode_args {
   uint16_t* out;
   int32_t n_splits; /* 0 = choose automatically */
   int32_t _pad1;
+  /* nullable device int64: when set, the kernel reads pos_q from it (the
+   * reference's cache_position[-1], attention.py:383) and `pos_q` is ignored,
+   * so the caller needs no host read-back of the position */
+  const int64_t* pos_q_dev;
 } shard_decode_args;
 
 /* Per-layer constant operands of shard_decode_attn, computed once after a

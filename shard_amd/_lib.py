@@ -42,6 +42,7 @@ class DecodeArgs(ctypes.Structure):
         ("s_k", c_void_p), ("s_v", c_void_p), ("n_stream", c_int32), ("_pad0", c_int32),
         ("mask", c_void_p), ("mask_stride", c_int64),
         ("out", c_void_p), ("n_splits", c_int32), ("_pad1", c_int32),
+        ("pos_q_dev", c_void_p),
     ]
 
 

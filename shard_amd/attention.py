@@ -31,7 +31,8 @@ def _workspace(device, nbytes):
 
 def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
     """q_rope (B, n_q, 1, hd) post-RoPE; returns (B, n_q, 1, hd) in q's dtype,
-    or None when the layer is not compressed (attention.py:270-274)."""
+    or None when the layer is not compressed (attention.py:270-274).  pos_q is
+    an int or a device int64 tensor whose last element is the position."""
     gc = getattr(layer, "_gpu_compressed", None)
     if gc is None:
         return None
@@ -108,8 +109,15 @@ def enable_llama_fused_attention(model=None):
                                    {"sin": sin, "cos": cos, "cache_position": cache_position})
         finally:
             past_key_values._fused_decode_update = False
-        pos_q = int(cache_position[-1].item()) if cache_position is not None \
-            else past_key_values.get_seq_length() - 1
+        # the reference reads cache_position[-1].item() (attention.py:383); a
+        # device int64 position goes to the kernel as a pointer instead, so the
+        # step needs no host read-back
+        if cache_position is None:
+            pos_q = past_key_values.get_seq_length() - 1
+        elif cache_position.is_cuda and cache_position.dtype == torch.int64:
+            pos_q = cache_position.reshape(-1)[-1:]
+        else:
+            pos_q = int(cache_position.reshape(-1)[-1].item())
         out = None
         if getattr(past_key_values, "_full_fused", False):
             past_key_values._full_fused_attempts = getattr(past_key_values, "_full_fused_attempts", 0) + 1

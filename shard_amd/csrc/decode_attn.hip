@@ -58,6 +58,7 @@ struct ExtraSegs {
 
 struct SplitParams {
   int32_t B, H, G, rank, n_comp, cstart, pos_q, n_splits;
+  const int64_t* pos_q_dev;  // when set, pos_q is read from device memory
   // Token ranges: splits [0, n_first) cover `chunk` tokens each, the others
   // `chunk2` (two_class: the first and the second workgroup of each CU).
   int32_t chunk, chunk2, n_first, two_class;
@@ -431,6 +432,7 @@ void k_decode_split(const SplitParams p) {
 
   // ---- loads that feed LDS and the q operand go out first: the first barrier
   // waits for these only, not for the tile and basis loads behind them.
+  const int pos_q = p.pos_q_dev ? (int)p.pos_q_dev[0] : p.pos_q;
   const uint2 cb_v = tid < 256 ? *(const uint2*)(p.vcb + 4 * tid) : make_uint2(0u, 0u);
   const float th_v = tid < 192 ? p.inv_freq[tid & 63] : 0.f;
   uint2 q_lo[2], q_hi[2];
@@ -487,8 +489,8 @@ void k_decode_split(const SplitParams p) {
   if (tid < 256) cbl[tid] = cb_v;
   if (tid < 192) {
     const int k = tid >> 6;  // 0: q position, 1: chunk start delta, 2: iteration step
-    const float x = k == 0 ? (float)p.pos_q * th_v
-                  : k == 1 ? (float)(p.cstart + t_begin - p.pos_q) * th_v
+    const float x = k == 0 ? (float)pos_q * th_v
+                  : k == 1 ? (float)(p.cstart + t_begin - pos_q) * th_v
                            : (float)TT * th_v;
     float sn, cn;
     sincosf(x, &sn, &cn);
@@ -909,6 +911,7 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   SplitParams sp;
   sp.B = a->batch; sp.H = a->n_q_heads; sp.G = a->n_kv_heads; sp.rank = a->rank;
   sp.n_comp = a->n_comp; sp.cstart = a->compress_start; sp.pos_q = a->pos_q;
+  sp.pos_q_dev = a->pos_q_dev;
   sp.n_splits = ns;
   // Compressed tiles per split, in whole 32-token tiles.  The last split of
   // each head also runs the extra tokens (an extra token costs about half a

@@ -295,7 +295,8 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
 
     q (B, H, D) fp16 (post-RoPE); ``fmt`` is the layer's device format dict
     (see cache.CompressedLayerFormat); decode_kv = (dec_k, dec_v) fp16
-    (B, G, S, D) or None."""
+    (B, G, S, D) or None.  ``pos_q`` is an int, or an int64 tensor on q's
+    device whose last element the kernel reads (no host read-back)."""
     _require_gpu(q)
     B, H, D = q.shape
     if tuple(fmt["v_centroids_f16"].shape) != (256, 4):
@@ -306,7 +307,14 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
     a = DecodeArgs()
     a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim = B, H, fmt["n_kv"], D
     a.rank, a.n_comp = fmt["rank_pad"], fmt["n_compress"]
-    a.compress_start, a.pos_q = fmt["compress_start"], int(pos_q)
+    if isinstance(pos_q, torch.Tensor):
+        if pos_q.dtype != torch.int64 or pos_q.device != q.device or pos_q.numel() < 1:
+            raise TypeError("a device pos_q must be a non-empty int64 tensor on q's device")
+        pos_t = pos_q.reshape(-1)[-1:]
+        a.compress_start, a.pos_q, a.pos_q_dev = fmt["compress_start"], 0, pos_t.data_ptr()
+        keep.append(pos_t)
+    else:
+        a.compress_start, a.pos_q = fmt["compress_start"], int(pos_q)
     inv_freq = fmt["inv_freq_dev"] if inv_freq is None else inv_freq
     for name, t in (("q", q), ("inv_freq", inv_freq), ("k_coeffs", fmt["k_coeffs_pad"]),
                     ("k_coeff_scale", fmt["k_coeff_scale_pad"]), ("k_basis", fmt["k_basis_pad"]),

@@ -149,3 +149,20 @@ def test_kv_reconstruct(cuda):
     diff = (kg - kw).abs()
     assert float(diff.max()) <= 2 * 2.0 ** -10
     assert float((diff > 0).float().mean()) < 0.02
+
+
+def test_decode_device_position_matches_host_position(cuda):
+    """pos_q read by the kernel from a device int64 (the patched forward passes
+    cache_position[-1:] instead of the reference's .item(), attention.py:383)
+    gives the same bits as the host integer, also with a position that is not
+    the last cached token."""
+    gc, inv = random_layer(B=2, n_comp=700, n_stream=4, seed=11)
+    q = torch.randn(2, 32, 1, 128, generator=torch.Generator().manual_seed(5)).half()
+    for pos_q in (4 + 700 + 64 + 4 - 1, 5000):
+        host = _run(cuda, gc, inv, q, pos_q)
+        dev = _run(cuda, gc, inv, q, torch.tensor([pos_q - 3, pos_q], dtype=torch.int64, device=cuda))
+        print(f"pos_q={pos_q} max diff={np.abs(host - dev).max():.3e}", flush=True)
+        assert np.array_equal(host, dev)
+        want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+        err, cos = compare(dev, want)
+        assert err <= TOL_ABS and cos >= TOL_COS
