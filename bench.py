@@ -72,7 +72,8 @@ def build_layer(T, dev, seed=0, n_stream=0, with_layer=False):
     return fmt, k, v
 
 
-def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, graph_len=100):
+def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, graph_len=100,
+                kernel=0):
     """Per-call time of shard_decode_attn, rotating over n_copies of the layer.
 
     The calls are captured in a HIP graph (graph_len calls per graph, each call
@@ -82,6 +83,8 @@ def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, 
     copies = [fmt] + [clone_format(fmt) for _ in range(n_copies - 1)]
     calls = [ops.make_decode_args(q, c, pos_q, None, n_splits=n_splits, stream_n=stream_n)
              for c in copies]
+    for c in calls:
+        c.args.kernel = kernel
     ws = ops.decode_workspace(calls[0])
     for i in range(warmup):
         ops.decode_attn(calls[i % n_copies], ws)
@@ -505,6 +508,8 @@ def main():
     ap.add_argument("--no-32k", dest="also_32k", action="store_false")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--n-splits", type=int, default=0)
+    ap.add_argument("--kernel", type=int, default=0,
+                    help="decode split kernel: 0 automatic, 1 row-split, 2 token-tiled")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a 256 MiB device copy (PMC byte-counter calibration) and exit")
     ap.add_argument("--stream-curve", action="store_true",
@@ -559,7 +564,7 @@ def main():
         nbytes = algorithmic_bytes(n, rank)
         n_copies = max(2, math.ceil(2 * 256e6 / nbytes))
         us, us_hot, us_eager = time_decode(fmt, q, T, args.steps, args.warmup, n_copies,
-                                           args.n_splits)
+                                           args.n_splits, kernel=args.kernel)
         res = {"T": T, "n_comp": n, "rank": fmt["rank"], "us": us, "us_hot": us_hot,
                "us_eager": us_eager,
                "bytes": nbytes, "flops": algorithmic_flops(n, rank), "copies": n_copies}

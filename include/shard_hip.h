@@ -227,7 +227,8 @@ typedef struct shard_decode_args {
   int64_t mask_stride;
   uint16_t* out;
   int32_t n_splits; /* 0 = choose automatically */
-  int32_t _pad1;
+  int32_t kernel;   /* split kernel: 0 = automatic, 1 = row-split (4 waves share a
+                     * tile), 2 = token-tiled (each wave owns whole tiles) */
   /* nullable device int64: when set, the kernel reads pos_q from it (the
    * reference's cache_position[-1], attention.py:383) and `pos_q` is ignored,
    * so the caller needs no host read-back of the position */

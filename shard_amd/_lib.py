@@ -41,7 +41,7 @@ class DecodeArgs(ctypes.Structure):
         ("dec_k", c_void_p), ("dec_v", c_void_p), ("n_dec", c_int32), ("dec_stride", c_int32),
         ("s_k", c_void_p), ("s_v", c_void_p), ("n_stream", c_int32), ("_pad0", c_int32),
         ("mask", c_void_p), ("mask_stride", c_int64),
-        ("out", c_void_p), ("n_splits", c_int32), ("_pad1", c_int32),
+        ("out", c_void_p), ("n_splits", c_int32), ("kernel", c_int32),
         ("pos_q_dev", c_void_p),
     ]
 

@@ -1,34 +1,37 @@
 // Fused decode attention over Shard's compressed KV cache, written for gfx950.
 //
-// Work split (one split launch + one combine launch per layer-step):
-//   split kernel   grid = (n_splits * n_kv, B); a 512-thread workgroup (one per
-//                  CU) owns one kv head x a chunk of compressed tokens, which it
-//                  walks 64 tokens at a time: waves 0-3 take the first 32-token
-//                  tile, waves 4-7 the second.  Wave w owns the 16 RoPE pairs
-//                  [16 (w%4), 16 (w%4) + 16) of the head, so the sin/cos of a
-//                  (token, pair) is computed once.
-//     1. no-RoPE keys are rebuilt on chip with MFMA 32x32x16 f16:
-//          K_n[rows, tok] = Basis'[rows, r] . coef[r, tok] + mean
-//        Basis' = fp16(basis_f16 * coeff_scale) lives in VGPRs for the whole
-//        kernel; coef are the packed nibbles (128-bit loads, prefetched one
-//        iteration ahead) turned into exact fp16 integers n-8 with a
-//        magic-number trick; the mean is one more k-step (times a constant 1).
+// One split launch + one combine launch per layer-step.  Two split kernels
+// compute the same partial rows; shard_decode_attn picks one by the work per CU.
+//
+//   k_decode_split (row-split)  grid = (n_splits * n_kv, B), 256-thread
+//     workgroups, two per CU; one kv head x a chunk of compressed tokens, walked
+//     32 tokens at a time.  The 4 waves share each tile: wave P rebuilds rows
+//     of the 16 RoPE pairs [16 P, 16 P + 16) (basis operand in VGPRs), the
+//     partial scores meet in LDS, then a shared online softmax and VQ value sum.
+//   k_decode_tok (token-tiled)  grid = (n_splits * n_kv, B), 512-thread
+//     workgroups, one per CU; the kv head's basis operand image sits in LDS
+//     and each wave takes whole tiles (all 128 rows) from an LDS counter, with
+//     its own softmax state; the waves merge once at the end.
+//   Per tile, both:
+//     1. rebuild the no-RoPE keys on chip with MFMA 32x32x16 f16:
+//          16 K_n[rows, tok] = Basis'[rows, r] . coef[r, tok] + 16 mean
+//        (coefficients: packed nibbles turned into exact fp16 integers by a
+//        magic-number trick; the mean is one more k-step times a constant 1).
 //        Keys never reach HBM.
-//     2. each (c, d) pair is rotated by phi = (pos_t - pos_q) * theta_i (the
-//        relative-delta RoPE identity, attention.py:3-6) and dotted with
-//        q_n = undo-RoPE(q, pos_q) by a second MFMA (rows = query heads).
-//        sin/cos(phi) advance by one fixed rotation per iteration.
-//     3. the 4 pair slices' partial scores are summed in LDS, online softmax
-//        (fp32, base 2), and the VQ values sum_t p_t * cb[idx_t] (rotated
-//        space) are accumulated with the codebook in LDS.
+//     2. rotate each (c, d) pair by its RoPE phase and dot with q on a second
+//        MFMA (rows = query heads) - the relative-delta identity of
+//        attention.py:3-6 in the row-split kernel, the equivalent absolute
+//        form (q_rope rotated by the tile phase) in the token-tiled one.
+//     3. online softmax (fp32, base 2) and the VQ values sum_t p_t cb[idx_t]
+//        (rotated space) with the codebook in LDS.
 //     4. per (query head, split): running max m, sum l and the 128-dim
 //        accumulator go to the workspace.
-//     The last split of each head first runs the extra tokens (fp16 sink,
-//     window and decode tokens, the dequantized stream) into one more partial
-//     row per query head.
-//   combine kernel grid = (n_q, B): merges the partial rows, applies ch and ONE
-//                  inverse Hadamard to the VQ part, adds the plain-basis part of
-//                  the extra tokens, normalizes, writes fp16.
+//   The last split of each head first runs the extra tokens (fp16 sink,
+//   window and decode tokens, the dequantized stream) into one more partial
+//   row per query head.
+//   k_decode_combine  grid = (n_q, B): merges the partial rows, applies ch and
+//     ONE inverse Hadamard to the VQ part, adds the plain-basis part of the
+//     extra tokens, normalizes, writes fp16.
 #include "common.h"
 
 namespace shard {
@@ -40,6 +43,13 @@ constexpr int kGQA = 4;           // query heads per kv head
 constexpr int kMaxExtra = 2048;   // sink + window + decode + stream tokens per call
 constexpr int kMaxSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw, unswizzled access (gfx9)
+// rope tables of the per-layer operands (k_decode_prepare): in-tile column
+// phases, the per-tile step, and the token-tiled kernel's two tile-offset tables
+constexpr int kRopeEntries = 32 * 64 + 64 + 2 * 32 * 64;
+constexpr int kRopeT2 = 32 * 64 + 64;       // (cos, sin)(32 b theta), b < 32
+constexpr int kRopeT1 = kRopeT2 + 32 * 64;  // (cos, sin)(1024 a theta), a < 32
+constexpr int kTokMaxTiles = 32 * 32;       // tiles per token-tiled chunk the tables cover
 #ifndef SHARD_SPLIT_PER_XCD
 #define SHARD_SPLIT_PER_XCD 1
 #endif
@@ -149,14 +159,17 @@ __device__ __forceinline__ void load_coef(const uint8_t* rowp, bool valid, uint3
 //        The parts hold |C| up to about 9.8e5 (greedy split, 15 x 65504 + rest),
 //        far above real keys (|C| is a few thousand).
 //   rope float2 [32][64] = (cos, sin)(col * theta_i) for the token column inside
-//        a tile, then float2 [64] = (cos, sin)(32 * theta_i), the per-tile step.
+//        a tile, then float2 [64] = (cos, sin)(32 * theta_i), the per-tile step,
+//        then the tile-offset tables of the token-tiled kernel: float2 [32][64] =
+//        (cos, sin)(32 b theta_i) and float2 [32][64] = (cos, sin)(1024 a theta_i)
+//        (tile k of a chunk is 32 (32 a + b) tokens from its start).
 __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint16_t* __restrict__ cs,
                                  const uint16_t* __restrict__ mean, const float* __restrict__ inv_freq,
                                  int G, int rank, uint4* __restrict__ op, float2* __restrict__ rope) {
   const int KS = rank / 16;
   const int64_t n_op = (int64_t)G * 4 * (KS + 1) * 64;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_op + 32 * 64 + 64; i += stride) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_op + kRopeEntries; i += stride) {
     if (i < n_op) {
       const int lane = (int)(i % 64);
       const int s = (int)((i / 64) % (KS + 1));
@@ -189,8 +202,15 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
     } else {
       const int k = (int)(i - n_op);
       float sn, cn;
-      if (k < 32 * 64) sincosf((float)(k / 64) * inv_freq[k % 64], &sn, &cn);
-      else sincosf((float)kTile * inv_freq[k - 32 * 64], &sn, &cn);
+      if (k < 32 * 64) {
+        sincosf((float)(k / 64) * inv_freq[k % 64], &sn, &cn);
+      } else if (k < 32 * 64 + 64) {
+        sincosf((float)kTile * inv_freq[k - 32 * 64], &sn, &cn);
+      } else {
+        const int k2 = k - (32 * 64 + 64);  // tile-offset tables
+        const int tab = k2 / (32 * 64), e = (k2 / 64) % 32, pi = k2 % 64;
+        sincosf((float)(tab == 0 ? kTile * e : kTile * 32 * e) * inv_freq[pi], &sn, &cn);
+      }
       rope[k] = make_float2(cn, sn);
     }
   }
@@ -251,13 +271,22 @@ static_assert(kTG == 1 || kTG == 2, "SHARD_DECODE_TG must be 1 or 2");
 // Writes partial row n_splits of each query head, in the plain (not rotated)
 // basis.
 template <int NW>
-__device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const int g, const int b) {
+struct XtLds {
+  float xsc[kGQA][32 * NW];     // scores of the pass (base 2)
+  float xpw[32 * NW][kGQA];     // softmax numerators, [token][head]
+  float2 xred[NW][kGQA][64];    // per-wave value sums
+  float xal[kGQA];              // rescale of the running sums
+};
+
+template <int NW>
+__device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const int g, const int b,
+                                                   XtLds<NW>& L) {
   constexpr int XT = 32 * NW;  // tokens per pass
   constexpr int XV = XT / 64;  // softmax values per lane
-  __shared__ __align__(16) float xsc[kGQA][XT];       // scores of the pass (base 2)
-  __shared__ __align__(16) float xpw[XT][kGQA];       // softmax numerators, [token][head]
-  __shared__ __align__(16) float2 xred[NW][kGQA][64]; // per-wave value sums
-  __shared__ float xal[kGQA];                         // rescale of the running sums
+  auto& xsc = L.xsc;
+  auto& xpw = L.xpw;
+  auto& xred = L.xred;
+  auto& xal = L.xal;
 
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -428,7 +457,8 @@ void k_decode_split(const SplitParams p) {
   // The last split of each head runs the extra tokens first (its compressed
   // chunk is shorter by their cost), so their cold loads overlap the other
   // workgroups' set-up instead of trailing the kernel.
-  if (split == p.n_splits - 1 && p.xs.n_x > 0) decode_extras_tail<4 * TG>(p, hg, b);
+  __shared__ __align__(16) XtLds<4 * TG> xt;
+  if (split == p.n_splits - 1 && p.xs.n_x > 0) decode_extras_tail<4 * TG>(p, hg, b, xt);
 
   // ---- loads that feed LDS and the q operand go out first: the first barrier
   // waits for these only, not for the tile and basis loads behind them.
@@ -688,6 +718,409 @@ void k_decode_split(const SplitParams p) {
 }
 
 // --------------------------------------------------------------------------
+// Token-tiled split kernel: each wave rebuilds all 128 rows of its own tiles.
+// --------------------------------------------------------------------------
+// One 512-thread workgroup (8 waves) per CU owns one kv head x a token chunk.
+// The head's basis operand image (4 row blocks x (KS + 1) k-steps, 52 KB at
+// rank 192) sits in LDS; the chunk's 32-token tiles are dealt to the waves in
+// turn (tile k to wave k % 8), and a wave works through its tiles with no
+// workgroup barrier: per tile it unpacks the coefficients once, runs the 4 x
+// (KS + 1) rebuild MFMAs with A from LDS, rotates, scores, and keeps its own
+// online softmax and VQ value sums.  The waves merge once, after the loop.
+//
+// Tiles go to the waves through an LDS counter: wave w starts with tile w and
+// claims its next one when it starts a tile (so the claim and the next tile's
+// loads are a tile ahead of their use); fast waves take more tiles.
+//
+// RoPE: undo-RoPE at pos_q followed by the relative rotation (pos_t - pos_q) of
+// the reference (attention.py:3-6, 74-79) is the rotation of q_rope by -pos_t
+// (pos_q cancels), so the score of token t is q_rope . R(pos_t theta) k_t with
+// k_t the no-RoPE key.  For token t0 + col of a tile, pos_t theta = phi0 +
+// col theta: the in-tile part is a constant per lane (table rc, with the 1/16 of
+// the rebuilt keys folded in) and the tile part rotates q instead,
+//   q . R(phi0 + phic) k = (R(-phi0) q) . (R(phic) k),
+// one rotation of the 4 query heads per tile (lane = pair).  phi0 of tile k of
+// the chunk is the chunk start's phase composed with the per-layer tables
+// (32 (k mod 32)) theta and (1024 (k / 32)) theta.
+constexpr int kTokWaves = 8;
+constexpr int kTokThreads = 64 * kTokWaves;
+
+template <int KS>
+struct TokLds {
+  union {
+    uint4 A[4][KS + 1][64];        // basis operand image of the kv head
+    XtLds<kTokWaves> xt;           // extra tokens (run before the image is loaded)
+    struct {                       // end-of-chunk merge (after the tile loop)
+      float acc[kTokWaves][kGQA][kHD];
+      float m[kTokWaves][kGQA];
+      float l[kTokWaves][kGQA];
+    } red;
+  } u;
+  uint2 cb[256];                       // VQ codebook, 4 x fp16 per entry
+  float2 rc[64][32];                   // (cos, sin)(col theta_i) / 16, [pair][column]
+  uint16_t qr[kTokWaves][5][2][64];    // per wave: R(-phi0) q_n in fp16, [head][a|b][k order]; head 4 = 0
+  uint32_t pb[kTokWaves][kGQA][2][8];  // per wave: softmax numerators, fp16 token pairs
+  uint32_t next_tile;                  // the chunk's next unclaimed tile
+};
+
+// Position in the score MFMA's k order (16 rb + 8 hh + e) of pair i, where the
+// rebuild MFMA puts pair 16 rb + 8 (e / 4) + 4 hh + e % 4 in element e of lane half hh.
+__device__ __forceinline__ int pair_k(int i) {
+  const int pl = i & 15;
+  return (i & ~15) + 8 * ((pl >> 2) & 1) + 4 * (pl >> 3) + (pl & 3);
+}
+
+template <int KS>
+__global__ __launch_bounds__(kTokThreads, 1)
+void k_decode_tok(const SplitParams p) {
+  constexpr int NW = kTokWaves;
+  constexpr int NQ = kGQA;
+  __shared__ __align__(16) TokLds<KS> L;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31;
+  const int hh = lane >> 5;
+
+  // block -> (kv head, split, batch row): as k_decode_split without two_class
+  const int HG = p.G;
+  const int bid = blockIdx.x;
+  int hg, split;
+  if (kSplitPerXcd && (p.n_splits & 7) == 0) {
+    const int slot = bid >> 3;
+    hg = slot % HG;
+    split = (slot / HG) * 8 + (bid & 7);
+  } else {
+    hg = bid % HG;
+    split = bid / HG;
+  }
+  const int b = blockIdx.y;
+
+  if (split == p.n_splits - 1 && p.xs.n_x > 0) {
+    decode_extras_tail<NW>(p, hg, b, L.u.xt);
+    __syncthreads();  // the image below overwrites the extras' LDS
+  }
+
+  const int t_begin = split * p.chunk;
+  int t_end = t_begin + p.chunk;
+  if (t_end > p.n_comp) t_end = p.n_comp;
+  const int n_t = t_end > t_begin ? (t_end - t_begin + kTile - 1) / kTile : 0;
+
+  // ---- first tile's loads, then the per-layer operands into LDS.  The
+  // chunk's coefficient rows and V indices are raw buffers: rows past the
+  // chunk end read as zeros (coefficient -8 and centroid 0: finite, and their
+  // scores are -inf), and the offsets of a tile are one base + immediates.
+  const int coef_row_bytes = p.rank / 2;
+  const int n_rows = t_end > t_begin ? t_end - t_begin : 0;
+  const __amdgpu_buffer_rsrc_t rcoef = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.coef + ((int64_t)b * p.n_comp + t_begin) * coef_row_bytes), (short)0,
+      n_rows * coef_row_bytes, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rvidx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.vidx + (((int64_t)b * p.G + hg) * p.n_comp + t_begin) * 32), (short)0,
+      n_rows * 32, kBufWord3);
+  const int vj = lane & 31, vpar = lane >> 5;  // V stage: subvector, token parity
+  auto load_vidx = [&](int t0, uint32_t (&vi_)[16]) {
+    const int voff = (t0 - t_begin + vpar) * 32 + vj;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) vi_[m] = __builtin_amdgcn_raw_buffer_load_b8(rvidx, voff + 64 * m, 0, 0);
+  };
+  const float2* t2tab = p.rope + kRopeT2 + lane;  // lane = pair
+  const float2* t1tab = p.rope + kRopeT1 + lane;
+  auto load_tile = [&](int k, uint32_t (&cw_)[KS], float2& f2, float2& f1) {
+    const int r0 = kTile * k;
+    f2 = t2tab[64 * (k & 31)];
+    f1 = t1tab[64 * (k >> 5)];
+    const int coff = (r0 + col) * coef_row_bytes + KS * 4 * hh;
+    if constexpr (KS % 4 == 0) {
+#pragma unroll
+      for (int s = 0; s < KS; s += 4) {
+        const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rcoef, coff + 4 * s, 0, 0));
+        cw_[s] = v.x; cw_[s + 1] = v.y; cw_[s + 2] = v.z; cw_[s + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; s += 2) {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rcoef, coff + 4 * s, 0, 0));
+        cw_[s] = v.x; cw_[s + 1] = v.y;
+      }
+    }
+  };
+  uint32_t cwA[KS], cwB[KS];
+  float2 fA2, fA1, fB2, fB1;
+  if (w < n_t) load_tile(w, cwA, fA2, fA1);
+
+  // every global load of the set-up goes out before the first LDS store, so
+  // the cold misses overlap (one round trip instead of one per copy step)
+  constexpr int kNA = 4 * (KS + 1) * 64;                       // uint4 of the image
+  constexpr int kPA = (kNA + kTokThreads - 1) / kTokThreads;   // per thread
+  constexpr int kPR = 32 * 64 / kTokThreads;                   // rope entries per thread
+  uint4 av[kPA];
+  float2 rv[kPR];
+  {
+    const uint4* src = p.op + (int64_t)hg * kNA;
+#pragma unroll
+    for (int j = 0; j < kPA; ++j) {
+      const int i = tid + kTokThreads * j;
+      av[j] = i < kNA ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int j = 0; j < kPR; ++j) rv[j] = p.rope[tid + kTokThreads * j];
+  }
+  const uint2 cbv = tid < 256 ? *(const uint2*)(p.vcb + 4 * tid) : make_uint2(0u, 0u);
+  const float th = p.inv_freq[lane];
+  uint16_t qlo[NQ], qhi[NQ];
+  {
+    const uint16_t* qv = p.q + ((int64_t)b * p.H + hg * NQ) * kHD;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      qlo[h] = qv[h * kHD + lane];
+      qhi[h] = qv[h * kHD + 64 + lane];
+    }
+  }
+  {
+    uint4* dst = &L.u.A[0][0][0];
+#pragma unroll
+    for (int j = 0; j < kPA; ++j) {
+      const int i = tid + kTokThreads * j;
+      if (i < kNA) dst[i] = av[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kPR; ++j) {  // rope table [col][pair] -> rc[pair][col] / 16
+      const int i = tid + kTokThreads * j;
+      L.rc[i & 63][i >> 6] = make_float2(rv[j].x * 0.0625f, rv[j].y * 0.0625f);
+    }
+  }
+  if (tid < 256) L.cb[tid] = cbv;
+  {  // zero row (head 4) of each wave's rotated-q slot
+    uint32_t* z = (uint32_t*)&L.qr[0][0][0][0];
+    for (int i = tid; i < NW * 64; i += kTokThreads) {
+      const int ww = i >> 6, k = i & 63;
+      z[((ww * 5 + 4) * 2 * 64) / 2 + k] = 0u;
+    }
+  }
+
+  // ---- per-lane pair state (lane = pair i): q_rope of the 4 heads, the
+  // phase of the chunk's first token
+  float qa[NQ], qb[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    qa[h] = h2f(qlo[h]);
+    qb[h] = h2f(qhi[h]);
+  }
+  float bs_c, bs_s;
+  sincosf((float)(p.cstart + t_begin) * th, &bs_s, &bs_c);
+  const int kq = pair_k(lane);  // this lane's slot in the rotated-q rows
+  if (tid == 0) L.next_tile = NW;
+
+  // rc rows of this lane: pairs 16 rb + pr[i]
+  int pr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) pr[i] = 8 * (i >> 2) + 4 * hh + (i & 3);
+  const int qrow = min(col, NQ);  // rows >= 4 of the score MFMA read the zero row
+  half8 one8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) one8[e] = (half_t)1.f;
+  __syncthreads();
+
+  const float sc = kLog2e * rsqrtf((float)kHD);
+  float m_run[NQ], l_part[NQ], vacc[NQ][4];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    m_run[h] = -INFINITY;
+    l_part[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vacc[h][e] = 0.f;
+  }
+
+  auto tile = [&](const int k, const uint32_t (&cw)[KS], const float2 f2, const float2 f1) {
+    const int t0 = t_begin + kTile * k;
+    uint32_t vi[16];  // V indices of the tile: needed at its end
+    load_vidx(t0, vi);
+    // 1. q rotated by -phi0 of this tile -> the wave's qr slot (lane = pair);
+    //    phi0 = chunk start + 32 (k mod 32) theta + 1024 (k / 32) theta
+    float ph_c = bs_c * f2.x - bs_s * f2.y;
+    float ph_s = bs_s * f2.x + bs_c * f2.y;
+    {
+      const float c = ph_c * f1.x - ph_s * f1.y;
+      ph_s = ph_s * f1.x + ph_c * f1.y;
+      ph_c = c;
+    }
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const float a2 = qa[h] * ph_c + qb[h] * ph_s;
+      const float b2 = qb[h] * ph_c - qa[h] * ph_s;
+      L.qr[w][h][0][kq] = f2h(a2);
+      L.qr[w][h][1][kq] = f2h(b2);
+    }
+    // 2. coefficients -> MFMA B operands, once for the 4 row blocks
+    half8 Bc[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) Bc[s] = nib8_to_mfma(cw[s]);
+    const float16v zero16 = {};
+    float16v sacc = zero16;
+    // A operands stream from LDS through a ring of kRing registers, so kRing
+    // reads are in flight ahead of the MFMA that consumes them
+    // Two row blocks at a time: their MFMA chains interleave (independent
+    // accumulators) and share each converted coefficient operand.  The A
+    // operands stream from LDS through a ring of kRing registers, so kRing
+    // reads are in flight ahead of the MFMA that consumes them.
+    constexpr int kRing = 4;
+    constexpr int NA = 4 * (KS + 1);  // A operands per tile, in (pair, k-step, block) order
+    auto a_at = [&](int j) {
+      const int qp = j / (2 * (KS + 1)), rem = j % (2 * (KS + 1));
+      const int s = rem >> 1, rb = 2 * qp + (rem & 1);
+      return __builtin_bit_cast(half8, L.u.A[rb][s == 0 ? KS : s - 1][lane]);
+    };
+    half8 ring[kRing];
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) ring[j] = a_at(j);
+#pragma unroll
+    for (int qp = 0; qp < 2; ++qp) {
+      float16v acc[2];
+#pragma unroll
+      for (int s = 0; s <= KS; ++s) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int j = (qp * (KS + 1) + s) * 2 + r;
+          const half8 a = ring[j % kRing];
+          if (j + kRing < NA) ring[j % kRing] = a_at(j + kRing);
+          acc[r] = s == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_f16(a, one8, zero16, 0, 0, 0)
+                          : __builtin_amdgcn_mfma_f32_32x32x16_f16(a, Bc[s - 1], acc[r], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int rb = 2 * qp + r;
+        half8 b0, b1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float2 rr = L.rc[16 * rb + pr[i]][col];
+          const float c = acc[r][i], d = acc[r][i + 8];
+          b0[i] = (half_t)(c * rr.x - d * rr.y);
+          b1[i] = (half_t)(d * rr.x + c * rr.y);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const half8 qa8 = *(const half8*)&L.qr[w][qrow][0][16 * rb + 8 * hh];
+        const half8 qb8 = *(const half8*)&L.qr[w][qrow][1][16 * rb + 8 * hh];
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa8, b0, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qb8, b1, sacc, 0, 0, 0);
+      }
+    }
+    // 3. online softmax of the 4 heads over the tile (lanes 0-31: token col)
+    float al[NQ];
+    {
+      const int tok = t0 + col;
+      const bool ok = hh == 0 && tok < t_end;
+      const float madd = (p.mask && ok) ? p.mask[(int64_t)b * p.mask_stride + p.n_sink + tok] * kLog2e : 0.f;
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        const float s = ok ? sacc[h] * sc + madd : -INFINITY;
+        const float m_new = fmaxf(m_run[h], wave64_reduce(s, OpMax()));
+        al[h] = m_new == -INFINITY ? 1.f : exp2f(m_run[h] - m_new);
+        const float pv = s == -INFINITY ? 0.f : exp2f(s - m_new);
+        l_part[h] = l_part[h] * al[h] + pv;
+        m_run[h] = m_new;
+        if (hh == 0)
+          ((uint16_t*)&L.pb[w][h][col & 1][0])[col >> 1] = f2h(pv);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // 4. VQ values of the tile: lane (subvector vj, parity vpar) takes tokens
+    //    2 m + vpar; dot2 over the token pairs (4 u + vpar, 4 u + 2 + vpar)
+#pragma unroll
+    for (int h = 0; h < NQ; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vacc[h][e] *= al[h];
+    uint4 pq[NQ][2];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      pq[h][0] = *(const uint4*)&L.pb[w][h][vpar][0];
+      pq[h][1] = *(const uint4*)&L.pb[w][h][vpar][4];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint2 ca = L.cb[vi[2 * u]], cb = L.cb[vi[2 * u + 1]];
+      half2v c2[4];
+      c2[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x05040100u));
+      c2[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x07060302u));
+      c2[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x05040100u));
+      c2[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x07060302u));
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        const uint4 v4 = pq[h][u >> 2];
+        const uint32_t pw = (u & 3) == 0 ? v4.x : (u & 3) == 1 ? v4.y : (u & 3) == 2 ? v4.z : v4.w;
+        const half2v p2 = __builtin_bit_cast(half2v, pw);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vacc[h][e] = __builtin_amdgcn_fdot2(p2, c2[e], vacc[h][e], false);
+      }
+    }
+  };
+
+  auto claim = [&]() {
+    uint32_t v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(&L.next_tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return (int)__builtin_amdgcn_readfirstlane(v);
+  };
+  int k = w;
+  while (k < n_t) {  // ping-pong: the claimed tile's loads fly during the current one
+    const int kb = claim();
+    if (kb < n_t) load_tile(kb, cwB, fB2, fB1);
+    tile(k, cwA, fA2, fA1);
+    if (kb >= n_t) break;
+    k = claim();
+    if (k < n_t) load_tile(k, cwA, fA2, fA1);
+    tile(kb, cwB, fB2, fB1);
+  }
+
+  // ---- merge the waves: (m, l, acc) of each query head
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    l_part[h] = wave64_reduce(l_part[h], OpAdd());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a, c;
+      perm32_swap(vacc[h][e], a, c);
+      vacc[h][e] = a + c;  // the two token parities
+    }
+  }
+  __syncthreads();  // every wave is done with the image the merge buffer overlays
+  if (lane < 32) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h)
+      *(float4*)&L.u.red.acc[w][h][4 * vj] = make_float4(vacc[h][0], vacc[h][1], vacc[h][2], vacc[h][3]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      L.u.red.m[w][h] = m_run[h];
+      L.u.red.l[w][h] = l_part[h];
+    }
+  }
+  __syncthreads();
+  {
+    const int h = tid >> 7, d = tid & 127;  // 512 threads = 4 heads x 128 dims
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, L.u.red.m[ww][h]);
+    float acc = 0.f, l = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float mw = L.u.red.m[ww][h];
+      const float wt = mw == -INFINITY ? 0.f : exp2f(mw - M);
+      acc += wt * L.u.red.acc[ww][h][d];
+      l += wt * L.u.red.l[ww][h];
+    }
+    const int64_t widx = ((int64_t)b * p.H + hg * NQ + h) * p.nsp + split;
+    p.ws_acc[widx * kHD + d] = acc;
+    if (d == 0) {
+      p.ws_m[widx] = M;
+      p.ws_l[widx] = l;
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
 // Combine: merge the partials of one query head, one inverse FWHT.
 // --------------------------------------------------------------------------
 struct CombineParams {
@@ -825,24 +1258,46 @@ void k_decode_combine(const CombineParams p) {
   }
 }
 
+// Which split kernel runs.  Automatic choice by the work per CU: the
+// token-tiled kernel has the higher tile throughput (measured on MI355X:
+// batch 16 x 16K 159 vs 184 us, batch 4 x 8K 32.2 vs 35.7 us, batch 1 x 32K
+// 31.2 vs 32.8 us per call) but a longer set-up and one tile per wave at
+// batch 1 x 8K (19.2 vs 16.8 us), so it takes over from 16 head-tiles per CU.
+constexpr int64_t kTokMinHeadTiles = 16 * 256;
+inline bool use_tok(const shard_decode_args* a) {
+  if (a->kernel == 2) return true;
+  if (a->kernel == 1) return false;
+  const int64_t tiles = (int64_t)((a->n_comp + kTile - 1) / kTile) * a->n_kv_heads * a->batch;
+  return tiles >= kTokMinHeadTiles;
+}
+
 inline int choose_splits(const shard_decode_args* a) {
   const int max_useful = (a->n_comp + kTile - 1) / kTile;
   int want;
   if (a->n_splits > 0) {
     want = a->n_splits;
   } else {
-    const int target = kTG == 1 ? 512 : 256;  // workgroups that fill 256 CUs
+    // workgroups that fill 256 CUs: one 512-thread token-tiled workgroup per
+    // CU, or two 256-thread row-split workgroups
+    const int target = use_tok(a) ? 256 : kTG == 1 ? 512 : 256;
     want = target / (a->n_kv_heads * a->batch);
   }
   if (want > max_useful) want = max_useful;
   if (want < 1) want = 1;
+  if (use_tok(a)) {  // a token-tiled chunk spans at most kTokMaxTiles tiles (phase tables)
+    const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
+    const int cap = max_useful + (n_x + 63) / 64;
+    const int need = (cap + kTokMaxTiles - 1) / kTokMaxTiles;
+    if (want < need) want = need;
+  }
   if (want > kMaxSplits) want = kMaxSplits;
   return want;
 }
 
 template <int KS>
-void launch_split(const SplitParams& sp, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((k_decode_split<KS, kTG>), grid, dim3(256 * kTG), 0, s, sp);
+void launch_split(const SplitParams& sp, dim3 grid, bool tok, hipStream_t s) {
+  if (tok) hipLaunchKernelGGL((k_decode_tok<KS>), grid, dim3(kTokThreads), 0, s, sp);
+  else hipLaunchKernelGGL((k_decode_split<KS, kTG>), grid, dim3(256 * kTG), 0, s, sp);
 }
 
 }  // namespace shard
@@ -857,7 +1312,7 @@ extern "C" {
 
 size_t shard_decode_prepare_bytes(int32_t n_kv_heads, int32_t rank) {
   if (n_kv_heads <= 0 || rank <= 0 || rank % 32 != 0) return 0;
-  return shard_decode_prepare_op_bytes(n_kv_heads, rank) + (32 * 64 + 64) * sizeof(float2);
+  return shard_decode_prepare_op_bytes(n_kv_heads, rank) + kRopeEntries * sizeof(float2);
 }
 
 int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
@@ -871,7 +1326,7 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
   hipStream_t s = (hipStream_t)stream;
   uint4* op = (uint4*)out;
   float2* rope = (float2*)((char*)out + shard_decode_prepare_op_bytes(n_kv_heads, rank));
-  const int64_t total = (int64_t)n_kv_heads * 4 * (rank / 16 + 1) * 64 + 32 * 64 + 64;
+  const int64_t total = (int64_t)n_kv_heads * 4 * (rank / 16 + 1) * 64 + kRopeEntries;
   hipLaunchKernelGGL(k_decode_prepare, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                      k_basis, k_coeff_scale, k_mean, inv_freq, n_kv_heads, rank, op, rope);
   SHARD_LAUNCH_CHECK("shard_decode_prepare");
@@ -895,6 +1350,7 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
     return SHARD_ERR_SHAPE;
   if (a->rank <= 0 || a->rank % 32 != 0 || a->rank > 192) return SHARD_ERR_SHAPE;
   if (a->n_sink < 0 || a->n_win < 0 || a->n_dec < 0 || a->n_stream < 0) return SHARD_ERR_ARG;
+  if (a->kernel < 0 || a->kernel > 2) return SHARD_ERR_ARG;
   const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
   if (n_x > kMaxExtra) return SHARD_ERR_SHAPE;
   if ((a->n_sink && (!a->sink_k || !a->sink_v)) || (a->n_win && (!a->win_k || !a->win_v)) ||
@@ -925,8 +1381,9 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   sp.chunk2 = sp.chunk;
   sp.n_first = ns;
   sp.two_class = 0;
+  const bool tok = use_tok(a);
   const int half = ns / 2;
-  if (kTG == 1 && kSplitBias && (int64_t)ns * a->n_kv_heads * a->batch == 512 &&
+  if (!tok && kTG == 1 && kSplitBias && (int64_t)ns * a->n_kv_heads * a->batch == 512 &&
       ns % 2 == 0 && 32 % a->n_kv_heads == 0 && n_tiles >= 2 * ns) {
     // first class: ta tiles per split, second class: tb (the last split also
     // runs the extra tokens, counted as x_cost tiles)
@@ -955,12 +1412,12 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
 
   dim3 grid((unsigned)(ns * a->n_kv_heads), (unsigned)a->batch);
   switch (a->rank / 16) {
-    case 2: launch_split<2>(sp, grid, s); break;
-    case 4: launch_split<4>(sp, grid, s); break;
-    case 6: launch_split<6>(sp, grid, s); break;
-    case 8: launch_split<8>(sp, grid, s); break;
-    case 10: launch_split<10>(sp, grid, s); break;
-    case 12: launch_split<12>(sp, grid, s); break;
+    case 2: launch_split<2>(sp, grid, tok, s); break;
+    case 4: launch_split<4>(sp, grid, tok, s); break;
+    case 6: launch_split<6>(sp, grid, tok, s); break;
+    case 8: launch_split<8>(sp, grid, tok, s); break;
+    case 10: launch_split<10>(sp, grid, tok, s); break;
+    case 12: launch_split<12>(sp, grid, tok, s); break;
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_decode_attn split");

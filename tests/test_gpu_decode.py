@@ -17,7 +17,7 @@ TOL_ABS = 2e-3
 TOL_COS = 0.9999
 
 
-def _run(cuda, gc, inv, q, pos_q, mask=None, n_splits=0, nkv=8):
+def _run(cuda, gc, inv, q, pos_q, mask=None, n_splits=0, nkv=8, kernel=0):
     from shard_amd import ops
     d = to_device(gc, cuda, inv, nkv=nkv)
     B = gc["batch"]
@@ -26,6 +26,7 @@ def _run(cuda, gc, inv, q, pos_q, mask=None, n_splits=0, nkv=8):
     m = None if mask is None else torch.from_numpy(mask).to(cuda)
     call = ops.make_decode_args(q.to(cuda).reshape(B, -1, 128), d, pos_q, None, mask=m,
                                 n_splits=n_splits, stream_n=stream_n, decode_kv=dec)
+    call.args.kernel = kernel
     out = ops.decode_attn(call)
     torch.cuda.synchronize()
     return out.cpu().float().numpy().reshape(B, -1, 1, 128)
@@ -47,8 +48,13 @@ CASES = [
 ]
 
 
+# split kernels: 1 = row-split (4 waves share a tile), 2 = token-tiled (a wave owns whole tiles)
+KERNELS = [1, 2]
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
-def test_decode_matches_exact_oracle(cuda, case):
+def test_decode_matches_exact_oracle(cuda, case, kernel):
     B, nkv, rank, n_comp, sink, win, n_stream, n_dec = case
     gc, inv = random_layer(B=B, nkv=nkv, rank=rank, n_comp=n_comp, sink=sink, win=win,
                            n_stream=n_stream, n_dec=n_dec, seed=n_comp + rank)
@@ -56,14 +62,15 @@ def test_decode_matches_exact_oracle(cuda, case):
     q = torch.randn(B, 4 * nkv, 1, 128, generator=g).half()
     pos_q = sink + n_comp + win + n_dec + n_stream - 1
     want = exact.decode_attention(q.numpy(), gc, nkv, pos_q, inv.numpy())
-    got = _run(cuda, gc, inv, q, pos_q, nkv=nkv)
+    got = _run(cuda, gc, inv, q, pos_q, nkv=nkv, kernel=kernel)
     err, cos = compare(got, want)
-    print(f"case={case} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    print(f"case={case} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}", flush=True)
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
+@pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("bits,qjl", [(4, True), (2, False), (8, True)])
-def test_decode_with_qjl_and_narrow_stream(cuda, bits, qjl):
+def test_decode_with_qjl_and_narrow_stream(cuda, bits, qjl, kernel):
     """Stream tokens quantized with 2/4-bit codes and the QJL residual
     (cache.py:234-240, 263-273): the oracle adds (2 sign - 1) * scale in the
     rotated domain before the inverse Hadamard."""
@@ -71,25 +78,27 @@ def test_decode_with_qjl_and_narrow_stream(cuda, bits, qjl):
     q = torch.randn(2, 32, 1, 128, generator=torch.Generator().manual_seed(4)).half()
     pos_q = 4 + 400 + 64 + 23 - 1
     want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
-    got = _run(cuda, gc, inv, q, pos_q)
+    got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
     err, cos = compare(got, want)
     print(f"bits={bits} qjl={qjl} max_abs={err:.3e} cos={cos:.7f}", flush=True)
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
-def test_decode_rank_padding_and_splits(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_decode_rank_padding_and_splits(cuda, kernel):
     """rank 100 (padded to 128 on the device) and several explicit split counts."""
     gc, inv = random_layer(rank=100, n_comp=1000, seed=5)
     q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(2)).half()
     pos_q = 4 + 1000 + 64 - 1
     want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
     for ns in (8, 16, 64, 200):
-        got = _run(cuda, gc, inv, q, pos_q, n_splits=ns)
+        got = _run(cuda, gc, inv, q, pos_q, n_splits=ns, kernel=kernel)
         err, cos = compare(got, want)
         assert err <= TOL_ABS and cos >= TOL_COS, (ns, err, cos)
 
 
-def test_decode_additive_mask(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_decode_additive_mask(cuda, kernel):
     gc, inv = random_layer(n_comp=700, n_stream=4, seed=8)
     q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(3)).half()
     T = 4 + 700 + 64 + 4
@@ -98,19 +107,20 @@ def test_decode_additive_mask(cuda):
     mask[0, rng.choice(T, 50, replace=False)] = -65504.0   # HF fp16 masked entries
     mask[0, rng.choice(T, 50, replace=False)] = 0.5
     want = exact.decode_attention(q.numpy(), gc, 8, T - 1, inv.numpy(), attn_mask=mask)
-    got = _run(cuda, gc, inv, q, T - 1, mask=mask)
+    got = _run(cuda, gc, inv, q, T - 1, mask=mask, kernel=kernel)
     err, cos = compare(got, want)
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
-def test_decode_vs_reference_golden(cuda, golden):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_decode_vs_reference_golden(cuda, golden, kernel):
     """The reference's own CPU output on its stub cache (fp16 intermediates)."""
     from tests.test_oracle import _gc_from_fixture
     f = golden("fused_attn.npz")
     gc, nkv = _gc_from_fixture(f)
     gc["v_idx_full"] = gc["v_idx_full"].reshape(1, nkv, gc["n_compress"], 32)
     inv = torch.from_numpy(f["inv_freq"])
-    got = _run(cuda, gc, inv, torch.from_numpy(f["q_rope"]), int(f["pos_q"]), nkv=nkv)
+    got = _run(cuda, gc, inv, torch.from_numpy(f["q_rope"]), int(f["pos_q"]), nkv=nkv, kernel=kernel)
     want64 = exact.decode_attention(f["q_rope"], gc, nkv, int(f["pos_q"]), f["inv_freq"])
     err, cos = compare(got, want64)
     assert err <= TOL_ABS and cos >= TOL_COS
@@ -119,7 +129,8 @@ def test_decode_vs_reference_golden(cuda, golden):
     assert err_ref <= 5e-3 and cos_ref >= 0.9999
 
 
-def test_decode_compressed_real_synthetic(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_decode_compressed_real_synthetic(cuda, kernel):
     """Config-1 synthetic K/V compressed by the CPU oracle (PCA + DP bits + int4 +
     k-means VQ), then decoded on the GPU."""
     from shard_amd import bench_data
@@ -129,7 +140,7 @@ def test_decode_compressed_real_synthetic(cuda):
     gc = ref.compress_layer(k, v, 0, inv, basis=basis)
     q = bench_data.make_q(seed=0)
     want = exact.decode_attention(q.numpy(), gc, 8, 2048, inv.numpy())
-    got = _run(cuda, gc, inv, q, 2048)
+    got = _run(cuda, gc, inv, q, 2048, kernel=kernel)
     err, cos = compare(got, want)
     print(f"synthetic T=2048: max_abs={err:.3e} cos={cos:.7f}")
     assert err <= TOL_ABS and cos >= TOL_COS
@@ -151,7 +162,8 @@ def test_kv_reconstruct(cuda):
     assert float((diff > 0).float().mean()) < 0.02
 
 
-def test_decode_device_position_matches_host_position(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_decode_device_position_matches_host_position(cuda, kernel):
     """pos_q read by the kernel from a device int64 (the patched forward passes
     cache_position[-1:] instead of the reference's .item(), attention.py:383)
     gives the same bits as the host integer, also with a position that is not
@@ -159,8 +171,9 @@ def test_decode_device_position_matches_host_position(cuda):
     gc, inv = random_layer(B=2, n_comp=700, n_stream=4, seed=11)
     q = torch.randn(2, 32, 1, 128, generator=torch.Generator().manual_seed(5)).half()
     for pos_q in (4 + 700 + 64 + 4 - 1, 5000):
-        host = _run(cuda, gc, inv, q, pos_q)
-        dev = _run(cuda, gc, inv, q, torch.tensor([pos_q - 3, pos_q], dtype=torch.int64, device=cuda))
+        host = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
+        dev = _run(cuda, gc, inv, q, torch.tensor([pos_q - 3, pos_q], dtype=torch.int64, device=cuda),
+                   kernel=kernel)
         print(f"pos_q={pos_q} max diff={np.abs(host - dev).max():.3e}", flush=True)
         assert np.array_equal(host, dev)
         want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
