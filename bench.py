@@ -48,6 +48,8 @@ def algorithmic_flops(n_comp, rank, n_kv=8, hd=128, n_q=32):
 def clone_format(fmt):
     out = {}
     for k, v in fmt.items():
+        if k == "_decode_call":  # points at fmt's own tensors
+            continue
         out[k] = v.clone() if torch.is_tensor(v) else v
     return out
 

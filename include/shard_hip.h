@@ -164,6 +164,16 @@ int shard_stream_quant_qjl(const uint16_t* x, int64_t rows, int32_t hd,
                            uint8_t* idx, uint16_t* norm, uint8_t* qsign, uint16_t* qscale,
                            uint16_t* deq, void* stream);
 
+/* One decode token's K and V in one launch: shard_stream_quant_qjl on k and on
+ * v (rows each), with the same signs and codebook, as _stream_append quantizes
+ * both per token (cache.py:207-215).  The QJL outputs are nullable in pairs. */
+int shard_stream_quant_kv(const uint16_t* k, const uint16_t* v, int64_t rows, int32_t hd,
+                          const float* signs, const float* codebook, int32_t n_codes,
+                          uint8_t* k_idx, uint16_t* k_norm, uint16_t* k_deq,
+                          uint8_t* v_idx, uint16_t* v_norm, uint16_t* v_deq,
+                          uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
+                          uint16_t* v_qscale, void* stream);
+
 /* shard_stream_dequant with the QJL residual term (streaming.py:76-77):
  * codebook[idx] + (2 qsign - 1) * qscale before the inverse Hadamard.
  * qsign (rows, hd) uint8 and qscale (rows) fp16 both null or both set. */

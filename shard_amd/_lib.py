@@ -69,6 +69,7 @@ SIGNATURES = [
     ("shard_kv_reconstruct", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_void_p, c_void_p]),
     ("shard_stream_dequant", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_stream_quant_qjl", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("shard_stream_quant_kv", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32] + [c_void_p] * 10 + [c_void_p]),
     ("shard_stream_dequant_qjl", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
 ]
 

@@ -55,11 +55,17 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
         mask = attn_mask.reshape(B, -1)[:, -(gc["sink_k"].shape[2] + gc["n_compress"] +
                                           gc["win_k"].shape[2] + stream_n +
                                           (dec[0].shape[2] if dec else 0)):]
-    call = ops.make_decode_args(q, gc, pos_q, inv, mask=mask,
-                                n_splits=getattr(c, "_n_splits", 0),
-                                stream_n=stream_n, decode_kv=dec)
-    ws = _workspace(q.device, ops.decode_workspace_bytes(call))
+    n_splits = getattr(c, "_n_splits", 0)
+    call = gc.get("_decode_call")
+    if call is None or call.args.batch != B or call.args.n_q_heads != n_q:
+        call = ops.make_decode_args(q, gc, pos_q, inv, mask=mask, n_splits=n_splits,
+                                    stream_n=stream_n, decode_kv=dec)
+        gc["_decode_call"] = call  # the layer's argument block, refreshed per step
+    else:
+        call.refresh(q, gc, pos_q, inv, mask, n_splits, None, stream_n, dec)
+    ws = _workspace(q.device, call.workspace_bytes())
     out = ops.decode_attn(call, ws)
+    call.step = []  # drop this step's tensors (the output is returned)
     return out.view(B, n_q, 1, hd).to(q_rope.dtype)
 
 

@@ -25,6 +25,23 @@ def _nb(t):
     return t.nelement() * t.element_size()
 
 
+# Stream buffers (cap, ...) of a layer: 8-bit codes and the fp16 rows the
+# reference's dequantization yields (cache.py:275-278; written once per token,
+# read by the decode kernel), fp16 norms; with _stream_qjl the residual signs
+# and scales (cache.py:234-240).
+_STREAM_BUFS = ("k_idx_buf", "v_idx_buf", "k_norm_buf", "v_norm_buf", "k_deq_buf", "v_deq_buf")
+_STREAM_BUFS_QJL = _STREAM_BUFS + ("k_qsign_buf", "v_qsign_buf", "k_qscale_buf", "v_qscale_buf")
+
+
+def _stream_buf_shape(name, B, G, D):
+    """(per-token shape, dtype) of stream buffer ``name``."""
+    if name.endswith("_idx_buf") or name.endswith("_qsign_buf"):
+        return (B, G, D), torch.uint8
+    if name.endswith("_deq_buf"):
+        return (B, G, D), torch.float16
+    return (B, G), torch.float16  # norms, QJL scales
+
+
 class CacheLayer(CacheLayerMixin):
     """One layer's cache (cache.py:64-292)."""
 
@@ -166,44 +183,35 @@ class CacheLayer(CacheLayerMixin):
             gc["stream_codebook"] = host.lloyd_max_codebook(D, bits).to(dev)
             gc["stream_bits"] = bits
         s = gc.get("stream_n", 0) // B
-        needed = s + 1
-
-        def _ensure(key, shape, dtype):
-            buf_key = f"{key}_buf"
-            buf = gc.get(buf_key)
-            if buf is not None and buf.shape[0] >= needed:
-                return buf
-            cap = max(needed, 16 if buf is None else buf.shape[0] * 2)
-            new = torch.empty((cap, *shape), device=dev, dtype=dtype)
-            if buf is not None:
-                new[:buf.shape[0]].copy_(buf)
-            gc[buf_key] = new
-            return new
-
-        kib = _ensure("k_idx", (B, G, D), torch.uint8)
-        vib = _ensure("v_idx", (B, G, D), torch.uint8)
-        knb = _ensure("k_norm", (B, G), torch.float16)
-        vnb = _ensure("v_norm", (B, G), torch.float16)
-        # fp16 tokens as the reference dequantizes them (cache.py:275-278), written
-        # once at append time and read by the decode kernel (runtime scratch)
-        kdb = _ensure("k_deq", (B, G, D), torch.float16)
-        vdb = _ensure("v_deq", (B, G, D), torch.float16)
-        kqs = vqs = kqc = vqc = None
-        if qjl:  # 1-bit residual signs and per-token scale (cache.py:234-240)
-            kqs = _ensure("k_qsign", (B, G, D), torch.uint8)[s]
-            vqs = _ensure("v_qsign", (B, G, D), torch.uint8)[s]
-            kqc = _ensure("k_qscale", (B, G), torch.float16)[s]
-            vqc = _ensure("v_qscale", (B, G), torch.float16)[s]
+        names = _STREAM_BUFS_QJL if qjl else _STREAM_BUFS
+        if gc.get("_stream_cap", 0) <= s or (qjl and "k_qsign_buf" not in gc):
+            # grow every buffer by doubling (cache.py:220-230), keeping the rows
+            cap = max(s + 1, 16 if gc.get("_stream_cap", 0) == 0 else 2 * gc["_stream_cap"])
+            for name in names:
+                per_token, dtype = _stream_buf_shape(name, B, G, D)
+                buf = gc.get(name)
+                new = torch.empty((cap, *per_token), device=dev, dtype=dtype)
+                if buf is not None:
+                    new[:buf.shape[0]].copy_(buf)
+                gc[name] = new
+            gc["_stream_cap"] = cap
         kx = k.reshape(B, G, D)
         vx = v.reshape(B, G, D)
         if not kx.is_contiguous():
             kx = kx.contiguous()
         if not vx.is_contiguous():
             vx = vx.contiguous()
-        ops.stream_quant_into(kx, gc["signs"], gc["stream_codebook"], kib[s], knb[s], kdb[s],
-                              kqs, kqc)
-        ops.stream_quant_into(vx, gc["signs"], gc["stream_codebook"], vib[s], vnb[s], vdb[s],
-                              vqs, vqc)
+        # row s of each buffer, by address: codes and fp16 rows hold B G D
+        # entries per token, norms and QJL scales B G (fp16)
+        rows = B * G
+        p8, p16, n16 = s * rows * D, 2 * s * rows * D, 2 * s * rows
+        a = lambda name, off: gc[name].data_ptr() + off
+        qjl_ptrs = ((a("k_qsign_buf", p8), a("k_qscale_buf", n16), a("v_qsign_buf", p8),
+                     a("v_qscale_buf", n16)) if qjl else (None, None, None, None))
+        ops.stream_quant_kv_at(kx, vx, gc["signs"], gc["stream_codebook"],
+                               a("k_idx_buf", p8), a("k_norm_buf", n16), a("k_deq_buf", p16),
+                               a("v_idx_buf", p8), a("v_norm_buf", n16), a("v_deq_buf", p16),
+                               *qjl_ptrs)
         gc["stream_n"] = gc.get("stream_n", 0) + B
 
     def _dequant_stream(self, gc, B, nkv=None, hd=None):

@@ -778,13 +778,29 @@ __global__ void k_km_zero(uint32_t* p) { *p = 0u; }
 // Per-token 8-bit Lloyd-Max stream quantizer (cache.py:207-215, streaming.py:59-72)
 // one wave per row, E = hd/64 elements per lane.
 // ---------------------------------------------------------------------------
+// Input and outputs of one tensor; blockIdx.y picks one of two (a token's K
+// and V quantized by one launch).
+struct StreamIO {
+  const uint16_t* x[2];
+  uint8_t* idx[2];
+  uint16_t* norm[2];
+  uint8_t* qsign[2];
+  uint16_t* qscale[2];
+  uint16_t* deq[2];
+};
+
 template <int E>
-__global__ void k_stream_quant(const uint16_t* __restrict__ x, int64_t rows,
+__global__ void k_stream_quant(const StreamIO io, int64_t rows,
                                const float* __restrict__ signs, const float* __restrict__ cb_g,
-                               int n_codes, uint8_t* __restrict__ idx,
-                               uint16_t* __restrict__ norm, uint8_t* __restrict__ qsign,
-                               uint16_t* __restrict__ qscale, uint16_t* __restrict__ deq) {
+                               int n_codes) {
   constexpr int D = 64 * E;
+  const int job = blockIdx.y;
+  const uint16_t* __restrict__ x = io.x[job];
+  uint8_t* __restrict__ idx = io.idx[job];
+  uint16_t* __restrict__ norm = io.norm[job];
+  uint8_t* __restrict__ qsign = io.qsign[job];
+  uint16_t* __restrict__ qscale = io.qscale[job];
+  uint16_t* __restrict__ deq = io.deq[job];
   __shared__ float cb[256];
   for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
   __syncthreads();
@@ -1114,22 +1130,44 @@ int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx
   return SHARD_OK;
 }
 
-int shard_stream_quant_qjl(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,
-                           const float* codebook, int32_t n_codes, uint8_t* idx, uint16_t* norm,
-                           uint8_t* qsign, uint16_t* qscale, uint16_t* deq, void* stream) {
-  if (!x || !signs || !codebook || !idx || !norm || rows <= 0 || n_codes <= 0) return SHARD_ERR_ARG;
-  if ((qsign == nullptr) != (qscale == nullptr)) return SHARD_ERR_ARG;
+static int stream_quant_launch(const StreamIO& io, int jobs, int64_t rows, int32_t hd,
+                               const float* signs, const float* codebook, int32_t n_codes,
+                               void* stream) {
+  if (!signs || !codebook || rows <= 0 || n_codes <= 0) return SHARD_ERR_ARG;
+  for (int j = 0; j < jobs; ++j) {
+    if (!io.x[j] || !io.idx[j] || !io.norm[j]) return SHARD_ERR_ARG;
+    if ((io.qsign[j] == nullptr) != (io.qscale[j] == nullptr)) return SHARD_ERR_ARG;
+  }
   if (n_codes > 256) return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  unsigned blocks = (unsigned)((rows + 3) / 4);
+  const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)jobs);
   switch (hd) {
-    case 64: hipLaunchKernelGGL(k_stream_quant<1>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, qsign, qscale, deq); break;
-    case 128: hipLaunchKernelGGL(k_stream_quant<2>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, qsign, qscale, deq); break;
-    case 256: hipLaunchKernelGGL(k_stream_quant<4>, dim3(blocks), dim3(256), 0, s, x, rows, signs, codebook, n_codes, idx, norm, qsign, qscale, deq); break;
+    case 64: hipLaunchKernelGGL(k_stream_quant<1>, grid, dim3(256), 0, s, io, rows, signs, codebook, n_codes); break;
+    case 128: hipLaunchKernelGGL(k_stream_quant<2>, grid, dim3(256), 0, s, io, rows, signs, codebook, n_codes); break;
+    case 256: hipLaunchKernelGGL(k_stream_quant<4>, grid, dim3(256), 0, s, io, rows, signs, codebook, n_codes); break;
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_stream_quant");
   return SHARD_OK;
+}
+
+int shard_stream_quant_qjl(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,
+                           const float* codebook, int32_t n_codes, uint8_t* idx, uint16_t* norm,
+                           uint8_t* qsign, uint16_t* qscale, uint16_t* deq, void* stream) {
+  const StreamIO io = {{x, nullptr}, {idx, nullptr}, {norm, nullptr},
+                       {qsign, nullptr}, {qscale, nullptr}, {deq, nullptr}};
+  return stream_quant_launch(io, 1, rows, hd, signs, codebook, n_codes, stream);
+}
+
+int shard_stream_quant_kv(const uint16_t* k, const uint16_t* v, int64_t rows, int32_t hd,
+                          const float* signs, const float* codebook, int32_t n_codes,
+                          uint8_t* k_idx, uint16_t* k_norm, uint16_t* k_deq,
+                          uint8_t* v_idx, uint16_t* v_norm, uint16_t* v_deq,
+                          uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
+                          uint16_t* v_qscale, void* stream) {
+  const StreamIO io = {{k, v}, {k_idx, v_idx}, {k_norm, v_norm},
+                       {k_qsign, v_qsign}, {k_qscale, v_qscale}, {k_deq, v_deq}};
+  return stream_quant_launch(io, 2, rows, hd, signs, codebook, n_codes, stream);
 }
 
 int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd, const float* signs,

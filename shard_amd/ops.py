@@ -245,6 +245,19 @@ def stream_quant_into(x, signs, codebook, idx_out, norm_out, deq_out=None, qsign
         _p(qsign_out), _p(qscale_out), _p(deq_out), _stream(x)))
 
 
+def stream_quant_kv_at(k, v, signs, codebook, k_idx, k_norm, k_deq, v_idx, v_norm, v_deq,
+                       k_qsign=None, k_qscale=None, v_qsign=None, v_qscale=None):
+    """One decode token's K and V (contiguous fp16 (..., D), same shape) quantized
+    by one launch into outputs given as device addresses (ints): the rows of the
+    cache's stream buffers (cache.py:207-215)."""
+    lib = _lib.load()
+    D = k.shape[-1]
+    _lib.check("shard_stream_quant_kv", lib.shard_stream_quant_kv(
+        k.data_ptr(), v.data_ptr(), k.numel() // D, D, signs.data_ptr(), codebook.data_ptr(),
+        codebook.numel(), k_idx, k_norm, k_deq, v_idx, v_norm, v_deq, k_qsign, k_qscale,
+        v_qsign, v_qscale, _stream(k)))
+
+
 def stream_dequant(idx: torch.Tensor, norm: torch.Tensor, signs: torch.Tensor,
                    codebook: torch.Tensor, qsign: torch.Tensor = None,
                    qscale: torch.Tensor = None) -> torch.Tensor:
@@ -268,11 +281,30 @@ def stream_dequant(idx: torch.Tensor, norm: torch.Tensor, signs: torch.Tensor,
 # decode attention
 # ---------------------------------------------------------------------------
 class DecodeCall:
-    """Holds the ctypes argument block and the tensors it points to."""
+    """The ctypes argument block of one layer's decode call and the tensors it
+    points to.  A layer keeps one and refreshes the per-step fields
+    (``refresh``), so a decode step sets a dozen fields instead of rebuilding
+    the block."""
 
-    def __init__(self, args: DecodeArgs, keep_alive: list):
+    def __init__(self, args: DecodeArgs, static: list):
         self.args = args
-        self.keep = keep_alive
+        self.static = static     # the layer format's tensors
+        self.step = []           # this step's q, out, mask, ... (set by refresh)
+        self.out = None
+        self._ws = {}            # workspace bytes by (n_splits, kernel, extra tokens present)
+
+    @property
+    def keep(self):
+        return self.static + self.step
+
+    def workspace_bytes(self) -> int:
+        a = self.args
+        key = (a.n_splits, a.kernel, a.n_sink + a.n_win + a.n_dec + a.n_stream > 0)
+        nb = self._ws.get(key)
+        if nb is None:
+            nb = int(_lib.load().shard_decode_attn_workspace(ctypes.byref(a)))
+            self._ws[key] = nb
+        return nb
 
 
 def decode_prepare(fmt) -> torch.Tensor:
@@ -301,22 +333,12 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
     B, H, D = q.shape
     if tuple(fmt["v_centroids_f16"].shape) != (256, 4):
         raise ValueError("decode kernel needs a (256, 4) VQ codebook")
-    if q.dtype != torch.float16 or not q.is_contiguous():
-        raise TypeError("q must be contiguous fp16 (B, H, D)")
-    keep = [q]
+    keep = []
     a = DecodeArgs()
     a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim = B, H, fmt["n_kv"], D
     a.rank, a.n_comp = fmt["rank_pad"], fmt["n_compress"]
-    if isinstance(pos_q, torch.Tensor):
-        if pos_q.dtype != torch.int64 or pos_q.device != q.device or pos_q.numel() < 1:
-            raise TypeError("a device pos_q must be a non-empty int64 tensor on q's device")
-        pos_t = pos_q.reshape(-1)[-1:]
-        a.compress_start, a.pos_q, a.pos_q_dev = fmt["compress_start"], 0, pos_t.data_ptr()
-        keep.append(pos_t)
-    else:
-        a.compress_start, a.pos_q = fmt["compress_start"], int(pos_q)
-    inv_freq = fmt["inv_freq_dev"] if inv_freq is None else inv_freq
-    for name, t in (("q", q), ("inv_freq", inv_freq), ("k_coeffs", fmt["k_coeffs_pad"]),
+    a.compress_start = fmt["compress_start"]
+    for name, t in (("inv_freq", fmt["inv_freq_dev"]), ("k_coeffs", fmt["k_coeffs_pad"]),
                     ("k_coeff_scale", fmt["k_coeff_scale_pad"]), ("k_basis", fmt["k_basis_pad"]),
                     ("k_mean", fmt["k_mean_f16"]), ("prep", fmt["decode_prep"]),
                     ("v_idx", fmt["v_indices"]),
@@ -327,15 +349,49 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
         keep.append(t)
     a.n_sink = fmt["sink_k"].shape[2]
     a.n_win = fmt["win_k"].shape[2]
+    call = DecodeCall(a, keep)
+    return call.refresh(q, fmt, pos_q, inv_freq, mask, n_splits, out, stream_n, decode_kv)
+
+
+def _decode_refresh(self, q, fmt, pos_q, inv_freq=None, mask=None, n_splits=0, out=None,
+                    stream_n=0, decode_kv=None):
+    """Point this call at one step's q, position, stream, decode tokens and mask
+    (the fields that change between decode steps; the layer's format pointers
+    stay).  Returns self; self.out is the (B, H, D) fp16 output tensor."""
+    _require_gpu(q)
+    if q.dtype != torch.float16 or not q.is_contiguous():
+        raise TypeError("q must be contiguous fp16 (B, H, D)")
+    a = self.args
+    B, H, D = q.shape
+    if (B, H, D) != (a.batch, a.n_q_heads, a.head_dim):
+        raise ValueError(f"q shape {(B, H, D)} does not match the call's {(a.batch, a.n_q_heads, a.head_dim)}")
+    step = [q]
+    a.q = q.data_ptr()
+    if isinstance(pos_q, torch.Tensor):
+        if pos_q.dtype != torch.int64 or pos_q.device != q.device or pos_q.numel() < 1:
+            raise TypeError("a device pos_q must be a non-empty int64 tensor on q's device")
+        pos_t = pos_q.reshape(-1)[-1:]
+        a.pos_q, a.pos_q_dev = 0, pos_t.data_ptr()
+        step.append(pos_t)
+    else:
+        a.pos_q, a.pos_q_dev = int(pos_q), None
+    inv = fmt["inv_freq_dev"] if inv_freq is None else inv_freq
+    a.inv_freq = inv.data_ptr()
+    step.append(inv)
     if decode_kv is not None:
         dk, dv = decode_kv
         a.dec_k, a.dec_v = dk.data_ptr(), dv.data_ptr()
         a.n_dec, a.dec_stride = dk.shape[2], dk.shape[2]
-        keep += [dk, dv]
+        step += [dk, dv]
+    else:
+        a.dec_k = a.dec_v = None
+        a.n_dec = a.dec_stride = 0
     if stream_n > 0:
         a.s_k, a.s_v = fmt["k_deq_buf"].data_ptr(), fmt["v_deq_buf"].data_ptr()
-        keep += [fmt["k_deq_buf"], fmt["v_deq_buf"]]
-        a.n_stream = stream_n
+        step += [fmt["k_deq_buf"], fmt["v_deq_buf"]]
+    else:
+        a.s_k = a.s_v = None
+    a.n_stream = stream_n
     if mask is not None:
         m = mask.reshape(B, -1)
         n_total = (a.n_sink + a.n_comp + a.n_win + a.n_dec + a.n_stream)
@@ -346,35 +402,42 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
         if m.stride(-1) != 1:
             m = m.contiguous()
         a.mask, a.mask_stride = m.data_ptr(), m.stride(0)
-        keep.append(m)
+        step.append(m)
+    else:
+        a.mask, a.mask_stride = None, 0
     if out is None:
         out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
     a.out = out.data_ptr()
-    keep.append(out)
+    step.append(out)
     a.n_splits = int(n_splits)
-    return DecodeCall(a, keep)
+    self.out = out
+    self.step = step
+    return self
+
+
+DecodeCall.refresh = _decode_refresh
 
 
 def decode_workspace(call: DecodeCall) -> torch.Tensor:
     """A decode workspace for ``call`` (zero-filled; reusable by later calls,
     one call at a time per buffer)."""
-    need = decode_workspace_bytes(call)
-    return torch.zeros(max(need, 16), dtype=torch.uint8, device=call.keep[0].device)
+    need = call.workspace_bytes()
+    return torch.zeros(max(need, 16), dtype=torch.uint8, device=call.out.device)
 
 
 def decode_attn(call: DecodeCall, ws: torch.Tensor = None) -> torch.Tensor:
+    """Run the decode call; returns its (B, H, D) fp16 output."""
     lib = _lib.load()
-    q = call.keep[0]
-    need = lib.shard_decode_attn_workspace(ctypes.byref(call.args))
+    need = call.workspace_bytes()
     if ws is None or ws.numel() < need:
         ws = decode_workspace(call)
     _lib.check("shard_decode_attn", lib.shard_decode_attn(
-        ctypes.byref(call.args), _p(ws), ws.numel(), _stream(q)))
-    return call.keep[-1]
+        ctypes.byref(call.args), ws.data_ptr(), ws.numel(), _stream(call.out)))
+    return call.out
 
 
 def decode_workspace_bytes(call: DecodeCall) -> int:
-    return int(_lib.load().shard_decode_attn_workspace(ctypes.byref(call.args)))
+    return call.workspace_bytes()
 
 
 def kv_reconstruct(fmt, batch: int):
