@@ -412,26 +412,27 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
         """Greedy decode of n tokens; with `forced` (batch, n) the inputs after
         `first` are those tokens, and each step's logits are compared with
         ref_logits[step] (top-1 agreement, cosine) or kept (ref_logits None)."""
-        nxt, toks, logits, agree, cos = first, [], [], [], []
+        nxt, toks, logits = first, [], []
         t0 = sync_time()
         with torch.no_grad():
             for i in range(n):
                 lg = model(nxt, past_key_values=cache, use_cache=True).logits[:, -1]
                 tok = lg.argmax(-1, keepdim=True)
                 toks.append(tok)
-                if forced is None:
-                    logits.append(lg.half())
-                    nxt = tok
-                else:
-                    ref = ref_logits[i].float()
-                    agree.append((tok[:, 0] == ref.argmax(-1)).float().mean())
-                    cos.append(torch.nn.functional.cosine_similarity(lg.float(), ref, dim=-1).mean())
-                    nxt = forced[:, i:i + 1]
+                logits.append(lg.half())  # both runs keep their logits (one copy per step)
+                nxt = tok if forced is None else forced[:, i:i + 1]
         t1 = sync_time()
         stats = None
-        if forced is not None:
+        if forced is not None:  # compared after the timed loop
+            agree, cos = [], []
+            with torch.no_grad():
+                for lg, ref in zip(logits, ref_logits):
+                    ref = ref.float()
+                    agree.append((lg.argmax(-1) == ref.argmax(-1)).float().mean())
+                    cos.append(torch.nn.functional.cosine_similarity(lg.float(), ref, dim=-1).mean())
             stats = {"teacher_forced_top1_agreement": round(torch.stack(agree).mean().item(), 4),
                      "teacher_forced_logit_cosine": round(torch.stack(cos).mean().item(), 5)}
+            logits = []
         return t1 - t0, torch.cat(toks, 1), logits, stats
 
     with torch.no_grad():                      # warm-up on a short prompt (kernels, allocator)
@@ -479,9 +480,11 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
         r["decode_s"] = round(dt, 3)
         r["tokens_per_s"] = round(batch * new_tokens / dt, 1)
         r["ms_per_step"] = round(dt / new_tokens * 1000.0, 3)
-        # the fp16 run's kept logits (alive during both decodes) are not part of
-        # either cache's footprint
+        # the kept logits are not part of either cache's footprint: the fp16 run's
+        # (alive during both decodes) and, in the shard run, its own (same size)
         kept = sum(x.numel() * x.element_size() for x in fp16_logits) / 1e9
+        if kind == "shard":
+            kept *= 2
         r["peak_decode_gb"] = round(torch.cuda.max_memory_allocated() / 1e9 - kept, 2)
         progress(f"{kind}: decode {r['decode_s']} s, {r['tokens_per_s']} tokens/s")
         res[kind] = r
@@ -613,6 +616,7 @@ def main():
         out["at_32k"] = {"us": round(r32["us"], 3), "us_hot": round(r32["us_hot"], 3),
                          "us_eager_python_launch": round(r32["us_eager"], 3),
                          "achieved_hbm_gbs": round(g32, 1), "frac": round(g32 / HBM_PEAK_GBS, 4),
+                         "traffic": read_traffic(32768),
                          "n_comp": r32["n_comp"], "rank": r32["rank"]}
     if not args.no_cpu:
         try:
