@@ -174,6 +174,28 @@ int shard_stream_quant_kv(const uint16_t* k, const uint16_t* v, int64_t rows, in
                           uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
                           uint16_t* v_qscale, void* stream);
 
+/* The decode step's front end for one layer, in one launch: RoPE of q and k
+ * exactly as transformers' apply_rotary_pos_emb computes it in fp16 (each
+ * product and the sum rounded to fp16), then the rotated k and v appended to
+ * the stream as shard_stream_quant_kv does.  Replaces the patched forward's
+ * apply_rotary_pos_emb + update(k, v) of a streaming layer
+ * (attention.py:376-381, cache.py:193-241).
+ *   q (B, n_q_heads, hd), k and v (B, n_kv_heads, hd): fp16; cos and sin fp16
+ *   rows of hd, batch row b at b * cos_stride (0: one row shared by the batch,
+ *   as transformers passes it when the positions are the same)
+ *   q_rope (B, n_q_heads, hd) fp16 out; the k_* / v_* outputs are the rows of
+ *   this token in the stream buffers (codes, norms, fp16 rows; QJL nullable).
+ * hd = 128 or 256. */
+int shard_rope_stream_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
+                             int32_t batch,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t hd,
+                             uint16_t* q_rope, const float* signs, const float* codebook,
+                             int32_t n_codes, uint8_t* k_idx, uint16_t* k_norm, uint16_t* k_deq,
+                             uint8_t* v_idx, uint16_t* v_norm, uint16_t* v_deq,
+                             uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
+                             uint16_t* v_qscale, void* stream);
+
 /* shard_stream_dequant with the QJL residual term (streaming.py:76-77):
  * codebook[idx] + (2 qsign - 1) * qscale before the inverse Hadamard.
  * qsign (rows, hd) uint8 and qscale (rows) fp16 both null or both set. */

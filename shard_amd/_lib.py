@@ -70,6 +70,7 @@ SIGNATURES = [
     ("shard_stream_dequant", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_stream_quant_qjl", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_stream_quant_kv", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32] + [c_void_p] * 10 + [c_void_p]),
+    ("shard_rope_stream_append", c_int32, [c_void_p] * 5 + [c_int64] + [c_int32] * 4 + [c_void_p] * 3 + [c_int32] + [c_void_p] * 10 + [c_void_p]),
     ("shard_stream_dequant_qjl", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
 ]
 

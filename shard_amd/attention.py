@@ -108,13 +108,20 @@ def enable_llama_fused_attention(model=None):
         k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         cos, sin = position_embeddings
-        q, k = apply_rotary_pos_emb(q, k, cos, sin)
-        past_key_values._fused_decode_update = True
-        try:
-            past_key_values.update(k, v, self.layer_idx,
-                                   {"sin": sin, "cos": cos, "cache_position": cache_position})
-        finally:
-            past_key_values._fused_decode_update = False
+        if (past_key_values._streaming and not getattr(past_key_values, "offloading", False)
+                and self.head_dim in (128, 256) and cos.shape[0] in (1, q.shape[0])
+                and all(t.dtype == torch.float16 for t in (q, k, v, cos, sin))):
+            # apply_rotary_pos_emb + update(k, v) of a streaming layer in one
+            # launch, with the same fp16 arithmetic (attention.py:376-381)
+            q = layer.fused_rope_append(q, k, v, cos, sin).unsqueeze(2)
+        else:
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            past_key_values._fused_decode_update = True
+            try:
+                past_key_values.update(k, v, self.layer_idx,
+                                       {"sin": sin, "cos": cos, "cache_position": cache_position})
+            finally:
+                past_key_values._fused_decode_update = False
         # the reference reads cache_position[-1].item() (attention.py:383); a
         # device int64 position goes to the kernel as a pointer instead, so the
         # step needs no host read-back

@@ -167,16 +167,15 @@ class CacheLayer(CacheLayerMixin):
         return self._keys, self._values
 
     # -- decode stream (cache.py:193-279) ----------------------------------
-    def _stream_append(self, k, v):
-        """Quantize one decode token (B, G, 1, D) of K and V into the 8-bit
-        stream buffers (growable, doubling, as cache.py:220-230)."""
+    def _stream_rows(self, B, G, D, dev):
+        """Device addresses of the next stream row of every buffer, growing the
+        buffers by doubling when full (cache.py:220-230).  Returns (codebook
+        tensors, k row pointers, v row pointers, QJL pointers)."""
         gc = self._gpu_compressed
         c = self._cache_ref
         bits, qjl = int(c._stream_bits), bool(c._stream_qjl)
         if not 1 <= bits <= 8:
             raise ValueError(f"_stream_bits must be in 1..8 (uint8 codes), got {bits}")
-        B, G, _, D = k.shape
-        dev = k.device
         if "signs" not in gc:
             gc["signs"] = host.stream_signs(self.layer_idx, D).to(dev)
         if gc.get("stream_bits") != bits:
@@ -185,7 +184,6 @@ class CacheLayer(CacheLayerMixin):
         s = gc.get("stream_n", 0) // B
         names = _STREAM_BUFS_QJL if qjl else _STREAM_BUFS
         if gc.get("_stream_cap", 0) <= s or (qjl and "k_qsign_buf" not in gc):
-            # grow every buffer by doubling (cache.py:220-230), keeping the rows
             cap = max(s + 1, 16 if gc.get("_stream_cap", 0) == 0 else 2 * gc["_stream_cap"])
             for name in names:
                 per_token, dtype = _stream_buf_shape(name, B, G, D)
@@ -195,24 +193,54 @@ class CacheLayer(CacheLayerMixin):
                     new[:buf.shape[0]].copy_(buf)
                 gc[name] = new
             gc["_stream_cap"] = cap
+        # row s of each buffer, by address: codes and fp16 rows hold B G D
+        # entries per token, norms and QJL scales B G (fp16)
+        rows = B * G
+        p8, p16, n16 = s * rows * D, 2 * s * rows * D, 2 * s * rows
+        a = lambda name, off: gc[name].data_ptr() + off
+        kp = (a("k_idx_buf", p8), a("k_norm_buf", n16), a("k_deq_buf", p16))
+        vp = (a("v_idx_buf", p8), a("v_norm_buf", n16), a("v_deq_buf", p16))
+        qp = ((a("k_qsign_buf", p8), a("k_qscale_buf", n16), a("v_qsign_buf", p8),
+               a("v_qscale_buf", n16)) if qjl else (None, None, None, None))
+        return (gc["signs"], gc["stream_codebook"]), kp, vp, qp
+
+    def _stream_append(self, k, v):
+        """Quantize one decode token (B, G, 1, D) of K and V into the 8-bit
+        stream buffers (growable, doubling, as cache.py:220-230)."""
+        gc = self._gpu_compressed
+        B, G, _, D = k.shape
+        cbs, kp, vp, qp = self._stream_rows(B, G, D, k.device)
         kx = k.reshape(B, G, D)
         vx = v.reshape(B, G, D)
         if not kx.is_contiguous():
             kx = kx.contiguous()
         if not vx.is_contiguous():
             vx = vx.contiguous()
-        # row s of each buffer, by address: codes and fp16 rows hold B G D
-        # entries per token, norms and QJL scales B G (fp16)
-        rows = B * G
-        p8, p16, n16 = s * rows * D, 2 * s * rows * D, 2 * s * rows
-        a = lambda name, off: gc[name].data_ptr() + off
-        qjl_ptrs = ((a("k_qsign_buf", p8), a("k_qscale_buf", n16), a("v_qsign_buf", p8),
-                     a("v_qscale_buf", n16)) if qjl else (None, None, None, None))
-        ops.stream_quant_kv_at(kx, vx, gc["signs"], gc["stream_codebook"],
-                               a("k_idx_buf", p8), a("k_norm_buf", n16), a("k_deq_buf", p16),
-                               a("v_idx_buf", p8), a("v_norm_buf", n16), a("v_deq_buf", p16),
-                               *qjl_ptrs)
+        ops.stream_quant_kv_at(kx, vx, *cbs, *kp, *vp, *qp)
         gc["stream_n"] = gc.get("stream_n", 0) + B
+
+    def fused_rope_append(self, q, k, v, cos, sin):
+        """One decode token of a streaming compressed layer: RoPE of q and k
+        (transformers' fp16 apply_rotary_pos_emb) and the rotated k and v
+        appended to the stream, in one launch - the patched forward's
+        apply_rotary_pos_emb + update (attention.py:376-381).  q (B, H, 1, D),
+        k and v (B, G, 1, D), cos and sin (B or 1, 1, D), all fp16 and contiguous
+        in memory; cos and sin may have batch 1 (positions shared by the
+        batch).  Returns q after RoPE as (B, H, D)."""
+        gc = self._gpu_compressed
+        B, H, _, D = q.shape
+        G = k.shape[1]
+        self._lazy_evict()
+        cbs, kp, vp, qp = self._stream_rows(B, G, D, q.device)
+        q_out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
+        c16 = lambda t, *shape: t.reshape(*shape).contiguous()
+        Bc = cos.shape[0]  # 1 when the batch shares its positions
+        ops.rope_stream_append_at(c16(q, B, H, D), c16(k, B, G, D), c16(v, B, G, D),
+                                  c16(cos, Bc, D), c16(sin, Bc, D), *cbs, q_out, *kp, *vp, *qp)
+        gc["stream_n"] = gc.get("stream_n", 0) + B
+        self._seq_len += 1
+        self._needs_decompress = True
+        return q_out
 
     def _dequant_stream(self, gc, B, nkv=None, hd=None):
         n = gc.get("stream_n", 0)

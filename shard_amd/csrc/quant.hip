@@ -789,31 +789,22 @@ struct StreamIO {
   uint16_t* deq[2];
 };
 
+// Quantize row r held by one wave (t = its fp16 values as fp32, lane l holds
+// elements l + 64 k) with the codebook cb (LDS); outputs at row r.
 template <int E>
-__global__ void k_stream_quant(const StreamIO io, int64_t rows,
-                               const float* __restrict__ signs, const float* __restrict__ cb_g,
-                               int n_codes) {
+__device__ __forceinline__ void stream_quant_row(float (&t)[E], int64_t r,
+                                                 const float* __restrict__ signs,
+                                                 const float* cb, int n_codes,
+                                                 uint8_t* __restrict__ idx,
+                                                 uint16_t* __restrict__ norm,
+                                                 uint8_t* __restrict__ qsign,
+                                                 uint16_t* __restrict__ qscale,
+                                                 uint16_t* __restrict__ deq) {
   constexpr int D = 64 * E;
-  const int job = blockIdx.y;
-  const uint16_t* __restrict__ x = io.x[job];
-  uint8_t* __restrict__ idx = io.idx[job];
-  uint16_t* __restrict__ norm = io.norm[job];
-  uint8_t* __restrict__ qsign = io.qsign[job];
-  uint16_t* __restrict__ qscale = io.qscale[job];
-  uint16_t* __restrict__ deq = io.deq[job];
-  __shared__ float cb[256];
-  for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
-  __syncthreads();
   const int l = (int)lane_id();
-  const int w = threadIdx.x >> 6;
-  int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + w;
-  if (r >= rows) return;  // no block-level barrier below this point
-  float t[E], sq[E], res[E];
+  float sq[E], res[E];
 #pragma unroll
-  for (int k = 0; k < E; ++k) {
-    t[k] = h2f(x[r * D + l + 64 * k]);
-    sq[k] = mul_rn(t[k], t[k]);  // exact: fp16-derived values square exactly in fp32
-  }
+  for (int k = 0; k < E; ++k) sq[k] = mul_rn(t[k], t[k]);  // exact: fp16-derived values square exactly in fp32
   // torch CPU fp32 norm: accumulator j (< 8) sums elements j, j+8, j+16, ... in
   // increasing order; the 8 accumulators are then added left to right.
   float acc = 0.f;
@@ -888,6 +879,88 @@ __global__ void k_stream_quant(const StreamIO io, int64_t rows,
     for (int k = 0; k < E; ++k)
       deq[r * D + l + 64 * k] = f2h_opaque(h2f(f2h(mul_sign(t[k], signs[l + 64 * k]))) * nf);
   }
+}
+
+template <int E>
+__global__ void k_stream_quant(const StreamIO io, int64_t rows,
+                               const float* __restrict__ signs, const float* __restrict__ cb_g,
+                               int n_codes) {
+  constexpr int D = 64 * E;
+  const int job = blockIdx.y;
+  __shared__ float cb[256];
+  for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
+  __syncthreads();
+  const int l = (int)lane_id();
+  const int w = threadIdx.x >> 6;
+  int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + w;
+  if (r >= rows) return;  // no block-level barrier below this point
+  const uint16_t* __restrict__ x = io.x[job];
+  float t[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) t[k] = h2f(x[r * D + l + 64 * k]);
+  stream_quant_row<E>(t, r, signs, cb, n_codes, io.idx[job], io.norm[job], io.qsign[job],
+                      io.qscale[job], io.deq[job]);
+}
+
+// ---------------------------------------------------------------------------
+// Decode-step front end: RoPE of q and k with transformers' fp16 arithmetic
+// (apply_rotary_pos_emb: q * cos + rotate_half(q) * sin, each product and the
+// sum rounded to fp16 as torch's half ops do), then the new token's k and v
+// quantized into the stream (as k_stream_quant).  One wave per row: rows
+// [0, B H) are q rows (-> q_out), the next B G rows k, the last B G rows v.
+// E >= 2 and even: the RoPE pair (d, d + D / 2) of element l + 64 k is element
+// l + 64 (k + E / 2) of the same lane.
+// ---------------------------------------------------------------------------
+template <int E>
+__device__ __forceinline__ void rope_row(float (&t)[E], const uint16_t* __restrict__ c,
+                                         const uint16_t* __restrict__ sn) {
+  const int l = (int)lane_id();
+  float o[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    const int d = l + 64 * k;
+    const float rot = k < E / 2 ? -t[k + E / 2] : t[k - E / 2];  // rotate_half
+    const float a = h2f(f2h(mul_rn(t[k], h2f(c[d]))));
+    const float b = h2f(f2h(mul_rn(rot, h2f(sn[d]))));
+    o[k] = h2f(f2h(add_rn(a, b)));
+  }
+#pragma unroll
+  for (int k = 0; k < E; ++k) t[k] = o[k];
+}
+
+template <int E>
+__global__ void k_rope_stream(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kx,
+                              const uint16_t* __restrict__ vx, const uint16_t* __restrict__ cosv,
+                              const uint16_t* __restrict__ sinv, int64_t cs_stride, int B,
+                              int H, int G, uint16_t* __restrict__ q_out, const StreamIO io,
+                              const float* __restrict__ signs, const float* __restrict__ cb_g,
+                              int n_codes) {
+  constexpr int D = 64 * E;
+  __shared__ float cb[256];
+  for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
+  __syncthreads();
+  const int l = (int)lane_id();
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t nq = (int64_t)B * H, nk = (int64_t)B * G;
+  if (r >= nq + 2 * nk) return;  // no block-level barrier below this point
+  float t[E];
+  if (r < nq) {
+    const int64_t b = r / H;
+#pragma unroll
+    for (int k = 0; k < E; ++k) t[k] = h2f(q[r * D + l + 64 * k]);
+    rope_row<E>(t, cosv + b * cs_stride, sinv + b * cs_stride);
+#pragma unroll
+    for (int k = 0; k < E; ++k) q_out[r * D + l + 64 * k] = f2h(t[k]);
+    return;
+  }
+  const int job = r < nq + nk ? 0 : 1;  // 0: k, 1: v
+  const int64_t rr = r - nq - job * nk;
+  const uint16_t* __restrict__ x = job == 0 ? kx : vx;
+#pragma unroll
+  for (int k = 0; k < E; ++k) t[k] = h2f(x[rr * D + l + 64 * k]);
+  if (job == 0) rope_row<E>(t, cosv + (rr / G) * cs_stride, sinv + (rr / G) * cs_stride);
+  stream_quant_row<E>(t, rr, signs, cb, n_codes, io.idx[job], io.norm[job], io.qsign[job],
+                      io.qscale[job], io.deq[job]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1157,6 +1230,37 @@ int shard_stream_quant_qjl(const uint16_t* x, int64_t rows, int32_t hd, const fl
   const StreamIO io = {{x, nullptr}, {idx, nullptr}, {norm, nullptr},
                        {qsign, nullptr}, {qscale, nullptr}, {deq, nullptr}};
   return stream_quant_launch(io, 1, rows, hd, signs, codebook, n_codes, stream);
+}
+
+int shard_rope_stream_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
+                             int32_t batch,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t hd,
+                             uint16_t* q_rope, const float* signs, const float* codebook,
+                             int32_t n_codes, uint8_t* k_idx, uint16_t* k_norm, uint16_t* k_deq,
+                             uint8_t* v_idx, uint16_t* v_norm, uint16_t* v_deq,
+                             uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
+                             uint16_t* v_qscale, void* stream) {
+  if (!q || !k || !v || !cos || !sin || !q_rope || !signs || !codebook || !k_idx || !k_norm ||
+      !v_idx || !v_norm)
+    return SHARD_ERR_ARG;
+  if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_codes <= 0) return SHARD_ERR_ARG;
+  if (cos_stride != 0 && cos_stride < hd) return SHARD_ERR_SHAPE;
+  if ((k_qsign == nullptr) != (k_qscale == nullptr) || (v_qsign == nullptr) != (v_qscale == nullptr))
+    return SHARD_ERR_ARG;
+  if (n_codes > 256) return SHARD_ERR_SHAPE;
+  const StreamIO io = {{k, v}, {k_idx, v_idx}, {k_norm, v_norm},
+                       {k_qsign, v_qsign}, {k_qscale, v_qscale}, {k_deq, v_deq}};
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t rows = (int64_t)batch * (n_q_heads + 2 * n_kv_heads);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  switch (hd) {
+    case 128: hipLaunchKernelGGL(k_rope_stream<2>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes); break;
+    case 256: hipLaunchKernelGGL(k_rope_stream<4>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes); break;
+    default: return SHARD_ERR_SHAPE;
+  }
+  SHARD_LAUNCH_CHECK("shard_rope_stream_append");
+  return SHARD_OK;
 }
 
 int shard_stream_quant_kv(const uint16_t* k, const uint16_t* v, int64_t rows, int32_t hd,

@@ -258,6 +258,28 @@ def stream_quant_kv_at(k, v, signs, codebook, k_idx, k_norm, k_deq, v_idx, v_nor
         v_qsign, v_qscale, _stream(k)))
 
 
+def rope_stream_append_at(q, k, v, cos, sin, signs, codebook, q_out, k_idx, k_norm, k_deq,
+                          v_idx, v_norm, v_deq, k_qsign=None, k_qscale=None, v_qsign=None,
+                          v_qscale=None):
+    """RoPE of q and k (transformers' fp16 arithmetic) and the rotated k and v
+    appended to the stream in one launch.  q (B, H, D), k and v (B, G, D):
+    contiguous fp16; cos and sin (B, D) or (1, D) (shared by the batch),
+    contiguous fp16; q_out (B, H, D) fp16; the stream outputs are device
+    addresses (ints) of this token's rows."""
+    lib = _lib.load()
+    B, H, D = q.shape
+    G = k.shape[1]
+    if cos.shape != sin.shape or cos.shape[-1] != D or cos.shape[0] not in (1, B):
+        raise ValueError(f"cos/sin {tuple(cos.shape)} do not fit q {tuple(q.shape)}")
+    cs_stride = 0 if cos.shape[0] == 1 else D
+    _lib.check("shard_rope_stream_append", lib.shard_rope_stream_append(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(), cs_stride,
+        B, H, G, D,
+        q_out.data_ptr(), signs.data_ptr(), codebook.data_ptr(), codebook.numel(),
+        k_idx, k_norm, k_deq, v_idx, v_norm, v_deq, k_qsign, k_qscale, v_qsign, v_qscale,
+        _stream(q)))
+
+
 def stream_dequant(idx: torch.Tensor, norm: torch.Tensor, signs: torch.Tensor,
                    codebook: torch.Tensor, qsign: torch.Tensor = None,
                    qscale: torch.Tensor = None) -> torch.Tensor:

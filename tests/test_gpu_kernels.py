@@ -258,3 +258,57 @@ def test_k_prepare(cuda):
     got = ops.k_prepare(k.to(cuda), start, n_comp, inv.to(cuda), mean.to(cuda)).cpu().float()
     # sin/cos may differ by an ulp from torch's CPU ones: allow one fp16 ulp
     assert float((got - want).abs().max()) <= 2e-3 * float(want.abs().max())
+
+
+@pytest.mark.parametrize("B,H,G,hd,bits,qjl,shared", [(16, 32, 8, 128, 8, False, True),
+                                                      (4, 32, 8, 128, 8, False, False),
+                                                      (2, 32, 8, 128, 4, True, False),
+                                                      (1, 8, 2, 256, 8, False, False)])
+def test_rope_stream_append_bitexact(cuda, B, H, G, hd, bits, qjl, shared):
+    """The decode-step front end (one launch) against its two reference steps:
+    transformers' apply_rotary_pos_emb on fp16 CPU tensors (the library routine
+    the reference's patched forward calls, attention.py:376) for q and k, then
+    the stream quantizer oracle on the rotated k and on v (cache.py:207-215).
+    shared: one cos/sin row for the whole batch, as the model passes it when
+    every sequence is at the same position."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    ops = _ops()
+    g = torch.Generator().manual_seed(B * 100 + hd + bits)
+    q = (torch.randn(B, H, 1, hd, generator=g) * 3).half()
+    k = (torch.randn(B, G, 1, hd, generator=g) * 3).half()
+    v = torch.randn(B, G, 1, hd, generator=g).half()
+    pos = torch.randint(0, 40000, (1 if shared else B, 1), generator=g)
+    inv = torch.as_tensor(ref.default_inv_freq(500000.0, hd), dtype=torch.float32)
+    freqs = pos[..., None].float() * inv[None, None, :]
+    emb = torch.cat([freqs, freqs], -1)
+    cos, sin = emb.cos().half(), emb.sin().half()          # (B, 1, hd), as the model passes them
+    q_ref, k_ref = apply_rotary_pos_emb(q, k, cos, sin)
+    cb = ref.lloyd_max_codebook(hd, bits)
+    signs = ref.stream_signs(3, hd)
+    wk = ref.quantize_stream_token(k_ref.reshape(B, G, hd).numpy(), signs, cb, qjl=qjl)
+    wv = ref.quantize_stream_token(v.reshape(B, G, hd).numpy(), signs, cb, qjl=qjl)
+
+    dev = lambda t: t.to(cuda).contiguous()
+    out = {n: torch.empty(B, G, hd, dtype=torch.uint8, device=cuda) for n in ("ki", "vi", "ks", "vs")}
+    out.update({n: torch.empty(B, G, dtype=torch.float16, device=cuda) for n in ("kn", "vn", "kc", "vc")})
+    out.update({n: torch.empty(B, G, hd, dtype=torch.float16, device=cuda) for n in ("kd", "vd")})
+    q_out = torch.empty(B, H, hd, dtype=torch.float16, device=cuda)
+    p = lambda n: out[n].data_ptr()
+    qj = (p("ks"), p("kc"), p("vs"), p("vc")) if qjl else (None, None, None, None)
+    ops.rope_stream_append_at(dev(q.reshape(B, H, hd)), dev(k.reshape(B, G, hd)),
+                              dev(v.reshape(B, G, hd)), dev(cos.reshape(-1, hd)),
+                              dev(sin.reshape(-1, hd)), dev(torch.from_numpy(signs)),
+                              dev(torch.from_numpy(cb)), q_out, p("ki"), p("kn"), p("kd"),
+                              p("vi"), p("vn"), p("vd"), *qj)
+    torch.cuda.synchronize()
+    _bits_eq(q_out.cpu().numpy(), q_ref.reshape(B, H, hd).numpy())
+    for want, (i, n, s, c, d) in ((wk, ("ki", "kn", "ks", "kc", "kd")),
+                                  (wv, ("vi", "vn", "vs", "vc", "vd"))):
+        assert np.array_equal(out[i].cpu().numpy(), want[0])
+        _bits_eq(out[n].cpu().numpy(), want[1])
+        if qjl:
+            assert np.array_equal(out[s].cpu().numpy(), want[2])
+            _bits_eq(out[c].cpu().numpy(), want[3])
+        want_y = ref.dequantize_stream_token(want[0], want[1], signs, cb,
+                                             *(want[2:4] if qjl else (None, None)))
+        _bits_eq(out[d].cpu().numpy(), want_y)
