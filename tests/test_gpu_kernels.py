@@ -312,3 +312,40 @@ def test_rope_stream_append_bitexact(cuda, B, H, G, hd, bits, qjl, shared):
         want_y = ref.dequantize_stream_token(want[0], want[1], signs, cb,
                                              *(want[2:4] if qjl else (None, None)))
         _bits_eq(out[d].cpu().numpy(), want_y)
+
+
+@pytest.mark.parametrize("bits,qjl", [(8, False), (3, True)])
+def test_stream_quant_kv_rows_bitexact(cuda, bits, qjl):
+    """One launch for a token's K and V (shard_stream_quant_kv) writing into row
+    s of (cap, B, G, D) buffers by address: the row equals the oracle's codes,
+    norms, QJL terms and fp16 rows, and the other rows are untouched."""
+    ops = _ops()
+    B, G, D, cap, s = 3, 8, 128, 5, 2
+    g = torch.Generator().manual_seed(bits)
+    k = (torch.randn(B, G, D, generator=g) * 2).half()
+    v = torch.randn(B, G, D, generator=g).half()
+    cb = ref.lloyd_max_codebook(D, bits)
+    signs = ref.stream_signs(7, D)
+    wk = ref.quantize_stream_token(k.numpy(), signs, cb, qjl=qjl)
+    wv = ref.quantize_stream_token(v.numpy(), signs, cb, qjl=qjl)
+    bufs = {n: torch.full((cap, B, G, D), 0x55, dtype=torch.uint8, device=cuda) for n in ("ki", "vi", "ks", "vs")}
+    bufs.update({n: torch.full((cap, B, G), 7.0, dtype=torch.float16, device=cuda) for n in ("kn", "vn", "kc", "vc")})
+    bufs.update({n: torch.full((cap, B, G, D), 7.0, dtype=torch.float16, device=cuda) for n in ("kd", "vd")})
+    row = lambda n: bufs[n][s].data_ptr()
+    qj = (row("ks"), row("kc"), row("vs"), row("vc")) if qjl else (None, None, None, None)
+    ops.stream_quant_kv_at(k.to(cuda), v.to(cuda), torch.from_numpy(signs).to(cuda),
+                           torch.from_numpy(cb).to(cuda), row("ki"), row("kn"), row("kd"),
+                           row("vi"), row("vn"), row("vd"), *qj)
+    torch.cuda.synchronize()
+    for want, (i, n, sg, c, d) in ((wk, ("ki", "kn", "ks", "kc", "kd")),
+                                   (wv, ("vi", "vn", "vs", "vc", "vd"))):
+        assert np.array_equal(bufs[i][s].cpu().numpy(), want[0])
+        _bits_eq(bufs[n][s].cpu().numpy(), want[1])
+        if qjl:
+            assert np.array_equal(bufs[sg][s].cpu().numpy(), want[2])
+            _bits_eq(bufs[c][s].cpu().numpy(), want[3])
+        want_y = ref.dequantize_stream_token(want[0], want[1], signs, cb,
+                                             *(want[2:4] if qjl else (None, None)))
+        _bits_eq(bufs[d][s].cpu().numpy(), want_y)
+        for other in (0, 1, 3, 4):  # rows other than s keep their fill
+            assert bool((bufs[i][other] == 0x55).all()) and bool((bufs[d][other] == 7.0).all())
