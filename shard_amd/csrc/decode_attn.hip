@@ -742,14 +742,99 @@ void k_decode_split(const SplitParams p) {
 // one rotation of the 4 query heads per tile (lane = pair).  phi0 of tile k of
 // the chunk is the chunk start's phase composed with the per-layer tables
 // (32 (k mod 32)) theta and (1024 (k / 32)) theta.
+// Extra tokens (sink, window, decode, stream; fp16 rows) of kv head g, batch
+// row b, processed by single waves with no workgroup barrier while the other
+// waves of the workgroup run compressed tiles.  A pass covers 32 tokens:
+// scores on MFMA (rows = the kGQA query heads, k = head dims, columns =
+// tokens), an online softmax per head in every lane, the numerators exchanged
+// through the wave's LDS slot, values lane-per-dim-pair.  XPass holds one
+// pass's operands, so a pass's loads can be issued well before its compute.
+struct XPass {
+  half8 Bk[8];       // keys of the pass's tokens, MFMA B operand
+  uint32_t vx[32];   // token t's value dims (2 lane, 2 lane + 1)
+  float madd;        // mask term of this lane's token
+  int x0;
+};
+
+__device__ __forceinline__ void xpass_load(const SplitParams& p, int g, int b, int x0, XPass& P) {
+  const int lane = (int)lane_id(), col = lane & 31, hh = lane >> 5;
+  const int xt = min(x0 + col, p.xs.n_x - 1);  // clamped: tokens past n_x are masked
+  int mpos;
+  const uint16_t* krow = extra_row(p.xs, p.B, p.G, p.n_comp, b, g, xt, false, &mpos);
+  const uint16_t* vrow = extra_row(p.xs, p.B, p.G, p.n_comp, b, g, xt, true, &mpos);
+#pragma unroll
+  for (int st = 0; st < 8; ++st) P.Bk[st] = __builtin_bit_cast(half8, *(const uint4*)(krow + 16 * st + 8 * hh));
+  P.madd = p.mask ? p.mask[(int64_t)b * p.mask_stride + mpos] * kLog2e : 0.f;
+  const uint64_t vb = (uint64_t)vrow;
+#pragma unroll
+  for (int t = 0; t < 32; ++t) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
+    P.vx[t] = *(const uint32_t*)((const uint16_t*)(((uint64_t)hi << 32) | lo) + 2 * lane);
+  }
+  P.x0 = x0;
+}
+
+// q rows of kv head g as the score MFMA's A operand (rows = query heads)
+__device__ __forceinline__ void xpass_q(const SplitParams& p, int g, int b, half8 (&Aq)[8]) {
+  const int lane = (int)lane_id(), col = lane & 31, hh = lane >> 5;
+  const uint16_t* qv = p.q + ((int64_t)b * p.H + g * kGQA + min(col, kGQA - 1)) * kHD + 8 * hh;
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const uint4 v4 = *(const uint4*)(qv + 16 * st);
+    Aq[st] = __builtin_bit_cast(half8, col < kGQA ? v4 : make_uint4(0u, 0u, 0u, 0u));
+  }
+}
+
+__device__ __forceinline__ void xpass_compute(const SplitParams& p, const XPass& P,
+                                              const half8 (&Aq)[8], float (&m_run)[kGQA],
+                                              float (&l_part)[kGQA], float2 (&acc)[kGQA],
+                                              float (*pw)[kGQA]) {
+  const int lane = (int)lane_id(), col = lane & 31, hh = lane >> 5;
+  const float sc = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
+  float16v sacc = {};
+#pragma unroll
+  for (int st = 0; st < 8; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[st], P.Bk[st], sacc, 0, 0, 0);
+  // lanes 0-31: sacc[h] = score of head h for token x0 + col
+  const bool ok = hh == 0 && P.x0 + col < p.xs.n_x;
+  float al[kGQA];
+#pragma unroll
+  for (int h = 0; h < kGQA; ++h) {
+    const float s = ok ? sacc[h] * sc + P.madd : -INFINITY;
+    const float m_new = fmaxf(m_run[h], wave64_reduce(s, OpMax()));
+    al[h] = m_new == -INFINITY ? 1.f : exp2f(m_run[h] - m_new);
+    const float pv = s == -INFINITY ? 0.f : exp2f(s - m_new);
+    l_part[h] = l_part[h] * al[h] + pv;
+    m_run[h] = m_new;
+    if (hh == 0) pw[col][h] = pv;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+  for (int h = 0; h < kGQA; ++h) {
+    acc[h].x *= al[h];
+    acc[h].y *= al[h];
+  }
+#pragma unroll
+  for (int t = 0; t < 32; ++t) {
+    const float4 pt = *(const float4*)&pw[t][0];
+    const half2v hv = __builtin_bit_cast(half2v, P.vx[t]);
+    const float v0 = (float)hv[0], v1 = (float)hv[1];
+    acc[0].x += pt.x * v0; acc[0].y += pt.x * v1;
+    acc[1].x += pt.y * v0; acc[1].y += pt.y * v1;
+    acc[2].x += pt.z * v0; acc[2].y += pt.z * v1;
+    acc[3].x += pt.w * v0; acc[3].y += pt.w * v1;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // pw is rewritten by the next pass
+}
+
 constexpr int kTokWaves = 8;
 constexpr int kTokThreads = 64 * kTokWaves;
+constexpr int kTokXWaves = 2;  // waves of the last split that take the extra tokens
 
 template <int KS>
 struct TokLds {
   union {
     uint4 A[4][KS + 1][64];        // basis operand image of the kv head
-    XtLds<kTokWaves> xt;           // extra tokens (run before the image is loaded)
     struct {                       // end-of-chunk merge (after the tile loop)
       float acc[kTokWaves][kGQA][kHD];
       float m[kTokWaves][kGQA];
@@ -761,6 +846,9 @@ struct TokLds {
   uint16_t qr[kTokWaves][5][2][64];    // per wave: R(-phi0) q_n in fp16, [head][a|b][k order]; head 4 = 0
   uint32_t pb[kTokWaves][kGQA][2][8];  // per wave: softmax numerators, fp16 token pairs
   uint32_t next_tile;                  // the chunk's next unclaimed tile
+  float xpw[kTokXWaves][32][kGQA];     // extras waves: softmax numerators of a pass
+  float xacc[kTokXWaves][kGQA][kHD];   // extras waves: value sums (plain basis)
+  float xm[kTokXWaves][kGQA], xl[kTokXWaves][kGQA];
 };
 
 // Position in the score MFMA's k order (16 rb + 8 hh + e) of pair i, where the
@@ -796,10 +884,21 @@ void k_decode_tok(const SplitParams p) {
     split = bid / HG;
   }
   const int b = blockIdx.y;
-
-  if (split == p.n_splits - 1 && p.xs.n_x > 0) {
-    decode_extras_tail<NW>(p, hg, b, L.u.xt);
-    __syncthreads();  // the image below overwrites the extras' LDS
+  // The last split's last n_xw waves take the extra tokens (pass j of 32
+  // tokens to extras wave j mod n_xw) while the others start on the compressed
+  // tiles; their first pass's loads go out now, under the set-up.  Then they
+  // join the tile queue.
+  const bool has_x = split == p.n_splits - 1 && p.xs.n_x > 0;
+  const int n_xp = has_x ? (p.xs.n_x + 31) / 32 : 0;
+  const int n_xw = n_xp < kTokXWaves ? n_xp : kTokXWaves;
+  const int xj = w - (NW - n_xw);  // this wave's extras index when >= 0
+  const bool xwave = xj >= 0;
+  const int first_claims = NW - n_xw;
+  XPass xp;
+  half8 xq[8];
+  if (xwave) {
+    xpass_q(p, hg, b, xq);
+    xpass_load(p, hg, b, 32 * xj, xp);
   }
 
   const int t_begin = split * p.chunk;
@@ -848,7 +947,7 @@ void k_decode_tok(const SplitParams p) {
   };
   uint32_t cwA[KS], cwB[KS];
   float2 fA2, fA1, fB2, fB1;
-  if (w < n_t) load_tile(w, cwA, fA2, fA1);
+  if (w < n_t && !xwave) load_tile(w, cwA, fA2, fA1);
 
   // every global load of the set-up goes out before the first LDS store, so
   // the cold misses overlap (one round trip instead of one per copy step)
@@ -911,7 +1010,7 @@ void k_decode_tok(const SplitParams p) {
   float bs_c, bs_s;
   sincosf((float)(p.cstart + t_begin) * th, &bs_s, &bs_c);
   const int kq = pair_k(lane);  // this lane's slot in the rotated-q rows
-  if (tid == 0) L.next_tile = NW;
+  if (tid == 0) L.next_tile = first_claims;
 
   // rc rows of this lane: pairs 16 rb + pr[i]
   int pr[8];
@@ -1063,6 +1162,31 @@ void k_decode_tok(const SplitParams p) {
     return (int)__builtin_amdgcn_readfirstlane(v);
   };
   int k = w;
+  if (xwave) {
+    float xm[kGQA], xl[kGQA];
+    float2 xa[kGQA];
+#pragma unroll
+    for (int h = 0; h < kGQA; ++h) {
+      xm[h] = -INFINITY;
+      xl[h] = 0.f;
+      xa[h] = make_float2(0.f, 0.f);
+    }
+    for (int pi = xj; pi < n_xp; pi += n_xw) {
+      if (pi != xj) xpass_load(p, hg, b, 32 * pi, xp);
+      xpass_compute(p, xp, xq, xm, xl, xa, L.xpw[xj]);
+    }
+#pragma unroll
+    for (int h = 0; h < kGQA; ++h) {
+      const float l = wave64_reduce(xl[h], OpAdd());
+      *(float2*)&L.xacc[xj][h][2 * lane] = xa[h];
+      if (lane == 0) {
+        L.xm[xj][h] = xm[h];
+        L.xl[xj][h] = l;
+      }
+    }
+    k = claim();
+    if (k < n_t) load_tile(k, cwA, fA2, fA1);
+  }
   while (k < n_t) {  // ping-pong: the claimed tile's loads fly during the current one
     const int kb = claim();
     if (kb < n_t) load_tile(kb, cwB, fB2, fB1);
@@ -1116,6 +1240,23 @@ void k_decode_tok(const SplitParams p) {
     if (d == 0) {
       p.ws_m[widx] = M;
       p.ws_l[widx] = l;
+    }
+    if (n_xw > 0) {  // the extras waves' states -> partial row n_splits (plain basis)
+      float Mx = -INFINITY;
+      for (int j = 0; j < n_xw; ++j) Mx = fmaxf(Mx, L.xm[j][h]);
+      float ax = 0.f, lx = 0.f;
+      for (int j = 0; j < n_xw; ++j) {
+        const float mj = L.xm[j][h];
+        const float wt = mj == -INFINITY ? 0.f : exp2f(mj - Mx);
+        ax += wt * L.xacc[j][h][d];
+        lx += wt * L.xl[j][h];
+      }
+      const int64_t xidx = ((int64_t)b * p.H + hg * NQ + h) * p.nsp + p.n_splits;
+      p.ws_acc[xidx * kHD + d] = ax;
+      if (d == 0) {
+        p.ws_m[xidx] = Mx;
+        p.ws_l[xidx] = lx;
+      }
     }
   }
 }
@@ -1264,11 +1405,15 @@ void k_decode_combine(const CombineParams p) {
 // 31.2 vs 32.8 us per call) but a longer set-up and one tile per wave at
 // batch 1 x 8K (19.2 vs 16.8 us), so it takes over from 16 head-tiles per CU.
 constexpr int64_t kTokMinHeadTiles = 16 * 256;
+constexpr int kTokMaxExtra = 256;
 inline bool use_tok(const shard_decode_args* a) {
   if (a->kernel == 2) return true;
   if (a->kernel == 1) return false;
   const int64_t tiles = (int64_t)((a->n_comp + kTile - 1) / kTile) * a->n_kv_heads * a->batch;
-  return tiles >= kTokMinHeadTiles;
+  // one wave of the token-tiled kernel takes the extra tokens, 32 per pass:
+  // longer extra spans (long 8-bit streams) go to the row-split kernel
+  const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
+  return tiles >= kTokMinHeadTiles && n_x <= kTokMaxExtra;
 }
 
 inline int choose_splits(const shard_decode_args* a) {
