@@ -100,19 +100,20 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
 // 8 packed nibbles (n0 in bits 0-3 ... n7 in bits 28-31) -> 8 fp16 values in
 // element order (n0, n4, n1, n5, n2, n6, n3, n7).  A nibble dropped into the
 // mantissa of 1024.0 (0x6400) reads as 1024 + n from bits 0-3 of a half and
-// as 1024 + 16 n from bits 4-7.  Elements 0, 1, 4, 5 (even nibbles) become the
-// exact integers n - 8 with one packed subtraction per pair; elements 2, 3, 6,
-// 7 (odd nibbles) stay 1024 + 16 n.  The basis operand carries 16 x the even
-// ranks' entries, and the mean k-step the constant that the odd ranks' 1152
-// offset leaves (k_decode_prepare), so the MFMA yields 16 K.  Seven VALU ops.
+// as 1024 + 16 n from bits 4-7, both exact.  The basis operand carries 16 x the
+// even ranks' entries (elements 0, 1, 4, 5) and 1 x the odd ranks' (2, 3, 6,
+// 7), so rank r contributes 16 A'(r) (n - 8) plus a constant:
+//   even: 16 A' (1024 + n) = 16 A' (n - 8) + 16512 A'
+//   odd:     A' (1024 + 16 n) = 16 A' (n - 8) + 1152 A'
+// and the mean k-step carries 16 mean minus those constants (k_decode_prepare),
+// so the MFMA yields 16 K.  Five VALU ops per 8 values.  The offsets put the
+// fp32 partial sums near 10^4 |A'|, whose rounding (about 1e-3 |A'|) stays
+// below the fp16 rounding of the rotated keys.
 __device__ __forceinline__ half8 nib8_to_mfma(uint32_t x) {
   const uint32_t x8 = x >> 8;
   const uint32_t m0 = 0x000F000Fu, m1 = 0x00F000F0u, magic = 0x64006400u;
-  const half2v k1032 = {(half_t)1032.f, (half_t)1032.f};
-  const half2v e0 = __builtin_bit_cast(half2v, bfi(m0, x, magic)) - k1032;
-  const half2v e2 = __builtin_bit_cast(half2v, bfi(m0, x8, magic)) - k1032;
-  const uint4 r = make_uint4(__builtin_bit_cast(uint32_t, e0), bfi(m1, x, magic),
-                             __builtin_bit_cast(uint32_t, e2), bfi(m1, x8, magic));
+  const uint4 r = make_uint4(bfi(m0, x, magic), bfi(m1, x, magic), bfi(m0, x8, magic),
+                             bfi(m1, x8, magic));
   return __builtin_bit_cast(half8, r);
 }
 
@@ -151,13 +152,12 @@ __device__ __forceinline__ void load_coef(const uint8_t* rowp, bool valid, uint3
 //   op   uint4 [G][4 P][KS+1][64 lanes]: the MFMA A operand of wave P of head g,
 //        k-steps 0..KS-1 = A'(r) = fp16(basis * coeff_scale) in the nibble order
 //        of the coefficient dwords, times 16 for even ranks r (see
-//        nib8_to_mfma); k-step KS = C = 16 mean - 1152 sum_{r odd} A'(r) as
-//        16 fp16 parts (paired with a constant-1 operand), which cancels the
-//        odd ranks' 1024 + 16 n encoding:
-//          16 sum_r A'(r)(n_r - 8) + 16 mean = C + sum_{r even} 16 A'(r)(n_r - 8)
+//        nib8_to_mfma); k-step KS = C = 16 mean - 16512 sum_{r even} A'(r)
+//        - 1152 sum_{r odd} A'(r) as 16 fp16 parts (paired with a constant-1
+//        operand), which cancels the 1024 offsets of the nibble encoding:
+//          16 sum_r A'(r)(n_r - 8) + 16 mean = C + sum_{r even} 16 A'(r)(1024 + n_r)
 //                                              + sum_{r odd} A'(r)(1024 + 16 n_r)
-//        The parts hold |C| up to about 9.8e5 (greedy split, 15 x 65504 + rest),
-//        far above real keys (|C| is a few thousand).
+//        The parts hold |C| up to about 9.8e5 (greedy split, 15 x 65504 + rest).
 //   rope float2 [32][64] = (cos, sin)(col * theta_i) for the token column inside
 //        a tile, then float2 [64] = (cos, sin)(32 * theta_i), the per-tile step,
 //        then the tile-offset tables of the token-tiled kernel: float2 [32][64] =
@@ -188,8 +188,9 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
         }
       } else {
         double c = 16.0 * (double)h2f(mean[row]);
-        for (int r = 1; r < rank; r += 2)
-          c -= 1152.0 * (double)(float)(half_t)(h2f(basis[(int64_t)row * rank + r]) * h2f(cs[r]));
+        for (int r = 0; r < rank; ++r)
+          c -= ((r & 1) ? 1152.0 : 16512.0) *
+               (double)(float)(half_t)(h2f(basis[(int64_t)row * rank + r]) * h2f(cs[r]));
         // greedy split into 16 fp16 parts (8 per lane half), largest first
         for (int part = 0; part < 16; ++part) {
           const double cl = c > 65504.0 ? 65504.0 : (c < -65504.0 ? -65504.0 : c);
