@@ -288,25 +288,32 @@ __global__ __launch_bounds__(256) void k_vq_rot(const uint16_t* __restrict__ v, 
       m[k] = 0.f;
       if constexpr (NORM) cs[k] = ch[b * d + E * l + k];
     }
+    // raw rows (E halves per lane) of a step; the next step's loads are issued
+    // before this step's transforms
+    auto load_rows = [&](int64_t tt, uint32_t (&u)[RS][(E + 1) / 2]) {
+#pragma unroll
+      for (int q = 0; q < RS; ++q) {
+        const uint16_t* p = src + (tt + q) * d + E * l;
+        if constexpr (E == 1) {
+          u[q][0] = tt + q < t1 ? p[0] : 0u;
+        } else if constexpr (E == 2) {
+          u[q][0] = tt + q < t1 ? *(const uint32_t*)p : 0u;
+        } else {
+          const uint2 v2 = tt + q < t1 ? *(const uint2*)p : make_uint2(0u, 0u);
+          u[q][0] = v2.x;
+          u[q][1] = v2.y;
+        }
+      }
+    };
+    uint32_t un[RS][(E + 1) / 2];
+    if (t0 < t1) load_rows(t0, un);
     for (int64_t t = t0; t < t1; t += RS) {
       float x[RS][E];
 #pragma unroll
-      for (int q = 0; q < RS; ++q) {
-        const uint16_t* p = src + (t + q) * d + E * l;
-        if constexpr (E == 1) {
-          x[q][0] = t + q < t1 ? h2f(p[0]) : 0.f;
-        } else if constexpr (E == 2) {
-          const uint32_t u = t + q < t1 ? *(const uint32_t*)p : 0u;
-          x[q][0] = h2f((uint16_t)u);
-          x[q][1] = h2f((uint16_t)(u >> 16));
-        } else {
-          const uint2 u = t + q < t1 ? *(const uint2*)p : make_uint2(0u, 0u);
-          x[q][0] = h2f((uint16_t)u.x);
-          x[q][1] = h2f((uint16_t)(u.x >> 16));
-          x[q][2] = h2f((uint16_t)u.y);
-          x[q][3] = h2f((uint16_t)(u.y >> 16));
-        }
-      }
+      for (int q = 0; q < RS; ++q)
+#pragma unroll
+        for (int k = 0; k < E; ++k) x[q][k] = h2f((uint16_t)(un[q][k >> 1] >> (16 * (k & 1))));
+      if (t + RS < t1) load_rows(t + RS, un);
 #pragma unroll
       for (int q = 0; q < RS; ++q) {
         if (t + q >= t1) break;  // wave-uniform
@@ -979,20 +986,36 @@ __global__ __launch_bounds__(256) void k_k_prepare(const uint16_t* __restrict__ 
   const int hd2 = hd >> 1, D = n_kv * hd;
   const int t = blockIdx.x, pos = start + t;
   const int flat = threadIdx.y * blockDim.x + threadIdx.x;
+  const int i0 = 4 * threadIdx.x;  // blockDim.x == hd / 8
+  // the first rows' loads go out before the phases are computed
+  const int nbg = batch * n_kv;
+  auto row_src = [&](int bg) {
+    const int b = bg / n_kv, g = bg - b * n_kv;
+    return k + (((int64_t)b * n_kv + g) * seq + pos) * hd;
+  };
+  uint2 lo_n = make_uint2(0u, 0u), hi_n = make_uint2(0u, 0u);
+  if (threadIdx.y < nbg) {
+    const uint16_t* src = row_src(threadIdx.y);
+    lo_n = *(const uint2*)(src + i0);
+    hi_n = *(const uint2*)(src + hd2 + i0);
+  }
   for (int i = flat; i < hd2; i += blockDim.x * blockDim.y) {
     float sn, cs;
     sincosf(mul_rn((float)pos, inv_freq[i]), &sn, &cs);
     ph[i] = make_float2(cs, sn);
   }
   __syncthreads();
-  const int i0 = 4 * threadIdx.x;  // blockDim.x == hd / 8
   float2 p[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) p[j] = ph[i0 + j];
-  for (int bg = threadIdx.y; bg < batch * n_kv; bg += blockDim.y) {
+  for (int bg = threadIdx.y; bg < nbg; bg += blockDim.y) {
     const int b = bg / n_kv, g = bg - b * n_kv;
-    const uint16_t* src = k + (((int64_t)b * n_kv + g) * seq + pos) * hd;
-    const uint2 lo4 = *(const uint2*)(src + i0), hi4 = *(const uint2*)(src + hd2 + i0);
+    const uint2 lo4 = lo_n, hi4 = hi_n;
+    if (bg + blockDim.y < nbg) {  // next row's loads before this row's math
+      const uint16_t* src = row_src(bg + blockDim.y);
+      lo_n = *(const uint2*)(src + i0);
+      hi_n = *(const uint2*)(src + hd2 + i0);
+    }
     const uint16_t lo[4] = {(uint16_t)lo4.x, (uint16_t)(lo4.x >> 16), (uint16_t)lo4.y,
                             (uint16_t)(lo4.y >> 16)};
     const uint16_t hi[4] = {(uint16_t)hi4.x, (uint16_t)(hi4.x >> 16), (uint16_t)hi4.y,
