@@ -93,10 +93,15 @@ def enable_llama_fused_attention(model=None):
                 past_key_values=None, cache_position=None, **kwargs):
         is_shard = isinstance(past_key_values, Cache)
         layer = past_key_values.layers[self.layer_idx] if is_shard else None
+        # the decode kernel's shapes: head_dim 128, 4 query heads per kv head;
+        # other models take the original forward (layer.keys/values rebuild
+        # fp16 K/V), as does every call the reference would not fuse
         fuse = (is_shard and layer is not None
                 and getattr(layer, "_gpu_compressed", None) is not None
                 and hidden_states.shape[1] == 1
-                and past_key_values._rope_inv_freq is not None)
+                and past_key_values._rope_inv_freq is not None
+                and self.head_dim == 128
+                and self.config.num_attention_heads == 4 * self.config.num_key_value_heads)
         if not fuse:
             if cache_position is not None:
                 kwargs["cache_position"] = cache_position
@@ -109,7 +114,7 @@ def enable_llama_fused_attention(model=None):
         v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         cos, sin = position_embeddings
         if (past_key_values._streaming and not getattr(past_key_values, "offloading", False)
-                and self.head_dim in (128, 256) and cos.shape[0] in (1, q.shape[0])
+                and cos.shape[0] in (1, q.shape[0])
                 and all(t.dtype == torch.float16 for t in (q, k, v, cos, sin))):
             # apply_rotary_pos_emb + update(k, v) of a streaming layer in one
             # launch, with the same fp16 arithmetic (attention.py:376-381)

@@ -60,8 +60,9 @@ def test_short_prompt_skips_compression():
 
 def _tiny_llama():
     from transformers import LlamaConfig, LlamaForCausalLM
-    cfg = LlamaConfig(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
-                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+    # the fused decode kernel's shapes: head_dim 128, 4 query heads per kv head
+    cfg = LlamaConfig(vocab_size=64, hidden_size=512, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=1, head_dim=128,
                       max_position_embeddings=256, rope_theta=500000.0)
     torch.manual_seed(0)
     return LlamaForCausalLM(cfg).eval()
@@ -126,3 +127,36 @@ def test_full_fused_error_is_counted_then_default_path_runs(monkeypatch):
     assert c._full_fused_attempts == 2 and c._full_fused_errors == 2
     assert "forced" in c._last_full_fused_error
     assert calls == [10, 10]
+
+
+def test_unsupported_shapes_take_the_original_forward(monkeypatch):
+    """A model outside the decode kernel's shapes (head_dim 16, 2 query heads per
+    kv head) decodes through the original forward on compressed layers, without
+    calling the fused path (which would raise on such shapes)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from shard_amd import attention, Cache, enable_llama_fused_attention
+    called = []
+    monkeypatch.setattr(attention, "fused_attention_compressed",
+                        lambda *a, **k: called.append(1) or None)
+    cfg = LlamaConfig(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                      max_position_embeddings=256, rope_theta=500000.0)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).eval()
+    enable_llama_fused_attention(model)
+    c = Cache.from_model(model)
+    for l in c.layers:
+        l._gpu_compressed = {"stub": True}
+        l._prefilled = True
+        l._seq_len = 10
+    c._compressed = True
+    seen = []
+
+    def upd(self, k, v, *a, **kw):  # the original forward's cache update
+        seen.append(self.layer_idx)
+        self._seq_len += 1
+        return k, v
+    monkeypatch.setattr(type(c.layers[0]), "update", upd)
+    with torch.no_grad():
+        model(torch.randint(0, 64, (1, 1)), past_key_values=c, use_cache=True)
+    assert called == [] and seen == [0, 1]
