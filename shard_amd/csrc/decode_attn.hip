@@ -89,6 +89,12 @@ struct SplitParams {
   float* ws_acc;
 };
 
+// 2^x for the online softmax, where x <= 0 (a difference from the running
+// maximum): the hardware v_exp_f32 alone.  exp2f adds a range reduction that
+// keeps full precision for results below 2^-126; such weights are below the
+// fp32 resolution of a sum that holds at least one weight of 1.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // (x & m) | (y & ~m) in one VALU op; the compiler would emit and + or for
 // literal masks (a three-operand op takes one literal at most).
 __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
@@ -343,11 +349,11 @@ __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const i
         mx = fmaxf(mx, s[k]);
       }
       const float m_new = fmaxf(m_run, wave64_reduce(mx, OpMax()));
-      const float al = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+      const float al = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
       float ps = 0.f;
 #pragma unroll
       for (int k = 0; k < XV; ++k) {
-        const float pk = s[k] == -INFINITY ? 0.f : exp2f(s[k] - m_new);
+        const float pk = s[k] == -INFINITY ? 0.f : fast_exp2(s[k] - m_new);
         ps += pk;
         xpw[lane + 64 * k][w] = pk;
       }
@@ -641,8 +647,8 @@ void k_decode_split(const SplitParams p) {
       }
       const float tmax = TT == 64 ? wave64_reduce(s, OpMax()) : half32_reduce(s, OpMax());
       const float m_new = fmaxf(m_run, tmax);
-      const float al = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
-      const float pv = (s == -INFINITY) ? 0.f : exp2f(s - m_new);
+      const float al = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
+      const float pv = (s == -INFINITY) ? 0.f : fast_exp2(s - m_new);
       l_part = l_part * al + pv;
       m_run = m_new;
       pp16[qr][tt] = (half_t)pv;
@@ -803,8 +809,8 @@ __device__ __forceinline__ void xpass_compute(const SplitParams& p, const XPass&
   for (int h = 0; h < kGQA; ++h) {
     const float s = ok ? sacc[h] * sc + P.madd : -INFINITY;
     const float m_new = fmaxf(m_run[h], wave64_reduce(s, OpMax()));
-    al[h] = m_new == -INFINITY ? 1.f : exp2f(m_run[h] - m_new);
-    const float pv = s == -INFINITY ? 0.f : exp2f(s - m_new);
+    al[h] = m_new == -INFINITY ? 1.f : fast_exp2(m_run[h] - m_new);
+    const float pv = s == -INFINITY ? 0.f : fast_exp2(s - m_new);
     l_part[h] = l_part[h] * al[h] + pv;
     m_run[h] = m_new;
     if (hh == 0) pw[col][h] = pv;
@@ -1117,8 +1123,8 @@ void k_decode_tok(const SplitParams p) {
       for (int h = 0; h < NQ; ++h) {
         const float s = ok ? sacc[h] * sc + madd : -INFINITY;
         const float m_new = fmaxf(m_run[h], wave64_reduce(s, OpMax()));
-        al[h] = m_new == -INFINITY ? 1.f : exp2f(m_run[h] - m_new);
-        const float pv = s == -INFINITY ? 0.f : exp2f(s - m_new);
+        al[h] = m_new == -INFINITY ? 1.f : fast_exp2(m_run[h] - m_new);
+        const float pv = s == -INFINITY ? 0.f : fast_exp2(s - m_new);
         l_part[h] = l_part[h] * al[h] + pv;
         m_run[h] = m_new;
         if (hh == 0)
