@@ -262,11 +262,12 @@ __device__ __forceinline__ const uint16_t* extra_row(const ExtraSegs& s, int B, 
 //   ta = 0.47 + 0.64 N  tiles  of every N = ta + tb.
 // SHARD_SPLIT_BIAS=0 keeps even chunks.
 constexpr bool kSplitBias = SHARD_SPLIT_BIAS;
-// 32-token tiles a split workgroup processes side by side, one per group of 4
-// waves.  Two tiles (512 threads, one workgroup per CU, 2 waves per SIMD in
-// lockstep) rather than two 256-thread workgroups per CU: the older of two
-// co-resident workgroups gets issue priority and the younger then finishes
-// alone at 1 wave per SIMD, a tail that costs up to a quarter of the kernel.
+// 32-token tiles a row-split workgroup processes side by side, one per group of
+// 4 waves.  The default is 1: two 256-thread workgroups per CU, with the
+// unequal chunks above.  SHARD_DECODE_TG=2 builds one 512-thread workgroup per
+// CU working two tiles at once, which avoids the younger workgroup's tail but
+// runs the two waves of each SIMD in the same phase; it measured slower on
+// MI355X (19.2 vs 18.4 us at 8K) and is kept as a build option only.
 constexpr int kTG = SHARD_DECODE_TG;
 static_assert(kTG == 1 || kTG == 2, "SHARD_DECODE_TG must be 1 or 2");
 
