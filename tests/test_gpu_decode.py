@@ -146,6 +146,42 @@ def test_decode_compressed_real_synthetic(cuda, kernel):
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
+# The bench's 32K context at batch 1, and batch 16 with enough tiles per
+# workgroup that every wave of the token-tiled kernel walks the claim loop many
+# times (batch 16 x 16K itself takes the fp64 oracle too long for a test).
+LARGE = [(1, 32700, 0), (16, 4000, 8)]
+
+
+_large_cases = {}
+
+
+def _large_case(shape):
+    """Layer, query and fp64 oracle output of a LARGE shape (the oracle takes
+    10-15 s, so it runs once per shape for the three kernel choices)."""
+    if shape not in _large_cases:
+        B, n_comp, n_stream = shape
+        gc, inv = random_layer(B=B, n_comp=n_comp, n_stream=n_stream, seed=11)
+        g = torch.Generator().manual_seed(2)
+        q = torch.randn(B, 32, 1, 128, generator=g).half()
+        pos_q = 4 + n_comp + 64 + n_stream - 1
+        want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+        _large_cases.clear()
+        _large_cases[shape] = (gc, inv, q, pos_q, want)
+    return _large_cases[shape]
+
+
+@pytest.mark.parametrize("kernel", [0, 1, 2])
+@pytest.mark.parametrize("shape", LARGE, ids=[f"B{b}xn{n}+s{s}" for b, n, s in LARGE])
+def test_decode_large_contexts(cuda, shape, kernel):
+    B, n_comp, n_stream = shape
+    gc, inv, q, pos_q, want = _large_case(shape)
+    got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
+    err, cos = compare(got, want)
+    print(f"B={B} n_comp={n_comp} stream={n_stream} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}",
+          flush=True)
+    assert err <= TOL_ABS and cos >= TOL_COS
+
+
 def test_kv_reconstruct(cuda):
     """Unfused fp16 reconstruction (_ensure_dequant): V bit-exact, K within fp16 rounding."""
     from shard_amd import ops
