@@ -349,3 +349,36 @@ def test_stream_quant_kv_rows_bitexact(cuda, bits, qjl):
         _bits_eq(bufs[d][s].cpu().numpy(), want_y)
         for other in (0, 1, 3, 4):  # rows other than s keep their fill
             assert bool((bufs[i][other] == 0x55).all()) and bool((bufs[d][other] == 7.0).all())
+
+
+def test_prefill_kernels_at_config4_layer_size(cuda):
+    """One layer of BASELINE config 4 (batch 4 x 8192 tokens, 8 kv heads): the V
+    front end and the int4 chain bit-exact, the projection within fp32 summation
+    error, at the sizes whose multi-block reductions and grid-stride loops the
+    small cases above do not reach."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(4)
+    B, G, T, D = 4, 8, 8192, 128
+    v = torch.randn(B, G, T, D, generator=g).half()
+    v[:, :, :, 3] *= 8
+    x, ch32, _ = ops.vq_prepare(v.to(cuda).reshape(B * G, T, D))
+    rot = ref.hadamard(v.float().reshape(B * G, T, D))
+    ch = rot.abs().amax(dim=1).clamp(min=1e-8)
+    assert np.array_equal(ch32.cpu().numpy(), ch.numpy())
+    assert np.array_equal(x.cpu().numpy(), (rot / ch.unsqueeze(1)).reshape(-1, 4).numpy())
+    del x, rot
+
+    m, k, n = B * T, G * D, 192
+    a = (torch.randn(m, k, generator=g) * 0.5).half()
+    bt = (torch.randn(n, k, generator=g) * 0.03).half()
+    proj = ops.pca_project(a.to(cuda), bt.to(cuda))
+    want = a.double() @ bt.double().T
+    scale = a.double().abs() @ bt.double().abs().T
+    assert float(((proj.cpu().double() - want).abs() / scale).max()) < 1e-5
+
+    p32 = proj.cpu().numpy()
+    alloc = [4] * n
+    chain = ref.k_code_chain(p32, alloc)
+    got = ops.int4_quant_pack(proj, torch.tensor(alloc, dtype=torch.int32))
+    assert np.array_equal(got["packed"].cpu().numpy(), chain["packed"])
+    assert np.array_equal(got["coeff_scale"].cpu().numpy(), chain["coeff_scale"])
