@@ -225,8 +225,11 @@ int shard_stream_dequant_qjl(const uint8_t* idx, const uint16_t* norm, const uin
  *                reference's concatenation order [sink, comp, win, dec, stream]
  *                (nullable)
  *   out          (B, H, D) fp16
- * rank must be a multiple of 32 (<= 192); pad coefficients and basis with
- * zeros otherwise.  The softmax and all sums run in fp32.
+ * H / G (query heads per kv head) is 1, 2 or a multiple of 4 (<= 64).  rank
+ * must be a multiple of 32 (<= 192); pad coefficients and basis with zeros
+ * otherwise.  Any number of sink, window, decode and stream tokens (the
+ * reference appends without limit, cache.py:156-181).  The softmax and all
+ * sums run in fp32.
  * Replaces fused_attention_compressed (attention.py:270-343) with its
  * compressed_scores (18-81) and _v_weighted_sum_compressed (83-121), and the
  * flash-mixing of fused_attention_compressed_full (183-267). */
@@ -260,7 +263,8 @@ typedef struct shard_decode_args {
   uint16_t* out;
   int32_t n_splits; /* 0 = choose automatically */
   int32_t kernel;   /* split kernel: 0 = automatic, 1 = row-split (4 waves share a
-                     * tile), 2 = token-tiled (each wave owns whole tiles) */
+                     * tile; 4 query heads per kv head, <= 2048 extra tokens),
+                     * 2 = token-tiled (each wave owns whole tiles; every shape) */
   /* nullable device int64: when set, the kernel reads pos_q from it (the
    * reference's cache_position[-1], attention.py:383) and `pos_q` is ignored,
    * so the caller needs no host read-back of the position */
@@ -279,6 +283,15 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
                          int32_t head_dim, int32_t rank, void* out, size_t out_bytes,
                          void* stream);
 
+/* 1 when shard_decode_attn takes the shapes in `args` (head_dim 128, query
+ * heads per kv head 1, 2 or a multiple of 4, rank a multiple of 32 up to 192),
+ * else 0: the caller then rebuilds fp16 K/V (shard_kv_reconstruct) and runs
+ * plain attention, as the reference's unfused path does (attention.py:411). */
+int shard_decode_supported(const shard_decode_args* args);
+
+/* Workspace bytes of one call with these arguments (0: unsupported shape).
+ * The size depends on every count (batch, context, extra tokens, n_splits,
+ * kernel), so ask again whenever one changes. */
 size_t shard_decode_attn_workspace(const shard_decode_args* args);
 int shard_decode_attn(const shard_decode_args* args, void* workspace,
                       size_t workspace_bytes, void* stream);

@@ -432,13 +432,14 @@ def kmeans(data: torch.Tensor, k: int, n_iter: int = 30, seed: int = 42, assign=
     return centroids, idx
 
 
-def vq_encode(v: torch.Tensor, group_size: int, codebook_size: int):
-    """cache.py:41-52 (bits=8 packing is the identity, rope.py:164-165)."""
+def vq_encode(v: torch.Tensor, group_size: int, codebook_size: int, assign=None):
+    """cache.py:41-52 (bits=8 packing is the identity, rope.py:164-165).
+    ``assign`` is passed to kmeans (default: the CPU fallback's cdist)."""
     bh, seq, hd = v.shape
     ng = hd // group_size
     ch_max = v.abs().amax(dim=1).clamp(min=1e-8)
     flat = (v / ch_max.unsqueeze(1)).reshape(bh * seq, ng, group_size).reshape(-1, group_size)
-    centroids, idx = kmeans(flat.float(), codebook_size, n_iter=30)
+    centroids, idx = kmeans(flat.float(), codebook_size, n_iter=30, assign=assign)
     return {"centroids": centroids.half(), "idx": idx.to(torch.uint8),
             "ch_maxabs": ch_max.half(), "shape": (bh, seq, hd),
             "group_size": group_size, "flat": flat, "centroids_f32": centroids}
@@ -459,12 +460,15 @@ def vq_decode(qd) -> torch.Tensor:
 # --------------------------------------------------------------------------
 def compress_layer(k_full: torch.Tensor, v_full: torch.Tensor, layer_idx: int,
                    inv_freq, sink=4, win=64, k_target_cr=20.0, max_rank=192,
-                   group_size=4, codebook_size=256, basis=None):
+                   group_size=4, codebook_size=256, basis=None, assign=None):
     """One layer of Cache.compress (cache.py:338-366) + _compress_k (368-396) +
     _compress_v (398-404) + _build_gpu_format (406-454), on the CPU.
 
     ``basis`` (1024 x rank fp32, columns = components) may be supplied to
     bypass torch.svd_lowrank (its randomized result depends on the device RNG).
+    ``assign`` is k-means' nearest-centroid rule (default: the CPU fallback's
+    cdist argmin; the reference's GPU kernel sums squared differences directly,
+    vq_assign_direct).
     Returns the gc dict with numpy/torch CPU arrays and all integer
     intermediates (codes, q) for parity tests.
     """
@@ -503,7 +507,7 @@ def compress_layer(k_full: torch.Tensor, v_full: torch.Tensor, layer_idx: int,
 
     v_mid = v_full[:, :, start:end, :]
     v_flat = v_mid.float().reshape(B * nkv, n_comp, hd)
-    qd = vq_encode(hadamard(v_flat), group_size, codebook_size)
+    qd = vq_encode(hadamard(v_flat), group_size, codebook_size, assign=assign)
 
     k_scale_h = scale.half()
     gc = {

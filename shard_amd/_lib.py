@@ -64,6 +64,7 @@ SIGNATURES = [
     ("shard_stream_quant", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_decode_prepare_bytes", c_size_t, [c_int32, c_int32]),
     ("shard_decode_prepare", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
+    ("shard_decode_supported", c_int32, [ctypes.POINTER(DecodeArgs)]),
     ("shard_decode_attn_workspace", c_size_t, [ctypes.POINTER(DecodeArgs)]),
     ("shard_decode_attn", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
     ("shard_kv_reconstruct", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_void_p, c_void_p]),

@@ -39,6 +39,8 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
     B, n_q, s, hd = q_rope.shape
     if s != 1:
         return None
+    if not fused_supported(gc, n_q):
+        return None
     q = q_rope.reshape(B, n_q, hd)
     if q.dtype != torch.float16:
         q = q.to(torch.float16)
@@ -69,6 +71,13 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
     return out.view(B, n_q, 1, hd).to(q_rope.dtype)
 
 
+def fused_supported(gc, n_q: int) -> bool:
+    """Whether the fused kernel takes this compressed layer with n_q query heads."""
+    return (gc.get("decode_prep") is not None
+            and ops.decode_supported(gc.get("head_dim", 0), n_q, gc.get("n_kv", 0),
+                                     gc.get("rank_pad", 0)))
+
+
 def fused_attention_compressed_full(q_rope, layer, pos_q, inv_freq, attn_mask=None):
     """The reference's opt-in single-pass variant (attention.py:183-267).  The HIP
     kernel is already single-pass over every segment, so both entry points run it."""
@@ -93,15 +102,18 @@ def enable_llama_fused_attention(model=None):
                 past_key_values=None, cache_position=None, **kwargs):
         is_shard = isinstance(past_key_values, Cache)
         layer = past_key_values.layers[self.layer_idx] if is_shard else None
-        # the decode kernel's shapes: head_dim 128, 4 query heads per kv head;
-        # other models take the original forward (layer.keys/values rebuild
-        # fp16 K/V), as does every call the reference would not fuse
-        fuse = (is_shard and layer is not None
-                and getattr(layer, "_gpu_compressed", None) is not None
-                and hidden_states.shape[1] == 1
-                and past_key_values._rope_inv_freq is not None
-                and self.head_dim == 128
-                and self.config.num_attention_heads == 4 * self.config.num_key_value_heads)
+        gc = getattr(layer, "_gpu_compressed", None) if layer is not None else None
+        fuse = (gc is not None and hidden_states.shape[1] == 1
+                and past_key_values._rope_inv_freq is not None)
+        if fuse and not fused_supported(gc, self.config.num_attention_heads):
+            # a shape the fused kernel does not take (head_dim other than 128,
+            # query groups other than 1, 2 or 4k, rank above 192): the original
+            # forward runs on the rebuilt fp16 K/V (layer.keys / values); counted
+            past_key_values._fused_fallbacks = getattr(past_key_values, "_fused_fallbacks", 0) + 1
+            past_key_values._last_fused_fallback = (
+                f"head_dim={gc.get('head_dim')} n_q={self.config.num_attention_heads} "
+                f"n_kv={gc.get('n_kv')} rank={gc.get('rank_pad')}")
+            fuse = False
         if not fuse:
             if cache_position is not None:
                 kwargs["cache_position"] = cache_position

@@ -439,12 +439,14 @@ def pca_basis(centered: torch.Tensor, rank: int):
 
 
 def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li: int,
-                   basis=None) -> dict:
+                   basis=None, debug=None) -> dict:
     """Compress one layer's prefill K/V (B, G, T, D) fp16 into the device format.
 
     _compress_k (cache.py:368-396), _compress_v (398-404), _build_gpu_format
     (406-454).  The projection runs on the MFMA GEMM, the integer chain, the
     Hadamard/normalization, the k-means assignment and update in HIP kernels.
+    ``debug``: a dict that receives the fp32 projection ``proj`` (rows, keep)
+    and the bit allocation ``alloc`` (for parity tests).
     """
     B, G, seq, D = k_full.shape
     dev = k_full.device
@@ -495,6 +497,8 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     del centered
     bits = torch.tensor(alloc, dtype=torch.int32, device=dev)
     chain = ops.int4_quant_pack(proj, bits)
+    if debug is not None:
+        debug["proj"], debug["alloc"] = proj, list(alloc)
     del proj
 
     # ---- V: Hadamard -> channel max -> 4-dim subvectors -> k-means (256)
@@ -563,4 +567,7 @@ def finalize_format(gc: dict, inv_freq, dev):
     if inv_freq is None:
         inv_freq = torch.zeros(gc["head_dim"] // 2)
     gc["inv_freq_dev"] = inv_freq.to(dev, torch.float32).contiguous()
-    gc["decode_prep"] = ops.decode_prepare(gc)
+    # decode-kernel operands for the shapes the fused kernel takes; other layers
+    # decode through kv_reconstruct and the model's own attention
+    gc["decode_prep"] = (ops.decode_prepare(gc) if gc["head_dim"] == 128 and rank_pad <= 192
+                         else None)

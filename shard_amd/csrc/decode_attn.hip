@@ -32,6 +32,8 @@
 //   k_decode_combine  grid = (n_q, B): merges the partial rows, applies ch and
 //     ONE inverse Hadamard to the VQ part, adds the plain-basis part of the
 //     extra tokens, normalizes, writes fp16.
+#include <algorithm>
+
 #include "common.h"
 
 namespace shard {
@@ -81,6 +83,7 @@ struct SplitParams {
   const float2* rope;       // per-layer rotation tables (k_decode_prepare)
   const uint8_t* vidx;
   const uint16_t* vcb;
+  const uint16_t* vch;
   const float* mask;
   int64_t mask_stride;
   int32_t n_sink;
@@ -247,6 +250,33 @@ __device__ __forceinline__ const uint16_t* extra_row(const ExtraSegs& s, int B, 
   }
   *mpos = x < e1 ? x : x + n_comp;
   return base + row * kHD;
+}
+
+// One butterfly stage at element stride 2*HL = lane stride HL.
+template <int HL>
+__device__ __forceinline__ void fwht_lane_stage(float& x0, float& x1, int l) {
+  const float p0 = xor_lane<HL>(x0), p1 = xor_lane<HL>(x1);
+  x0 = (l & HL) ? p0 - x0 : x0 + p0;
+  x1 = (l & HL) ? p1 - x1 : x1 + p1;
+}
+
+// Butterflies over 128 values held as (2l, 2l+1) in lane l (Sylvester order).
+__device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
+  const int l = (int)lane_id();
+  {
+    const float a = x0, c = x1;
+    x0 = a + c;
+    x1 = a - c;
+  }
+  fwht_lane_stage<1>(x0, x1, l);
+  fwht_lane_stage<2>(x0, x1, l);
+  fwht_lane_stage<4>(x0, x1, l);
+  fwht_lane_stage<8>(x0, x1, l);
+  fwht_lane_stage<16>(x0, x1, l);
+  fwht_lane_stage<32>(x0, x1, l);
+  const float s = 0.08838834764831845f;  // 1/sqrt(128)
+  x0 *= s;
+  x1 *= s;
 }
 
 #ifndef SHARD_DECODE_TG
@@ -716,29 +746,45 @@ void k_decode_split(const SplitParams p) {
     for (int e = 0; e < 4; ++e) red[tid][4 * a + e] = vacc[a][e];
   __syncthreads();
   // thread (vG, i): value i = 4 a + e of dim group vG, summed over the TS subsets
+  __shared__ __align__(16) float racc[NQ][kHD];
   for (int i = tid >> 5; i < 16; i += NT / 32) {
     float s = red[vG][i];
 #pragma unroll
     for (int u = 1; u < TS; ++u) s += red[32 * u + vG][i];
-    const int qh = hg * NQ + (i >> 2);
-    p.ws_acc[(((int64_t)b * p.H + qh) * p.nsp + split) * kHD + 4 * vG + (i & 3)] = s;
+    racc[i >> 2][4 * vG + (i & 3)] = s;
+  }
+  __syncthreads();
+  // wave h < NQ: ch and one inverse FWHT of query head h, so the partial row is
+  // in the plain basis (the FWHT is linear and commutes with the merge)
+  if (wv < NQ) {
+    const uint32_t ch2 = *(const uint32_t*)(p.vch + ((int64_t)b * p.G + hg) * kHD + 2 * lane);
+    const half2v chh = __builtin_bit_cast(half2v, ch2);
+    const float2 rv = *(const float2*)&racc[wv][2 * lane];
+    float x0 = rv.x * (float)chh[0], x1 = rv.y * (float)chh[1];
+    fwht128_pairs(x0, x1);
+    const int qh = hg * NQ + wv;
+    *(float2*)(p.ws_acc + (((int64_t)b * p.H + qh) * p.nsp + split) * kHD + 2 * lane) = make_float2(x0, x1);
   }
 }
 
 // --------------------------------------------------------------------------
 // Token-tiled split kernel: each wave rebuilds all 128 rows of its own tiles.
 // --------------------------------------------------------------------------
-// One 512-thread workgroup (8 waves) per CU owns one kv head x a token chunk.
-// The head's basis operand image (4 row blocks x (KS + 1) k-steps, 52 KB at
-// rank 192) sits in LDS; the chunk's 32-token tiles are dealt to the waves in
-// turn (tile k to wave k % 8), and a wave works through its tiles with no
-// workgroup barrier: per tile it unpacks the coefficients once, runs the 4 x
-// (KS + 1) rebuild MFMAs with A from LDS, rotates, scores, and keeps its own
-// online softmax and VQ value sums.  The waves merge once, after the loop.
+// One 512-thread workgroup (8 waves, 2 per SIMD) per CU owns one kv head x a
+// range of tiles.  The head's basis operand image (4 row blocks x (KS + 1)
+// k-steps, 52 KB at rank 192) sits in LDS; the waves claim 32-token tiles
+// from an LDS counter and work through them with no workgroup barrier: per
+// tile a wave unpacks the coefficients once, runs the 4 x (KS + 1) rebuild
+// MFMAs with A from LDS, rotates, scores, and keeps its own online softmax and
+// VQ value sums.  The waves merge once, after the loop.
 //
-// Tiles go to the waves through an LDS counter: wave w starts with tile w and
-// claims its next one when it starts a tile (so the claim and the next tile's
-// loads are a tile ahead of their use); fast waves take more tiles.
+// Tiles: the split's compressed tiles first (claimed from one counter), then
+// its extra tiles (sink, window, decode and stream tokens as fp16 rows,
+// claimed from a second counter) with the same softmax state: scores against
+// q_rope on MFMA, values lane-per-dim-pair in the plain basis.  The host
+// spreads the extra tiles over the last splits (a compressed tile counts as 3
+// cost units, an extra tile as 1), so any number of extra tokens runs on many
+// workgroups.
 //
 // RoPE: undo-RoPE at pos_q followed by the relative rotation (pos_t - pos_q) of
 // the reference (attention.py:3-6, 74-79) is the rotation of q_rope by -pos_t
@@ -747,116 +793,59 @@ void k_decode_split(const SplitParams p) {
 // col theta: the in-tile part is a constant per lane (table rc, with the 1/16 of
 // the rebuilt keys folded in) and the tile part rotates q instead,
 //   q . R(phi0 + phic) k = (R(-phi0) q) . (R(phic) k),
-// one rotation of the 4 query heads per tile (lane = pair).  phi0 of tile k of
-// the chunk is the chunk start's phase composed with the per-layer tables
+// one rotation of the query heads per tile (lane = pair).  phi0 of tile k of
+// the split is its first token's phase composed with the per-layer tables
 // (32 (k mod 32)) theta and (1024 (k / 32)) theta.
-// Extra tokens (sink, window, decode, stream; fp16 rows) of kv head g, batch
-// row b, processed by single waves with no workgroup barrier while the other
-// waves of the workgroup run compressed tiles.  A pass covers 32 tokens:
-// scores on MFMA (rows = the kGQA query heads, k = head dims, columns =
-// tokens), an online softmax per head in every lane, the numerators exchanged
-// through the wave's LDS slot, values lane-per-dim-pair.  XPass holds one
-// pass's operands, so a pass's loads can be issued well before its compute.
-struct XPass {
-  half8 Bk[8];       // keys of the pass's tokens, MFMA B operand
-  uint32_t vx[32];   // token t's value dims (2 lane, 2 lane + 1)
-  float madd;        // mask term of this lane's token
-  int x0;
-};
-
-__device__ __forceinline__ void xpass_load(const SplitParams& p, int g, int b, int x0, XPass& P) {
-  const int lane = (int)lane_id(), col = lane & 31, hh = lane >> 5;
-  const int xt = min(x0 + col, p.xs.n_x - 1);  // clamped: tokens past n_x are masked
-  int mpos;
-  const uint16_t* krow = extra_row(p.xs, p.B, p.G, p.n_comp, b, g, xt, false, &mpos);
-  const uint16_t* vrow = extra_row(p.xs, p.B, p.G, p.n_comp, b, g, xt, true, &mpos);
-#pragma unroll
-  for (int st = 0; st < 8; ++st) P.Bk[st] = __builtin_bit_cast(half8, *(const uint4*)(krow + 16 * st + 8 * hh));
-  P.madd = p.mask ? p.mask[(int64_t)b * p.mask_stride + mpos] * kLog2e : 0.f;
-  const uint64_t vb = (uint64_t)vrow;
-#pragma unroll
-  for (int t = 0; t < 32; ++t) {
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
-    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
-    P.vx[t] = *(const uint32_t*)((const uint16_t*)(((uint64_t)hi << 32) | lo) + 2 * lane);
-  }
-  P.x0 = x0;
-}
-
-// q rows of kv head g as the score MFMA's A operand (rows = query heads)
-__device__ __forceinline__ void xpass_q(const SplitParams& p, int g, int b, half8 (&Aq)[8]) {
-  const int lane = (int)lane_id(), col = lane & 31, hh = lane >> 5;
-  const uint16_t* qv = p.q + ((int64_t)b * p.H + g * kGQA + min(col, kGQA - 1)) * kHD + 8 * hh;
-#pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    const uint4 v4 = *(const uint4*)(qv + 16 * st);
-    Aq[st] = __builtin_bit_cast(half8, col < kGQA ? v4 : make_uint4(0u, 0u, 0u, 0u));
-  }
-}
-
-__device__ __forceinline__ void xpass_compute(const SplitParams& p, const XPass& P,
-                                              const half8 (&Aq)[8], float (&m_run)[kGQA],
-                                              float (&l_part)[kGQA], float2 (&acc)[kGQA],
-                                              float (*pw)[kGQA]) {
-  const int lane = (int)lane_id(), col = lane & 31, hh = lane >> 5;
-  const float sc = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
-  float16v sacc = {};
-#pragma unroll
-  for (int st = 0; st < 8; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[st], P.Bk[st], sacc, 0, 0, 0);
-  // lanes 0-31: sacc[h] = score of head h for token x0 + col
-  const bool ok = hh == 0 && P.x0 + col < p.xs.n_x;
-  float al[kGQA];
-#pragma unroll
-  for (int h = 0; h < kGQA; ++h) {
-    const float s = ok ? sacc[h] * sc + P.madd : -INFINITY;
-    const float m_new = fmaxf(m_run[h], wave64_reduce(s, OpMax()));
-    al[h] = m_new == -INFINITY ? 1.f : fast_exp2(m_run[h] - m_new);
-    const float pv = s == -INFINITY ? 0.f : fast_exp2(s - m_new);
-    l_part[h] = l_part[h] * al[h] + pv;
-    m_run[h] = m_new;
-    if (hh == 0) pw[col][h] = pv;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-  for (int h = 0; h < kGQA; ++h) {
-    acc[h].x *= al[h];
-    acc[h].y *= al[h];
-  }
-#pragma unroll
-  for (int t = 0; t < 32; ++t) {
-    const float4 pt = *(const float4*)&pw[t][0];
-    const half2v hv = __builtin_bit_cast(half2v, P.vx[t]);
-    const float v0 = (float)hv[0], v1 = (float)hv[1];
-    acc[0].x += pt.x * v0; acc[0].y += pt.x * v1;
-    acc[1].x += pt.y * v0; acc[1].y += pt.y * v1;
-    acc[2].x += pt.z * v0; acc[2].y += pt.z * v1;
-    acc[3].x += pt.w * v0; acc[3].y += pt.w * v1;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // pw is rewritten by the next pass
-}
-
+//
+// Score layout (32x32 MFMA, rows = query heads): element i < 4 of lane half
+// hh holds head 4 hh + i of token col = lane % 32.
+//
+// Epilogue: the 8 waves' states merge in LDS; per query head the VQ part (in
+// the Hadamard-rotated basis) is scaled by ch and rotated back with one FWHT,
+// the extra tokens' part (plain basis) added, and one partial row (m, l,
+// acc[128]) written per (batch row, query head, split).  The FWHT is linear, so
+// it commutes with the log-sum-exp merge of k_decode_merge.
 constexpr int kTokWaves = 8;
 constexpr int kTokThreads = 64 * kTokWaves;
-constexpr int kTokXWaves = 2;  // waves of the last split that take the extra tokens
 
-template <int KS>
+struct TokParams {
+  int32_t B, H, G, QG, n_comp, cstart;  // QG: groups of NQ query heads per kv head
+  int32_t n_ct, n_xt;      // compressed tiles (32 tokens each) and extra tiles
+  int32_t n_splits, per_u; // splits per (batch row, kv head); cost units per split
+  ExtraSegs xs;
+  const uint16_t* q;
+  const float* inv_freq;
+  const uint8_t* coef;
+  const uint4* op;
+  const float2* rope;
+  const uint8_t* vidx;
+  const uint16_t* vcb;
+  const uint16_t* vch;
+  const float* mask;
+  int64_t mask_stride;
+  int32_t n_sink;
+  float* ws_m;
+  float* ws_l;
+  float* ws_acc;
+};
+
+template <int KS, int NQ>
 struct TokLds {
   union {
-    uint4 A[4][KS + 1][64];        // basis operand image of the kv head
-    struct {                       // end-of-chunk merge (after the tile loop)
-      float acc[kTokWaves][kGQA][kHD];
-      float m[kTokWaves][kGQA];
-      float l[kTokWaves][kGQA];
+    uint4 A[4][KS + 1][64];             // basis operand image of the kv head
+    struct {                            // end-of-split merge (after the tile loops)
+      float r[kTokWaves][NQ][kHD];      // value sums, rotated basis
+      float pl[kTokWaves][NQ][kHD];     // value sums, plain basis (extra tokens)
+      float m[kTokWaves][NQ];
+      float l[kTokWaves][NQ];
     } red;
   } u;
-  uint2 cb[256];                       // VQ codebook, 4 x fp16 per entry
-  float2 rc[64][32];                   // (cos, sin)(col theta_i) / 16, [pair][column]
-  uint16_t qr[kTokWaves][5][2][64];    // per wave: R(-phi0) q_n in fp16, [head][a|b][k order]; head 4 = 0
-  uint32_t pb[kTokWaves][kGQA][2][8];  // per wave: softmax numerators, fp16 token pairs
-  uint32_t next_tile;                  // the chunk's next unclaimed tile
-  float xpw[kTokXWaves][32][kGQA];     // extras waves: softmax numerators of a pass
-  float xacc[kTokXWaves][kGQA][kHD];   // extras waves: value sums (plain basis)
-  float xm[kTokXWaves][kGQA], xl[kTokXWaves][kGQA];
+  uint2 cb[256];                        // VQ codebook, 4 x fp16 per entry
+  uint32_t rc[64][32];                  // [pair][col]: fp16 (cos, sin)(col theta) / 16
+  uint16_t qr[kTokWaves][NQ + 1][2][64];  // per wave: R(-phi0) q (fp16, score k order); row NQ = 0
+  uint32_t pb[kTokWaves][NQ + 1][2][8];   // per wave: fp16 numerators by token parity; row NQ: lanes with no head
+  float xp[kTokWaves][32][NQ + 1];        // per wave: numerators of an extra tile, [token][head]
+  uint32_t next_c, next_x;              // the next unclaimed compressed / extra tile
 };
 
 // Position in the score MFMA's k order (16 rb + 8 hh + e) of pair i, where the
@@ -866,12 +855,13 @@ __device__ __forceinline__ int pair_k(int i) {
   return (i & ~15) + 8 * ((pl >> 2) & 1) + 4 * (pl >> 3) + (pl & 3);
 }
 
-template <int KS>
+template <int KS, int NQ>
 __global__ __launch_bounds__(kTokThreads, 1)
-void k_decode_tok(const SplitParams p) {
+void k_decode_tok(const TokParams p) {
+  static_assert(NQ == 1 || NQ == 2 || NQ == 4, "query heads per workgroup");
   constexpr int NW = kTokWaves;
-  constexpr int NQ = kGQA;
-  __shared__ __align__(16) TokLds<KS> L;
+  constexpr int NE = NQ < 4 ? NQ : 4;  // score elements holding heads, per lane half
+  __shared__ __align__(16) TokLds<KS, NQ> L;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -879,66 +869,69 @@ void k_decode_tok(const SplitParams p) {
   const int col = lane & 31;
   const int hh = lane >> 5;
 
-  // block -> (kv head, split, batch row): as k_decode_split without two_class
-  const int HG = p.G;
+  // ---- block -> (kv head, query group, batch row, split).  A kv head with
+  // more than 4 query heads is split into QG groups of NQ = 4, each its own
+  // workgroup.  The dispatcher deals blocks to the 8 XCDs in turn (block id
+  // mod 8); with B n_splits % 8 == 0 the heads of one (batch row, split)
+  // share an XCD, whose L2 then fetches the split's coefficient rows (read by
+  // every head) once.
+  const int HG = p.G * p.QG;
   const int bid = blockIdx.x;
-  int hg, split;
-  if (kSplitPerXcd && (p.n_splits & 7) == 0) {
+  int vh, pair;  // vh = kv head * QG + query group; pair = b * n_splits + split
+  if (((p.B * p.n_splits) & 7) == 0) {
     const int slot = bid >> 3;
-    hg = slot % HG;
-    split = (slot / HG) * 8 + (bid & 7);
+    vh = slot % HG;
+    pair = (slot / HG) * 8 + (bid & 7);
   } else {
-    hg = bid % HG;
-    split = bid / HG;
+    vh = bid % HG;
+    pair = bid / HG;
   }
-  const int b = blockIdx.y;
-  // The last split's last n_xw waves take the extra tokens (pass j of 32
-  // tokens to extras wave j mod n_xw) while the others start on the compressed
-  // tiles; their first pass's loads go out now, under the set-up.  Then they
-  // join the tile queue.
-  const bool has_x = split == p.n_splits - 1 && p.xs.n_x > 0;
-  const int n_xp = has_x ? (p.xs.n_x + 31) / 32 : 0;
-  const int n_xw = n_xp < kTokXWaves ? n_xp : kTokXWaves;
-  const int xj = w - (NW - n_xw);  // this wave's extras index when >= 0
-  const bool xwave = xj >= 0;
-  const int first_claims = NW - n_xw;
-  XPass xp;
-  half8 xq[8];
-  if (xwave) {
-    xpass_q(p, hg, b, xq);
-    xpass_load(p, hg, b, 32 * xj, xp);
-  }
+  const int hg = vh / p.QG;          // kv head
+  const int qh0 = vh * NQ;           // first query head of the group
+  const int b = pair / p.n_splits;
+  const int split = pair - b * p.n_splits;
 
-  const int t_begin = split * p.chunk;
-  int t_end = t_begin + p.chunk;
-  if (t_end > p.n_comp) t_end = p.n_comp;
-  const int n_t = t_end > t_begin ? (t_end - t_begin + kTile - 1) / kTile : 0;
+  // ---- the split's tiles.  Cost units: a compressed tile 3, an extra tile 1;
+  // split s covers units [s per_u, (s + 1) per_u), compressed tile j belongs to
+  // the split holding unit 3 j, extra tile x to the one holding unit 3 n_ct + x.
+  const int uc = 3 * p.n_ct;
+  const int u0 = split * p.per_u, u1 = min(u0 + p.per_u, uc + p.n_xt);
+  const int ct0 = min((u0 + 2) / 3, p.n_ct), ct1 = min((u1 + 2) / 3, p.n_ct);
+  const int xt0 = min(max(u0 - uc, 0), p.n_xt), xt1 = min(max(u1 - uc, 0), p.n_xt);
+  const int n_c = ct1 > ct0 ? ct1 - ct0 : 0;
+  const int n_x = xt1 > xt0 ? xt1 - xt0 : 0;
 
-  // ---- first tile's loads, then the per-layer operands into LDS.  The
-  // chunk's coefficient rows and V indices are raw buffers: rows past the
-  // chunk end read as zeros (coefficient -8 and centroid 0: finite, and their
-  // scores are -inf), and the offsets of a tile are one base + immediates.
-  const int coef_row_bytes = p.rank / 2;
-  const int n_rows = t_end > t_begin ? t_end - t_begin : 0;
+  // ---- raw buffers of the split's coefficient rows and V indices: rows past
+  // the compressed span read as zeros (coefficient -8, centroid 0: finite;
+  // their scores are set to -inf), and the offsets of a tile are one base +
+  // immediates
+  const int coef_row_bytes = 8 * KS;  // rank / 2
+  const int r0 = 32 * ct0;
+  const int n_rows = min(32 * ct1, p.n_comp) > r0 ? min(32 * ct1, p.n_comp) - r0 : 0;
   const __amdgpu_buffer_rsrc_t rcoef = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.coef + ((int64_t)b * p.n_comp + t_begin) * coef_row_bytes), (short)0,
+      (void*)(p.coef + ((int64_t)b * p.n_comp + r0) * coef_row_bytes), (short)0,
       n_rows * coef_row_bytes, kBufWord3);
   const __amdgpu_buffer_rsrc_t rvidx = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.vidx + (((int64_t)b * p.G + hg) * p.n_comp + t_begin) * 32), (short)0,
-      n_rows * 32, kBufWord3);
+      (void*)(p.vidx + (((int64_t)b * p.G + hg) * p.n_comp + r0) * 32), (short)0, n_rows * 32,
+      kBufWord3);
+  // the additive mask row of batch row b: no mask reads as 0 (zero-length buffer)
+  const int64_t n_keys = (int64_t)p.n_sink + p.n_comp + p.xs.n_x;
+  const __amdgpu_buffer_rsrc_t rmask = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.mask ? p.mask + (int64_t)b * p.mask_stride : p.ws_m), (short)0,
+      p.mask ? (int)(n_keys * 4) : 0, kBufWord3);
   const int vj = lane & 31, vpar = lane >> 5;  // V stage: subvector, token parity
-  auto load_vidx = [&](int t0, uint32_t (&vi_)[16]) {
-    const int voff = (t0 - t_begin + vpar) * 32 + vj;
+  auto load_vidx = [&](int k, uint32_t (&vi_)[16]) {
+    const int voff = (32 * k + vpar) * 32 + vj;
 #pragma unroll
     for (int m = 0; m < 16; ++m) vi_[m] = __builtin_amdgcn_raw_buffer_load_b8(rvidx, voff + 64 * m, 0, 0);
   };
   const float2* t2tab = p.rope + kRopeT2 + lane;  // lane = pair
   const float2* t1tab = p.rope + kRopeT1 + lane;
   auto load_tile = [&](int k, uint32_t (&cw_)[KS], float2& f2, float2& f1) {
-    const int r0 = kTile * k;
-    f2 = t2tab[64 * (k & 31)];
-    f1 = t1tab[64 * (k >> 5)];
-    const int coff = (r0 + col) * coef_row_bytes + KS * 4 * hh;
+    const int kc = min(k, kTokMaxTiles - 1);  // a claim past the split: any valid entry (unused)
+    f2 = t2tab[64 * (kc & 31)];
+    f1 = t1tab[64 * (kc >> 5)];
+    const int coff = (32 * k + col) * coef_row_bytes + KS * 4 * hh;
     if constexpr (KS % 4 == 0) {
 #pragma unroll
       for (int s = 0; s < KS; s += 4) {
@@ -955,7 +948,7 @@ void k_decode_tok(const SplitParams p) {
   };
   uint32_t cwA[KS], cwB[KS];
   float2 fA2, fA1, fB2, fB1;
-  if (w < n_t && !xwave) load_tile(w, cwA, fA2, fA1);
+  if (w < n_c) load_tile(w, cwA, fA2, fA1);
 
   // every global load of the set-up goes out before the first LDS store, so
   // the cold misses overlap (one round trip instead of one per copy step)
@@ -978,7 +971,7 @@ void k_decode_tok(const SplitParams p) {
   const float th = p.inv_freq[lane];
   uint16_t qlo[NQ], qhi[NQ];
   {
-    const uint16_t* qv = p.q + ((int64_t)b * p.H + hg * NQ) * kHD;
+    const uint16_t* qv = p.q + ((int64_t)b * p.H + qh0) * kHD;
 #pragma unroll
     for (int h = 0; h < NQ; ++h) {
       qlo[h] = qv[h * kHD + lane];
@@ -993,22 +986,26 @@ void k_decode_tok(const SplitParams p) {
       if (i < kNA) dst[i] = av[j];
     }
 #pragma unroll
-    for (int j = 0; j < kPR; ++j) {  // rope table [col][pair] -> rc[pair][col] / 16
+    for (int j = 0; j < kPR; ++j) {  // rope table [col][pair] -> rc[pair][col] / 16, fp16 pairs
       const int i = tid + kTokThreads * j;
-      L.rc[i & 63][i >> 6] = make_float2(rv[j].x * 0.0625f, rv[j].y * 0.0625f);
+      half2v hcs;
+      hcs[0] = (half_t)(rv[j].x * 0.0625f);
+      hcs[1] = (half_t)(rv[j].y * 0.0625f);
+      L.rc[i & 63][i >> 6] = __builtin_bit_cast(uint32_t, hcs);
     }
   }
   if (tid < 256) L.cb[tid] = cbv;
-  {  // zero row (head 4) of each wave's rotated-q slot
-    uint32_t* z = (uint32_t*)&L.qr[0][0][0][0];
-    for (int i = tid; i < NW * 64; i += kTokThreads) {
-      const int ww = i >> 6, k = i & 63;
-      z[((ww * 5 + 4) * 2 * 64) / 2 + k] = 0u;
-    }
+  for (int i = tid; i < NW * 64; i += kTokThreads) {  // zero row NQ of each wave's rotated-q slot
+    const int ww = i >> 6, k = i & 63;
+    ((uint32_t*)&L.qr[ww][NQ][0][0])[k] = 0u;
+  }
+  if (tid == 0) {
+    L.next_c = NW;
+    L.next_x = NW;
   }
 
-  // ---- per-lane pair state (lane = pair i): q_rope of the 4 heads, the
-  // phase of the chunk's first token
+  // ---- per-lane pair state (lane = pair i): q_rope of the query heads, the
+  // phase of the split's first compressed token
   float qa[NQ], qb[NQ];
 #pragma unroll
   for (int h = 0; h < NQ; ++h) {
@@ -1016,36 +1013,61 @@ void k_decode_tok(const SplitParams p) {
     qb[h] = h2f(qhi[h]);
   }
   float bs_c, bs_s;
-  sincosf((float)(p.cstart + t_begin) * th, &bs_s, &bs_c);
+  sincosf((float)(p.cstart + r0) * th, &bs_s, &bs_c);
   const int kq = pair_k(lane);  // this lane's slot in the rotated-q rows
-  if (tid == 0) L.next_tile = first_claims;
-
-  // rc rows of this lane: pairs 16 rb + pr[i]
-  int pr[8];
+  int pr[8];                    // rc rows of this lane: pairs 16 rb + pr[i]
 #pragma unroll
   for (int i = 0; i < 8; ++i) pr[i] = 8 * (i >> 2) + 4 * hh + (i & 3);
-  const int qrow = min(col, NQ);  // rows >= 4 of the score MFMA read the zero row
+  const int qrow = min(col, NQ);  // rows >= NQ of the score MFMA read the zero row
   half8 one8;
 #pragma unroll
   for (int e = 0; e < 8; ++e) one8[e] = (half_t)1.f;
   __syncthreads();
 
   const float sc = kLog2e * rsqrtf((float)kHD);
-  float m_run[NQ], l_part[NQ], vacc[NQ][4];
+  float m_run[NE], l_part[NE], vacc[NQ][4];
+  float2 xacc[NQ];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    m_run[i] = -INFINITY;
+    l_part[i] = 0.f;
+  }
 #pragma unroll
   for (int h = 0; h < NQ; ++h) {
-    m_run[h] = -INFINITY;
-    l_part[h] = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) vacc[h][e] = 0.f;
+    xacc[h] = make_float2(0.f, 0.f);
   }
 
+  // Online softmax of one tile's scores (lanes: token col; element i of lane
+  // half hh: head 4 hh + i).  Returns the rescale factor of head h in al[h]
+  // (wave-uniform) and stores the numerators through put(row, pv), row NQ for
+  // lanes that hold no head (every lane stores: no branch).
+  auto softmax = [&](const float16v& sacc, int n_valid, int mpos, float (&al)[NQ], auto put) {
+    const bool tok_ok = col < n_valid;
+    const float madd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rmask, 4 * mpos, 0, 0));
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int h = 4 * hh + i;
+      const float s = (tok_ok && h < NQ) ? sacc[i] * sc + madd * kLog2e : -INFINITY;
+      const float m_new = fmaxf(m_run[i], half32_reduce(s, OpMax()));
+      const float a = m_new == -INFINITY ? 1.f : fast_exp2(m_run[i] - m_new);
+      const float pv = s == -INFINITY ? 0.f : fast_exp2(s - m_new);
+      l_part[i] = l_part[i] * a + pv;
+      m_run[i] = m_new;
+      put(h < NQ ? h : NQ, pv);
+#pragma unroll
+      for (int hf = 0; hf < (NQ > 4 ? 2 : 1); ++hf)
+        if (4 * hf + i < NQ) al[4 * hf + i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32 * hf));
+    }
+  };
+
+  // ---- one compressed tile (relative index k) on this wave
   auto tile = [&](const int k, const uint32_t (&cw)[KS], const float2 f2, const float2 f1) {
-    const int t0 = t_begin + kTile * k;
+    const int t0 = 32 * (ct0 + k);
     uint32_t vi[16];  // V indices of the tile: needed at its end
-    load_vidx(t0, vi);
-    // 1. q rotated by -phi0 of this tile -> the wave's qr slot (lane = pair);
-    //    phi0 = chunk start + 32 (k mod 32) theta + 1024 (k / 32) theta
+    load_vidx(k, vi);
+    // 1. q rotated by -phi0 of this tile -> the wave's qr slot (lane = pair)
     float ph_c = bs_c * f2.x - bs_s * f2.y;
     float ph_s = bs_s * f2.x + bs_c * f2.y;
     {
@@ -1055,10 +1077,8 @@ void k_decode_tok(const SplitParams p) {
     }
 #pragma unroll
     for (int h = 0; h < NQ; ++h) {
-      const float a2 = qa[h] * ph_c + qb[h] * ph_s;
-      const float b2 = qb[h] * ph_c - qa[h] * ph_s;
-      L.qr[w][h][0][kq] = f2h(a2);
-      L.qr[w][h][1][kq] = f2h(b2);
+      L.qr[w][h][0][kq] = f2h(qa[h] * ph_c + qb[h] * ph_s);
+      L.qr[w][h][1][kq] = f2h(qb[h] * ph_c - qa[h] * ph_s);
     }
     // 2. coefficients -> MFMA B operands, once for the 4 row blocks
     half8 Bc[KS];
@@ -1066,8 +1086,6 @@ void k_decode_tok(const SplitParams p) {
     for (int s = 0; s < KS; ++s) Bc[s] = nib8_to_mfma(cw[s]);
     const float16v zero16 = {};
     float16v sacc = zero16;
-    // A operands stream from LDS through a ring of kRing registers, so kRing
-    // reads are in flight ahead of the MFMA that consumes them
     // Two row blocks at a time: their MFMA chains interleave (independent
     // accumulators) and share each converted coefficient operand.  The A
     // operands stream from LDS through a ring of kRing registers, so kRing
@@ -1102,10 +1120,11 @@ void k_decode_tok(const SplitParams p) {
         half8 b0, b1;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float2 rr = L.rc[16 * rb + pr[i]][col];
+          const half2v rr = __builtin_bit_cast(half2v, L.rc[16 * rb + pr[i]][col]);
           const float c = acc[r][i], d = acc[r][i + 8];
-          b0[i] = (half_t)(c * rr.x - d * rr.y);
-          b1[i] = (half_t)(d * rr.x + c * rr.y);
+          // c cos - d sin, d cos + c sin: fp32 products and sums, one fp16 rounding
+          b0[i] = (half_t)__builtin_fmaf(c, (float)rr[0], -__builtin_fmaf(d, (float)rr[1], 0.0f));
+          b1[i] = (half_t)__builtin_fmaf(d, (float)rr[0], __builtin_fmaf(c, (float)rr[1], 0.0f));
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         const half8 qa8 = *(const half8*)&L.qr[w][qrow][0][16 * rb + 8 * hh];
@@ -1114,24 +1133,10 @@ void k_decode_tok(const SplitParams p) {
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qb8, b1, sacc, 0, 0, 0);
       }
     }
-    // 3. online softmax of the 4 heads over the tile (lanes 0-31: token col)
+    // 3. online softmax of the query heads over the tile
     float al[NQ];
-    {
-      const int tok = t0 + col;
-      const bool ok = hh == 0 && tok < t_end;
-      const float madd = (p.mask && ok) ? p.mask[(int64_t)b * p.mask_stride + p.n_sink + tok] * kLog2e : 0.f;
-#pragma unroll
-      for (int h = 0; h < NQ; ++h) {
-        const float s = ok ? sacc[h] * sc + madd : -INFINITY;
-        const float m_new = fmaxf(m_run[h], wave64_reduce(s, OpMax()));
-        al[h] = m_new == -INFINITY ? 1.f : fast_exp2(m_run[h] - m_new);
-        const float pv = s == -INFINITY ? 0.f : fast_exp2(s - m_new);
-        l_part[h] = l_part[h] * al[h] + pv;
-        m_run[h] = m_new;
-        if (hh == 0)
-          ((uint16_t*)&L.pb[w][h][col & 1][0])[col >> 1] = f2h(pv);
-      }
-    }
+    softmax(sacc, p.n_comp - t0, p.n_sink + t0 + col, al,
+            [&](int row, float pv) { ((uint16_t*)&L.pb[w][row][col & 1][0])[col >> 1] = f2h(pv); });
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     // 4. VQ values of the tile: lane (subvector vj, parity vpar) takes tokens
     //    2 m + vpar; dot2 over the token pairs (4 u + vpar, 4 u + 2 + vpar)
@@ -1139,318 +1144,392 @@ void k_decode_tok(const SplitParams p) {
     for (int h = 0; h < NQ; ++h)
 #pragma unroll
       for (int e = 0; e < 4; ++e) vacc[h][e] *= al[h];
-    uint4 pq[NQ][2];
+#pragma unroll
+    for (int ub = 0; ub < 2; ++ub) {  // token pairs u = 4 ub .. 4 ub + 3: one 16-byte numerator load per head
+      uint4 pq[NQ];
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) pq[h] = *(const uint4*)&L.pb[w][h][vpar][4 * ub];
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+        const int u = 4 * ub + uu;
+        const uint2 ca = L.cb[vi[2 * u]], cbb = L.cb[vi[2 * u + 1]];
+        half2v c2[4];
+        c2[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.x, ca.x, 0x05040100u));
+        c2[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.x, ca.x, 0x07060302u));
+        c2[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.y, ca.y, 0x05040100u));
+        c2[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.y, ca.y, 0x07060302u));
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) {
+          const uint32_t pw = uu == 0 ? pq[h].x : uu == 1 ? pq[h].y : uu == 2 ? pq[h].z : pq[h].w;
+          const half2v p2 = __builtin_bit_cast(half2v, pw);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vacc[h][e] = __builtin_amdgcn_fdot2(p2, c2[e], vacc[h][e], false);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // pb is rewritten by the next tile
+  };
+
+  // ---- one extra tile (relative index x): fp16 K (RoPE applied) and V rows
+  half8 Aq[8];  // rows = query heads (rows >= NQ zero), k = head dims; loaded at the first extra tile
+  bool aq_loaded = false;
+  auto xtile = [&](const int x) {
+    if (!aq_loaded) {
+      const uint16_t* qv = p.q + ((int64_t)b * p.H + qh0 + min(col, NQ - 1)) * kHD + 8 * hh;
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        const uint4 v4 = *(const uint4*)(qv + 16 * st);
+        Aq[st] = __builtin_bit_cast(half8, col < NQ ? v4 : make_uint4(0u, 0u, 0u, 0u));
+      }
+      aq_loaded = true;
+    }
+    const int n_xtok = p.xs.n_x;
+    const int x0 = 32 * (xt0 + x);
+    const int xt = min(x0 + col, n_xtok - 1);  // clamped: tokens past n_x are masked
+    int mp;
+    const uint16_t* krow = extra_row(p.xs, p.B, p.G, p.n_comp, b, hg, xt, false, &mp);
+    const uint16_t* vrow = extra_row(p.xs, p.B, p.G, p.n_comp, b, hg, xt, true, &mp);
+    half8 Bk[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) Bk[st] = __builtin_bit_cast(half8, *(const uint4*)(krow + 16 * st + 8 * hh));
+    uint32_t vx[32];
+    const uint64_t vb = (uint64_t)vrow;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
+      vx[t] = *(const uint32_t*)((const uint16_t*)(((uint64_t)hi << 32) | lo) + 2 * lane);
+    }
+    float16v sacc = {};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[st], Bk[st], sacc, 0, 0, 0);
+    float al[NQ];
+    softmax(sacc, n_xtok - x0, mp, al, [&](int row, float pv) { L.xp[w][col][row] = pv; });
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
     for (int h = 0; h < NQ; ++h) {
-      pq[h][0] = *(const uint4*)&L.pb[w][h][vpar][0];
-      pq[h][1] = *(const uint4*)&L.pb[w][h][vpar][4];
+      xacc[h].x *= al[h];
+      xacc[h].y *= al[h];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vacc[h][e] *= al[h];
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint2 ca = L.cb[vi[2 * u]], cb = L.cb[vi[2 * u + 1]];
-      half2v c2[4];
-      c2[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x05040100u));
-      c2[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x07060302u));
-      c2[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x05040100u));
-      c2[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x07060302u));
+    for (int t = 0; t < 32; ++t) {
+      const half2v hv = __builtin_bit_cast(half2v, vx[t]);
+      const float v0 = (float)hv[0], v1 = (float)hv[1];
 #pragma unroll
       for (int h = 0; h < NQ; ++h) {
-        const uint4 v4 = pq[h][u >> 2];
-        const uint32_t pw = (u & 3) == 0 ? v4.x : (u & 3) == 1 ? v4.y : (u & 3) == 2 ? v4.z : v4.w;
-        const half2v p2 = __builtin_bit_cast(half2v, pw);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vacc[h][e] = __builtin_amdgcn_fdot2(p2, c2[e], vacc[h][e], false);
+        const float pt = L.xp[w][t][h];
+        xacc[h].x += pt * v0;
+        xacc[h].y += pt * v1;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // xp is rewritten by the next tile
   };
 
-  auto claim = [&]() {
+  auto claim = [&](uint32_t* ctr) {
     uint32_t v = 0;
-    if (lane == 0) v = __hip_atomic_fetch_add(&L.next_tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (lane == 0) v = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return (int)__builtin_amdgcn_readfirstlane(v);
   };
+  // compressed tiles: ping-pong, the claimed tile's loads fly during the current one
   int k = w;
-  if (xwave) {
-    float xm[kGQA], xl[kGQA];
-    float2 xa[kGQA];
-#pragma unroll
-    for (int h = 0; h < kGQA; ++h) {
-      xm[h] = -INFINITY;
-      xl[h] = 0.f;
-      xa[h] = make_float2(0.f, 0.f);
-    }
-    for (int pi = xj; pi < n_xp; pi += n_xw) {
-      if (pi != xj) xpass_load(p, hg, b, 32 * pi, xp);
-      xpass_compute(p, xp, xq, xm, xl, xa, L.xpw[xj]);
-    }
-#pragma unroll
-    for (int h = 0; h < kGQA; ++h) {
-      const float l = wave64_reduce(xl[h], OpAdd());
-      *(float2*)&L.xacc[xj][h][2 * lane] = xa[h];
-      if (lane == 0) {
-        L.xm[xj][h] = xm[h];
-        L.xl[xj][h] = l;
-      }
-    }
-    k = claim();
-    if (k < n_t) load_tile(k, cwA, fA2, fA1);
-  }
-  while (k < n_t) {  // ping-pong: the claimed tile's loads fly during the current one
-    const int kb = claim();
-    if (kb < n_t) load_tile(kb, cwB, fB2, fB1);
+  while (k < n_c) {
+    const int kb = claim(&L.next_c);
+    if (kb < n_c) load_tile(kb, cwB, fB2, fB1);
     tile(k, cwA, fA2, fA1);
-    if (kb >= n_t) break;
-    k = claim();
-    if (k < n_t) load_tile(k, cwA, fA2, fA1);
+    if (kb >= n_c) break;
+    k = claim(&L.next_c);
+    if (k < n_c) load_tile(k, cwA, fA2, fA1);
     tile(kb, cwB, fB2, fB1);
   }
+  // extra tiles
+  for (int x = w; x < n_x; x = claim(&L.next_x)) xtile(x);
 
-  // ---- merge the waves: (m, l, acc) of each query head
+  // ---- merge the waves; per query head: ch, one inverse FWHT, plain part
 #pragma unroll
-  for (int h = 0; h < NQ; ++h) {
-    l_part[h] = wave64_reduce(l_part[h], OpAdd());
+  for (int i = 0; i < NE; ++i) l_part[i] = half32_reduce(l_part[i], OpAdd());
+#pragma unroll
+  for (int h = 0; h < NQ; ++h)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float a, c;
       perm32_swap(vacc[h][e], a, c);
       vacc[h][e] = a + c;  // the two token parities
     }
-  }
   __syncthreads();  // every wave is done with the image the merge buffer overlays
   if (lane < 32) {
 #pragma unroll
     for (int h = 0; h < NQ; ++h)
-      *(float4*)&L.u.red.acc[w][h][4 * vj] = make_float4(vacc[h][0], vacc[h][1], vacc[h][2], vacc[h][3]);
+      *(float4*)&L.u.red.r[w][h][4 * vj] = make_float4(vacc[h][0], vacc[h][1], vacc[h][2], vacc[h][3]);
   }
-  if (lane == 0) {
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      L.u.red.m[w][h] = m_run[h];
-      L.u.red.l[w][h] = l_part[h];
-    }
+  for (int h = 0; h < NQ; ++h) *(float2*)&L.u.red.pl[w][h][2 * lane] = xacc[h];
+  if (col == 0) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i)
+      if (4 * hh + i < NQ) {
+        L.u.red.m[w][4 * hh + i] = m_run[i];
+        L.u.red.l[w][4 * hh + i] = l_part[i];
+      }
   }
   __syncthreads();
-  {
-    const int h = tid >> 7, d = tid & 127;  // 512 threads = 4 heads x 128 dims
+  const uint32_t ch2 = *(const uint32_t*)(p.vch + ((int64_t)b * p.G + hg) * kHD + 2 * lane);
+  const half2v chh = __builtin_bit_cast(half2v, ch2);
+  for (int h = w; h < NQ; h += NW) {
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, L.u.red.m[ww][h]);
-    float acc = 0.f, l = 0.f;
+    float r0v = 0.f, r1v = 0.f, p0 = 0.f, p1 = 0.f, l = 0.f;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
       const float mw = L.u.red.m[ww][h];
       const float wt = mw == -INFINITY ? 0.f : exp2f(mw - M);
-      acc += wt * L.u.red.acc[ww][h][d];
+      const float2 rvv = *(const float2*)&L.u.red.r[ww][h][2 * lane];
+      const float2 pvv = *(const float2*)&L.u.red.pl[ww][h][2 * lane];
+      r0v += wt * rvv.x; r1v += wt * rvv.y;
+      p0 += wt * pvv.x; p1 += wt * pvv.y;
       l += wt * L.u.red.l[ww][h];
     }
-    const int64_t widx = ((int64_t)b * p.H + hg * NQ + h) * p.nsp + split;
-    p.ws_acc[widx * kHD + d] = acc;
-    if (d == 0) {
+    r0v *= (float)chh[0];
+    r1v *= (float)chh[1];
+    fwht128_pairs(r0v, r1v);
+    const int64_t widx = ((int64_t)b * p.H + qh0 + h) * p.n_splits + split;
+    *(float2*)(p.ws_acc + widx * kHD + 2 * lane) = make_float2(r0v + p0, r1v + p1);
+    if (lane == 0) {
       p.ws_m[widx] = M;
       p.ws_l[widx] = l;
-    }
-    if (n_xw > 0) {  // the extras waves' states -> partial row n_splits (plain basis)
-      float Mx = -INFINITY;
-      for (int j = 0; j < n_xw; ++j) Mx = fmaxf(Mx, L.xm[j][h]);
-      float ax = 0.f, lx = 0.f;
-      for (int j = 0; j < n_xw; ++j) {
-        const float mj = L.xm[j][h];
-        const float wt = mj == -INFINITY ? 0.f : exp2f(mj - Mx);
-        ax += wt * L.xacc[j][h][d];
-        lx += wt * L.xl[j][h];
-      }
-      const int64_t xidx = ((int64_t)b * p.H + hg * NQ + h) * p.nsp + p.n_splits;
-      p.ws_acc[xidx * kHD + d] = ax;
-      if (d == 0) {
-        p.ws_m[xidx] = Mx;
-        p.ws_l[xidx] = lx;
-      }
     }
   }
 }
 
 // --------------------------------------------------------------------------
-// Combine: merge the partials of one query head, one inverse FWHT.
+// Merge of the split partial rows (all in the plain basis): one 4-wave
+// workgroup per (query head, batch row); wave w takes a quarter of the rows,
+// lane = dim pair.  out = sum_s w_s acc_s / sum_s w_s l_s, w_s = 2^(m_s - M).
+// Each wave issues all its row loads (up to kMergePF per round) before it
+// uses the first; two barriers exchange the wave maxima and the sums.
 // --------------------------------------------------------------------------
-struct CombineParams {
-  int32_t B, H, G, n_splits, nsp;
-  const uint16_t* vch;
+constexpr int kMergeWaves = 4;
+constexpr int kMergePF = 32;
+struct MergeParams {
+  int32_t H, nsp;
   const float* ws_m;
   const float* ws_l;
   const float* ws_acc;
   uint16_t* out;
 };
 
-// One butterfly stage at element stride 2*HL = lane stride HL.
-template <int HL>
-__device__ __forceinline__ void fwht_lane_stage(float& x0, float& x1, int l) {
-  const float p0 = xor_lane<HL>(x0), p1 = xor_lane<HL>(x1);
-  x0 = (l & HL) ? p0 - x0 : x0 + p0;
-  x1 = (l & HL) ? p1 - x1 : x1 + p1;
-}
-
-// Butterflies over 128 values held as (2l, 2l+1) in lane l (Sylvester order).
-__device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
-  const int l = (int)lane_id();
-  {
-    const float a = x0, c = x1;
-    x0 = a + c;
-    x1 = a - c;
-  }
-  fwht_lane_stage<1>(x0, x1, l);
-  fwht_lane_stage<2>(x0, x1, l);
-  fwht_lane_stage<4>(x0, x1, l);
-  fwht_lane_stage<8>(x0, x1, l);
-  fwht_lane_stage<16>(x0, x1, l);
-  fwht_lane_stage<32>(x0, x1, l);
-  const float s = 0.08838834764831845f;  // 1/sqrt(128)
-  x0 *= s;
-  x1 *= s;
-}
-
-constexpr int kCombPF = 24;  // partials per wave held in registers: 4 waves cover 96 rows in one round trip
-
-// One workgroup per (query head, batch row); wave w merges a quarter of the
-// partial rows.  Rows [0, n_splits) hold VQ values in the rotated basis (summed,
-// scaled by ch and rotated back once), rows [n_splits, nsp) the extra tokens in
-// the plain basis.  Every load is issued at entry; one barrier publishes the
-// wave maxima, the next the partial sums.
-__global__ __launch_bounds__(kThreads)
-void k_decode_combine(const CombineParams p) {
-  __shared__ __align__(16) float2 rrot[4][64];   // per-wave rotated-basis sums
-  __shared__ __align__(16) float2 rpl[4][64];    // per-wave plain-basis sums
-  __shared__ float wmax[4], wsum[4];
-
+__global__ __launch_bounds__(64 * kMergeWaves)
+void k_decode_merge(const MergeParams p) {
+  __shared__ float wmax[kMergeWaves];
+  __shared__ __align__(16) float2 wacc[kMergeWaves][64];
+  __shared__ float wl[kMergeWaves];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qh = blockIdx.x, b = blockIdx.y, g = qh / kGQA;
-  const int64_t hrow = (int64_t)b * p.H + qh;
-  const int nsp = p.nsp, ns = p.n_splits;
-  const int per = (nsp + 3) / 4;
-  const int s_lo = min(nsp, w * per);
-  const int s_hi = min(nsp, s_lo + per);
-  const float* mrow = p.ws_m + hrow * nsp;
-  const float* lrow = p.ws_l + hrow * nsp;
-  const float* arow = p.ws_acc + hrow * nsp * kHD + 2 * lane;
-
-  const uint32_t ch2 = *(const uint32_t*)(p.vch + ((int64_t)b * p.G + g) * kHD + 2 * lane);
-  float2 av[kCombPF];
+  const int64_t hrow = (int64_t)blockIdx.y * p.H + blockIdx.x;
+  const int per = (p.nsp + kMergeWaves - 1) / kMergeWaves;
+  const int s_lo = min(p.nsp, w * per), s_hi = min(p.nsp, s_lo + per);
+  const float* mrow = p.ws_m + hrow * p.nsp;
+  const float* lrow = p.ws_l + hrow * p.nsp;
+  const float* arow = p.ws_acc + hrow * p.nsp * kHD + 2 * lane;
+  // first round's loads, then the maxima
+  float2 av[kMergePF];
+  float mv[kMergePF], lv[kMergePF];
 #pragma unroll
-  for (int u = 0; u < kCombPF; ++u)
-    av[u] = s_lo + u < s_hi ? *(const float2*)(arow + (int64_t)(s_lo + u) * kHD) : make_float2(0.f, 0.f);
-  float m0 = -INFINITY, l0 = 0.f;
-  if (s_lo + lane < s_hi) { m0 = mrow[s_lo + lane]; l0 = lrow[s_lo + lane]; }
-  float mw = m0;
-  for (int s = s_lo + 64 + lane; s < s_hi; s += 64) mw = fmaxf(mw, mrow[s]);
-  mw = wave64_reduce(mw, OpMax());
-  if (lane == 0) wmax[w] = mw;
+  for (int u = 0; u < kMergePF; ++u) {
+    const int s = min(s_lo + u, p.nsp - 1);
+    av[u] = *(const float2*)(arow + (int64_t)s * kHD);
+    mv[u] = mrow[s];
+    lv[u] = lrow[s];
+  }
+  float mx = -INFINITY;
+  for (int s = s_lo + lane; s < s_hi; s += 64) mx = fmaxf(mx, mrow[s]);
+  mx = wave64_reduce(mx, OpMax());
+  if (lane == 0) wmax[w] = mx;
   __syncthreads();
-
-  float M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  float M = wmax[0];
+#pragma unroll
+  for (int u = 1; u < kMergeWaves; ++u) M = fmaxf(M, wmax[u]);
   if (M == -INFINITY) M = 0.f;  // everything masked: all weights are zero
-
-  const float wt0 = m0 == -INFINITY ? 0.f : exp2f(m0 - M);
-  float L = wt0 * l0;
-  for (int s = s_lo + 64 + lane; s < s_hi; s += 64) {
-    const float m = mrow[s];
-    if (m != -INFINITY) L += exp2f(m - M) * lrow[s];
-  }
-  float2 Sr = make_float2(0.f, 0.f), Sp = make_float2(0.f, 0.f);
+  float a0 = 0.f, a1 = 0.f, l = 0.f;
+  for (int s0 = s_lo;; s0 += kMergePF) {
 #pragma unroll
-  for (int u = 0; u < kCombPF; ++u) {
-    const float wg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt0), u));
-    const bool rot = s_lo + u < ns;
-    const float wr = rot ? wg : 0.f, wp = rot ? 0.f : wg;
-    Sr.x += wr * av[u].x; Sr.y += wr * av[u].y;
-    Sp.x += wp * av[u].x; Sp.y += wp * av[u].y;
-  }
-  for (int s0 = s_lo + kCombPF; s0 < s_hi; s0 += kCombPF) {
-    float2 bv[kCombPF];
+    for (int u = 0; u < kMergePF; ++u) {
+      const float wt = (s0 + u < s_hi && mv[u] != -INFINITY) ? exp2f(mv[u] - M) : 0.f;
+      a0 += wt * av[u].x;
+      a1 += wt * av[u].y;
+      l += wt * lv[u];
+    }
+    if (s0 + kMergePF >= s_hi) break;
 #pragma unroll
-    for (int u = 0; u < kCombPF; ++u)
-      bv[u] = s0 + u < s_hi ? *(const float2*)(arow + (int64_t)(s0 + u) * kHD) : make_float2(0.f, 0.f);
-#pragma unroll
-    for (int u = 0; u < kCombPF; ++u) {
-      const int s = s0 + u;
-      if (s < s_hi) {
-        const float m = mrow[s];
-        const float wg = m == -INFINITY ? 0.f : exp2f(m - M);
-        const float wr = s < ns ? wg : 0.f, wp = s < ns ? 0.f : wg;
-        Sr.x += wr * bv[u].x; Sr.y += wr * bv[u].y;
-        Sp.x += wp * bv[u].x; Sp.y += wp * bv[u].y;
-      }
+    for (int u = 0; u < kMergePF; ++u) {
+      const int s = min(s0 + kMergePF + u, p.nsp - 1);
+      av[u] = *(const float2*)(arow + (int64_t)s * kHD);
+      mv[u] = mrow[s];
+      lv[u] = lrow[s];
     }
   }
-  rrot[w][lane] = Sr;
-  rpl[w][lane] = Sp;
-  L = wave64_reduce(L, OpAdd());
-  if (lane == 0) wsum[w] = L;
+  wacc[w][lane] = make_float2(a0, a1);
+  if (lane == 0) wl[w] = l;
   __syncthreads();
-
-  // wave 0: ch, one inverse FWHT, the plain-basis part, normalization
   if (w == 0) {
-    float2 t = rrot[0][lane], xs = rpl[0][lane];
+    float2 t = wacc[0][lane];
+    float lt = wl[0];
 #pragma unroll
-    for (int u = 1; u < 4; ++u) {
-      const float2 a = rrot[u][lane], c = rpl[u][lane];
-      t.x += a.x; t.y += a.y;
-      xs.x += c.x; xs.y += c.y;
+    for (int u = 1; u < kMergeWaves; ++u) {
+      t.x += wacc[u][lane].x;
+      t.y += wacc[u][lane].y;
+      lt += wl[u];
     }
-    const half2v chh = __builtin_bit_cast(half2v, ch2);
-    float f0 = t.x * (float)chh[0], f1 = t.y * (float)chh[1];
-    fwht128_pairs(f0, f1);
-    const float inv_l = 1.0f / (wsum[0] + wsum[1] + wsum[2] + wsum[3]);
+    const float inv_l = 1.0f / lt;
     half2v o;
-    o[0] = (half_t)((f0 + xs.x) * inv_l);
-    o[1] = (half_t)((f1 + xs.y) * inv_l);
+    o[0] = (half_t)(t.x * inv_l);
+    o[1] = (half_t)(t.y * inv_l);
     *(half2v*)(p.out + hrow * kHD + 2 * lane) = o;
   }
 }
 
-// Which split kernel runs.  Automatic choice by the work per CU: the
-// token-tiled kernel has the higher tile throughput (measured on MI355X:
-// batch 16 x 16K 159 vs 184 us, batch 4 x 8K 32.2 vs 35.7 us, batch 1 x 32K
-// 31.2 vs 32.8 us per call) but a longer set-up and one tile per wave at
-// batch 1 x 8K (19.2 vs 16.8 us), so it takes over from 16 head-tiles per CU.
-constexpr int64_t kTokMinHeadTiles = 16 * 256;
-constexpr int kTokMaxExtra = 256;
+// Which split kernel runs.  The row-split kernel takes query groups of 4 and
+// at most kMaxExtra extra tokens; the token-tiled kernel takes every supported
+// shape.  Automatic choice by the work per CU: the token-tiled kernel has the
+// higher tile throughput but a longer set-up, so it takes over from 16
+// head-tiles per CU (measured on MI355X: batch 16 x 16K 148 vs 167 us, batch 1
+// x 32K 29 vs 31 us; batch 1 x 8K 18.2 vs 15.5 us).
+constexpr int kTokMinHeadTilesPerCU = 16;
+
+inline int device_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+inline int64_t n_extra(const shard_decode_args* a) {
+  return (int64_t)a->n_sink + a->n_win + a->n_dec + a->n_stream;
+}
+
+// query heads per kv head: 1, 2, or a multiple of 4 (groups of 4 per workgroup)
+inline bool tok_supported(const shard_decode_args* a) {
+  if (a->head_dim != kHD || a->n_kv_heads <= 0 || a->n_q_heads <= 0) return false;
+  const int g = a->n_q_heads / a->n_kv_heads;
+  return a->n_q_heads == g * a->n_kv_heads && (g == 1 || g == 2 || (g % 4 == 0 && g <= 64)) &&
+         a->rank > 0 && a->rank % 32 == 0 && a->rank <= 192;
+}
+
+inline int tok_nq(const shard_decode_args* a) {
+  const int g = a->n_q_heads / a->n_kv_heads;
+  return g < 4 ? g : 4;
+}
+
+inline bool split_supported(const shard_decode_args* a) {
+  return a->head_dim == kHD && a->n_q_heads == kGQA * a->n_kv_heads && a->rank > 0 &&
+         a->rank % 32 == 0 && a->rank <= 192 && n_extra(a) <= kMaxExtra;
+}
+
 inline bool use_tok(const shard_decode_args* a) {
   if (a->kernel == 2) return true;
   if (a->kernel == 1) return false;
+  if (!split_supported(a)) return true;
   const int64_t tiles = (int64_t)((a->n_comp + kTile - 1) / kTile) * a->n_kv_heads * a->batch;
-  // one wave of the token-tiled kernel takes the extra tokens, 32 per pass:
-  // longer extra spans (long 8-bit streams) go to the row-split kernel
-  const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
-  return tiles >= kTokMinHeadTiles && n_x <= kTokMaxExtra;
+  return tiles >= (int64_t)kTokMinHeadTilesPerCU * device_cus();
 }
 
-inline int choose_splits(const shard_decode_args* a) {
+// Row-split kernel: splits per (batch row, kv head), two workgroups per CU.
+inline int split_count(const shard_decode_args* a) {
   const int max_useful = (a->n_comp + kTile - 1) / kTile;
-  int want;
-  if (a->n_splits > 0) {
-    want = a->n_splits;
-  } else {
-    // workgroups that fill 256 CUs: one 512-thread token-tiled workgroup per
-    // CU, or two 256-thread row-split workgroups
-    const int target = use_tok(a) ? 256 : kTG == 1 ? 512 : 256;
-    want = target / (a->n_kv_heads * a->batch);
-  }
+  int want = a->n_splits > 0 ? a->n_splits
+                             : (kTG == 1 ? 2 : 1) * device_cus() / (a->n_kv_heads * a->batch);
   if (want > max_useful) want = max_useful;
   if (want < 1) want = 1;
-  if (use_tok(a)) {  // a token-tiled chunk spans at most kTokMaxTiles tiles (phase tables)
-    const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
-    const int cap = max_useful + (n_x + 63) / 64;
-    const int need = (cap + kTokMaxTiles - 1) / kTokMaxTiles;
-    if (want < need) want = need;
-  }
   if (want > kMaxSplits) want = kMaxSplits;
   return want;
 }
 
+// Token-tiled kernel: the split count and the cost units per split.
+struct TokPlan {
+  int n_ct, n_xt, ns, per_u;
+};
+
+inline TokPlan tok_plan(const shard_decode_args* a) {
+  TokPlan w;
+  w.n_ct = (a->n_comp + kTile - 1) / kTile;
+  w.n_xt = (int)((n_extra(a) + kTile - 1) / kTile);
+  const int64_t U = 3LL * w.n_ct + w.n_xt;
+  // one 8-wave workgroup per CU: n_splits x (kv heads x query groups) x batch
+  // workgroups fill the CUs once
+  const int qg = a->n_q_heads / a->n_kv_heads / tok_nq(a);
+  int64_t want = a->n_splits > 0 ? a->n_splits
+                                 : std::max(1, device_cus() / std::max(1, a->n_kv_heads * qg * a->batch));
+  want = std::min<int64_t>(std::max<int64_t>(want, 1), std::max<int64_t>(U, 1));
+  int64_t per = (U + want - 1) / want;
+  per = std::min<int64_t>(per, 3LL * kTokMaxTiles);  // compressed tiles per split: phase tables
+  w.per_u = (int)std::max<int64_t>(per, 1);
+  w.ns = (int)((U + w.per_u - 1) / w.per_u);
+  return w;
+}
+
 template <int KS>
-void launch_split(const SplitParams& sp, dim3 grid, bool tok, hipStream_t s) {
-  if (tok) hipLaunchKernelGGL((k_decode_tok<KS>), grid, dim3(kTokThreads), 0, s, sp);
-  else hipLaunchKernelGGL((k_decode_split<KS, kTG>), grid, dim3(256 * kTG), 0, s, sp);
+void launch_tok(const TokParams& tp, int nq, dim3 grid, hipStream_t s) {
+  switch (nq) {
+    case 1: hipLaunchKernelGGL((k_decode_tok<KS, 1>), grid, dim3(kTokThreads), 0, s, tp); break;
+    case 2: hipLaunchKernelGGL((k_decode_tok<KS, 2>), grid, dim3(kTokThreads), 0, s, tp); break;
+    default: hipLaunchKernelGGL((k_decode_tok<KS, 4>), grid, dim3(kTokThreads), 0, s, tp); break;
+  }
+}
+
+int launch_merge(const shard_decode_args* a, const float* ws, int nsp, hipStream_t s) {
+  const int64_t nm = (int64_t)a->batch * a->n_q_heads * nsp;
+  MergeParams mp;
+  mp.H = a->n_q_heads; mp.nsp = nsp;
+  mp.ws_m = ws; mp.ws_l = ws + nm; mp.ws_acc = ws + 2 * nm; mp.out = a->out;
+  hipLaunchKernelGGL(k_decode_merge, dim3((unsigned)a->n_q_heads, (unsigned)a->batch),
+                     dim3(64 * kMergeWaves), 0, s, mp);
+  SHARD_LAUNCH_CHECK("shard_decode_attn merge");
+  return SHARD_OK;
+}
+
+// Token-tiled split kernel + merge for one decode call (arguments checked by the caller).
+int decode_attn_tok(const shard_decode_args* a, float* ws, hipStream_t s) {
+  const TokPlan pl = tok_plan(a);
+  const int nq = tok_nq(a);
+  const int64_t nm = (int64_t)a->batch * a->n_q_heads * pl.ns;
+  TokParams tp;
+  tp.B = a->batch; tp.H = a->n_q_heads; tp.G = a->n_kv_heads; tp.n_comp = a->n_comp;
+  tp.QG = a->n_q_heads / a->n_kv_heads / nq;
+  tp.cstart = a->compress_start;
+  tp.n_ct = pl.n_ct; tp.n_xt = pl.n_xt; tp.n_splits = pl.ns; tp.per_u = pl.per_u;
+  tp.xs.sink_k = a->sink_k; tp.xs.sink_v = a->sink_v;
+  tp.xs.win_k = a->win_k; tp.xs.win_v = a->win_v;
+  tp.xs.dec_k = a->dec_k; tp.xs.dec_v = a->dec_v;
+  tp.xs.s_k = a->s_k; tp.xs.s_v = a->s_v;
+  tp.xs.n_sink = a->n_sink; tp.xs.n_win = a->n_win; tp.xs.n_dec = a->n_dec;
+  tp.xs.dec_stride = a->dec_stride; tp.xs.n_stream = a->n_stream;
+  tp.xs.n_x = (int32_t)n_extra(a);
+  tp.q = a->q; tp.inv_freq = a->inv_freq; tp.coef = a->k_coeffs;
+  tp.op = (const uint4*)a->prep;
+  tp.rope = (const float2*)((const char*)a->prep + (size_t)a->n_kv_heads * 4 * (a->rank / 16 + 1) * 64 * sizeof(uint4));
+  tp.vidx = a->v_idx; tp.vcb = a->v_codebook; tp.vch = a->v_ch;
+  tp.mask = a->mask; tp.mask_stride = a->mask_stride; tp.n_sink = a->n_sink;
+  tp.ws_m = ws; tp.ws_l = ws + nm; tp.ws_acc = ws + 2 * nm;
+  const dim3 grid((unsigned)((int64_t)pl.ns * a->n_kv_heads * tp.QG * a->batch));
+  switch (a->rank / 16) {
+    case 2: launch_tok<2>(tp, nq, grid, s); break;
+    case 4: launch_tok<4>(tp, nq, grid, s); break;
+    case 6: launch_tok<6>(tp, nq, grid, s); break;
+    case 8: launch_tok<8>(tp, nq, grid, s); break;
+    case 10: launch_tok<10>(tp, nq, grid, s); break;
+    case 12: launch_tok<12>(tp, nq, grid, s); break;
+    default: return SHARD_ERR_SHAPE;
+  }
+  SHARD_LAUNCH_CHECK("shard_decode_attn token-tiled kernel");
+  return launch_merge(a, ws, pl.ns, s);
 }
 
 }  // namespace shard
@@ -1486,10 +1565,17 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
   return SHARD_OK;
 }
 
+int shard_decode_supported(const shard_decode_args* a) {
+  return a && tok_supported(a) ? 1 : 0;
+}
+
 size_t shard_decode_attn_workspace(const shard_decode_args* a) {
-  if (!a || a->batch <= 0 || a->n_q_heads <= 0 || a->n_comp <= 0) return 0;
-  const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
-  const int nsp = choose_splits(a) + (n_x > 0 ? 1 : 0);
+  if (!a || a->batch <= 0 || a->n_q_heads <= 0 || a->n_comp <= 0 || !tok_supported(a)) return 0;
+  if (use_tok(a)) {
+    const TokPlan pl = tok_plan(a);
+    return (size_t)a->batch * a->n_q_heads * pl.ns * (kHD + 2) * sizeof(float);
+  }
+  const int nsp = split_count(a) + (n_extra(a) > 0 ? 1 : 0);
   return (size_t)a->batch * a->n_q_heads * nsp * (kHD + 2) * sizeof(float);
 }
 
@@ -1499,22 +1585,22 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
       !a->v_ch || !a->out)
     return SHARD_ERR_ARG;
   if (a->batch <= 0 || a->n_comp <= 0) return SHARD_ERR_ARG;
-  if (a->head_dim != kHD || a->n_q_heads != kGQA * a->n_kv_heads)
-    return SHARD_ERR_SHAPE;
-  if (a->rank <= 0 || a->rank % 32 != 0 || a->rank > 192) return SHARD_ERR_SHAPE;
   if (a->n_sink < 0 || a->n_win < 0 || a->n_dec < 0 || a->n_stream < 0) return SHARD_ERR_ARG;
   if (a->kernel < 0 || a->kernel > 2) return SHARD_ERR_ARG;
-  const int n_x = a->n_sink + a->n_win + a->n_dec + a->n_stream;
-  if (n_x > kMaxExtra) return SHARD_ERR_SHAPE;
   if ((a->n_sink && (!a->sink_k || !a->sink_v)) || (a->n_win && (!a->win_k || !a->win_v)) ||
       (a->n_dec && (!a->dec_k || !a->dec_v || a->dec_stride < a->n_dec)) ||
       (a->n_stream && (!a->s_k || !a->s_v)))
     return SHARD_ERR_ARG;
-  const int ns = choose_splits(a);
-  const int nsp = ns + (n_x > 0 ? 1 : 0);
+  if (!tok_supported(a) || n_extra(a) > (int64_t)INT32_MAX / 4) return SHARD_ERR_SHAPE;
+  const bool tok = use_tok(a);
+  if (!tok && !split_supported(a)) return SHARD_ERR_SHAPE;  // kernel 1 forced on a shape it lacks
   if (!workspace || workspace_bytes < shard_decode_attn_workspace(a)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
+  if (tok) return decode_attn_tok(a, (float*)workspace, s);
 
+  const int n_x = (int)n_extra(a);
+  const int ns = split_count(a);
+  const int nsp = ns + (n_x > 0 ? 1 : 0);
   float* ws = (float*)workspace;
   const int64_t nm = (int64_t)a->batch * a->n_q_heads * nsp;
   SplitParams sp;
@@ -1534,9 +1620,8 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   sp.chunk2 = sp.chunk;
   sp.n_first = ns;
   sp.two_class = 0;
-  const bool tok = use_tok(a);
   const int half = ns / 2;
-  if (!tok && kTG == 1 && kSplitBias && (int64_t)ns * a->n_kv_heads * a->batch == 512 &&
+  if (kTG == 1 && kSplitBias && (int64_t)ns * a->n_kv_heads * a->batch == 2 * device_cus() &&
       ns % 2 == 0 && 32 % a->n_kv_heads == 0 && n_tiles >= 2 * ns) {
     // first class: ta tiles per split, second class: tb (the last split also
     // runs the extra tokens, counted as x_cost tiles)
@@ -1559,30 +1644,22 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   sp.q = a->q; sp.inv_freq = a->inv_freq; sp.coef = a->k_coeffs;
   sp.op = (const uint4*)a->prep;
   sp.rope = (const float2*)((const char*)a->prep + shard_decode_prepare_op_bytes(a->n_kv_heads, a->rank));
-  sp.vidx = a->v_idx; sp.vcb = a->v_codebook;
+  sp.vidx = a->v_idx; sp.vcb = a->v_codebook; sp.vch = a->v_ch;
   sp.mask = a->mask; sp.mask_stride = a->mask_stride; sp.n_sink = a->n_sink;
   sp.ws_m = ws; sp.ws_l = ws + nm; sp.ws_acc = ws + 2 * nm;
 
   dim3 grid((unsigned)(ns * a->n_kv_heads), (unsigned)a->batch);
   switch (a->rank / 16) {
-    case 2: launch_split<2>(sp, grid, tok, s); break;
-    case 4: launch_split<4>(sp, grid, tok, s); break;
-    case 6: launch_split<6>(sp, grid, tok, s); break;
-    case 8: launch_split<8>(sp, grid, tok, s); break;
-    case 10: launch_split<10>(sp, grid, tok, s); break;
-    case 12: launch_split<12>(sp, grid, tok, s); break;
+    case 2: hipLaunchKernelGGL((k_decode_split<2, kTG>), grid, dim3(256 * kTG), 0, s, sp); break;
+    case 4: hipLaunchKernelGGL((k_decode_split<4, kTG>), grid, dim3(256 * kTG), 0, s, sp); break;
+    case 6: hipLaunchKernelGGL((k_decode_split<6, kTG>), grid, dim3(256 * kTG), 0, s, sp); break;
+    case 8: hipLaunchKernelGGL((k_decode_split<8, kTG>), grid, dim3(256 * kTG), 0, s, sp); break;
+    case 10: hipLaunchKernelGGL((k_decode_split<10, kTG>), grid, dim3(256 * kTG), 0, s, sp); break;
+    case 12: hipLaunchKernelGGL((k_decode_split<12, kTG>), grid, dim3(256 * kTG), 0, s, sp); break;
     default: return SHARD_ERR_SHAPE;
   }
-  SHARD_LAUNCH_CHECK("shard_decode_attn split");
-
-  CombineParams cp;
-  cp.B = a->batch; cp.H = a->n_q_heads; cp.G = a->n_kv_heads;
-  cp.n_splits = ns; cp.nsp = nsp; cp.vch = a->v_ch;
-  cp.ws_m = sp.ws_m; cp.ws_l = sp.ws_l; cp.ws_acc = sp.ws_acc; cp.out = a->out;
-  hipLaunchKernelGGL(k_decode_combine, dim3((unsigned)a->n_q_heads, (unsigned)a->batch),
-                     dim3(kThreads), 0, s, cp);
-  SHARD_LAUNCH_CHECK("shard_decode_attn combine");
-  return SHARD_OK;
+  SHARD_LAUNCH_CHECK("shard_decode_attn row-split kernel");
+  return launch_merge(a, ws, nsp, s);
 }
 
 }  // extern "C"

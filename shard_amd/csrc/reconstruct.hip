@@ -8,19 +8,20 @@
 namespace shard {
 
 constexpr int kRcTok = 32;   // tokens per block
-constexpr int kRcHD = 128;
 
 // K: block = (b, 32-token tile, kv head g); 256 threads = 32 tokens x 8 lanes,
-// each lane owns 8 RoPE pairs (16 dims) of its token.  The head's basis rows
-// and the tile's coefficients are staged in LDS.
+// each lane owns HD / 16 RoPE pairs of its token.  The head's basis rows and
+// the tile's coefficients are staged in LDS.
+template <int HD>
 __global__ __launch_bounds__(256)
 void k_reconstruct_k(const uint8_t* __restrict__ coef, const uint16_t* __restrict__ cs,
                      const uint16_t* __restrict__ basis, const uint16_t* __restrict__ mean,
                      const float* __restrict__ inv_freq, int B, int G, int rank, int n_comp,
                      int cstart, uint16_t* __restrict__ k_out) {
+  constexpr int kRcHD = HD;
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* cf = (uint16_t*)smem;                  // [kRcTok][rank] fp16(nib*cs)
-  uint16_t* bb = cf + kRcTok * rank;               // [kRcHD][rank] basis rows of head g
+  uint16_t* bb = cf + kRcTok * rank;               // [HD][rank] basis rows of head g
   const int tid = threadIdx.x;
   const int g = blockIdx.y, b = blockIdx.z;
   const int t0 = blockIdx.x * kRcTok;
@@ -45,12 +46,13 @@ void k_reconstruct_k(const uint8_t* __restrict__ coef, const uint16_t* __restric
   if (t >= n_comp) return;
   const uint16_t* cr = cf + tt * rank;
   const int pos = cstart + t;
+  constexpr int PL = HD / 16;  // pairs per lane
 #pragma unroll 1
-  for (int u = 0; u < 8; ++u) {
-    const int i = part * 8 + u;  // pair index 0..63
+  for (int u = 0; u < PL; ++u) {
+    const int i = part * PL + u;  // pair index 0 .. HD/2 - 1
     float c = 0.f, d = 0.f;
     const uint16_t* b0 = bb + i * rank;
-    const uint16_t* b1 = bb + (i + 64) * rank;
+    const uint16_t* b1 = bb + (i + HD / 2) * rank;
     for (int r = 0; r < rank; ++r) {
       const float cv = h2f(cr[r]);
       c += cv * h2f(b0[r]);
@@ -58,33 +60,39 @@ void k_reconstruct_k(const uint8_t* __restrict__ coef, const uint16_t* __restric
     }
     // recon = fp16(coeffs @ basis^T) + mean, both fp16
     const float cm = h2f(f2h(h2f(f2h(c)) + h2f(mean[g * kRcHD + i])));
-    const float dm = h2f(f2h(h2f(f2h(d)) + h2f(mean[g * kRcHD + i + 64])));
+    const float dm = h2f(f2h(h2f(f2h(d)) + h2f(mean[g * kRcHD + i + HD / 2])));
     // reapply_rope: k*cos + rotate_half(k)*sin with fp32 phase fl(pos*theta)
     float sn, csn;
     sincosf(__fmul_rn((float)pos, inv_freq[i]), &sn, &csn);
     uint16_t* o = k_out + (((int64_t)b * G + g) * n_comp + t) * kRcHD;
     o[i] = f2h(__fsub_rn(__fmul_rn(cm, csn), __fmul_rn(dm, sn)));
-    o[i + 64] = f2h(__fadd_rn(__fmul_rn(dm, csn), __fmul_rn(cm, sn)));
+    o[i + HD / 2] = f2h(__fadd_rn(__fmul_rn(dm, csn), __fmul_rn(cm, sn)));
   }
 }
 
-// V: one wave per (b, g, t): fp16(hadamard(cb[idx] * ch)), fp32 math.
+// V: one wave per (b, g, t): fp16(hadamard(cb[idx] * ch)), fp32 math; 4-dim
+// subvectors, head dim D = 64 E (element i = lane + 64 k).
+template <int E>
 __global__ void k_reconstruct_v(const uint8_t* __restrict__ vidx, const uint16_t* __restrict__ vcb,
                                 const uint16_t* __restrict__ vch, int64_t rows, int G, int n_comp,
                                 uint16_t* __restrict__ v_out) {
+  constexpr int D = 64 * E;
   const int l = (int)lane_id();
   int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
   for (int64_t r = wave; r < rows; r += nw) {  // r = (b*G + g)*n_comp + t
     const int64_t bg = r / n_comp;
-    const uint8_t* ix = vidx + r * 32;
-    const uint16_t* ch = vch + bg * kRcHD;
-    const int d0 = l, d1 = l + 64;
-    float x[2] = {__fmul_rn(h2f(vcb[4 * ix[d0 >> 2] + (d0 & 3)]), h2f(ch[d0])),
-                  __fmul_rn(h2f(vcb[4 * ix[d1 >> 2] + (d1 & 3)]), h2f(ch[d1]))};
-    wave_fwht<2>(x, kRcHD);
-    v_out[r * kRcHD + d0] = f2h_opaque(x[0]);
-    v_out[r * kRcHD + d1] = f2h_opaque(x[1]);
+    const uint8_t* ix = vidx + r * (D / 4);
+    const uint16_t* ch = vch + bg * D;
+    float x[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      const int d = l + 64 * k;
+      x[k] = __fmul_rn(h2f(vcb[4 * ix[d >> 2] + (d & 3)]), h2f(ch[d]));
+    }
+    wave_fwht<E>(x, D);
+#pragma unroll
+    for (int k = 0; k < E; ++k) v_out[r * D + l + 64 * k] = f2h_opaque(x[k]);
   }
 }
 
@@ -131,17 +139,42 @@ int shard_kv_reconstruct(const shard_decode_args* a, uint16_t* k_out, uint16_t* 
       !a->v_codebook || !a->v_ch || !a->inv_freq || !k_out || !v_out)
     return SHARD_ERR_ARG;
   if (a->batch <= 0 || a->n_comp <= 0 || a->n_kv_heads <= 0) return SHARD_ERR_ARG;
-  if (a->head_dim != kRcHD || a->rank <= 0 || (a->rank & 1) || a->rank > 192) return SHARD_ERR_SHAPE;
+  const int hd = a->head_dim;
+  if ((hd != 64 && hd != 128 && hd != 256) || a->rank <= 0 || (a->rank & 1) || a->rank > 192)
+    return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  const size_t lds = (size_t)(kRcTok + kRcHD) * a->rank * sizeof(uint16_t);  // <= 60 KB at rank 192
+  const size_t lds = (size_t)(kRcTok + hd) * a->rank * sizeof(uint16_t);  // <= 108 KB at hd 256, rank 192
   dim3 grid((unsigned)((a->n_comp + kRcTok - 1) / kRcTok), (unsigned)a->n_kv_heads,
             (unsigned)a->batch);
-  hipLaunchKernelGGL(k_reconstruct_k, grid, dim3(256), lds, s, a->k_coeffs, a->k_coeff_scale,
-                     a->k_basis, a->k_mean, a->inv_freq, a->batch, a->n_kv_heads, a->rank,
-                     a->n_comp, a->compress_start, k_out);
+  auto launch_k = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, a->k_coeffs, a->k_coeff_scale, a->k_basis,
+                       a->k_mean, a->inv_freq, a->batch, a->n_kv_heads, a->rank, a->n_comp,
+                       a->compress_start, k_out);
+  };
   const int64_t rows = (int64_t)a->batch * a->n_kv_heads * a->n_comp;
-  hipLaunchKernelGGL(k_reconstruct_v, dim3(grid_cap((rows + 3) / 4, 16384)), dim3(256), 0, s,
-                     a->v_idx, a->v_codebook, a->v_ch, rows, a->n_kv_heads, a->n_comp, v_out);
+  const dim3 vgrid(grid_cap((rows + 3) / 4, 16384));
+  auto launch_v = [&](auto kern) {
+    hipLaunchKernelGGL(kern, vgrid, dim3(256), 0, s, a->v_idx, a->v_codebook, a->v_ch, rows,
+                       a->n_kv_heads, a->n_comp, v_out);
+  };
+  if (lds > 64 * 1024) {  // LDS beyond the default dynamic limit (160 KB per CU on gfx950)
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_reconstruct_k<256>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_last_error("shard_kv_reconstruct LDS attribute", e);
+      return SHARD_ERR_HIP;
+    }
+  }
+  if (hd == 64) {
+    launch_k(k_reconstruct_k<64>);
+    launch_v(k_reconstruct_v<1>);
+  } else if (hd == 128) {
+    launch_k(k_reconstruct_k<128>);
+    launch_v(k_reconstruct_v<2>);
+  } else {
+    launch_k(k_reconstruct_k<256>);
+    launch_v(k_reconstruct_v<4>);
+  }
   SHARD_LAUNCH_CHECK("shard_kv_reconstruct");
   return SHARD_OK;
 }

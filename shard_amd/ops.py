@@ -313,20 +313,27 @@ class DecodeCall:
         self.static = static     # the layer format's tensors
         self.step = []           # this step's q, out, mask, ... (set by refresh)
         self.out = None
-        self._ws = {}            # workspace bytes by (n_splits, kernel, extra tokens present)
 
     @property
     def keep(self):
         return self.static + self.step
 
     def workspace_bytes(self) -> int:
-        a = self.args
-        key = (a.n_splits, a.kernel, a.n_sink + a.n_win + a.n_dec + a.n_stream > 0)
-        nb = self._ws.get(key)
-        if nb is None:
-            nb = int(_lib.load().shard_decode_attn_workspace(ctypes.byref(a)))
-            self._ws[key] = nb
-        return nb
+        """The library's workspace size for the block as it stands: asked on
+        every call, since it depends on every count the split choice reads
+        (context, extra tokens, batch, requested splits)."""
+        return int(_lib.load().shard_decode_attn_workspace(ctypes.byref(self.args)))
+
+
+def decode_supported(head_dim: int, n_q_heads: int, n_kv_heads: int, rank_pad: int) -> bool:
+    """The shapes shard_decode_attn takes (its shard_decode_supported): head_dim
+    128, 1, 2 or a multiple of 4 (up to 64) query heads per kv head, rank a
+    multiple of 32 up to 192.  Other layers run the reference's unfused path
+    (fp16 K/V rebuilt by shard_kv_reconstruct, attention.py:411)."""
+    if head_dim != 128 or n_kv_heads <= 0 or n_q_heads <= 0 or n_q_heads % n_kv_heads:
+        return False
+    g = n_q_heads // n_kv_heads
+    return (g in (1, 2) or (g % 4 == 0 and g <= 64)) and 0 < rank_pad <= 192 and rank_pad % 32 == 0
 
 
 def decode_prepare(fmt) -> torch.Tensor:
@@ -362,11 +369,14 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
     a.compress_start = fmt["compress_start"]
     for name, t in (("inv_freq", fmt["inv_freq_dev"]), ("k_coeffs", fmt["k_coeffs_pad"]),
                     ("k_coeff_scale", fmt["k_coeff_scale_pad"]), ("k_basis", fmt["k_basis_pad"]),
-                    ("k_mean", fmt["k_mean_f16"]), ("prep", fmt["decode_prep"]),
+                    ("k_mean", fmt["k_mean_f16"]), ("prep", fmt.get("decode_prep")),
                     ("v_idx", fmt["v_indices"]),
                     ("v_codebook", fmt["v_centroids_f16"]), ("v_ch", fmt["v_ch_f16"]),
                     ("sink_k", fmt["sink_k"]), ("sink_v", fmt["sink_v"]),
                     ("win_k", fmt["win_k"]), ("win_v", fmt["win_v"])):
+        if t is None:  # no decode operands: a layer shape only kv_reconstruct takes
+            setattr(a, name, None)
+            continue
         setattr(a, name, t.data_ptr())
         keep.append(t)
     a.n_sink = fmt["sink_k"].shape[2]

@@ -14,6 +14,13 @@ invariant or library routine pins are recorded here:
                      sink, window and an 8-bit stream: pins the reference's
                      fp16 cast points.  Same stub technique as the reference's
                      own benchmarks/kernel_test.py:178-259.
+  int4_chain.npz     the K coefficient chain of _compress_k / _build_gpu_format:
+                     quantize_group -> dequantize_group (rope.py:95-161) ->
+                     col-max/7 scale and round/clamp (cache.py:416-419) ->
+                     int4_pack (triton_kernels.py:665-676, CPU branch) on
+                     2000 x 192 fp32 projections with 0/2/4/6/8-bit columns,
+                     including columns whose values land exactly on .5 code
+                     boundaries in either rounding step (half-even pinned).
 
 Usage:  python tests/golden/make_golden.py /root/reference [fixture ...]
         (no fixture names: write all of them)
@@ -28,6 +35,78 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
+# Column parameters (bits, lo * 8, rng * 8) whose dequantized values divided by
+# col-max/7 land exactly on k + 0.5 in fp32 for two or more codes (found by
+# enumerating lo, rng over multiples of 1/8).
+_INT4_TIE_COLS = [(2, -60, 90), (2, -56, 36), (4, -56, 20), (4, -58, 87), (6, -62, 93),
+                  (6, -60, 30), (8, -60, 102), (8, -56, 15)]
+
+
+def int4_chain_inputs(n=2000, seed=11):
+    """(proj (n, 192) fp32, alloc) for int4_chain.npz.
+
+    Columns: Gaussian with varied scales and offsets (most); for each width,
+    columns on the group quantizer's exact .5 boundaries (min 0, max L 2^e,
+    values (j + 0.5) 2^e, which (x - lo) / rng * L maps to j + 0.5 exactly);
+    columns of _INT4_TIE_COLS, filled with exact code points so the int4
+    rounding meets .5 ties; a constant column and one with a range below the
+    1e-6 clamp."""
+    rs = np.random.default_rng(seed)
+    alloc = [8] * 40 + [6] * 30 + [4] * 50 + [2] * 30 + [0] * 10 + [4] * 20 + [8] * 12
+    keep = len(alloc)
+    proj = (rs.standard_normal((n, keep)) * rs.uniform(0.05, 4.0, keep)
+            + rs.uniform(-1.0, 1.0, keep)).astype(np.float32)
+    nxt = {b: alloc.index(b) for b in (2, 4, 6, 8)}  # next unused column of each width
+
+    def take(b):
+        c = nxt[b]
+        nxt[b] = alloc.index(b, c + 1)
+        return c
+
+    for b in (2, 4, 6, 8):  # stage-1 ties, two columns per width
+        for e in (-3, 1):
+            c = take(b)
+            L = (1 << b) - 1
+            j = rs.integers(0, L, n)
+            x = ((j + 0.5) * 2.0 ** e).astype(np.float32)
+            x[0], x[1] = 0.0, L * 2.0 ** e
+            proj[:, c] = x
+    for b, lo8, r8 in _INT4_TIE_COLS:  # stage-2 ties
+        c = take(b)
+        L = (1 << b) - 1
+        lo, r = np.float32(lo8 / 8.0), np.float32(r8 / 8.0)
+        codes = rs.integers(0, L + 1, n).astype(np.float32)
+        codes[0], codes[1] = 0, L
+        proj[:, c] = ((codes / np.float32(L)).astype(np.float32) * r).astype(np.float32) + lo
+    proj[:, take(8)] = np.float32(0.75)                                 # constant column
+    proj[:, take(8)] = np.float32(0.5) + rs.integers(0, 2, n).astype(np.float32) * np.float32(2e-7)
+    return proj, alloc
+
+
+def group_header(blob, alloc):
+    """Per-column (lo, rng) fp32 from a quantize_group blob (rope.py:120-124's
+    layout: int32 group count and rows, int16 (start, size, bits) per group,
+    then (lo, rng) fp32 per column of the non-zero groups); zero for 0-bit
+    columns."""
+    import zlib
+    raw = zlib.decompress(blob)
+    ng = int(np.frombuffer(raw[:4], np.int32)[0])
+    off, groups = 8, []
+    for _ in range(ng):
+        s, g, b = (int(v) for v in np.frombuffer(raw[off:off + 6], np.int16))
+        groups.append((s, g, b))
+        off += 6
+    nz = sum(g for _, g, _ in groups)
+    hdr = np.frombuffer(raw[off:off + nz * 8], np.float32).reshape(-1, 2)
+    lo = np.zeros(len(alloc), np.float32)
+    rng = np.zeros(len(alloc), np.float32)
+    ci = 0
+    for s, g, _ in groups:
+        lo[s:s + g] = hdr[ci:ci + g, 0]
+        rng[s:s + g] = hdr[ci:ci + g, 1]
+        ci += g
+    return lo, rng
+
 
 def main(ref_root, only=()):
     sys.path.insert(0, os.path.join(ref_root, "src"))
@@ -36,6 +115,26 @@ def main(ref_root, only=()):
     from shard.attention import fused_attention_compressed
 
     want = lambda name: not only or name in only
+
+    # 0. int4 coefficient chain
+    if want("int4_chain.npz"):
+        from shard.rope import dequantize_group, quantize_group
+        from shard.triton_kernels import int4_pack
+        proj, alloc = int4_chain_inputs()
+        n = proj.shape[0]
+        blob = quantize_group(torch.from_numpy(proj), alloc)
+        deq = dequantize_group(blob, alloc, n, "cpu")
+        # _build_gpu_format, cache.py:416-419 (its device is hard-coded to
+        # "cuda"; the four statements are run here on the CPU tensors)
+        col_max = deq.abs().amax(dim=0).clamp(min=1e-6)
+        coeff_scale = col_max / 7.0
+        q = (deq / coeff_scale).round().clamp(-7, 7).to(torch.int8)
+        packed = int4_pack(q)
+        lo, rng = group_header(blob, alloc)
+        np.savez_compressed(os.path.join(HERE, "int4_chain.npz"), proj=proj,
+                 alloc=np.asarray(alloc, np.int32), lo=lo, rng=rng,
+                 deq=deq.numpy().astype(np.float32), q=q.numpy(),
+                 coeff_scale=coeff_scale.numpy().astype(np.float32), packed=packed.numpy())
 
     # 1. Lloyd-Max codebooks
     if want("lloyd_max.npz"):

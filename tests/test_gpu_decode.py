@@ -41,20 +41,23 @@ CASES = [
     (2, 8, 192, 300, 4, 64, 3, 0),       # batch 2
     (1, 2, 64, 33, 2, 3, 1, 0),          # tiny, 2 kv heads
     (1, 8, 96, 1, 4, 64, 0, 0),          # a single compressed token
-    # batch 4 / 16: the grid is again 2 x 256 workgroups (16 and 4 splits per
-    # head), so the two-class chunks and block map run with other class sizes
-    (4, 8, 192, 1100, 4, 64, 2, 0),
-    (16, 8, 128, 300, 4, 16, 1, 0),
+    (4, 8, 192, 1100, 4, 64, 2, 0),      # batch 4
+    (16, 8, 128, 300, 4, 16, 1, 0),      # batch 16
+    (1, 8, 192, 700, 4, 64, 3000, 0),    # 3,068 extra tokens: spread over many splits
+    (2, 4, 160, 900, 4, 64, 700, 9),     # long stream and decode tokens together
 ]
 
+# split kernels: 0 = automatic, 1 = row-split, 2 = token-tiled
+KERNELS = [0, 1, 2]
 
-# split kernels: 1 = row-split (4 waves share a tile), 2 = token-tiled (a wave owns whole tiles)
-KERNELS = [1, 2]
+
+def _kernels_for(n_x):
+    # the earlier split kernels take at most 2048 extra tokens
+    return [k for k in KERNELS if k != 1 or n_x <= 2048]
 
 
-@pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
-def test_decode_matches_exact_oracle(cuda, case, kernel):
+def test_decode_matches_exact_oracle(cuda, case):
     B, nkv, rank, n_comp, sink, win, n_stream, n_dec = case
     gc, inv = random_layer(B=B, nkv=nkv, rank=rank, n_comp=n_comp, sink=sink, win=win,
                            n_stream=n_stream, n_dec=n_dec, seed=n_comp + rank)
@@ -62,10 +65,52 @@ def test_decode_matches_exact_oracle(cuda, case, kernel):
     q = torch.randn(B, 4 * nkv, 1, 128, generator=g).half()
     pos_q = sink + n_comp + win + n_dec + n_stream - 1
     want = exact.decode_attention(q.numpy(), gc, nkv, pos_q, inv.numpy())
-    got = _run(cuda, gc, inv, q, pos_q, nkv=nkv, kernel=kernel)
+    for kernel in _kernels_for(sink + win + n_stream + n_dec):
+        got = _run(cuda, gc, inv, q, pos_q, nkv=nkv, kernel=kernel)
+        err, cos = compare(got, want)
+        print(f"case={case} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (kernel, err, cos)
+
+
+GQA_CASES = [
+    # (B, nkv, query heads per kv head, rank, n_comp, n_stream)
+    (1, 8, 1, 192, 1500, 10),   # multi-head attention (no grouping)
+    (2, 4, 2, 128, 900, 40),
+    (1, 4, 8, 192, 2000, 70),   # 8 query heads per kv head: two workgroups of 4 per head
+    (3, 2, 8, 64, 333, 5),
+    (1, 2, 16, 128, 700, 3),    # 16 query heads per kv head
+]
+
+
+@pytest.mark.parametrize("case", GQA_CASES, ids=[str(c) for c in GQA_CASES])
+def test_decode_other_gqa_groups(cuda, case):
+    """Query-head groups of 1, 2, 8 and 16 on the token-tiled kernel (the
+    reference's fused path takes any n_q / n_kv, attention.py:18-81)."""
+    B, nkv, gqa, rank, n_comp, n_stream = case
+    gc, inv = random_layer(B=B, nkv=nkv, rank=rank, n_comp=n_comp, n_stream=n_stream,
+                           seed=7 * gqa + n_comp)
+    q = torch.randn(B, gqa * nkv, 1, 128, generator=torch.Generator().manual_seed(6)).half()
+    pos_q = 4 + n_comp + 64 + n_stream - 1
+    want = exact.decode_attention(q.numpy(), gc, nkv, pos_q, inv.numpy())
+    got = _run(cuda, gc, inv, q, pos_q, nkv=nkv, kernel=0)
     err, cos = compare(got, want)
-    print(f"case={case} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    print(f"gqa case={case} max_abs={err:.3e} cos={cos:.7f}", flush=True)
     assert err <= TOL_ABS and cos >= TOL_COS
+
+
+def test_decode_split_counts_with_long_extras(cuda):
+    """Explicit split counts from 1 to more splits than tiles: splits that hold
+    only extra tiles, only compressed tiles, both, or nothing to do."""
+    gc, inv = random_layer(n_comp=260, n_stream=300, n_dec=0, seed=21)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(8)).half()
+    pos_q = 4 + 260 + 64 + 300 - 1
+    want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    for kernel in KERNELS:
+        for ns in (1, 2, 3, 7, 13, 40, 500):
+            got = _run(cuda, gc, inv, q, pos_q, n_splits=ns, kernel=kernel)
+            err, cos = compare(got, want)
+            print(f"kernel={kernel} n_splits={ns} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+            assert err <= TOL_ABS and cos >= TOL_COS, (kernel, ns, err, cos)
 
 
 @pytest.mark.parametrize("kernel", KERNELS)
@@ -149,7 +194,7 @@ def test_decode_compressed_real_synthetic(cuda, kernel):
 # The bench's 32K context at batch 1, and batch 16 with enough tiles per
 # workgroup that every wave of the token-tiled kernel walks the claim loop many
 # times (batch 16 x 16K itself takes the fp64 oracle too long for a test).
-LARGE = [(1, 32700, 0), (16, 4000, 8)]
+LARGE = [(1, 32700, 0), (1, 32700, 512), (16, 4000, 8)]
 
 
 _large_cases = {}
@@ -170,16 +215,18 @@ def _large_case(shape):
     return _large_cases[shape]
 
 
-@pytest.mark.parametrize("kernel", [0, 1, 2])
 @pytest.mark.parametrize("shape", LARGE, ids=[f"B{b}xn{n}+s{s}" for b, n, s in LARGE])
-def test_decode_large_contexts(cuda, shape, kernel):
+def test_decode_large_contexts(cuda, shape):
+    """BASELINE configs 2-3 shapes: 32K context, also with the 512-token 8-bit
+    stream of config 3 (the extra tokens spread over several splits)."""
     B, n_comp, n_stream = shape
     gc, inv, q, pos_q, want = _large_case(shape)
-    got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
-    err, cos = compare(got, want)
-    print(f"B={B} n_comp={n_comp} stream={n_stream} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}",
-          flush=True)
-    assert err <= TOL_ABS and cos >= TOL_COS
+    for kernel in KERNELS:
+        got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
+        err, cos = compare(got, want)
+        print(f"B={B} n_comp={n_comp} stream={n_stream} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}",
+              flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (kernel, err, cos)
 
 
 def test_kv_reconstruct(cuda):

@@ -41,6 +41,22 @@ def test_int4_quant_pack_bitexact(cuda, n, alloc, want_codes):
     assert np.array_equal(got["rng"].cpu().numpy()[nz], want["rng"][nz])
 
 
+def test_int4_quant_pack_reference_golden(cuda, golden):
+    """The HIP chain against the reference's own outputs (int4_chain.npz):
+    group-quantizer ranges, coefficient scales and packed nibbles bit for bit,
+    on .5-boundary columns of every width."""
+    ops = _ops()
+    g = golden("int4_chain.npz")
+    alloc = [int(b) for b in g["alloc"]]
+    got = ops.int4_quant_pack(torch.from_numpy(g["proj"]).to(cuda),
+                              torch.tensor(alloc, dtype=torch.int32), want_codes=True)
+    assert np.array_equal(got["packed"].cpu().numpy(), g["packed"])
+    assert np.array_equal(got["coeff_scale"].cpu().numpy(), g["coeff_scale"])
+    nz = np.array(alloc) > 0
+    assert np.array_equal(got["lo"].cpu().numpy()[nz], g["lo"][nz])
+    assert np.array_equal(got["rng"].cpu().numpy()[nz], g["rng"][nz])
+
+
 @pytest.mark.parametrize("rows", [1, 16, 4099])
 def test_stream_quant_bitexact(cuda, rows):
     ops = _ops()

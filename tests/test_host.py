@@ -110,8 +110,8 @@ def test_full_fused_error_is_counted_then_default_path_runs(monkeypatch):
     enable_llama_fused_attention(model)
     c = Cache.from_model(model)
     c._full_fused = True
-    for l in c.layers:
-        l._gpu_compressed = {"stub": True}
+    for l in c.layers:  # stub format of a shape the fused kernel takes
+        l._gpu_compressed = {"head_dim": 128, "n_kv": 1, "rank_pad": 32, "decode_prep": object()}
         l._prefilled = True
         l._seq_len = 10
     c._compressed = True
@@ -130,9 +130,9 @@ def test_full_fused_error_is_counted_then_default_path_runs(monkeypatch):
 
 
 def test_unsupported_shapes_take_the_original_forward(monkeypatch):
-    """A model outside the decode kernel's shapes (head_dim 16, 2 query heads per
-    kv head) decodes through the original forward on compressed layers, without
-    calling the fused path (which would raise on such shapes)."""
+    """A model outside the decode kernel's shapes (head_dim 16) decodes through
+    the original forward on compressed layers, without calling the fused path,
+    and every such layer-step is counted with its shape."""
     from transformers import LlamaConfig, LlamaForCausalLM
     from shard_amd import attention, Cache, enable_llama_fused_attention
     called = []
@@ -145,8 +145,8 @@ def test_unsupported_shapes_take_the_original_forward(monkeypatch):
     model = LlamaForCausalLM(cfg).eval()
     enable_llama_fused_attention(model)
     c = Cache.from_model(model)
-    for l in c.layers:
-        l._gpu_compressed = {"stub": True}
+    for l in c.layers:  # what finalize_format leaves for a head_dim the kernel lacks
+        l._gpu_compressed = {"head_dim": 16, "n_kv": 2, "rank_pad": 32, "decode_prep": None}
         l._prefilled = True
         l._seq_len = 10
     c._compressed = True
@@ -160,3 +160,21 @@ def test_unsupported_shapes_take_the_original_forward(monkeypatch):
     with torch.no_grad():
         model(torch.randint(0, 64, (1, 1)), past_key_values=c, use_cache=True)
     assert called == [] and seen == [0, 1]
+    assert c._fused_fallbacks == 2 and "head_dim=16" in c._last_fused_fallback
+
+
+def test_decode_supported_shapes():
+    """The host mirror of shard_decode_supported agrees with the library's own
+    answer (no GPU needed) on every combination it distinguishes."""
+    import ctypes
+    from shard_amd import _lib, ops
+    lib = _lib.load()
+    for hd in (64, 128, 256):
+        for n_kv in (1, 2, 8):
+            for g in (1, 2, 3, 4, 6, 8, 16, 64, 68):
+                for rank in (32, 96, 100, 192, 224):
+                    a = _lib.DecodeArgs()
+                    a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim = 1, g * n_kv, n_kv, hd
+                    a.rank, a.n_comp = rank, 100
+                    want = bool(lib.shard_decode_supported(ctypes.byref(a)))
+                    assert ops.decode_supported(hd, g * n_kv, n_kv, rank) == want, (hd, n_kv, g, rank)

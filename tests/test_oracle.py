@@ -106,6 +106,30 @@ def test_group_quant_error_bound():
         assert np.max(np.abs(deq[:, c] - proj[:, c])) <= step / 2 * (1 + 1e-4) + 1e-6
 
 
+def test_int4_chain_matches_reference_golden(golden):
+    """The whole K code chain against the reference's own quantize_group ->
+    dequantize_group -> int4 -> int4_pack (tests/golden/int4_chain.npz): every
+    intermediate bit for bit, on columns of all widths, including thousands of
+    values on exact .5 boundaries in both rounding steps."""
+    g = golden("int4_chain.npz")
+    proj, alloc = g["proj"], [int(b) for b in g["alloc"]]
+    ch = ref.k_code_chain(proj, alloc)
+    for key, want in (("lo", g["lo"]), ("rng", g["rng"]), ("deq", g["deq"]), ("q", g["q"]),
+                      ("coeff_scale", g["coeff_scale"]), ("packed", g["packed"])):
+        assert ch[key].dtype == want.dtype or key in ("q",), key
+        assert np.array_equal(ch[key], want), key
+    # the fixture does exercise both tie rules: values on j + 0.5 exactly
+    F = np.float32
+    ties = 0
+    for c, b in enumerate(alloc):
+        if b:
+            v = np.clip(((proj[:, c] - g["lo"][c]) / g["rng"][c]).astype(F), 0, 1)
+            v = (v * F((1 << b) - 1)).astype(F)
+            ties += int(np.sum(v - np.floor(v) == 0.5))
+    r = (g["deq"] / g["coeff_scale"]).astype(F)
+    assert ties > 1000 and int(np.sum(r - np.floor(r) == 0.5)) > 1000
+
+
 def test_int4_chain_pack_relation_and_roundtrip():
     rng = np.random.default_rng(1)
     y = (rng.standard_normal((301, 12)) * rng.uniform(0.1, 3, 12)).astype(np.float32)
@@ -251,6 +275,24 @@ def test_vq_assign_direct_matches_cdist_and_fp64():
     d64 = ((x.double()[:, None, :] - c.double()[None]) ** 2).sum(-1).argmin(1).numpy()
     assert np.array_equal(direct, cd)
     assert np.array_equal(direct, d64)
+
+
+def test_c_vq_assign_direct_equals_numpy():
+    """oracle/cref.c restates ref.vq_assign_direct: same index on every row,
+    including exact ties (duplicate centroids, midpoints), zero and NaN rows."""
+    from oracle import cref
+    if cref.load() is None:
+        cref.build()
+    rs = np.random.default_rng(3)
+    c = rs.standard_normal((256, 4)).astype(np.float32)
+    c[17] = c[200]
+    c[31] = 0.0
+    x = rs.standard_normal((30000, 4)).astype(np.float32)
+    x[:64] = (c[rs.integers(0, 256, 64)] + c[rs.integers(0, 256, 64)]) / 2
+    x[64:80] = c[200]
+    x[80:90] = 0.0
+    x[90:95] = np.nan
+    assert np.array_equal(cref.vq_assign_direct(x, c), ref.vq_assign_direct(x, c))
 
 
 def test_kmeans_matches_reference_golden(golden):
