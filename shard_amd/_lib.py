@@ -115,6 +115,6 @@ def available() -> bool:
 def check(name: str, code: int):
     if code != 0:
         detail = ""
-        if code == -3 and _lib is not None:
+        if code in (-3, -4) and _lib is not None:
             detail = _lib.shard_last_error().decode(errors="replace")
         raise ShardHipError(name, code, detail)

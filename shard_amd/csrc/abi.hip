@@ -13,6 +13,8 @@ void set_last_error(const char* what, hipError_t err) {
            (int)err);
 }
 
+void set_last_text(const char* text) { snprintf(g_last_error, sizeof(g_last_error), "%s", text); }
+
 }  // namespace shard
 
 extern "C" {

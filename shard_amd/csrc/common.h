@@ -17,6 +17,8 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 
 // Records the text of a failed HIP call for shard_last_error().
 void set_last_error(const char* what, hipError_t err);
+// Records a plain message (a failed check that is not a HIP call).
+void set_last_text(const char* text);
 
 #define SHARD_LAUNCH_CHECK(what)                       \
   do {                                                 \

@@ -1,18 +1,23 @@
 // Fused decode attention over Shard's compressed KV cache, written for gfx950.
 //
-// One split launch + one combine launch per layer-step.  Two split kernels
+// One split launch + one merge launch per layer-step.  Two split kernels
 // compute the same partial rows; shard_decode_attn picks one by the work per CU.
 //
 //   k_decode_split (row-split)  grid = (n_splits * n_kv, B), 256-thread
-//     workgroups, two per CU; one kv head x a chunk of compressed tokens, walked
-//     32 tokens at a time.  The 4 waves share each tile: wave P rebuilds rows
-//     of the 16 RoPE pairs [16 P, 16 P + 16) (basis operand in VGPRs), the
-//     partial scores meet in LDS, then a shared online softmax and VQ value sum.
-//   k_decode_tok (token-tiled)  grid = (n_splits * n_kv, B), 512-thread
-//     workgroups, one per CU; the kv head's basis operand image sits in LDS
-//     and each wave takes whole tiles (all 128 rows) from an LDS counter, with
-//     its own softmax state; the waves merge once at the end.
-//   Per tile, both:
+//     workgroups, two per CU, 4 query heads per kv head; one kv head x a chunk
+//     of compressed tokens, walked 32 tokens at a time.  The 4 waves share each
+//     tile: wave P rebuilds rows of the 16 RoPE pairs [16 P, 16 P + 16) (basis
+//     operand in VGPRs), the partial scores meet in LDS, then a shared online
+//     softmax and VQ value sum.  The last split of each head first runs the
+//     extra tokens (at most 2048) into one more partial row per query head.
+//   k_decode_tok (token-tiled)  grid = n_splits * n_kv * query groups * B,
+//     512-thread workgroups, one per CU, 1, 2 or 4 query heads per workgroup;
+//     the kv head's basis operand image sits in LDS and each wave takes whole
+//     tiles (all 128 rows) from an LDS counter, with its own softmax state.
+//     Every split owns a run of cost units (a compressed tile costs 3, a tile
+//     of 32 extra tokens 1), so any number of extra tokens spreads over the
+//     last splits.  The waves merge once at the end.
+//   Per compressed tile, both:
 //     1. rebuild the no-RoPE keys on chip with MFMA 32x32x16 f16:
 //          16 K_n[rows, tok] = Basis'[rows, r] . coef[r, tok] + 16 mean
 //        (coefficients: packed nibbles turned into exact fp16 integers by a
@@ -24,15 +29,14 @@
 //        form (q_rope rotated by the tile phase) in the token-tiled one.
 //     3. online softmax (fp32, base 2) and the VQ values sum_t p_t cb[idx_t]
 //        (rotated space) with the codebook in LDS.
-//     4. per (query head, split): running max m, sum l and the 128-dim
-//        accumulator go to the workspace.
-//   The last split of each head first runs the extra tokens (fp16 sink,
-//   window and decode tokens, the dequantized stream) into one more partial
-//   row per query head.
-//   k_decode_combine  grid = (n_q, B): merges the partial rows, applies ch and
-//     ONE inverse Hadamard to the VQ part, adds the plain-basis part of the
-//     extra tokens, normalizes, writes fp16.
+//   Each workgroup applies ch and ONE inverse Hadamard to its VQ sum (both
+//   linear, so they commute with the merge), adds the plain-basis sum of its
+//   extra tokens and writes per (query head, split) the running max m, the
+//   sum l and the 128-dim accumulator to the workspace.
+//   k_decode_merge  grid = (n_q, B): the log-sum-exp weighted sum of the
+//     partial rows, normalized, written as fp16.
 #include <algorithm>
+#include <stdio.h>
 
 #include "common.h"
 
@@ -772,15 +776,18 @@ void k_decode_split(const SplitParams p) {
 // --------------------------------------------------------------------------
 // One 512-thread workgroup (8 waves, 2 per SIMD) per CU owns one kv head x a
 // range of tiles.  The head's basis operand image (4 row blocks x (KS + 1)
-// k-steps, 52 KB at rank 192) sits in LDS; the waves claim 32-token tiles
-// from an LDS counter and work through them with no workgroup barrier: per
+// k-steps, 52 KB at rank 192) sits in LDS; wave w takes the 32-token tiles
+// w, w + 8, w + 16, ... and works through them with no workgroup barrier: per
 // tile a wave unpacks the coefficients once, runs the 4 x (KS + 1) rebuild
 // MFMAs with A from LDS, rotates, scores, and keeps its own online softmax and
-// VQ value sums.  The waves merge once, after the loop.
+// VQ value sums.  The waves merge once, after the loop, in a fixed order.
+// The tile-to-wave map is static (not claimed from a counter), so a call's
+// result does not depend on the timing of the waves: repeated calls give the
+// same bits.
 //
-// Tiles: the split's compressed tiles first (claimed from one counter), then
-// its extra tiles (sink, window, decode and stream tokens as fp16 rows,
-// claimed from a second counter) with the same softmax state: scores against
+// Tiles: the split's compressed tiles first, then its extra tiles (sink,
+// window, decode and stream tokens as fp16 rows), round robin over the waves
+// and with the same softmax state: scores against
 // q_rope on MFMA, values lane-per-dim-pair in the plain basis.  The host
 // spreads the extra tiles over the last splits (a compressed tile counts as 3
 // cost units, an extra tile as 1), so any number of extra tokens runs on many
@@ -845,7 +852,6 @@ struct TokLds {
   uint16_t qr[kTokWaves][NQ + 1][2][64];  // per wave: R(-phi0) q (fp16, score k order); row NQ = 0
   uint32_t pb[kTokWaves][NQ + 1][2][8];   // per wave: fp16 numerators by token parity; row NQ: lanes with no head
   float xp[kTokWaves][32][NQ + 1];        // per wave: numerators of an extra tile, [token][head]
-  uint32_t next_c, next_x;              // the next unclaimed compressed / extra tile
 };
 
 // Position in the score MFMA's k order (16 rb + 8 hh + e) of pair i, where the
@@ -928,7 +934,7 @@ void k_decode_tok(const TokParams p) {
   const float2* t2tab = p.rope + kRopeT2 + lane;  // lane = pair
   const float2* t1tab = p.rope + kRopeT1 + lane;
   auto load_tile = [&](int k, uint32_t (&cw_)[KS], float2& f2, float2& f1) {
-    const int kc = min(k, kTokMaxTiles - 1);  // a claim past the split: any valid entry (unused)
+    const int kc = min(k, kTokMaxTiles - 1);  // a tile past the split: any valid entry (unused)
     f2 = t2tab[64 * (kc & 31)];
     f1 = t1tab[64 * (kc >> 5)];
     const int coff = (32 * k + col) * coef_row_bytes + KS * 4 * hh;
@@ -998,10 +1004,6 @@ void k_decode_tok(const TokParams p) {
   for (int i = tid; i < NW * 64; i += kTokThreads) {  // zero row NQ of each wave's rotated-q slot
     const int ww = i >> 6, k = i & 63;
     ((uint32_t*)&L.qr[ww][NQ][0][0])[k] = 0u;
-  }
-  if (tid == 0) {
-    L.next_c = NW;
-    L.next_x = NW;
   }
 
   // ---- per-lane pair state (lane = pair i): q_rope of the query heads, the
@@ -1227,24 +1229,20 @@ void k_decode_tok(const TokParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // xp is rewritten by the next tile
   };
 
-  auto claim = [&](uint32_t* ctr) {
-    uint32_t v = 0;
-    if (lane == 0) v = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    return (int)__builtin_amdgcn_readfirstlane(v);
-  };
-  // compressed tiles: ping-pong, the claimed tile's loads fly during the current one
+  // compressed tiles w, w + NW, ...: ping-pong, the next tile's loads fly
+  // during the current one
   int k = w;
   while (k < n_c) {
-    const int kb = claim(&L.next_c);
+    const int kb = k + NW;
     if (kb < n_c) load_tile(kb, cwB, fB2, fB1);
     tile(k, cwA, fA2, fA1);
     if (kb >= n_c) break;
-    k = claim(&L.next_c);
+    k = kb + NW;
     if (k < n_c) load_tile(k, cwA, fA2, fA1);
     tile(kb, cwB, fB2, fB1);
   }
-  // extra tiles
-  for (int x = w; x < n_x; x = claim(&L.next_x)) xtile(x);
+  // extra tiles w, w + NW, ...
+  for (int x = w; x < n_x; x += NW) xtile(x);
 
   // ---- merge the waves; per query head: ch, one inverse FWHT, plain part
 #pragma unroll
@@ -1579,8 +1577,9 @@ size_t shard_decode_attn_workspace(const shard_decode_args* a) {
   return (size_t)a->batch * a->n_q_heads * nsp * (kHD + 2) * sizeof(float);
 }
 
-int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+}  // extern "C"
+
+static int decode_attn_check(const shard_decode_args* a) {
   if (!a || !a->q || !a->inv_freq || !a->k_coeffs || !a->prep || !a->v_idx || !a->v_codebook ||
       !a->v_ch || !a->out)
     return SHARD_ERR_ARG;
@@ -1592,11 +1591,13 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
       (a->n_stream && (!a->s_k || !a->s_v)))
     return SHARD_ERR_ARG;
   if (!tok_supported(a) || n_extra(a) > (int64_t)INT32_MAX / 4) return SHARD_ERR_SHAPE;
-  const bool tok = use_tok(a);
-  if (!tok && !split_supported(a)) return SHARD_ERR_SHAPE;  // kernel 1 forced on a shape it lacks
-  if (!workspace || workspace_bytes < shard_decode_attn_workspace(a)) return SHARD_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
-  if (tok) return decode_attn_tok(a, (float*)workspace, s);
+  if (!use_tok(a) && !split_supported(a)) return SHARD_ERR_SHAPE;  // kernel 1 forced on a shape it lacks
+  return SHARD_OK;
+}
+
+// One decode call on a checked `a` with a workspace of shard_decode_attn_workspace(a) bytes.
+static int decode_attn_run(const shard_decode_args* a, void* workspace, hipStream_t s) {
+  if (use_tok(a)) return decode_attn_tok(a, (float*)workspace, s);
 
   const int n_x = (int)n_extra(a);
   const int ns = split_count(a);
@@ -1660,6 +1661,23 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
   }
   SHARD_LAUNCH_CHECK("shard_decode_attn row-split kernel");
   return launch_merge(a, ws, nsp, s);
+}
+
+extern "C" {
+
+int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  const int st = decode_attn_check(a);
+  if (st != SHARD_OK) return st;
+  const size_t need = shard_decode_attn_workspace(a);
+  if (!workspace || workspace_bytes < need) {
+    char msg[128];
+    snprintf(msg, sizeof(msg), "shard_decode_attn: workspace of %zu bytes, the call needs %zu",
+             workspace ? workspace_bytes : (size_t)0, need);
+    set_last_text(msg);
+    return SHARD_ERR_WORKSPACE;
+  }
+  return decode_attn_run(a, workspace, (hipStream_t)stream);
 }
 
 }  // extern "C"

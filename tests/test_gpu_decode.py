@@ -113,6 +113,23 @@ def test_decode_split_counts_with_long_extras(cuda):
             assert err <= TOL_ABS and cos >= TOL_COS, (kernel, ns, err, cos)
 
 
+def test_decode_is_deterministic(cuda):
+    """Repeated calls give the same bits with every split kernel: the tile to
+    wave map and every merge order are fixed, nothing depends on wave timing."""
+    from shard_amd import ops
+    gc, inv = random_layer(B=2, n_comp=6000, n_stream=37, seed=5)
+    d = to_device(gc, cuda, inv)
+    q = torch.randn(2, 32, 128, generator=torch.Generator().manual_seed(6)).half().to(cuda)
+    call = ops.make_decode_args(q, d, 4 + 6000 + 64 + 37 - 1, None, stream_n=37)
+    for kernel in KERNELS:
+        call.args.kernel = kernel
+        first = ops.decode_attn(call).clone()
+        for rep in range(4):
+            again = ops.decode_attn(call)
+            torch.cuda.synchronize()
+            assert torch.equal(again.view(torch.int16), first.view(torch.int16)), (kernel, rep)
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("bits,qjl", [(4, True), (2, False), (8, True)])
 def test_decode_with_qjl_and_narrow_stream(cuda, bits, qjl, kernel):
