@@ -296,6 +296,20 @@ size_t shard_decode_attn_workspace(const shard_decode_args* args);
 int shard_decode_attn(const shard_decode_args* args, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* shard_decode_attn without a workspace argument and without any allocation:
+ * the partial rows go to a device array of the library,
+ * SHARD_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same kernels and results as shard_decode_attn; a call whose
+ * shard_decode_attn_workspace(args) exceeds the scratch returns
+ * SHARD_ERR_WORKSPACE (shard_last_error says by how much).  Runs on the
+ * current device, whose scratch every call shares: calls that overlap on one
+ * GPU (two streams, two threads) race on it.  Nothing in it needs clearing
+ * between calls (every split writes its whole partial row). */
+#define SHARD_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int shard_decode_attn_noalloc(const shard_decode_args* args, void* stream);
+
 /* Full fp16 reconstruction of the compressed segment for unfused consumers,
  * _ensure_dequant (cache.py:87-124), using the compressed-segment fields of
  * `args` (q, out and the fp16 segments are ignored):

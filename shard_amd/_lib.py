@@ -67,6 +67,7 @@ SIGNATURES = [
     ("shard_decode_supported", c_int32, [ctypes.POINTER(DecodeArgs)]),
     ("shard_decode_attn_workspace", c_size_t, [ctypes.POINTER(DecodeArgs)]),
     ("shard_decode_attn", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
+    ("shard_decode_attn_noalloc", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
     ("shard_kv_reconstruct", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_void_p, c_void_p]),
     ("shard_stream_dequant", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_stream_quant_qjl", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -36,6 +36,7 @@
 //   k_decode_merge  grid = (n_q, B): the log-sum-exp weighted sum of the
 //     partial rows, normalized, written as fp16.
 #include <algorithm>
+#include <mutex>
 #include <stdio.h>
 
 #include "common.h"
@@ -1663,6 +1664,44 @@ static int decode_attn_run(const shard_decode_args* a, void* workspace, hipStrea
   return launch_merge(a, ws, nsp, s);
 }
 
+// ---- scratch of shard_decode_attn_noalloc: the partial rows (m, l, acc) of
+// every (batch row, query head, split), in one device array per GPU that is
+// never freed.  Host code uses the per-device address that
+// hipGetSymbolAddress returns, never the array's own name (on the host that
+// name is a stand-in, not a device address).
+static __device__ __align__(256) unsigned char scratch[SHARD_DECODE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_dev[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, looked up on the first
+// call there.
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_last_error("shard_decode_attn_noalloc hipGetDevice", e);
+    return SHARD_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_last_text("shard_decode_attn_noalloc: device index beyond 63");
+    return SHARD_ERR_ARG;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_last_error("shard_decode_attn_noalloc hipGetSymbolAddress", e);
+      return SHARD_ERR_HIP;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return SHARD_OK;
+}
+
 extern "C" {
 
 int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t workspace_bytes,
@@ -1678,6 +1717,25 @@ int shard_decode_attn(const shard_decode_args* a, void* workspace, size_t worksp
     return SHARD_ERR_WORKSPACE;
   }
   return decode_attn_run(a, workspace, (hipStream_t)stream);
+}
+
+int shard_decode_attn_noalloc(const shard_decode_args* a, void* stream) {
+  const int st = decode_attn_check(a);
+  if (st != SHARD_OK) return st;
+  const size_t need = shard_decode_attn_workspace(a);
+  if (need > SHARD_DECODE_NOALLOC_SCRATCH_BYTES) {
+    char msg[160];
+    snprintf(msg, sizeof(msg),
+             "shard_decode_attn_noalloc: the call needs %zu workspace bytes, more than the %zu of "
+             "its scratch (fewer splits or a smaller batch fit)",
+             need, (size_t)SHARD_DECODE_NOALLOC_SCRATCH_BYTES);
+    set_last_text(msg);
+    return SHARD_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  const int sa = scratch_address(&ws);
+  if (sa != SHARD_OK) return sa;
+  return decode_attn_run(a, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

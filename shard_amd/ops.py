@@ -468,6 +468,21 @@ def decode_attn(call: DecodeCall, ws: torch.Tensor = None) -> torch.Tensor:
     return call.out
 
 
+# SHARD_DECODE_NOALLOC_SCRATCH_BYTES of include/shard_hip.h
+DECODE_NOALLOC_SCRATCH_BYTES = 8 << 20
+
+
+def decode_attn_noalloc(call: DecodeCall) -> torch.Tensor:
+    """The decode call through shard_decode_attn_noalloc: no workspace, no
+    allocation (the library's per-GPU scratch holds the partial rows; calls
+    that overlap on one GPU race on it).  Raises ShardHipError when the call's
+    workspace would exceed DECODE_NOALLOC_SCRATCH_BYTES."""
+    lib = _lib.load()
+    _lib.check("shard_decode_attn_noalloc", lib.shard_decode_attn_noalloc(
+        ctypes.byref(call.args), _stream(call.out)))
+    return call.out
+
+
 def decode_workspace_bytes(call: DecodeCall) -> int:
     return call.workspace_bytes()
 

@@ -45,6 +45,25 @@ def test_argument_errors_without_gpu_work():
     assert lib.shard_decode_attn(None, None, 0, None) == -1
     args = _lib.DecodeArgs()
     assert lib.shard_decode_attn_workspace(ctypes.byref(args)) == 0
+    assert lib.shard_decode_attn_noalloc(None, None) == -1
+    assert lib.shard_decode_attn_noalloc(ctypes.byref(args), None) == -1
+
+
+def test_noalloc_refuses_calls_beyond_its_scratch_before_any_launch():
+    """The size check of shard_decode_attn_noalloc runs on the host: with
+    placeholder pointers (never dereferenced) and 375 forced splits the call
+    needs 12.48 MB of partial rows, more than the 8 MiB scratch."""
+    from shard_amd import _lib, ops
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim, a.rank, a.n_comp = 2, 32, 8, 128, 192, 4000
+    for f in ("q", "inv_freq", "k_coeffs", "prep", "v_idx", "v_codebook", "v_ch", "out"):
+        setattr(a, f, 16)
+    a.n_splits, a.kernel = 375, 2
+    need = lib.shard_decode_attn_workspace(ctypes.byref(a))
+    assert need == 2 * 32 * 375 * (128 + 2) * 4 > ops.DECODE_NOALLOC_SCRATCH_BYTES
+    assert lib.shard_decode_attn_noalloc(ctypes.byref(a), None) == -4
+    assert str(need).encode() in lib.shard_last_error()
 
 
 def test_cpu_tensor_is_rejected_loudly():
