@@ -28,21 +28,25 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "decode attn µs/layer-step + achieved HBM GB/s @8K/32K; e2e tokens/sec"
 
 
-def algorithmic_bytes(n_comp, rank, n_stream=0, n_sink=4, n_win=64, n_kv=8, hd=128, n_q=32):
-    """Bytes one decode call must move at minimum (per layer-step, batch 1):
-    int4 coefficients + u8 V indices per compressed token, fp16 sink/window K,V,
-    the basis/scales/mean/codebook/channel scales, stream codes+norms, q in, out."""
+def algorithmic_bytes(n_comp, rank, n_stream=0, n_sink=4, n_win=64, n_kv=8, hd=128, n_q=32, batch=1):
+    """Bytes one decode call must move at minimum (per layer-step): per
+    compressed token the int4 coefficients and the u8 V indices, the fp16 sink
+    and window K/V, the stored tables as the reference keeps them (int8 basis,
+    fp16 basis and coefficient scales, fp16 mean, fp16 codebook, fp16 channel
+    scales), stream codes + norms, q in and out.  At rank 192, batch 1:
+    352 n + 278,528 + 203,520 + 2,080 s + 16,384."""
     per_tok = rank // 2 + n_kv * hd // 4
     fixed = (n_sink + n_win) * n_kv * hd * 2 * 2
-    tables = n_kv * hd * rank * 2 + rank * 2 + n_kv * hd * 2 + 256 * 4 * 2 + n_kv * hd * 2
-    stream = n_stream * (2 * n_kv * hd + 2 * n_kv * 2)
+    tables = n_kv * hd * rank + rank * 2 + rank * 2 + n_kv * hd * 2 + 256 * 4 * 2 + n_kv * hd * 2
+    stream = n_stream * 2 * (n_kv * hd + n_kv * 2)
     io = 2 * n_q * hd * 2
-    return n_comp * per_tok + fixed + tables + stream + io
+    return batch * (n_comp * per_tok + fixed + stream + io + n_kv * hd * 2) + tables - n_kv * hd * 2
 
 
-def algorithmic_flops(n_comp, rank, n_kv=8, hd=128, n_q=32):
-    """Key reconstruction (2*n_kv*hd*rank) + scores and rotation + VQ accumulate per token."""
-    return n_comp * (2 * n_kv * hd * rank + n_q * hd * 4 + n_q * hd * 2)
+def algorithmic_flops(n_comp, rank, n_stream=0, n_kv=8, hd=128, n_q=32, batch=1):
+    """Key reconstruction (2 n_kv hd rank) + rotation and scores + V accumulate
+    per compressed token (413,696 at rank 192), 16,384 per stream token."""
+    return batch * (n_comp * (2 * n_kv * hd * rank + n_q * hd * 5) + n_stream * n_q * hd * 4)
 
 
 def clone_format(fmt):
@@ -71,6 +75,17 @@ def build_layer(T, dev, seed=0, n_stream=0, with_layer=False):
     torch.cuda.synchronize()
     if with_layer:
         return fmt, k, v, layer
+    return fmt, k, v
+
+
+def build_layer_batch(T, batch, dev, seed=0):
+    """A compressed layer of `batch` rows of T tokens (K/V generated on the device)."""
+    from shard_amd import Cache, bench_data
+    from shard_amd.cache import compress_layer
+    k, v, _ = bench_data.make_kv_device(T, batch, seed, dev)
+    cache = Cache(num_layers=1, rope_inv_freq=bench_data.inv_freq())
+    fmt = compress_layer(cache, k, v, 0)
+    torch.cuda.synchronize()
     return fmt, k, v
 
 
@@ -133,30 +148,20 @@ def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, 
     return res[0], res[1], us_eager
 
 
-def time_sdpa(k, v, q, steps, warmup, dev, graph_len=50):
-    """fp16 uncompressed decode attention on the same K/V (torch SDPA with GQA),
-    rotating over copies and replayed from a HIP graph like the compressed call."""
-    import torch.nn.functional as F
-    T = k.shape[2]
-    n_copies = max(1, math.ceil(512e6 / (2 * k.numel() * 2)))
-    ks = [k.to(dev) for _ in range(n_copies)]
-    vs = [v.to(dev) for _ in range(n_copies)]
-    qq = q.to(dev)
-
-    def call(i):
-        return F.scaled_dot_product_attention(qq, ks[i % n_copies], vs[i % n_copies], enable_gqa=True)
-
+def graph_time(fns, steps, warmup, graph_len=100):
+    """Per-call time of fns[i % len(fns)] replayed from a HIP graph of
+    graph_len calls (each call on the next copy), HIP events around the replays."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for i in range(max(warmup, graph_len)):
-            call(i)
+            fns[i % len(fns)]()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(graph_len):
-            call(i)
+            fns[i % len(fns)]()
     g.replay()
     torch.cuda.synchronize()
     reps = max(1, steps // graph_len)
@@ -166,10 +171,55 @@ def time_sdpa(k, v, q, steps, warmup, dev, graph_len=50):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / (reps * graph_len), 2 * T * 8 * 128 * 2
+    del g
+    return e0.elapsed_time(e1) * 1000.0 / (reps * graph_len)
 
 
-def cpu_baseline(fmt, q, pos_q, inv, budget_s=15.0):
+def time_fp16_decode(k, v, q, steps, warmup):
+    """The fp16 FlashDecoding-style baseline (split-K GQA over uncompressed K/V,
+    ops.bench_fp16_decode) on the same K/V, timed like the compressed call:
+    graph replay over rotated copies (together >= 512 MB, more than the MALL
+    holds).  Returns (us per call, bytes of K and V per call)."""
+    from shard_amd import ops
+    per_copy = 2 * k.numel() * 2
+    n_copies = max(1, math.ceil(512e6 / per_copy))
+    ks = [k] + [k.clone() for _ in range(n_copies - 1)]
+    vs = [v] + [v.clone() for _ in range(n_copies - 1)]
+    out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=q.device)
+    fns = [lambda i=i: ops.bench_fp16_decode(q, ks[i], vs[i], out=out, ws=ws) for i in range(n_copies)]
+    us = graph_time(fns, steps, warmup)
+    del ks, vs
+    torch.cuda.empty_cache()
+    return us, per_copy
+
+
+def time_sdpa(k, v, q, steps, warmup, dev, graph_len=50):
+    """torch SDPA (fp16, GQA) on the same K/V, rotated and replayed the same way."""
+    import torch.nn.functional as F
+    n_copies = max(1, math.ceil(512e6 / (2 * k.numel() * 2)))
+    ks = [k.to(dev) for _ in range(n_copies)]
+    vs = [v.to(dev) for _ in range(n_copies)]
+    qq = q.to(dev)
+    fns = [lambda i=i: F.scaled_dot_product_attention(qq, ks[i], vs[i], enable_gqa=True)
+           for i in range(n_copies)]
+    return graph_time(fns, steps, warmup, graph_len)
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the baseline record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(fmt, q, pos_q, inv, budget_s=15.0, max_calls=50):
     """The reference's CPU fallback (oracle.ref restatement) on this host's cores."""
     from oracle import ref
     B = fmt["batch"]
@@ -189,11 +239,11 @@ def cpu_baseline(fmt, q, pos_q, inv, budget_s=15.0):
         t0 = time.perf_counter()
         ref.fused_attention_compressed(qc, gc, nkv, pos_q, inv)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 50:
+        if time.perf_counter() - t_start > budget_s or len(times) >= max_calls:
             break
     times.sort()
     return {"value": round(times[len(times) // 2] * 1e6, 1), "unit": "us/layer-step",
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": torch.get_num_threads(), "cpu": cpu_model(), "kind": "port",
             "sample": f"{len(times)} decode calls of the reference CPU fallback path "
                       f"(oracle.ref.fused_attention_compressed, torch CPU) on the same 1-layer "
                       f"{n}-token compressed context, median"}
@@ -435,6 +485,29 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
             logits = []
         return t1 - t0, torch.cat(toks, 1), logits, stats
 
+    def fused_vs_unfused(cache, tok):
+        """One more decode step computed twice from the same cache state: with
+        the fused kernel, then (stream position restored) through the original
+        forward over the rebuilt fp16 K/V (kv_reconstruct + stream dequant).
+        Both read the same compressed representation, so their logits must
+        agree; this is the run's quality check (random weights make agreement
+        with the fp16 cache meaningless)."""
+        snap = [(l._seq_len, l._gpu_compressed.get("stream_n", 0)) for l in cache.layers]
+        with torch.no_grad():
+            fused = model(tok, past_key_values=cache, use_cache=True).logits[:, -1].float()
+            for l, (sl, sn) in zip(cache.layers, snap):
+                l._seq_len, l._gpu_compressed["stream_n"] = sl, sn
+            inv = cache._rope_inv_freq
+            cache._rope_inv_freq = None            # the patched forward then takes the original path
+            try:
+                plain = model(tok, past_key_values=cache, use_cache=True).logits[:, -1].float()
+            finally:
+                cache._rope_inv_freq = inv
+        return {"top1_agreement": round((fused.argmax(-1) == plain.argmax(-1)).float().mean().item(), 4),
+                "logit_cosine": round(torch.nn.functional.cosine_similarity(fused, plain, dim=-1)
+                                      .min().item(), 6),
+                "max_abs_logit_diff": round((fused - plain).abs().max().item(), 5)}
+
     with torch.no_grad():                      # warm-up on a short prompt (kernels, allocator)
         wc = Cache.from_model(model)
         wc._streaming = True
@@ -469,7 +542,8 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
             t2 = sync_time()
             r["compress_s"] = round(t2 - t1, 3)
             r["peak_compress_gb"] = round(torch.cuda.max_memory_allocated() / 1e9, 2)
-            r["clean_compress_ratio"] = round(cache.clean_compress_ratio(), 2)
+            r["clean_compress_ratio"] = round(cache.clean_compress_ratio(), 2)   # one row (reference)
+            r["clean_compress_ratio_all_rows"] = round(cache.clean_compress_ratio_all_rows(), 2)
         torch.cuda.reset_peak_memory_stats()
         if kind == "fp16":
             dt, toks, fp16_logits, _ = decode(cache, first, new_tokens)
@@ -487,6 +561,9 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
             kept *= 2
         r["peak_decode_gb"] = round(torch.cuda.max_memory_allocated() / 1e9 - kept, 2)
         progress(f"{kind}: decode {r['decode_s']} s, {r['tokens_per_s']} tokens/s")
+        if kind == "shard":
+            r["fused_vs_unfused_step"] = fused_vs_unfused(cache, fp16_toks[:, -1:])
+            progress(f"shard: fused vs unfused step {r['fused_vs_unfused_step']}")
         res[kind] = r
         del cache
     return {"metric": "e2e decode tokens/s, shard cache vs fp16 cache (BASELINE config 5)",
@@ -512,6 +589,10 @@ def main():
     ap.add_argument("--also-32k", action="store_true", default=True)
     ap.add_argument("--no-32k", dest="also_32k", action="store_false")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-b16", dest="b16", action="store_false", default=True,
+                    help="skip the batch-16 x 16K layer (config 5's decode shape)")
+    ap.add_argument("--no-e2e", dest="with_e2e", action="store_false", default=True,
+                    help="skip the config-5 end-to-end run in the default line")
     ap.add_argument("--n-splits", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0,
                     help="decode split kernel: 0 automatic, 1 row-split, 2 token-tiled")
@@ -562,28 +643,63 @@ def main():
         print(json.dumps(pmc_workload(dev, args.ctx, layer_path=args.layer)), flush=True)
         return
 
-    def measure(T, with_baselines):
-        fmt, k, v = build_layer(T, dev)
+    def measure(T, batch=1, baselines=()):
+        """The compressed decode call on a T-token layer of `batch` rows, and the
+        named same-GPU baselines on its uncompressed K/V."""
+        if batch == 1:
+            fmt, k, v = build_layer(T, dev)
+        else:
+            fmt, k, v = build_layer_batch(T, batch, dev)
         n, rank = fmt["n_compress"], fmt["rank_pad"]
-        q = bench_data.make_q().to(dev).view(1, 32, 128)
-        nbytes = algorithmic_bytes(n, rank)
+        q = bench_data.make_q(batch).to(dev).view(batch, 32, 128)
+        nbytes = algorithmic_bytes(n, rank, batch=batch)
         n_copies = max(2, math.ceil(2 * 256e6 / nbytes))
         us, us_hot, us_eager = time_decode(fmt, q, T, args.steps, args.warmup, n_copies,
                                            args.n_splits, kernel=args.kernel)
-        res = {"T": T, "n_comp": n, "rank": fmt["rank"], "us": us, "us_hot": us_hot,
-               "us_eager": us_eager,
-               "bytes": nbytes, "flops": algorithmic_flops(n, rank), "copies": n_copies}
-        if with_baselines:
-            res["sdpa_us"], res["sdpa_bytes"] = time_sdpa(k, v, q.view(1, 32, 1, 128),
-                                                          min(args.steps, 200), 20, dev)
-            res["fmt"] = fmt
+        res = {"T": T, "batch": batch, "n_comp": n, "rank": fmt["rank"], "us": us,
+               "us_hot": us_hot, "us_eager": us_eager, "bytes": nbytes,
+               "flops": algorithmic_flops(n, rank, batch=batch), "copies": n_copies}
+        kd, vd = k.to(dev), v.to(dev)
+        if "fp16" in baselines:
+            res["fp16_us"], res["fp16_bytes"] = time_fp16_decode(kd, vd, q, args.steps, args.warmup)
+        if "sdpa" in baselines:
+            res["sdpa_us"] = time_sdpa(kd, vd, q.view(batch, 32, 1, 128), min(args.steps, 200),
+                                       20, dev)
+        if batch == 1:
+            res["fmt_cpu"] = {kk: (vv.cpu() if torch.is_tensor(vv) else vv) for kk, vv in fmt.items()
+                              if kk in ("k_coeffs", "k_coeff_scale", "k_basis_f16", "k_mean_f16",
+                                        "v_centroids_f16", "v_ch_f16", "sink_k", "sink_v",
+                                        "win_k", "win_v", "k_coeffs_shape", "n_compress",
+                                        "batch", "compress_start", "v_indices", "n_kv",
+                                        "head_dim")}
+        del fmt, k, v, kd, vd
+        torch.cuda.empty_cache()
         return res
 
-    r8 = measure(args.ctx, True)
-    r32 = measure(32768, False) if args.also_32k and args.ctx != 32768 else None
+    def summary(r):
+        g = r["bytes"] / (r["us"] * 1e-6) / 1e9
+        d = {"us": round(r["us"], 3), "us_hot": round(r["us_hot"], 3),
+             "us_eager_python_launch": round(r["us_eager"], 3),
+             "achieved_hbm_gbs": round(g, 1), "frac": round(g / HBM_PEAK_GBS, 4),
+             "algorithmic_bytes": r["bytes"],
+             "mfma_frac_fp16": round(r["flops"] / (r["us"] * 1e-6) / 2.5e15, 4),
+             "n_comp": r["n_comp"], "rank": r["rank"], "rotated_copies": r["copies"]}
+        if "fp16_us" in r:
+            d["fp16_flashdecode_us"] = round(r["fp16_us"], 3)
+            d["fp16_flashdecode_hbm_gbs"] = round(r["fp16_bytes"] / (r["fp16_us"] * 1e-6) / 1e9, 1)
+            d["speedup_vs_fp16_flashdecode"] = round(r["fp16_us"] / r["us"], 3)
+        if "sdpa_us" in r:
+            d["fp16_sdpa_us"] = round(r["sdpa_us"], 3)
+            d["speedup_vs_fp16_sdpa"] = round(r["sdpa_us"] / r["us"], 3)
+        return d
+
+    r8 = measure(args.ctx, baselines=("fp16", "sdpa"))
+    r32 = measure(32768, baselines=("fp16",)) if args.also_32k and args.ctx != 32768 else None
+    rb16 = measure(16384, 16, baselines=("fp16",)) if args.b16 else None
 
     us = r8["us"]
     gbs = r8["bytes"] / (us * 1e-6) / 1e9
+    s8 = summary(r8)
     out = {
         "metric": METRIC,
         "value": round(us, 3),
@@ -601,29 +717,45 @@ def main():
                    "n_comp": r8["n_comp"], "rank": r8["rank"], "sink": 4, "window": 64,
                    "rotated_copies": r8["copies"]},
         "achieved_hbm_gbs": round(gbs, 1),
-        "us_hot": round(r8["us_hot"], 3),
-        "us_eager_python_launch": round(r8["us_eager"], 3),
-        "fp16_sdpa_us": round(r8["sdpa_us"], 3),
-        "speedup_vs_fp16_sdpa": round(r8["sdpa_us"] / us, 3),
+        "us_hot": s8["us_hot"],
+        "us_eager_python_launch": s8["us_eager_python_launch"],
+        "fp16_flashdecode_us": s8.get("fp16_flashdecode_us"),
+        "speedup_vs_fp16_flashdecode": s8.get("speedup_vs_fp16_flashdecode"),
+        "fp16_sdpa_us": s8.get("fp16_sdpa_us"),
+        "speedup_vs_fp16_sdpa": s8.get("speedup_vs_fp16_sdpa"),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(args.ctx),
-                     "kernel": "shard_decode_attn (k_decode_split + k_decode_combine), per call",
-                     "mfma_frac_fp16": round(r8["flops"] / (us * 1e-6) / 2.5e15, 4)},
+                     "traffic_source": "profiles/decode_traffic.md (rocprofv3 --pmc FETCH_SIZE "
+                                       "and WRITE_SIZE of the same call, copy-calibrated)",
+                     "kernel": "shard_decode_attn (split kernel + k_decode_merge), per call, "
+                               "HIP events around graph replays",
+                     "algorithmic_bytes": r8["bytes"],
+                     "mfma_frac_fp16": s8["mfma_frac_fp16"]},
     }
     if r32 is not None:
-        g32 = r32["bytes"] / (r32["us"] * 1e-6) / 1e9
-        out["at_32k"] = {"us": round(r32["us"], 3), "us_hot": round(r32["us_hot"], 3),
-                         "us_eager_python_launch": round(r32["us_eager"], 3),
-                         "achieved_hbm_gbs": round(g32, 1), "frac": round(g32 / HBM_PEAK_GBS, 4),
-                         "traffic": read_traffic(32768),
-                         "n_comp": r32["n_comp"], "rank": r32["rank"]}
+        out["at_32k"] = summary(r32)
+        out["at_32k"]["traffic"] = read_traffic(32768)
+    if rb16 is not None:
+        out["batch16_16k_layer"] = summary(rb16)
+        out["batch16_16k_layer"]["workload"] = ("one layer of BASELINE config 5's decode step: "
+                                                "batch 16 x 16384-token compressed context")
     if not args.no_cpu:
         try:
-            out["cpu_baseline"] = cpu_baseline(r8["fmt"], bench_data.make_q().view(1, 32, 128),
-                                               args.ctx, bench_data.inv_freq())
+            qc = bench_data.make_q().view(1, 32, 128)
+            cb = cpu_baseline(r8["fmt_cpu"], qc, args.ctx, bench_data.inv_freq())
+            if r32 is not None:
+                c32 = cpu_baseline(r32["fmt_cpu"], qc, 32768, bench_data.inv_freq(),
+                                   budget_s=10.0, max_calls=20)
+                cb["at_32k"] = {"value": c32["value"], "unit": c32["unit"], "sample": c32["sample"]}
+            out["cpu_baseline"] = cb
         except Exception as e:  # reported, never replaces the GPU number
             out["cpu_baseline"] = {"error": repr(e)}
+    if args.with_e2e:
+        try:
+            out["e2e"] = e2e(dev, args.e2e_batch, args.e2e_prompt, args.e2e_new, args.e2e_layers)
+        except Exception as e:  # reported, never replaces the decode number
+            out["e2e"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
 
 

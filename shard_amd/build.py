@@ -29,6 +29,7 @@ PER_FILE = {
     "pca.hip": [],
     "reconstruct.hip": ["-ffp-contract=off"],
     "abi.hip": [],
+    "fp16_decode.hip": [],
 }
 
 

@@ -349,6 +349,46 @@ class Cache(HFCache):
 
     # -- memory accounting (cache.py:462-539) ------------------------------
     def memory_bytes(self):
+        """Compressed bytes as the reference counts them (cache.py:462-497): its
+        key set, under this format's names (``v_indices`` holds what the
+        reference calls ``v_indices_u8``), stream codes at their bit width.
+        ``device_bytes`` counts every tensor this format keeps resident."""
+        total = 0
+        has_gc = False
+        for l in self.layers:
+            gc = l._gpu_compressed
+            if gc is None:
+                continue
+            has_gc = True
+            total += sum(_nb(gc[k]) for k in
+                         ("k_coeffs", "k_coeff_scale", "k_basis_q", "k_basis_scale", "k_mean",
+                          "v_packed", "sink_k", "sink_v", "win_k", "win_v"))
+            for k in ("k_basis_f16", "k_mean_f16", "v_indices", "v_centroids_f16", "v_ch_f16"):
+                if k in gc:
+                    total += _nb(gc[k])
+            for k, v in gc.items():
+                if k.endswith("_f32") and torch.is_tensor(v):
+                    total += _nb(v)
+            total += _nb(gc["v_qdata"]["ch_maxabs"])
+            if gc["v_qdata"].get("centroids") is not None:
+                total += _nb(gc["v_qdata"]["centroids"])
+            if "k_idx_buf" in gc:
+                s = gc.get("stream_n", 0) // max(gc.get("batch", 1), 1)
+                bpv = self._stream_bits / 8.0
+                for k in ("k_idx_buf", "v_idx_buf"):
+                    total += int(gc[k][:s].nelement() * bpv)
+                for k in ("k_norm_buf", "v_norm_buf"):
+                    total += _nb(gc[k][:s])
+            if "decode_k" in gc:
+                total += _nb(gc["decode_k"]) + _nb(gc["decode_v"])
+        if has_gc:
+            return total
+        return sum(_nb(l._keys) + _nb(l._values) for l in self.layers if l._keys is not None)
+
+    def device_bytes(self):
+        """Every device tensor the compressed layers keep (each counted once),
+        including the decode kernel's per-layer operands and the dequantized
+        stream rows; stream codes at their bit width, QJL signs at 1 bit."""
         total = 0
         has_gc = False
         for l in self.layers:
@@ -390,15 +430,33 @@ class Cache(HFCache):
                          ("k_coeffs", "k_coeff_scale", "k_basis_q", "k_basis_scale", "k_mean",
                           "v_packed", "sink_k", "sink_v", "win_k", "win_v"))
             total += _nb(gc["v_qdata"]["ch_maxabs"])
-            total += _nb(gc["v_qdata"]["centroids"])
+            if gc["v_qdata"].get("centroids") is not None:
+                total += _nb(gc["v_qdata"]["centroids"])
         if has_gc:
             return total
         return sum(_nb(l._keys) + _nb(l._values) for l in self.layers if l._keys is not None)
 
+    def _fp16_seq(self, with_stream):
+        gc = self.layers[0]._gpu_compressed
+        if gc is not None:
+            return (gc["n_compress"] + self._sink_tokens + self._residual_window
+                    + (gc.get("stream_n", 0) if with_stream else 0))
+        if self._compressed_layers:
+            return (next(iter(self._compressed_layers.values()))["n_compress"]
+                    + self._sink_tokens + self._residual_window)
+        if self.layers[0]._keys is not None:
+            return self.layers[0]._keys.shape[2]
+        return 0
+
     def fp16_equivalent_bytes(self):
-        # the reference counts one batch row (cache.py:518-528); all rows here,
-        # so that the ratios stay meaningful for batch > 1 (stream_n counts
-        # tokens x batch rows)
+        """fp16 K+V bytes of the same context, as the reference counts them
+        (cache.py:518-528): one batch row, plus ``stream_n`` (stream tokens x
+        batch rows) stream positions.  ``fp16_equivalent_bytes_all_rows`` counts
+        every batch row."""
+        return self._fp16_seq(True) * self._n_kv_heads * self.head_dim * 4 * self._num_layers
+
+    def fp16_equivalent_bytes_all_rows(self):
+        """fp16 K+V bytes of the whole batch (every row, stream tokens once per row)."""
         gc = self.layers[0]._gpu_compressed
         if gc is not None:
             batch = gc.get("batch", 1)
@@ -414,13 +472,20 @@ class Cache(HFCache):
         return self.fp16_equivalent_bytes() / max(self.memory_bytes(), 1)
 
     def clean_compress_ratio(self):
-        gc = self.layers[0]._gpu_compressed
-        if gc is not None:
-            seq = gc["n_compress"] + self._sink_tokens + self._residual_window
-            fp16_bytes = (gc.get("batch", 1) * seq * self._n_kv_heads * self.head_dim * 4
-                          * self._num_layers)   # all batch rows (the reference counts one)
+        """cache.py:534-539: one batch row of fp16 over the stored bytes."""
+        if self.layers[0]._gpu_compressed is not None:
+            fp16_bytes = (self._fp16_seq(False) * self._n_kv_heads * self.head_dim * 4
+                          * self._num_layers)
             return fp16_bytes / max(self.clean_memory_bytes(), 1)
         return self.compress_ratio()
+
+    def clean_compress_ratio_all_rows(self):
+        """fp16 bytes of every batch row over the stored bytes (the storage
+        compression of a batch > 1)."""
+        gc = self.layers[0]._gpu_compressed
+        if gc is not None:
+            return gc.get("batch", 1) * self.clean_compress_ratio()
+        return self.fp16_equivalent_bytes_all_rows() / max(self.memory_bytes(), 1)
 
 
 def pca_basis(centered: torch.Tensor, rank: int):

@@ -1592,6 +1592,7 @@ static int decode_attn_check(const shard_decode_args* a) {
       (a->n_stream && (!a->s_k || !a->s_v)))
     return SHARD_ERR_ARG;
   if (!tok_supported(a) || n_extra(a) > (int64_t)INT32_MAX / 4) return SHARD_ERR_SHAPE;
+  if (((uintptr_t)a->q & 15) || ((uintptr_t)a->out & 3)) return SHARD_ERR_ARG;  // vector accesses
   if (!use_tok(a) && !split_supported(a)) return SHARD_ERR_SHAPE;  // kernel 1 forced on a shape it lacks
   return SHARD_OK;
 }

@@ -483,6 +483,33 @@ def decode_attn_noalloc(call: DecodeCall) -> torch.Tensor:
     return call.out
 
 
+def bench_fp16_decode(q, k, v, n_splits=0, out=None, ws=None):
+    """The benchmark's same-GPU baseline: fp16 split-K GQA decode attention over
+    uncompressed K/V (shard_bench_fp16_decode).  q (B, H, 128) with H = 4 G,
+    k / v (B, G, T, 128) fp16 contiguous; n_splits 0 = two workgroups per CU."""
+    _require_gpu(q)
+    lib = _lib.load()
+    B, H, D = q.shape
+    G, T = k.shape[1], k.shape[2]
+    if D != 128 or H != 4 * G or tuple(k.shape) != (B, G, T, D) or k.shape != v.shape:
+        raise ValueError("bench_fp16_decode: q (B, 4G, 128), k/v (B, G, T, 128)")
+    for t in (q, k, v):
+        if t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError("bench_fp16_decode takes contiguous fp16 tensors")
+    if n_splits <= 0:
+        cus = torch.cuda.get_device_properties(q.device).multi_processor_count
+        n_splits = max(1, min((T + 31) // 32, 2 * cus // max(1, G * B)))
+    if out is None:
+        out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
+    need = lib.shard_bench_fp16_decode_workspace(B, G, n_splits)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _lib.check("shard_bench_fp16_decode", lib.shard_bench_fp16_decode(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), B, G, T, n_splits, out.data_ptr(),
+        ws.data_ptr(), ws.numel(), _stream(q)))
+    return out
+
+
 def decode_workspace_bytes(call: DecodeCall) -> int:
     return call.workspace_bytes()
 

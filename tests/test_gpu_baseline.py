@@ -1,0 +1,41 @@
+"""The benchmark's same-GPU fp16 baseline (shard_bench_fp16_decode: split-K
+GQA decode attention over uncompressed K/V) against fp64 softmax attention on
+the same fp16 inputs, to the decode bar (max-abs-err 2e-3, cosine 0.9999)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import compare
+
+pytestmark = pytest.mark.gpu
+
+
+def _fp64_attention(q, k, v):
+    """q (B, H, D), k / v (B, G, T, D) -> (B, H, D); query head h uses kv head h // (H / G)."""
+    q, k, v = (x.double().numpy() for x in (q, k, v))
+    B, H, D = q.shape
+    G = k.shape[1]
+    kk = np.repeat(k, H // G, axis=1)
+    vv = np.repeat(v, H // G, axis=1)
+    s = np.einsum("bhd,bhtd->bht", q, kk) / np.sqrt(D)
+    s -= s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("bht,bhtd->bhd", p, vv)
+
+
+@pytest.mark.parametrize("B,G,T,n_splits", [(1, 8, 8192, 0), (1, 8, 1000, 7), (2, 4, 333, 0),
+                                             (3, 2, 100, 50), (1, 8, 32, 1)])
+def test_fp16_baseline_matches_fp64(cuda, B, G, T, n_splits):
+    from shard_amd import ops
+    g = torch.Generator().manual_seed(T + B)
+    q = torch.randn(B, 4 * G, 128, generator=g).half()
+    k = (torch.randn(B, G, T, 128, generator=g) * 1.5).half()
+    v = torch.randn(B, G, T, 128, generator=g).half()
+    print(f"[fp16 baseline] B={B} G={G} T={T} n_splits={n_splits}", flush=True)
+    got = ops.bench_fp16_decode(q.to(cuda), k.to(cuda), v.to(cuda), n_splits=n_splits)
+    torch.cuda.synchronize()
+    want = _fp64_attention(q, k, v)
+    err, cos = compare(got.cpu().float().numpy(), want)
+    print(f"[fp16 baseline] max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= 2e-3 and cos >= 0.9999

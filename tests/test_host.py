@@ -42,6 +42,21 @@ def test_cache_constructs_and_prefill_glue():
     assert c.fp16_equivalent_bytes() == 100 * 8 * 128 * 4 * 2
 
 
+def test_accounting_counts_one_batch_row_like_the_reference():
+    """fp16_equivalent_bytes / compress_ratio count one batch row, as
+    cache.py:518-532 does; the *_all_rows variants count the whole batch."""
+    from shard_amd import Cache
+    c = Cache(num_layers=2)
+    k = torch.randn(3, 8, 50, 128).half()
+    c.update(k, k.clone(), 0)
+    c.update(k.clone(), k.clone(), 1)
+    one_row = 50 * 8 * 128 * 4 * 2
+    assert c.fp16_equivalent_bytes() == one_row
+    assert c.fp16_equivalent_bytes_all_rows() == 3 * one_row
+    assert c.memory_bytes() == 4 * k.numel() * 2
+    assert c.compress_ratio() == one_row / c.memory_bytes()
+
+
 def test_compress_on_cpu_fails_loudly():
     from shard_amd import Cache, ops
     c = Cache(num_layers=1)
