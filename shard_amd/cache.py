@@ -268,12 +268,19 @@ class CacheLayer(CacheLayerMixin):
         pass
 
     def reorder_cache(self, beam_idx):
+        """Beam reordering (cache.py:287-292): the dequantized K/V are rebuilt and
+        their batch rows selected, as the reference does.  The reference leaves
+        the compressed representation as it was, so the next decode step (which
+        reads it) sees the old row order; here its per-row tensors are selected
+        too, so every later step runs on the reordered beams."""
         if self._needs_decompress:
             _ = self.keys
         if self._keys is not None:
             self._keys = self._keys.index_select(0, beam_idx.to(self._keys.device))
         if self._values is not None:
             self._values = self._values.index_select(0, beam_idx.to(self._values.device))
+        if self._gpu_compressed is not None:
+            reorder_rows(self._gpu_compressed, beam_idx)
 
 
 class Cache(HFCache):
@@ -606,6 +613,39 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
         gc["v_indices_u8"] = v_indices.view(G, n_comp, ng)
     finalize_format(gc, inv_freq, dev)
     return gc
+
+
+def reorder_rows(gc: dict, beam_idx) -> None:
+    """Select the batch rows `beam_idx` of every per-row tensor of a compressed
+    layer (coefficients, V indices and channel scales, fp16 segments, stream
+    rows); the basis, mean, codebooks and decode operands are shared by the
+    rows and stay."""
+    B = gc["batch"]
+    idx = beam_idx.to(gc["k_coeffs"].device, torch.long)
+    if idx.numel() != B:
+        raise ValueError(f"reorder_cache: {idx.numel()} indices for batch {B}")
+    n = gc["n_compress"]
+    rows = lambda t, dim=0: t.index_select(dim, idx).contiguous()
+    same_pad = gc.get("k_coeffs_pad") is gc["k_coeffs"]
+    gc["k_coeffs"] = rows(gc["k_coeffs"].view(B, -1)).view(-1)
+    if same_pad:
+        gc["k_coeffs_pad"] = gc["k_coeffs"]
+    elif "k_coeffs_pad" in gc:
+        gc["k_coeffs_pad"] = rows(gc["k_coeffs_pad"].view(B, -1)).view(-1)
+    gc["v_indices"] = rows(gc["v_indices"])
+    gc["v_packed"] = gc["v_indices"].view(-1)
+    gc["v_ch_f16"] = rows(gc["v_ch_f16"])
+    qd = gc["v_qdata"]
+    qd["packed"] = gc["v_packed"]
+    qd["ch_maxabs"] = gc["v_ch_f16"].view(B * gc["n_kv"], -1)
+    for k in ("sink_k", "sink_v", "win_k", "win_v", "decode_k", "decode_v"):
+        if k in gc:
+            gc[k] = rows(gc[k])
+    for k in _STREAM_BUFS_QJL:
+        if k in gc:
+            gc[k] = rows(gc[k], 1)
+    assert gc["v_indices"].shape[2] == n
+    gc.pop("_decode_call", None)  # held pointers to the old tensors
 
 
 def finalize_format(gc: dict, inv_freq, dev):

@@ -1,0 +1,162 @@
+"""The shard Cache driven by a real (random-init) Llama on the GPU:
+
+* batch 16 (BASELINE config 5's decode shape, shorter prompt): the fused
+  decode call the patched forward makes, checked against the fp64 oracle over
+  the layer's own compressed representation (attention.py:300-343,
+  cache.py:156-181);
+* beam reordering of a compressed cache (cache.py:287-292): the dequantized
+  rows are selected as the reference does, and later decode steps read the
+  reordered compressed rows;
+* a head_dim-64 model: compression and decode through the original forward
+  on rebuilt K/V, every such layer-step counted.
+"""
+import pytest
+import torch
+
+from oracle import exact
+from tests.helpers import compare
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 512
+
+
+def _llama(dev, n_q=32, n_kv=8, hd=128, hidden=1024):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=hidden, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=n_q, num_key_value_heads=n_kv,
+                      head_dim=hd, max_position_embeddings=4096, rope_theta=500000.0)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).to(dev, torch.float16).eval()
+
+
+def _oracle_format(gc):
+    """The oracle's view (CPU) of a device-format compressed layer, stream rows
+    up to the current length."""
+    B = gc["batch"]
+    o = {k: gc[k].detach().cpu() for k in ("k_coeffs", "k_coeff_scale", "k_basis_f16", "k_mean_f16",
+                                           "v_centroids_f16", "v_ch_f16", "sink_k", "sink_v",
+                                           "win_k", "win_v")}
+    o.update({"k_coeffs_shape": gc["k_coeffs_shape"], "n_compress": gc["n_compress"], "batch": B,
+              "compress_start": gc["compress_start"], "v_idx_full": gc["v_indices"].cpu()})
+    s = gc.get("stream_n", 0) // B
+    if s:
+        o.update({"stream_n": gc["stream_n"], "signs": gc["signs"].cpu().numpy(),
+                  "stream_codebook": gc["stream_codebook"].cpu().numpy()})
+        for k in ("k_idx_buf", "v_idx_buf", "k_norm_buf", "v_norm_buf"):
+            o[k] = gc[k][:s].cpu().numpy()
+    if "decode_k" in gc:
+        o["decode_k"], o["decode_v"] = gc["decode_k"].cpu(), gc["decode_v"].cpu()
+    return o
+
+
+def test_batch16_cache_decode_matches_oracle(cuda, monkeypatch):
+    from shard_amd import Cache, attention, enable_llama_fused_attention
+    model = _llama(cuda)
+    assert enable_llama_fused_attention(model)
+    seen = []
+    inner = attention.fused_attention_compressed
+
+    def record(q, layer, pos_q, inv, mask=None):
+        out = inner(q, layer, pos_q, inv, mask)
+        if layer.layer_idx == 1:
+            p = int(pos_q.reshape(-1)[-1].item()) if torch.is_tensor(pos_q) else int(pos_q)
+            seen.append((q.detach().cpu(), p, out.detach().cpu(),
+                         _oracle_format(layer._gpu_compressed), inv.cpu()))
+        return out
+    monkeypatch.setattr(attention, "fused_attention_compressed", record)
+    g = torch.Generator().manual_seed(3)
+    B, T = 16, 600
+    ids = torch.randint(0, VOCAB, (B, T), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (B, 3), generator=g).to(cuda)
+    cache = Cache.from_model(model)
+    cache._streaming = True
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        for s in range(steps.shape[1]):
+            model(steps[:, s:s + 1], past_key_values=cache, use_cache=True)
+    assert len(seen) == 3 and cache.layers[1]._gpu_compressed["batch"] == B
+    for i, (q, pos_q, out, gc, inv) in enumerate(seen):
+        assert pos_q == T + i and gc["stream_n"] == B * (i + 1)
+        want = exact.decode_attention(q.float().numpy().reshape(B, 32, 1, 128), gc, 8, pos_q,
+                                      inv.numpy())
+        err, cos = compare(out.float().numpy().reshape(want.shape), want)
+        print(f"[batch16 cache] step {i} pos_q={pos_q} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= 2e-3 and cos >= 0.9999
+
+
+def test_reorder_cache_selects_compressed_rows(cuda):
+    from shard_amd import Cache, attention, enable_llama_fused_attention
+    model = _llama(cuda)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(4)
+    B = 4
+    ids = torch.randint(0, VOCAB, (B, 400), generator=g).to(cuda)
+    tok = torch.randint(0, VOCAB, (B, 1), generator=g).to(cuda)
+    caches = []
+    for _ in range(2):
+        c = Cache.from_model(model)
+        c._streaming = True
+        with torch.no_grad():
+            model(ids, past_key_values=c, use_cache=True)
+            model(tok, past_key_values=c, use_cache=True)   # compress + one stream token
+        caches.append(c)
+    base, beam = caches
+    order = torch.tensor([2, 0, 3, 1])
+    layer = beam.layers[1]
+    want_keys = base.layers[1].keys.index_select(0, order.to(cuda))
+    beam.reorder_cache(order)   # the HF Cache entry point: every layer
+    # the reference's semantics for the dequantized rows
+    assert torch.equal(layer._keys, want_keys)
+    # the next fused step reads the reordered compressed rows: row b of the
+    # reordered cache equals row order[b] of the original, bit for bit
+    q = torch.randn(B, 32, 1, 128, generator=g).half().to(cuda)
+    inv = base._rope_inv_freq
+    pos = 400 + 1
+    with torch.no_grad():
+        a = attention.fused_attention_compressed(q[order.to(cuda)], layer, pos, inv)
+        b = attention.fused_attention_compressed(q, base.layers[1], pos, inv)
+    assert torch.equal(a.view(torch.int16), b[order.to(cuda)].view(torch.int16))
+    # and the rebuilt K/V of the reordered layer are the original rows, reordered
+    layer._needs_decompress = True
+    assert torch.equal(layer.keys, base.layers[1].keys.index_select(0, order.to(cuda)))
+
+
+def test_head_dim_64_model_compresses_and_decodes(cuda):
+    """A shape the fused kernel does not take (head_dim 64): Cache.compress
+    builds the format without the fused operands, decode steps run the original
+    forward over kv_reconstruct's K/V, and each layer-step is counted."""
+    from transformers.models.llama.modeling_llama import LlamaAttention
+    from shard_amd import Cache, enable_llama_fused_attention
+    model = _llama(cuda, n_q=8, n_kv=2, hd=64, hidden=512)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, VOCAB, (1, 300), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (1, 2), generator=g).to(cuda)
+
+    def run():
+        c = Cache.from_model(model)
+        c._streaming = True
+        out = []
+        with torch.no_grad():
+            model(ids, past_key_values=c, use_cache=True)
+            for s in range(steps.shape[1]):
+                out.append(model(steps[:, s:s + 1], past_key_values=c, use_cache=True).logits.float())
+        return torch.cat(out, 1), c
+
+    got, cache = run()
+    gc = cache.layers[0]._gpu_compressed
+    assert gc is not None and gc["head_dim"] == 64 and gc["decode_prep"] is None
+    # layer 0 of the first decode step is not compressed yet when the forward
+    # routes it (its own cache update compresses every layer), so it is not a
+    # fallback; every later layer-step is
+    assert cache._fused_fallbacks == 2 * steps.shape[1] - 1
+    assert "head_dim=64" in cache._last_fused_fallback
+    patched = LlamaAttention.forward
+    try:
+        LlamaAttention.forward = patched.__wrapped__
+        want, _ = run()
+    finally:
+        LlamaAttention.forward = patched
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want)
