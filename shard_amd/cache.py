@@ -13,7 +13,11 @@ CacheLayer: 64-292):
   fused decode attention  attention.fused_attention_compressed (HIP kernel)
   unfused consumers       layer.keys / layer.values rebuild fp16 K/V on the GPU
                           (_ensure_dequant, cache.py:87-124; HIP reconstruct)
-All device work runs in HIP kernels of libshard_hip.so; CPU tensors are rejected.
+The compression's per-token work runs in HIP kernels of libshard_hip.so (undo
+RoPE and centring, projection, int4 chain, Hadamard and VQ assignment, k-means
+update); torch computes the column mean and the covariance GEMM of the fp16
+operand, and the host a float64 eigendecomposition of the (p, p) covariance.
+CPU tensors are rejected.
 """
 import torch
 from transformers.cache_utils import Cache as HFCache, CacheLayerMixin
@@ -495,6 +499,51 @@ class Cache(HFCache):
         return self.fp16_equivalent_bytes_all_rows() / max(self.memory_bytes(), 1)
 
 
+def _undo_rope_mean(k_full: torch.Tensor, start: int, end: int, inv_freq,
+                    chunk: int = 2048) -> torch.Tensor:
+    """Column mean (over batch rows and tokens [start, end)) of the keys with
+    RoPE undone, in fp32 as cache.py:370-374 computes it, a token chunk at a
+    time; (G * D,) with column g * D + d."""
+    B, G, _, D = k_full.shape
+    acc = torch.zeros(G, D, dtype=torch.float32, device=k_full.device)
+    for t0 in range(start, end, chunk):
+        t1 = min(end, t0 + chunk)
+        km = k_full[:, :, t0:t1, :].float()
+        if inv_freq is not None:
+            km = host.undo_rope(km, torch.arange(t0, t1, device=k_full.device),
+                                inv_freq.to(k_full.device))
+        acc += km.sum(dim=(0, 2))
+    return acc.reshape(-1) / (B * (end - start))
+
+
+def _covariance(x16: torch.Tensor, chunk: int = 1 << 15) -> torch.Tensor:
+    """X^T X / n of the fp16 rows in fp32, a row chunk at a time (no fp32 copy
+    of the whole operand)."""
+    n, p = x16.shape
+    cov = torch.zeros(p, p, dtype=torch.float32, device=x16.device)
+    for i in range(0, n, chunk):
+        xc = x16[i:i + chunk].float()
+        cov.addmm_(xc.t(), xc)
+    return cov / n
+
+
+def _column_energy(x16: torch.Tensor, basis: torch.Tensor, chunk: int = 1 << 15) -> torch.Tensor:
+    """mean over rows of (x @ basis)^2 (the variances along a supplied basis)."""
+    acc = torch.zeros(basis.shape[1], dtype=torch.float32, device=x16.device)
+    for i in range(0, x16.shape[0], chunk):
+        acc += (x16[i:i + chunk].float() @ basis).pow(2).sum(dim=0)
+    return acc / x16.shape[0]
+
+
+def pca_basis_cov(cov: torch.Tensor, rank: int):
+    """Top-`rank` eigenvectors of a (p, p) covariance and their eigenvalues, by
+    a float64 symmetric eigendecomposition on the host (deterministic)."""
+    evals, evecs = torch.linalg.eigh(cov.double().cpu())
+    evals = evals.flip(0)[:rank].clamp(min=0.0)
+    evecs = evecs.flip(1)[:, :rank]
+    return evecs.float().to(cov.device), evals.float().to(cov.device)
+
+
 def pca_basis(centered: torch.Tensor, rank: int):
     """Top-`rank` principal directions of the centered rows and their variances
     (S^2 / n), the quantities _compress_k takes from svd_lowrank(q=rank,
@@ -503,11 +552,7 @@ def pca_basis(centered: torch.Tensor, rank: int):
     deterministically: the fp32 covariance X^T X / n on the GPU (one GEMM), then
     a float64 symmetric eigendecomposition of the (p, p) matrix on the host."""
     n = centered.shape[0]
-    cov = (centered.t() @ centered) / n
-    evals, evecs = torch.linalg.eigh(cov.double().cpu())
-    evals = evals.flip(0)[:rank].clamp(min=0.0)
-    evecs = evecs.flip(1)[:, :rank]
-    return evecs.float().to(centered.device), evals.float().to(centered.device)
+    return pca_basis_cov((centered.t() @ centered) / n, rank)
 
 
 def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li: int,
@@ -528,26 +573,23 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     inv_freq = cache._rope_inv_freq
     torch.manual_seed(42 + li)
 
-    # ---- K: undo RoPE (fp32), PCA basis, DP bits, int8 basis
-    k_mid = k_full[:, :, start:end, :].float()
-    if inv_freq is not None:
-        pos = torch.arange(start, end, device=dev)
-        k_mid = host.undo_rope(k_mid, pos, inv_freq.to(dev))
+    # ---- K: undo RoPE and centring (shard_k_prepare: fp32 math, fp16 rows of
+    # the projection operand), PCA basis, DP bits, int8 basis
     p_dim = G * D
-    flat = k_mid.permute(0, 2, 1, 3).reshape(B * n_comp, p_dim)
-    del k_mid
-    n = flat.shape[0]
-    mean = flat.mean(dim=0)
+    n = B * n_comp
+    invf = (inv_freq.to(dev, torch.float32) if inv_freq is not None
+            else torch.zeros(D // 2, dtype=torch.float32, device=dev))  # phase 0: no rotation
+    k_full = k_full.contiguous()
+    mean = _undo_rope_mean(k_full, start, end, inv_freq)
+    centered = ops.k_prepare(k_full, start, n_comp, invf, mean)   # (n, p_dim) fp16
     rank = min(cache._max_rank_k, p_dim, n - 1)
-    centered = flat - mean
-    del flat
     if basis is None and cache._basis_override is not None:
         basis = cache._basis_override.get(li)
     if basis is None:
-        basis, eig = pca_basis(centered, rank)
+        basis, eig = pca_basis_cov(_covariance(centered), rank)
     else:
         basis = basis.to(dev, torch.float32)[:, :rank]
-        eig = (centered @ basis).pow(2).mean(dim=0)
+        eig = _column_energy(centered, basis)
     budget = max(64, int(p_dim * 16 / cache._k_target_cr))
     alloc = host.dp_bit_allocation(eig, budget)
     keep = sum(1 for b in alloc if b > 0)
@@ -565,7 +607,7 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     keep32 = ((keep + 31) // 32) * 32
     bt = torch.zeros(keep32, p_dim, dtype=torch.float16, device=dev)
     bt[:keep] = basis_deq.t().half()
-    proj = ops.pca_project(centered.half(), bt)[:, :keep].contiguous()
+    proj = ops.pca_project(centered, bt)[:, :keep].contiguous()
     del centered
     bits = torch.tensor(alloc, dtype=torch.int32, device=dev)
     chain = ops.int4_quant_pack(proj, bits)
