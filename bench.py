@@ -386,33 +386,34 @@ def _to(x, dev):
     return x
 
 
-def save_layer(dev, T, path):
+def save_layer(dev, T, path, batch=1):
     """Compress the benchmark layer once and store it (the PMC runs load it, so
-    the profiled process runs no SVD)."""
-    fmt, _, _ = build_layer(T, dev)
+    the profiled process runs no compression)."""
+    fmt, _, _ = build_layer(T, dev) if batch == 1 else build_layer_batch(T, batch, dev)
     torch.save(_to(fmt, "cpu"), path)
-    return {"saved_layer": path, "context": T}
+    return {"saved_layer": path, "context": T, "batch": batch}
 
 
-def pmc_workload(dev, T, calls=200, layer_path=None):
+def pmc_workload(dev, T, calls=200, layer_path=None, batch=1):
     """Eager decode calls rotating over cold copies of the layer: the workload
-    profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (no graph replay)."""
+    profiled with rocprofv3 --pmc (no graph replay)."""
     from shard_amd import ops, bench_data
     if layer_path:
         fmt = _to(torch.load(layer_path, weights_only=True), dev)
     else:
-        fmt, _, _ = build_layer(T, dev)
-    q = bench_data.make_q().to(dev).view(1, 32, 128)
-    n_copies = max(2, math.ceil(2 * 256e6 / algorithmic_bytes(fmt["n_compress"], fmt["rank_pad"])))
+        fmt, _, _ = build_layer(T, dev) if batch == 1 else build_layer_batch(T, batch, dev)
+    batch = fmt["batch"]
+    q = bench_data.make_q(batch).to(dev).view(batch, 32, 128)
+    nbytes = algorithmic_bytes(fmt["n_compress"], fmt["rank_pad"], batch=batch)
+    n_copies = max(2, math.ceil(2 * 256e6 / nbytes))
     copies = [fmt] + [clone_format(fmt) for _ in range(n_copies - 1)]
     cl = [ops.make_decode_args(q, c, T, None) for c in copies]
     ws = ops.decode_workspace(cl[0])
     for i in range(calls):
         ops.decode_attn(cl[i % n_copies], ws)
     torch.cuda.synchronize()
-    return {"pmc_workload": {"context": T, "calls": calls, "copies": n_copies,
-                             "algorithmic_bytes_per_call": algorithmic_bytes(fmt["n_compress"],
-                                                                             fmt["rank_pad"])}}
+    return {"pmc_workload": {"context": T, "batch": batch, "calls": calls, "copies": n_copies,
+                             "algorithmic_bytes_per_call": nbytes}}
 
 
 def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
@@ -613,6 +614,8 @@ def main():
     ap.add_argument("--save-layer", default=None,
                     help="compress the --ctx layer, save it to this path and exit")
     ap.add_argument("--layer", default=None, help="--pmc-workload: load the layer saved here")
+    ap.add_argument("--batch", type=int, default=1, help="--save-layer / --pmc-workload: batch rows")
+    ap.add_argument("--calls", type=int, default=200, help="--pmc-workload: decode calls")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the compressed-KV decode path "
@@ -637,10 +640,11 @@ def main():
                              args.e2e_layers)), flush=True)
         return
     if args.save_layer:
-        print(json.dumps(save_layer(dev, args.ctx, args.save_layer)), flush=True)
+        print(json.dumps(save_layer(dev, args.ctx, args.save_layer, args.batch)), flush=True)
         return
     if args.pmc_workload:
-        print(json.dumps(pmc_workload(dev, args.ctx, layer_path=args.layer)), flush=True)
+        print(json.dumps(pmc_workload(dev, args.ctx, calls=args.calls, layer_path=args.layer,
+                                      batch=args.batch)), flush=True)
         return
 
     def measure(T, batch=1, baselines=()):
