@@ -851,7 +851,7 @@ struct TokLds {
   uint2 cb[256];                        // VQ codebook, 4 x fp16 per entry
   uint32_t rc[64][32];                  // [pair][col]: fp16 (cos, sin)(col theta) / 16
   uint16_t qr[kTokWaves][NQ + 1][2][64];  // per wave: R(-phi0) q (fp16, score k order); row NQ = 0
-  uint32_t pb[kTokWaves][NQ + 1][2][8];   // per wave: fp16 numerators by token parity; row NQ: lanes with no head
+  uint16_t pa[kTokWaves][NQ + 1][32];     // per wave: fp16 numerators [head][token]; row NQ stays 0
   float xp[kTokWaves][32][NQ + 1];        // per wave: numerators of an extra tile, [token][head]
 };
 
@@ -926,11 +926,15 @@ void k_decode_tok(const TokParams p) {
   const __amdgpu_buffer_rsrc_t rmask = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.mask ? p.mask + (int64_t)b * p.mask_stride : p.ws_m), (short)0,
       p.mask ? (int)(n_keys * 4) : 0, kBufWord3);
-  const int vj = lane & 31, vpar = lane >> 5;  // V stage: subvector, token parity
+  // V stage on MFMA 16x16x32 f16: rows = query heads (NQ of 16 used), columns
+  // = 16 subvectors, k = the tile's 32 tokens.  Lane (vn = lane % 16, vt =
+  // lane / 16) holds tokens 8 vt .. 8 vt + 7 of subvector vn + 16 jg, jg = 0, 1.
+  const int vn = lane & 15, vt = lane >> 4;
   auto load_vidx = [&](int k, uint32_t (&vi_)[16]) {
-    const int voff = (32 * k + vpar) * 32 + vj;
+    const int voff = (32 * k + 8 * vt) * 32 + vn;
 #pragma unroll
-    for (int m = 0; m < 16; ++m) vi_[m] = __builtin_amdgcn_raw_buffer_load_b8(rvidx, voff + 64 * m, 0, 0);
+    for (int m = 0; m < 16; ++m)
+      vi_[m] = __builtin_amdgcn_raw_buffer_load_b8(rvidx, voff + 32 * (m & 7) + 16 * (m >> 3), 0, 0);
   };
   const float2* t2tab = p.rope + kRopeT2 + lane;  // lane = pair
   const float2* t1tab = p.rope + kRopeT1 + lane;
@@ -1028,7 +1032,8 @@ void k_decode_tok(const TokParams p) {
   __syncthreads();
 
   const float sc = kLog2e * rsqrtf((float)kHD);
-  float m_run[NE], l_part[NE], vacc[NQ][4];
+  float m_run[NE], l_part[NE];
+  float4v vacc[2][4];  // [subvector group][component]: rows (heads) 4 vt + i, column vn
   float2 xacc[NQ];
 #pragma unroll
   for (int i = 0; i < NE; ++i) {
@@ -1036,11 +1041,23 @@ void k_decode_tok(const TokParams p) {
     l_part[i] = 0.f;
   }
 #pragma unroll
-  for (int h = 0; h < NQ; ++h) {
+  for (int h = 0; h < NQ; ++h) xacc[h] = make_float2(0.f, 0.f);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) vacc[h][e] = 0.f;
-    xacc[h] = make_float2(0.f, 0.f);
-  }
+  for (int jg = 0; jg < 2; ++jg)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vacc[jg][e] = float4v{0.f, 0.f, 0.f, 0.f};
+  // the rescale of the value sums by the rows' softmax factors: row 4 vt + i
+  // holds a head only for vt = 0, i < NQ (other rows are zero)
+  auto rescale_v = [&](const float (&al)[NQ]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = al[i < NQ ? i : NQ - 1];
+#pragma unroll
+      for (int jg = 0; jg < 2; ++jg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vacc[jg][e][i] *= a;
+    }
+  };
 
   // Online softmax of one tile's scores (lanes: token col; element i of lane
   // half hh: head 4 hh + i).  Returns the rescale factor of head h in al[h]
@@ -1139,38 +1156,31 @@ void k_decode_tok(const TokParams p) {
     // 3. online softmax of the query heads over the tile
     float al[NQ];
     softmax(sacc, p.n_comp - t0, p.n_sink + t0 + col, al,
-            [&](int row, float pv) { ((uint16_t*)&L.pb[w][row][col & 1][0])[col >> 1] = f2h(pv); });
+            [&](int row, float pv) { L.pa[w][row][col] = f2h(pv); });
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    // 4. VQ values of the tile: lane (subvector vj, parity vpar) takes tokens
-    //    2 m + vpar; dot2 over the token pairs (4 u + vpar, 4 u + 2 + vpar)
+    // 4. VQ values of the tile on MFMA: A = the numerators of the query heads
+    //    (row vn, tokens 8 vt ..), B_e = component e of the codebook entries of
+    //    the lane's 8 tokens in subvector vn + 16 jg
+    rescale_v(al);
+    const half8 pa8 = __builtin_bit_cast(half8, *(const uint4*)&L.pa[w][vn < NQ ? vn : NQ][8 * vt]);
 #pragma unroll
-    for (int h = 0; h < NQ; ++h)
+    for (int jg = 0; jg < 2; ++jg) {
+      uint2 en[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vacc[h][e] *= al[h];
+      for (int t = 0; t < 8; ++t) en[t] = L.cb[vi[8 * jg + t]];
 #pragma unroll
-    for (int ub = 0; ub < 2; ++ub) {  // token pairs u = 4 ub .. 4 ub + 3: one 16-byte numerator load per head
-      uint4 pq[NQ];
-#pragma unroll
-      for (int h = 0; h < NQ; ++h) pq[h] = *(const uint4*)&L.pb[w][h][vpar][4 * ub];
-#pragma unroll
-      for (int uu = 0; uu < 4; ++uu) {
-        const int u = 4 * ub + uu;
-        const uint2 ca = L.cb[vi[2 * u]], cbb = L.cb[vi[2 * u + 1]];
-        half2v c2[4];
-        c2[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.x, ca.x, 0x05040100u));
-        c2[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.x, ca.x, 0x07060302u));
-        c2[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.y, ca.y, 0x05040100u));
-        c2[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cbb.y, ca.y, 0x07060302u));
-#pragma unroll
-        for (int h = 0; h < NQ; ++h) {
-          const uint32_t pw = uu == 0 ? pq[h].x : uu == 1 ? pq[h].y : uu == 2 ? pq[h].z : pq[h].w;
-          const half2v p2 = __builtin_bit_cast(half2v, pw);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) vacc[h][e] = __builtin_amdgcn_fdot2(p2, c2[e], vacc[h][e], false);
-        }
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        uint4 bw;
+        bw.x = __builtin_amdgcn_perm(e < 2 ? en[1].x : en[1].y, e < 2 ? en[0].x : en[0].y, sel);
+        bw.y = __builtin_amdgcn_perm(e < 2 ? en[3].x : en[3].y, e < 2 ? en[2].x : en[2].y, sel);
+        bw.z = __builtin_amdgcn_perm(e < 2 ? en[5].x : en[5].y, e < 2 ? en[4].x : en[4].y, sel);
+        bw.w = __builtin_amdgcn_perm(e < 2 ? en[7].x : en[7].y, e < 2 ? en[6].x : en[6].y, sel);
+        vacc[jg][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa8, __builtin_bit_cast(half8, bw),
+                                                             vacc[jg][e], 0, 0, 0);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // pb is rewritten by the next tile
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // pa is rewritten by the next tile
   };
 
   // ---- one extra tile (relative index x): fp16 K (RoPE applied) and V rows
@@ -1213,9 +1223,8 @@ void k_decode_tok(const TokParams p) {
     for (int h = 0; h < NQ; ++h) {
       xacc[h].x *= al[h];
       xacc[h].y *= al[h];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vacc[h][e] *= al[h];
     }
+    rescale_v(al);
 #pragma unroll
     for (int t = 0; t < 32; ++t) {
       const half2v hv = __builtin_bit_cast(half2v, vx[t]);
@@ -1248,19 +1257,14 @@ void k_decode_tok(const TokParams p) {
   // ---- merge the waves; per query head: ch, one inverse FWHT, plain part
 #pragma unroll
   for (int i = 0; i < NE; ++i) l_part[i] = half32_reduce(l_part[i], OpAdd());
-#pragma unroll
-  for (int h = 0; h < NQ; ++h)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float a, c;
-      perm32_swap(vacc[h][e], a, c);
-      vacc[h][e] = a + c;  // the two token parities
-    }
   __syncthreads();  // every wave is done with the image the merge buffer overlays
-  if (lane < 32) {
+  if (vt == 0) {  // rows 0..3 of the value sums: head i, subvector vn + 16 jg
 #pragma unroll
-    for (int h = 0; h < NQ; ++h)
-      *(float4*)&L.u.red.r[w][h][4 * vj] = make_float4(vacc[h][0], vacc[h][1], vacc[h][2], vacc[h][3]);
+    for (int i = 0; i < NQ; ++i)
+#pragma unroll
+      for (int jg = 0; jg < 2; ++jg)
+        *(float4*)&L.u.red.r[w][i][4 * (vn + 16 * jg)] =
+            make_float4(vacc[jg][0][i], vacc[jg][1][i], vacc[jg][2][i], vacc[jg][3][i]);
   }
 #pragma unroll
   for (int h = 0; h < NQ; ++h) *(float2*)&L.u.red.pl[w][h][2 * lane] = xacc[h];
