@@ -370,6 +370,7 @@ def prefill(dev, layers=32, batch=4, T=8192):
     flops = 2.0 * batch * T * G * D * R * layers
     return {"metric": "prefill compression tokens/s (BASELINE config 4)", "unit": "tokens/s",
             "value": round(batch * T / total_s, 1),
+            "layer_tokens_per_s": round(layers * batch * T / total_s, 1),
             "config": {"layers": layers, "batch": batch, "tokens": T, "rank": R,
                        "data": "synthetic, generated on device"},
             "ms_total": round(total_s * 1000.0, 3),

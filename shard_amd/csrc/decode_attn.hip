@@ -1100,48 +1100,45 @@ void k_decode_tok(const TokParams p) {
       L.qr[w][h][0][kq] = f2h(qa[h] * ph_c + qb[h] * ph_s);
       L.qr[w][h][1][kq] = f2h(qb[h] * ph_c - qa[h] * ph_s);
     }
-    // 2. coefficients -> MFMA B operands, once for the 4 row blocks
-    half8 Bc[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) Bc[s] = nib8_to_mfma(cw[s]);
+    // 2. rebuild, k-step major: per k-step one converted coefficient operand
+    //    feeds the 4 row blocks' independent accumulators.  The A operands
+    //    stream from LDS through a ring of kRing registers, kRing reads ahead
+    //    of the MFMA that consumes them (the order is pinned: the scheduler
+    //    otherwise sinks each read to its MFMA and waits for it there).
     const float16v zero16 = {};
     float16v sacc = zero16;
-    // Two row blocks at a time: their MFMA chains interleave (independent
-    // accumulators) and share each converted coefficient operand.  The A
-    // operands stream from LDS through a ring of kRing registers, so kRing
-    // reads are in flight ahead of the MFMA that consumes them.
-    constexpr int kRing = 4;
-    constexpr int NA = 4 * (KS + 1);  // A operands per tile, in (pair, k-step, block) order
+    constexpr int kRing = 8;
+    constexpr int NA = 4 * (KS + 1);  // A operands per tile, in (k-step, block) order
     auto a_at = [&](int j) {
-      const int qp = j / (2 * (KS + 1)), rem = j % (2 * (KS + 1));
-      const int s = rem >> 1, rb = 2 * qp + (rem & 1);
+      const int s = j >> 2, rb = j & 3;
       return __builtin_bit_cast(half8, L.u.A[rb][s == 0 ? KS : s - 1][lane]);
     };
     half8 ring[kRing];
 #pragma unroll
     for (int j = 0; j < kRing; ++j) ring[j] = a_at(j);
+    __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);
+    float16v acc[4];
 #pragma unroll
-    for (int qp = 0; qp < 2; ++qp) {
-      float16v acc[2];
+    for (int s = 0; s <= KS; ++s) {
+      const half8 bs = s == 0 ? one8 : nib8_to_mfma(cw[s - 1]);
 #pragma unroll
-      for (int s = 0; s <= KS; ++s) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int j = (qp * (KS + 1) + s) * 2 + r;
-          const half8 a = ring[j % kRing];
-          if (j + kRing < NA) ring[j % kRing] = a_at(j + kRing);
-          acc[r] = s == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_f16(a, one8, zero16, 0, 0, 0)
-                          : __builtin_amdgcn_mfma_f32_32x32x16_f16(a, Bc[s - 1], acc[r], 0, 0, 0);
-        }
+      for (int rb = 0; rb < 4; ++rb) {
+        const int j = 4 * s + rb;
+        const half8 a = ring[j % kRing];
+        if (j + kRing < NA) ring[j % kRing] = a_at(j + kRing);
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bs, s == 0 ? zero16 : acc[rb], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (j + kRing < NA) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
+    }
+    {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int rb = 2 * qp + r;
+      for (int rb = 0; rb < 4; ++rb) {
         half8 b0, b1;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const half2v rr = __builtin_bit_cast(half2v, L.rc[16 * rb + pr[i]][col]);
-          const float c = acc[r][i], d = acc[r][i + 8];
+          const float c = acc[rb][i], d = acc[rb][i + 8];
           // c cos - d sin, d cos + c sin: fp32 products and sums, one fp16 rounding
           b0[i] = (half_t)__builtin_fmaf(c, (float)rr[0], -__builtin_fmaf(d, (float)rr[1], 0.0f));
           b1[i] = (half_t)__builtin_fmaf(d, (float)rr[0], __builtin_fmaf(c, (float)rr[1], 0.0f));
