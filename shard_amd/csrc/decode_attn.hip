@@ -12,8 +12,9 @@
 //     extra tokens (at most 2048) into one more partial row per query head.
 //   k_decode_tok (token-tiled)  grid = n_splits * n_kv * query groups * B,
 //     512-thread workgroups, one per CU, 1, 2 or 4 query heads per workgroup;
-//     the kv head's basis operand image sits in LDS and each wave takes whole
-//     tiles (all 128 rows) from an LDS counter, with its own softmax state.
+//     the kv head's basis operand image sits in LDS and wave w takes whole
+//     tiles (all 128 rows) w, w + 8, w + 16, ... of the split, with its own
+//     softmax state (a static map: results do not depend on wave timing).
 //     Every split owns a run of cost units (a compressed tile costs 3, a tile
 //     of 32 extra tokens 1), so any number of extra tokens spreads over the
 //     last splits.  The waves merge once at the end.
@@ -50,6 +51,7 @@ constexpr int kGQA = 4;           // query heads per kv head
 constexpr int kMaxExtra = 2048;   // sink + window + decode + stream tokens per call
 constexpr int kMaxSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyTau = 8.f;   // token-tiled softmax: numerators stay below 2^kLazyTau
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw, unswizzled access (gfx9)
 // rope tables of the per-layer operands (k_decode_prepare): in-tile column
 // phases, the per-tile step, and the token-tiled kernel's two tile-offset tables
@@ -1060,26 +1062,47 @@ void k_decode_tok(const TokParams p) {
   };
 
   // Online softmax of one tile's scores (lanes: token col; element i of lane
-  // half hh: head 4 hh + i).  Returns the rescale factor of head h in al[h]
-  // (wave-uniform) and stores the numerators through put(row, pv), row NQ for
-  // lanes that hold no head (every lane stores: no branch).
-  auto softmax = [&](const float16v& sacc, int n_valid, int mpos, float (&al)[NQ], auto put) {
+  // half hh: head 4 hh + i) with a lazily moved reference max.  The numerators
+  // are 2^(s - m_run); m_run moves (with the rescale of l and of the value
+  // sums) only when some score of the tile exceeds it by more than kLazyTau,
+  // so every numerator stays below 2^kLazyTau (exact range for fp16) and most
+  // tiles skip the cross-lane max and the rescale.  The partial rows carry
+  // m_run as their max, so the merge is unchanged.  Returns whether m_run
+  // moved (wave-uniform); then al[h] holds head h's rescale factor.  Stores
+  // the numerators through put(row, pv), row NQ for lanes that hold no head
+  // (every lane stores: no branch).
+  auto softmax = [&](const float (&sv)[NE], int n_valid, int mpos, float (&al)[NQ], auto put) {
     const bool tok_ok = col < n_valid;
     const float madd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rmask, 4 * mpos, 0, 0));
+    float s[NE];
+    bool over = false;
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
       const int h = 4 * hh + i;
-      const float s = (tok_ok && h < NQ) ? sacc[i] * sc + madd * kLog2e : -INFINITY;
-      const float m_new = fmaxf(m_run[i], half32_reduce(s, OpMax()));
-      const float a = m_new == -INFINITY ? 1.f : fast_exp2(m_run[i] - m_new);
-      const float pv = s == -INFINITY ? 0.f : fast_exp2(s - m_new);
-      l_part[i] = l_part[i] * a + pv;
-      m_run[i] = m_new;
-      put(h < NQ ? h : NQ, pv);
-#pragma unroll
-      for (int hf = 0; hf < (NQ > 4 ? 2 : 1); ++hf)
-        if (4 * hf + i < NQ) al[4 * hf + i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32 * hf));
+      s[i] = (tok_ok && h < NQ) ? sv[i] * sc + madd * kLog2e : -INFINITY;
+      over |= s[i] > m_run[i] + kLazyTau;
     }
+    const bool moved = __builtin_amdgcn_ballot_w64(over) != 0;
+    if (moved) {
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        const float m_new = fmaxf(m_run[i], half32_reduce(s[i], OpMax()));
+        const float a = m_new == -INFINITY ? 1.f : fast_exp2(m_run[i] - m_new);
+        l_part[i] *= a;
+        m_run[i] = m_new;
+#pragma unroll
+        for (int hf = 0; hf < (NQ > 4 ? 2 : 1); ++hf)
+          if (4 * hf + i < NQ) al[4 * hf + i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32 * hf));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int h = 4 * hh + i;
+      const float pv = s[i] == -INFINITY ? 0.f : fast_exp2(s[i] - m_run[i]);
+      l_part[i] += pv;
+      put(h < NQ ? h : NQ, pv);
+    }
+    return moved;
   };
 
   // ---- one compressed tile (relative index k) on this wave
@@ -1151,14 +1174,16 @@ void k_decode_tok(const TokParams p) {
       }
     }
     // 3. online softmax of the query heads over the tile
-    float al[NQ];
-    softmax(sacc, p.n_comp - t0, p.n_sink + t0 + col, al,
-            [&](int row, float pv) { L.pa[w][row][col] = f2h(pv); });
+    float sv[NE], al[NQ];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) sv[i] = sacc[i];
+    const bool moved = softmax(sv, p.n_comp - t0, p.n_sink + t0 + col, al,
+                               [&](int row, float pv) { L.pa[w][row][col] = f2h(pv); });
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     // 4. VQ values of the tile on MFMA: A = the numerators of the query heads
     //    (row vn, tokens 8 vt ..), B_e = component e of the codebook entries of
     //    the lane's 8 tokens in subvector vn + 16 jg
-    rescale_v(al);
+    if (moved) rescale_v(al);
     const half8 pa8 = __builtin_bit_cast(half8, *(const uint4*)&L.pa[w][vn < NQ ? vn : NQ][8 * vt]);
 #pragma unroll
     for (int jg = 0; jg < 2; ++jg) {
@@ -1213,15 +1238,19 @@ void k_decode_tok(const TokParams p) {
     float16v sacc = {};
 #pragma unroll
     for (int st = 0; st < 8; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[st], Bk[st], sacc, 0, 0, 0);
-    float al[NQ];
-    softmax(sacc, n_xtok - x0, mp, al, [&](int row, float pv) { L.xp[w][col][row] = pv; });
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    float sv[NE], al[NQ];
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      xacc[h].x *= al[h];
-      xacc[h].y *= al[h];
+    for (int i = 0; i < NE; ++i) sv[i] = sacc[i];
+    const bool moved = softmax(sv, n_xtok - x0, mp, al, [&](int row, float pv) { L.xp[w][col][row] = pv; });
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (moved) {
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        xacc[h].x *= al[h];
+        xacc[h].y *= al[h];
+      }
+      rescale_v(al);
     }
-    rescale_v(al);
 #pragma unroll
     for (int t = 0; t < 32; ++t) {
       const half2v hv = __builtin_bit_cast(half2v, vx[t]);

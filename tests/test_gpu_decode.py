@@ -175,6 +175,26 @@ def test_decode_additive_mask(cuda, kernel):
 
 
 @pytest.mark.parametrize("kernel", KERNELS)
+def test_decode_softmax_max_moves_late(cuda, kernel):
+    """Scores that keep rising along the context (an additive ramp, then steps of
+    +5.4 and +30 in natural-log units): the token-tiled kernel's reference max
+    then moves in later tiles (rescaling the sums it holds) and, between moves,
+    numerators come within 2^0.2 of their 2^8 bound."""
+    gc, inv = random_layer(n_comp=4000, n_stream=4, seed=11)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(5)).half()
+    T = 4 + 4000 + 64 + 4
+    mask = np.zeros((1, T), np.float32)
+    mask[0, 4:4004] = np.linspace(0.0, 60.0, 4000, dtype=np.float32)
+    mask[0, 2500:2600] += 5.4      # log2 7.8 above its neighbours: no move, large numerators
+    mask[0, 3300:3310] += 30.0     # forces a move inside the compressed span
+    want = exact.decode_attention(q.numpy(), gc, 8, T - 1, inv.numpy(), attn_mask=mask)
+    got = _run(cuda, gc, inv, q, T - 1, mask=mask, kernel=kernel)
+    err, cos = compare(got, want)
+    print(f"[max moves late] kernel={kernel} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= TOL_ABS and cos >= TOL_COS
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
 def test_decode_vs_reference_golden(cuda, golden, kernel):
     """The reference's own CPU output on its stub cache (fp16 intermediates)."""
     from tests.test_oracle import _gc_from_fixture
