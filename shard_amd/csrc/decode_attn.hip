@@ -817,6 +817,7 @@ void k_decode_split(const SplitParams p) {
 // it commutes with the log-sum-exp merge of k_decode_merge.
 constexpr int kTokWaves = 8;
 constexpr int kTokThreads = 64 * kTokWaves;
+constexpr int kShareMinTiles = 64;  // splits with fewer tiles give both waves of a SIMD equal shares
 
 struct TokParams {
   int32_t B, H, G, QG, n_comp, cstart;  // QG: groups of NQ query heads per kv head
@@ -959,9 +960,25 @@ void k_decode_tok(const TokParams p) {
       }
     }
   };
+  // ---- the wave's compressed tiles (a static map: the result does not depend
+  // on wave timing).  Waves p and p + 4 share a SIMD, whose arbiter favours
+  // the first-dispatched one (w < 4): measured at 5.8K vs 7.7K clocks per tile
+  // while both run.  SIMD p takes tiles p, p + 4, p + 8, ... (its j-th at
+  // p + 4 j).  In a split of at least kShareMinTiles tiles the favoured wave
+  // takes 3 of every 5 (j = 0, 2, 4 mod 5) and its partner 2 (j = 1, 3), so
+  // the two finish closer together; shorter splits alternate (j even / odd).
+  const int wp = w & 3;
+  const bool w_old = w < 4;
+  const bool uneven = n_c >= kShareMinTiles;
+  auto tile_of = [&](int m) {  // index of this wave's m-th compressed tile
+    int j;
+    if (uneven) j = w_old ? 5 * (m / 3) + 2 * (m % 3) : 5 * (m >> 1) + 2 * (m & 1) + 1;
+    else j = 2 * m + (w_old ? 0 : 1);
+    return wp + 4 * j;
+  };
   uint32_t cwA[KS], cwB[KS];
   float2 fA2, fA1, fB2, fB1;
-  if (w < n_c) load_tile(w, cwA, fA2, fA1);
+  if (tile_of(0) < n_c) load_tile(tile_of(0), cwA, fA2, fA1);
 
   // every global load of the set-up goes out before the first LDS store, so
   // the cold misses overlap (one round trip instead of one per copy step)
@@ -1173,18 +1190,10 @@ void k_decode_tok(const TokParams p) {
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qb8, b1, sacc, 0, 0, 0);
       }
     }
-    // 3. online softmax of the query heads over the tile
-    float sv[NE], al[NQ];
-#pragma unroll
-    for (int i = 0; i < NE; ++i) sv[i] = sacc[i];
-    const bool moved = softmax(sv, p.n_comp - t0, p.n_sink + t0 + col, al,
-                               [&](int row, float pv) { L.pa[w][row][col] = f2h(pv); });
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    // 4. VQ values of the tile on MFMA: A = the numerators of the query heads
-    //    (row vn, tokens 8 vt ..), B_e = component e of the codebook entries of
-    //    the lane's 8 tokens in subvector vn + 16 jg
-    if (moved) rescale_v(al);
-    const half8 pa8 = __builtin_bit_cast(half8, *(const uint4*)&L.pa[w][vn < NQ ? vn : NQ][8 * vt]);
+    // 3. the value operands of step 4 (codebook lookups, read-only LDS) go out
+    //    before the softmax, so their latency overlaps it: B_e = component e of
+    //    the codebook entries of the lane's 8 tokens in subvector vn + 16 jg
+    uint4 bw[2][4];
 #pragma unroll
     for (int jg = 0; jg < 2; ++jg) {
       uint2 en[8];
@@ -1193,15 +1202,29 @@ void k_decode_tok(const TokParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        uint4 bw;
-        bw.x = __builtin_amdgcn_perm(e < 2 ? en[1].x : en[1].y, e < 2 ? en[0].x : en[0].y, sel);
-        bw.y = __builtin_amdgcn_perm(e < 2 ? en[3].x : en[3].y, e < 2 ? en[2].x : en[2].y, sel);
-        bw.z = __builtin_amdgcn_perm(e < 2 ? en[5].x : en[5].y, e < 2 ? en[4].x : en[4].y, sel);
-        bw.w = __builtin_amdgcn_perm(e < 2 ? en[7].x : en[7].y, e < 2 ? en[6].x : en[6].y, sel);
-        vacc[jg][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa8, __builtin_bit_cast(half8, bw),
-                                                             vacc[jg][e], 0, 0, 0);
+        bw[jg][e].x = __builtin_amdgcn_perm(e < 2 ? en[1].x : en[1].y, e < 2 ? en[0].x : en[0].y, sel);
+        bw[jg][e].y = __builtin_amdgcn_perm(e < 2 ? en[3].x : en[3].y, e < 2 ? en[2].x : en[2].y, sel);
+        bw[jg][e].z = __builtin_amdgcn_perm(e < 2 ? en[5].x : en[5].y, e < 2 ? en[4].x : en[4].y, sel);
+        bw[jg][e].w = __builtin_amdgcn_perm(e < 2 ? en[7].x : en[7].y, e < 2 ? en[6].x : en[6].y, sel);
       }
     }
+    //    online softmax of the query heads over the tile
+    float sv[NE], al[NQ];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) sv[i] = sacc[i];
+    const bool moved = softmax(sv, p.n_comp - t0, p.n_sink + t0 + col, al,
+                               [&](int row, float pv) { L.pa[w][row][col] = f2h(pv); });
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // 4. VQ values of the tile on MFMA: A = the numerators of the query heads
+    //    (row vn, tokens 8 vt ..), B as above
+    if (moved) rescale_v(al);
+    const half8 pa8 = __builtin_bit_cast(half8, *(const uint4*)&L.pa[w][vn < NQ ? vn : NQ][8 * vt]);
+#pragma unroll
+    for (int jg = 0; jg < 2; ++jg)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        vacc[jg][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa8, __builtin_bit_cast(half8, bw[jg][e]),
+                                                             vacc[jg][e], 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // pa is rewritten by the next tile
   };
 
@@ -1265,15 +1288,15 @@ void k_decode_tok(const TokParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // xp is rewritten by the next tile
   };
 
-  // compressed tiles w, w + NW, ...: ping-pong, the next tile's loads fly
-  // during the current one
-  int k = w;
-  while (k < n_c) {
-    const int kb = k + NW;
+  // compressed tiles tile_of(0), tile_of(1), ... (increasing): ping-pong, the
+  // next tile's loads fly during the current one
+  int k = tile_of(0);
+  for (int m = 0; k < n_c; m += 2) {
+    const int kb = tile_of(m + 1);
     if (kb < n_c) load_tile(kb, cwB, fB2, fB1);
     tile(k, cwA, fA2, fA1);
     if (kb >= n_c) break;
-    k = kb + NW;
+    k = tile_of(m + 2);
     if (k < n_c) load_tile(k, cwA, fA2, fA1);
     tile(kb, cwB, fB2, fB1);
   }

@@ -115,19 +115,21 @@ def test_decode_split_counts_with_long_extras(cuda):
 
 def test_decode_is_deterministic(cuda):
     """Repeated calls give the same bits with every split kernel: the tile to
-    wave map and every merge order are fixed, nothing depends on wave timing."""
+    wave map and every merge order are fixed, nothing depends on wave timing.
+    One split (188 tiles) takes the token-tiled kernel's unequal wave shares."""
     from shard_amd import ops
     gc, inv = random_layer(B=2, n_comp=6000, n_stream=37, seed=5)
     d = to_device(gc, cuda, inv)
     q = torch.randn(2, 32, 128, generator=torch.Generator().manual_seed(6)).half().to(cuda)
-    call = ops.make_decode_args(q, d, 4 + 6000 + 64 + 37 - 1, None, stream_n=37)
-    for kernel in KERNELS:
-        call.args.kernel = kernel
-        first = ops.decode_attn(call).clone()
-        for rep in range(4):
-            again = ops.decode_attn(call)
-            torch.cuda.synchronize()
-            assert torch.equal(again.view(torch.int16), first.view(torch.int16)), (kernel, rep)
+    for ns in (0, 1):
+        call = ops.make_decode_args(q, d, 4 + 6000 + 64 + 37 - 1, None, stream_n=37, n_splits=ns)
+        for kernel in KERNELS:
+            call.args.kernel = kernel
+            first = ops.decode_attn(call).clone()
+            for rep in range(4):
+                again = ops.decode_attn(call)
+                torch.cuda.synchronize()
+                assert torch.equal(again.view(torch.int16), first.view(torch.int16)), (ns, kernel, rep)
 
 
 @pytest.mark.parametrize("kernel", KERNELS)
@@ -228,10 +230,10 @@ def test_decode_compressed_real_synthetic(cuda, kernel):
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
-# The bench's 32K context at batch 1, and batch 16 with enough tiles per
-# workgroup that every wave of the token-tiled kernel walks the claim loop many
-# times (batch 16 x 16K itself takes the fp64 oracle too long for a test).
-LARGE = [(1, 32700, 0), (1, 32700, 512), (16, 4000, 8)]
+# The bench's 32K context at batch 1, and batch 16 with more than 64 tiles per
+# split, where the token-tiled kernel gives the two waves of a SIMD unequal
+# shares (batch 16 x 16K itself takes the fp64 oracle too long for a test).
+LARGE = [(1, 32700, 0), (1, 32700, 512), (16, 4200, 8)]
 
 
 _large_cases = {}
