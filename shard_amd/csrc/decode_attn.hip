@@ -51,7 +51,7 @@ constexpr int kGQA = 4;           // query heads per kv head
 constexpr int kMaxExtra = 2048;   // sink + window + decode + stream tokens per call
 constexpr int kMaxSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLazyTau = 8.f;   // token-tiled softmax: numerators stay below 2^kLazyTau
+constexpr float kLazyTau = 8.f;   // softmax numerators stay below 2^kLazyTau (lazily moved max)
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw, unswizzled access (gfx9)
 // rope tables of the per-layer operands (k_decode_prepare): in-tile column
 // phases, the per-tile step, and the token-tiled kernel's two tile-offset tables
@@ -524,6 +524,19 @@ void k_decode_split(const SplitParams p) {
                                          : p.n_first * p.chunk + (split - p.n_first) * p.chunk2;
   int t_end = t_begin + (split < p.n_first ? p.chunk : p.chunk2);
   if (t_end > p.n_comp) t_end = p.n_comp;
+  if (t_end <= t_begin) {
+    // no compressed tokens (a last split that only holds the extra tokens):
+    // the empty partial row is m = -inf, l = 0, acc = 0; skip the set-up
+    if (tid < 64 * NQ) {
+      const int64_t widx = ((int64_t)b * p.H + hg * NQ + wv) * p.nsp + split;
+      *(float2*)(p.ws_acc + widx * kHD + 2 * lane) = make_float2(0.f, 0.f);
+      if (lane == 0) {
+        p.ws_m[widx] = -INFINITY;
+        p.ws_l[widx] = 0.f;
+      }
+    }
+    return;
+  }
 
   // ---- first iteration's loads go out before the setup work.  Token indices
   // are clamped to the chunk (no divergent loads); rows past the chunk end get
@@ -671,6 +684,18 @@ void k_decode_split(const SplitParams p) {
     }
     __syncthreads();
 
+    // the value operands of 3b (codebook entries of the thread's VT tokens,
+    // read-only LDS) go out before the softmax, so their latency overlaps it
+    half2v c2v[VT / 2][4];
+#pragma unroll
+    for (int u = 0; u < VT / 2; ++u) {
+      const uint2 ca = cbl[vc[2 * u]], cb = cbl[vc[2 * u + 1]];
+      c2v[u][0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x05040100u));
+      c2v[u][1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x07060302u));
+      c2v[u][2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x05040100u));
+      c2v[u][3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x07060302u));
+    }
+
     // 3a. online softmax over the iteration's TT tokens (base 2, scores scaled
     //     by log2e/sqrt(D)); a head's tokens fill one wave (TT = 64) or half
     if (tid < NQ * TT) {
@@ -683,12 +708,19 @@ void k_decode_split(const SplitParams p) {
         s *= sc;
         if (p.mask) s += p.mask[(int64_t)b * p.mask_stride + p.n_sink + tok] * kLog2e;
       }
-      const float tmax = TT == 64 ? wave64_reduce(s, OpMax()) : half32_reduce(s, OpMax());
-      const float m_new = fmaxf(m_run, tmax);
-      const float al = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
-      const float pv = (s == -INFINITY) ? 0.f : fast_exp2(s - m_new);
-      l_part = l_part * al + pv;
-      m_run = m_new;
+      // the reference max m_run moves (with the rescale of l and of the value
+      // sums) only when a score exceeds it by more than kLazyTau: numerators
+      // stay below 2^kLazyTau and most tiles skip the cross-lane max
+      float al = 1.f;
+      if (__builtin_amdgcn_ballot_w64(s > m_run + kLazyTau) != 0) {
+        const float tmax = TT == 64 ? wave64_reduce(s, OpMax()) : half32_reduce(s, OpMax());
+        const float m_new = fmaxf(m_run, tmax);
+        al = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
+        l_part *= al;
+        m_run = m_new;
+      }
+      const float pv = (s == -INFINITY) ? 0.f : fast_exp2(s - m_run);
+      l_part += pv;
       pp16[qr][tt] = (half_t)pv;
       if (tt == 0) alpha_s[qr] = al;
     }
@@ -712,17 +744,11 @@ void k_decode_split(const SplitParams p) {
       }
 #pragma unroll
       for (int u = 0; u < VT / 2; ++u) {
-        const uint2 ca = cbl[vc[2 * u]], cb = cbl[vc[2 * u + 1]];
-        half2v c2[4];
-        c2[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x05040100u));
-        c2[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.x, ca.x, 0x07060302u));
-        c2[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x05040100u));
-        c2[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(cb.y, ca.y, 0x07060302u));
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
           const half2v p2 = __builtin_bit_cast(half2v, pq[a][u]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) vacc[a][e] = __builtin_amdgcn_fdot2(p2, c2[e], vacc[a][e], false);
+          for (int e = 0; e < 4; ++e) vacc[a][e] = __builtin_amdgcn_fdot2(p2, c2v[u][e], vacc[a][e], false);
         }
       }
     }
