@@ -1421,9 +1421,16 @@ void k_decode_merge(const MergeParams p) {
     mv[u] = mrow[s];
     lv[u] = lrow[s];
   }
+  // the wave's maximum: its first kMergePF rows from the loads above (the same
+  // in every lane), rows past them (more than 4 kMergePF splits) loaded here
   float mx = -INFINITY;
-  for (int s = s_lo + lane; s < s_hi; s += 64) mx = fmaxf(mx, mrow[s]);
-  mx = wave64_reduce(mx, OpMax());
+#pragma unroll
+  for (int u = 0; u < kMergePF; ++u)
+    if (s_lo + u < s_hi) mx = fmaxf(mx, mv[u]);
+  if (s_hi - s_lo > kMergePF) {
+    for (int s = s_lo + kMergePF + lane; s < s_hi; s += 64) mx = fmaxf(mx, mrow[s]);
+    mx = wave64_reduce(mx, OpMax());
+  }
   if (lane == 0) wmax[w] = mx;
   __syncthreads();
   float M = wmax[0];
