@@ -9,13 +9,14 @@ relative-delta RoPE identity
     pair_i(D) = (a_i c_i + b_i d_i) cos(theta_i D) + (b_i c_i - a_i d_i) sin(theta_i D)
 
 (q_n = [a, b] = undo-RoPE(q, pos_q), k_n = [c, d], D = pos_t - pos_q), and
-accumulates the VQ values in Hadamard-rotated space; a combine kernel merges
-the splits with the fp16 segments and the 8-bit stream and applies one
-inverse Hadamard.
+accumulates the VQ values in Hadamard-rotated space, together with the fp16
+segments and the 8-bit stream in one online softmax; each split applies ch and
+one inverse Hadamard to its partial row, and a merge kernel combines the rows.
 """
 import torch
 
 from . import ops
+from ._lib import ShardHipError
 
 _workspaces = {}
 
@@ -65,8 +66,14 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
         gc["_decode_call"] = call  # the layer's argument block, refreshed per step
     else:
         call.refresh(q, gc, pos_q, inv, mask, n_splits, None, stream_n, dec)
-    ws = _workspace(q.device, call.workspace_bytes())
-    out = ops.decode_attn(call, ws)
+    # the device's shared workspace; the size query runs only when the library
+    # reports it too small (before launching anything)
+    try:
+        out = ops.decode_attn(call, _workspace(q.device, 0), allocate=False)
+    except ShardHipError as exc:
+        if exc.code != ops.ERR_WORKSPACE:
+            raise
+        out = ops.decode_attn(call, _workspace(q.device, call.workspace_bytes()), allocate=False)
     call.step = []  # drop this step's tensors (the output is returned)
     return out.view(B, n_q, 1, hd).to(q_rope.dtype)
 

@@ -198,14 +198,21 @@ class CacheLayer(CacheLayerMixin):
                 gc[name] = new
             gc["_stream_cap"] = cap
         # row s of each buffer, by address: codes and fp16 rows hold B G D
-        # entries per token, norms and QJL scales B G (fp16)
+        # entries per token, norms and QJL scales B G (fp16).  The buffers'
+        # base addresses are kept until the buffers change.
+        base = gc.get("_stream_base")
+        if base is None or base[0] is not gc["k_idx_buf"] or base[1] != qjl:
+            ptr = lambda name: gc[name].data_ptr() if name in gc else None
+            base = (gc["k_idx_buf"], qjl, tuple(ptr(n) for n in (
+                "k_idx_buf", "k_norm_buf", "k_deq_buf", "v_idx_buf", "v_norm_buf", "v_deq_buf",
+                "k_qsign_buf", "k_qscale_buf", "v_qsign_buf", "v_qscale_buf")))
+            gc["_stream_base"] = base
+        ki, kn, kd, vi, vn, vd, kqs, kqc, vqs, vqc = base[2]
         rows = B * G
         p8, p16, n16 = s * rows * D, 2 * s * rows * D, 2 * s * rows
-        a = lambda name, off: gc[name].data_ptr() + off
-        kp = (a("k_idx_buf", p8), a("k_norm_buf", n16), a("k_deq_buf", p16))
-        vp = (a("v_idx_buf", p8), a("v_norm_buf", n16), a("v_deq_buf", p16))
-        qp = ((a("k_qsign_buf", p8), a("k_qscale_buf", n16), a("v_qsign_buf", p8),
-               a("v_qscale_buf", n16)) if qjl else (None, None, None, None))
+        kp = (ki + p8, kn + n16, kd + p16)
+        vp = (vi + p8, vn + n16, vd + p16)
+        qp = (kqs + p8, kqc + n16, vqs + p8, vqc + n16) if qjl else (None, None, None, None)
         return (gc["signs"], gc["stream_codebook"]), kp, vp, qp
 
     def _stream_append(self, k, v):
@@ -236,7 +243,12 @@ class CacheLayer(CacheLayerMixin):
         G = k.shape[1]
         self._lazy_evict()
         cbs, kp, vp, qp = self._stream_rows(B, G, D, q.device)
-        q_out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
+        # q after RoPE goes to a per-layer buffer: this step's attention reads it
+        # (stream-ordered before the next step's append rewrites it)
+        q_out = gc.get("_q_rope")
+        if q_out is None or q_out.shape != (B, H, D) or q_out.device != q.device:
+            q_out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
+            gc["_q_rope"] = q_out
         c16 = lambda t, *shape: t.reshape(*shape).contiguous()
         Bc = cos.shape[0]  # 1 when the batch shares its positions
         ops.rope_stream_append_at(c16(q, B, H, D), c16(k, B, G, D), c16(v, B, G, D),
@@ -409,7 +421,8 @@ class Cache(HFCache):
             has_gc = True
             seen = set()
             for k, v in gc.items():
-                if torch.is_tensor(v) and v.data_ptr() not in seen and not k.endswith("_buf"):
+                if (torch.is_tensor(v) and v.data_ptr() not in seen and not k.endswith("_buf")
+                        and not k.startswith("_")):  # "_" keys: per-step scratch
                     seen.add(v.data_ptr())
                     total += _nb(v)
             if "k_idx_buf" in gc:
@@ -687,7 +700,8 @@ def reorder_rows(gc: dict, beam_idx) -> None:
         if k in gc:
             gc[k] = rows(gc[k], 1)
     assert gc["v_indices"].shape[2] == n
-    gc.pop("_decode_call", None)  # held pointers to the old tensors
+    for k in ("_decode_call", "_stream_base", "_q_rope"):  # held the old tensors or addresses
+        gc.pop(k, None)
 
 
 def finalize_format(gc: dict, inv_freq, dev):

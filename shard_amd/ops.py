@@ -24,8 +24,19 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t):
+    """The current stream of t's device: torch's raw stream query (the handle
+    torch.cuda.current_stream(t.device).cuda_stream returns, without building
+    a Stream object on every call)."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(t.get_device()))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+ERR_WORKSPACE = -4  # SHARD_ERR_WORKSPACE of include/shard_hip.h
 
 
 def _contig(t, dtype, name):
@@ -457,14 +468,23 @@ def decode_workspace(call: DecodeCall) -> torch.Tensor:
     return torch.zeros(max(need, 16), dtype=torch.uint8, device=call.out.device)
 
 
-def decode_attn(call: DecodeCall, ws: torch.Tensor = None) -> torch.Tensor:
-    """Run the decode call; returns its (B, H, D) fp16 output."""
+def decode_attn(call: DecodeCall, ws: torch.Tensor = None, allocate: bool = True) -> torch.Tensor:
+    """Run the decode call; returns its (B, H, D) fp16 output.  A workspace ws
+    that is missing or too small (the library checks before it launches
+    anything) is replaced by a fresh one of the size the call needs, or, with
+    allocate=False, raises ShardHipError with code SHARD_ERR_WORKSPACE."""
     lib = _lib.load()
-    need = call.workspace_bytes()
-    if ws is None or ws.numel() < need:
-        ws = decode_workspace(call)
+    stream = _stream(call.out)
+    if ws is not None:
+        rc = lib.shard_decode_attn(ctypes.byref(call.args), ws.data_ptr(), ws.numel(), stream)
+        if rc != ERR_WORKSPACE or not allocate:
+            _lib.check("shard_decode_attn", rc)
+            return call.out
+    elif not allocate:
+        raise _lib.ShardHipError("shard_decode_attn", ERR_WORKSPACE, "no workspace given")
+    ws = decode_workspace(call)
     _lib.check("shard_decode_attn", lib.shard_decode_attn(
-        ctypes.byref(call.args), ws.data_ptr(), ws.numel(), _stream(call.out)))
+        ctypes.byref(call.args), ws.data_ptr(), ws.numel(), stream))
     return call.out
 
 
