@@ -301,3 +301,39 @@ def test_decode_device_position_matches_host_position(cuda, kernel):
         want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
         err, cos = compare(dev, want)
         assert err <= TOL_ABS and cos >= TOL_COS
+
+
+def test_fused_attention_grows_a_small_workspace(cuda):
+    """The patched forward's call runs on the device's shared workspace and asks
+    for the size only when the library reports it too small (before it
+    launches anything): a too-small buffer is replaced and the call retried,
+    with the same bits as a call on a workspace of the queried size."""
+    from shard_amd import attention, ops
+    gc, inv = random_layer(B=2, n_comp=3000, n_stream=5, seed=17)
+    d = to_device(gc, cuda, inv)
+    q = torch.randn(2, 32, 1, 128, generator=torch.Generator().manual_seed(9)).half().to(cuda)
+    pos_q = 4 + 3000 + 64 + 5 - 1
+
+    class _CacheRef:
+        _rope_inv_freq = d["inv_freq_dev"]
+        _n_splits = 0
+
+    class _Layer:
+        _gpu_compressed = d
+        _cache_ref = _CacheRef()
+
+    key = (cuda.type, cuda.index)
+    saved = attention._workspaces.get(key)
+    try:
+        attention._workspaces[key] = torch.zeros(16, dtype=torch.uint8, device=cuda)
+        got = attention.fused_attention_compressed(q, _Layer(), pos_q, d["inv_freq_dev"]).clone()
+        call = d["_decode_call"]
+        assert attention._workspaces[key].numel() >= call.workspace_bytes() > 16
+        want = ops.decode_attn(ops.make_decode_args(q.reshape(2, 32, 128), d, pos_q, None, stream_n=5))
+        torch.cuda.synchronize()
+        assert torch.equal(got.reshape(2, 32, 128).view(torch.int16), want.view(torch.int16))
+    finally:
+        if saved is None:
+            attention._workspaces.pop(key, None)
+        else:
+            attention._workspaces[key] = saved
