@@ -12,9 +12,9 @@
 //     extra tokens (at most 2048) into one more partial row per query head.
 //   k_decode_tok (token-tiled)  grid = n_splits * n_kv * query groups * B,
 //     512-thread workgroups, one per CU, 1, 2 or 4 query heads per workgroup;
-//     the kv head's basis operand image sits in LDS and wave w takes whole
-//     tiles (all 128 rows) w, w + 8, w + 16, ... of the split, with its own
-//     softmax state (a static map: results do not depend on wave timing).
+//     the kv head's basis operand image sits in LDS and each wave takes whole
+//     tiles (all 128 rows) of the split by a static map (results do not depend
+//     on wave timing), with its own softmax state.
 //     Every split owns a run of cost units (a compressed tile costs 3, a tile
 //     of 32 extra tokens 1), so any number of extra tokens spreads over the
 //     last splits.  The waves merge once at the end.
@@ -805,14 +805,16 @@ void k_decode_split(const SplitParams p) {
 // --------------------------------------------------------------------------
 // One 512-thread workgroup (8 waves, 2 per SIMD) per CU owns one kv head x a
 // range of tiles.  The head's basis operand image (4 row blocks x (KS + 1)
-// k-steps, 52 KB at rank 192) sits in LDS; wave w takes the 32-token tiles
-// w, w + 8, w + 16, ... and works through them with no workgroup barrier: per
-// tile a wave unpacks the coefficients once, runs the 4 x (KS + 1) rebuild
-// MFMAs with A from LDS, rotates, scores, and keeps its own online softmax and
-// VQ value sums.  The waves merge once, after the loop, in a fixed order.
-// The tile-to-wave map is static (not claimed from a counter), so a call's
-// result does not depend on the timing of the waves: repeated calls give the
-// same bits.
+// k-steps, 52 KB at rank 192) sits in LDS; the 32-token tiles p, p + 4,
+// p + 8, ... go to SIMD p, whose two waves (p and p + 4) alternate over them
+// (3 to 2 for the first-dispatched wave in splits of 64 tiles or more), and
+// each wave works through its tiles with no workgroup barrier: per tile it
+// unpacks the coefficients once, runs the 4 x (KS + 1) rebuild MFMAs with A
+// from LDS, rotates, scores, and keeps its own online softmax and VQ value
+// sums.  The waves merge once, after the loop, in a fixed order.  The
+// tile-to-wave map is static (not claimed from a counter), so a call's result
+// does not depend on the timing of the waves: repeated calls give the same
+// bits.
 //
 // Tiles: the split's compressed tiles first, then its extra tiles (sink,
 // window, decode and stream tokens as fp16 rows), round robin over the waves
