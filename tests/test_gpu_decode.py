@@ -337,3 +337,19 @@ def test_fused_attention_grows_a_small_workspace(cuda):
             attention._workspaces.pop(key, None)
         else:
             attention._workspaces[key] = saved
+
+
+@pytest.mark.parametrize("case", [(1, 8, 1, 192, 2500), (1, 4, 8, 128, 2300), (2, 2, 2, 192, 2200)],
+                         ids=["gqa1", "gqa8", "gqa2_b2"])
+def test_decode_long_split_other_groups(cuda, case):
+    """One split of 70+ tiles (the token-tiled kernel's 3:2 wave shares) with
+    1, 2 and 8 query heads per kv head."""
+    B, nkv, gqa, rank, n_comp = case
+    gc, inv = random_layer(B=B, nkv=nkv, rank=rank, n_comp=n_comp, n_stream=7, seed=31 + gqa)
+    q = torch.randn(B, gqa * nkv, 1, 128, generator=torch.Generator().manual_seed(12)).half()
+    pos_q = 4 + n_comp + 64 + 7 - 1
+    want = exact.decode_attention(q.numpy(), gc, nkv, pos_q, inv.numpy())
+    got = _run(cuda, gc, inv, q, pos_q, nkv=nkv, n_splits=1, kernel=2)
+    err, cos = compare(got, want)
+    print(f"long split {case}: max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= TOL_ABS and cos >= TOL_COS
