@@ -105,3 +105,29 @@ def compare(got, want):
     err = float(np.max(np.abs(g - w)))
     cos = float(g @ w / (np.linalg.norm(g) * np.linalg.norm(w) + 1e-300))
     return err, cos
+
+
+def batch_rows(gc, rows):
+    """The oracle-format layer gc restricted to the batch rows `rows` (in that
+    order): per-row coefficient bytes, V indices, channel scales and fp16
+    segments; the shared tables are kept.  Stream tokens are not carried."""
+    assert not gc.get("stream_n", 0), "batch_rows: layers without stream tokens"
+    B, n_comp = gc["batch"], gc["n_compress"]
+    n_total, rank = gc["k_coeffs_shape"]
+    assert n_total == B * n_comp and rank % 2 == 0
+    rows = list(rows)
+    idx = torch.as_tensor(rows, dtype=torch.long)
+    packed = torch.as_tensor(np.asarray(gc["k_coeffs"])).reshape(B, n_comp * rank // 2)
+    out = dict(gc)
+    out.update({
+        "k_coeffs": packed[idx].reshape(-1).contiguous(),
+        "k_coeffs_shape": (len(rows) * n_comp, rank),
+        "v_idx_full": gc["v_idx_full"][idx].contiguous(),
+        "v_ch_f16": gc["v_ch_f16"][idx].contiguous(),
+        "batch": len(rows),
+    })
+    out.pop("v_qdata", None)
+    for k in ("sink_k", "sink_v", "win_k", "win_v", "decode_k", "decode_v"):
+        if k in gc:
+            out[k] = gc[k][idx].contiguous()
+    return out

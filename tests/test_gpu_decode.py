@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import exact, ref
-from tests.helpers import compare, random_layer, to_device
+from tests.helpers import batch_rows, compare, random_layer, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -232,7 +232,7 @@ def test_decode_compressed_real_synthetic(cuda, kernel):
 
 # The bench's 32K context at batch 1, and batch 16 with more than 64 tiles per
 # split, where the token-tiled kernel gives the two waves of a SIMD unequal
-# shares (batch 16 x 16K itself takes the fp64 oracle too long for a test).
+# shares (batch 16 x 16K itself: test_decode_config5_layer_full_size).
 LARGE = [(1, 32700, 0), (1, 32700, 512), (16, 4200, 8)]
 
 
@@ -266,6 +266,31 @@ def test_decode_large_contexts(cuda, shape):
         print(f"B={B} n_comp={n_comp} stream={n_stream} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}",
               flush=True)
         assert err <= TOL_ABS and cos >= TOL_COS, (kernel, err, cos)
+
+
+def test_decode_config5_layer_full_size(cuda):
+    """BASELINE config 5's layer at full size: batch 16 x 16,316 compressed
+    tokens (16,384 with the 4 sink and 64 window tokens).  Every kernel against
+    the fp64 oracle on batch rows 0 and 15 (the oracle over all 16 rows takes
+    minutes), and the 16 rows of the row-split and token-tiled kernels against
+    each other (two independent split schemes)."""
+    B, n_comp = 16, 16316
+    gc, inv = random_layer(B=B, n_comp=n_comp, seed=13)
+    q = torch.randn(B, 32, 1, 128, generator=torch.Generator().manual_seed(4)).half()
+    pos_q = 4 + n_comp + 64 - 1
+    rows = [0, 15]
+    want = exact.decode_attention(q[rows].numpy(), batch_rows(gc, rows), 8, pos_q, inv.numpy())
+    outs = {}
+    for kernel in KERNELS:
+        got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
+        err, cos = compare(got[rows], want)
+        print(f"B=16 n_comp={n_comp} kernel={kernel} rows {rows}: max_abs={err:.3e} cos={cos:.7f}",
+              flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (kernel, err, cos)
+        outs[kernel] = got
+    err, cos = compare(outs[1], outs[2])
+    print(f"row-split vs token-tiled, all rows: max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= TOL_ABS and cos >= TOL_COS, (err, cos)
 
 
 def test_kv_reconstruct(cuda):

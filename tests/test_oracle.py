@@ -386,3 +386,18 @@ def test_relative_delta_identity_against_reapplied_rope(golden):
     bad = np.einsum("bhd,bhkd->bhk", q[:, :, 0], np.repeat(bad, 4, axis=1)) / math.sqrt(128)
     assert np.max(np.abs(bad - got)) > 1e-2
     del qph
+
+
+def test_batch_rows_slice_matches_full_oracle():
+    """tests.helpers.batch_rows: the oracle on a subset of batch rows (in any
+    order) equals those rows of the oracle on the whole layer, fp16 segments
+    and decode tokens included; a slice that swapped per-row data would not."""
+    from tests.helpers import batch_rows, random_layer
+    gc, inv = random_layer(B=4, n_comp=300, n_dec=3, seed=5)
+    q = torch.randn(4, 32, 1, 128, generator=torch.Generator().manual_seed(4)).half()
+    pos_q = 4 + 300 + 64 + 3 - 1
+    full = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    part = exact.decode_attention(q[[3, 1]].numpy(), batch_rows(gc, [3, 1]), 8, pos_q, inv.numpy())
+    np.testing.assert_array_equal(part, full[[3, 1]])
+    swapped = exact.decode_attention(q[[3, 1]].numpy(), batch_rows(gc, [1, 3]), 8, pos_q, inv.numpy())
+    assert np.max(np.abs(swapped - full[[3, 1]])) > 1e-2
