@@ -196,6 +196,22 @@ int shard_rope_stream_append(const uint16_t* q, const uint16_t* k, const uint16_
                              uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
                              uint16_t* v_qscale, void* stream);
 
+/* shard_rope_stream_append with the token's stream row read from device
+ * memory: the k_* / v_* outputs are the stream buffers' first rows, and the
+ * token goes to row *row_dev of them (rows of B n_kv_heads entries), written
+ * only when 0 <= *row_dev < row_cap (the buffers' rows).  No counterpart in
+ * the reference; it lets one captured HIP graph append every decode step's
+ * token while the stream grows (with shard_decode_args.n_stream_dev). */
+int shard_rope_stream_append_dev(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
+                                 int32_t batch, int32_t n_q_heads, int32_t n_kv_heads, int32_t hd,
+                                 uint16_t* q_rope, const float* signs, const float* codebook,
+                                 int32_t n_codes, uint8_t* k_idx, uint16_t* k_norm,
+                                 uint16_t* k_deq, uint8_t* v_idx, uint16_t* v_norm,
+                                 uint16_t* v_deq, uint8_t* k_qsign, uint16_t* k_qscale,
+                                 uint8_t* v_qsign, uint16_t* v_qscale, const int32_t* row_dev,
+                                 int32_t row_cap, void* stream);
+
 /* shard_stream_dequant with the QJL residual term (streaming.py:76-77):
  * codebook[idx] + (2 qsign - 1) * qscale before the inverse Hadamard.
  * qsign (rows, hd) uint8 and qscale (rows) fp16 both null or both set. */
@@ -269,6 +285,12 @@ typedef struct shard_decode_args {
    * reference's cache_position[-1], attention.py:383) and `pos_q` is ignored,
    * so the caller needs no host read-back of the position */
   const int64_t* pos_q_dev;
+  /* nullable device int32: when set, the call attends over the first
+   * min(*n_stream_dev, n_stream) stream rows, read at run time; n_stream then
+   * bounds the count and sizes the work plan, so one captured HIP graph serves
+   * every decode step while the stream grows.  No counterpart in the
+   * reference (its counts are host integers).  Not together with `mask`. */
+  const int32_t* n_stream_dev;
 } shard_decode_args;
 
 /* Per-layer constant operands of shard_decode_attn, computed once after a

@@ -43,6 +43,7 @@ class DecodeArgs(ctypes.Structure):
         ("mask", c_void_p), ("mask_stride", c_int64),
         ("out", c_void_p), ("n_splits", c_int32), ("kernel", c_int32),
         ("pos_q_dev", c_void_p),
+        ("n_stream_dev", c_void_p),
     ]
 
 
@@ -76,6 +77,7 @@ SIGNATURES = [
     ("shard_stream_quant_qjl", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_stream_quant_kv", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32] + [c_void_p] * 10 + [c_void_p]),
     ("shard_rope_stream_append", c_int32, [c_void_p] * 5 + [c_int64] + [c_int32] * 4 + [c_void_p] * 3 + [c_int32] + [c_void_p] * 10 + [c_void_p]),
+    ("shard_rope_stream_append_dev", c_int32, [c_void_p] * 5 + [c_int64] + [c_int32] * 4 + [c_void_p] * 3 + [c_int32] + [c_void_p] * 10 + [c_void_p, c_int32] + [c_void_p]),
     ("shard_stream_dequant_qjl", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
 ]
 

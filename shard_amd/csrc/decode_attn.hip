@@ -73,7 +73,17 @@ struct ExtraSegs {
   const uint16_t *dec_k, *dec_v;
   const uint16_t *s_k, *s_v;
   int32_t n_sink, n_win, n_dec, dec_stride, n_stream, n_x;
+  // when set, the stream tokens of the call are the first *n_stream_dev of the
+  // n_stream the launch was planned for (read at run time)
+  const int32_t* n_stream_dev;
 };
+
+// The extra tokens of the call: n_x, less the planned stream rows past the
+// device stream count when there is one.
+__device__ __forceinline__ int extras_now(const ExtraSegs& s) {
+  if (!s.n_stream_dev) return s.n_x;
+  return s.n_x - s.n_stream + min(max(*s.n_stream_dev, 0), s.n_stream);
+}
 
 struct SplitParams {
   int32_t B, H, G, rank, n_comp, cstart, pos_q, n_splits;
@@ -335,7 +345,7 @@ __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const i
 
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n_x = p.xs.n_x;
+  const int n_x = extras_now(p.xs);
   const float sc = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
 
   half8 Aq[8];
@@ -938,6 +948,7 @@ void k_decode_tok(const TokParams p) {
   const int xt0 = min(max(u0 - uc, 0), p.n_xt), xt1 = min(max(u1 - uc, 0), p.n_xt);
   const int n_c = ct1 > ct0 ? ct1 - ct0 : 0;
   const int n_x = xt1 > xt0 ? xt1 - xt0 : 0;
+  const int n_xact = extras_now(p.xs);  // extra tokens of the call (<= 32 n_xt)
 
   // ---- raw buffers of the split's coefficient rows and V indices: rows past
   // the compressed span read as zeros (coefficient -8, centroid 0: finite;
@@ -1269,7 +1280,7 @@ void k_decode_tok(const TokParams p) {
       }
       aq_loaded = true;
     }
-    const int n_xtok = p.xs.n_x;
+    const int n_xtok = n_xact;
     const int x0 = 32 * (xt0 + x);
     const int xt = min(x0 + col, n_xtok - 1);  // clamped: tokens past n_x are masked
     int mp;
@@ -1328,8 +1339,8 @@ void k_decode_tok(const TokParams p) {
     if (k < n_c) load_tile(k, cwA, fA2, fA1);
     tile(kb, cwB, fB2, fB1);
   }
-  // extra tiles w, w + NW, ...
-  for (int x = w; x < n_x; x += NW) xtile(x);
+  // extra tiles w, w + NW, ... (those holding tokens of this call)
+  for (int x = w; x < n_x && 32 * (xt0 + x) < n_xact; x += NW) xtile(x);
 
   // ---- merge the waves; per query head: ch, one inverse FWHT, plain part
 #pragma unroll
@@ -1599,6 +1610,7 @@ int decode_attn_tok(const shard_decode_args* a, float* ws, hipStream_t s) {
   tp.xs.n_sink = a->n_sink; tp.xs.n_win = a->n_win; tp.xs.n_dec = a->n_dec;
   tp.xs.dec_stride = a->dec_stride; tp.xs.n_stream = a->n_stream;
   tp.xs.n_x = (int32_t)n_extra(a);
+  tp.xs.n_stream_dev = a->n_stream_dev;
   tp.q = a->q; tp.inv_freq = a->inv_freq; tp.coef = a->k_coeffs;
   tp.op = (const uint4*)a->prep;
   tp.rope = (const float2*)((const char*)a->prep + (size_t)a->n_kv_heads * 4 * (a->rank / 16 + 1) * 64 * sizeof(uint4));
@@ -1675,6 +1687,9 @@ static int decode_attn_check(const shard_decode_args* a) {
   if (a->batch <= 0 || a->n_comp <= 0) return SHARD_ERR_ARG;
   if (a->n_sink < 0 || a->n_win < 0 || a->n_dec < 0 || a->n_stream < 0) return SHARD_ERR_ARG;
   if (a->kernel < 0 || a->kernel > 2) return SHARD_ERR_ARG;
+  // a device stream count bounds the stream by n_stream; the mask row would
+  // have to follow the count, so the two do not go together
+  if (a->n_stream_dev && (a->mask || !a->n_stream)) return SHARD_ERR_ARG;
   if ((a->n_sink && (!a->sink_k || !a->sink_v)) || (a->n_win && (!a->win_k || !a->win_v)) ||
       (a->n_dec && (!a->dec_k || !a->dec_v || a->dec_stride < a->n_dec)) ||
       (a->n_stream && (!a->s_k || !a->s_v)))
@@ -1732,6 +1747,7 @@ static int decode_attn_run(const shard_decode_args* a, void* workspace, hipStrea
   sp.xs.s_k = a->s_k; sp.xs.s_v = a->s_v;
   sp.xs.n_sink = a->n_sink; sp.xs.n_win = a->n_win; sp.xs.n_dec = a->n_dec;
   sp.xs.dec_stride = a->dec_stride; sp.xs.n_stream = a->n_stream; sp.xs.n_x = n_x;
+  sp.xs.n_stream_dev = a->n_stream_dev;
   sp.q = a->q; sp.inv_freq = a->inv_freq; sp.coef = a->k_coeffs;
   sp.op = (const uint4*)a->prep;
   sp.rope = (const float2*)((const char*)a->prep + shard_decode_prepare_op_bytes(a->n_kv_heads, a->rank));

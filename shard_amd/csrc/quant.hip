@@ -941,7 +941,7 @@ __global__ void k_rope_stream(const uint16_t* __restrict__ q, const uint16_t* __
                               const uint16_t* __restrict__ sinv, int64_t cs_stride, int B,
                               int H, int G, uint16_t* __restrict__ q_out, const StreamIO io,
                               const float* __restrict__ signs, const float* __restrict__ cb_g,
-                              int n_codes) {
+                              int n_codes, const int32_t* __restrict__ row_dev, int row_cap) {
   constexpr int D = 64 * E;
   __shared__ float cb[256];
   for (int i = threadIdx.x; i < n_codes; i += blockDim.x) cb[i] = cb_g[i];
@@ -966,8 +966,26 @@ __global__ void k_rope_stream(const uint16_t* __restrict__ q, const uint16_t* __
 #pragma unroll
   for (int k = 0; k < E; ++k) t[k] = h2f(x[rr * D + l + 64 * k]);
   if (job == 0) rope_row<E>(t, cosv + (rr / G) * cs_stride, sinv + (rr / G) * cs_stride);
-  stream_quant_row<E>(t, rr, signs, cb, n_codes, io.idx[job], io.norm[job], io.qsign[job],
-                      io.qscale[job], io.deq[job]);
+  uint8_t* idx = io.idx[job];
+  uint16_t* norm = io.norm[job];
+  uint8_t* qsign = io.qsign[job];
+  uint16_t* qscale = io.qscale[job];
+  uint16_t* deq = io.deq[job];
+  if (row_dev) {
+    // the outputs are the buffers' bases and the token's row comes from device
+    // memory (a captured graph replays one launch for every decode step); a
+    // row outside [0, row_cap) writes nothing
+    const int64_t row = *row_dev;
+    if (row < 0 || row >= row_cap) return;
+    idx += row * nk * D;
+    norm += row * nk;
+    if (qsign) {
+      qsign += row * nk * D;
+      qscale += row * nk;
+    }
+    if (deq) deq += row * nk * D;
+  }
+  stream_quant_row<E>(t, rr, signs, cb, n_codes, idx, norm, qsign, qscale, deq);
 }
 
 // ---------------------------------------------------------------------------
@@ -1255,15 +1273,15 @@ int shard_stream_quant_qjl(const uint16_t* x, int64_t rows, int32_t hd, const fl
   return stream_quant_launch(io, 1, rows, hd, signs, codebook, n_codes, stream);
 }
 
-int shard_rope_stream_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                             const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
-                             int32_t batch,
-                             int32_t n_q_heads, int32_t n_kv_heads, int32_t hd,
-                             uint16_t* q_rope, const float* signs, const float* codebook,
-                             int32_t n_codes, uint8_t* k_idx, uint16_t* k_norm, uint16_t* k_deq,
-                             uint8_t* v_idx, uint16_t* v_norm, uint16_t* v_deq,
-                             uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
-                             uint16_t* v_qscale, void* stream) {
+static int rope_stream_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
+                              int32_t batch, int32_t n_q_heads, int32_t n_kv_heads, int32_t hd,
+                              uint16_t* q_rope, const float* signs, const float* codebook,
+                              int32_t n_codes, uint8_t* k_idx, uint16_t* k_norm, uint16_t* k_deq,
+                              uint8_t* v_idx, uint16_t* v_norm, uint16_t* v_deq,
+                              uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
+                              uint16_t* v_qscale, const int32_t* row_dev, int32_t row_cap,
+                              void* stream) {
   if (!q || !k || !v || !cos || !sin || !q_rope || !signs || !codebook || !k_idx || !k_norm ||
       !v_idx || !v_norm)
     return SHARD_ERR_ARG;
@@ -1278,12 +1296,43 @@ int shard_rope_stream_append(const uint16_t* q, const uint16_t* k, const uint16_
   const int64_t rows = (int64_t)batch * (n_q_heads + 2 * n_kv_heads);
   const dim3 grid((unsigned)((rows + 3) / 4));
   switch (hd) {
-    case 128: hipLaunchKernelGGL(k_rope_stream<2>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes); break;
-    case 256: hipLaunchKernelGGL(k_rope_stream<4>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes); break;
+    case 128: hipLaunchKernelGGL(k_rope_stream<2>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes, row_dev, row_cap); break;
+    case 256: hipLaunchKernelGGL(k_rope_stream<4>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes, row_dev, row_cap); break;
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_rope_stream_append");
   return SHARD_OK;
+}
+
+int shard_rope_stream_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
+                             int32_t batch,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t hd,
+                             uint16_t* q_rope, const float* signs, const float* codebook,
+                             int32_t n_codes, uint8_t* k_idx, uint16_t* k_norm, uint16_t* k_deq,
+                             uint8_t* v_idx, uint16_t* v_norm, uint16_t* v_deq,
+                             uint8_t* k_qsign, uint16_t* k_qscale, uint8_t* v_qsign,
+                             uint16_t* v_qscale, void* stream) {
+  return rope_stream_launch(q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, hd,
+                            q_rope, signs, codebook, n_codes, k_idx, k_norm, k_deq, v_idx,
+                            v_norm, v_deq, k_qsign, k_qscale, v_qsign, v_qscale, nullptr, 0,
+                            stream);
+}
+
+int shard_rope_stream_append_dev(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
+                                 int32_t batch, int32_t n_q_heads, int32_t n_kv_heads, int32_t hd,
+                                 uint16_t* q_rope, const float* signs, const float* codebook,
+                                 int32_t n_codes, uint8_t* k_idx, uint16_t* k_norm,
+                                 uint16_t* k_deq, uint8_t* v_idx, uint16_t* v_norm,
+                                 uint16_t* v_deq, uint8_t* k_qsign, uint16_t* k_qscale,
+                                 uint8_t* v_qsign, uint16_t* v_qscale, const int32_t* row_dev,
+                                 int32_t row_cap, void* stream) {
+  if (!row_dev || row_cap <= 0) return SHARD_ERR_ARG;
+  return rope_stream_launch(q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, hd,
+                            q_rope, signs, codebook, n_codes, k_idx, k_norm, k_deq, v_idx,
+                            v_norm, v_deq, k_qsign, k_qscale, v_qsign, v_qscale, row_dev,
+                            row_cap, stream);
 }
 
 int shard_stream_quant_kv(const uint16_t* k, const uint16_t* v, int64_t rows, int32_t hd,

@@ -271,24 +271,32 @@ def stream_quant_kv_at(k, v, signs, codebook, k_idx, k_norm, k_deq, v_idx, v_nor
 
 def rope_stream_append_at(q, k, v, cos, sin, signs, codebook, q_out, k_idx, k_norm, k_deq,
                           v_idx, v_norm, v_deq, k_qsign=None, k_qscale=None, v_qsign=None,
-                          v_qscale=None):
+                          v_qscale=None, row_dev=None, row_cap=0):
     """RoPE of q and k (transformers' fp16 arithmetic) and the rotated k and v
     appended to the stream in one launch.  q (B, H, D), k and v (B, G, D):
     contiguous fp16; cos and sin (B, D) or (1, D) (shared by the batch),
     contiguous fp16; q_out (B, H, D) fp16; the stream outputs are device
-    addresses (ints) of this token's rows."""
+    addresses (ints) of this token's rows, or, with row_dev (a one-element
+    int32 tensor on q's device), of the buffers' first rows: the token then
+    goes to row row_dev[0] (written only when it is below row_cap), read at
+    run time, so a captured graph appends every step's token."""
     lib = _lib.load()
     B, H, D = q.shape
     G = k.shape[1]
     if cos.shape != sin.shape or cos.shape[-1] != D or cos.shape[0] not in (1, B):
         raise ValueError(f"cos/sin {tuple(cos.shape)} do not fit q {tuple(q.shape)}")
     cs_stride = 0 if cos.shape[0] == 1 else D
-    _lib.check("shard_rope_stream_append", lib.shard_rope_stream_append(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(), cs_stride,
-        B, H, G, D,
-        q_out.data_ptr(), signs.data_ptr(), codebook.data_ptr(), codebook.numel(),
-        k_idx, k_norm, k_deq, v_idx, v_norm, v_deq, k_qsign, k_qscale, v_qsign, v_qscale,
-        _stream(q)))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(), cs_stride,
+            B, H, G, D,
+            q_out.data_ptr(), signs.data_ptr(), codebook.data_ptr(), codebook.numel(),
+            k_idx, k_norm, k_deq, v_idx, v_norm, v_deq, k_qsign, k_qscale, v_qsign, v_qscale)
+    if row_dev is None:
+        _lib.check("shard_rope_stream_append", lib.shard_rope_stream_append(*args, _stream(q)))
+        return
+    if row_dev.dtype != torch.int32 or row_dev.device != q.device or row_dev.numel() < 1:
+        raise TypeError("row_dev must be an int32 tensor on q's device")
+    _lib.check("shard_rope_stream_append_dev", lib.shard_rope_stream_append_dev(
+        *args, row_dev.data_ptr(), int(row_cap), _stream(q)))
 
 
 def stream_dequant(idx: torch.Tensor, norm: torch.Tensor, signs: torch.Tensor,
@@ -362,13 +370,15 @@ def decode_prepare(fmt) -> torch.Tensor:
 
 
 def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
-                     stream_n=0, decode_kv=None) -> DecodeCall:
+                     stream_n=0, decode_kv=None, stream_n_dev=None) -> DecodeCall:
     """Build shard_decode_args for one layer.
 
     q (B, H, D) fp16 (post-RoPE); ``fmt`` is the layer's device format dict
     (see cache.CompressedLayerFormat); decode_kv = (dec_k, dec_v) fp16
     (B, G, S, D) or None.  ``pos_q`` is an int, or an int64 tensor on q's
-    device whose last element the kernel reads (no host read-back)."""
+    device whose last element the kernel reads (no host read-back).  With
+    ``stream_n_dev`` (a one-element int32 tensor on q's device) the call
+    attends over its value's worth of stream rows, at most stream_n."""
     _require_gpu(q)
     B, H, D = q.shape
     if tuple(fmt["v_centroids_f16"].shape) != (256, 4):
@@ -393,11 +403,12 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
     a.n_sink = fmt["sink_k"].shape[2]
     a.n_win = fmt["win_k"].shape[2]
     call = DecodeCall(a, keep)
-    return call.refresh(q, fmt, pos_q, inv_freq, mask, n_splits, out, stream_n, decode_kv)
+    return call.refresh(q, fmt, pos_q, inv_freq, mask, n_splits, out, stream_n, decode_kv,
+                        stream_n_dev)
 
 
 def _decode_refresh(self, q, fmt, pos_q, inv_freq=None, mask=None, n_splits=0, out=None,
-                    stream_n=0, decode_kv=None):
+                    stream_n=0, decode_kv=None, stream_n_dev=None):
     """Point this call at one step's q, position, stream, decode tokens and mask
     (the fields that change between decode steps; the layer's format pointers
     stay).  Returns self; self.out is the (B, H, D) fp16 output tensor."""
@@ -435,6 +446,14 @@ def _decode_refresh(self, q, fmt, pos_q, inv_freq=None, mask=None, n_splits=0, o
     else:
         a.s_k = a.s_v = None
     a.n_stream = stream_n
+    if stream_n_dev is not None:
+        if (stream_n_dev.dtype != torch.int32 or stream_n_dev.device != q.device
+                or stream_n_dev.numel() < 1):
+            raise TypeError("stream_n_dev must be an int32 tensor on q's device")
+        a.n_stream_dev = stream_n_dev.data_ptr()
+        step.append(stream_n_dev)
+    else:
+        a.n_stream_dev = None
     if mask is not None:
         m = mask.reshape(B, -1)
         n_total = (a.n_sink + a.n_comp + a.n_win + a.n_dec + a.n_stream)

@@ -378,3 +378,51 @@ def test_decode_long_split_other_groups(cuda, case):
     err, cos = compare(got, want)
     print(f"long split {case}: max_abs={err:.3e} cos={cos:.7f}", flush=True)
     assert err <= TOL_ABS and cos >= TOL_COS
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_decode_stream_count_from_device(cuda, kernel):
+    """shard_decode_args.n_stream_dev: a call planned for 40 stream rows that
+    reads a smaller count (and a larger one, clamped) from the device attends
+    over exactly that many rows: against the fp64 oracle of the layer holding
+    only those rows, and one call block reused with new counts (as a captured
+    graph replays it)."""
+    from shard_amd import ops
+    B, n_comp, n_plan = 2, 700, 40
+    gc, inv = random_layer(B=B, n_comp=n_comp, n_stream=n_plan, seed=21)
+    d = to_device(gc, cuda, inv)
+    q = torch.randn(B, 32, 1, 128, generator=torch.Generator().manual_seed(6)).half()
+    cnt = torch.zeros(1, dtype=torch.int32, device=cuda)
+    pos = torch.zeros(1, dtype=torch.int64, device=cuda)
+    call = ops.make_decode_args(q.to(cuda).reshape(B, 32, 128), d, pos, None, stream_n=n_plan,
+                                stream_n_dev=cnt)
+    call.args.kernel = kernel
+    ws = ops.decode_workspace(call)
+    for n_now in (25, 0, 1, 40, 57):
+        s = min(n_now, n_plan)
+        part = dict(gc, stream_n=s * B)
+        pos_q = 4 + n_comp + 64 + s - 1
+        want = exact.decode_attention(q.numpy(), part, 8, pos_q, inv.numpy())
+        cnt.fill_(n_now)
+        pos.fill_(pos_q)
+        got = ops.decode_attn(call, ws).cpu().float().numpy().reshape(B, 32, 1, 128)
+        err, cos = compare(got, want)
+        print(f"kernel={kernel} count={n_now}: max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (n_now, err, cos)
+
+
+def test_decode_stream_count_from_device_rejects_mask(cuda):
+    """A device stream count with an attention mask is refused (the mask row
+    would have to follow the count) before anything is launched."""
+    from shard_amd import ops
+    from shard_amd._lib import ShardHipError
+    gc, inv = random_layer(B=1, n_comp=100, n_stream=8, seed=22)
+    d = to_device(gc, cuda, inv)
+    q = torch.randn(1, 32, 128).half().to(cuda)
+    mask = torch.zeros(1, 4 + 100 + 64 + 8, device=cuda)
+    cnt = torch.full((1,), 8, dtype=torch.int32, device=cuda)
+    call = ops.make_decode_args(q, d, 4 + 100 + 64 + 7, None, mask=mask, stream_n=8,
+                                stream_n_dev=cnt)
+    with pytest.raises(ShardHipError) as exc:
+        ops.decode_attn(call)
+    assert exc.value.code == -1  # SHARD_ERR_ARG

@@ -398,3 +398,55 @@ def test_prefill_kernels_at_config4_layer_size(cuda):
     got = ops.int4_quant_pack(proj, torch.tensor(alloc, dtype=torch.int32))
     assert np.array_equal(got["packed"].cpu().numpy(), chain["packed"])
     assert np.array_equal(got["coeff_scale"].cpu().numpy(), chain["coeff_scale"])
+
+
+@pytest.mark.parametrize("qjl", [False, True])
+def test_rope_stream_append_dev_row(cuda, qjl):
+    """shard_rope_stream_append_dev: the token goes to the buffers' row
+    row_dev[0] (read on the device), bit-identical to shard_rope_stream_append
+    writing that row by address; every other row is untouched, and a row at or
+    past row_cap writes no stream row (q after RoPE is still written)."""
+    ops = _ops()
+    B, H, G, hd, cap = 3, 8, 2, 128, 6
+    g = torch.Generator().manual_seed(71)
+    q = (torch.randn(B, H, hd, generator=g) * 3).half().to(cuda)
+    k = (torch.randn(B, G, hd, generator=g) * 3).half().to(cuda)
+    v = torch.randn(B, G, hd, generator=g).half().to(cuda)
+    inv = torch.as_tensor(ref.default_inv_freq(500000.0, hd), dtype=torch.float32)
+    emb = torch.cat([inv * 777.0, inv * 777.0])[None]
+    cos, sin = emb.cos().half().to(cuda), emb.sin().half().to(cuda)
+    signs = torch.from_numpy(ref.stream_signs(4, hd)).to(cuda)
+    cb = torch.from_numpy(ref.lloyd_max_codebook(hd, 8)).to(cuda)
+
+    def buffers():
+        torch.manual_seed(5)
+        u8 = lambda: torch.randint(0, 256, (cap, B, G, hd), dtype=torch.uint8).to(cuda)
+        f16 = lambda *s: torch.randn(cap, B, G, *s).half().to(cuda)
+        return {"ki": u8(), "vi": u8(), "ks": u8(), "vs": u8(), "kn": f16(), "vn": f16(),
+                "kc": f16(), "vc": f16(), "kd": f16(hd), "vd": f16(hd)}
+
+    order = ("ki", "kn", "kd", "vi", "vn", "vd")
+    qorder = ("ks", "kc", "vs", "vc")
+    for row in (0, 4, cap):
+        want, got = buffers(), buffers()
+        q_want = torch.empty(B, H, hd, dtype=torch.float16, device=cuda)
+        q_got = torch.empty_like(q_want)
+        r = min(row, cap - 1)
+        if row < cap:
+            at = lambda n: want[n][r].data_ptr()
+            ops.rope_stream_append_at(q, k, v, cos, sin, signs, cb, q_want, *(at(n) for n in order),
+                                      *((at(n) for n in qorder) if qjl else (None,) * 4))
+        else:
+            ops.rope_stream_append_at(q, k, v, cos, sin, signs, cb, q_want,
+                                      *(want[n][r].data_ptr() for n in order),
+                                      *((want[n][r].data_ptr() for n in qorder) if qjl else (None,) * 4))
+            want = buffers()  # a row past the buffers: nothing is written
+        row_dev = torch.tensor([row], dtype=torch.int32, device=cuda)
+        base = lambda n: got[n].data_ptr()
+        ops.rope_stream_append_at(q, k, v, cos, sin, signs, cb, q_got, *(base(n) for n in order),
+                                  *((base(n) for n in qorder) if qjl else (None,) * 4),
+                                  row_dev=row_dev, row_cap=cap)
+        torch.cuda.synchronize()
+        assert torch.equal(q_got, q_want), row
+        for n in order + (qorder if qjl else ()):
+            assert torch.equal(got[n], want[n]), (row, n)
