@@ -511,6 +511,23 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
                                       .min().item(), 6),
                 "max_abs_logit_diff": round((fused - plain).abs().max().item(), 5)}
 
+    def graph_decode(cache, tok, n):
+        """n more greedy steps from the cache's state, captured once in a HIP
+        graph (shard_amd.graph.DecodeGraph) and replayed: one eager step and
+        the capture first, then n replays timed."""
+        from shard_amd.graph import DecodeGraph
+        dg = DecodeGraph(model, cache, tok, max_steps=n + 2)
+        dg.step()
+        dg.step()
+        t0 = sync_time()
+        for _ in range(n):
+            dg.step()
+        t1 = sync_time()
+        dg.close()
+        return {"decode_s": round(t1 - t0, 3), "tokens_per_s": round(batch * n / (t1 - t0), 1),
+                "ms_per_step": round((t1 - t0) / n * 1000.0, 3), "steps": n,
+                "how": "greedy steps replayed from one captured HIP graph of the whole decode step"}
+
     with torch.no_grad():                      # warm-up on a short prompt (kernels, allocator)
         wc = Cache.from_model(model)
         wc._streaming = True
@@ -567,11 +584,14 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
         if kind == "shard":
             r["fused_vs_unfused_step"] = fused_vs_unfused(cache, fp16_toks[:, -1:])
             progress(f"shard: fused vs unfused step {r['fused_vs_unfused_step']}")
+            r["graph"] = graph_decode(cache, fp16_toks[:, -1:], new_tokens)
+            progress(f"shard: graph decode {r['graph']['tokens_per_s']} tokens/s")
         res[kind] = r
         del cache
     return {"metric": "e2e decode tokens/s, shard cache vs fp16 cache (BASELINE config 5)",
             "unit": "tokens/s", "value": res["shard"]["tokens_per_s"],
             "vs_fp16_cache": round(res["shard"]["tokens_per_s"] / res["fp16"]["tokens_per_s"], 3),
+            "graph_tokens_per_s": res["shard"]["graph"]["tokens_per_s"],
             "config": {"model": "Llama-3.1-8B architecture, random init, fp16", "layers": layers,
                        "batch": batch, "prompt": prompt, "new_tokens": new_tokens,
                        "data": "random token ids (seeded)"},

@@ -59,13 +59,23 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
                                           gc["win_k"].shape[2] + stream_n +
                                           (dec[0].shape[2] if dec else 0)):]
     n_splits = getattr(c, "_n_splits", 0)
+    stream_n_dev = None
+    graph = getattr(c, "_graph", None)
+    if graph is not None:
+        # a captured decode step: the stream count and the position come from
+        # the graph's device counters, the plan covers the reserved rows.  The
+        # graph runs the model without an attention mask (rows of equal
+        # length), so the causal mask transformers builds for the one query
+        # token keeps every key: the call takes none.
+        mask = None
+        stream_n, stream_n_dev, pos_q = graph.cap, graph.rows[1:2], graph.pos
     call = gc.get("_decode_call")
     if call is None or call.args.batch != B or call.args.n_q_heads != n_q:
         call = ops.make_decode_args(q, gc, pos_q, inv, mask=mask, n_splits=n_splits,
-                                    stream_n=stream_n, decode_kv=dec)
+                                    stream_n=stream_n, decode_kv=dec, stream_n_dev=stream_n_dev)
         gc["_decode_call"] = call  # the layer's argument block, refreshed per step
     else:
-        call.refresh(q, gc, pos_q, inv, mask, n_splits, None, stream_n, dec)
+        call.refresh(q, gc, pos_q, inv, mask, n_splits, None, stream_n, dec, stream_n_dev)
     # the device's shared workspace; the size query runs only when the library
     # reports it too small (before launching anything)
     try:

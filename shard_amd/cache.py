@@ -171,10 +171,12 @@ class CacheLayer(CacheLayerMixin):
         return self._keys, self._values
 
     # -- decode stream (cache.py:193-279) ----------------------------------
-    def _stream_rows(self, B, G, D, dev):
+    def _stream_rows(self, B, G, D, dev, min_cap=0, row=None):
         """Device addresses of the next stream row of every buffer, growing the
-        buffers by doubling when full (cache.py:220-230).  Returns (codebook
-        tensors, k row pointers, v row pointers, QJL pointers)."""
+        buffers by doubling when full (cache.py:220-230), and to at least
+        min_cap rows.  row: the row whose addresses are returned instead of the
+        next one (0: the buffers' bases).  Returns (codebook tensors, k row
+        pointers, v row pointers, QJL pointers)."""
         gc = self._gpu_compressed
         c = self._cache_ref
         bits, qjl = int(c._stream_bits), bool(c._stream_qjl)
@@ -187,8 +189,9 @@ class CacheLayer(CacheLayerMixin):
             gc["stream_bits"] = bits
         s = gc.get("stream_n", 0) // B
         names = _STREAM_BUFS_QJL if qjl else _STREAM_BUFS
-        if gc.get("_stream_cap", 0) <= s or (qjl and "k_qsign_buf" not in gc):
-            cap = max(s + 1, 16 if gc.get("_stream_cap", 0) == 0 else 2 * gc["_stream_cap"])
+        if (gc.get("_stream_cap", 0) <= max(s, min_cap - 1)
+                or (qjl and "k_qsign_buf" not in gc)):
+            cap = max(s + 1, min_cap, 16 if gc.get("_stream_cap", 0) == 0 else 2 * gc["_stream_cap"])
             for name in names:
                 per_token, dtype = _stream_buf_shape(name, B, G, D)
                 buf = gc.get(name)
@@ -209,6 +212,8 @@ class CacheLayer(CacheLayerMixin):
             gc["_stream_base"] = base
         ki, kn, kd, vi, vn, vd, kqs, kqc, vqs, vqc = base[2]
         rows = B * G
+        if row is not None:
+            s = row
         p8, p16, n16 = s * rows * D, 2 * s * rows * D, 2 * s * rows
         kp = (ki + p8, kn + n16, kd + p16)
         vp = (vi + p8, vn + n16, vd + p16)
@@ -242,7 +247,10 @@ class CacheLayer(CacheLayerMixin):
         B, H, _, D = q.shape
         G = k.shape[1]
         self._lazy_evict()
-        cbs, kp, vp, qp = self._stream_rows(B, G, D, q.device)
+        graph = getattr(self._cache_ref, "_graph", None)
+        # under a decode graph the token's row comes from the graph's device
+        # counter, so the launch takes the buffers' bases
+        cbs, kp, vp, qp = self._stream_rows(B, G, D, q.device, row=0 if graph else None)
         # q after RoPE goes to a per-layer buffer: this step's attention reads it
         # (stream-ordered before the next step's append rewrites it)
         q_out = gc.get("_q_rope")
@@ -251,8 +259,10 @@ class CacheLayer(CacheLayerMixin):
             gc["_q_rope"] = q_out
         c16 = lambda t, *shape: t.reshape(*shape).contiguous()
         Bc = cos.shape[0]  # 1 when the batch shares its positions
+        dev_row = {} if graph is None else {"row_dev": graph.rows[0:1], "row_cap": gc["_stream_cap"]}
         ops.rope_stream_append_at(c16(q, B, H, D), c16(k, B, G, D), c16(v, B, G, D),
-                                  c16(cos, Bc, D), c16(sin, Bc, D), *cbs, q_out, *kp, *vp, *qp)
+                                  c16(cos, Bc, D), c16(sin, Bc, D), *cbs, q_out, *kp, *vp, *qp,
+                                  **dev_row)
         gc["stream_n"] = gc.get("stream_n", 0) + B
         self._seq_len += 1
         self._needs_decompress = True
@@ -332,6 +342,7 @@ class Cache(HFCache):
         self._fused_decode_update = False
         # decode-attention knobs of the HIP kernel (0 = automatic split count)
         self._n_splits = 0
+        self._graph = None  # the DecodeGraph whose device counters decode steps use
         self._basis_override = None  # {layer_idx: (1024, rank) fp32} to pin the PCA basis
         super().__init__(layers=[CacheLayer(i) for i in range(num_layers)])
         for l in self.layers:

@@ -1,0 +1,128 @@
+"""A decode step captured in a HIP graph (shard_amd.graph.DecodeGraph) against
+eager decode steps of the same random-init Llama on an identical cache state.
+The graph's attention calls read the stream count and the position from
+device counters and plan for the reserved stream rows, so their split plan
+differs from the eager calls': the logits agree to fp32 summation order, and
+layer 0's stream codes (its K/V do not depend on attention) are bit-identical,
+which also shows that every replay appended its token to the next row."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 512
+
+
+def _model(dev):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=1024, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                      head_dim=128, max_position_embeddings=4096, rope_theta=500000.0)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).to(dev, torch.float16).eval()
+
+
+def _prefilled(model, ids, first, qjl):
+    """Prefill, then one eager decode step (it compresses the layers and
+    starts the stream)."""
+    from shard import Cache
+    cache = Cache.from_model(model)
+    cache._streaming = True
+    cache._stream_qjl = qjl
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        model(first, past_key_values=cache, use_cache=True)
+    return cache
+
+
+def _compare(got, want, what):
+    err = (got - want).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0).item()
+    scale = want.abs().max().item()
+    print(f"{what}: max|diff| {err:.3e} (scale {scale:.3f}) cos {cos:.7f}", flush=True)
+    assert err <= 1e-2 * max(scale, 1.0) and cos >= 0.9999, (what, err, cos)
+
+
+@pytest.mark.parametrize("B,qjl", [(1, False), (3, False), (2, True)])
+def test_decode_graph_matches_eager_steps(cuda, B, qjl):
+    from shard import enable_llama_fused_attention
+    from shard_amd.graph import DecodeGraph
+    model = _model(cuda)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(B)
+    ids = torch.randint(0, VOCAB, (B, 300), generator=g).to(cuda)
+    first = torch.randint(0, VOCAB, (B, 1), generator=g).to(cuda)
+    feed = torch.randint(0, VOCAB, (B, 12), generator=g).to(cuda)  # teacher-forced tokens
+    cache_e = _prefilled(model, ids, first, qjl)
+    cache_g = _prefilled(model, ids, first, qjl)
+    steps = feed.shape[1]
+
+    want = []
+    with torch.no_grad():
+        for s in range(steps):
+            want.append(model(feed[:, s:s + 1], past_key_values=cache_e, use_cache=True).logits[:, -1].float())
+    dg = DecodeGraph(model, cache_g, feed[:, :1], max_steps=steps)
+    got = []
+    for s in range(steps):
+        tok = dg.step(feed[:, s:s + 1])
+        got.append(dg.logits.float().clone())
+        assert torch.equal(tok, got[-1].argmax(-1))
+    for s in range(steps):
+        _compare(got[s], want[s], f"[graph B={B} qjl={qjl}] step {s}")
+    with pytest.raises(RuntimeError):
+        dg.step()
+
+    # the host counters followed the replays; layer 0's stream rows are the eager ones
+    for le, lg in zip(cache_e.layers, cache_g.layers):
+        assert lg._gpu_compressed["stream_n"] == le._gpu_compressed["stream_n"] == (steps + 1) * B
+        assert lg._seq_len == le._seq_len
+    ge, gg = cache_e.layers[0]._gpu_compressed, cache_g.layers[0]._gpu_compressed
+    n = steps + 1
+    names = ["k_idx_buf", "v_idx_buf", "k_norm_buf", "v_norm_buf", "k_deq_buf", "v_deq_buf"]
+    if qjl:
+        names += ["k_qsign_buf", "v_qsign_buf", "k_qscale_buf", "v_qscale_buf"]
+    for name in names:
+        assert torch.equal(gg[name][:n].view(torch.uint8), ge[name][:n].view(torch.uint8)), name
+
+    # back to eager steps on the graph's cache
+    dg.close()
+    nxt = torch.randint(0, VOCAB, (B, 1), generator=g).to(cuda)
+    with torch.no_grad():
+        a = model(nxt, past_key_values=cache_e, use_cache=True).logits[:, -1].float()
+        b = model(nxt, past_key_values=cache_g, use_cache=True).logits[:, -1].float()
+    _compare(b, a, f"[graph B={B} qjl={qjl}] eager step after close")
+
+
+def test_decode_graph_greedy_feeds_its_own_tokens(cuda):
+    """Without supplied tokens each replay decodes the previous step's argmax:
+    the same tokens as eager greedy steps from the same state."""
+    from shard import enable_llama_fused_attention
+    from shard_amd.graph import DecodeGraph
+    model = _model(cuda)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, VOCAB, (2, 300), generator=g).to(cuda)
+    first = torch.randint(0, VOCAB, (2, 1), generator=g).to(cuda)
+    cache_e = _prefilled(model, ids, first, False)
+    cache_g = _prefilled(model, ids, first, False)
+    start = torch.randint(0, VOCAB, (2, 1), generator=g).to(cuda)
+    steps = 8
+    dg = DecodeGraph(model, cache_g, start, max_steps=steps)
+    got = [dg.step() for _ in range(steps)]
+    cur, want, agree = start, [], 0
+    with torch.no_grad():
+        for s in range(steps):
+            logits = model(cur, past_key_values=cache_e, use_cache=True).logits[:, -1]
+            nxt = logits.argmax(-1)
+            want.append(nxt)
+            if not torch.equal(nxt, got[s]):
+                # a near-tie may flip under the graph's other summation order;
+                # then the two runs decode different tokens from here on
+                top2 = logits.float().topk(2, dim=-1).values
+                assert (top2[:, 0] - top2[:, 1]).min().item() < 5e-2, s
+                break
+            agree += 1
+            cur = nxt.view(-1, 1)
+    print(f"[graph greedy] {agree} of {steps} steps agree", flush=True)
+    assert agree >= 1
+    dg.close()

@@ -193,3 +193,16 @@ def test_decode_supported_shapes():
                     a.rank, a.n_comp = rank, 100
                     want = bool(lib.shard_decode_supported(ctypes.byref(a)))
                     assert ops.decode_supported(hd, g * n_kv, n_kv, rank) == want, (hd, n_kv, g, rank)
+
+
+def test_decode_graph_refuses_other_caches():
+    """DecodeGraph takes a compressed, streaming shard Cache only (checked before
+    anything touches the GPU)."""
+    import torch
+    from shard_amd import Cache
+    from shard_amd.graph import DecodeGraph
+    ids = torch.zeros(1, 1, dtype=torch.long)
+    with pytest.raises(TypeError):
+        DecodeGraph(None, object(), ids, 4)
+    with pytest.raises(ValueError):
+        DecodeGraph(None, Cache(num_layers=1, device="cpu"), ids, 4)
