@@ -224,6 +224,10 @@ class CacheLayer(CacheLayerMixin):
         """Quantize one decode token (B, G, 1, D) of K and V into the 8-bit
         stream buffers (growable, doubling, as cache.py:220-230)."""
         gc = self._gpu_compressed
+        if getattr(self._cache_ref, "_graph", None) is not None:
+            # this launch takes the row by address, which a replay would repeat
+            raise RuntimeError("under a decode graph tokens are appended by fused_rope_append "
+                               "(fp16 q, k, v, cos and sin)")
         B, G, _, D = k.shape
         cbs, kp, vp, qp = self._stream_rows(B, G, D, k.device)
         kx = k.reshape(B, G, D)
