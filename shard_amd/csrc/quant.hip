@@ -652,51 +652,55 @@ void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __res
 }
 
 // ---------------------------------------------------------------------------
-// Deterministic k-means update: stable counting sort by centroid, then each
-// (centroid, dim) sums its rows in increasing row order (torch CPU index_add_
-// order), divides by the count, and keeps empty centroids.
+// Deterministic k-means update: stable counting sort of the rows by centroid
+// into a sorted copy, then each (centroid, dim) sums its rows in increasing
+// row order (torch CPU index_add_ order), divides by the count, and keeps
+// empty centroids.
+//   blk[q * nblk + b]: rows of block b (KM_R rows) with centroid q; after the
+//   scan, the first slot of those rows within centroid q's run.
 // ---------------------------------------------------------------------------
-constexpr int KM_BLOCK = 256;
+constexpr int KM_R = 4096;   // rows per block of the counting sort
+constexpr int KM_DMAX = 8;   // widest rows the sorted copy holds
 
-__global__ void k_km_hist(const int32_t* __restrict__ idx, int64_t n, int k,
-                          int32_t* __restrict__ blk_hist) {
+__global__ __launch_bounds__(256) void k_km_hist(const int32_t* __restrict__ idx, int64_t n, int k,
+                                                 int64_t nblk, int32_t* __restrict__ blk) {
   __shared__ int32_t h[1024];
   for (int i = threadIdx.x; i < k; i += blockDim.x) h[i] = 0;
   __syncthreads();
-  int64_t r = (int64_t)blockIdx.x * KM_BLOCK + threadIdx.x;
-  if (r < n) atomicAdd(&h[idx[r]], 1);
+  const int64_t r0 = (int64_t)blockIdx.x * KM_R;
+  for (int i = threadIdx.x; i < KM_R; i += blockDim.x)
+    if (r0 + i < n) atomicAdd(&h[idx[r0 + i]], 1);
   __syncthreads();
-  for (int i = threadIdx.x; i < k; i += blockDim.x) blk_hist[(int64_t)blockIdx.x * k + i] = h[i];
+  for (int q = threadIdx.x; q < k; q += blockDim.x) blk[(int64_t)q * nblk + blockIdx.x] = h[q];
 }
 
 // For each centroid (one workgroup): exclusive scan of its per-block counts
-// over the blocks (in place) and its total count.  Thread t owns a contiguous
-// run of blocks; run totals are scanned in LDS.
-__global__ __launch_bounds__(256) void k_km_scan_blocks(int32_t* __restrict__ blk_hist, int64_t nblk,
-                                                        int k, int32_t* __restrict__ count) {
-  __shared__ int32_t part[256];
-  const int q = blockIdx.x;
-  const int t = threadIdx.x;
-  const int64_t per = (nblk + 255) / 256;
-  const int64_t b0 = (int64_t)t * per;
-  const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
-  int32_t sum = 0;
-  for (int64_t b = b0; b < b1; ++b) sum += blk_hist[b * k + q];
-  part[t] = sum;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {  // inclusive Hillis-Steele scan
-    const int32_t v = t >= o ? part[t - o] : 0;
+// (contiguous, 256 at a time: wave scans, then the four wave totals) in place,
+// and its total count.
+__global__ __launch_bounds__(256) void k_km_scan_blocks(int32_t* __restrict__ blk, int64_t nblk,
+                                                        int32_t* __restrict__ count) {
+  __shared__ int32_t wsum[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int32_t* row = blk + (int64_t)blockIdx.x * nblk;
+  int32_t carry = 0;
+  for (int64_t base = 0; base < nblk; base += 256) {
+    const int64_t i = base + t;
+    const int32_t v = i < nblk ? row[i] : 0;
+    int32_t sc = v;  // inclusive scan over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t u = __shfl_up(sc, o, 64);
+      if (lane >= o) sc += u;
+    }
+    if (lane == 63) wsum[w] = sc;
     __syncthreads();
-    part[t] += v;
-    __syncthreads();
+    int32_t pre = carry;
+    for (int u = 0; u < w; ++u) pre += wsum[u];
+    if (i < nblk) row[i] = pre + sc - v;
+    carry += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();  // wsum is rewritten by the next round
   }
-  int32_t run = t > 0 ? part[t - 1] : 0;
-  for (int64_t b = b0; b < b1; ++b) {
-    const int32_t v = blk_hist[b * k + q];
-    blk_hist[b * k + q] = run;
-    run += v;
-  }
-  if (t == 255) count[q] = part[255];
+  if (t == 0) count[blockIdx.x] = carry;
 }
 
 __global__ void k_km_offsets(const int32_t* __restrict__ count, int k, int32_t* __restrict__ off) {
@@ -709,64 +713,127 @@ __global__ void k_km_offsets(const int32_t* __restrict__ count, int k, int32_t* 
   }
 }
 
-__global__ void k_km_scatter(const int32_t* __restrict__ idx, int64_t n, int k,
-                             const int32_t* __restrict__ blk_off, const int32_t* __restrict__ off,
-                             int32_t* __restrict__ perm) {
-  __shared__ int32_t s[KM_BLOCK];
-  int64_t r = (int64_t)blockIdx.x * KM_BLOCK + threadIdx.x;
-  int my = r < n ? idx[r] : -1;
-  s[threadIdx.x] = my;
+// One wave per block of KM_R rows, 64 rows per round in increasing order.  A
+// row's slot is its centroid's running count in the block (LDS) plus the
+// number of lower lanes of the round with the same centroid (lanes that agree
+// on every bit of the centroid index, from one ballot per bit); the last lane
+// of each centroid's group then advances the count.  The row's D values go to
+// the sorted copy at that slot.
+template <int D>
+__global__ __launch_bounds__(64) void k_km_scatter(const float* __restrict__ x,
+                                                   const int32_t* __restrict__ idx, int64_t n,
+                                                   int k, int64_t nblk,
+                                                   const int32_t* __restrict__ blk,
+                                                   const int32_t* __restrict__ off,
+                                                   float* __restrict__ xs) {
+  __shared__ int32_t run[1024];
+  const int lane = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  for (int q = lane; q < k; q += 64) run[q] = off[q] + blk[(int64_t)q * nblk + b];
   __syncthreads();
-  if (r >= n) return;
-  int rank = 0;
-  for (int j = 0; j < (int)threadIdx.x; ++j) rank += (s[j] == my);
-  perm[off[my] + blk_off[(int64_t)blockIdx.x * k + my] + rank] = (int32_t)r;
+  const int nbits = k > 1 ? 32 - __builtin_clz((unsigned)(k - 1)) : 0;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t r0 = b * KM_R;
+  for (int rr = 0; rr < KM_R && r0 + rr < n; rr += 64) {
+    const int64_t r = r0 + rr + lane;
+    const bool valid = r < n;
+    const int key = valid ? idx[r] : 0;
+    float xv[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) xv[j] = valid ? x[r * D + j] : 0.f;
+    uint64_t m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (key >> bit) & 1;
+      const uint64_t bb = __ballot(on);
+      m &= on ? bb : ~bb;
+    }
+    const int rank = __popcll(m & below);
+    const int grp = __popcll(m);
+    const int slot = valid ? run[key] + rank : 0;
+    // every lane has read its centroid's count (LDS is in order within the
+    // wave) before the group's last lane advances it
+    if (valid && rank == grp - 1) run[key] += grp;
+    if (valid) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) xs[(int64_t)slot * D + j] = xv[j];
+    }
+  }
 }
 
-// One workgroup per centroid.  Its rows (perm[off .. off+cnt), increasing row
-// order) are gathered 256 at a time into LDS, dim-major, double-buffered; lanes
-// 0..D-1 of wave 0 then add them in order, one running sum per dim, while the
-// other threads gather the next chunk.
+// One workgroup per centroid over its run of the sorted copy (increasing row
+// order).  Chunks of 256 P rows are loaded (coalesced) one chunk ahead and
+// staged in LDS dim-major (columns padded so the D lanes read distinct
+// banks), double-buffered; lanes 0..D-1 of wave 0 add them in order, one
+// running sum per dim, with the LDS reads of the next 32 values in flight
+// while the current 32 are added.
 template <int D>
-__global__ __launch_bounds__(256) void k_km_sum(const float* __restrict__ x, const int32_t* __restrict__ perm,
+__global__ __launch_bounds__(256) void k_km_sum(const float* __restrict__ xs,
                                                 const int32_t* __restrict__ count,
                                                 const int32_t* __restrict__ off,
                                                 const float* __restrict__ c, int k,
                                                 float* __restrict__ newc, uint32_t* __restrict__ maxd) {
-  __shared__ __align__(16) float buf[2][D][256];
+  constexpr int P = D <= 4 ? 4 : 2;  // rows per thread per chunk
+  constexpr int CH = 256 * P;        // rows per chunk
+  constexpr int CS = CH + 4;         // column stride
+  __shared__ __align__(16) float buf[2][D][CS];
   const int q = blockIdx.x;
   const int t = threadIdx.x;
-  const int32_t cnt = count[q], o = off[q];
-  float xv[D];
-  auto gather = [&](int32_t base) {
-    if (base + t < cnt) {
-      const int64_t row = perm[o + base + t];
+  const int32_t cnt = count[q];
+  const float* src = xs + (int64_t)off[q] * D;
+  float xv[P][D];
+  auto load = [&](int32_t base) {
 #pragma unroll
-      for (int j = 0; j < D; ++j) xv[j] = x[row * D + j];
+    for (int p = 0; p < P; ++p) {
+      const int32_t row = base + 256 * p + t;
+      if (row < cnt) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) xv[p][j] = src[(int64_t)row * D + j];
+      }
     }
   };
-  gather(0);
+  load(0);
   float acc = 0.f;
   int cur = 0;
-  for (int32_t base = 0; base < cnt; base += 256) {
-    if (base + t < cnt) {
+  for (int32_t base = 0; base < cnt; base += CH) {
 #pragma unroll
-      for (int j = 0; j < D; ++j) buf[cur][j][t] = xv[j];
+    for (int p = 0; p < P; ++p) {
+      if (base + 256 * p + t < cnt) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) buf[cur][j][256 * p + t] = xv[p][j];
+      }
     }
     __syncthreads();
-    gather(base + 256);
+    load(base + CH);
     if (t < D) {
-      const int n_here = cnt - base < 256 ? cnt - base : 256;
+      const int n_here = cnt - base < CH ? cnt - base : CH;
       const float* col = buf[cur][t];
-      int i = 0;
-      for (; i + 4 <= n_here; i += 4) {
-        const float4 v = *(const float4*)(col + i);
-        acc = add_rn(acc, v.x);
-        acc = add_rn(acc, v.y);
-        acc = add_rn(acc, v.z);
-        acc = add_rn(acc, v.w);
+      const float4* c4 = (const float4*)col;
+      const int nb = n_here >> 5;  // blocks of 32 values
+      float4 va[8], vb[8];
+      auto rd = [&](float4 (&r)[8], int blk) {  // a block past the end reads the last one (unused)
+        const int bb = blk < nb ? blk : nb - 1;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r[u] = c4[8 * bb + u];
+      };
+      auto sum32 = [&](const float4 (&r)[8]) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          acc = add_rn(acc, r[u].x);
+          acc = add_rn(acc, r[u].y);
+          acc = add_rn(acc, r[u].z);
+          acc = add_rn(acc, r[u].w);
+        }
+      };
+      if (nb > 0) rd(va, 0);
+      int blk = 0;
+      for (; blk + 2 <= nb; blk += 2) {  // va holds block blk
+        rd(vb, blk + 1);
+        sum32(va);
+        rd(va, blk + 2);
+        sum32(vb);
       }
-      for (; i < n_here; ++i) acc = add_rn(acc, col[i]);
+      if (blk < nb) sum32(va);
+      for (int i = nb * 32; i < n_here; ++i) acc = add_rn(acc, col[i]);
     }
     cur ^= 1;
   }
@@ -1210,8 +1277,10 @@ int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids
 
 size_t shard_kmeans_update_workspace(int64_t n, int32_t k) {
   if (n <= 0 || k <= 0) return 0;
-  int64_t nblk = (n + KM_BLOCK - 1) / KM_BLOCK;
-  return (size_t)(nblk * k + 2 * (int64_t)k + n) * sizeof(int32_t);
+  const int64_t nblk = (n + KM_R - 1) / KM_R;
+  // per-block counts, counts, offsets, then the sorted copy (rows up to KM_DMAX wide)
+  const int64_t ints = ((nblk * k + 2 * (int64_t)k) + 3) & ~(int64_t)3;
+  return (size_t)ints * sizeof(int32_t) + (size_t)n * KM_DMAX * sizeof(float);
 }
 
 int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx,
@@ -1221,24 +1290,36 @@ int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx
   if (!x || !idx || !centroids || !new_centroids || !max_delta || n <= 0 || k <= 0)
     return SHARD_ERR_ARG;
   if (k > 1024 || (d != 1 && d != 2 && d != 4 && d != 8)) return SHARD_ERR_SHAPE;
+  if (n > INT32_MAX) return SHARD_ERR_SHAPE;  // slots are int32
   if (!workspace || workspace_bytes < shard_kmeans_update_workspace(n, k)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
-  int64_t nblk = (n + KM_BLOCK - 1) / KM_BLOCK;
+  const int64_t nblk = (n + KM_R - 1) / KM_R;
   int32_t* blk = (int32_t*)workspace;
   int32_t* count = blk + nblk * k;
   int32_t* off = count + k;
-  int32_t* perm = off + k;
-  hipLaunchKernelGGL(k_km_hist, dim3((unsigned)nblk), dim3(KM_BLOCK), 0, s, idx, n, k, blk);
-  hipLaunchKernelGGL(k_km_scan_blocks, dim3((unsigned)k), dim3(256), 0, s, blk, nblk, k, count);
+  float* xs = (float*)(blk + (((nblk * k + 2 * (int64_t)k) + 3) & ~(int64_t)3));
+  hipLaunchKernelGGL(k_km_hist, dim3((unsigned)nblk), dim3(256), 0, s, idx, n, k, nblk, blk);
+  hipLaunchKernelGGL(k_km_scan_blocks, dim3((unsigned)k), dim3(256), 0, s, blk, nblk, count);
   hipLaunchKernelGGL(k_km_offsets, dim3(1), dim3(64), 0, s, count, k, off);
-  hipLaunchKernelGGL(k_km_scatter, dim3((unsigned)nblk), dim3(KM_BLOCK), 0, s, idx, n, k, blk, off, perm);
   hipLaunchKernelGGL(k_km_zero, dim3(1), dim3(1), 0, s, (uint32_t*)max_delta);
-  const unsigned kb = (unsigned)k;
+  const unsigned kb = (unsigned)k, nb = (unsigned)nblk;
   switch (d) {
-    case 1: hipLaunchKernelGGL(k_km_sum<1>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
-    case 2: hipLaunchKernelGGL(k_km_sum<2>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
-    case 4: hipLaunchKernelGGL(k_km_sum<4>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
-    default: hipLaunchKernelGGL(k_km_sum<8>, dim3(kb), dim3(256), 0, s, x, perm, count, off, centroids, k, new_centroids, (uint32_t*)max_delta); break;
+    case 1:
+      hipLaunchKernelGGL(k_km_scatter<1>, dim3(nb), dim3(64), 0, s, x, idx, n, k, nblk, blk, off, xs);
+      hipLaunchKernelGGL(k_km_sum<1>, dim3(kb), dim3(256), 0, s, xs, count, off, centroids, k, new_centroids, (uint32_t*)max_delta);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_km_scatter<2>, dim3(nb), dim3(64), 0, s, x, idx, n, k, nblk, blk, off, xs);
+      hipLaunchKernelGGL(k_km_sum<2>, dim3(kb), dim3(256), 0, s, xs, count, off, centroids, k, new_centroids, (uint32_t*)max_delta);
+      break;
+    case 4:
+      hipLaunchKernelGGL(k_km_scatter<4>, dim3(nb), dim3(64), 0, s, x, idx, n, k, nblk, blk, off, xs);
+      hipLaunchKernelGGL(k_km_sum<4>, dim3(kb), dim3(256), 0, s, xs, count, off, centroids, k, new_centroids, (uint32_t*)max_delta);
+      break;
+    default:
+      hipLaunchKernelGGL(k_km_scatter<8>, dim3(nb), dim3(64), 0, s, x, idx, n, k, nblk, blk, off, xs);
+      hipLaunchKernelGGL(k_km_sum<8>, dim3(kb), dim3(256), 0, s, xs, count, off, centroids, k, new_centroids, (uint32_t*)max_delta);
+      break;
   }
   SHARD_LAUNCH_CHECK("shard_kmeans_update");
   return SHARD_OK;

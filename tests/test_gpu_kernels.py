@@ -220,17 +220,30 @@ def test_vq_assign_out_of_range_centroids_bitexact(cuda, case):
     assert np.array_equal(got, want)
 
 
-def test_kmeans_update_bitexact(cuda):
+@pytest.mark.parametrize("n,k,d,assign", [(70000, 256, 4, "nearest"), (9000, 1000, 8, "random"),
+                                          (4097, 3, 2, "random"), (130, 1, 1, "random"),
+                                          (200000, 64, 4, "skewed")])
+def test_kmeans_update_bitexact(cuda, n, k, d, assign):
+    """The update against torch CPU index_add_ (the reference's order:
+    cache.py:30-33): rows summed per centroid in increasing row order, across
+    sort blocks of 4096 rows, partial blocks and rounds, 1 to 1000 centroids
+    (a centroid with most rows, one without rows) and rows of 1 to 8 values."""
     ops = _ops()
-    g = torch.Generator().manual_seed(4)
-    x = torch.randn(70000, 4, generator=g)
-    c = x[torch.randperm(70000, generator=g)[:256]].clone()
-    c[17] = 100.0  # an empty cluster keeps its centroid
-    idx = torch.from_numpy(ref.vq_assign_direct(x.numpy(), c.numpy()))
+    g = torch.Generator().manual_seed(n + k)
+    x = torch.randn(n, d, generator=g)
+    c = x[torch.randperm(n, generator=g)[:k]].clone()
+    if assign == "nearest":
+        c[17] = 100.0  # an empty cluster keeps its centroid
+        idx = torch.from_numpy(ref.vq_assign_direct(x.numpy(), c.numpy()))
+    elif assign == "skewed":
+        idx = torch.where(torch.rand(n, generator=g) < 0.7, torch.zeros(n, dtype=torch.int64),
+                          torch.randint(0, k - 1, (n,), generator=g))
+    else:
+        idx = torch.randint(0, max(k - 1, 1), (n,), generator=g)  # the last centroid empty (k > 1)
     new = torch.zeros_like(c)
-    cnt = torch.zeros(256)
+    cnt = torch.zeros(k)
     new.index_add_(0, idx, x)
-    cnt.index_add_(0, idx, torch.ones(70000))
+    cnt.index_add_(0, idx, torch.ones(n))
     nz = cnt > 0
     new[nz] /= cnt[nz].unsqueeze(1)
     new[~nz] = c[~nz]
