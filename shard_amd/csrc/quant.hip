@@ -734,28 +734,38 @@ __global__ __launch_bounds__(64) void k_km_scatter(const float* __restrict__ x,
   const int nbits = k > 1 ? 32 - __builtin_clz((unsigned)(k - 1)) : 0;
   const uint64_t below = (1ull << lane) - 1ull;
   const int64_t r0 = b * KM_R;
-  for (int rr = 0; rr < KM_R && r0 + rr < n; rr += 64) {
-    const int64_t r = r0 + rr + lane;
-    const bool valid = r < n;
-    const int key = valid ? idx[r] : 0;
-    float xv[D];
+  constexpr int RU = 4;  // rounds whose loads go out together
+  for (int rr = 0; rr < KM_R && r0 + rr < n; rr += 64 * RU) {
+    int key[RU];
+    float xv[RU][D];
 #pragma unroll
-    for (int j = 0; j < D; ++j) xv[j] = valid ? x[r * D + j] : 0.f;
-    uint64_t m = __ballot(valid);
-    for (int bit = 0; bit < nbits; ++bit) {
-      const bool on = (key >> bit) & 1;
-      const uint64_t bb = __ballot(on);
-      m &= on ? bb : ~bb;
+    for (int u = 0; u < RU; ++u) {
+      const int64_t r = r0 + rr + 64 * u + lane;
+      const bool valid = rr + 64 * u < KM_R && r < n;
+      key[u] = valid ? idx[r] : -1;
+#pragma unroll
+      for (int j = 0; j < D; ++j) xv[u][j] = valid ? x[r * D + j] : 0.f;
     }
-    const int rank = __popcll(m & below);
-    const int grp = __popcll(m);
-    const int slot = valid ? run[key] + rank : 0;
-    // every lane has read its centroid's count (LDS is in order within the
-    // wave) before the group's last lane advances it
-    if (valid && rank == grp - 1) run[key] += grp;
-    if (valid) {
 #pragma unroll
-      for (int j = 0; j < D; ++j) xs[(int64_t)slot * D + j] = xv[j];
+    for (int u = 0; u < RU; ++u) {
+      const bool valid = key[u] >= 0;
+      const int kk = valid ? key[u] : 0;
+      uint64_t m = __ballot(valid);
+      for (int bit = 0; bit < nbits; ++bit) {
+        const bool on = (kk >> bit) & 1;
+        const uint64_t bb = __ballot(on);
+        m &= on ? bb : ~bb;
+      }
+      const int rank = __popcll(m & below);
+      const int grp = __popcll(m);
+      const int slot = valid ? run[kk] + rank : 0;
+      // every lane has read its centroid's count (LDS is in order within the
+      // wave) before the group's last lane advances it
+      if (valid && rank == grp - 1) run[kk] += grp;
+      if (valid) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) xs[(int64_t)slot * D + j] = xv[u][j];
+      }
     }
   }
 }
