@@ -7,6 +7,7 @@ Tensors must live on a ROCm device; there is no CPU path.
 """
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -186,16 +187,44 @@ def kmeans_update(x: torch.Tensor, idx: torch.Tensor, centroids: torch.Tensor, w
 _init_rows = {}
 
 
+# torch's CPU randperm below this size: a forward Fisher-Yates shuffle of
+# 0..n-1 where step i swaps entry i with entry i + (random() % (n - i)),
+# random() being the generator's next 32-bit MT19937 output
+_RANDPERM_SHUFFLE_MAX = (2**32 - 1) // 20
+
+
+def _randperm_head(n: int, k: int, seed: int) -> torch.Tensor:
+    """The first k entries of torch.randperm(n) from a CPU generator seeded
+    with `seed`, without building the n-entry permutation.  The shuffle fixes
+    entry i at step i, so k steps decide the first k entries; they are replayed
+    on a sparse map of the swapped entries.  The generator is MT19937 seeded
+    like the standard init_genrand(seed), whose 32-bit outputs numpy's legacy
+    RandomState reproduces.  Sizes or seeds outside that form fall back to
+    torch.randperm."""
+    if not (0 < n < _RANDPERM_SHUFFLE_MAX and 0 <= seed < 2**32):
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        return torch.randperm(n, generator=g)[:k].clone()
+    steps = min(k, n - 1)
+    raw = np.random.RandomState(seed).randint(0, 2**32, size=max(steps, 0), dtype=np.uint64)
+    moved = {}
+    out = []
+    for i in range(min(k, n)):
+        if i < n - 1:
+            z = i + int(raw[i]) % (n - i)
+            a, b = moved.get(i, i), moved.get(z, z)
+            moved[i], moved[z] = b, a
+        out.append(moved.get(i, i))
+    return torch.tensor(out, dtype=torch.int64)
+
+
 def _kmeans_init_rows(n: int, k: int, seed: int) -> torch.Tensor:
-    """First k entries of randperm(n) from a CPU generator seeded with `seed`.
-    Every layer of a cache draws with the same seed (cache.py:21-26), so the
-    rows repeat for equal n; a full CPU randperm of tens of millions of rows
-    takes seconds, so it is drawn once per (n, k, seed)."""
+    """First k entries of randperm(n) from a CPU generator seeded with `seed`
+    (cache.py:21-26), kept per (n, k, seed): every layer of a cache draws with
+    the same seed, so the rows repeat for equal n."""
     key = (int(n), int(k), int(seed))
     rows = _init_rows.get(key)
     if rows is None:
-        g = torch.Generator(device="cpu").manual_seed(seed)
-        rows = torch.randperm(n, generator=g)[:k].clone()
+        rows = _randperm_head(int(n), int(k), int(seed))
         if len(_init_rows) > 64:
             _init_rows.clear()
         _init_rows[key] = rows

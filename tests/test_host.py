@@ -206,3 +206,15 @@ def test_decode_graph_refuses_other_caches():
         DecodeGraph(None, object(), ids, 4)
     with pytest.raises(ValueError):
         DecodeGraph(None, Cache(num_layers=1, device="cpu"), ids, 4)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 10, 256, 257, 1000, 123457, 5_000_000])
+@pytest.mark.parametrize("seed", [0, 7, 42])
+def test_kmeans_init_rows_equal_torch_randperm(n, seed):
+    """The k-means init rows (the first 256 entries of the reference's CPU
+    torch.randperm, cache.py:25) computed without the full permutation equal
+    torch.randperm's own."""
+    import torch
+    from shard_amd import ops
+    want = torch.randperm(n, generator=torch.Generator().manual_seed(seed))[:256]
+    assert torch.equal(ops._randperm_head(n, 256, seed), want)
