@@ -584,14 +584,18 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
         if kind == "shard":
             r["fused_vs_unfused_step"] = fused_vs_unfused(cache, fp16_toks[:, -1:])
             progress(f"shard: fused vs unfused step {r['fused_vs_unfused_step']}")
-            r["graph"] = graph_decode(cache, fp16_toks[:, -1:], new_tokens)
-            progress(f"shard: graph decode {r['graph']['tokens_per_s']} tokens/s")
+            try:
+                r["graph"] = graph_decode(cache, fp16_toks[:, -1:], new_tokens)
+                progress(f"shard: graph decode {r['graph']['tokens_per_s']} tokens/s")
+            except Exception as e:  # reported; the eager figures stand
+                r["graph"] = {"error": repr(e)}
+                progress(f"shard: graph decode failed: {e!r}")
         res[kind] = r
         del cache
     return {"metric": "e2e decode tokens/s, shard cache vs fp16 cache (BASELINE config 5)",
             "unit": "tokens/s", "value": res["shard"]["tokens_per_s"],
             "vs_fp16_cache": round(res["shard"]["tokens_per_s"] / res["fp16"]["tokens_per_s"], 3),
-            "graph_tokens_per_s": res["shard"]["graph"]["tokens_per_s"],
+            "graph_tokens_per_s": res["shard"]["graph"].get("tokens_per_s"),
             "config": {"model": "Llama-3.1-8B architecture, random init, fp16", "layers": layers,
                        "batch": batch, "prompt": prompt, "new_tokens": new_tokens,
                        "data": "random token ids (seeded)"},
