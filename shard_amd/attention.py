@@ -76,6 +76,7 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
         gc["_decode_call"] = call  # the layer's argument block, refreshed per step
     else:
         call.refresh(q, gc, pos_q, inv, mask, n_splits, None, stream_n, dec, stream_n_dev)
+    call.args.kernel = int(getattr(c, "_decode_kernel", 0))
     # the device's shared workspace; the size query runs only when the library
     # reports it too small (before launching anything)
     try:

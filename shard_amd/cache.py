@@ -346,6 +346,7 @@ class Cache(HFCache):
         self._fused_decode_update = False
         # decode-attention knobs of the HIP kernel (0 = automatic split count)
         self._n_splits = 0
+        self._decode_kernel = 0  # decode split kernel: 0 automatic, 1 row-split, 2 token-tiled
         self._graph = None  # the DecodeGraph whose device counters decode steps use
         self._basis_override = None  # {layer_idx: (1024, rank) fp32} to pin the PCA basis
         super().__init__(layers=[CacheLayer(i) for i in range(num_layers)])

@@ -43,8 +43,8 @@ def _compare(got, want, what):
     assert err <= 1e-2 * max(scale, 1.0) and cos >= 0.9999, (what, err, cos)
 
 
-@pytest.mark.parametrize("B,qjl", [(1, False), (3, False), (2, True)])
-def test_decode_graph_matches_eager_steps(cuda, B, qjl):
+@pytest.mark.parametrize("B,qjl,kernel", [(1, False, 0), (3, False, 0), (2, True, 0), (2, False, 2)])
+def test_decode_graph_matches_eager_steps(cuda, B, qjl, kernel):
     from shard import enable_llama_fused_attention
     from shard_amd.graph import DecodeGraph
     model = _model(cuda)
@@ -55,6 +55,7 @@ def test_decode_graph_matches_eager_steps(cuda, B, qjl):
     feed = torch.randint(0, VOCAB, (B, 12), generator=g).to(cuda)  # teacher-forced tokens
     cache_e = _prefilled(model, ids, first, qjl)
     cache_g = _prefilled(model, ids, first, qjl)
+    cache_e._decode_kernel = cache_g._decode_kernel = kernel  # 2: the token-tiled kernel
     steps = feed.shape[1]
 
     want = []
@@ -68,7 +69,7 @@ def test_decode_graph_matches_eager_steps(cuda, B, qjl):
         got.append(dg.logits.float().clone())
         assert torch.equal(tok, got[-1].argmax(-1))
     for s in range(steps):
-        _compare(got[s], want[s], f"[graph B={B} qjl={qjl}] step {s}")
+        _compare(got[s], want[s], f"[graph B={B} qjl={qjl} kernel={kernel}] step {s}")
     with pytest.raises(RuntimeError):
         dg.step()
 
@@ -90,7 +91,7 @@ def test_decode_graph_matches_eager_steps(cuda, B, qjl):
     with torch.no_grad():
         a = model(nxt, past_key_values=cache_e, use_cache=True).logits[:, -1].float()
         b = model(nxt, past_key_values=cache_g, use_cache=True).logits[:, -1].float()
-    _compare(b, a, f"[graph B={B} qjl={qjl}] eager step after close")
+    _compare(b, a, f"[graph B={B} qjl={qjl} kernel={kernel}] eager step after close")
 
 
 def test_decode_graph_greedy_feeds_its_own_tokens(cuda):
