@@ -380,6 +380,33 @@ def prefill(dev, layers=32, batch=4, T=8192):
                            "mfma_util_fp16": round(flops / gemm_s / (MFMA_PEAK_TFLOPS * 1e12), 4)}}
 
 
+def kmeans_update_bench(dev, batch=16, T=16384, k=256, reps=5):
+    """The k-means step of one config-5 layer's V compression at its full size:
+    B x 8 heads x (T - 68) tokens x 32 subvectors of 4 values, one assignment
+    (shard_vq_assign) and one update (shard_kmeans_update), each timed with
+    HIP events over `reps` calls.  Synthetic rows: N(0, 1), the first k rows as
+    centroids."""
+    from shard_amd import ops
+    n = batch * 8 * (T - 68) * 32
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(n, 4, device=dev, generator=g)
+    cent = x[:k].clone()
+    idx = ops.vq_assign(x, cent)
+    ops.kmeans_update(x, idx, cent)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {"rows": n, "k": k}
+    for name, fn in (("assign_ms", lambda: ops.vq_assign(x, cent)),
+                     ("update_ms", lambda: ops.kmeans_update(x, idx, cent))):
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) / reps, 3)
+    return {"metric": "k-means iteration at config 5's layer size", "unit": "ms", **out}
+
+
 def _to(x, dev):
     if torch.is_tensor(x):
         return x.to(dev)
@@ -627,6 +654,8 @@ def main():
                     help="run a 256 MiB device copy (PMC byte-counter calibration) and exit")
     ap.add_argument("--stream-curve", action="store_true",
                     help="BASELINE config 3: decode time vs 8-bit stream length at 32K")
+    ap.add_argument("--kmeans", action="store_true",
+                    help="time one k-means assignment and update at config 5's layer size")
     ap.add_argument("--prefill", action="store_true",
                     help="BASELINE config 4: prefill compression kernels, tokens/s")
     ap.add_argument("--pmc-workload", action="store_true",
@@ -660,6 +689,9 @@ def main():
         return
     if args.prefill:
         print(json.dumps(prefill(dev)), flush=True)
+        return
+    if args.kmeans:
+        print(json.dumps(kmeans_update_bench(dev)), flush=True)
         return
     if args.e2e:
         print(json.dumps(e2e(dev, args.e2e_batch, args.e2e_prompt, args.e2e_new,
