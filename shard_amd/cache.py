@@ -564,13 +564,31 @@ def _column_energy(x16: torch.Tensor, basis: torch.Tensor, chunk: int = 1 << 15)
     return acc / x16.shape[0]
 
 
+def _eigh_top(cov_host: torch.Tensor, rank: int):
+    """Top-`rank` eigenvectors and eigenvalues of a host float64 (p, p)
+    covariance (symmetric eigendecomposition, deterministic)."""
+    evals, evecs = torch.linalg.eigh(cov_host)
+    return evecs.flip(1)[:, :rank].float(), evals.flip(0)[:rank].clamp(min=0.0).float()
+
+
 def pca_basis_cov(cov: torch.Tensor, rank: int):
     """Top-`rank` eigenvectors of a (p, p) covariance and their eigenvalues, by
     a float64 symmetric eigendecomposition on the host (deterministic)."""
-    evals, evecs = torch.linalg.eigh(cov.double().cpu())
-    evals = evals.flip(0)[:rank].clamp(min=0.0)
-    evecs = evecs.flip(1)[:, :rank]
-    return evecs.float().to(cov.device), evals.float().to(cov.device)
+    evecs, evals = _eigh_top(cov.double().cpu(), rank)
+    return evecs.to(cov.device), evals.to(cov.device)
+
+
+_host_pool = None
+
+
+def _host_worker():
+    """One background thread for host work that overlaps the GPU (the PCA
+    eigendecomposition runs there while the V codec's kernels run)."""
+    global _host_pool
+    if _host_pool is None:
+        import concurrent.futures
+        _host_pool = concurrent.futures.ThreadPoolExecutor(max_workers=1, thread_name_prefix="shard-host")
+    return _host_pool
 
 
 def pca_basis(centered: torch.Tensor, rank: int):
@@ -614,11 +632,22 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     rank = min(cache._max_rank_k, p_dim, n - 1)
     if basis is None and cache._basis_override is not None:
         basis = cache._basis_override.get(li)
+    eig_job = None
     if basis is None:
-        basis, eig = pca_basis_cov(_covariance(centered), rank)
+        # the host eigendecomposition overlaps the V codec's GPU work below
+        cov_host = _covariance(centered).double().cpu()
+        eig_job = _host_worker().submit(_eigh_top, cov_host, rank)
     else:
         basis = basis.to(dev, torch.float32)[:, :rank]
         eig = _column_energy(centered, basis)
+
+    # ---- V: Hadamard -> channel max -> 4-dim subvectors -> k-means (256)
+    x, ch32, ch16 = ops.vq_prepare(v_full[:, :, start:end, :].reshape(B * G, n_comp, D),
+                                   cache._v_vq_group_size)
+    centroids, idx = ops.kmeans(x, cache._v_vq_codebook_size, n_iter=30, seed=42)
+    del x
+    if eig_job is not None:
+        basis, eig = (t.to(dev) for t in eig_job.result())
     budget = max(64, int(p_dim * 16 / cache._k_target_cr))
     alloc = host.dp_bit_allocation(eig, budget)
     keep = sum(1 for b in alloc if b > 0)
@@ -644,11 +673,6 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
         debug["proj"], debug["alloc"] = proj, list(alloc)
     del proj
 
-    # ---- V: Hadamard -> channel max -> 4-dim subvectors -> k-means (256)
-    x, ch32, ch16 = ops.vq_prepare(v_full[:, :, start:end, :].reshape(B * G, n_comp, D),
-                                   cache._v_vq_group_size)
-    centroids, idx = ops.kmeans(x, cache._v_vq_codebook_size, n_iter=30, seed=42)
-    del x
     ng = D // cache._v_vq_group_size
     v_idx = idx.to(torch.uint8)
     v_indices = v_idx.view(B, G, n_comp, ng)
