@@ -118,8 +118,10 @@ int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids
  * the rows assigned to k (empty clusters keep c[k]); also writes
  * max |new_c - c| to *max_delta (device fp32).  Sums are accumulated per
  * centroid in increasing row order, so the result is deterministic.
- * workspace: shard_kmeans_update_workspace(n, k) bytes (per-block counts of
- * the counting sort and the rows' sorted copy, rows of up to 8 values). */
+ * workspace: shard_kmeans_update_workspace_d(n, k, d) bytes (per-block
+ * counts of the counting sort and the rows' sorted copy);
+ * shard_kmeans_update_workspace(n, k) is the size for rows of up to 8 values. */
+size_t shard_kmeans_update_workspace_d(int64_t n, int32_t k, int32_t d);
 size_t shard_kmeans_update_workspace(int64_t n, int32_t k);
 int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx,
                         const float* centroids, int32_t k, float* new_centroids,

@@ -61,6 +61,7 @@ SIGNATURES = [
     ("shard_vq_prepare", c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("shard_vq_assign", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     ("shard_kmeans_update_workspace", c_size_t, [c_int64, c_int32]),
+    ("shard_kmeans_update_workspace_d", c_size_t, [c_int64, c_int32, c_int32]),
     ("shard_kmeans_update", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("shard_stream_quant", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_decode_prepare_bytes", c_size_t, [c_int32, c_int32]),

@@ -1285,12 +1285,16 @@ int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids
   return SHARD_OK;
 }
 
-size_t shard_kmeans_update_workspace(int64_t n, int32_t k) {
-  if (n <= 0 || k <= 0) return 0;
+size_t shard_kmeans_update_workspace_d(int64_t n, int32_t k, int32_t d) {
+  if (n <= 0 || k <= 0 || d <= 0 || d > KM_DMAX) return 0;
   const int64_t nblk = (n + KM_R - 1) / KM_R;
-  // per-block counts, counts, offsets, then the sorted copy (rows up to KM_DMAX wide)
+  // per-block counts, counts, offsets, then the sorted copy of the rows
   const int64_t ints = ((nblk * k + 2 * (int64_t)k) + 3) & ~(int64_t)3;
-  return (size_t)ints * sizeof(int32_t) + (size_t)n * KM_DMAX * sizeof(float);
+  return (size_t)ints * sizeof(int32_t) + (size_t)n * d * sizeof(float);
+}
+
+size_t shard_kmeans_update_workspace(int64_t n, int32_t k) {
+  return shard_kmeans_update_workspace_d(n, k, KM_DMAX);
 }
 
 int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx,
@@ -1301,7 +1305,7 @@ int shard_kmeans_update(const float* x, int64_t n, int32_t d, const int32_t* idx
     return SHARD_ERR_ARG;
   if (k > 1024 || (d != 1 && d != 2 && d != 4 && d != 8)) return SHARD_ERR_SHAPE;
   if (n > INT32_MAX) return SHARD_ERR_SHAPE;  // slots are int32
-  if (!workspace || workspace_bytes < shard_kmeans_update_workspace(n, k)) return SHARD_ERR_WORKSPACE;
+  if (!workspace || workspace_bytes < shard_kmeans_update_workspace_d(n, k, d)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   const int64_t nblk = (n + KM_R - 1) / KM_R;
   int32_t* blk = (int32_t*)workspace;

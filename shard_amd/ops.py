@@ -176,7 +176,7 @@ def kmeans_update(x: torch.Tensor, idx: torch.Tensor, centroids: torch.Tensor, w
     k = c.shape[0]
     newc = torch.empty_like(c)
     maxd = torch.empty(1, dtype=torch.float32, device=x.device)
-    need = lib.shard_kmeans_update_workspace(n, k)
+    need = lib.shard_kmeans_update_workspace_d(n, k, d)
     if ws is None or ws.numel() < need:
         ws = _workspace(need, x.device)
     _lib.check("shard_kmeans_update", lib.shard_kmeans_update(
@@ -240,7 +240,7 @@ def kmeans(data: torch.Tensor, k: int, n_iter: int = 30, seed: int = 42):
     perm = _kmeans_init_rows(n, k, seed).to(data.device)
     centroids = data[perm].clone()
     lib = _lib.load()
-    ws = _workspace(lib.shard_kmeans_update_workspace(n, centroids.shape[0]), data.device)
+    ws = _workspace(lib.shard_kmeans_update_workspace_d(n, centroids.shape[0], d), data.device)
     idx = None
     deltas = []
     for it in range(n_iter):
