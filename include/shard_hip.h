@@ -9,8 +9,10 @@
  *   - fp16 tensors are passed as uint16_t* (IEEE binary16 bit patterns);
  *   - return 0 on success, a negative SHARD_ERR_* code otherwise; nothing is
  *     allocated inside: scratch memory comes in through `workspace`, sized by
- *     the matching *_workspace() query;
- *   - entry points are stateless and re-entrant (no mutable globals).
+ *     the matching *_workspace() query (shard_decode_attn_noalloc alone uses
+ *     a static device array of the library instead, see its declaration);
+ *   - entry points are stateless and re-entrant (no mutable globals; calls of
+ *     shard_decode_attn_noalloc share its array and must not overlap).
  *
  * Each declaration names the reference code (bhengubv/shard, src/shard/...)
  * whose role it takes over.
