@@ -50,6 +50,26 @@ def algorithmic_flops(n_comp, rank, n_stream=0, n_kv=8, hd=128, n_q=32, batch=1)
     return batch * (n_comp * (2 * n_kv * hd * rank + n_q * hd * 5) + n_stream * n_q * hd * 4)
 
 
+def roofline(flops, nbytes, us):
+    """The roof that binds a call of `flops` algorithmic flops over `nbytes`
+    algorithmic bytes: the MFMA peak when its time at that peak exceeds the
+    bytes' time at the HBM peak (intensity above the ridge), else HBM; the
+    achieved rate and its fraction of that peak, with the other roof's view in
+    `hbm` or `mfma`."""
+    s = us * 1e-6
+    tflops, gbs = flops / s / 1e12, nbytes / s / 1e9
+    mfma = {"achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_PEAK_TFLOPS, 4)}
+    hbm = {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    bound = "mfma" if flops / MFMA_PEAK_TFLOPS > nbytes / HBM_PEAK_GBS * 1e3 else "hbm"
+    out = {"bound": bound, **(mfma if bound == "mfma" else hbm),
+           "intensity_flop_per_byte": round(flops / nbytes, 1),
+           "ridge_flop_per_byte": round(MFMA_PEAK_TFLOPS * 1e3 / HBM_PEAK_GBS, 1)}
+    out["hbm" if bound == "mfma" else "mfma"] = hbm if bound == "mfma" else mfma
+    return out
+
+
 def clone_format(fmt):
     out = {}
     for k, v in fmt.items():
@@ -788,22 +808,14 @@ def main():
         # The binding roof: the call's algorithmic intensity (key rebuild flops
         # per compressed byte) lies above the fp16 MFMA ridge, so the MFMA peak
         # bounds it before HBM does; the HBM figures are reported beside it.
-        "roofline": {"bound": "mfma" if r8["flops"] / MFMA_PEAK_TFLOPS > r8["bytes"] / HBM_PEAK_GBS * 1e3
-                     else "hbm",
-                     "achieved": round(r8["flops"] / (us * 1e-6) / 1e12, 2),
-                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": s8["mfma_frac_fp16"],
+        "roofline": {**roofline(r8["flops"], r8["bytes"], us),
                      "traffic": read_traffic(args.ctx),
                      "traffic_source": "profiles/decode_traffic.md (rocprofv3 --pmc FETCH_SIZE "
                                        "and WRITE_SIZE of the same call, copy-calibrated)",
                      "kernel": "shard_decode_attn (split kernel + k_decode_merge), per call, "
                                "HIP events around graph replays",
                      "algorithmic_flops": r8["flops"],
-                     "algorithmic_bytes": r8["bytes"],
-                     "intensity_flop_per_byte": round(r8["flops"] / r8["bytes"], 1),
-                     "ridge_flop_per_byte": round(MFMA_PEAK_TFLOPS * 1e3 / HBM_PEAK_GBS, 1),
-                     "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(gbs / HBM_PEAK_GBS, 4)}},
+                     "algorithmic_bytes": r8["bytes"]},
     }
     if r32 is not None:
         out["at_32k"] = summary(r32)

@@ -218,3 +218,20 @@ def test_kmeans_init_rows_equal_torch_randperm(n, seed):
     from shard_amd import ops
     want = torch.randperm(n, generator=torch.Generator().manual_seed(seed))[:256]
     assert torch.equal(ops._randperm_head(n, 256, seed), want)
+
+
+def test_bench_roofline_picks_the_binding_roof():
+    """bench.roofline: above the fp16 MFMA ridge (312.5 flop/B) the MFMA peak
+    binds and `achieved` is TFLOP/s; below it HBM binds and `achieved` is GB/s;
+    the other roof is reported beside it.  The 8K decode call's algorithmic
+    figures (about 1,000 flop/B) are MFMA-bound."""
+    import bench
+    r = bench.roofline(bench.algorithmic_flops(8124, 192), bench.algorithmic_bytes(8124, 192), 17.5)
+    assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and r["peak"] == 2500.0
+    assert abs(r["achieved"] - 3_360_866_304 / 17.5e-6 / 1e12) < 0.01
+    assert abs(r["frac"] - r["achieved"] / 2500.0) < 1e-4
+    assert r["hbm"]["unit"] == "GB/s" and abs(r["hbm"]["achieved"] - 3_358_080 / 17.5e-6 / 1e9) < 0.1
+    assert r["ridge_flop_per_byte"] == 312.5 and 990 < r["intensity_flop_per_byte"] < 1010
+    low = bench.roofline(1e9, 1e8, 100.0)  # 10 flop/B: HBM-bound
+    assert low["bound"] == "hbm" and low["unit"] == "GB/s" and low["achieved"] == 1000.0
+    assert low["mfma"]["unit"] == "TFLOP/s"
