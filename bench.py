@@ -1,6 +1,6 @@
 """Benchmark of the compressed-KV decode attention path on one MI355X.
 
-Default workload = BASELINE config 2: one Llama-3.1-8B-shaped attention layer
+Default workload: one Llama-3.1-8B-shaped attention layer
 (32 q heads, 8 kv heads, head_dim 128, theta 500000), batch 1, 8192-token
 prompt compressed by shard_amd (PCA rank <= 192 int4 keys, Hadamard + k-means
 VQ values, 4 sink + 64 window fp16 tokens), then the fused decode-attention
@@ -301,7 +301,7 @@ def calibrate_copy(dev, mib=256, reps=10):
 
 
 def stream_curve(dev, T=32768, n_stream=512, reps=10):
-    """BASELINE config 3: 32K compressed context, append a 512-token 8-bit
+    """32K compressed context, append a 512-token 8-bit
     stream one token at a time (K and V through the Lloyd-Max quantizer) and
     time the decode call at every stream length."""
     from shard_amd import ops, bench_data
@@ -343,7 +343,7 @@ def stream_curve(dev, T=32768, n_stream=512, reps=10):
 
 
 def prefill(dev, layers=32, batch=4, T=8192):
-    """compression kernels over `layers` x batch x T tokens of
+    """Prefill compression kernels over `layers` x batch x T tokens of
     synthetic K (low-rank Gaussian, RoPE'd) and V.  Per layer: undo-RoPE into
     the fp16 GEMM operand, MFMA projection onto a fixed random-orthonormal
     1024x192 basis, per-column int4 quantization + packing, FWHT + channel
@@ -466,7 +466,7 @@ def pmc_workload(dev, T, calls=200, layer_path=None, batch=1):
 
 
 def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
-    """random-init Llama-3.1-8B architecture (fp16) with the
+    """End to end: random-init Llama-3.1-8B architecture (fp16) with the
     shard Cache (8-bit stream on, fused decode attention) against the fp16
     DynamicCache on the same GPU, as benchmarks/benchmark.py:614-726 measures it:
     prefill, one-time compression and greedy decode timed separately;

@@ -16,7 +16,8 @@ Modules:
                (fp16 cast points kept), numpy for the bit-exact integer chains.
   ``exact``  — fp64 evaluation of attention over the dequantized representation
                (the accuracy yardstick for attention outputs).
-  ``synth``  — seeded synthetic inputs of the BASELINE configs.
+  ``synth``  — seeded synthetic inputs of the benchmark workloads (Llama-3.1-8B
+               attention-layer shapes).
 
 Parity-pinning status of every function is listed in each module's header.
 """

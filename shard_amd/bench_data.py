@@ -1,4 +1,5 @@
-"""Seeded synthetic inputs shaped like BASELINE's Llama-3.1-8B attention layer.
+"""Seeded synthetic inputs shaped like a Llama-3.1-8B attention layer (32 query
+heads, 8 kv heads, head_dim 128, RoPE theta 500000).
 
 Used by bench.py, tests and smoke() to build identical inputs on every run:
 all tensors come from ``torch.Generator().manual_seed(seed)`` on the CPU in

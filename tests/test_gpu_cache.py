@@ -1,6 +1,6 @@
 """The shard Cache driven by a real (random-init) Llama on the GPU:
 
-* batch 16 (BASELINE config 5's decode shape, shorter prompt): the fused
+* batch 16 (the end-to-end decode batch, shorter prompt): the fused
   decode call the patched forward makes, checked against the fp64 oracle over
   the layer's own compressed representation (attention.py:300-343,
   cache.py:156-181);

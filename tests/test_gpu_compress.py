@@ -1,7 +1,7 @@
 """The product compression (shard_amd.cache.compress_layer, HIP kernels) against
 the oracle's restatement of the reference's _compress_k / _compress_v /
-_build_gpu_format (oracle.ref.compress_layer, cache.py:338-460) on BASELINE
-config 1's layer: 2048 tokens of the seeded synthetic K/V, one PCA basis
+_build_gpu_format (oracle.ref.compress_layer, cache.py:338-460) on one
+Llama-3.1-8B-shaped layer: 2048 tokens of the seeded synthetic K/V, one PCA basis
 supplied to both (the reference's svd_lowrank is randomized).
 
 What must agree:

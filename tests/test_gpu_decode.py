@@ -256,8 +256,8 @@ def _large_case(shape):
 
 @pytest.mark.parametrize("shape", LARGE, ids=[f"B{b}xn{n}+s{s}" for b, n, s in LARGE])
 def test_decode_large_contexts(cuda, shape):
-    """BASELINE configs 2-3 shapes: 32K context, also with the 512-token 8-bit
-    stream of config 3 (the extra tokens spread over several splits)."""
+    """32K context, also with a 512-token 8-bit stream (the extra tokens spread
+    over several splits)."""
     B, n_comp, n_stream = shape
     gc, inv, q, pos_q, want = _large_case(shape)
     for kernel in KERNELS:
@@ -269,7 +269,7 @@ def test_decode_large_contexts(cuda, shape):
 
 
 def test_decode_config5_layer_full_size(cuda):
-    """BASELINE config 5's layer at full size: batch 16 x 16,316 compressed
+    """The end-to-end workload's layer at full size: batch 16 x 16,316 compressed
     tokens (16,384 with the 4 sink and 64 window tokens).  Every kernel against
     the fp64 oracle on batch rows 0 and 15 (the oracle over all 16 rows takes
     minutes), and the 16 rows of the row-split and token-tiled kernels against

@@ -381,7 +381,7 @@ def test_stream_quant_kv_rows_bitexact(cuda, bits, qjl):
 
 
 def test_prefill_kernels_at_config4_layer_size(cuda):
-    """One layer of BASELINE config 4 (batch 4 x 8192 tokens, 8 kv heads): the V
+    """One layer of the prefill workload (batch 4 x 8192 tokens, 8 kv heads): the V
     front end and the int4 chain bit-exact, the projection within fp32 summation
     error, at the sizes whose multi-block reductions and grid-stride loops the
     small cases above do not reach."""
