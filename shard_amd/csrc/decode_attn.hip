@@ -1017,7 +1017,6 @@ void k_decode_tok(const TokParams p) {
   };
   uint32_t cwA[KS], cwB[KS];
   float2 fA2, fA1, fB2, fB1;
-  if (tile_of(0) < n_c) load_tile(tile_of(0), cwA, fA2, fA1);
 
   // every global load of the set-up goes out before the first LDS store, so
   // the cold misses overlap (one round trip instead of one per copy step)
@@ -1036,6 +1035,9 @@ void k_decode_tok(const TokParams p) {
 #pragma unroll
     for (int j = 0; j < kPR; ++j) rv[j] = p.rope[tid + kTokThreads * j];
   }
+  // the first tile's coefficients queue behind the image: the image is needed
+  // first (the barrier), the tile after it
+  if (tile_of(0) < n_c) load_tile(tile_of(0), cwA, fA2, fA1);
   const uint2 cbv = tid < 256 ? *(const uint2*)(p.vcb + 4 * tid) : make_uint2(0u, 0u);
   const float th = p.inv_freq[lane];
   uint16_t qlo[NQ], qhi[NQ];
