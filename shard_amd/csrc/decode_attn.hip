@@ -1035,9 +1035,6 @@ void k_decode_tok(const TokParams p) {
 #pragma unroll
     for (int j = 0; j < kPR; ++j) rv[j] = p.rope[tid + kTokThreads * j];
   }
-  // the first tile's coefficients queue behind the image: the image is needed
-  // first (the barrier), the tile after it
-  if (tile_of(0) < n_c) load_tile(tile_of(0), cwA, fA2, fA1);
   const uint2 cbv = tid < 256 ? *(const uint2*)(p.vcb + 4 * tid) : make_uint2(0u, 0u);
   const float th = p.inv_freq[lane];
   uint16_t qlo[NQ], qhi[NQ];
@@ -1049,6 +1046,9 @@ void k_decode_tok(const TokParams p) {
       qhi[h] = qv[h * kHD + 64 + lane];
     }
   }
+  // the first tile's coefficients queue behind the set-up's loads: those are
+  // needed first (the LDS stores before the barrier), the tile after it
+  if (tile_of(0) < n_c) load_tile(tile_of(0), cwA, fA2, fA1);
   {
     uint4* dst = &L.u.A[0][0][0];
 #pragma unroll
