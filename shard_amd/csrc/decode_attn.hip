@@ -243,6 +243,13 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
   }
 }
 
+// A 32-bit load from a global address held as an integer (a row pointer
+// broadcast from another lane): a global load, not a flat one, so the wait for
+// it does not hold back LDS accesses.
+__device__ __forceinline__ uint32_t ld_global_u32(uint64_t addr) {
+  return *(const __attribute__((address_space(1))) uint32_t*)addr;
+}
+
 // Row x of the extra tokens (sink, window, decode, stream) of kv head g in
 // batch row b, and its column in the attention mask (the compressed span sits
 // between the sink and the window).
@@ -377,7 +384,7 @@ __device__ __forceinline__ void decode_extras_tail(const SplitParams& p, const i
     for (int t = 0; t < 32; ++t) {
       const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
       const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
-      vx[t] = *(const uint32_t*)((const uint16_t*)(((uint64_t)hi << 32) | lo) + 2 * lane);
+      vx[t] = ld_global_u32((((uint64_t)hi << 32) | lo) + 4 * lane);
     }
     float16v sacc = {};
 #pragma unroll
@@ -1297,7 +1304,7 @@ void k_decode_tok(const TokParams p) {
     for (int t = 0; t < 32; ++t) {
       const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
       const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
-      vx[t] = *(const uint32_t*)((const uint16_t*)(((uint64_t)hi << 32) | lo) + 2 * lane);
+      vx[t] = ld_global_u32((((uint64_t)hi << 32) | lo) + 4 * lane);
     }
     float16v sacc = {};
 #pragma unroll
