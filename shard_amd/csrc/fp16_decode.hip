@@ -11,10 +11,11 @@
 //     dims of one token in 4, 16-byte loads), the next tile's K and V loads in
 //     flight during the current one.  The waves merge in LDS and write one
 //     partial row (m, l, 128 sums) per query head and split.
-//   k_fp16_merge  grid = (H, B): the log-sum-exp weighted sum of the splits.
+//   k_decode_merge (merge.h): the log-sum-exp weighted sum of the splits.
 #include <math.h>
 
 #include "common.h"
+#include "merge.h"
 
 namespace shard {
 
@@ -192,42 +193,6 @@ void k_fp16_split(const Fp16Params p) {
   }
 }
 
-struct Fp16MergeParams {
-  int32_t H, n_splits;
-  const float* ws_m;
-  const float* ws_l;
-  const float* ws_acc;
-  uint16_t* out;
-};
-
-// One wave per (query head, batch row); lane = dims 2 lane, 2 lane + 1.
-__global__ __launch_bounds__(64)
-void k_fp16_merge(const Fp16MergeParams p) {
-  const int lane = threadIdx.x;
-  const int64_t row = (int64_t)blockIdx.y * p.H + blockIdx.x;
-  const float* mrow = p.ws_m + row * p.n_splits;
-  const float* lrow = p.ws_l + row * p.n_splits;
-  const float* arow = p.ws_acc + row * p.n_splits * kFdHD + 2 * lane;
-  float M = -INFINITY;
-  for (int s = lane; s < p.n_splits; s += 64) M = fmaxf(M, mrow[s]);
-  M = wave64_reduce(M, OpMax());
-  float a0 = 0.f, a1 = 0.f, l = 0.f;
-#pragma unroll 8
-  for (int s = 0; s < p.n_splits; ++s) {
-    const float ms = mrow[s];
-    const float wt = ms == -INFINITY ? 0.f : exp2f(ms - M);
-    const float2 a = *(const float2*)(arow + (int64_t)s * kFdHD);
-    a0 += wt * a.x;
-    a1 += wt * a.y;
-    l += wt * lrow[s];
-  }
-  const float inv = 1.0f / l;
-  half2v o;
-  o[0] = (half_t)(a0 * inv);
-  o[1] = (half_t)(a1 * inv);
-  *(half2v*)(p.out + row * kFdHD + 2 * lane) = o;
-}
-
 }  // namespace
 
 }  // namespace shard
@@ -262,10 +227,10 @@ int shard_bench_fp16_decode(const uint16_t* q, const uint16_t* k, const uint16_t
   hipLaunchKernelGGL(k_fp16_split, dim3((unsigned)(n_splits * n_kv_heads), (unsigned)batch),
                      dim3(64 * kFdWaves), 0, s, p);
   SHARD_LAUNCH_CHECK("shard_bench_fp16_decode split");
-  Fp16MergeParams mp;
-  mp.H = n_kv_heads * kFdGQA; mp.n_splits = n_splits;
+  MergeParams mp;
+  mp.H = n_kv_heads * kFdGQA; mp.nsp = n_splits;
   mp.ws_m = p.ws_m; mp.ws_l = p.ws_l; mp.ws_acc = p.ws_acc; mp.out = out;
-  hipLaunchKernelGGL(k_fp16_merge, dim3((unsigned)mp.H, (unsigned)batch), dim3(64), 0, s, mp);
+  launch_partial_merge(mp, batch, s);
   SHARD_LAUNCH_CHECK("shard_bench_fp16_decode merge");
   return SHARD_OK;
 }
