@@ -43,8 +43,11 @@ void k_decode_merge(const MergeParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int dp = tid % DP, g = tid / DP;
-  const int slice = blockIdx.x % MS;
-  const int64_t hrow = (int64_t)blockIdx.y * p.H + blockIdx.x / MS;
+  // the MS slices of a head share one XCD (workgroups go to XCD id mod 8), so
+  // one L2 fetches each 128-byte line of the partial rows once
+  const int bx = blockIdx.x, slice = (bx >> 3) % MS;
+  const int head = (bx & 7) + 8 * (bx / (8 * MS));
+  const int64_t hrow = (int64_t)blockIdx.y * p.H + head;
   const int nsp = p.nsp;
   const float* mrow = p.ws_m + hrow * nsp;
   const float* lrow = p.ws_l + hrow * nsp;
@@ -117,9 +120,10 @@ void k_decode_merge(const MergeParams p) {
 
 // The slice count is the most of 8, 4, 2, 1 that keeps the grid at or below
 // 512 workgroups (measured best at batch 1, 4 and 16 of 32 heads).
+// The XCD-aware slice order needs H % 8 == 0; other head counts take one slice.
 inline void launch_partial_merge(const MergeParams& mp, int batch, hipStream_t s) {
   const int64_t pairs = (int64_t)batch * mp.H;
-  const int ms = pairs * 8 <= 512 ? 8 : pairs * 4 <= 512 ? 4 : pairs * 2 <= 512 ? 2 : 1;
+  const int ms = mp.H % 8 ? 1 : pairs * 8 <= 512 ? 8 : pairs * 4 <= 512 ? 4 : pairs * 2 <= 512 ? 2 : 1;
   const dim3 grid((unsigned)(mp.H * ms), (unsigned)batch);
   switch (ms) {
     case 8: hipLaunchKernelGGL(k_decode_merge<8>, grid, dim3(256), 0, s, mp); break;
