@@ -24,8 +24,11 @@ def _fp64_attention(q, k, v):
     return np.einsum("bht,bhtd->bhd", p, vv)
 
 
+# the merge runs 8, 4, 2 or 1 slices per query head by batch x heads, and one
+# slice when the head count is not a multiple of 8: (1, 1, ...) has 4 heads
 @pytest.mark.parametrize("B,G,T,n_splits", [(1, 8, 8192, 0), (1, 8, 1000, 7), (2, 4, 333, 0),
-                                             (3, 2, 100, 50), (1, 8, 32, 1)])
+                                             (3, 2, 100, 50), (1, 8, 32, 1), (4, 8, 300, 0),
+                                             (8, 8, 256, 0), (16, 8, 64, 3), (1, 1, 500, 9)])
 def test_fp16_baseline_matches_fp64(cuda, B, G, T, n_splits):
     from shard_amd import ops
     g = torch.Generator().manual_seed(T + B)

@@ -42,6 +42,7 @@ CASES = [
     (1, 2, 64, 33, 2, 3, 1, 0),          # tiny, 2 kv heads
     (1, 8, 96, 1, 4, 64, 0, 0),          # a single compressed token
     (4, 8, 192, 1100, 4, 64, 2, 0),      # batch 4
+    (8, 8, 192, 400, 4, 64, 2, 0),       # batch 8 (the merge's 2-slice grid)
     (16, 8, 128, 300, 4, 16, 1, 0),      # batch 16
     (1, 8, 192, 700, 4, 64, 3000, 0),    # 3,068 extra tokens: spread over many splits
     (2, 4, 160, 900, 4, 64, 700, 9),     # long stream and decode tokens together
