@@ -427,3 +427,53 @@ def test_decode_stream_count_from_device_rejects_mask(cuda):
     with pytest.raises(ShardHipError) as exc:
         ops.decode_attn(call)
     assert exc.value.code == -1  # SHARD_ERR_ARG
+
+
+def test_fused_attention_across_the_kernel_switch(cuda):
+    """One layer's argument block refreshed across the automatic kernel switch:
+    with 257 extra tokens (4 sink + 64 window + 189 stream) the call takes the
+    token-tiled kernel, with 256 the row-split one, whose plan needs a larger
+    workspace.  The patched forward's shared workspace, sized by the first
+    call, grows for the second; both match the fp64 oracle."""
+    from shard_amd import attention
+    n_comp, n_st = 1500, 189
+    gc, inv = random_layer(B=1, n_comp=n_comp, n_stream=n_st, seed=23)
+    d = to_device(gc, cuda, inv)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(4)).half()
+
+    class _CacheRef:
+        _rope_inv_freq = d["inv_freq_dev"]
+        _n_splits = 0
+
+    class _Layer:
+        _gpu_compressed = d
+        _cache_ref = _CacheRef()
+
+    key = (cuda.type, cuda.index)
+    saved = attention._workspaces.get(key)
+    try:
+        attention._workspaces[key] = torch.zeros(16, dtype=torch.uint8, device=cuda)
+        sizes = []
+        for s in (189, 188):
+            d["stream_n"] = s
+            pos_q = 4 + n_comp + 64 + s - 1
+            print(f"[kernel switch] extra tokens {68 + s}", flush=True)
+            got = attention.fused_attention_compressed(q.to(cuda), _Layer(), pos_q, d["inv_freq_dev"])
+            torch.cuda.synchronize()
+            sizes.append(d["_decode_call"].workspace_bytes())
+            assert attention._workspaces[key].numel() >= sizes[-1]
+            g_s = dict(gc)
+            g_s["stream_n"] = s
+            for name in ("k_idx_buf", "v_idx_buf", "k_norm_buf", "v_norm_buf"):
+                g_s[name] = gc[name][:s]
+            want = exact.decode_attention(q.numpy(), g_s, 8, pos_q, inv.numpy())
+            err, cos = compare(got.cpu().float().numpy().reshape(want.shape), want)
+            print(f"[kernel switch] extras {68 + s}: workspace {sizes[-1]} B max_abs={err:.3e} cos={cos:.7f}",
+                  flush=True)
+            assert err <= TOL_ABS and cos >= TOL_COS
+        assert sizes[1] > sizes[0], sizes  # the row-split plan has more partial rows
+    finally:
+        if saved is None:
+            attention._workspaces.pop(key, None)
+        else:
+            attention._workspaces[key] = saved
