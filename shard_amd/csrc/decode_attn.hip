@@ -1407,10 +1407,11 @@ void k_decode_tok(const TokParams p) {
 // Which split kernel runs.  The row-split kernel takes query groups of 4 and
 // at most kMaxExtra extra tokens; the token-tiled kernel takes every supported
 // shape.  Automatic choice by the work per CU: the token-tiled kernel has the
-// higher tile throughput but a longer set-up, so it takes over from 16
-// head-tiles per CU (measured on MI355X: batch 16 x 16K 148 vs 167 us, batch 1
-// x 32K 29 vs 31 us; batch 1 x 8K 18.2 vs 15.5 us).
-constexpr int kTokMinHeadTilesPerCU = 16;
+// higher tile throughput but a longer set-up, so it takes over from 9
+// head-tiles per CU (measured on MI355X, row-split vs token-tiled, us per
+// call: batch 1 x 8K (7.9 per CU) 14.5-14.6 vs 14.8; 1 x 10K (9.9) 16.2 vs
+// 15.3; 1 x 12K 18.0 vs 17.7; 2 x 8K 20.5 vs 17.9; 1 x 16K 19.4-19.8 vs 17.8).
+constexpr int kTokMinHeadTilesPerCU = 9;
 
 inline int device_cus() {
   static int n = 0;
