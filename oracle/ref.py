@@ -28,8 +28,13 @@ How each function is pinned (checked in ``tests/test_oracle.py``):
                       triton_kernels.py:733-734) and fp64 brute force.
   kmeans              golden vectors from the reference import.
   fused attention     golden vectors from the reference import on a stub cache
-                      (the reference's own kernel_test.py:178-259 technique), and
-                      exact.py's fp64 evaluation.
+                      (the reference's own kernel_test.py:178-259 technique),
+                      reproduced bit for bit, and exact.py's fp64 evaluation.
+  compress_layer      golden vectors of the reference's _compress_k +
+                      _compress_v + _build_gpu_format (svd_lowrank replaced by
+                      a fixed (S, V) on both sides, ``svd=``), bit for bit.
+  reconstruct_kv,     golden vectors of the reference's _ensure_dequant on a
+  vq_decode           two-batch-row stub layer and of vq_decode, bit for bit.
 """
 import math
 
@@ -460,12 +465,16 @@ def vq_decode(qd) -> torch.Tensor:
 # --------------------------------------------------------------------------
 def compress_layer(k_full: torch.Tensor, v_full: torch.Tensor, layer_idx: int,
                    inv_freq, sink=4, win=64, k_target_cr=20.0, max_rank=192,
-                   group_size=4, codebook_size=256, basis=None, assign=None):
+                   group_size=4, codebook_size=256, basis=None, assign=None, svd=None):
     """One layer of Cache.compress (cache.py:338-366) + _compress_k (368-396) +
     _compress_v (398-404) + _build_gpu_format (406-454), on the CPU.
 
     ``basis`` (1024 x rank fp32, columns = components) may be supplied to
-    bypass torch.svd_lowrank (its randomized result depends on the device RNG).
+    bypass torch.svd_lowrank (its randomized result depends on the device RNG);
+    the variances are then the mean squared projections.  ``svd`` = (S, V)
+    instead stands for svd_lowrank's result itself (cache.py:376-378): the
+    basis is V[:, :rank] and the variances S[:rank]^2 / n, as the reference
+    takes them.
     ``assign`` is k-means' nearest-centroid rule (default: the CPU fallback's
     cdist argmin; the reference's GPU kernel sums squared differences directly,
     vq_assign_direct).
@@ -484,7 +493,11 @@ def compress_layer(k_full: torch.Tensor, v_full: torch.Tensor, layer_idx: int,
     n = flat.shape[0]
     mean = flat.mean(dim=0)
     rank = min(max_rank, p_dim, n - 1)
-    if basis is None:
+    if svd is not None:
+        S, V = (torch.as_tensor(t, dtype=torch.float32) for t in svd)
+        basis = V[:, :rank]
+        eig = (S[:rank].float() ** 2) / n
+    elif basis is None:
         _, S, V = torch.svd_lowrank(flat - mean, q=rank, niter=24)
         basis = V[:, :rank]
         eig = (S[:rank].float() ** 2) / n

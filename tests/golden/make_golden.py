@@ -22,6 +22,26 @@ invariant or library routine pins are recorded here:
                      including columns whose values land exactly on .5 code
                      boundaries in either rounding step (half-even pinned).
 
+  compress.npz       one layer of Cache.compress (cache.py:338-366): the
+                     reference's own _compress_k (368-396) and _compress_v
+                     (398-404) on a two-batch-row, 2-kv-head layer with RoPE'd
+                     low-rank keys and outlier V channels, then the K/V
+                     statements of _build_gpu_format (406-454) on the CPU (it
+                     hard-codes "cuda").  torch.svd_lowrank is replaced by a
+                     stub returning a fixed (S, V) (the float64 SVD of the
+                     centred keys, stored in the fixture): the randomized
+                     routine depends on the device RNG.  Pins the flatten
+                     order, centring, DP allocation, keep-even, int8 basis,
+                     fp32 projection -> group codes -> int4 chain, and the V
+                     codec's Hadamard, channel scales, subvector order and
+                     k-means.
+  ensure_dequant.npz CacheLayer._ensure_dequant (cache.py:87-124) on a stub
+                     layer (B = 2, 2 kv heads, rank 48, 3 stream
+                     tokens, 2 fp16 decode tokens): the rebuilt K (int4 ->
+                     basis -> mean -> view(B, n, nkv, hd) -> RoPE) and V
+                     (vq_decode -> Hadamard) with the sink / window / stream /
+                     decode concatenation; plus vq_decode (cache.py:54-61) alone.
+
 Usage:  python tests/golden/make_golden.py /root/reference [fixture ...]
         (no fixture names: write all of them)
 The fixtures hold inputs and outputs only (arrays), no reference source.
@@ -108,6 +128,148 @@ def group_header(blob, alloc):
     return lo, rng
 
 
+def compress_inputs(seed=21, B=2, nkv=2, hd=128, T=200):
+    """(k_full, v_full fp16 (B, nkv, T, hd), inv_freq fp32) for compress.npz.
+
+    K: no-RoPE rows z diag(sigma) W^T + offset (W a random orthonormal p x p,
+    sigma_i = exp(-i / 24), so a few dozen components hold the energy),
+    normalized to unit per-dim std, then RoPE at positions 0..T-1 (theta
+    500000), fp16.  V: N(0, 1) with two channels scaled x8, fp16."""
+    g = torch.Generator().manual_seed(seed)
+    p = nkv * hd
+    W, _ = torch.linalg.qr(torch.randn(p, p, generator=g, dtype=torch.float64))
+    sig = torch.exp(-torch.arange(p, dtype=torch.float64) / 24.0)
+    z = torch.randn(B * T, p, generator=g, dtype=torch.float64)
+    kn = (z * sig) @ W.T
+    kn = kn / kn.std(dim=0).clamp(min=1e-12) + torch.randn(p, generator=g, dtype=torch.float64) * 0.3
+    kn = kn.view(B, T, nkv, hd).permute(0, 2, 1, 3)
+    inv_freq = 1.0 / (500000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    ph = torch.arange(T, dtype=torch.float64)[:, None] * inv_freq.double()[None, :]
+    c, s = ph.cos(), ph.sin()
+    k1, k2 = kn[..., : hd // 2], kn[..., hd // 2:]
+    k_full = torch.cat([k1 * c - k2 * s, k2 * c + k1 * s], dim=-1).half()
+    v = torch.randn(B, nkv, T, hd, generator=g)
+    out_ch = torch.randperm(p, generator=g)[:2]
+    vf = v.permute(0, 2, 1, 3).reshape(B, T, p)
+    vf[:, :, out_ch] *= 8.0
+    v_full = vf.view(B, T, nkv, hd).permute(0, 2, 1, 3).contiguous().half()
+    return k_full.contiguous(), v_full, inv_freq
+
+
+def write_compress(rcache):
+    """compress.npz: see the module docstring."""
+    import types
+    from shard.rope import dequantize_group, unpack_nbits
+    from shard.triton_kernels import int4_pack
+    B, nkv, hd, T, sink, win, max_rank, cr = 2, 2, 128, 200, 4, 64, 192, 4.0
+    k_full, v_full, inv_freq = compress_inputs(B=B, nkv=nkv, hd=hd, T=T)
+    start, end = sink, T - win
+    n_comp = end - start
+    positions = torch.arange(T)[start:end]
+    p = nkv * hd
+    # the fixed (S, V) the svd_lowrank stub returns: the float64 SVD of the
+    # centred no-RoPE keys, computed with the reference's own statements
+    from shard.rope import undo_rope
+    kk = undo_rope(k_full[:, :, start:end, :].float(), positions, inv_freq)
+    flat = kk.permute(0, 2, 1, 3).reshape(B * n_comp, p)
+    x64 = (flat - flat.mean(dim=0)).double()
+    _, S64, Vh64 = torch.linalg.svd(x64, full_matrices=False)
+    S_fix, V_fix = S64.float().contiguous(), Vh64.t().float().contiguous()
+    stub = types.SimpleNamespace(_rope_inv_freq=inv_freq, _per_layer_dim=p, _max_rank_k=max_rank,
+                                 _k_target_cr=cr, _n_kv_heads=nkv, head_dim=hd,
+                                 _v_vq_group_size=4, _v_vq_codebook_size=256)
+    saved = torch.svd_lowrank
+    torch.svd_lowrank = lambda A, q=6, niter=2, M=None: (None, S_fix, V_fix)
+    try:
+        torch.manual_seed(42)  # Cache.compress seeds 42 + layer index before layer 0
+        kd = rcache.Cache._compress_k(stub, k_full[:, :, start:end, :], positions, B, n_comp)
+        vd = rcache.Cache._compress_v(stub, v_full[:, :, start:end, :], B)
+    finally:
+        torch.svd_lowrank = saved
+    # _build_gpu_format's K and V statements (cache.py:412-427) on the CPU
+    n_total = kd["k_n_total"]
+    keep = len(kd["k_alloc"])
+    coeffs = dequantize_group(kd["k_bytes"], kd["k_alloc"], n_total, "cpu")
+    col_max = coeffs.abs().amax(dim=0).clamp(min=1e-6)
+    coeff_scale = col_max / 7.0
+    q = (coeffs / coeff_scale).round().clamp(-7, 7).to(torch.int8)
+    k_coeffs = int4_pack(q)
+    qd = vd["v_qdata"]
+    ng = hd // qd["group_size"]
+    v_idx = unpack_nbits(qd["packed"], qd["bits"], qd["n_orig"])
+    v_idx_row0 = v_idx[: nkv * n_comp * ng].view(nkv, n_comp, ng).to(torch.uint8)
+    k_basis_f16 = (kd["k_basis_q"][:, :keep].to(torch.float16)
+                   * kd["k_scale"][:keep].to(torch.float16)).contiguous()
+    lo, rng = group_header(kd["k_bytes"], kd["k_alloc"])
+    np.savez_compressed(
+        os.path.join(HERE, "compress.npz"),
+        k_full=k_full.numpy(), v_full=v_full.numpy(), inv_freq=inv_freq.numpy(),
+        sink=sink, win=win, max_rank=max_rank, k_target_cr=cr,
+        svd_S=S_fix.numpy(), svd_V=V_fix.numpy(),
+        k_basis_q=kd["k_basis_q"].numpy(), k_scale=kd["k_scale"].numpy(),
+        k_mean=kd["k_mean"].numpy(), alloc=np.asarray(kd["k_alloc"], np.int32),
+        lo=lo, rng=rng, deq=coeffs.numpy().astype(np.float32), q=q.numpy(),
+        coeff_scale=coeff_scale.numpy().astype(np.float32), k_coeffs=k_coeffs.numpy(),
+        k_basis_f16=k_basis_f16.numpy(),
+        centroids=qd["centroids"].numpy(), v_packed=qd["packed"].numpy().astype(np.uint8),
+        ch_maxabs=qd["ch_maxabs"].numpy(), v_indices_row0=v_idx_row0.numpy())
+
+
+def write_ensure_dequant(rcache):
+    """ensure_dequant.npz: see the module docstring."""
+    import types
+    g = torch.Generator().manual_seed(31)
+    B, nkv, hd, rank, n_comp, sink, win, n_stream, n_dec = 2, 2, 128, 48, 37, 4, 8, 3, 2
+    start = sink
+    inv_freq = 1.0 / (500000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    basis_q = torch.randint(-127, 128, (nkv * hd, rank), generator=g).to(torch.int8)
+    basis_scale = (torch.rand(rank, generator=g) * 0.004 + 0.001).half()
+    q4 = torch.randint(-7, 8, (B * n_comp, rank), generator=g)
+    sh = (q4 + 8).to(torch.uint8).reshape(-1)
+    packed = sh[0::2] | (sh[1::2] << 4)
+    coeff_scale = (torch.rand(rank, generator=g) * 0.3 + 0.05).half()
+    mean = (torch.randn(nkv * hd, generator=g) * 0.2).half()
+    v_idx = torch.randint(0, 256, (B * nkv * n_comp * (hd // 4),), generator=g).to(torch.uint8)
+    cent_h = (torch.randn(256, 4, generator=g) * 0.5).half()
+    ch = (torch.rand(B * nkv, hd, generator=g) * 2 + 0.5).half()
+    seg = lambda n: torch.randn(B, nkv, n, hd, generator=g).half()
+    sink_k, sink_v, win_k, win_v, dec_k, dec_v = seg(sink), seg(sink), seg(win), seg(win), seg(n_dec), seg(n_dec)
+    s_kidx = torch.randint(0, 256, (n_stream, B, nkv, hd), generator=g).to(torch.uint8)
+    s_vidx = torch.randint(0, 256, (n_stream, B, nkv, hd), generator=g).to(torch.uint8)
+    s_kn = (torch.rand(n_stream, B, nkv, generator=g) * 10 + 1).half()
+    s_vn = (torch.rand(n_stream, B, nkv, generator=g) * 10 + 1).half()
+    signs = ((torch.randint(0, 2, (hd,), generator=g) * 2 - 1).float())
+    qdata = {"centroids": cent_h, "packed": v_idx, "ch_maxabs": ch, "shape": (B * nkv, n_comp, hd),
+             "group_size": 4, "bits": 8, "n_orig": v_idx.numel()}
+    gc = {
+        "k_coeffs": packed, "k_coeffs_shape": (B * n_comp, rank), "k_coeff_scale": coeff_scale,
+        "k_basis_q": basis_q, "k_basis_scale": basis_scale, "k_mean": mean,
+        "v_qdata": qdata, "sink_k": sink_k, "sink_v": sink_v, "win_k": win_k, "win_v": win_v,
+        "n_compress": n_comp, "batch": B, "compress_start": start,
+        "signs": signs, "stream_n": n_stream * B,
+        "k_idx_buf": s_kidx, "v_idx_buf": s_vidx, "k_norm_buf": s_kn, "v_norm_buf": s_vn,
+        "decode_k": dec_k, "decode_v": dec_v,
+    }
+    cref = types.SimpleNamespace(_n_kv_heads=nkv, head_dim=hd, _rope_inv_freq=inv_freq,
+                                 _stream_bits=8, _stream_qjl=False)
+    layer = types.SimpleNamespace(_gpu_compressed=gc, _cache_ref=cref, _needs_decompress=True,
+                                  _keys=None, _values=None)
+    layer._dequant_stream = types.MethodType(rcache.CacheLayer._dequant_stream, layer)
+    with torch.no_grad():
+        rcache.CacheLayer._ensure_dequant(layer)
+        vdec = rcache.vq_decode(qdata, "cpu")
+    np.savez_compressed(
+        os.path.join(HERE, "ensure_dequant.npz"),
+        inv_freq=inv_freq.numpy(), rank=rank, n_comp=n_comp, start=start, batch=B,
+        k_coeffs=packed.numpy(), k_coeff_scale=coeff_scale.numpy(), k_basis_q=basis_q.numpy(),
+        k_basis_scale=basis_scale.numpy(), k_mean=mean.numpy(), v_idx=v_idx.numpy(),
+        centroids=cent_h.numpy(), ch=ch.numpy(), sink_k=sink_k.numpy(), sink_v=sink_v.numpy(),
+        win_k=win_k.numpy(), win_v=win_v.numpy(), decode_k=dec_k.numpy(), decode_v=dec_v.numpy(),
+        s_kidx=s_kidx.numpy(), s_vidx=s_vidx.numpy(), s_knorm=s_kn.numpy(), s_vnorm=s_vn.numpy(),
+        signs=signs.numpy(), keys=layer._keys.numpy(), values=layer._values.numpy(),
+        vq_decoded=vdec.numpy())
+
+
 def main(ref_root, only=()):
     sys.path.insert(0, os.path.join(ref_root, "src"))
     from shard.streaming import lloyd_max_codebook, quantize_per_token  # noqa: F401
@@ -152,6 +314,10 @@ def main(ref_root, only=()):
         cent, idx = rcache.kmeans(data, 16, n_iter=30, seed=42)
         np.savez(os.path.join(HERE, "kmeans.npz"), data=data.numpy(), centroids=cent.numpy(),
                  idx=idx.numpy().astype(np.int64), k=16, n_iter=30, seed=42)
+    if want("compress.npz"):
+        write_compress(rcache)
+    if want("ensure_dequant.npz"):
+        write_ensure_dequant(rcache)
     if not want("fused_attn.npz"):
         return
 

@@ -347,7 +347,7 @@ def test_reference_fused_path_matches_golden(golden):
     gc, nkv = _gc_from_fixture(f)
     out = ref.fused_attention_compressed(torch.from_numpy(f["q_rope"]), gc, nkv, int(f["pos_q"]),
                                          torch.from_numpy(f["inv_freq"]))
-    np.testing.assert_allclose(out.float().numpy(), f["out"].astype(np.float32), atol=2e-3, rtol=0)
+    assert np.array_equal(out.numpy(), f["out"])
 
 
 def test_exact_oracle_close_to_reference_fused_path(golden):
@@ -401,3 +401,105 @@ def test_batch_rows_slice_matches_full_oracle():
     np.testing.assert_array_equal(part, full[[3, 1]])
     swapped = exact.decode_attention(q[[3, 1]].numpy(), batch_rows(gc, [1, 3]), 8, pos_q, inv.numpy())
     assert np.max(np.abs(swapped - full[[3, 1]])) > 1e-2
+
+
+# --------------------------------------------------------------------------
+# Composites: one layer of Cache.compress and _ensure_dequant (reference
+# outputs of tests/golden/compress.npz and ensure_dequant.npz)
+# --------------------------------------------------------------------------
+def _compress_golden(golden):
+    g = golden("compress.npz")
+    gc = ref.compress_layer(torch.from_numpy(g["k_full"]), torch.from_numpy(g["v_full"]), 0,
+                            torch.from_numpy(g["inv_freq"]), sink=int(g["sink"]), win=int(g["win"]),
+                            k_target_cr=float(g["k_target_cr"]), max_rank=int(g["max_rank"]),
+                            svd=(g["svd_S"], g["svd_V"]))
+    return g, gc
+
+
+def test_compress_layer_matches_reference_golden(golden):
+    """oracle.ref.compress_layer reproduces the reference's _compress_k +
+    _compress_v + _build_gpu_format bit for bit (svd_lowrank stubbed to the
+    same fixed (S, V) on both sides): int8 basis and scales, mean, the DP
+    allocation, the group codes' (lo, rng), the dequantized coefficients, the
+    int4 codes and their packing, the V codebook, indices and channel scales."""
+    g, gc = _compress_golden(golden)
+    assert gc["alloc"] == list(g["alloc"])
+    assert np.array_equal(gc["k_basis_q"].numpy(), g["k_basis_q"])
+    assert np.array_equal(gc["k_basis_scale"].numpy(), g["k_scale"])
+    assert np.array_equal(gc["k_mean"].numpy(), g["k_mean"])
+    assert np.array_equal(gc["k_basis_f16"].numpy(), g["k_basis_f16"])
+    ch = gc["chain"]
+    assert np.array_equal(ch["lo"], g["lo"]) and np.array_equal(ch["rng"], g["rng"])
+    assert np.array_equal(ch["deq"], g["deq"])
+    assert np.array_equal(ch["q"], g["q"])
+    assert np.array_equal(ch["coeff_scale"], g["coeff_scale"])
+    assert np.array_equal(gc["k_coeffs"].numpy(), g["k_coeffs"])
+    assert np.array_equal(gc["v_centroids_f16"].numpy(), g["centroids"])
+    assert np.array_equal(gc["v_qdata"]["idx"].numpy(), g["v_packed"])
+    assert np.array_equal(gc["v_qdata"]["ch_maxabs"].numpy(), g["ch_maxabs"])
+    # the reference's on-device V index view keeps batch row 0 (cache.py:426-427);
+    # the batch-major layout's row 0 is that view
+    assert np.array_equal(gc["v_idx_full"][0].numpy(), g["v_indices_row0"])
+
+
+def test_compress_golden_is_sensitive_to_layout():
+    """A flatten order with heads and tokens swapped, or no centring, changes
+    the reference's codes: the golden pins the stitching, not only the leaves."""
+    import os
+    from tests.conftest import GOLDEN
+    g = np.load(os.path.join(GOLDEN, "compress.npz"))
+    k = torch.from_numpy(g["k_full"])
+    swapped = k.view(2, 2, 200, 128).permute(0, 2, 1, 3).reshape(2, 2, 200, 128)  # heads <-> tokens mixed
+    gc = ref.compress_layer(swapped.contiguous(), torch.from_numpy(g["v_full"]), 0,
+                            torch.from_numpy(g["inv_freq"]), k_target_cr=float(g["k_target_cr"]),
+                            max_rank=int(g["max_rank"]), svd=(g["svd_S"], g["svd_V"]))
+    assert not np.array_equal(gc["k_coeffs"].numpy(), g["k_coeffs"])
+    assert not np.array_equal(gc["k_mean"].numpy(), g["k_mean"])
+
+
+def _ensure_dequant_gc(f):
+    B, rank, n_comp, start = int(f["batch"]), int(f["rank"]), int(f["n_comp"]), int(f["start"])
+    nkv = f["sink_k"].shape[1]
+    return {
+        "k_coeffs": torch.from_numpy(f["k_coeffs"]), "k_coeffs_shape": (B * n_comp, rank),
+        "k_coeff_scale": torch.from_numpy(f["k_coeff_scale"]),
+        "k_basis_q": torch.from_numpy(f["k_basis_q"]),
+        "k_basis_scale": torch.from_numpy(f["k_basis_scale"]),
+        "k_mean": torch.from_numpy(f["k_mean"]),
+        "v_qdata": {"centroids": torch.from_numpy(f["centroids"]), "idx": torch.from_numpy(f["v_idx"]),
+                    "ch_maxabs": torch.from_numpy(f["ch"]), "shape": (B * nkv, n_comp, 128),
+                    "group_size": 4},
+        "n_compress": n_comp, "batch": B, "compress_start": start,
+    }, nkv
+
+
+def test_vq_decode_matches_reference_golden(golden):
+    f = golden("ensure_dequant.npz")
+    gc, _ = _ensure_dequant_gc(f)
+    assert np.array_equal(ref.vq_decode(gc["v_qdata"]).numpy(), f["vq_decoded"])
+
+
+def test_reconstruct_kv_matches_reference_golden(golden):
+    """oracle.ref.reconstruct_kv is the compressed segment of the reference's
+    _ensure_dequant output (batch 2: the view(B, n, nkv, hd).permute order),
+    bit for bit; the stream and decode tokens of the same golden are the
+    oracle's stream dequantization and the stored fp16 rows."""
+    f = golden("ensure_dequant.npz")
+    gc, nkv = _ensure_dequant_gc(f)
+    k_mid, v_mid = ref.reconstruct_kv(gc, nkv, 128, torch.from_numpy(f["inv_freq"]))
+    sink, n = f["sink_k"].shape[2], int(f["n_comp"])
+    keys, values = f["keys"], f["values"]
+    assert np.array_equal(k_mid.numpy(), keys[:, :, sink:sink + n])
+    assert np.array_equal(v_mid.numpy(), values[:, :, sink:sink + n])
+    win = f["win_k"].shape[2]
+    assert np.array_equal(keys[:, :, :sink], f["sink_k"])
+    assert np.array_equal(keys[:, :, sink + n:sink + n + win], f["win_k"])
+    s = f["s_kidx"].shape[0]
+    cb = ref.lloyd_max_codebook(128, 8)
+    sk = ref.dequantize_stream_token(f["s_kidx"], f["s_knorm"], f["signs"], cb)
+    sv = ref.dequantize_stream_token(f["s_vidx"], f["s_vnorm"], f["signs"], cb)
+    off = sink + n + win
+    assert np.array_equal(keys[:, :, off:off + s], np.transpose(sk, (1, 2, 0, 3)))
+    assert np.array_equal(values[:, :, off:off + s], np.transpose(sv, (1, 2, 0, 3)))
+    assert np.array_equal(keys[:, :, off + s:], f["decode_k"])
+    assert np.array_equal(values[:, :, off + s:], f["decode_v"])
