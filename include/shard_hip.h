@@ -55,6 +55,15 @@ int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_t lda,
                       const uint16_t* bt, int32_t n, float* c, int64_t ldc,
                       void* stream);
 
+/* The same projection with fp32 operands, as the reference computes it
+ * (cache.py:389-392: (flat - mean) @ (basis_q.float() * scale.float()), fp32):
+ * C[m, n] = A[m, k] (fp32) . Bt[n, k]^T (fp32) on v_mfma_f32_32x32x2_f32,
+ * fp32 sums.  k % 8 == 0, n % 32 == 0, n <= 256, lda % 4 == 0, a and bt
+ * 16-byte aligned.  The path Cache.compress takes. */
+int shard_pca_project_f32(const float* a, int64_t m, int32_t k, int64_t lda,
+                          const float* bt, int32_t n, float* c, int64_t ldc,
+                          void* stream);
+
 /* Prefill K preparation fused with the projection input: reads post-RoPE keys
  * k (B, n_kv, T, hd) fp16, undoes RoPE at positions start+t with fp32 phases
  * fl(pos * inv_freq[i]) (rope.py:13-24), subtracts mean[n_kv*hd] (fp32) and
@@ -66,6 +75,14 @@ int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
                     int32_t hd, int32_t start, int32_t n_comp,
                     const float* inv_freq, const float* mean, uint16_t* out,
                     void* stream);
+
+/* shard_k_prepare writing the centred rows in fp32 (no fp16 rounding): the
+ * (flat - mean) operand of cache.py:392 as the reference holds it.  out is
+ * 16-byte aligned. */
+int shard_k_prepare_f32(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
+                        int32_t hd, int32_t start, int32_t n_comp,
+                        const float* inv_freq, const float* mean, float* out,
+                        void* stream);
 
 /* Integer chain of the key coefficients, bit-exact with the reference:
  *   per column c with bits[c] > 0: lo = min, rng = max(max - lo, 1e-6),
@@ -284,7 +301,8 @@ typedef struct shard_decode_args {
   uint16_t* out;
   int32_t n_splits; /* 0 = choose automatically */
   int32_t kernel;   /* split kernel: 0 = automatic, 1 = row-split (4 waves share a
-                     * tile; 4 query heads per kv head, <= 2048 extra tokens),
+                     * tile; 4 query heads per kv head, <= 2048 extra tokens;
+                     * a call outside that runs on the token-tiled kernel),
                      * 2 = token-tiled (each wave owns whole tiles; every shape) */
   /* nullable device int64: when set, the kernel reads pos_q from it (the
    * reference's cache_position[-1], attention.py:383) and `pos_q` is ignored,

@@ -61,6 +61,8 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
     n_splits = getattr(c, "_n_splits", 0)
     stream_n_dev = None
     graph = getattr(c, "_graph", None)
+    if graph is None:
+        c._last_attn_mask = mask  # checked once when a decode graph opens
     if graph is not None:
         # a captured decode step: the stream count and the position come from
         # the graph's device counters, the plan covers the reserved rows.  The

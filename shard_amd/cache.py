@@ -5,7 +5,7 @@ CacheLayer: 64-292):
   prefill (q_len > 1)     fp16 K/V kept as-is (cache.py:142-147)
   first decode step       Cache.compress() of every layer (cache.py:149-151, 338-460):
                           K -> undo RoPE -> PCA (covariance eigh) -> DP bits -> int8
-                          basis -> projection (MFMA) -> group quant -> int4 (HIP);
+                          basis -> fp32 projection (MFMA) -> group quant -> int4 (HIP);
                           V -> Hadamard -> k-means VQ (HIP assign + update);
                           sink (4) and window (64) tokens stay fp16.
   decode tokens           8-bit Lloyd-Max stream (_streaming=True, HIP quantizer)
@@ -15,8 +15,8 @@ CacheLayer: 64-292):
                           (_ensure_dequant, cache.py:87-124; HIP reconstruct)
 The compression's per-token work runs in HIP kernels of libshard_hip.so (undo
 RoPE and centring, projection, int4 chain, Hadamard and VQ assignment, k-means
-update); torch computes the column mean and the covariance GEMM of the fp16
-operand, and the host a float64 eigendecomposition of the (p, p) covariance.
+update); torch computes the column mean and the covariance GEMM of the fp32
+rows, and the host a float64 eigendecomposition of the (p, p) covariance.
 CPU tensors are rejected.
 """
 import torch
@@ -303,6 +303,9 @@ class CacheLayer(CacheLayerMixin):
         the compressed representation as it was, so the next decode step (which
         reads it) sees the old row order; here its per-row tensors are selected
         too, so every later step runs on the reordered beams."""
+        if getattr(self._cache_ref, "_graph", None) is not None:
+            # a captured decode step holds the addresses of the rows reordered here
+            raise RuntimeError("reorder_cache while a decode graph is open: close() it first")
         if self._needs_decompress:
             _ = self.keys
         if self._keys is not None:
@@ -546,8 +549,7 @@ def _undo_rope_mean(k_full: torch.Tensor, start: int, end: int, inv_freq,
 
 
 def _covariance(x16: torch.Tensor, chunk: int = 1 << 15) -> torch.Tensor:
-    """X^T X / n of the fp16 rows in fp32, a row chunk at a time (no fp32 copy
-    of the whole operand)."""
+    """X^T X / n of the rows (fp16 or fp32) in fp32, a row chunk at a time."""
     n, p = x16.shape
     cov = torch.zeros(p, p, dtype=torch.float32, device=x16.device)
     for i in range(0, n, chunk):
@@ -607,7 +609,7 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     """Compress one layer's prefill K/V (B, G, T, D) fp16 into the device format.
 
     _compress_k (cache.py:368-396), _compress_v (398-404), _build_gpu_format
-    (406-454).  The projection runs on the MFMA GEMM, the integer chain, the
+    (406-454).  The projection runs on the fp32 MFMA GEMM, the integer chain, the
     Hadamard/normalization, the k-means assignment and update in HIP kernels.
     ``debug``: a dict that receives the fp32 projection ``proj`` (rows, keep)
     and the bit allocation ``alloc`` (for parity tests).
@@ -620,15 +622,15 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     inv_freq = cache._rope_inv_freq
     torch.manual_seed(42 + li)
 
-    # ---- K: undo RoPE and centring (shard_k_prepare: fp32 math, fp16 rows of
-    # the projection operand), PCA basis, DP bits, int8 basis
+    # ---- K: undo RoPE and centring (shard_k_prepare_f32: the fp32 rows of
+    # (flat - mean), cache.py:370-392), PCA basis, DP bits, int8 basis
     p_dim = G * D
     n = B * n_comp
     invf = (inv_freq.to(dev, torch.float32) if inv_freq is not None
             else torch.zeros(D // 2, dtype=torch.float32, device=dev))  # phase 0: no rotation
     k_full = k_full.contiguous()
     mean = _undo_rope_mean(k_full, start, end, inv_freq)
-    centered = ops.k_prepare(k_full, start, n_comp, invf, mean)   # (n, p_dim) fp16
+    centered = ops.k_prepare(k_full, start, n_comp, invf, mean, out_dtype=torch.float32)  # (n, p_dim)
     rank = min(cache._max_rank_k, p_dim, n - 1)
     if basis is None and cache._basis_override is not None:
         basis = cache._basis_override.get(li)
@@ -661,11 +663,12 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     basis_q = (basis / scale).round().clamp(-127, 127).to(torch.int8)
     basis_deq = basis_q.float() * scale.float()                  # (p_dim, keep)
 
-    # ---- projection on MFMA (fp16 operands, fp32 accumulate); columns padded to 32
+    # ---- projection on fp32 MFMA, fp32 operands as the reference's
+    # (flat - mean) @ (basis_q * scale) (cache.py:392); columns padded to 32
     keep32 = ((keep + 31) // 32) * 32
-    bt = torch.zeros(keep32, p_dim, dtype=torch.float16, device=dev)
-    bt[:keep] = basis_deq.t().half()
-    proj = ops.pca_project(centered, bt)[:, :keep].contiguous()
+    bt = torch.zeros(keep32, p_dim, dtype=torch.float32, device=dev)
+    bt[:keep] = basis_deq.t()
+    proj = ops.pca_project_f32(centered, bt)[:, :keep].contiguous()
     del centered
     bits = torch.tensor(alloc, dtype=torch.int32, device=dev)
     chain = ops.int4_quant_pack(proj, bits)

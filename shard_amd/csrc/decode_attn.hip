@@ -1454,9 +1454,12 @@ inline bool split_supported(const shard_decode_args* a) {
 // tokens, 23.3 vs 21.9 with 468, 34.3 vs 22.7 with 1,068).
 constexpr int kRowSplitMaxExtraAuto = 256;
 
+// kernel = 1 asks for the row-split kernel; a call it cannot take (query
+// groups other than 4, more than kMaxExtra extra tokens: the reference appends
+// stream tokens without limit, cache.py:156-181) runs on the token-tiled one.
 inline bool use_tok(const shard_decode_args* a) {
   if (a->kernel == 2) return true;
-  if (a->kernel == 1) return false;
+  if (a->kernel == 1) return !split_supported(a);
   if (!split_supported(a) || n_extra(a) > kRowSplitMaxExtraAuto) return true;
   const int64_t tiles = (int64_t)((a->n_comp + kTile - 1) / kTile) * a->n_kv_heads * a->batch;
   return tiles >= (int64_t)kTokMinHeadTilesPerCU * device_cus();
@@ -1618,7 +1621,6 @@ static int decode_attn_check(const shard_decode_args* a) {
     return SHARD_ERR_ARG;
   if (!tok_supported(a) || n_extra(a) > (int64_t)INT32_MAX / 4) return SHARD_ERR_SHAPE;
   if (((uintptr_t)a->q & 15) || ((uintptr_t)a->out & 3)) return SHARD_ERR_ARG;  // vector accesses
-  if (!use_tok(a) && !split_supported(a)) return SHARD_ERR_SHAPE;  // kernel 1 forced on a shape it lacks
   return SHARD_OK;
 }
 

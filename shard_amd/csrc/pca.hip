@@ -136,6 +136,123 @@ void k_pca_project(const uint16_t* __restrict__ A, int64_t m, int k, int64_t lda
   }
 }
 
+// The same GEMM in fp32 (C = A . Bt^T with fp32 A and Bt): the projection of
+// _compress_k in the reference's own arithmetic (cache.py:389-392 projects
+// (flat - mean) @ (basis_q * scale) with fp32 operands).  v_mfma_f32_32x32x2_f32
+// multiplies fp32 operands with an fp32 sum, so the projection differs from a
+// sequential fp32 dot product only by the order of its roundings.
+// Same workgroup shape as k_pca_project (8 waves, 128 rows, two column
+// halves).  A k step of the MFMA takes k pairs {k0 + j, k0 + 4 + j} from the
+// two lane halves: lane (row, hh) loads A[row][k0 + 4 hh .. + 3] as one 16-byte
+// vector and feeds element j to step j, and the B side (from LDS) follows the
+// same order, so four MFMAs consume 8 consecutive k.  Bt is staged in LDS 32 k
+// at a time, double-buffered, with A and the Bt pieces loaded three chunks
+// ahead into a 4-slot register ring (raw buffer loads, out-of-range offsets
+// read zeros, as in k_pca_project).
+template <int NB32>
+__global__ __launch_bounds__(kPcaThreads, 1)
+void k_pca_project_f32(const float* __restrict__ A, int64_t m, int k, int64_t lda,
+                       const float* __restrict__ Bt, float* __restrict__ C, int64_t ldc) {
+  constexpr int KC = 32;                          // k chunk staged in LDS
+  constexpr int kRowStride = KC + 4;              // floats per staged row (bank spread)
+  constexpr int NH = (NB32 + 1) / 2;              // column blocks per wave half
+  constexpr int kPieces = NB32 * 32 * (KC / 4);   // 16-byte pieces of one Bt chunk
+  constexpr int kPer = (kPieces + kPcaThreads - 1) / kPcaThreads;
+  __shared__ __align__(16) float bs[2][NB32 * 32 * kRowStride];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rw = w & 3, half = w >> 2;
+  const int col = lane & 31, hh = lane >> 5;
+  const int j0 = half * NH;
+  const int nj = NB32 - j0 < NH ? NB32 - j0 : NH;
+  const int64_t blk0 = (int64_t)blockIdx.x * kPcaRows;
+  const int64_t row0 = blk0 + 32 * rw;
+  const int64_t nrows = m - blk0 < kPcaRows ? m - blk0 : kPcaRows;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + blk0 * lda), (short)0, (int)(nrows * lda * 4), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)Bt, (short)0, NB32 * 32 * k * 4, kBufWord3);
+  const int a_off = (32 * rw + col) * (int)lda * 4;
+  const int nc = (k + KC - 1) / KC;
+
+  auto load_b = [&](int c, float4v (&pb)[kPer]) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int pc = tid + kPcaThreads * u;
+      const int r = pc / (KC / 4), kk = KC * c + 4 * (pc % (KC / 4));
+      const int off = (pc < kPieces && kk < k) ? (r * k + kk) * 4 : kOutOfRange;
+      pb[u] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+    }
+  };
+  auto store_b = [&](int buf, const float4v (&pb)[kPer]) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int pc = tid + kPcaThreads * u;
+      if (pc < kPieces) *(float4v*)(&bs[buf][(pc / (KC / 4)) * kRowStride + 4 * (pc % (KC / 4))]) = pb[u];
+    }
+  };
+  auto load_a = [&](int c, float4v (&af)[KC / 8]) {
+#pragma unroll
+    for (int s = 0; s < KC / 8; ++s) {
+      const int kk = KC * c + 8 * s + 4 * hh;
+      const int off = kk < k ? a_off + kk * 4 : kOutOfRange;
+      af[s] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+    }
+  };
+
+  float16v acc[NH];
+#pragma unroll
+  for (int j = 0; j < NH; ++j) acc[j] = {};
+
+  float4v pb[4][kPer];
+  float4v af[4][KC / 8];
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    load_b(d, pb[d]);
+    load_a(d, af[d]);
+  }
+  store_b(0, pb[0]);
+  __syncthreads();
+
+  auto step = [&](const int c, const float4v (&a)[KC / 8], float4v (&a3)[KC / 8],
+                  const float4v (&b1)[kPer], float4v (&b3)[kPer]) {
+    const float* b = bs[c & 1];
+#pragma unroll
+    for (int s = 0; s < KC / 8; ++s) {
+#pragma unroll
+      for (int jj = 0; jj < NH; ++jj) {
+        if (NB32 % 2 == 0 || jj < nj) {
+          const float4v bv = *(const float4v*)(b + (32 * (j0 + jj) + col) * kRowStride + 8 * s + 4 * hh);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][j], bv[j], acc[jj], 0, 0, 0);
+        }
+      }
+    }
+    store_b((c + 1) & 1, b1);
+    load_b(c + 3, b3);
+    load_a(c + 3, a3);
+    __syncthreads();
+  };
+  const int nc4 = (nc + 3) & ~3;
+  for (int c0 = 0; c0 < nc4; c0 += 4) {
+    step(c0, af[0], af[3], pb[1], pb[3]);
+    step(c0 + 1, af[1], af[0], pb[2], pb[0]);
+    step(c0 + 2, af[2], af[1], pb[3], pb[1]);
+    step(c0 + 3, af[3], af[2], pb[0], pb[2]);
+  }
+#pragma unroll
+  for (int jj = 0; jj < NH; ++jj) {
+    if (jj < nj) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t r = row0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (r < m) C[r * ldc + 32 * (j0 + jj) + col] = acc[jj][i];
+      }
+    }
+  }
+}
+
 }  // namespace shard
 
 using namespace shard;
@@ -163,5 +280,31 @@ extern "C" int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_pca_project");
+  return SHARD_OK;
+}
+
+extern "C" int shard_pca_project_f32(const float* a, int64_t m, int32_t k, int64_t lda,
+                                     const float* bt, int32_t n, float* c, int64_t ldc,
+                                     void* stream) {
+  if (!a || !bt || !c || m <= 0 || k <= 0 || n <= 0) return SHARD_ERR_ARG;
+  if (k % 8 != 0 || n % 32 != 0 || n > 256 || lda < k || ldc < n || (lda % 4) != 0)
+    return SHARD_ERR_SHAPE;
+  if (((uintptr_t)a & 15) || ((uintptr_t)bt & 15)) return SHARD_ERR_SHAPE;  // 16-byte vectors
+  if ((int64_t)kPcaRows * lda * 4 >= (1ll << 31) - 256 || (int64_t)n * k * 4 >= (1ll << 31) - 256)
+    return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)((m + kPcaRows - 1) / kPcaRows));
+  switch (n / 32) {
+    case 1: hipLaunchKernelGGL(k_pca_project_f32<1>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    case 2: hipLaunchKernelGGL(k_pca_project_f32<2>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    case 3: hipLaunchKernelGGL(k_pca_project_f32<3>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    case 4: hipLaunchKernelGGL(k_pca_project_f32<4>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    case 5: hipLaunchKernelGGL(k_pca_project_f32<5>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    case 6: hipLaunchKernelGGL(k_pca_project_f32<6>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    case 7: hipLaunchKernelGGL(k_pca_project_f32<7>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    case 8: hipLaunchKernelGGL(k_pca_project_f32<8>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
+    default: return SHARD_ERR_SHAPE;
+  }
+  SHARD_LAUNCH_CHECK("shard_pca_project_f32");
   return SHARD_OK;
 }

@@ -1071,12 +1071,15 @@ __global__ void k_rope_stream(const uint16_t* __restrict__ q, const uint16_t* __
 // One workgroup per token t of the window: the token's hd/2 RoPE phases are
 // computed once (shared by every batch row and kv head), then thread (i4, y)
 // undoes pairs 4 i4 .. 4 i4 + 3 of the (b, g) rows y, y + blockDim.y, ...
-// (8-byte loads and stores; hd a multiple of 8).
+// (8-byte loads; hd a multiple of 8).  OutT = uint16_t writes the centred rows
+// rounded once to fp16 (the fp16 GEMM operand); OutT = float writes them as
+// computed, the fp32 rows the reference projects (cache.py:370-392).
+template <typename OutT>
 __global__ __launch_bounds__(256) void k_k_prepare(const uint16_t* __restrict__ k, int batch,
                                                    int n_kv, int seq, int hd, int start, int n_comp,
                                                    const float* __restrict__ inv_freq,
                                                    const float* __restrict__ mean,
-                                                   uint16_t* __restrict__ out) {
+                                                   OutT* __restrict__ out) {
   __shared__ float2 ph[256];  // (cos, sin) of the token's phases, hd / 2 <= 256
   const int hd2 = hd >> 1, D = n_kv * hd;
   const int t = blockIdx.x, pos = start + t;
@@ -1116,21 +1119,49 @@ __global__ __launch_bounds__(256) void k_k_prepare(const uint16_t* __restrict__ 
     const uint16_t hi[4] = {(uint16_t)hi4.x, (uint16_t)(hi4.x >> 16), (uint16_t)hi4.y,
                             (uint16_t)(hi4.y >> 16)};
     const float* mn = mean + g * hd;
-    uint16_t olo[4], ohi[4];
+    float clo[4], chi[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float l = h2f(lo[j]), h = h2f(hi[j]);
       // undo_rope: k*cos - rotate_half(k)*sin, rotate_half = [-hi, lo]
       const float ulo = add_rn(mul_rn(l, p[j].x), mul_rn(h, p[j].y));
       const float uhi = sub_rn(mul_rn(h, p[j].x), mul_rn(l, p[j].y));
-      olo[j] = f2h(sub_rn(ulo, mn[i0 + j]));
-      ohi[j] = f2h(sub_rn(uhi, mn[hd2 + i0 + j]));
+      clo[j] = sub_rn(ulo, mn[i0 + j]);
+      chi[j] = sub_rn(uhi, mn[hd2 + i0 + j]);
     }
-    uint16_t* o = out + ((int64_t)b * n_comp + t) * D + g * hd;
-    *(uint2*)(o + i0) = make_uint2(olo[0] | ((uint32_t)olo[1] << 16), olo[2] | ((uint32_t)olo[3] << 16));
-    *(uint2*)(o + hd2 + i0) =
-        make_uint2(ohi[0] | ((uint32_t)ohi[1] << 16), ohi[2] | ((uint32_t)ohi[3] << 16));
+    OutT* o = out + ((int64_t)b * n_comp + t) * D + g * hd;
+    if constexpr (sizeof(OutT) == 4) {
+      *(float4*)(o + i0) = make_float4(clo[0], clo[1], clo[2], clo[3]);
+      *(float4*)(o + hd2 + i0) = make_float4(chi[0], chi[1], chi[2], chi[3]);
+    } else {
+      uint16_t olo[4], ohi[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        olo[j] = f2h(clo[j]);
+        ohi[j] = f2h(chi[j]);
+      }
+      *(uint2*)(o + i0) = make_uint2(olo[0] | ((uint32_t)olo[1] << 16), olo[2] | ((uint32_t)olo[3] << 16));
+      *(uint2*)(o + hd2 + i0) =
+          make_uint2(ohi[0] | ((uint32_t)ohi[1] << 16), ohi[2] | ((uint32_t)ohi[3] << 16));
+    }
   }
+}
+
+template <typename OutT>
+inline int k_prepare_launch(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq, int32_t hd,
+                            int32_t start, int32_t n_comp, const float* inv_freq, const float* mean,
+                            OutT* out, void* stream, const char* name) {
+  if (!k || !inv_freq || !mean || !out || batch <= 0 || n_kv <= 0 || n_comp <= 0) return SHARD_ERR_ARG;
+  if ((hd & 7) || hd > 512 || start < 0 || start + n_comp > seq) return SHARD_ERR_SHAPE;
+  // 8-byte input vectors, 4-element output vectors
+  if (((uintptr_t)k & 7) || ((uintptr_t)out & (4 * sizeof(OutT) - 1))) return SHARD_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  const int hd8 = hd / 8;
+  const dim3 block(hd8, 256 / hd8 < 1 ? 1 : 256 / hd8);
+  hipLaunchKernelGGL(k_k_prepare<OutT>, dim3((unsigned)n_comp), block, 0, s, k, batch, n_kv, seq, hd,
+                     start, n_comp, inv_freq, mean, out);
+  SHARD_LAUNCH_CHECK(name);
+  return SHARD_OK;
 }
 
 }  // namespace shard
@@ -1451,16 +1482,15 @@ int shard_stream_quant(const uint16_t* x, int64_t rows, int32_t hd, const float*
 int shard_k_prepare(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq, int32_t hd,
                     int32_t start, int32_t n_comp, const float* inv_freq, const float* mean,
                     uint16_t* out, void* stream) {
-  if (!k || !inv_freq || !mean || !out || batch <= 0 || n_kv <= 0 || n_comp <= 0) return SHARD_ERR_ARG;
-  if ((hd & 7) || hd > 512 || start < 0 || start + n_comp > seq) return SHARD_ERR_SHAPE;
-  if (((uintptr_t)k & 7) || ((uintptr_t)out & 7)) return SHARD_ERR_SHAPE;  // 8-byte vectors
-  hipStream_t s = (hipStream_t)stream;
-  const int hd8 = hd / 8;
-  const dim3 block(hd8, 256 / hd8 < 1 ? 1 : 256 / hd8);
-  hipLaunchKernelGGL(k_k_prepare, dim3((unsigned)n_comp), block, 0, s, k, batch, n_kv, seq, hd,
-                     start, n_comp, inv_freq, mean, out);
-  SHARD_LAUNCH_CHECK("shard_k_prepare");
-  return SHARD_OK;
+  return k_prepare_launch(k, batch, n_kv, seq, hd, start, n_comp, inv_freq, mean, out, stream,
+                          "shard_k_prepare");
+}
+
+int shard_k_prepare_f32(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq, int32_t hd,
+                        int32_t start, int32_t n_comp, const float* inv_freq, const float* mean,
+                        float* out, void* stream) {
+  return k_prepare_launch(k, batch, n_kv, seq, hd, start, n_comp, inv_freq, mean, out, stream,
+                          "shard_k_prepare_f32");
 }
 
 }  // extern "C"

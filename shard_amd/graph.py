@@ -13,12 +13,17 @@ the cache's own counters (stream length, sequence length) in step with the
 replays, so the cache can go back to eager steps afterwards.
 
 Requirements: a compressed, streaming cache whose every layer takes the fused
-kernel, rows of equal length (no attention mask) and transformers' Llama
-attention patched by `enable_llama_fused_attention`.
+kernel, rows of equal length (no attention mask: refused when the cache's last
+eager decode step was masked) and transformers' Llama attention patched by
+`enable_llama_fused_attention`.  While the graph is open the cache's device
+tensors must keep their addresses: `reorder_cache` raises, and eager appends
+go through the graph's rows.  The graph keeps the shared decode workspace it
+captured alive.  The work plan of every captured call (its kernel choice and
+split balance) covers the stream rows of all `max_steps` steps from step 0.
 """
 import torch
 
-from .attention import fused_supported
+from .attention import _workspaces, fused_supported
 
 
 class DecodeGraph:
@@ -36,6 +41,12 @@ class DecodeGraph:
             raise ValueError("DecodeGraph needs a compressed cache in streaming mode")
         if getattr(cache, "_graph", None) is not None:
             raise ValueError("the cache already runs a decode graph")
+        mask = getattr(cache, "_last_attn_mask", None)
+        if mask is not None and bool((mask != 0).any()):
+            # the replays attend without a mask; eager steps that were masked
+            # (a left-padded batch) would attend to pad tokens under the graph
+            raise ValueError("the cache's last decode step attended with a padding mask; "
+                             "a decode graph needs rows of equal length")
         if next_ids.dim() != 2 or next_ids.shape[1] != 1 or not next_ids.is_cuda:
             raise ValueError("next_ids must be (B, 1) on the GPU")
         if max_steps < 1:
@@ -72,6 +83,7 @@ class DecodeGraph:
         self.graph = None
         self.next = None
         self.logits = None
+        self._pinned = None
         cache._graph = self
 
     def _body(self):
@@ -111,6 +123,10 @@ class DecodeGraph:
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph):
                 self.logits, self.next = self._body()
+            # the captured attention calls hold the address of the device's
+            # shared decode workspace; a later eager call that needs a larger
+            # one replaces it in the dict, so the graph keeps this one alive
+            self._pinned = dict(_workspaces)
             self.graph.replay()
         else:
             self._advance_host()
@@ -123,3 +139,4 @@ class DecodeGraph:
         if self.cache._graph is self:
             self.cache._graph = None
         self.graph = None
+        self._pinned = None

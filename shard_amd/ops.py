@@ -69,18 +69,41 @@ def pca_project(a: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
     return c
 
 
+def pca_project_f32(a: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
+    """C = A @ Bt^T on fp32 MFMA; A (m, k) fp32, Bt (n, k) fp32 -> (m, n) fp32
+    (the reference's fp32 projection, cache.py:389-392)."""
+    _require_gpu(a, bt)
+    lib = _lib.load()
+    a = _contig(a, torch.float32, "a")
+    bt = _contig(bt, torch.float32, "bt")
+    m, k = a.shape
+    n, k2 = bt.shape
+    if k != k2:
+        raise ValueError("pca_project_f32: inner dims differ")
+    c = torch.empty(m, n, dtype=torch.float32, device=a.device)
+    _lib.check("shard_pca_project_f32", lib.shard_pca_project_f32(
+        _p(a), m, k, k, _p(bt), n, _p(c), n, _stream(a)))
+    return c
+
+
 def k_prepare(k: torch.Tensor, start: int, n_comp: int, inv_freq: torch.Tensor,
-              mean: torch.Tensor) -> torch.Tensor:
-    """undo-RoPE + mean subtraction of keys (B, G, T, D) fp16 -> (B*n_comp, G*D) fp16."""
+              mean: torch.Tensor, out_dtype=torch.float16) -> torch.Tensor:
+    """undo-RoPE + mean subtraction of keys (B, G, T, D) fp16 -> (B*n_comp, G*D)
+    rows in out_dtype: fp16 (the fp16 GEMM operand) or fp32 (no rounding)."""
     _require_gpu(k, inv_freq, mean)
     lib = _lib.load()
     k = _contig(k, torch.float16, "k")
     B, G, T, D = k.shape
     inv_freq = _contig(inv_freq.to(k.device), torch.float32, "inv_freq")
     mean = _contig(mean, torch.float32, "mean")
-    out = torch.empty(B * n_comp, G * D, dtype=torch.float16, device=k.device)
-    _lib.check("shard_k_prepare", lib.shard_k_prepare(
-        _p(k), B, G, T, D, start, n_comp, _p(inv_freq), _p(mean), _p(out), _stream(k)))
+    out = torch.empty(B * n_comp, G * D, dtype=out_dtype, device=k.device)
+    if out_dtype == torch.float16:
+        fn, name = lib.shard_k_prepare, "shard_k_prepare"
+    elif out_dtype == torch.float32:
+        fn, name = lib.shard_k_prepare_f32, "shard_k_prepare_f32"
+    else:
+        raise TypeError(f"k_prepare: out_dtype must be float16 or float32, got {out_dtype}")
+    _lib.check(name, fn(_p(k), B, G, T, D, start, n_comp, _p(inv_freq), _p(mean), _p(out), _stream(k)))
     return out
 
 

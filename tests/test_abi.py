@@ -74,3 +74,25 @@ def test_cpu_tensor_is_rejected_loudly():
     from shard_amd import ops
     with pytest.raises(ops.ShardHipUnavailable):
         ops.fwht(torch.zeros(4, 128))
+
+
+def test_forced_row_split_beyond_its_extras_runs_token_tiled():
+    """kernel = 1 (Cache._decode_kernel = 1) on a call with more than 2,048
+    extra tokens (a long 8-bit stream; the reference appends without limit,
+    cache.py:156-181) is planned on the token-tiled kernel instead of being
+    refused: the workspace query (host only, no launch) gives the token-tiled
+    plan's size, while a call within the row-split kernel's range keeps the
+    row-split plan."""
+    from shard_amd import _lib
+    lib = _lib.load()
+
+    def ws(kernel, n_stream):
+        a = _lib.DecodeArgs()
+        a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim, a.rank, a.n_comp = 1, 32, 8, 128, 192, 8124
+        a.n_sink, a.n_win, a.n_stream, a.kernel = 4, 64, n_stream, kernel
+        return lib.shard_decode_attn_workspace(ctypes.byref(a))
+
+    assert ws(1, 3000) == ws(2, 3000) > 0
+    assert ws(1, 100) != ws(2, 100)
+    assert ws(1, 2048 - 68) != ws(2, 2048 - 68)   # the last count the row-split kernel takes
+    assert ws(1, 2048 - 67) == ws(2, 2048 - 67)

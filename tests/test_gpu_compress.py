@@ -1,19 +1,22 @@
 """The product compression (shard_amd.cache.compress_layer, HIP kernels) against
 the oracle's restatement of the reference's _compress_k / _compress_v /
-_build_gpu_format (oracle.ref.compress_layer, cache.py:338-460) on one
-Llama-3.1-8B-shaped layer: 2048 tokens of the seeded synthetic K/V, one PCA basis
-supplied to both (the reference's svd_lowrank is randomized).
+_build_gpu_format (oracle.ref.compress_layer, cache.py:338-460) and against the
+reference's own output (tests/golden/compress.npz).
 
 What must agree:
   * V: channel scales, k-means centroids (fp16) and VQ indices bit for bit;
     the oracle's k-means uses the reference GPU kernel's nearest-centroid rule
     (direct fp32 sum of squared differences, first index on ties), restated in
     oracle/cref.c.
-  * K: the int4 chain bit for bit given the product's own projection, and the
-    packed codes against the oracle's fp32 projection at a measured agreement
-    rate (the product projects with fp16 MFMA operands and an fp32 sum, the
-    reference in fp32, so a code can flip where the value sits on a rounding
-    boundary).
+  * K: the int4 chain bit for bit given the product's own projection; the
+    packed codes against the fp32 projection of the oracle (and of the
+    reference) with at most 1 in 10^5 differing, every difference a code whose
+    value lies within rounding of a .5 boundary.  The product projects in fp32
+    on MFMA like the reference (cache.py:389-392); only the summation order of
+    the 1024-term dot products differs.
+  * The PCA basis that production takes (fp32 covariance on the GPU, float64
+    eigendecomposition) against a float64 SVD of the same centred rows: its
+    subspace, its variances and the bit allocation they set.
 """
 import numpy as np
 import pytest
@@ -23,9 +26,42 @@ from oracle import cref, ref
 
 pytestmark = pytest.mark.gpu
 
-# Share of int4 codes equal to the fp32-projection oracle's at this config:
-# 0.99955 measured on MI355X; asserted with margin.
-K_CODE_AGREEMENT_FLOOR = 0.999
+# Share of int4 codes equal to the fp32-projection oracle's: at most 1 in 10^5
+# may differ, and each difference must sit on a rounding boundary (below).
+K_CODE_AGREEMENT_FLOOR = 0.99999
+# Distance (in code units) from a .5 rounding boundary within which a code may
+# legitimately differ: the fp32 projections differ by their summation order,
+# about 1e-6 of a row's magnitude, which moves a value by < 1e-3 code units.
+TIE_WINDOW = 2e-3
+
+
+def tie_distances(proj, alloc, chain):
+    """For the oracle's chain of fp32 proj: the distance of each element's
+    stage-1 value (x - lo) / rng * L and stage-2 value y / cs from the nearest
+    .5 boundary (fp64), the two rounding steps of rope.py:108-111 and
+    cache.py:418."""
+    proj = np.asarray(proj, np.float64)
+    lo, rng = chain["lo"].astype(np.float64), chain["rng"].astype(np.float64)
+    L = np.array([(1 << int(b)) - 1 for b in alloc], np.float64)
+    t1 = np.clip((proj - lo) / rng, 0, 1) * L
+    d1 = np.abs(t1 - np.floor(t1) - 0.5)
+    t2 = chain["deq"].astype(np.float64) / chain["coeff_scale"].astype(np.float64)
+    d2 = np.abs(t2 - np.floor(t2) - 0.5)
+    d1[:, L == 0] = np.inf
+    return d1, d2
+
+
+def assert_codes_agree(got_packed, want_chain, want_proj, alloc, n, keep, label):
+    gq = ref.int4_unpack(np.asarray(got_packed), n, keep)
+    wq = want_chain["q"].astype(np.int16)
+    diff = gq != wq
+    agree = 1.0 - float(diff.mean())
+    d1, d2 = tie_distances(want_proj, alloc, want_chain)
+    near = np.minimum(d1, d2)[diff]
+    print(f"[{label}] int4 codes {diff.size}, differing {int(diff.sum())} (agreement {agree:.7f}); "
+          f"their boundary distances {np.sort(near)[:8]}", flush=True)
+    assert agree >= K_CODE_AGREEMENT_FLOOR
+    assert bool(np.all(near < TIE_WINDOW)), near
 
 
 @pytest.fixture(scope="module")
@@ -76,21 +112,125 @@ def test_compress_k_chain_bitexact_given_projection(config1):
 def test_compress_k_codes_agree_with_fp32_projection(config1):
     got, want, dbg = config1
     n, keep = got["k_coeffs_shape"]
-    gq = ref.int4_unpack(got["k_coeffs"].cpu().numpy(), n, keep)
-    wq = ref.int4_unpack(want["k_coeffs"].numpy(), n, keep)
-    agree = float(np.mean(gq == wq))
-    # where they differ, the cause is the first rounding step: the group codes
-    # (2-8 bit levels of each column) differ by one level at most; one level of
-    # a 2-bit column moves the int4 code by several steps
-    g_codes = ref.k_code_chain(dbg["proj"].cpu().numpy(), dbg["alloc"])["codes"].astype(np.int32)
-    w_codes = want["chain"]["codes"].astype(np.int32)
-    code_step = int(np.abs(g_codes - w_codes).max())
     proj_err = float((dbg["proj"].cpu() - want["proj"]).abs().max())
+    scale = float(want["proj"].abs().max())
     mean_ulps = np.abs(got["k_mean_f16"].cpu().view(torch.int16).numpy().astype(np.int32)
                        - want["k_mean_f16"].view(torch.int16).numpy().astype(np.int32)).max()
-    print(f"[compress config1] int4 code agreement {agree:.6f}, group codes "
-          f"{float(np.mean(g_codes == w_codes)):.6f} (max level step {code_step}), "
-          f"max |proj - proj_fp32| {proj_err:.3e}, k_mean max ulp diff {mean_ulps}", flush=True)
-    assert agree >= K_CODE_AGREEMENT_FLOOR
-    assert code_step <= 1
+    print(f"[compress config1] max |proj - proj_fp32| {proj_err:.3e} of max |proj| {scale:.3e}; "
+          f"k_mean max ulp diff {mean_ulps}", flush=True)
+    assert proj_err <= 1e-5 * scale
     assert mean_ulps <= 1
+    assert_codes_agree(got["k_coeffs"].cpu().numpy(), want["chain"], want["proj"].numpy(), want["alloc"],
+                       n, keep, "compress config1")
+
+
+def test_compress_layer_matches_reference_golden(cuda, golden):
+    """The product compress_layer on the reference's own compress.npz inputs
+    (2 batch rows, 2 kv heads, rank 192 with 8/6/2-bit groups), given the
+    fixture's basis: V bit for bit, basis, scales and allocation equal, int4
+    codes as above against the reference's codes."""
+    from shard_amd.cache import Cache, compress_layer
+    g = golden("compress.npz")
+    inv = torch.from_numpy(g["inv_freq"])
+    cache = Cache(head_dim=128, num_layers=1, n_kv_heads=2, device="cuda", rope_inv_freq=inv,
+                  k_target_cr=float(g["k_target_cr"]), max_rank_k=int(g["max_rank"]))
+    k = torch.from_numpy(g["k_full"]).to(cuda)
+    v = torch.from_numpy(g["v_full"]).to(cuda)
+    basis = torch.from_numpy(g["svd_V"][:, :int(g["max_rank"])]).to(cuda)
+    dbg = {}
+    got = compress_layer(cache, k, v, 0, basis=basis, debug=dbg)
+    torch.cuda.synchronize()
+    assert dbg["alloc"] == list(g["alloc"])
+    assert np.array_equal(got["k_basis_q"].cpu().numpy(), g["k_basis_q"])
+    assert np.array_equal(got["k_basis_scale"].cpu().numpy(), g["k_scale"])
+    assert np.array_equal(got["k_basis_f16"].cpu().numpy(), g["k_basis_f16"])
+    mean_ulps = np.abs(got["k_mean_f16"].cpu().numpy().view(np.int16).astype(np.int32)
+                       - g["k_mean"].view(np.int16).astype(np.int32)).max()
+    assert mean_ulps <= 1
+    assert np.array_equal(got["v_centroids_f16"].cpu().numpy(), g["centroids"])
+    assert np.array_equal(got["v_indices"].cpu().numpy().reshape(-1), g["v_packed"])
+    assert np.array_equal(got["v_ch_f16"].cpu().numpy().reshape(-1, 128), g["ch_maxabs"])
+    assert np.array_equal(got["v_indices"][0].cpu().numpy(), g["v_indices_row0"])
+    # the reference's chain of its fp32 projection, restated from the fixture's
+    # group parameters (the oracle reproduces it bit for bit on the CPU)
+    want = ref.compress_layer(torch.from_numpy(g["k_full"]), torch.from_numpy(g["v_full"]), 0, inv,
+                              k_target_cr=float(g["k_target_cr"]), max_rank=int(g["max_rank"]),
+                              svd=(g["svd_S"], g["svd_V"]), assign=cref.vq_assign_direct_t)
+    assert np.array_equal(want["k_coeffs"].numpy(), g["k_coeffs"])
+    n, keep = got["k_coeffs_shape"]
+    assert_codes_agree(got["k_coeffs"].cpu().numpy(), want["chain"], want["proj"].numpy(), want["alloc"],
+                       n, keep, "compress golden")
+
+
+def _centred_rows(k, inv, sink=4, win=64):
+    T = k.shape[2]
+    k_mid = ref.undo_rope(k[:, :, sink:T - win, :].float(), torch.arange(sink, T - win), inv)
+    flat = k_mid.permute(0, 2, 1, 3).reshape(-1, k.shape[1] * k.shape[3])
+    return flat - flat.mean(0)
+
+
+def test_production_pca_basis_matches_exact_svd(cuda):
+    """The basis Cache.compress takes without a supplied one (fp32 covariance
+    of the fp32 centred rows on the GPU, float64 eigh on the host) against the
+    float64 SVD of the same rows on the CPU (the quantities svd_lowrank
+    approximates, cache.py:376-378): principal angles of the top-keep subspace,
+    the variances S^2 / n, and the same dp_bit_allocation."""
+    from shard_amd import bench_data, host, ops
+    from shard_amd.cache import _covariance, pca_basis_cov, _undo_rope_mean
+    k, _ = bench_data.make_kv(2048)
+    inv = bench_data.inv_freq()
+    x = _centred_rows(k, inv).double()
+    n = x.shape[0]
+    _, S, Vh = torch.linalg.svd(x, full_matrices=False)
+    ev_want = (S[:192] ** 2 / n)
+    kd = k.to(cuda)
+    mean = _undo_rope_mean(kd, 4, 2048 - 64, inv)
+    centered = ops.k_prepare(kd, 4, 2048 - 68, inv.to(cuda), mean, out_dtype=torch.float32)
+    basis, ev = pca_basis_cov(_covariance(centered), 192)
+    basis, ev = basis.cpu().double(), ev.cpu().double()
+    rel = float(((ev - ev_want).abs() / ev_want).max())
+    budget = max(64, int(1024 * 16 / 20.0))
+    alloc_got = host.dp_bit_allocation(ev.float(), budget)
+    alloc_want = ref.dp_bit_allocation(ev_want.float(), budget)
+    keep = sum(1 for b in alloc_want if b > 0) & ~1
+    # principal angles between the two top-keep subspaces: singular values of Q1^T Q2
+    cosines = torch.linalg.svdvals(basis[:, :keep].T @ Vh[:keep].T)
+    max_angle = float(torch.arccos(cosines.min().clamp(max=1.0)))
+    print(f"[pca basis] keep {keep}: max rel eigenvalue error {rel:.3e}, "
+          f"max principal angle {max_angle:.3e} rad", flush=True)
+    assert alloc_got == alloc_want
+    assert rel < 1e-4
+    assert max_angle < 1e-2
+
+
+def test_compress_layer_own_basis_vs_oracle_exact_svd(cuda):
+    """compress_layer without a basis (the production path) against the oracle
+    given the exact SVD of the same rows: the same allocation, and keys rebuilt
+    from either side's stored codes equally close to the true centred keys
+    (eigenvector signs and the int8 basis may differ at rounding, so the codes
+    themselves are compared through what they rebuild)."""
+    from shard_amd import bench_data
+    from shard_amd.cache import Cache, compress_layer
+    k, v = bench_data.make_kv(2048)
+    inv = bench_data.inv_freq()
+    x = _centred_rows(k, inv)
+    _, S, Vh = torch.linalg.svd(x.double(), full_matrices=False)
+    cache = Cache(head_dim=128, num_layers=1, n_kv_heads=8, device="cuda", rope_inv_freq=inv)
+    got = compress_layer(cache, k.to(cuda), v.to(cuda), 0)
+    torch.cuda.synchronize()
+    want = ref.compress_layer(k, v, 0, inv, svd=(S.float(), Vh.T.float()), assign=cref.vq_assign_direct_t)
+    assert got["k_alloc"] == want["alloc"]
+
+    def rebuilt(gc, packed):
+        n, keep = gc["k_coeffs_shape"]
+        q = ref.int4_unpack(np.asarray(packed), n, keep).astype(np.float64)
+        cs = np.asarray(gc["k_coeff_scale"].cpu(), np.float64)
+        b = gc["k_basis_q"].cpu().double().numpy() * np.asarray(gc["k_basis_scale"].cpu(), np.float64)
+        return (q * cs) @ b.T
+
+    xt = x.double().numpy()
+    e_got = np.linalg.norm(rebuilt(got, got["k_coeffs"].cpu()) - xt) / np.linalg.norm(xt)
+    e_want = np.linalg.norm(rebuilt(want, want["k_coeffs"]) - xt) / np.linalg.norm(xt)
+    print(f"[own basis] relative key error: product {e_got:.5f}, oracle (exact SVD) {e_want:.5f}",
+          flush=True)
+    assert e_got <= 1.01 * e_want + 1e-4

@@ -127,3 +127,55 @@ def test_decode_graph_greedy_feeds_its_own_tokens(cuda):
     print(f"[graph greedy] {agree} of {steps} steps agree", flush=True)
     assert agree >= 1
     dg.close()
+
+
+def test_decode_graph_keeps_its_workspace_when_another_call_grows_it(cuda):
+    """The captured attention calls write their partial rows into the device's
+    shared decode workspace.  An eager call elsewhere that needs a larger one
+    replaces the shared buffer; the graph still holds the one it captured, so
+    that memory is not handed out again and later replays match eager steps."""
+    from shard import enable_llama_fused_attention
+    from shard_amd import attention
+    from shard_amd.graph import DecodeGraph
+    model = _model(cuda)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(21)
+    ids = torch.randint(0, VOCAB, (1, 300), generator=g).to(cuda)
+    first = torch.randint(0, VOCAB, (1, 1), generator=g).to(cuda)
+    feed = torch.randint(0, VOCAB, (1, 6), generator=g).to(cuda)
+    cache_e = _prefilled(model, ids, first, False)
+    cache_g = _prefilled(model, ids, first, False)
+    want = []
+    with torch.no_grad():
+        for s in range(feed.shape[1]):
+            want.append(model(feed[:, s:s + 1], past_key_values=cache_e, use_cache=True).logits[:, -1].float())
+    dg = DecodeGraph(model, cache_g, feed[:, :1], max_steps=feed.shape[1])
+    key = (cuda.type, cuda.index if cuda.index is not None else torch.cuda.current_device())
+    for s in range(feed.shape[1]):
+        if s == 3:  # captured at step 1, replayed at step 2
+            old = attention._workspaces[key]
+            old_ptr, old_n = old.data_ptr(), old.numel()
+            del old
+            attention._workspace(cuda, 4 * old_n)      # another call grows the shared buffer
+            assert attention._workspaces[key].data_ptr() != old_ptr
+            junk = torch.full((old_n,), 0x7F, dtype=torch.uint8, device=cuda)
+            assert junk.data_ptr() != old_ptr, "the captured workspace was freed and reused"
+        dg.step(feed[:, s:s + 1])
+        _compare(dg.logits.float(), want[s], f"[graph workspace] step {s}")
+    dg.close()
+
+
+def test_decode_graph_refuses_reorder_while_open(cuda):
+    from shard import enable_llama_fused_attention
+    from shard_amd.graph import DecodeGraph
+    model = _model(cuda)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(22)
+    ids = torch.randint(0, VOCAB, (2, 300), generator=g).to(cuda)
+    first = torch.randint(0, VOCAB, (2, 1), generator=g).to(cuda)
+    cache = _prefilled(model, ids, first, False)
+    dg = DecodeGraph(model, cache, first, max_steps=3)
+    with pytest.raises(RuntimeError):
+        cache.reorder_cache(torch.tensor([1, 0], device=cuda))
+    dg.close()
+    cache.reorder_cache(torch.tensor([1, 0], device=cuda))

@@ -273,6 +273,43 @@ def test_pca_project_mfma(cuda, m, k, n):
     assert float(((got - want).abs() / scale).max()) < 1e-5
 
 
+@pytest.mark.parametrize("m,k,n", [(1980, 1024, 192), (4099, 1024, 64), (257, 512, 256), (31, 40, 32),
+                                   (130, 1024, 96)])
+def test_pca_project_f32_mfma(cuda, m, k, n):
+    """The fp32 projection (Cache.compress's GEMM) within fp32 summation error
+    of the float64 product, including row tails, k past the last 32-chunk and
+    column counts that leave a wave half idle."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(m + n)
+    a = torch.randn(m, k, generator=g)
+    bt = torch.randn(n, k, generator=g) * 0.05
+    got = ops.pca_project_f32(a.to(cuda), bt.to(cuda)).cpu().double()
+    want = a.double() @ bt.double().T
+    scale = a.double().abs() @ bt.double().abs().T
+    err = float(((got - want).abs() / scale).max())
+    print(f"pca_project_f32 m={m} k={k} n={n}: max rel err {err:.3e}", flush=True)
+    assert err < 4e-7 * (k / 1024) ** 0.5 * 8
+
+
+def test_k_prepare_f32(cuda):
+    """The fp32 centred rows of (flat - mean) (cache.py:370-392): undo RoPE
+    with fp32 phases, the mean subtracted in fp32, no fp16 rounding."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(3)
+    B, G, T, D, start, n_comp = 2, 8, 200, 128, 4, 132
+    k = torch.randn(B, G, T, D, generator=g).half()
+    inv = ref.default_inv_freq(500000.0, D)
+    pos = torch.arange(start, start + n_comp)
+    un = ref.undo_rope(k[:, :, start:start + n_comp].float(), pos, inv)
+    flat = un.permute(0, 2, 1, 3).reshape(B * n_comp, G * D)
+    mean = flat.mean(0)
+    want = flat - mean
+    got = ops.k_prepare(k.to(cuda), start, n_comp, inv.to(cuda), mean.to(cuda),
+                        out_dtype=torch.float32).cpu()
+    # sin/cos may differ by an ulp from torch's CPU ones
+    assert float((got - want).abs().max()) <= 4e-7 * float(want.abs().max())
+
+
 def test_k_prepare(cuda):
     ops = _ops()
     g = torch.Generator().manual_seed(2)

@@ -235,3 +235,23 @@ def test_bench_roofline_picks_the_binding_roof():
     low = bench.roofline(1e9, 1e8, 100.0)  # 10 flop/B: HBM-bound
     assert low["bound"] == "hbm" and low["unit"] == "GB/s" and low["achieved"] == 1000.0
     assert low["mfma"]["unit"] == "TFLOP/s"
+
+
+def test_decode_graph_refuses_a_masked_cache_and_reorder_under_a_graph():
+    """A decode graph replays without an attention mask: it refuses a cache
+    whose last eager decode step attended with a padding mask.  While a graph
+    is open, reorder_cache (which replaces tensors the graph captured) raises."""
+    import torch
+    from shard_amd.cache import Cache
+    from shard_amd.graph import DecodeGraph
+    cache = Cache(head_dim=128, num_layers=2, n_kv_heads=8, device="cpu")
+    cache._compressed, cache._streaming = True, True
+    cache._last_attn_mask = torch.tensor([[0.0, float("-inf"), 0.0]])
+    with pytest.raises(ValueError, match="padding mask"):
+        DecodeGraph(None, cache, torch.zeros(1, 1, dtype=torch.long), 3)
+    cache._last_attn_mask = torch.zeros(1, 3)
+    with pytest.raises(ValueError, match="on the GPU"):
+        DecodeGraph(None, cache, torch.zeros(1, 1, dtype=torch.long), 3)
+    cache._graph = object()
+    with pytest.raises(RuntimeError, match="decode graph"):
+        cache.reorder_cache(torch.tensor([0]))
