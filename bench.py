@@ -99,6 +99,22 @@ def build_layer(T, dev, seed=0, n_stream=0, with_layer=False):
     return fmt, k, v
 
 
+def compress_ratios(fmt, T=None):
+    """Storage ratios of one compressed layer as the reference computes them
+    (cache.py:511-539, one layer here): fp16 K+V bytes of the context over the
+    stored bytes.  ``clean_compress_ratio`` counts one batch row of fp16 (the
+    reference's numerator); README.md:15-16 quote 10.0x at 8K and 11.2x at 32K
+    for Llama-3.1-8B on the reference."""
+    from shard_amd import Cache
+    c = Cache(num_layers=1, n_kv_heads=fmt["n_kv"], head_dim=fmt["head_dim"])
+    c.layers[0]._gpu_compressed = fmt
+    c._compressed = True
+    return {"clean_compress_ratio": round(c.clean_compress_ratio(), 3),
+            "clean_compress_ratio_all_rows": round(c.clean_compress_ratio_all_rows(), 3),
+            "compress_ratio": round(c.compress_ratio(), 3),
+            "reference_published": {8192: 10.0, 32768: 11.2}.get(T)}
+
+
 def build_layer_batch(T, batch, dev, seed=0):
     """A compressed layer of `batch` rows of T tokens (K/V generated on the device)."""
     from shard_amd import Cache, bench_data
@@ -121,13 +137,26 @@ def warm_replays(g, seconds=0.5):
         torch.cuda.synchronize()
 
 
+MIN_REPLAYS = 10  # timed graph replays per figure, whatever --steps is (median, p10, p90)
+
+
+def spread(per_call_us):
+    """median / p10 / p90 / mean of per-replay per-call times (us)."""
+    xs = sorted(per_call_us)
+    q = lambda f: xs[min(len(xs) - 1, max(0, int(round(f * (len(xs) - 1)))))]
+    return {"median": q(0.5), "p10": q(0.1), "p90": q(0.9), "mean": sum(xs) / len(xs),
+            "replays": len(xs)}
+
+
 def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, graph_len=100,
                 kernel=0):
     """Per-call time of shard_decode_attn, rotating over n_copies of the layer.
 
     The calls are captured in a HIP graph (graph_len calls per graph, each call
-    on the next copy) and the graph is replayed, so the host's per-launch cost
-    is not part of the measurement.  Returns (us rotated, us hot, us eager)."""
+    on the next copy) and the graph is replayed max(10, steps / graph_len)
+    times, each replay between its own pair of HIP events, so the host's
+    per-launch cost is not part of the measurement.  Returns (rotated spread,
+    hot spread, us eager); a spread is spread()'s dict of per-call times."""
     from shard_amd import ops
     copies = [fmt] + [clone_format(fmt) for _ in range(n_copies - 1)]
     calls = [ops.make_decode_args(q, c, pos_q, None, n_splits=n_splits, stream_n=stream_n)
@@ -164,17 +193,19 @@ def time_decode(fmt, q, pos_q, steps, warmup, n_copies, n_splits=0, stream_n=0, 
         torch.cuda.synchronize()
         return g
 
-    reps = max(1, steps // graph_len)
+    reps = max(MIN_REPLAYS, math.ceil(steps / graph_len))
     res = []
     for idx_fn in (lambda i: i % n_copies, lambda i: 0):
         g = graph_of(idx_fn)
         warm_replays(g)
-        e0.record(st)
-        for _ in range(reps):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps)]
+        for a, b in evs:
+            a.record(st)
             g.replay()
-        e1.record(st)
+            b.record(st)
         torch.cuda.synchronize()
-        res.append(e0.elapsed_time(e1) * 1000.0 / (reps * graph_len))
+        res.append(spread([a.elapsed_time(b) * 1000.0 / graph_len for a, b in evs]))
         del g
     return res[0], res[1], us_eager
 
@@ -351,6 +382,34 @@ def stream_curve(dev, T=32768, n_stream=512, reps=10):
             "timing": f"HIP events around {reps} eager calls per stream length"}
 
 
+def stream_points(dev, steps, warmup, T=32768, n_stream=512, pts=(1, 128, 256, 512)):
+    """BASELINE config 3 in the default line: a 32K compressed context with a
+    512-token 8-bit Lloyd-Max stream appended token by token (the layer's own
+    quantizer), then the decode call attending the first s stream tokens timed
+    like the headline (graph replay over rotated copies, median of >= 10
+    replays) at s in pts; the slope is per stream token between the ends."""
+    from shard_amd import bench_data
+    fmt, _, _, _ = build_layer(T, dev, n_stream=n_stream, with_layer=True)
+    q = bench_data.make_q().to(dev).view(1, 32, 128)
+    n, rank = fmt["n_compress"], fmt["rank_pad"]
+    nbytes = algorithmic_bytes(n, rank, n_stream=n_stream)
+    n_copies = max(2, math.ceil(2 * 256e6 / nbytes))
+    points = []
+    for sn in pts:
+        rot, _, _ = time_decode(fmt, q, T + sn - 1, steps, warmup, n_copies, stream_n=sn)
+        points.append({"stream_tokens": sn, "us": round(rot["median"], 3),
+                       "us_p10": round(rot["p10"], 3), "us_p90": round(rot["p90"], 3),
+                       "achieved_hbm_gbs": round(algorithmic_bytes(n, rank, n_stream=sn)
+                                                 / (rot["median"] * 1e-6) / 1e9, 1)})
+    slope = (points[-1]["us"] - points[0]["us"]) / (pts[-1] - pts[0])
+    del fmt
+    torch.cuda.empty_cache()
+    return {"metric": "decode attn us/layer-step vs 8-bit stream length (BASELINE config 3)",
+            "context": T, "n_comp": n, "points": points,
+            "slope_ns_per_stream_token": round(slope * 1000.0, 2),
+            "timing": "graph replay over rotated copies, median of >= 10 replays of 100 calls"}
+
+
 def prefill(dev, layers=32, batch=4, T=8192):
     """Prefill compression kernels over `layers` x batch x T tokens of
     synthetic K (low-rank Gaussian, RoPE'd) and V.  Per layer: undo-RoPE into
@@ -472,6 +531,101 @@ def pmc_workload(dev, T, calls=200, layer_path=None, batch=1):
     torch.cuda.synchronize()
     return {"pmc_workload": {"context": T, "batch": batch, "calls": calls, "copies": n_copies,
                              "algorithmic_bytes_per_call": nbytes}}
+
+
+def splitk_fp16_cache(n_layers, cap):
+    """A bench-only fp16 KV cache with preallocated (B, G, cap, D) buffers per
+    layer (no per-step concatenation), for the second fp16 baseline of the e2e
+    run, whose decode attention is shard_bench_fp16_decode over the buffers'
+    first rows.  Layer glue as shard_amd.cache.CacheLayer's."""
+    from transformers.cache_utils import Cache as HFCache, CacheLayerMixin
+
+    class Layer(CacheLayerMixin):
+        is_sliding = False
+        is_compileable = False
+
+        cap_rows = cap
+
+        def __init__(self):
+            self.k = self.v = None
+            self.n = 0
+            self.is_initialized = False
+
+        def update(self, key_states, value_states, *args, **kwargs):
+            B, G, t, D = key_states.shape
+            if self.k is None:
+                self.k = torch.empty(B, G, cap, D, dtype=key_states.dtype, device=key_states.device)
+                self.v = torch.empty_like(self.k)
+            if self.n + t > cap:
+                raise RuntimeError("splitk_fp16_cache: capacity exceeded")
+            self.k[:, :, self.n:self.n + t] = key_states
+            self.v[:, :, self.n:self.n + t] = value_states
+            self.n += t
+            self.is_initialized = True
+            return self.k[:, :, :self.n], self.v[:, :, :self.n]
+
+        def get_seq_length(self):
+            return self.n
+
+        def get_max_length(self):
+            return -1
+
+        def get_max_cache_shape(self):
+            return None
+
+        def get_mask_sizes(self, query_length, *args, **kwargs):
+            return self.n + query_length, 0
+
+        def lazy_initialization(self, *args, **kwargs):
+            pass
+
+    class SplitKCache(HFCache):
+        def __init__(self):
+            super().__init__(layers=[Layer() for _ in range(n_layers)])
+
+    return SplitKCache()
+
+
+class splitk_attention:
+    """Context manager: Llama decode steps (q_len 1) over a splitk_fp16_cache run
+    q/k/v projections, transformers' RoPE, the cache append and
+    shard_bench_fp16_decode; everything else calls the forward installed
+    before (the shard patch)."""
+
+    def __enter__(self):
+        from transformers.models.llama.modeling_llama import LlamaAttention, apply_rotary_pos_emb
+        from shard_amd import ops
+        self.cls, prev = LlamaAttention, LlamaAttention.forward
+        self.prev = prev
+        ws = {}
+
+        def forward(attn, hidden_states, *args, **kwargs):
+            pkv = kwargs.get("past_key_values")
+            layers = getattr(pkv, "layers", None)
+            if (hidden_states.shape[1] != 1 or not layers
+                    or not hasattr(layers[attn.layer_idx], "cap_rows")):
+                return prev(attn, hidden_states, *args, **kwargs)
+            B = hidden_states.shape[0]
+            shape = (B, 1, -1, attn.head_dim)
+            q = attn.q_proj(hidden_states).view(shape).transpose(1, 2)
+            k = attn.k_proj(hidden_states).view(shape).transpose(1, 2)
+            v = attn.v_proj(hidden_states).view(shape).transpose(1, 2)
+            cos, sin = kwargs["position_embeddings"]
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            layer = layers[attn.layer_idx]
+            layer.update(k, v)
+            qq = q.reshape(B, -1, attn.head_dim).contiguous()
+            if "ws" not in ws:
+                ws["ws"] = torch.empty(64 << 20, dtype=torch.uint8, device=qq.device)
+            out = ops.bench_fp16_decode(qq, layer.k, layer.v, ws=ws["ws"], seq=layer.n)
+            return attn.o_proj(out.view(B, 1, -1)), None
+
+        LlamaAttention.forward = forward
+        return self
+
+    def __exit__(self, *exc):
+        self.cls.forward = self.prev
+        return False
 
 
 def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
@@ -597,14 +751,19 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
     progress("warm-up done")
     res = {}
     fp16_toks = fp16_logits = None
-    for kind in ("fp16", "shard"):
+    for kind in ("fp16", "fp16_splitk", "shard"):
         torch.cuda.empty_cache()
         torch.cuda.reset_peak_memory_stats()
         if kind == "fp16":
             cache = DynamicCache()
+        elif kind == "fp16_splitk":
+            cache = splitk_fp16_cache(layers, prompt + new_tokens + 4)
         else:
             cache = Cache.from_model(model)
             cache._streaming = True
+        patch = splitk_attention() if kind == "fp16_splitk" else None
+        if patch is not None:
+            patch.__enter__()
         t0 = sync_time()
         with torch.no_grad():
             out = model(ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
@@ -627,13 +786,15 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
         else:
             dt, toks, _, stats = decode(cache, first, new_tokens, forced=fp16_toks, ref_logits=fp16_logits)
             r.update(stats)
+        if patch is not None:
+            patch.__exit__(None, None, None)
         r["decode_s"] = round(dt, 3)
         r["tokens_per_s"] = round(batch * new_tokens / dt, 1)
         r["ms_per_step"] = round(dt / new_tokens * 1000.0, 3)
         # the kept logits are not part of either cache's footprint: the fp16 run's
         # (alive during both decodes) and, in the shard run, its own (same size)
         kept = sum(x.numel() * x.element_size() for x in fp16_logits) / 1e9
-        if kind == "shard":
+        if kind != "fp16":
             kept *= 2
         r["peak_decode_gb"] = round(torch.cuda.max_memory_allocated() / 1e9 - kept, 2)
         progress(f"{kind}: decode {r['decode_s']} s, {r['tokens_per_s']} tokens/s")
@@ -651,11 +812,16 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
     return {"metric": "e2e decode tokens/s, shard cache vs fp16 cache (BASELINE config 5)",
             "unit": "tokens/s", "value": res["shard"]["tokens_per_s"],
             "vs_fp16_cache": round(res["shard"]["tokens_per_s"] / res["fp16"]["tokens_per_s"], 3),
+            "vs_fp16_splitk_cache": round(res["shard"]["tokens_per_s"]
+                                          / res["fp16_splitk"]["tokens_per_s"], 3),
+            "fp16_splitk_how": ("fp16 K/V in preallocated per-layer buffers, decode attention by "
+                                "shard_bench_fp16_decode (split-K GQA FlashDecoding-style HIP "
+                                "kernel) through a bench-only patched forward"),
             "graph_tokens_per_s": res["shard"]["graph"].get("tokens_per_s"),
             "config": {"model": "Llama-3.1-8B architecture, random init, fp16", "layers": layers,
                        "batch": batch, "prompt": prompt, "new_tokens": new_tokens,
                        "data": "random token ids (seeded)"},
-            "shard": res["shard"], "fp16": res["fp16"],
+            "shard": res["shard"], "fp16": res["fp16"], "fp16_splitk": res["fp16_splitk"],
             "note": ("teacher-forced agreement with the fp16 cache is low by construction with "
                      "random weights: keys are full-rank (the rank-limited PCA keeps a fraction of "
                      "their energy), V is Gaussian (2 bits per value after VQ) and attention "
@@ -676,6 +842,10 @@ def main():
                     help="skip the batch-16 x 16K layer (config 5's decode shape)")
     ap.add_argument("--no-e2e", dest="with_e2e", action="store_false", default=True,
                     help="skip the config-5 end-to-end run in the default line")
+    ap.add_argument("--no-stream", dest="with_stream", action="store_false", default=True,
+                    help="skip config 3's stream points in the default line")
+    ap.add_argument("--no-prefill", dest="with_prefill", action="store_false", default=True,
+                    help="skip config 4's prefill compression in the default line")
     ap.add_argument("--n-splits", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0,
                     help="decode split kernel: 0 automatic, 1 row-split, 2 token-tiled")
@@ -745,11 +915,12 @@ def main():
         q = bench_data.make_q(batch).to(dev).view(batch, 32, 128)
         nbytes = algorithmic_bytes(n, rank, batch=batch)
         n_copies = max(2, math.ceil(2 * 256e6 / nbytes))
-        us, us_hot, us_eager = time_decode(fmt, q, T, args.steps, args.warmup, n_copies,
-                                           args.n_splits, kernel=args.kernel)
-        res = {"T": T, "batch": batch, "n_comp": n, "rank": fmt["rank"], "us": us,
-               "us_hot": us_hot, "us_eager": us_eager, "bytes": nbytes,
-               "flops": algorithmic_flops(n, rank, batch=batch), "copies": n_copies}
+        rot, hot, us_eager = time_decode(fmt, q, T, args.steps, args.warmup, n_copies,
+                                         args.n_splits, kernel=args.kernel)
+        res = {"T": T, "batch": batch, "n_comp": n, "rank": fmt["rank"], "us": rot["median"],
+               "spread": rot, "us_hot": hot["median"], "us_eager": us_eager, "bytes": nbytes,
+               "flops": algorithmic_flops(n, rank, batch=batch), "copies": n_copies,
+               "compress_ratio": compress_ratios(fmt, T if batch == 1 else None)}
         kd, vd = k.to(dev), v.to(dev)
         if "fp16" in baselines:
             res["fp16_us"], res["fp16_bytes"] = time_fp16_decode(kd, vd, q, args.steps, args.warmup)
@@ -769,7 +940,10 @@ def main():
 
     def summary(r):
         g = r["bytes"] / (r["us"] * 1e-6) / 1e9
-        d = {"us": round(r["us"], 3), "us_hot": round(r["us_hot"], 3),
+        sp = r["spread"]
+        d = {"us": round(r["us"], 3), "us_p10": round(sp["p10"], 3), "us_p90": round(sp["p90"], 3),
+             "us_mean": round(sp["mean"], 3), "timed_calls": sp["replays"] * 100,
+             "us_hot": round(r["us_hot"], 3),
              "us_eager_python_launch": round(r["us_eager"], 3),
              "achieved_hbm_gbs": round(g, 1), "frac": round(g / HBM_PEAK_GBS, 4),
              "algorithmic_bytes": r["bytes"],
@@ -782,6 +956,7 @@ def main():
         if "sdpa_us" in r:
             d["fp16_sdpa_us"] = round(r["sdpa_us"], 3)
             d["speedup_vs_fp16_sdpa"] = round(r["sdpa_us"] / r["us"], 3)
+        d["compress_ratio"] = r["compress_ratio"]
         return d
 
     r8 = measure(args.ctx, baselines=("fp16", "sdpa"))
@@ -807,6 +982,11 @@ def main():
                                f"(BASELINE config 2)",
                    "n_comp": r8["n_comp"], "rank": r8["rank"], "sink": 4, "window": 64,
                    "rotated_copies": r8["copies"]},
+        "timed_calls": s8["timed_calls"],
+        "spread_us": {"median": s8["us"], "p10": s8["us_p10"], "p90": s8["us_p90"],
+                      "mean": s8["us_mean"],
+                      "how": "per-call time of each of >= 10 timed replays of a 100-call graph"},
+        "compress_ratio": s8["compress_ratio"],
         "achieved_hbm_gbs": round(gbs, 1),
         "us_hot": s8["us_hot"],
         "us_eager_python_launch": s8["us_eager_python_launch"],
@@ -833,6 +1013,17 @@ def main():
         out["batch16_16k_layer"] = summary(rb16)
         out["batch16_16k_layer"]["workload"] = ("one layer of BASELINE config 5's decode step: "
                                                 "batch 16 x 16384-token compressed context")
+    if args.with_stream:
+        try:
+            out["stream_curve"] = stream_points(dev, args.steps, args.warmup)
+        except Exception as e:  # reported, never replaces the decode number
+            out["stream_curve"] = {"error": repr(e)}
+    if args.with_prefill:
+        try:
+            out["prefill"] = prefill(dev)
+        except Exception as e:
+            out["prefill"] = {"error": repr(e)}
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         try:
             qc = bench_data.make_q().view(1, 32, 128)

@@ -20,6 +20,13 @@ int shard_bench_fp16_decode(const uint16_t* q, const uint16_t* k, const uint16_t
                             int32_t batch, int32_t n_kv_heads, int32_t seq, int32_t n_splits,
                             uint16_t* out, void* workspace, size_t workspace_bytes,
                             void* stream);
+/* The same over k / v buffers holding head_rows >= seq rows per (batch row,
+ * kv head), of which the first seq are attended: k (B, G, head_rows, 128), as
+ * a preallocated fp16 cache keeps them between decode steps. */
+int shard_bench_fp16_decode_ld(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               int32_t batch, int32_t n_kv_heads, int32_t seq, int64_t head_rows,
+                               int32_t n_splits, uint16_t* out, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -75,6 +75,7 @@ SIGNATURES = [
     # benchmark-only baseline (include/shard_bench.h)
     ("shard_bench_fp16_decode_workspace", c_size_t, [c_int32, c_int32, c_int32]),
     ("shard_bench_fp16_decode", c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]),
+    ("shard_bench_fp16_decode_ld", c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("shard_kv_reconstruct", c_int32, [ctypes.POINTER(DecodeArgs), c_void_p, c_void_p, c_void_p]),
     ("shard_stream_dequant", c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_stream_quant_qjl", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -28,6 +28,7 @@ constexpr float kFdLog2e = 1.4426950408889634f;
 
 struct Fp16Params {
   int32_t B, G, T, n_splits, chunk;
+  int64_t ld;  // rows between consecutive (batch row, kv head) heads in k / v (>= T)
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
@@ -50,8 +51,8 @@ void k_fp16_split(const Fp16Params p) {
   const int t_end = min(t_begin + p.chunk, p.T);
   const int n_tiles = t_end > t_begin ? (t_end - t_begin + 31) / 32 : 0;
 
-  const uint16_t* kh = p.k + ((int64_t)b * p.G + g) * p.T * kFdHD;
-  const uint16_t* vh = p.v + ((int64_t)b * p.G + g) * p.T * kFdHD;
+  const uint16_t* kh = p.k + ((int64_t)b * p.G + g) * p.ld * kFdHD;
+  const uint16_t* vh = p.v + ((int64_t)b * p.G + g) * p.ld * kFdHD;
 
   // A operand: q rows 0-3 (query heads), k-step s covers dims 16 s .. 16 s + 15
   const int col = lane & 31, hh = lane >> 5;
@@ -206,18 +207,19 @@ size_t shard_bench_fp16_decode_workspace(int32_t batch, int32_t n_kv_heads, int3
   return (size_t)batch * n_kv_heads * kFdGQA * n_splits * (kFdHD + 2) * sizeof(float);
 }
 
-int shard_bench_fp16_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, int32_t batch,
-                            int32_t n_kv_heads, int32_t seq, int32_t n_splits, uint16_t* out,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+int shard_bench_fp16_decode_ld(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               int32_t batch, int32_t n_kv_heads, int32_t seq, int64_t head_rows,
+                               int32_t n_splits, uint16_t* out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !out || !workspace || batch <= 0 || n_kv_heads <= 0 || seq <= 0 ||
-      n_splits <= 0)
+      n_splits <= 0 || head_rows < seq)
     return SHARD_ERR_ARG;
   if (((uintptr_t)q & 15) || ((uintptr_t)k & 15) || ((uintptr_t)v & 15) || ((uintptr_t)out & 3))
     return SHARD_ERR_ARG;
   if (workspace_bytes < shard_bench_fp16_decode_workspace(batch, n_kv_heads, n_splits))
     return SHARD_ERR_WORKSPACE;
   Fp16Params p;
-  p.B = batch; p.G = n_kv_heads; p.T = seq; p.n_splits = n_splits;
+  p.B = batch; p.G = n_kv_heads; p.T = seq; p.n_splits = n_splits; p.ld = head_rows;
   p.chunk = ((seq + n_splits - 1) / n_splits + 31) / 32 * 32;
   const int64_t nm = (int64_t)batch * n_kv_heads * kFdGQA * n_splits;
   float* ws = (float*)workspace;
@@ -233,6 +235,13 @@ int shard_bench_fp16_decode(const uint16_t* q, const uint16_t* k, const uint16_t
   launch_partial_merge(mp, batch, s);
   SHARD_LAUNCH_CHECK("shard_bench_fp16_decode merge");
   return SHARD_OK;
+}
+
+int shard_bench_fp16_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, int32_t batch,
+                            int32_t n_kv_heads, int32_t seq, int32_t n_splits, uint16_t* out,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  return shard_bench_fp16_decode_ld(q, k, v, batch, n_kv_heads, seq, seq, n_splits, out, workspace,
+                                    workspace_bytes, stream);
 }
 
 }  // extern "C"

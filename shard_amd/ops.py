@@ -574,16 +574,20 @@ def decode_attn_noalloc(call: DecodeCall) -> torch.Tensor:
     return call.out
 
 
-def bench_fp16_decode(q, k, v, n_splits=0, out=None, ws=None):
+def bench_fp16_decode(q, k, v, n_splits=0, out=None, ws=None, seq=None):
     """The benchmark's same-GPU baseline: fp16 split-K GQA decode attention over
     uncompressed K/V (shard_bench_fp16_decode).  q (B, H, 128) with H = 4 G,
-    k / v (B, G, T, 128) fp16 contiguous; n_splits 0 = two workgroups per CU."""
+    k / v (B, G, T, 128) fp16 contiguous; n_splits 0 = two workgroups per CU.
+    seq < T attends the first seq rows of each head (a preallocated cache)."""
     _require_gpu(q)
     lib = _lib.load()
     B, H, D = q.shape
-    G, T = k.shape[1], k.shape[2]
-    if D != 128 or H != 4 * G or tuple(k.shape) != (B, G, T, D) or k.shape != v.shape:
+    G, rows = k.shape[1], k.shape[2]
+    T = rows if seq is None else int(seq)
+    if D != 128 or H != 4 * G or tuple(k.shape) != (B, G, rows, D) or k.shape != v.shape:
         raise ValueError("bench_fp16_decode: q (B, 4G, 128), k/v (B, G, T, 128)")
+    if not 0 < T <= rows:
+        raise ValueError("bench_fp16_decode: seq must be in 1..T")
     for t in (q, k, v):
         if t.dtype != torch.float16 or not t.is_contiguous():
             raise ValueError("bench_fp16_decode takes contiguous fp16 tensors")
@@ -595,8 +599,8 @@ def bench_fp16_decode(q, k, v, n_splits=0, out=None, ws=None):
     need = lib.shard_bench_fp16_decode_workspace(B, G, n_splits)
     if ws is None or ws.numel() < need:
         ws = torch.empty(need, dtype=torch.uint8, device=q.device)
-    _lib.check("shard_bench_fp16_decode", lib.shard_bench_fp16_decode(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), B, G, T, n_splits, out.data_ptr(),
+    _lib.check("shard_bench_fp16_decode", lib.shard_bench_fp16_decode_ld(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), B, G, T, rows, n_splits, out.data_ptr(),
         ws.data_ptr(), ws.numel(), _stream(q)))
     return out
 

@@ -42,3 +42,23 @@ def test_fp16_baseline_matches_fp64(cuda, B, G, T, n_splits):
     err, cos = compare(got.cpu().float().numpy(), want)
     print(f"[fp16 baseline] max_abs={err:.3e} cos={cos:.7f}", flush=True)
     assert err <= 2e-3 and cos >= 0.9999
+
+
+@pytest.mark.parametrize("B,G,T,rows", [(2, 8, 700, 1024), (16, 8, 257, 300)])
+def test_fp16_baseline_over_a_preallocated_cache(cuda, B, G, T, rows):
+    """shard_bench_fp16_decode_ld: the first T of `rows` rows per head (the
+    e2e fp16 baseline's preallocated cache); rows past T hold NaN and must not
+    reach the result."""
+    from shard_amd import ops
+    g = torch.Generator().manual_seed(T)
+    q = torch.randn(B, 4 * G, 128, generator=g).half()
+    k = torch.full((B, G, rows, 128), float("nan")).half()
+    v = torch.full((B, G, rows, 128), float("nan")).half()
+    k[:, :, :T] = (torch.randn(B, G, T, 128, generator=g) * 1.5).half()
+    v[:, :, :T] = torch.randn(B, G, T, 128, generator=g).half()
+    got = ops.bench_fp16_decode(q.to(cuda), k.to(cuda), v.to(cuda), seq=T)
+    torch.cuda.synchronize()
+    want = _fp64_attention(q, k[:, :, :T].contiguous(), v[:, :, :T].contiguous())
+    err, cos = compare(got.cpu().float().numpy(), want)
+    print(f"[fp16 baseline ld] B={B} T={T} rows={rows}: max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= 2e-3 and cos >= 0.9999
