@@ -129,7 +129,9 @@ int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
 /* Nearest-centroid assignment: idx[i] = argmin_k sum_j (x[i,j] - c[k,j])^2 with
  * the squared differences summed in fp32 in j order without FMA, first index
  * on ties.  d <= 8, k <= 1024.  Replaces vq_assign, triton_kernels.py:689-746
- * (whose CPU fallback is cdist(...).argmin, triton_kernels.py:733-734). */
+ * (whose CPU fallback is cdist(...).argmin, triton_kernels.py:733-734).  The
+ * unfused sum is this library's reading of the kernel's `dist += diff * diff`,
+ * which Triton's default fp fusion may contract into an FMA. */
 int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids,
                     int32_t k, int32_t* idx, void* stream);
 

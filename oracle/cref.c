@@ -2,12 +2,15 @@
  * cpu_baseline leg load this through oracle/cref.py; the product never does).
  *
  * vq_assign_direct: the nearest-centroid rule of the reference's assignment
- * kernel (triton_kernels.py:703-725): for each row, the squared distance to
- * centroid k is summed over dims 0..d-1 in order as fp32 (difference, square,
- * add: three roundings, no fused multiply-add), and the first centroid with
- * the strictly smallest distance wins.  It restates oracle/ref.py's numpy
- * vq_assign_direct row by row; built with -ffp-contract=off so the compiler
- * keeps the three roundings.  Rows are independent, so the OpenMP split over
+ * kernel's statement (triton_kernels.py:703-725), uncontracted: for each row,
+ * the squared distance to centroid k is summed over dims 0..d-1 in order as
+ * fp32 (difference, square, add: three roundings, no fused multiply-add), and
+ * the first centroid with the strictly smallest distance wins.  Leaving the
+ * multiply-add unfused is this project's choice: Triton's default fp fusion
+ * may compile the kernel's `dist += diff * diff` to an FMA, which can pick
+ * another centroid on exact near-ties; that form is not restated here.
+ * It restates oracle/ref.py's numpy vq_assign_direct row by row; built with
+ * -ffp-contract=off so the compiler keeps the three roundings.  Rows are independent, so the OpenMP split over
  * rows does not change any result.
  */
 #include <math.h>

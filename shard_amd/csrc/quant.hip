@@ -440,7 +440,8 @@ __global__ void k_vq_assign(const float* __restrict__ x, int64_t n,
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// the reference's distance: fp32 sum of squared differences in dim order
+// the direct distance of the reference kernel's statement, uncontracted (this
+// library's rule: no FMA): fp32 sum of squared differences in dim order
 __device__ __forceinline__ float vq_dist4(const float (&xv)[4], const float4 cv) {
   const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
   float dist = 0.f;
