@@ -432,7 +432,38 @@ def test_prefill_kernels_at_config4_layer_size(cuda):
     ch = rot.abs().amax(dim=1).clamp(min=1e-8)
     assert np.array_equal(ch32.cpu().numpy(), ch.numpy())
     assert np.array_equal(x.cpu().numpy(), (rot / ch.unsqueeze(1)).reshape(-1, 4).numpy())
-    del x, rot
+    del rot
+    # the layer's nearest-centroid stage at full size: its 8.4M subvectors
+    # against a seeded codebook drawn from them, bit-exact with the C oracle
+    from oracle import cref
+    if cref.load() is None:
+        cref.build()
+    gsel = torch.Generator().manual_seed(42)
+    xc = x.cpu()
+    codebook = xc[torch.randperm(xc.shape[0], generator=gsel)[:256]].contiguous()
+    print(f"[config4 layer] vq_assign on {xc.shape[0]} subvectors", flush=True)
+    idx = ops.vq_assign(x, codebook.to(cuda)).cpu().numpy().astype(np.int64)
+    want_idx = cref.vq_assign_direct(xc.numpy(), codebook.numpy())
+    assert np.array_equal(idx, want_idx), int((idx != want_idx).sum())
+    del x, xc
+
+    # the K front end at full size: undo RoPE and centring into the fp16 operand
+    kk = (torch.randn(B, G, T, D, generator=g) * 2).half()
+    inv = ref.default_inv_freq(500000.0, D)
+    un = ref.undo_rope(kk.float(), torch.arange(T), inv).permute(0, 2, 1, 3).reshape(B * T, G * D)
+    mean = un.mean(0)
+    want_kp = (un - mean).half().float()
+    kp = ops.k_prepare(kk.to(cuda), 0, T, inv.to(cuda), mean.to(cuda)).cpu().float()
+    # sin/cos of phases up to 8191 rad may differ by a few fp32 ulps from torch's
+    # CPU ones: |k| <= 12 gives an fp32 difference below 1e-5 before the fp16
+    # rounding, so the operands agree to one fp16 ulp plus that
+    ulp = torch.where(want_kp.abs() < 6.1e-5, torch.full_like(want_kp, 2.0 ** -24),
+                      2.0 ** (torch.floor(torch.log2(want_kp.abs().clamp(min=6.1e-5))) - 10))
+    err = (kp - want_kp).abs()
+    print(f"[config4 layer] k_prepare: {int((err > 0).sum())} of {err.numel()} operands differ, "
+          f"max {float(err.max()):.3e}", flush=True)
+    assert bool((err <= ulp + 1e-5).all())
+    del kk, un, kp, want_kp
 
     m, k, n = B * T, G * D, 192
     a = (torch.randn(m, k, generator=g) * 0.5).half()
