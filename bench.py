@@ -412,17 +412,19 @@ def stream_points(dev, steps, warmup, T=32768, n_stream=512, pts=(1, 128, 256, 5
 
 def prefill(dev, layers=32, batch=4, T=8192):
     """Prefill compression kernels over `layers` x batch x T tokens of
-    synthetic K (low-rank Gaussian, RoPE'd) and V.  Per layer: undo-RoPE into
-    the fp16 GEMM operand, MFMA projection onto a fixed random-orthonormal
-    1024x192 basis, per-column int4 quantization + packing, FWHT + channel
-    normalization of V, nearest-centroid assignment to a seeded codebook."""
+    synthetic K (low-rank Gaussian, RoPE'd) and V.  Per layer: the fp16 MFMA
+    projection onto a fixed random-orthonormal 1024x192 basis with undo-RoPE
+    fused into its operand loads (the RoPE phase table is computed once per
+    pass: every layer has the same positions), per-column int4 quantization +
+    packing, FWHT + channel normalization of V, nearest-centroid assignment to
+    a seeded codebook."""
     from shard_amd import ops, bench_data
     G, D, R = 8, 128, 192
     basis = bench_data.random_orthonormal_basis(G * D, R).to(dev)
     bt = basis.t().contiguous().half()                            # (R, G*D)
+    btp = ops.rope_basis(bt)
     bits = torch.full((R,), 4, dtype=torch.int32, device=dev)
     invf = bench_data.inv_freq().to(dev)
-    mean = torch.zeros(G * D, dtype=torch.float32, device=dev)
     data, mix = [], None
     for li in range(layers):
         k, v, mix = bench_data.make_kv_device(T, batch, li, dev, mix=mix)
@@ -432,11 +434,10 @@ def prefill(dev, layers=32, batch=4, T=8192):
     codebook = x0[torch.randperm(x0.shape[0], generator=gsel, device=dev)[:256]].contiguous()
     del x0
 
-    def layer_pass(k, v, ev=None):
-        kp = ops.k_prepare(k, 0, T, invf, mean)
+    def layer_pass(k, v, ph, ev=None):
         if ev is not None:
             ev[0].record()
-        proj = ops.pca_project(kp, bt)
+        proj = ops.pca_project_rope(k, 0, T, ph, btp)
         if ev is not None:
             ev[1].record()
         chain = ops.int4_quant_pack(proj, bits)
@@ -444,14 +445,15 @@ def prefill(dev, layers=32, batch=4, T=8192):
         idx = ops.vq_assign(x, codebook)
         return chain, idx
 
-    layer_pass(*data[0])                                           # warm-up
+    layer_pass(*data[0], ops.rope_phases(0, T, invf))              # warm-up
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(layers)]
     e0.record()
+    ph = ops.rope_phases(0, T, invf)
     for li in range(layers):
-        layer_pass(*data[li], evs[li])
+        layer_pass(*data[li], ph, evs[li])
     e1.record()
     torch.cuda.synchronize()
     total_s = e0.elapsed_time(e1) / 1000.0
@@ -464,6 +466,7 @@ def prefill(dev, layers=32, batch=4, T=8192):
                        "data": "synthetic, generated on device"},
             "ms_total": round(total_s * 1000.0, 3),
             "projection": {"ms": round(gemm_s * 1000.0, 3),
+                           "what": "shard_pca_project_rope: undo-RoPE fused into the fp16 GEMM",
                            "tflops": round(flops / gemm_s / 1e12, 2),
                            "mfma_util_fp16": round(flops / gemm_s / (MFMA_PEAK_TFLOPS * 1e12), 4)}}
 

@@ -64,6 +64,27 @@ int shard_pca_project_f32(const float* a, int64_t m, int32_t k, int64_t lda,
                           const float* bt, int32_t n, float* c, int64_t ldc,
                           void* stream);
 
+/* The fp16 projection with its front end fused (the fp16 operand of
+ * shard_k_prepare is never written): C[b * n_comp + t, j] =
+ *   sum_k fp16(undo_rope(k)[.., col(k)]) * btp[j, k] - bias[j]
+ * for the post-RoPE keys k (B, n_kv, seq, 128) fp16 at positions start + t,
+ * undone with phases[(t, i)] = (cos, sin) of shard_rope_phases (the arithmetic
+ * of shard_k_prepare), in the permuted k order of the header of csrc/pca.hip
+ * (btp = the basis columns in that order, n rows of n_kv * 128; the host
+ * permutes them once); bias (n, nullable) = mean . basis stands for the
+ * centring.  hd == 128, n % 32 == 0, n <= 256; k, phases, btp 16-byte aligned.
+ * Replaces undo_rope + (flat - mean) @ basis of cache.py:370-392 on the fp16
+ * path. */
+int shard_pca_project_rope(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
+                           int32_t hd, int32_t start, int32_t n_comp,
+                           const float* phases, const uint16_t* btp, int32_t n,
+                           const float* bias, float* c, int64_t ldc, void* stream);
+
+/* (cos, sin)(fl((start + t) * inv_freq[i])) as float pairs, out (n, hd2, 2):
+ * the phases of rope_cos_sin (rope.py:13-18) that undo_rope uses. */
+int shard_rope_phases(int32_t start, int32_t n, int32_t hd2, const float* inv_freq,
+                      float* out, void* stream);
+
 /* Prefill K preparation fused with the projection input: reads post-RoPE keys
  * k (B, n_kv, T, hd) fp16, undoes RoPE at positions start+t with fp32 phases
  * fl(pos * inv_freq[i]) (rope.py:13-24), subtracts mean[n_kv*hd] (fp32) and

@@ -55,6 +55,8 @@ SIGNATURES = [
     ("shard_pca_project", c_int32, [c_void_p, c_int64, c_int32, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
     ("shard_k_prepare", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_pca_project_f32", c_int32, [c_void_p, c_int64, c_int32, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
+    ("shard_pca_project_rope", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_void_p]),
+    ("shard_rope_phases", c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     ("shard_k_prepare_f32", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("shard_int4_quant_pack_workspace", c_size_t, [c_int64, c_int32]),
     ("shard_int4_quant_pack", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -26,7 +26,7 @@ COMMON = [
 PER_FILE = {
     "quant.hip": ["-ffp-contract=off"],
     "decode_attn.hip": [],
-    "pca.hip": [],
+    "pca.hip": ["-ffp-contract=off"],  # the fused undo-RoPE rounds as k_prepare does
     "reconstruct.hip": ["-ffp-contract=off"],
     "abi.hip": [],
     "fp16_decode.hip": [],

@@ -253,6 +253,196 @@ void k_pca_project_f32(const float* __restrict__ A, int64_t m, int k, int64_t ld
   }
 }
 
+// ---------------------------------------------------------------------------
+// The fp16 projection with its front end fused: A is undo-RoPE of post-RoPE
+// keys read straight from the K cache layout (B, G, T, 128) fp16, so the fp16
+// operand of k_k_prepare is never written.  Row r = b * n_comp + t takes the
+// token at position start + t; its undo rotation uses the phase table
+// (cos, sin)(fl(pos * inv_freq[i])) of k_rope_phases (the phases k_k_prepare
+// computes) and k_k_prepare's arithmetic (this file is built without fp
+// contraction, so the fp16 operand is bit-identical to k_k_prepare's).
+// Workgroup shape as k_pca_project (8 waves, 128 rows, two column halves).
+// The k order is permuted so that one lane's 8-element MFMA fragment holds 4
+// dims of the low half of a head and their 4 RoPE partners of the high half:
+// chunk c (64 k) = head c % G, pairs 32 (c / G) .. + 31 (every head's first
+// pair half, then their second), k step s = 2 j + o and lane half hh: element
+// e is dim d0 + 4 o + e (e < 4) or 64 + d0 + 4 o + e - 4 (e >= 4),
+// d0 = 32 (c / G) + 16 j + 8 hh.  Btp holds the basis columns in that order
+// (the host permutes them once).  A lane meets 16 pairs per pair half, the
+// same in every head: their phases sit in registers (reloaded once, halfway).
+// C = fp16(undo(k)) . Btp^T - bias (bias: mean . basis, nullable).  Btp is
+// staged in LDS 64 k at a time, double-buffered; the keys and the Btp pieces
+// are loaded R - 1 chunks ahead into an R-slot register ring.
+constexpr int kRopePairs = 64;  // head_dim 128
+#ifndef SHARD_ROPE_RING
+#define SHARD_ROPE_RING 4
+#endif
+
+template <int NB32>
+__global__ __launch_bounds__(kPcaThreads, 1)
+void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int start, int n_comp,
+                        int64_t m, const float2* __restrict__ phases,
+                        const uint16_t* __restrict__ Btp, const float* __restrict__ bias,
+                        float* __restrict__ C, int64_t ldc) {
+  constexpr int kRowStride = kKc + 8;
+  constexpr int NH = (NB32 + 1) / 2;
+  constexpr int kPieces = NB32 * 32 * (kKc / 8);
+  constexpr int kPer = (kPieces + kPcaThreads - 1) / kPcaThreads;
+  constexpr int R = SHARD_ROPE_RING;
+  static_assert(kKc == 64, "a chunk is half a head: 32 RoPE pairs");
+  static_assert(R == 3 || R == 4, "ring of 3 or 4 slots");
+  __shared__ __align__(16) uint16_t bs[2][NB32 * 32 * kRowStride];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rw = w & 3, half = w >> 2;
+  const int col = lane & 31, hh = lane >> 5;
+  const int j0 = half * NH;
+  const int nj = NB32 - j0 < NH ? NB32 - j0 : NH;
+  const int k = n_kv * 128;
+  const int64_t row0 = (int64_t)blockIdx.x * kPcaRows + 32 * rw;
+  // this lane's A row (clamped past m: its loads stay in bounds, never stored)
+  const int64_t r = row0 + col < m ? row0 + col : m - 1;
+  const int64_t bb = r / n_comp, t = r - bb * n_comp;
+  const uint16_t* krow = K + ((bb * n_kv) * (int64_t)seq + start + t) * 128 + 8 * hh;  // head 0
+  const int64_t head_stride = (int64_t)seq * 128;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)Btp, (short)0, NB32 * 32 * k * 2, kBufWord3);
+  const int nc = k / kKc;
+
+  // the lane's phases of pair half ph: pairs 32 ph + 16 j + 8 hh + 0..7 -> ph_[j][0..7]
+  float2 ph_[2][8];
+  auto load_phases = [&](int ph) {
+    const float2* pt = phases + t * kRopePairs + 32 * ph + 8 * hh;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float4 v = *(const float4*)(pt + 16 * q + e);
+        ph_[q][e] = make_float2(v.x, v.y);
+        ph_[q][e + 1] = make_float2(v.z, v.w);
+      }
+  };
+  load_phases(0);
+
+  auto load_b = [&](int c, uint4 (&pb)[kPer]) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int pc = tid + kPcaThreads * u;
+      const int rr = pc / (kKc / 8), kk = kKc * c + 8 * (pc % (kKc / 8));
+      const int off = (pc < kPieces && kk < k) ? (rr * k + kk) * 2 : kOutOfRange;
+      pb[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+    }
+  };
+  auto store_b = [&](int buf, const uint4 (&pb)[kPer]) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int pc = tid + kPcaThreads * u;
+      if (pc < kPieces) *(uint4*)(&bs[buf][(pc / (kKc / 8)) * kRowStride + 8 * (pc % (kKc / 8))]) = pb[u];
+    }
+  };
+  // raw keys of chunk c (chunks past the end read chunk 0: loaded, multiplied
+  // by zero pieces): [2 j] = dims d0 .. d0 + 7, [2 j + 1] = dims 64 + d0 .. + 7
+  auto load_a = [&](int c, uint4 (&ka)[4]) {
+    const int cc = c < nc ? c : 0;
+    const int ph = cc >= n_kv ? 1 : 0;
+    const uint16_t* kh = krow + (cc - ph * n_kv) * head_stride + 32 * ph;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      ka[2 * j] = *(const uint4*)(kh + 16 * j);
+      ka[2 * j + 1] = *(const uint4*)(kh + 64 + 16 * j);
+    }
+  };
+
+  float16v acc[NH];
+#pragma unroll
+  for (int j = 0; j < NH; ++j) acc[j] = {};
+
+  uint4 pb[R][kPer];
+  uint4 ka[R][4];
+#pragma unroll
+  for (int d = 0; d < R - 1; ++d) {
+    load_b(d, pb[d]);
+    load_a(d, ka[d]);
+  }
+  store_b(0, pb[0]);
+  __syncthreads();
+
+  auto step = [&](const int c, const uint4 (&a)[4], uint4 (&an)[4],
+                  const uint4 (&b1)[kPer], uint4 (&bn)[kPer]) {
+    if (c == n_kv) load_phases(1);
+    const uint16_t* b = bs[c & 1];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint16_t* lo = (const uint16_t*)&a[2 * j];
+      const uint16_t* hi = (const uint16_t*)&a[2 * j + 1];
+      half8 f[2];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float2 cs = ph_[j][e];
+        const float l = h2f(lo[e]), h = h2f(hi[e]);
+        // undo_rope: k cos - rotate_half(k) sin, rotate_half = [-hi, lo] (k_k_prepare's arithmetic)
+        f[e >> 2][e & 3] = (half_t)__fadd_rn(__fmul_rn(l, cs.x), __fmul_rn(h, cs.y));
+        f[e >> 2][4 + (e & 3)] = (half_t)__fsub_rn(__fmul_rn(h, cs.x), __fmul_rn(l, cs.y));
+      }
+#pragma unroll
+      for (int o = 0; o < 2; ++o) {
+        const int s = 2 * j + o;
+#pragma unroll
+        for (int jj = 0; jj < NH; ++jj) {
+          if (NB32 % 2 == 0 || jj < nj) {
+            const uint4 bv = *(const uint4*)(b + (32 * (j0 + jj) + col) * kRowStride + 16 * s + 8 * hh);
+            acc[jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[o], __builtin_bit_cast(half8, bv), acc[jj], 0, 0, 0);
+          }
+        }
+      }
+    }
+    store_b((c + 1) & 1, b1);
+    load_b(c + R - 1, bn);
+    load_a(c + R - 1, an);
+    __syncthreads();
+  };
+  // the chunk count rounded up to the ring: chunks past nc multiply by zero
+  // Btp pieces (out-of-range reads) and add exact zeros
+  const int ncr = (nc + R - 1) / R * R;
+  for (int c0 = 0; c0 < ncr; c0 += R) {
+    if constexpr (R == 3) {
+      step(c0, ka[0], ka[2], pb[1], pb[2]);
+      step(c0 + 1, ka[1], ka[0], pb[2], pb[0]);
+      step(c0 + 2, ka[2], ka[1], pb[0], pb[1]);
+    } else {
+      step(c0, ka[0], ka[3], pb[1], pb[3]);
+      step(c0 + 1, ka[1], ka[0], pb[2], pb[0]);
+      step(c0 + 2, ka[2], ka[1], pb[3], pb[1]);
+      step(c0 + 3, ka[3], ka[2], pb[0], pb[2]);
+    }
+  }
+  // C layout of the 32x32 block: lane (col, hh), reg i -> row 8 (i / 4) + 4 hh + i % 4
+#pragma unroll
+  for (int jj = 0; jj < NH; ++jj) {
+    if (jj < nj) {
+      const float bz = bias ? bias[32 * (j0 + jj) + col] : 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t rr = row0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (rr < m) C[rr * ldc + 32 * (j0 + jj) + col] = acc[jj][i] - bz;
+      }
+    }
+  }
+}
+
+// (cos, sin)(fl(pos * inv_freq[i])) for pos = start + t, t < n, i < hd2: the
+// phases of k_k_prepare, one table per token range (shared by every batch
+// row, head and layer that undoes RoPE at those positions).
+__global__ void k_rope_phases(int start, int n, int hd2, const float* __restrict__ inv_freq,
+                              float2* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)n * hd2) return;
+  const int t = (int)(i / hd2), p = (int)(i - (int64_t)t * hd2);
+  float sn, cs;
+  sincosf(__fmul_rn((float)(start + t), inv_freq[p]), &sn, &cs);
+  out[i] = make_float2(cs, sn);
+}
+
 }  // namespace shard
 
 using namespace shard;
@@ -306,5 +496,48 @@ extern "C" int shard_pca_project_f32(const float* a, int64_t m, int32_t k, int64
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_pca_project_f32");
+  return SHARD_OK;
+}
+
+extern "C" int shard_rope_phases(int32_t start, int32_t n, int32_t hd2, const float* inv_freq,
+                                 float* out, void* stream) {
+  if (!inv_freq || !out || n <= 0 || hd2 <= 0 || start < 0) return SHARD_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t total = (int64_t)n * hd2;
+  hipLaunchKernelGGL(k_rope_phases, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, start, n,
+                     hd2, inv_freq, (float2*)out);
+  SHARD_LAUNCH_CHECK("shard_rope_phases");
+  return SHARD_OK;
+}
+
+extern "C" int shard_pca_project_rope(const uint16_t* k, int32_t batch, int32_t n_kv, int32_t seq,
+                                      int32_t hd, int32_t start, int32_t n_comp,
+                                      const float* phases, const uint16_t* btp, int32_t n,
+                                      const float* bias, float* c, int64_t ldc, void* stream) {
+  if (!k || !phases || !btp || !c || batch <= 0 || n_kv <= 0 || n_comp <= 0 || n <= 0)
+    return SHARD_ERR_ARG;
+  if (hd != 128 || n % 32 != 0 || n > 256 || ldc < n || start < 0 ||
+      start + n_comp > seq)
+    return SHARD_ERR_SHAPE;
+  if (((uintptr_t)k & 15) || ((uintptr_t)phases & 15) || ((uintptr_t)btp & 15)) return SHARD_ERR_SHAPE;
+  if ((int64_t)n * n_kv * 128 * 2 >= (1ll << 31) - 256) return SHARD_ERR_SHAPE;
+  const int64_t m = (int64_t)batch * n_comp;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)((m + kPcaRows - 1) / kPcaRows));
+#define SHARD_PR(NB) hipLaunchKernelGGL(k_pca_project_rope<NB>, grid, dim3(kPcaThreads), 0, s, k, n_kv, \
+                                        seq, start, n_comp, m, (const float2*)phases, btp, bias, c, ldc)
+  switch (n / 32) {
+    case 1: SHARD_PR(1); break;
+    case 2: SHARD_PR(2); break;
+    case 3: SHARD_PR(3); break;
+    case 4: SHARD_PR(4); break;
+    case 5: SHARD_PR(5); break;
+    case 6: SHARD_PR(6); break;
+    case 7: SHARD_PR(7); break;
+    case 8: SHARD_PR(8); break;
+    default: return SHARD_ERR_SHAPE;
+  }
+#undef SHARD_PR
+  SHARD_LAUNCH_CHECK("shard_pca_project_rope");
   return SHARD_OK;
 }

@@ -86,6 +86,73 @@ def pca_project_f32(a: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
     return c
 
 
+def rope_phases(start: int, n: int, inv_freq: torch.Tensor) -> torch.Tensor:
+    """(n, hd/2, 2) fp32 (cos, sin) of fl((start + t) * inv_freq[i])."""
+    _require_gpu(inv_freq)
+    lib = _lib.load()
+    inv_freq = _contig(inv_freq, torch.float32, "inv_freq")
+    hd2 = inv_freq.numel()
+    out = torch.empty(n, hd2, 2, dtype=torch.float32, device=inv_freq.device)
+    _lib.check("shard_rope_phases", lib.shard_rope_phases(start, n, hd2, _p(inv_freq), _p(out),
+                                                          _stream(inv_freq)))
+    return out
+
+
+_ROPE_K_ORDER = {}
+
+
+def rope_k_order(n_kv: int) -> torch.Tensor:
+    """Basis column of each k position of shard_pca_project_rope's permuted k
+    order (head_dim 128): k = 64 c + 16 s + 8 hh + e with chunk c = head c % G,
+    pair half c // G, step s = 2 j + o, element e -> dim d0 + 4 o + e (e < 4)
+    or 64 + d0 + 4 o + e - 4, d0 = 32 (c // G) + 16 j + 8 hh."""
+    order = _ROPE_K_ORDER.get(n_kv)
+    if order is None:
+        cols = []
+        for c in range(2 * n_kv):
+            ph, g = divmod(c, n_kv)
+            for s in range(4):
+                j, o = divmod(s, 2)
+                for hh in range(2):
+                    d0 = 32 * ph + 16 * j + 8 * hh
+                    for e in range(8):
+                        d = d0 + 4 * o + e if e < 4 else 64 + d0 + 4 * o + e - 4
+                        cols.append(g * 128 + d)
+        order = torch.tensor(cols, dtype=torch.long)
+        _ROPE_K_ORDER[n_kv] = order
+    return order
+
+
+def rope_basis(bt: torch.Tensor) -> torch.Tensor:
+    """The basis bt (n, G*128) fp16 with its columns in pca_project_rope's k order."""
+    G = bt.shape[1] // 128
+    return _contig(bt, torch.float16, "bt")[:, rope_k_order(G).to(bt.device)].contiguous()
+
+
+def pca_project_rope(k: torch.Tensor, start: int, n_comp: int, phases: torch.Tensor,
+                     btp: torch.Tensor, bias=None) -> torch.Tensor:
+    """undo-RoPE of post-RoPE keys k (B, G, T, 128) fp16 at positions start +
+    t, times the basis: (B*n_comp, n) fp32 = fp16(undo(k)) @ bt^T - bias, with
+    btp = rope_basis(bt) for bt (n, G*128) fp16 and the undo in k_prepare's
+    arithmetic (phases from rope_phases); one launch, no operand round trip."""
+    _require_gpu(k, phases, btp)
+    lib = _lib.load()
+    k = _contig(k, torch.float16, "k")
+    B, G, T, D = k.shape
+    phases = _contig(phases, torch.float32, "phases")
+    n = btp.shape[0]
+    if btp.shape[1] != G * D or phases.shape[0] < n_comp:
+        raise ValueError("pca_project_rope: basis or phase table does not match the keys")
+    btp = _contig(btp, torch.float16, "btp")
+    if bias is not None:
+        bias = _contig(bias, torch.float32, "bias")
+    c = torch.empty(B * n_comp, n, dtype=torch.float32, device=k.device)
+    _lib.check("shard_pca_project_rope", lib.shard_pca_project_rope(
+        _p(k), B, G, T, D, start, n_comp, _p(phases), _p(btp), n,
+        _p(bias) if bias is not None else None, _p(c), n, _stream(k)))
+    return c
+
+
 def k_prepare(k: torch.Tensor, start: int, n_comp: int, inv_freq: torch.Tensor,
               mean: torch.Tensor, out_dtype=torch.float16) -> torch.Tensor:
     """undo-RoPE + mean subtraction of keys (B, G, T, D) fp16 -> (B*n_comp, G*D)

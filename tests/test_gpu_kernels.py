@@ -310,6 +310,43 @@ def test_k_prepare_f32(cuda):
     assert float((got - want).abs().max()) <= 4e-7 * float(want.abs().max())
 
 
+@pytest.mark.parametrize("B,G,T,start,n_comp,n", [(2, 8, 300, 4, 232, 192), (1, 8, 700, 4, 632, 64),
+                                                    (3, 4, 200, 0, 200, 256)])
+def test_pca_project_rope_equals_prepare_then_project(cuda, B, G, T, start, n_comp, n):
+    """The fused front end (undo RoPE in the A loads, permuted k order) computes
+    the same fp16 operand as shard_k_prepare with a zero mean, so it matches
+    k_prepare + pca_project to fp32 summation order; with a mean, the bias
+    mean . basis stands for the centring (fp64 check)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(T + n)
+    k = (torch.randn(B, G, T, 128, generator=g) * 2).half()
+    bt = (torch.randn(n, G * 128, generator=g) * 0.03).half()
+    inv = ref.default_inv_freq(500000.0, 128)
+    kd, btd, invd = k.to(cuda), bt.to(cuda), inv.to(cuda)
+    ph = ops.rope_phases(start, n_comp, invd)
+    zero = torch.zeros(G * 128, device=cuda)
+    want = ops.pca_project(ops.k_prepare(kd, start, n_comp, invd, zero), btd).cpu().double()
+    btp = ops.rope_basis(btd)
+    got = ops.pca_project_rope(kd, start, n_comp, ph, btp).cpu().double()
+    a16 = ops.k_prepare(kd, start, n_comp, invd, zero).cpu().double()
+    exact = a16 @ bt.double().T              # the common fp16 operand, summed in fp64
+    scale = a16.abs() @ bt.double().abs().T
+    err = float(((got - exact).abs() / scale).max())
+    err_u = float(((want - exact).abs() / scale).max())
+    print(f"pca_project_rope B={B} G={G} n_comp={n_comp} n={n}: max rel err {err:.3e} "
+          f"(unfused {err_u:.3e})", flush=True)
+    assert err < 1e-6 and err_u < 1e-6
+    # a mean: fp16(undo(k)) . B - mean . B against fp64 (undo(k) - mean) . B
+    mean = torch.randn(G * 128, generator=g) * 0.1
+    bias = (mean.double() @ bt.double().T).float()
+    got_m = ops.pca_project_rope(kd, start, n_comp, ph, btp, bias=bias.to(cuda)).cpu().double()
+    un = ref.undo_rope(k[:, :, start:start + n_comp].float(), torch.arange(start, start + n_comp), inv)
+    x = un.permute(0, 2, 1, 3).reshape(B * n_comp, G * 128).double() - mean.double()
+    want_m = x @ bt.double().T
+    err_m = float(((got_m - want_m).abs() / (x.abs() @ bt.double().abs().T)).max())
+    assert err_m < 2e-3
+
+
 def test_k_prepare(cuda):
     ops = _ops()
     g = torch.Generator().manual_seed(2)
