@@ -886,6 +886,9 @@ struct TokParams {
   float* ws_acc;
 };
 
+#ifndef SHARD_RC_PAD
+#define SHARD_RC_PAD 8  // rows of 40 dwords: the two lane halves (pairs 4 apart) read other banks
+#endif
 template <int KS, int NQ>
 struct TokLds {
   union {
@@ -898,7 +901,7 @@ struct TokLds {
     } red;
   } u;
   uint2 cb[256];                        // VQ codebook, 4 x fp16 per entry
-  uint32_t rc[64][32];                  // [pair][col]: fp16 (cos, sin)(col theta) / 16
+  uint32_t rc[64][32 + SHARD_RC_PAD];   // [pair][col]: fp16 (cos, sin)(col theta) / 16
   uint16_t qr[kTokWaves][NQ + 1][2][64];  // per wave: R(-phi0) q (fp16, score k order); row NQ = 0
   uint16_t pa[kTokWaves][NQ + 1][32];     // per wave: fp16 numerators [head][token]; row NQ stays 0
   float xp[kTokWaves][32][NQ + 1];        // per wave: numerators of an extra tile, [token][head]
