@@ -234,3 +234,42 @@ def test_compress_layer_own_basis_vs_oracle_exact_svd(cuda):
     print(f"[own basis] relative key error: product {e_got:.5f}, oracle (exact SVD) {e_want:.5f}",
           flush=True)
     assert e_got <= 1.01 * e_want + 1e-4
+
+
+def test_compress_rank_not_a_multiple_of_32(cuda):
+    """max_rank_k = 100 (DP groups of 64 and 36 components): the fp32
+    projection's column padding (to 128) and the int4 chain on 100 columns
+    agree with the oracle as above, and the padded decode operands give the
+    exact oracle's attention output."""
+    from oracle import exact
+    from shard_amd import bench_data, ops
+    from shard_amd.cache import Cache, compress_layer
+    from tests.helpers import compare
+    k, v = bench_data.make_kv(1024, seed=3)
+    inv = bench_data.inv_freq()
+    x = _centred_rows(k, inv)
+    _, S, Vh = torch.linalg.svd(x.double(), full_matrices=False)
+    basis = Vh[:100].T.float().contiguous()
+    cache = Cache(head_dim=128, num_layers=1, n_kv_heads=8, device="cuda", rope_inv_freq=inv,
+                  max_rank_k=100, k_target_cr=8.0)
+    dbg = {}
+    got = compress_layer(cache, k.to(cuda), v.to(cuda), 0, basis=basis.to(cuda), debug=dbg)
+    torch.cuda.synchronize()
+    want = ref.compress_layer(k, v, 0, inv, k_target_cr=8.0, max_rank=100, basis=basis,
+                              assign=cref.vq_assign_direct_t)
+    n, keep = got["k_coeffs_shape"]
+    assert keep == len(want["alloc"]) and keep % 32 != 0 and got["rank_pad"] == 128, (keep, got["rank_pad"])
+    assert dbg["alloc"] == list(want["alloc"])
+    assert_codes_agree(got["k_coeffs"].cpu().numpy(), want["chain"], want["proj"].numpy(), want["alloc"],
+                       n, keep, "compress rank 100")
+    # decode over the padded operands against the fp64 oracle on the same stored layer
+    q = bench_data.make_q().to(cuda).view(1, 32, 128)
+    pos_q = 1023
+    call = ops.make_decode_args(q, got, pos_q, None)
+    out = ops.decode_attn(call).cpu().float().numpy()
+    gp = dict(got)
+    gp["v_idx_full"] = got["v_indices"]
+    ref_out = exact.decode_attention(q.cpu().view(1, 32, 1, 128).numpy(), gp, 8, pos_q, inv.numpy())
+    err, cos = compare(out, ref_out)
+    print(f"[compress rank 100] decode max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= 2e-3 and cos >= 0.9999
