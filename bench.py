@@ -267,6 +267,57 @@ def time_sdpa(k, v, q, steps, warmup, dev, graph_len=50):
     return graph_time(fns, steps, warmup, graph_len)
 
 
+def hd64(dev, steps, warmup, contexts=(8192, 32768)):
+    """Decode on a head_dim-64 layer shaped like Llama-3.2-1B's attention (32
+    query heads over 8 kv heads of 64 dims, RoPE theta 500000; synthetic K/V of
+    bench_data's spectrum): the fused call, which runs kv heads 2j and 2j+1 as
+    one 128-dim head on the token-tiled kernel, against the path such a layer
+    took without it (the whole compressed span rebuilt to fp16 by
+    shard_kv_reconstruct, concatenated with sink and window, torch SDPA) and
+    SDPA on the uncompressed fp16 K/V.  Per-call times from graph replays over
+    rotated copies, as the headline's."""
+    import torch.nn.functional as F
+    from shard_amd import Cache, bench_data, ops
+    from shard_amd.cache import compress_layer
+    n_q, n_kv, hd = 32, 8, 64
+    res = {"workload": "one Llama-3.2-1B-shaped layer (32q/8kv heads, hd 64), batch 1"}
+    for T in contexts:
+        k, v = bench_data.make_kv(T, n_kv=n_kv, hd=hd)
+        cache = Cache(num_layers=1, head_dim=hd, n_kv_heads=n_kv,
+                      rope_inv_freq=bench_data.inv_freq(hd))
+        fmt = compress_layer(cache, k.to(dev), v.to(dev), 0)
+        torch.cuda.synchronize()
+        n, rank = fmt["n_compress"], fmt["rank_pad"]
+        q = bench_data.make_q(1, n_q=n_q, hd=hd).to(dev).view(1, n_q, hd)
+        nbytes = algorithmic_bytes(n, rank, n_kv=n_kv, hd=hd, n_q=n_q)
+        n_copies = max(2, math.ceil(2 * 256e6 / nbytes))
+        rot, hot, _ = time_decode(fmt, q, T - 1, steps, warmup, n_copies)
+
+        def unfused():
+            kc, vc = ops.kv_reconstruct(fmt, 1)
+            kk = torch.cat([fmt["sink_k"], kc, fmt["win_k"]], dim=2)
+            vv = torch.cat([fmt["sink_v"], vc, fmt["win_v"]], dim=2)
+            return F.scaled_dot_product_attention(q.view(1, n_q, 1, hd), kk, vv, enable_gqa=True)
+        us_unfused = graph_time([unfused], min(steps, 200), 10, graph_len=20)
+        us_sdpa = time_sdpa(k.to(dev), v.to(dev), q.view(1, n_q, 1, hd), min(steps, 200), 20, dev)
+        flops = algorithmic_flops(n, rank, n_kv=n_kv, hd=hd, n_q=n_q)
+        res[str(T)] = {"us": round(rot["median"], 3), "us_p10": round(rot["p10"], 3),
+                       "us_p90": round(rot["p90"], 3), "us_hot": round(hot["median"], 3),
+                       "n_comp": n, "rank": fmt["rank"], "rank_pad": rank,
+                       "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+                       "roofline": roofline(flops, nbytes, rot["median"]),
+                       "unfused_rebuild_sdpa_us": round(us_unfused, 3),
+                       "speedup_vs_unfused": round(us_unfused / rot["median"], 2),
+                       "fp16_sdpa_us": round(us_sdpa, 3),
+                       "speedup_vs_fp16_sdpa": round(us_sdpa / rot["median"], 3),
+                       "compress_ratio": compress_ratios(fmt)}
+        print(f"[hd64] T={T} fused {rot['median']:.2f} us, unfused {us_unfused:.1f} us, "
+              f"sdpa {us_sdpa:.1f} us", flush=True)
+        del fmt, k, v
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_model():
     """The host CPU's model name (/proc/cpuinfo), for the baseline record."""
     try:
@@ -862,6 +913,8 @@ def main():
                     help="BASELINE config 4: prefill compression kernels, tokens/s")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="eager decode calls over cold layer copies at --ctx (for rocprofv3 --pmc)")
+    ap.add_argument("--hd64", action="store_true",
+                    help="decode on a head_dim-64 (Llama-3.2-1B-shaped) layer at 8K and 32K")
     ap.add_argument("--e2e", action="store_true",
                     help="BASELINE config 5: random Llama-3.1-8B, shard cache vs fp16 cache")
     ap.add_argument("--e2e-batch", type=int, default=16)
@@ -894,6 +947,9 @@ def main():
         return
     if args.kmeans:
         print(json.dumps(kmeans_update_bench(dev)), flush=True)
+        return
+    if args.hd64:
+        print(json.dumps(hd64(dev, args.steps, args.warmup)), flush=True)
         return
     if args.e2e:
         print(json.dumps(e2e(dev, args.e2e_batch, args.e2e_prompt, args.e2e_new,

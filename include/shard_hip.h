@@ -230,7 +230,7 @@ int shard_stream_quant_kv(const uint16_t* k, const uint16_t* v, int64_t rows, in
  *   as transformers passes it when the positions are the same)
  *   q_rope (B, n_q_heads, hd) fp16 out; the k_* / v_* outputs are the rows of
  *   this token in the stream buffers (codes, norms, fp16 rows; QJL nullable).
- * hd = 128 or 256. */
+ * hd = 64, 128 or 256. */
 int shard_rope_stream_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                              const uint16_t* cos, const uint16_t* sin, int64_t cos_stride,
                              int32_t batch,
@@ -270,7 +270,7 @@ int shard_stream_dequant_qjl(const uint8_t* idx, const uint16_t* norm, const uin
  * ------------------------------------------------------------------------ */
 
 /* Arguments of one decode-attention call (one layer, one query token per row).
- * Layouts (B = batch, H = n_q_heads, G = n_kv_heads, D = head_dim = 128):
+ * Layouts (B = batch, H = n_q_heads, G = n_kv_heads, D = head_dim, 128 or 64):
  *   q            (B, H, D) fp16, post-RoPE at position pos_q
  *   inv_freq     (D/2) fp32
  *   k_coeffs     (B*n_comp, rank/2) packed int4 (row-major, low nibble first)
@@ -288,7 +288,10 @@ int shard_stream_dequant_qjl(const uint8_t* idx, const uint16_t* norm, const uin
  *   out          (B, H, D) fp16
  * H / G (query heads per kv head) is 1, 2 or a multiple of 4 (<= 64).  rank
  * must be a multiple of 32 (<= 192); pad coefficients and basis with zeros
- * otherwise.  Any number of sink, window, decode and stream tokens (the
+ * otherwise.  head_dim 64 needs an even G and H / G 1 or even (<= 32): the
+ * kernel runs kv heads 2j and 2j+1 as one 128-dim head (the token-tiled
+ * kernel; `prep` from shard_decode_prepare with head_dim 64), every layout
+ * above with D = 64 as it stands.  Any number of sink, window, decode and stream tokens (the
  * reference appends without limit, cache.py:156-181).  The softmax and all
  * sums run in fp32.
  * Replaces fused_attention_compressed (attention.py:270-343) with its
@@ -343,16 +346,20 @@ typedef struct shard_decode_args {
  * layer is compressed (they depend only on its basis, scales, mean and RoPE
  * frequencies): the MFMA operand image of fp16(k_basis * k_coeff_scale) with
  * the mean folded in, and the in-tile RoPE rotation tables.  `out` holds
- * shard_decode_prepare_bytes(n_kv_heads, rank) bytes and is passed to
- * shard_decode_attn as args->prep.  rank % 32 == 0, rank <= 192. */
+ * shard_decode_prepare_bytes(n_kv_heads, rank) bytes (head_dim 64:
+ * shard_decode_prepare_bytes(n_kv_heads / 2, rank), one image per pair of kv
+ * heads) and is passed to shard_decode_attn as args->prep.  head_dim 128, or
+ * 64 with n_kv_heads even; rank % 32 == 0, rank <= 192. */
 size_t shard_decode_prepare_bytes(int32_t n_kv_heads, int32_t rank);
 int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
                          const uint16_t* k_mean, const float* inv_freq, int32_t n_kv_heads,
                          int32_t head_dim, int32_t rank, void* out, size_t out_bytes,
                          void* stream);
 
-/* 1 when shard_decode_attn takes the shapes in `args` (head_dim 128, query
- * heads per kv head 1, 2 or a multiple of 4, rank a multiple of 32 up to 192),
+/* 1 when shard_decode_attn takes the shapes in `args` (head_dim 128 with query
+ * heads per kv head 1, 2 or a multiple of 4 up to 64, or head_dim 64 with an
+ * even number of kv heads and 1 or an even number up to 32 query heads per kv
+ * head; rank a multiple of 32 up to 192),
  * else 0: the caller then rebuilds fp16 K/V (shard_kv_reconstruct) and runs
  * plain attention, as the reference's unfused path does (attention.py:411). */
 int shard_decode_supported(const shard_decode_args* args);

@@ -515,6 +515,13 @@ def compress_layer(k_full: torch.Tensor, v_full: torch.Tensor, layer_idx: int,
     col_max = basis.abs().max(dim=0).values.clamp(min=1e-6)
     scale = col_max / 127.0
     basis_q = (basis / scale).round().clamp(-127, 127).to(torch.int8)
+    if keep == 0:
+        # every component dropped: _compress_k leaves basis and alloc whole and
+        # projects onto none (cache.py:383-392); _build_gpu_format then stores
+        # keep = len(k_alloc) columns of zero coefficients (cache.py:412-420),
+        # kept even here as the device format stores ranks
+        keep = len(alloc) - (len(alloc) & 1)
+        basis_q, scale, alloc = basis_q[:, :keep], scale[:keep], alloc[:keep]
     proj = (flat - mean.float()) @ (basis_q.float() * scale.float())[:, :keep]
     chain = k_code_chain(proj.numpy(), alloc)
 

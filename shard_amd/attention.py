@@ -126,9 +126,10 @@ def enable_llama_fused_attention(model=None):
         fuse = (gc is not None and hidden_states.shape[1] == 1
                 and past_key_values._rope_inv_freq is not None)
         if fuse and not fused_supported(gc, self.config.num_attention_heads):
-            # a shape the fused kernel does not take (head_dim other than 128,
-            # query groups other than 1, 2 or 4k, rank above 192): the original
-            # forward runs on the rebuilt fp16 K/V (layer.keys / values); counted
+            # a shape the fused kernel does not take (head_dim other than 128 or
+            # 64, an odd kv head count at 64, query groups it cannot split,
+            # rank above 192): the original forward runs on the rebuilt fp16
+            # K/V (layer.keys / values); counted
             past_key_values._fused_fallbacks = getattr(past_key_values, "_fused_fallbacks", 0) + 1
             past_key_values._last_fused_fallback = (
                 f"head_dim={gc.get('head_dim')} n_q={self.config.num_attention_heads} "

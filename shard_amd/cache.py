@@ -655,9 +655,14 @@ def compress_layer(cache: Cache, k_full: torch.Tensor, v_full: torch.Tensor, li:
     keep = sum(1 for b in alloc if b > 0)
     if keep & 1:
         keep -= 1
-    if keep > 0:
-        basis = basis[:, :keep].contiguous()
-        alloc = alloc[:keep]
+    if keep == 0:
+        # every component dropped (a budget below one group's cheapest option):
+        # the reference keeps them all, with zero coefficients, so the keys
+        # decode to the mean (_build_gpu_format takes keep = len(k_alloc),
+        # cache.py:412); an even count, as every stored rank here
+        keep = len(alloc) - (len(alloc) & 1)
+    basis = basis[:, :keep].contiguous()
+    alloc = alloc[:keep]
     col_max = basis.abs().max(dim=0).values.clamp(min=1e-6)
     scale = col_max / 127.0
     basis_q = (basis / scale).round().clamp(-127, 127).to(torch.int8)
@@ -771,7 +776,10 @@ def finalize_format(gc: dict, inv_freq, dev):
     if inv_freq is None:
         inv_freq = torch.zeros(gc["head_dim"] // 2)
     gc["inv_freq_dev"] = inv_freq.to(dev, torch.float32).contiguous()
-    # decode-kernel operands for the shapes the fused kernel takes; other layers
-    # decode through kv_reconstruct and the model's own attention
-    gc["decode_prep"] = (ops.decode_prepare(gc) if gc["head_dim"] == 128 and rank_pad <= 192
+    # decode-kernel operands for the shapes the fused kernel takes (head_dim
+    # 128, or 64 with an even kv head count); other layers decode through
+    # kv_reconstruct and the model's own attention
+    hd, G = gc["head_dim"], gc["n_kv"]
+    gc["decode_prep"] = (ops.decode_prepare(gc)
+                         if (hd == 128 or (hd == 64 and G % 2 == 0)) and rank_pad <= 192
                          else None)

@@ -190,9 +190,18 @@ __device__ __forceinline__ void load_coef(const uint8_t* rowp, bool valid, uint3
 //        then the tile-offset tables of the token-tiled kernel: float2 [32][64] =
 //        (cos, sin)(32 b theta_i) and float2 [32][64] = (cos, sin)(1024 a theta_i)
 //        (tile k of a chunk is 32 (32 a + b) tokens from its start).
+// Head pairs (hp = 1, head_dim-64 layers): G counts pairs of kv heads; pair g
+// is one 128-dim head whose dims are [head 2g dims 0-31, head 2g+1 dims 0-31,
+// head 2g dims 32-63, head 2g+1 dims 32-63], so that RoPE pairs (d, d + 32 of
+// a 64-dim head) sit 64 apart as in a 128-dim head; the basis and mean rows
+// are read in that order and inv_freq has 32 entries.
+__device__ __forceinline__ int pair_row(int g, int vd) {
+  return (2 * g + ((vd >> 5) & 1)) * 64 + 32 * (vd >> 6) + (vd & 31);
+}
+
 __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint16_t* __restrict__ cs,
                                  const uint16_t* __restrict__ mean, const float* __restrict__ inv_freq,
-                                 int G, int rank, uint4* __restrict__ op, float2* __restrict__ rope) {
+                                 int G, int rank, int hp, uint4* __restrict__ op, float2* __restrict__ rope) {
   const int KS = rank / 16;
   const int64_t n_op = (int64_t)G * 4 * (KS + 1) * 64;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -203,7 +212,7 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
       const int P = (int)((i / (64 * (KS + 1))) % 4);
       const int g = (int)(i / (64 * (KS + 1) * 4));
       const int col = lane & 31, hh = lane >> 5;
-      const int row = g * kHD + row_dim(P, col);
+      const int row = hp ? pair_row(g, row_dim(P, col)) : g * kHD + row_dim(P, col);
       half8 v;
       if (s < KS) {
         const int r0 = 8 * (KS * hh + s);
@@ -229,15 +238,16 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
       op[i] = __builtin_bit_cast(uint4, v);
     } else {
       const int k = (int)(i - n_op);
+      const int fm = hp ? 31 : 63;  // pair -> inv_freq entry
       float sn, cn;
       if (k < 32 * 64) {
-        sincosf((float)(k / 64) * inv_freq[k % 64], &sn, &cn);
+        sincosf((float)(k / 64) * inv_freq[k % 64 & fm], &sn, &cn);
       } else if (k < 32 * 64 + 64) {
-        sincosf((float)kTile * inv_freq[k - 32 * 64], &sn, &cn);
+        sincosf((float)kTile * inv_freq[(k - 32 * 64) & fm], &sn, &cn);
       } else {
         const int k2 = k - (32 * 64 + 64);  // tile-offset tables
         const int tab = k2 / (32 * 64), e = (k2 / 64) % 32, pi = k2 % 64;
-        sincosf((float)(tab == 0 ? kTile * e : kTile * 32 * e) * inv_freq[pi], &sn, &cn);
+        sincosf((float)(tab == 0 ? kTile * e : kTile * 32 * e) * inv_freq[pi & fm], &sn, &cn);
       }
       rope[k] = make_float2(cn, sn);
     }
@@ -252,29 +262,40 @@ __device__ __forceinline__ uint32_t ld_global_u32(uint64_t addr) {
 }
 
 // Row x of the extra tokens (sink, window, decode, stream) of kv head g in
-// batch row b, and its column in the attention mask (the compressed span sits
-// between the sink and the window).
+// batch row b (HD dims per row, G kv heads), and its column in the attention
+// mask (the compressed span sits between the sink and the window).  *next =
+// the element distance from this row to the same row of kv head g + 1: a
+// segment's rows of one head are contiguous, stream rows hold the kv heads of
+// a token side by side.
+template <int HD = kHD>
 __device__ __forceinline__ const uint16_t* extra_row(const ExtraSegs& s, int B, int G, int n_comp,
-                                                     int b, int g, int x, bool v, int* mpos) {
+                                                     int b, int g, int x, bool v, int* mpos,
+                                                     int* next = nullptr) {
   const int e1 = s.n_sink, e2 = e1 + s.n_win, e3 = e2 + s.n_dec;
   const int64_t bg = (int64_t)b * G + g;
   const uint16_t* base;
   int64_t row;
+  int seg;
   if (x < e1) {
     base = v ? s.sink_v : s.sink_k;
     row = bg * s.n_sink + x;
+    seg = s.n_sink;
   } else if (x < e2) {
     base = v ? s.win_v : s.win_k;
     row = bg * s.n_win + (x - e1);
+    seg = s.n_win;
   } else if (x < e3) {
     base = v ? s.dec_v : s.dec_k;
     row = bg * s.dec_stride + (x - e2);
+    seg = s.dec_stride;
   } else {
     base = v ? s.s_v : s.s_k;
     row = ((int64_t)(x - e3) * B + b) * G + g;
+    seg = 1;
   }
   *mpos = x < e1 ? x : x + n_comp;
-  return base + row * kHD;
+  if (next) *next = HD * seg;
+  return base + row * HD;
 }
 
 // One butterfly stage at element stride 2*HL = lane stride HL.
@@ -286,6 +307,9 @@ __device__ __forceinline__ void fwht_lane_stage(float& x0, float& x1, int l) {
 }
 
 // Butterflies over 128 values held as (2l, 2l+1) in lane l (Sylvester order).
+// HALVES: two transforms of 64 (lanes 0-31 and 32-63), the stage across the
+// halves left out and the scale 1/sqrt(64).
+template <bool HALVES = false>
 __device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
   const int l = (int)lane_id();
   {
@@ -298,8 +322,8 @@ __device__ __forceinline__ void fwht128_pairs(float& x0, float& x1) {
   fwht_lane_stage<4>(x0, x1, l);
   fwht_lane_stage<8>(x0, x1, l);
   fwht_lane_stage<16>(x0, x1, l);
-  fwht_lane_stage<32>(x0, x1, l);
-  const float s = 0.08838834764831845f;  // 1/sqrt(128)
+  if constexpr (!HALVES) fwht_lane_stage<32>(x0, x1, l);
+  const float s = HALVES ? 0.125f : 0.08838834764831845f;  // 1/sqrt(64), 1/sqrt(128)
   x0 *= s;
   x1 *= s;
 }
@@ -861,6 +885,18 @@ void k_decode_split(const SplitParams p) {
 // the extra tokens' part (plain basis) added, and one partial row (m, l,
 // acc[128]) written per (batch row, query head, split).  The FWHT is linear, so
 // it commutes with the log-sum-exp merge of k_decode_merge.
+//
+// Head pairs (HP, head_dim-64 layers): kv heads 2g and 2g + 1 run as one
+// 128-dim head g (G counts the pairs).  The rebuilt keys come from the pair's
+// operand image (k_decode_prepare, hp = 1: dims [2g low, 2g+1 low, 2g high,
+// 2g+1 high], RoPE pairs 64 apart); a query head reads its 64-dim q into its
+// own head's pairs and zeros into the other's, so its scores are against its
+// own head's keys, softmax scale 1/sqrt(64).  The V indices of the two heads
+// (16 bytes per token each, in their own rows) form the 32 subvectors, the
+// fp16 rows of the extra tokens are read per head, ch and the plain-basis
+// sums are the two heads' 64 dims side by side, and the inverse Hadamard runs
+// per 64 dims.  A query head keeps its own head's 64 dims (the first 64 of its
+// partial row); the other half of its value sums is discarded.
 constexpr int kTokWaves = 8;
 constexpr int kTokThreads = 64 * kTokWaves;
 constexpr int kShareMinTiles = 64;  // splits with fewer tiles give both waves of a SIMD equal shares
@@ -914,7 +950,7 @@ __device__ __forceinline__ int pair_k(int i) {
   return (i & ~15) + 8 * ((pl >> 2) & 1) + 4 * (pl >> 3) + (pl & 3);
 }
 
-template <int KS, int NQ>
+template <int KS, int NQ, bool HP>
 __global__ __launch_bounds__(kTokThreads, 1)
 void k_decode_tok(const TokParams p) {
   static_assert(NQ == 1 || NQ == 2 || NQ == 4, "query heads per workgroup");
@@ -971,9 +1007,14 @@ void k_decode_tok(const TokParams p) {
   const __amdgpu_buffer_rsrc_t rcoef = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.coef + ((int64_t)b * p.n_comp + r0) * coef_row_bytes), (short)0,
       n_rows * coef_row_bytes, kBufWord3);
-  const __amdgpu_buffer_rsrc_t rvidx = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.vidx + (((int64_t)b * p.G + hg) * p.n_comp + r0) * 32), (short)0, n_rows * 32,
-      kBufWord3);
+  // head pairs: each head of the pair has its own rows (16 bytes per token),
+  // read through a buffer of its own (rvidx: the first head, rvidx2: the second)
+  const uint8_t* vbase = HP ? p.vidx + (2 * ((int64_t)b * p.G + hg) * p.n_comp + r0) * 16
+                            : p.vidx + (((int64_t)b * p.G + hg) * p.n_comp + r0) * 32;
+  const __amdgpu_buffer_rsrc_t rvidx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, n_rows * (HP ? 16 : 32), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rvidx2 = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(vbase + (HP ? (int64_t)p.n_comp * 16 : 0)), (short)0, HP ? n_rows * 16 : 0, kBufWord3);
   // the additive mask row of batch row b: no mask reads as 0 (zero-length buffer)
   const int64_t n_keys = (int64_t)p.n_sink + p.n_comp + p.xs.n_x;
   const __amdgpu_buffer_rsrc_t rmask = __builtin_amdgcn_make_buffer_rsrc(
@@ -984,10 +1025,17 @@ void k_decode_tok(const TokParams p) {
   // lane / 16) holds tokens 8 vt .. 8 vt + 7 of subvector vn + 16 jg, jg = 0, 1.
   const int vn = lane & 15, vt = lane >> 4;
   auto load_vidx = [&](int k, uint32_t (&vi_)[16]) {
-    const int voff = (32 * k + 8 * vt) * 32 + vn;
+    if constexpr (HP) {
+      const int voff = (32 * k + 8 * vt) * 16 + vn;
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
-      vi_[m] = __builtin_amdgcn_raw_buffer_load_b8(rvidx, voff + 32 * (m & 7) + 16 * (m >> 3), 0, 0);
+      for (int m = 0; m < 16; ++m)
+        vi_[m] = __builtin_amdgcn_raw_buffer_load_b8((m >> 3) ? rvidx2 : rvidx, voff + 16 * (m & 7), 0, 0);
+    } else {
+      const int voff = (32 * k + 8 * vt) * 32 + vn;
+#pragma unroll
+      for (int m = 0; m < 16; ++m)
+        vi_[m] = __builtin_amdgcn_raw_buffer_load_b8(rvidx, voff + 32 * (m & 7) + 16 * (m >> 3), 0, 0);
+    }
   };
   const float2* t2tab = p.rope + kRopeT2 + lane;  // lane = pair
   const float2* t1tab = p.rope + kRopeT1 + lane;
@@ -1047,9 +1095,19 @@ void k_decode_tok(const TokParams p) {
     for (int j = 0; j < kPR; ++j) rv[j] = p.rope[tid + kTokThreads * j];
   }
   const uint2 cbv = tid < 256 ? *(const uint2*)(p.vcb + 4 * tid) : make_uint2(0u, 0u);
-  const float th = p.inv_freq[lane];
+  const float th = p.inv_freq[HP ? (lane & 31) : lane];
+  // head pairs: query heads per kv head; a query head's kv head is 2 hg + its half
+  const int gq = HP ? p.H / (2 * p.G) : 1;
   uint16_t qlo[NQ], qhi[NQ];
-  {
+  if constexpr (HP) {  // pairs 0..31: the pair's first head, 32..63 its second
+    const uint16_t* qv = p.q + ((int64_t)b * p.H + qh0) * 64 + (lane & 31);
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const bool mine = (((qh0 + h) / gq) & 1) == hh;
+      qlo[h] = mine ? qv[h * 64] : (uint16_t)0;
+      qhi[h] = mine ? qv[h * 64 + 32] : (uint16_t)0;
+    }
+  } else {
     const uint16_t* qv = p.q + ((int64_t)b * p.H + qh0) * kHD;
 #pragma unroll
     for (int h = 0; h < NQ; ++h) {
@@ -1102,7 +1160,7 @@ void k_decode_tok(const TokParams p) {
   for (int e = 0; e < 8; ++e) one8[e] = (half_t)1.f;
   __syncthreads();
 
-  const float sc = kLog2e * rsqrtf((float)kHD);
+  const float sc = kLog2e * rsqrtf(HP ? 64.f : (float)kHD);
   float m_run[NE], l_part[NE];
   float4v vacc[2][4];  // [subvector group][component]: rows (heads) 4 vt + i, column vn
   float2 xacc[NQ];
@@ -1285,11 +1343,25 @@ void k_decode_tok(const TokParams p) {
   bool aq_loaded = false;
   auto xtile = [&](const int x) {
     if (!aq_loaded) {
-      const uint16_t* qv = p.q + ((int64_t)b * p.H + qh0 + min(col, NQ - 1)) * kHD + 8 * hh;
+      if constexpr (HP) {  // k chunk st: 16 dims of slot st / 2 = (first low, second low, first high, second high)
+        const int qh = qh0 + min(col, NQ - 1);
+        const int own = (qh / gq) & 1;
+        const uint16_t* qv = p.q + ((int64_t)b * p.H + qh) * 64 + 8 * hh;
 #pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        const uint4 v4 = *(const uint4*)(qv + 16 * st);
-        Aq[st] = __builtin_bit_cast(half8, col < NQ ? v4 : make_uint4(0u, 0u, 0u, 0u));
+        for (int st = 0; st < 8; ++st) {
+          const int slot = st >> 1;
+          const bool use = col < NQ && (slot & 1) == own;
+          const uint4 v4 = use ? *(const uint4*)(qv + 32 * (slot >> 1) + 16 * (st & 1))
+                               : make_uint4(0u, 0u, 0u, 0u);
+          Aq[st] = __builtin_bit_cast(half8, v4);
+        }
+      } else {
+        const uint16_t* qv = p.q + ((int64_t)b * p.H + qh0 + min(col, NQ - 1)) * kHD + 8 * hh;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+          const uint4 v4 = *(const uint4*)(qv + 16 * st);
+          Aq[st] = __builtin_bit_cast(half8, col < NQ ? v4 : make_uint4(0u, 0u, 0u, 0u));
+        }
       }
       aq_loaded = true;
     }
@@ -1297,18 +1369,43 @@ void k_decode_tok(const TokParams p) {
     const int x0 = 32 * (xt0 + x);
     const int xt = min(x0 + col, n_xtok - 1);  // clamped: tokens past n_x are masked
     int mp;
-    const uint16_t* krow = extra_row(p.xs, p.B, p.G, p.n_comp, b, hg, xt, false, &mp);
-    const uint16_t* vrow = extra_row(p.xs, p.B, p.G, p.n_comp, b, hg, xt, true, &mp);
     half8 Bk[8];
-#pragma unroll
-    for (int st = 0; st < 8; ++st) Bk[st] = __builtin_bit_cast(half8, *(const uint4*)(krow + 16 * st + 8 * hh));
     uint32_t vx[32];
-    const uint64_t vb = (uint64_t)vrow;
+    if constexpr (HP) {
+      // rows of the pair's first head (kv head 2 hg, 64 dims); the second's
+      // are nx elements on.  V: lanes 32..63 hold the second head's row.
+      int nx;
+      const uint16_t* krow = extra_row<64>(p.xs, p.B, 2 * p.G, p.n_comp, b, 2 * hg, xt, false, &mp, &nx);
+      const uint16_t* vrow = extra_row<64>(p.xs, p.B, 2 * p.G, p.n_comp, b, 2 * hg, xt, true, &mp) +
+                             (hh ? nx : 0);
 #pragma unroll
-    for (int t = 0; t < 32; ++t) {
-      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
-      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
-      vx[t] = ld_global_u32((((uint64_t)hi << 32) | lo) + 4 * lane);
+      for (int st = 0; st < 8; ++st) {
+        const int slot = st >> 1;
+        Bk[st] = __builtin_bit_cast(
+            half8, *(const uint4*)(krow + ((slot & 1) ? nx : 0) + 32 * (slot >> 1) + 16 * (st & 1) + 8 * hh));
+      }
+      const uint64_t vb = (uint64_t)vrow;
+#pragma unroll
+      for (int t = 0; t < 32; ++t) {
+        const uint32_t lo0 = __builtin_amdgcn_readlane((uint32_t)vb, t);
+        const uint32_t hi0 = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
+        const uint32_t lo1 = __builtin_amdgcn_readlane((uint32_t)vb, 32 + t);
+        const uint32_t hi1 = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), 32 + t);
+        const uint64_t row = hh ? (((uint64_t)hi1 << 32) | lo1) : (((uint64_t)hi0 << 32) | lo0);
+        vx[t] = ld_global_u32(row + 4 * (lane & 31));
+      }
+    } else {
+      const uint16_t* krow = extra_row(p.xs, p.B, p.G, p.n_comp, b, hg, xt, false, &mp);
+      const uint16_t* vrow = extra_row(p.xs, p.B, p.G, p.n_comp, b, hg, xt, true, &mp);
+#pragma unroll
+      for (int st = 0; st < 8; ++st) Bk[st] = __builtin_bit_cast(half8, *(const uint4*)(krow + 16 * st + 8 * hh));
+      const uint64_t vb = (uint64_t)vrow;
+#pragma unroll
+      for (int t = 0; t < 32; ++t) {
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)vb, t);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(vb >> 32), t);
+        vx[t] = ld_global_u32((((uint64_t)hi << 32) | lo) + 4 * lane);
+      }
     }
     float16v sacc = {};
 #pragma unroll
@@ -1397,9 +1494,14 @@ void k_decode_tok(const TokParams p) {
     }
     r0v *= (float)chh[0];
     r1v *= (float)chh[1];
-    fwht128_pairs(r0v, r1v);
+    fwht128_pairs<HP>(r0v, r1v);
     const int64_t widx = ((int64_t)b * p.H + qh0 + h) * p.n_splits + split;
-    *(float2*)(p.ws_acc + widx * kHD + 2 * lane) = make_float2(r0v + p0, r1v + p1);
+    if (HP) {  // the query head's own head: its 64 dims first in the row
+      if (hh == (((qh0 + h) / gq) & 1))
+        *(float2*)(p.ws_acc + widx * kHD + 2 * (lane & 31)) = make_float2(r0v + p0, r1v + p1);
+    } else {
+      *(float2*)(p.ws_acc + widx * kHD + 2 * lane) = make_float2(r0v + p0, r1v + p1);
+    }
     if (lane == 0) {
       p.ws_m[widx] = M;
       p.ws_l[widx] = l;
@@ -1433,16 +1535,27 @@ inline int64_t n_extra(const shard_decode_args* a) {
   return (int64_t)a->n_sink + a->n_win + a->n_dec + a->n_stream;
 }
 
-// query heads per kv head: 1, 2, or a multiple of 4 (groups of 4 per workgroup)
+// The token-tiled kernel's kv heads: head_dim-64 layers run their kv heads in
+// pairs (one 128-dim head per pair).
+inline bool head_pairs(const shard_decode_args* a) { return a->head_dim == 64; }
+inline int tok_g(const shard_decode_args* a) {
+  return head_pairs(a) ? a->n_kv_heads / 2 : a->n_kv_heads;
+}
+
+// head_dim 128, or 64 with an even number of kv heads; query heads per kernel
+// kv head: 1, 2, or a multiple of 4 (groups of 4 per workgroup)
 inline bool tok_supported(const shard_decode_args* a) {
-  if (a->head_dim != kHD || a->n_kv_heads <= 0 || a->n_q_heads <= 0) return false;
-  const int g = a->n_q_heads / a->n_kv_heads;
-  return a->n_q_heads == g * a->n_kv_heads && (g == 1 || g == 2 || (g % 4 == 0 && g <= 64)) &&
-         a->rank > 0 && a->rank % 32 == 0 && a->rank <= 192;
+  if ((a->head_dim != kHD && a->head_dim != 64) || a->n_kv_heads <= 0 || a->n_q_heads <= 0 ||
+      a->n_q_heads % a->n_kv_heads)
+    return false;
+  if (head_pairs(a) && (a->n_kv_heads & 1)) return false;
+  const int g = a->n_q_heads / tok_g(a);
+  return (g == 1 || g == 2 || (g % 4 == 0 && g <= 64)) && a->rank > 0 && a->rank % 32 == 0 &&
+         a->rank <= 192;
 }
 
 inline int tok_nq(const shard_decode_args* a) {
-  const int g = a->n_q_heads / a->n_kv_heads;
+  const int g = a->n_q_heads / tok_g(a);
   return g < 4 ? g : 4;
 }
 
@@ -1491,9 +1604,10 @@ inline TokPlan tok_plan(const shard_decode_args* a) {
   const int64_t U = 3LL * w.n_ct + w.n_xt;
   // one 8-wave workgroup per CU: n_splits x (kv heads x query groups) x batch
   // workgroups fill the CUs once
-  const int qg = a->n_q_heads / a->n_kv_heads / tok_nq(a);
+  const int G = tok_g(a);
+  const int qg = a->n_q_heads / G / tok_nq(a);
   int64_t want = a->n_splits > 0 ? a->n_splits
-                                 : std::max(1, device_cus() / std::max(1, a->n_kv_heads * qg * a->batch));
+                                 : std::max(1, device_cus() / std::max(1, G * qg * a->batch));
   want = std::min<int64_t>(std::max<int64_t>(want, 1), std::max<int64_t>(U, 1));
   int64_t per = (U + want - 1) / want;
   per = std::min<int64_t>(per, 3LL * kTokMaxTiles);  // compressed tiles per split: phase tables
@@ -1503,18 +1617,23 @@ inline TokPlan tok_plan(const shard_decode_args* a) {
 }
 
 template <int KS>
-void launch_tok(const TokParams& tp, int nq, dim3 grid, hipStream_t s) {
+void launch_tok(const TokParams& tp, int nq, bool hp, dim3 grid, hipStream_t s) {
+  if (hp) {  // head pairs: 2 or more query heads per pair
+    if (nq == 2) hipLaunchKernelGGL((k_decode_tok<KS, 2, true>), grid, dim3(kTokThreads), 0, s, tp);
+    else hipLaunchKernelGGL((k_decode_tok<KS, 4, true>), grid, dim3(kTokThreads), 0, s, tp);
+    return;
+  }
   switch (nq) {
-    case 1: hipLaunchKernelGGL((k_decode_tok<KS, 1>), grid, dim3(kTokThreads), 0, s, tp); break;
-    case 2: hipLaunchKernelGGL((k_decode_tok<KS, 2>), grid, dim3(kTokThreads), 0, s, tp); break;
-    default: hipLaunchKernelGGL((k_decode_tok<KS, 4>), grid, dim3(kTokThreads), 0, s, tp); break;
+    case 1: hipLaunchKernelGGL((k_decode_tok<KS, 1, false>), grid, dim3(kTokThreads), 0, s, tp); break;
+    case 2: hipLaunchKernelGGL((k_decode_tok<KS, 2, false>), grid, dim3(kTokThreads), 0, s, tp); break;
+    default: hipLaunchKernelGGL((k_decode_tok<KS, 4, false>), grid, dim3(kTokThreads), 0, s, tp); break;
   }
 }
 
 int launch_merge(const shard_decode_args* a, const float* ws, int nsp, hipStream_t s) {
   const int64_t nm = (int64_t)a->batch * a->n_q_heads * nsp;
   MergeParams mp;
-  mp.H = a->n_q_heads; mp.nsp = nsp;
+  mp.H = a->n_q_heads; mp.nsp = nsp; mp.hd = a->head_dim;
   mp.ws_m = ws; mp.ws_l = ws + nm; mp.ws_acc = ws + 2 * nm; mp.out = a->out;
   launch_partial_merge(mp, a->batch, s);
   SHARD_LAUNCH_CHECK("shard_decode_attn merge");
@@ -1526,9 +1645,10 @@ int decode_attn_tok(const shard_decode_args* a, float* ws, hipStream_t s) {
   const TokPlan pl = tok_plan(a);
   const int nq = tok_nq(a);
   const int64_t nm = (int64_t)a->batch * a->n_q_heads * pl.ns;
+  const bool hp = head_pairs(a);
   TokParams tp;
-  tp.B = a->batch; tp.H = a->n_q_heads; tp.G = a->n_kv_heads; tp.n_comp = a->n_comp;
-  tp.QG = a->n_q_heads / a->n_kv_heads / nq;
+  tp.B = a->batch; tp.H = a->n_q_heads; tp.G = tok_g(a); tp.n_comp = a->n_comp;
+  tp.QG = a->n_q_heads / tp.G / nq;
   tp.cstart = a->compress_start;
   tp.n_ct = pl.n_ct; tp.n_xt = pl.n_xt; tp.n_splits = pl.ns; tp.per_u = pl.per_u;
   tp.xs.sink_k = a->sink_k; tp.xs.sink_v = a->sink_v;
@@ -1541,18 +1661,18 @@ int decode_attn_tok(const shard_decode_args* a, float* ws, hipStream_t s) {
   tp.xs.n_stream_dev = a->n_stream_dev;
   tp.q = a->q; tp.inv_freq = a->inv_freq; tp.coef = a->k_coeffs;
   tp.op = (const uint4*)a->prep;
-  tp.rope = (const float2*)((const char*)a->prep + (size_t)a->n_kv_heads * 4 * (a->rank / 16 + 1) * 64 * sizeof(uint4));
+  tp.rope = (const float2*)((const char*)a->prep + (size_t)tp.G * 4 * (a->rank / 16 + 1) * 64 * sizeof(uint4));
   tp.vidx = a->v_idx; tp.vcb = a->v_codebook; tp.vch = a->v_ch;
   tp.mask = a->mask; tp.mask_stride = a->mask_stride; tp.n_sink = a->n_sink;
   tp.ws_m = ws; tp.ws_l = ws + nm; tp.ws_acc = ws + 2 * nm;
-  const dim3 grid((unsigned)((int64_t)pl.ns * a->n_kv_heads * tp.QG * a->batch));
+  const dim3 grid((unsigned)((int64_t)pl.ns * tp.G * tp.QG * a->batch));
   switch (a->rank / 16) {
-    case 2: launch_tok<2>(tp, nq, grid, s); break;
-    case 4: launch_tok<4>(tp, nq, grid, s); break;
-    case 6: launch_tok<6>(tp, nq, grid, s); break;
-    case 8: launch_tok<8>(tp, nq, grid, s); break;
-    case 10: launch_tok<10>(tp, nq, grid, s); break;
-    case 12: launch_tok<12>(tp, nq, grid, s); break;
+    case 2: launch_tok<2>(tp, nq, hp, grid, s); break;
+    case 4: launch_tok<4>(tp, nq, hp, grid, s); break;
+    case 6: launch_tok<6>(tp, nq, hp, grid, s); break;
+    case 8: launch_tok<8>(tp, nq, hp, grid, s); break;
+    case 10: launch_tok<10>(tp, nq, hp, grid, s); break;
+    case 12: launch_tok<12>(tp, nq, hp, grid, s); break;
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_decode_attn token-tiled kernel");
@@ -1580,14 +1700,18 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
                          void* stream) {
   if (!k_basis || !k_coeff_scale || !k_mean || !inv_freq || !out || n_kv_heads <= 0)
     return SHARD_ERR_ARG;
-  if (head_dim != kHD || rank <= 0 || rank % 32 != 0 || rank > 192) return SHARD_ERR_SHAPE;
-  if (out_bytes < shard_decode_prepare_bytes(n_kv_heads, rank)) return SHARD_ERR_WORKSPACE;
+  if ((head_dim != kHD && head_dim != 64) || rank <= 0 || rank % 32 != 0 || rank > 192)
+    return SHARD_ERR_SHAPE;
+  const int hp = head_dim == 64;  // head pairs: one operand image per two kv heads
+  if (hp && (n_kv_heads & 1)) return SHARD_ERR_SHAPE;
+  const int G = hp ? n_kv_heads / 2 : n_kv_heads;
+  if (out_bytes < shard_decode_prepare_bytes(G, rank)) return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   uint4* op = (uint4*)out;
-  float2* rope = (float2*)((char*)out + shard_decode_prepare_op_bytes(n_kv_heads, rank));
-  const int64_t total = (int64_t)n_kv_heads * 4 * (rank / 16 + 1) * 64 + kRopeEntries;
+  float2* rope = (float2*)((char*)out + shard_decode_prepare_op_bytes(G, rank));
+  const int64_t total = (int64_t)G * 4 * (rank / 16 + 1) * 64 + kRopeEntries;
   hipLaunchKernelGGL(k_decode_prepare, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                     k_basis, k_coeff_scale, k_mean, inv_freq, n_kv_heads, rank, op, rope);
+                     k_basis, k_coeff_scale, k_mean, inv_freq, G, rank, hp, op, rope);
   SHARD_LAUNCH_CHECK("shard_decode_prepare");
   return SHARD_OK;
 }

@@ -1,7 +1,8 @@
 // Merge of split partial rows into the attention output, shared by the
 // compressed decode call and the fp16 split-K baseline.  Layout of the
 // partial rows (one per (batch row, query head, split), row-major in that
-// order): m (base-2 running max), l (sum of 2^(s - m)), acc (128 fp32 sums).
+// order): m (base-2 running max), l (sum of 2^(s - m)), acc (128 fp32 sums,
+// of which the first `hd` are the output's: hd 64 for head_dim-64 layers).
 #pragma once
 
 #include "common.h"
@@ -25,6 +26,7 @@ constexpr int kMergeHD = 128;
 // --------------------------------------------------------------------------
 struct MergeParams {
   int32_t H, nsp;   // query heads per batch row, partial rows per query head
+  int32_t hd;       // output dims per query head: 128, or 64 (the first 64 of each row)
   const float* ws_m;
   const float* ws_l;
   const float* ws_acc;
@@ -46,6 +48,7 @@ void k_decode_merge(const MergeParams p) {
   // the MS slices of a head share one XCD (workgroups go to XCD id mod 8), so
   // one L2 fetches each 128-byte line of the partial rows once
   const int bx = blockIdx.x, slice = (bx >> 3) % MS;
+  if (slice * 2 * DP >= p.hd) return;  // a slice past the output's dims (whole workgroup)
   const int head = (bx & 7) + 8 * (bx / (8 * MS));
   const int64_t hrow = (int64_t)blockIdx.y * p.H + head;
   const int nsp = p.nsp;
@@ -101,7 +104,7 @@ void k_decode_merge(const MergeParams p) {
   if (lane < DP) wacc[w][lane] = make_float2(a0, a1);
   if (lane == 0) wl[w] = l;
   __syncthreads();
-  if (tid < DP) {
+  if (tid < DP && slice * (2 * DP) + 2 * tid < p.hd) {
     float2 t = wacc[0][tid];
     float lt = wl[0];
 #pragma unroll
@@ -114,7 +117,7 @@ void k_decode_merge(const MergeParams p) {
     half2v o;
     o[0] = (half_t)(t.x * inv_l);
     o[1] = (half_t)(t.y * inv_l);
-    *(half2v*)(p.out + hrow * kMergeHD + slice * (2 * DP) + 2 * tid) = o;
+    *(half2v*)(p.out + hrow * p.hd + slice * (2 * DP) + 2 * tid) = o;
   }
 }
 

@@ -1004,7 +1004,13 @@ __device__ __forceinline__ void rope_row(float (&t)[E], const uint16_t* __restri
 #pragma unroll
   for (int k = 0; k < E; ++k) {
     const int d = l + 64 * k;
-    const float rot = k < E / 2 ? -t[k + E / 2] : t[k - E / 2];  // rotate_half
+    float rot;  // rotate_half
+    if constexpr (E == 1) {  // head_dim 64: the partner dim is 32 lanes away
+      const float pt = __shfl_xor(t[0], 32);
+      rot = l < 32 ? -pt : pt;
+    } else {
+      rot = k < E / 2 ? -t[k + E / 2] : t[k - E / 2];
+    }
     const float a = h2f(f2h(mul_rn(t[k], h2f(c[d]))));
     const float b = h2f(f2h(mul_rn(rot, h2f(sn[d]))));
     o[k] = h2f(f2h(add_rn(a, b)));
@@ -1423,6 +1429,7 @@ static int rope_stream_launch(const uint16_t* q, const uint16_t* k, const uint16
   const int64_t rows = (int64_t)batch * (n_q_heads + 2 * n_kv_heads);
   const dim3 grid((unsigned)((rows + 3) / 4));
   switch (hd) {
+    case 64: hipLaunchKernelGGL(k_rope_stream<1>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes, row_dev, row_cap); break;
     case 128: hipLaunchKernelGGL(k_rope_stream<2>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes, row_dev, row_cap); break;
     case 256: hipLaunchKernelGGL(k_rope_stream<4>, grid, dim3(256), 0, s, q, k, v, cos, sin, cos_stride, batch, n_q_heads, n_kv_heads, q_rope, io, signs, codebook, n_codes, row_dev, row_cap); break;
     default: return SHARD_ERR_SHAPE;

@@ -465,12 +465,18 @@ class DecodeCall:
 
 def decode_supported(head_dim: int, n_q_heads: int, n_kv_heads: int, rank_pad: int) -> bool:
     """The shapes shard_decode_attn takes (its shard_decode_supported): head_dim
-    128, 1, 2 or a multiple of 4 (up to 64) query heads per kv head, rank a
+    128 with 1, 2 or a multiple of 4 (up to 64) query heads per kv head, or
+    head_dim 64 with an even number of kv heads (run in pairs as 128-dim heads)
+    and 1 or an even number (up to 32) of query heads per kv head; rank a
     multiple of 32 up to 192.  Other layers run the reference's unfused path
     (fp16 K/V rebuilt by shard_kv_reconstruct, attention.py:411)."""
-    if head_dim != 128 or n_kv_heads <= 0 or n_q_heads <= 0 or n_q_heads % n_kv_heads:
+    if head_dim not in (64, 128) or n_kv_heads <= 0 or n_q_heads <= 0 or n_q_heads % n_kv_heads:
         return False
     g = n_q_heads // n_kv_heads
+    if head_dim == 64:
+        if n_kv_heads % 2:
+            return False
+        g *= 2  # query heads per pair
     return (g in (1, 2) or (g % 4 == 0 and g <= 64)) and 0 < rank_pad <= 192 and rank_pad % 32 == 0
 
 
@@ -481,7 +487,9 @@ def decode_prepare(fmt) -> torch.Tensor:
     _require_gpu(basis, cs, mean)
     G, rank = fmt["n_kv"], fmt["rank_pad"]
     inv = fmt["inv_freq_dev"]
-    buf = torch.empty(lib.shard_decode_prepare_bytes(G, rank), dtype=torch.uint8, device=basis.device)
+    images = G // 2 if fmt["head_dim"] == 64 else G  # head_dim 64: one image per pair of kv heads
+    buf = torch.empty(lib.shard_decode_prepare_bytes(images, rank), dtype=torch.uint8,
+                      device=basis.device)
     _lib.check("shard_decode_prepare", lib.shard_decode_prepare(
         _p(basis), _p(cs), _p(mean), _p(inv), G, fmt["head_dim"], rank, _p(buf), buf.numel(),
         _stream(basis)))

@@ -96,3 +96,33 @@ def test_forced_row_split_beyond_its_extras_runs_token_tiled():
     assert ws(1, 100) != ws(2, 100)
     assert ws(1, 2048 - 68) != ws(2, 2048 - 68)   # the last count the row-split kernel takes
     assert ws(1, 2048 - 67) == ws(2, 2048 - 67)
+
+
+def test_head_dim_64_shapes_and_sizes_on_the_host():
+    """head_dim 64: the library takes an even kv head count with 1 or an even
+    number of query heads per kv head (kv heads run in pairs as 128-dim heads)
+    and agrees with ops.decode_supported; the workspace keeps 128-float partial
+    rows and the prepare buffer holds one operand image per pair.  Host-only
+    queries, no launch."""
+    from shard_amd import _lib, ops
+    lib = _lib.load()
+
+    def supported(hd, n_q, n_kv, rank=192):
+        a = _lib.DecodeArgs()
+        a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim, a.rank, a.n_comp = 1, n_q, n_kv, hd, rank, 1000
+        return lib.shard_decode_supported(ctypes.byref(a)) == 1
+
+    for hd, n_q, n_kv, want in ((64, 32, 8, True), (64, 32, 4, True), (64, 8, 8, True),
+                                (64, 4, 2, True), (64, 24, 4, True), (64, 12, 4, False),
+                                (64, 9, 3, False), (64, 4, 8, False), (64, 64, 2, True),
+                                (64, 128, 2, False), (96, 32, 8, False), (128, 24, 8, False)):
+        assert supported(hd, n_q, n_kv) == want, (hd, n_q, n_kv)
+        assert ops.decode_supported(hd, n_q, n_kv, 192) == want, (hd, n_q, n_kv)
+    assert not supported(64, 32, 8, rank=100)   # rank must be padded to a multiple of 32
+    a = _lib.DecodeArgs()
+    a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim, a.rank, a.n_comp = 2, 32, 8, 64, 192, 4000
+    a.n_splits, a.kernel = 10, 1
+    assert lib.shard_decode_attn_workspace(ctypes.byref(a)) == 2 * 32 * 10 * (128 + 2) * 4
+    assert lib.shard_decode_prepare_bytes(4, 192) < lib.shard_decode_prepare_bytes(8, 192)
+    # an odd kv head count at head_dim 64 is refused before any launch
+    assert lib.shard_decode_prepare(16, 16, 16, 16, 3, 64, 192, 16, 1 << 30, None) == -2

@@ -7,8 +7,9 @@
 * beam reordering of a compressed cache (cache.py:287-292): the dequantized
   rows are selected as the reference does, and later decode steps read the
   reordered compressed rows;
-* a head_dim-64 model: compression and decode through the original forward
-  on rebuilt K/V, every such layer-step counted.
+* head_dim-64 models: with an even kv head count every decode step is fused
+  (kv heads paired) and checked against the oracle; with one kv head decode
+  runs the original forward on rebuilt K/V, every such layer-step counted.
 """
 import pytest
 import torch
@@ -122,13 +123,56 @@ def test_reorder_cache_selects_compressed_rows(cuda):
     assert torch.equal(layer.keys, base.layers[1].keys.index_select(0, order.to(cuda)))
 
 
-def test_head_dim_64_model_compresses_and_decodes(cuda):
-    """A shape the fused kernel does not take (head_dim 64): Cache.compress
-    builds the format without the fused operands, decode steps run the original
-    forward over kv_reconstruct's K/V, and each layer-step is counted."""
+def test_head_dim_64_model_decodes_fused(cuda, monkeypatch):
+    """A head_dim-64 model (8 query heads over 2 kv heads, streaming): every
+    decode step of every compressed layer takes the fused kernel (kv heads
+    paired into 128-dim heads), none falls back, and the fused call matches
+    the fp64 oracle over the layer's own representation."""
+    from shard_amd import Cache, attention, enable_llama_fused_attention
+    model = _llama(cuda, n_q=8, n_kv=2, hd=64, hidden=512)
+    assert enable_llama_fused_attention(model)
+    seen = []
+    inner = attention.fused_attention_compressed
+
+    def record(q, layer, pos_q, inv, mask=None):
+        out = inner(q, layer, pos_q, inv, mask)
+        if layer.layer_idx == 1:
+            p = int(pos_q.reshape(-1)[-1].item()) if torch.is_tensor(pos_q) else int(pos_q)
+            seen.append((q.detach().cpu(), p, out.detach().cpu(),
+                         _oracle_format(layer._gpu_compressed), inv.cpu()))
+        return out
+    monkeypatch.setattr(attention, "fused_attention_compressed", record)
+    g = torch.Generator().manual_seed(5)
+    B, T = 2, 300
+    ids = torch.randint(0, VOCAB, (B, T), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (B, 3), generator=g).to(cuda)
+    cache = Cache.from_model(model)
+    cache._streaming = True
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        for s in range(steps.shape[1]):
+            model(steps[:, s:s + 1], past_key_values=cache, use_cache=True)
+    gc = cache.layers[0]._gpu_compressed
+    assert gc is not None and gc["head_dim"] == 64 and gc["decode_prep"] is not None
+    assert getattr(cache, "_fused_fallbacks", 0) == 0
+    assert len(seen) == 3
+    for i, (q, pos_q, out, ogc, inv) in enumerate(seen):
+        assert pos_q == T + i and ogc["stream_n"] == B * (i + 1)
+        want = exact.decode_attention(q.float().numpy().reshape(B, 8, 1, 64), ogc, 2, pos_q,
+                                      inv.numpy())
+        err, cos = compare(out.float().numpy().reshape(want.shape), want)
+        print(f"[hd64 cache] step {i} pos_q={pos_q} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= 2e-3 and cos >= 0.9999
+
+
+def test_head_dim_64_odd_kv_heads_fall_back(cuda):
+    """A shape the fused kernel does not take (head_dim 64 with one kv head:
+    no pair): Cache.compress builds the format without the fused operands,
+    decode steps run the original forward over kv_reconstruct's K/V, and each
+    layer-step is counted."""
     from transformers.models.llama.modeling_llama import LlamaAttention
     from shard_amd import Cache, enable_llama_fused_attention
-    model = _llama(cuda, n_q=8, n_kv=2, hd=64, hidden=512)
+    model = _llama(cuda, n_q=8, n_kv=1, hd=64, hidden=512)
     assert enable_llama_fused_attention(model)
     g = torch.Generator().manual_seed(5)
     ids = torch.randint(0, VOCAB, (1, 300), generator=g).to(cuda)
@@ -147,11 +191,14 @@ def test_head_dim_64_model_compresses_and_decodes(cuda):
     got, cache = run()
     gc = cache.layers[0]._gpu_compressed
     assert gc is not None and gc["head_dim"] == 64 and gc["decode_prep"] is None
+    # a 64-dim K: the bit budget drops every component, which the format keeps
+    # with zero coefficients (the reference's keep = len(k_alloc))
+    assert gc["k_alloc"] == [0] * 64 and gc["k_coeffs_shape"][1] == 64
     # layer 0 of the first decode step is not compressed yet when the forward
     # routes it (its own cache update compresses every layer), so it is not a
     # fallback; every later layer-step is
     assert cache._fused_fallbacks == 2 * steps.shape[1] - 1
-    assert "head_dim=64" in cache._last_fused_fallback
+    assert "head_dim=64" in cache._last_fused_fallback and "n_kv=1" in cache._last_fused_fallback
     patched = LlamaAttention.forward
     try:
         LlamaAttention.forward = patched.__wrapped__

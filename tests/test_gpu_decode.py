@@ -17,19 +17,19 @@ TOL_ABS = 2e-3
 TOL_COS = 0.9999
 
 
-def _run(cuda, gc, inv, q, pos_q, mask=None, n_splits=0, nkv=8, kernel=0):
+def _run(cuda, gc, inv, q, pos_q, mask=None, n_splits=0, nkv=8, kernel=0, hd=128):
     from shard_amd import ops
-    d = to_device(gc, cuda, inv, nkv=nkv)
+    d = to_device(gc, cuda, inv, nkv=nkv, hd=hd)
     B = gc["batch"]
     stream_n = gc.get("stream_n", 0) // B
     dec = (d["decode_k"], d["decode_v"]) if "decode_k" in d else None
     m = None if mask is None else torch.from_numpy(mask).to(cuda)
-    call = ops.make_decode_args(q.to(cuda).reshape(B, -1, 128), d, pos_q, None, mask=m,
+    call = ops.make_decode_args(q.to(cuda).reshape(B, -1, hd), d, pos_q, None, mask=m,
                                 n_splits=n_splits, stream_n=stream_n, decode_kv=dec)
     call.args.kernel = kernel
     out = ops.decode_attn(call)
     torch.cuda.synchronize()
-    return out.cpu().float().numpy().reshape(B, -1, 1, 128)
+    return out.cpu().float().numpy().reshape(B, -1, 1, hd)
 
 
 CASES = [
@@ -97,6 +97,58 @@ def test_decode_other_gqa_groups(cuda, case):
     err, cos = compare(got, want)
     print(f"gqa case={case} max_abs={err:.3e} cos={cos:.7f}", flush=True)
     assert err <= TOL_ABS and cos >= TOL_COS
+
+
+HD64_CASES = [
+    # (B, nkv, query heads per kv head, rank, n_comp, sink, win, n_stream, n_dec)
+    (1, 8, 4, 192, 2000, 4, 64, 10, 0),    # 32 query heads over 8 kv heads of 64 dims
+    (2, 4, 2, 128, 900, 4, 64, 40, 5),     # groups of 2: a workgroup holds both heads of a pair
+    (1, 2, 1, 64, 333, 2, 3, 3, 0),        # no grouping: 2 query heads per pair
+    (3, 2, 8, 100, 517, 4, 16, 1, 2),      # rank 100 (padded to 128), ragged tile
+    (1, 4, 16, 192, 700, 4, 64, 2100, 0),  # 32 query heads per pair, 2,168 extra tokens
+    (16, 8, 4, 128, 300, 4, 16, 1, 0),     # batch 16
+    (1, 2, 6, 96, 1, 4, 64, 0, 0),         # a single compressed token, groups of 6 (12 per pair)
+]
+
+
+@pytest.mark.parametrize("case", HD64_CASES, ids=[str(c) for c in HD64_CASES])
+def test_decode_head_dim_64_matches_exact_oracle(cuda, case):
+    """head_dim-64 layers (Llama-3.2-1B and TinyLlama shapes): the library runs
+    kv heads 2j and 2j+1 as one 128-dim head on the token-tiled kernel (the
+    reference's fused path takes any head_dim, attention.py:18-121); every
+    kernel request, explicit split counts, same bar as head_dim 128."""
+    B, nkv, gqa, rank, n_comp, sink, win, n_stream, n_dec = case
+    gc, inv = random_layer(B=B, nkv=nkv, hd=64, rank=rank, n_comp=n_comp, sink=sink, win=win,
+                           n_stream=n_stream, n_dec=n_dec, seed=3 * n_comp + gqa)
+    q = torch.randn(B, gqa * nkv, 1, 64, generator=torch.Generator().manual_seed(9)).half()
+    pos_q = sink + n_comp + win + n_dec + n_stream - 1
+    want = exact.decode_attention(q.numpy(), gc, nkv, pos_q, inv.numpy())
+    for kernel, ns in ((0, 0), (1, 0), (2, 0), (2, 1), (2, 7), (0, 300)):
+        got = _run(cuda, gc, inv, q, pos_q, nkv=nkv, kernel=kernel, n_splits=ns, hd=64)
+        err, cos = compare(got, want)
+        print(f"hd64 case={case} kernel={kernel} n_splits={ns} max_abs={err:.3e} cos={cos:.7f}",
+              flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (kernel, ns, err, cos)
+
+
+def test_decode_head_dim_64_mask_and_device_position(cuda):
+    """head_dim 64 with an additive mask over every segment, and the position
+    read from device memory giving the host position's bits."""
+    gc, inv = random_layer(B=2, nkv=4, hd=64, rank=128, n_comp=1200, n_stream=9, n_dec=3, seed=17)
+    q = torch.randn(2, 16, 1, 64, generator=torch.Generator().manual_seed(2)).half()
+    T = 4 + 1200 + 64 + 3 + 9
+    mask = np.zeros((2, T), np.float32)
+    rng = np.random.default_rng(1)
+    mask[0, rng.choice(T, 60, replace=False)] = -65504.0
+    mask[1, rng.choice(T, 60, replace=False)] = 0.75
+    want = exact.decode_attention(q.numpy(), gc, 4, T - 1, inv.numpy(), attn_mask=mask)
+    got = _run(cuda, gc, inv, q, T - 1, mask=mask, nkv=4, hd=64)
+    err, cos = compare(got, want)
+    print(f"hd64 mask max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= TOL_ABS and cos >= TOL_COS
+    host = _run(cuda, gc, inv, q, T - 1, nkv=4, hd=64)
+    dev = _run(cuda, gc, inv, q, torch.tensor([T - 1], dtype=torch.int64, device=cuda), nkv=4, hd=64)
+    assert np.array_equal(host, dev)
 
 
 def test_decode_split_counts_with_long_extras(cuda):

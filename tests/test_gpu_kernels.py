@@ -366,7 +366,9 @@ def test_k_prepare(cuda):
 @pytest.mark.parametrize("B,H,G,hd,bits,qjl,shared", [(16, 32, 8, 128, 8, False, True),
                                                       (4, 32, 8, 128, 8, False, False),
                                                       (2, 32, 8, 128, 4, True, False),
-                                                      (1, 8, 2, 256, 8, False, False)])
+                                                      (1, 8, 2, 256, 8, False, False),
+                                                      (3, 32, 8, 64, 8, False, False),
+                                                      (2, 8, 2, 64, 4, True, True)])
 def test_rope_stream_append_bitexact(cuda, B, H, G, hd, bits, qjl, shared):
     """The decode-step front end (one launch) against its two reference steps:
     transformers' apply_rotary_pos_emb on fp16 CPU tensors (the library routine

@@ -457,6 +457,28 @@ def test_compress_golden_is_sensitive_to_layout():
     assert not np.array_equal(gc["k_mean"].numpy(), g["k_mean"])
 
 
+def test_compress_with_every_component_dropped_decodes_to_the_mean():
+    """A 64-dim K (one kv head of 64 dims): the budget max(64, 64*16/20) = 64
+    bits is 5 units, below the cheapest option of a 64-component group (2 bits
+    = 8 units), so the DP drops every component.  _compress_k then keeps basis
+    and allocation whole and _build_gpu_format stores them with zero
+    coefficients (cache.py:383-392, 412-420): every int4 code is 0 (nibble 8),
+    each coefficient scale is max(0, 1e-6) / 7, and the rebuilt keys are the
+    mean exactly."""
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(1, 1, 300, 64, generator=g).half()
+    v = torch.randn(1, 1, 300, 64, generator=g).half()
+    inv = ref.default_inv_freq(10000.0, 64)
+    gc = ref.compress_layer(k, v, 0, inv, k_target_cr=20.0, max_rank=192)
+    n = 300 - 4 - 64
+    assert gc["k_coeffs_shape"] == (n, 64)
+    assert gc["alloc"] == [0] * 64
+    assert np.all(gc["k_coeffs"].numpy() == 0x88)
+    assert np.all(gc["k_coeff_scale"].numpy() == np.float16(np.float32(1e-6) / np.float32(7)))
+    kn = exact.keys_norope(gc, 1, 64)
+    assert np.array_equal(kn[0, 0], np.broadcast_to(gc["k_mean_f16"].numpy().astype(np.float64), (n, 64)))
+
+
 def _ensure_dequant_gc(f):
     B, rank, n_comp, start = int(f["batch"]), int(f["rank"]), int(f["n_comp"]), int(f["start"])
     nkv = f["sink_k"].shape[1]
