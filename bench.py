@@ -267,20 +267,31 @@ def time_sdpa(k, v, q, steps, warmup, dev, graph_len=50):
     return graph_time(fns, steps, warmup, graph_len)
 
 
-def hd64(dev, steps, warmup, contexts=(8192, 32768)):
-    """Decode on a head_dim-64 layer shaped like Llama-3.2-1B's attention (32
-    query heads over 8 kv heads of 64 dims, RoPE theta 500000; synthetic K/V of
-    bench_data's spectrum): the fused call, which runs kv heads 2j and 2j+1 as
-    one 128-dim head on the token-tiled kernel, against the path such a layer
-    took without it (the whole compressed span rebuilt to fp16 by
-    shard_kv_reconstruct, concatenated with sink and window, torch SDPA) and
-    SDPA on the uncompressed fp16 K/V.  Per-call times from graph replays over
-    rotated copies, as the headline's."""
+SHAPES = {"llama-3.2-1b": (32, 8, 64), "llama-3.2-3b": (24, 8, 128)}
+
+
+def other_shapes(dev, steps, warmup, contexts=(8192, 32768)):
+    """Decode on layers of the other Llama shapes the fused call takes (RoPE
+    theta 500000, synthetic K/V of bench_data's spectrum): Llama-3.2-1B (32
+    query heads over 8 kv heads of 64 dims: kv heads 2j and 2j+1 run as one
+    128-dim head) and Llama-3.2-3B (24 query heads over 8 kv heads of 128
+    dims: groups of 3 query heads), both on the token-tiled kernel, against the
+    path such a layer took without it (the whole compressed span rebuilt to
+    fp16 by shard_kv_reconstruct, concatenated with sink and window, torch
+    SDPA) and SDPA on the uncompressed fp16 K/V.  Per-call times from graph
+    replays over rotated copies, as the headline's."""
+    out = {}
+    for name, shape in SHAPES.items():
+        out[name] = shape_decode(dev, steps, warmup, shape, contexts)
+    return out
+
+
+def shape_decode(dev, steps, warmup, shape, contexts):
     import torch.nn.functional as F
     from shard_amd import Cache, bench_data, ops
     from shard_amd.cache import compress_layer
-    n_q, n_kv, hd = 32, 8, 64
-    res = {"workload": "one Llama-3.2-1B-shaped layer (32q/8kv heads, hd 64), batch 1"}
+    n_q, n_kv, hd = shape
+    res = {"workload": f"one layer of {n_q}q/{n_kv}kv heads, head_dim {hd}, batch 1"}
     for T in contexts:
         k, v = bench_data.make_kv(T, n_kv=n_kv, hd=hd)
         cache = Cache(num_layers=1, head_dim=hd, n_kv_heads=n_kv,
@@ -311,8 +322,8 @@ def hd64(dev, steps, warmup, contexts=(8192, 32768)):
                        "fp16_sdpa_us": round(us_sdpa, 3),
                        "speedup_vs_fp16_sdpa": round(us_sdpa / rot["median"], 3),
                        "compress_ratio": compress_ratios(fmt)}
-        print(f"[hd64] T={T} fused {rot['median']:.2f} us, unfused {us_unfused:.1f} us, "
-              f"sdpa {us_sdpa:.1f} us", flush=True)
+        print(f"[{n_q}q/{n_kv}kv hd{hd}] T={T} fused {rot['median']:.2f} us, "
+              f"unfused {us_unfused:.1f} us, sdpa {us_sdpa:.1f} us", flush=True)
         del fmt, k, v
         torch.cuda.empty_cache()
     return res
@@ -913,8 +924,9 @@ def main():
                     help="BASELINE config 4: prefill compression kernels, tokens/s")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="eager decode calls over cold layer copies at --ctx (for rocprofv3 --pmc)")
-    ap.add_argument("--hd64", action="store_true",
-                    help="decode on a head_dim-64 (Llama-3.2-1B-shaped) layer at 8K and 32K")
+    ap.add_argument("--shapes", action="store_true",
+                    help="decode on Llama-3.2-1B (head_dim 64) and -3B (3 query heads per kv "
+                         "head) layers at 8K and 32K")
     ap.add_argument("--e2e", action="store_true",
                     help="BASELINE config 5: random Llama-3.1-8B, shard cache vs fp16 cache")
     ap.add_argument("--e2e-batch", type=int, default=16)
@@ -948,8 +960,8 @@ def main():
     if args.kmeans:
         print(json.dumps(kmeans_update_bench(dev)), flush=True)
         return
-    if args.hd64:
-        print(json.dumps(hd64(dev, args.steps, args.warmup)), flush=True)
+    if args.shapes:
+        print(json.dumps(other_shapes(dev, args.steps, args.warmup)), flush=True)
         return
     if args.e2e:
         print(json.dumps(e2e(dev, args.e2e_batch, args.e2e_prompt, args.e2e_new,

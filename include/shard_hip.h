@@ -286,12 +286,13 @@ int shard_stream_dequant_qjl(const uint8_t* idx, const uint16_t* norm, const uin
  *                reference's concatenation order [sink, comp, win, dec, stream]
  *                (nullable)
  *   out          (B, H, D) fp16
- * H / G (query heads per kv head) is 1, 2 or a multiple of 4 (<= 64).  rank
- * must be a multiple of 32 (<= 192); pad coefficients and basis with zeros
- * otherwise.  head_dim 64 needs an even G and H / G 1 or even (<= 32): the
- * kernel runs kv heads 2j and 2j+1 as one 128-dim head (the token-tiled
- * kernel; `prep` from shard_decode_prepare with head_dim 64), every layout
- * above with D = 64 as it stands.  Any number of sink, window, decode and stream tokens (the
+ * H / G (query heads per kv head) is at most 64 (128 / D up to 32 at D = 64):
+ * the token-tiled kernel takes them in groups of 4, 3, 2 or 1 (the largest
+ * that divides the count) per workgroup.  rank must be a multiple of 32
+ * (<= 192); pad coefficients and basis with zeros otherwise.  head_dim 64
+ * needs an even G: the kernel runs kv heads 2j and 2j+1 as one 128-dim head
+ * (the token-tiled kernel; `prep` from shard_decode_prepare with head_dim
+ * 64), every layout above with D = 64 as it stands.  Any number of sink, window, decode and stream tokens (the
  * reference appends without limit, cache.py:156-181).  The softmax and all
  * sums run in fp32.
  * Replaces fused_attention_compressed (attention.py:270-343) with its
@@ -356,10 +357,9 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
                          int32_t head_dim, int32_t rank, void* out, size_t out_bytes,
                          void* stream);
 
-/* 1 when shard_decode_attn takes the shapes in `args` (head_dim 128 with query
- * heads per kv head 1, 2 or a multiple of 4 up to 64, or head_dim 64 with an
- * even number of kv heads and 1 or an even number up to 32 query heads per kv
- * head; rank a multiple of 32 up to 192),
+/* 1 when shard_decode_attn takes the shapes in `args` (head_dim 128 with up
+ * to 64 query heads per kv head, or head_dim 64 with an even number of kv
+ * heads and up to 32 query heads per kv head; rank a multiple of 32 up to 192),
  * else 0: the caller then rebuilds fp16 K/V (shard_kv_reconstruct) and runs
  * plain attention, as the reference's unfused path does (attention.py:411). */
 int shard_decode_supported(const shard_decode_args* args);

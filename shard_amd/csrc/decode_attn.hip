@@ -953,7 +953,7 @@ __device__ __forceinline__ int pair_k(int i) {
 template <int KS, int NQ, bool HP>
 __global__ __launch_bounds__(kTokThreads, 1)
 void k_decode_tok(const TokParams p) {
-  static_assert(NQ == 1 || NQ == 2 || NQ == 4, "query heads per workgroup");
+  static_assert(NQ >= 1 && NQ <= 4, "query heads per workgroup");
   constexpr int NW = kTokWaves;
   constexpr int NE = NQ < 4 ? NQ : 4;  // score elements holding heads, per lane half
   __shared__ __align__(16) TokLds<KS, NQ> L;
@@ -964,8 +964,8 @@ void k_decode_tok(const TokParams p) {
   const int col = lane & 31;
   const int hh = lane >> 5;
 
-  // ---- block -> (kv head, query group, batch row, split).  A kv head with
-  // more than 4 query heads is split into QG groups of NQ = 4, each its own
+  // ---- block -> (kv head, query group, batch row, split).  A kv head's
+  // query heads are split into QG groups of NQ (4, 3, 2 or 1), each its own
   // workgroup.  The dispatcher deals blocks to the 8 XCDs in turn (block id
   // mod 8); with B n_splits % 8 == 0 the heads of one (batch row, split)
   // share an XCD, whose L2 then fetches the split's coefficient rows (read by
@@ -1542,21 +1542,21 @@ inline int tok_g(const shard_decode_args* a) {
   return head_pairs(a) ? a->n_kv_heads / 2 : a->n_kv_heads;
 }
 
-// head_dim 128, or 64 with an even number of kv heads; query heads per kernel
-// kv head: 1, 2, or a multiple of 4 (groups of 4 per workgroup)
+// head_dim 128, or 64 with an even number of kv heads; up to 64 query heads
+// per kernel kv head, in groups of NQ (4, 3, 2 or 1: the largest dividing the
+// count) per workgroup
 inline bool tok_supported(const shard_decode_args* a) {
   if ((a->head_dim != kHD && a->head_dim != 64) || a->n_kv_heads <= 0 || a->n_q_heads <= 0 ||
       a->n_q_heads % a->n_kv_heads)
     return false;
   if (head_pairs(a) && (a->n_kv_heads & 1)) return false;
   const int g = a->n_q_heads / tok_g(a);
-  return (g == 1 || g == 2 || (g % 4 == 0 && g <= 64)) && a->rank > 0 && a->rank % 32 == 0 &&
-         a->rank <= 192;
+  return g <= 64 && a->rank > 0 && a->rank % 32 == 0 && a->rank <= 192;
 }
 
 inline int tok_nq(const shard_decode_args* a) {
   const int g = a->n_q_heads / tok_g(a);
-  return g < 4 ? g : 4;
+  return g % 4 == 0 ? 4 : g % 3 == 0 ? 3 : g % 2 == 0 ? 2 : 1;
 }
 
 inline bool split_supported(const shard_decode_args* a) {
@@ -1618,14 +1618,18 @@ inline TokPlan tok_plan(const shard_decode_args* a) {
 
 template <int KS>
 void launch_tok(const TokParams& tp, int nq, bool hp, dim3 grid, hipStream_t s) {
-  if (hp) {  // head pairs: 2 or more query heads per pair
-    if (nq == 2) hipLaunchKernelGGL((k_decode_tok<KS, 2, true>), grid, dim3(kTokThreads), 0, s, tp);
-    else hipLaunchKernelGGL((k_decode_tok<KS, 4, true>), grid, dim3(kTokThreads), 0, s, tp);
+  if (hp) {  // head pairs: an even number of query heads per pair, groups of 2, 3 or 4
+    switch (nq) {
+      case 2: hipLaunchKernelGGL((k_decode_tok<KS, 2, true>), grid, dim3(kTokThreads), 0, s, tp); break;
+      case 3: hipLaunchKernelGGL((k_decode_tok<KS, 3, true>), grid, dim3(kTokThreads), 0, s, tp); break;
+      default: hipLaunchKernelGGL((k_decode_tok<KS, 4, true>), grid, dim3(kTokThreads), 0, s, tp); break;
+    }
     return;
   }
   switch (nq) {
     case 1: hipLaunchKernelGGL((k_decode_tok<KS, 1, false>), grid, dim3(kTokThreads), 0, s, tp); break;
     case 2: hipLaunchKernelGGL((k_decode_tok<KS, 2, false>), grid, dim3(kTokThreads), 0, s, tp); break;
+    case 3: hipLaunchKernelGGL((k_decode_tok<KS, 3, false>), grid, dim3(kTokThreads), 0, s, tp); break;
     default: hipLaunchKernelGGL((k_decode_tok<KS, 4, false>), grid, dim3(kTokThreads), 0, s, tp); break;
   }
 }

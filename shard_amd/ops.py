@@ -465,11 +465,11 @@ class DecodeCall:
 
 def decode_supported(head_dim: int, n_q_heads: int, n_kv_heads: int, rank_pad: int) -> bool:
     """The shapes shard_decode_attn takes (its shard_decode_supported): head_dim
-    128 with 1, 2 or a multiple of 4 (up to 64) query heads per kv head, or
-    head_dim 64 with an even number of kv heads (run in pairs as 128-dim heads)
-    and 1 or an even number (up to 32) of query heads per kv head; rank a
-    multiple of 32 up to 192.  Other layers run the reference's unfused path
-    (fp16 K/V rebuilt by shard_kv_reconstruct, attention.py:411)."""
+    128 with up to 64 query heads per kv head, or head_dim 64 with an even
+    number of kv heads (run in pairs as 128-dim heads) and up to 32 query heads
+    per kv head; rank a multiple of 32 up to 192.  Other layers run the
+    reference's unfused path (fp16 K/V rebuilt by shard_kv_reconstruct,
+    attention.py:411)."""
     if head_dim not in (64, 128) or n_kv_heads <= 0 or n_q_heads <= 0 or n_q_heads % n_kv_heads:
         return False
     g = n_q_heads // n_kv_heads
@@ -477,7 +477,7 @@ def decode_supported(head_dim: int, n_q_heads: int, n_kv_heads: int, rank_pad: i
         if n_kv_heads % 2:
             return False
         g *= 2  # query heads per pair
-    return (g in (1, 2) or (g % 4 == 0 and g <= 64)) and 0 < rank_pad <= 192 and rank_pad % 32 == 0
+    return g <= 64 and 0 < rank_pad <= 192 and rank_pad % 32 == 0
 
 
 def decode_prepare(fmt) -> torch.Tensor:

@@ -98,12 +98,13 @@ def test_forced_row_split_beyond_its_extras_runs_token_tiled():
     assert ws(1, 2048 - 67) == ws(2, 2048 - 67)
 
 
-def test_head_dim_64_shapes_and_sizes_on_the_host():
-    """head_dim 64: the library takes an even kv head count with 1 or an even
-    number of query heads per kv head (kv heads run in pairs as 128-dim heads)
-    and agrees with ops.decode_supported; the workspace keeps 128-float partial
-    rows and the prepare buffer holds one operand image per pair.  Host-only
-    queries, no launch."""
+def test_decode_shapes_and_sizes_on_the_host():
+    """Up to 64 query heads per kv head at head_dim 128 (any count: groups of
+    4, 3, 2 or 1 per workgroup), and head_dim 64 with an even kv head count
+    (kv heads run in pairs as 128-dim heads, up to 32 query heads per kv head);
+    the library agrees with ops.decode_supported; at head_dim 64 the workspace
+    keeps 128-float partial rows and the prepare buffer holds one operand image
+    per pair.  Host-only queries, no launch."""
     from shard_amd import _lib, ops
     lib = _lib.load()
 
@@ -113,9 +114,11 @@ def test_head_dim_64_shapes_and_sizes_on_the_host():
         return lib.shard_decode_supported(ctypes.byref(a)) == 1
 
     for hd, n_q, n_kv, want in ((64, 32, 8, True), (64, 32, 4, True), (64, 8, 8, True),
-                                (64, 4, 2, True), (64, 24, 4, True), (64, 12, 4, False),
+                                (64, 4, 2, True), (64, 24, 4, True), (64, 12, 4, True),
                                 (64, 9, 3, False), (64, 4, 8, False), (64, 64, 2, True),
-                                (64, 128, 2, False), (96, 32, 8, False), (128, 24, 8, False)):
+                                (64, 66, 2, False), (64, 128, 2, False), (96, 32, 8, False),
+                                (128, 24, 8, True), (128, 40, 8, True), (128, 56, 8, True),
+                                (128, 512, 8, True), (128, 520, 8, False), (128, 12, 8, False)):
         assert supported(hd, n_q, n_kv) == want, (hd, n_q, n_kv)
         assert ops.decode_supported(hd, n_q, n_kv, 192) == want, (hd, n_q, n_kv)
     assert not supported(64, 32, 8, rank=100)   # rank must be padded to a multiple of 32

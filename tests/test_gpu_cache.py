@@ -7,9 +7,10 @@
 * beam reordering of a compressed cache (cache.py:287-292): the dequantized
   rows are selected as the reference does, and later decode steps read the
   reordered compressed rows;
-* head_dim-64 models: with an even kv head count every decode step is fused
-  (kv heads paired) and checked against the oracle; with one kv head decode
-  runs the original forward on rebuilt K/V, every such layer-step counted.
+* a head_dim-64 model with an even kv head count (kv heads paired) and
+  Llama-3.2-3B's 3 query heads per kv head: every decode step is fused and
+  checked against the oracle; head_dim 64 with one kv head: decode runs the
+  original forward on rebuilt K/V, every such layer-step counted.
 """
 import pytest
 import torch
@@ -123,13 +124,16 @@ def test_reorder_cache_selects_compressed_rows(cuda):
     assert torch.equal(layer.keys, base.layers[1].keys.index_select(0, order.to(cuda)))
 
 
-def test_head_dim_64_model_decodes_fused(cuda, monkeypatch):
-    """A head_dim-64 model (8 query heads over 2 kv heads, streaming): every
-    decode step of every compressed layer takes the fused kernel (kv heads
-    paired into 128-dim heads), none falls back, and the fused call matches
-    the fp64 oracle over the layer's own representation."""
+@pytest.mark.parametrize("n_q,n_kv,hd", [(8, 2, 64), (24, 8, 128)],
+                         ids=["hd64-gqa4", "llama32-3b-gqa3"])
+def test_other_shapes_decode_fused(cuda, monkeypatch, n_q, n_kv, hd):
+    """A head_dim-64 model (8 query heads over 2 kv heads: kv heads paired into
+    128-dim heads) and Llama-3.2-3B's grouping (24 query heads over 8 kv heads,
+    groups of 3), streaming: every decode step of every compressed layer takes
+    the fused kernel, none falls back, and the fused call matches the fp64
+    oracle over the layer's own representation."""
     from shard_amd import Cache, attention, enable_llama_fused_attention
-    model = _llama(cuda, n_q=8, n_kv=2, hd=64, hidden=512)
+    model = _llama(cuda, n_q=n_q, n_kv=n_kv, hd=hd, hidden=n_q * hd)
     assert enable_llama_fused_attention(model)
     seen = []
     inner = attention.fused_attention_compressed
@@ -153,15 +157,16 @@ def test_head_dim_64_model_decodes_fused(cuda, monkeypatch):
         for s in range(steps.shape[1]):
             model(steps[:, s:s + 1], past_key_values=cache, use_cache=True)
     gc = cache.layers[0]._gpu_compressed
-    assert gc is not None and gc["head_dim"] == 64 and gc["decode_prep"] is not None
+    assert gc is not None and gc["head_dim"] == hd and gc["decode_prep"] is not None
     assert getattr(cache, "_fused_fallbacks", 0) == 0
     assert len(seen) == 3
     for i, (q, pos_q, out, ogc, inv) in enumerate(seen):
         assert pos_q == T + i and ogc["stream_n"] == B * (i + 1)
-        want = exact.decode_attention(q.float().numpy().reshape(B, 8, 1, 64), ogc, 2, pos_q,
+        want = exact.decode_attention(q.float().numpy().reshape(B, n_q, 1, hd), ogc, n_kv, pos_q,
                                       inv.numpy())
         err, cos = compare(out.float().numpy().reshape(want.shape), want)
-        print(f"[hd64 cache] step {i} pos_q={pos_q} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        print(f"[{n_q}q/{n_kv}kv hd{hd} cache] step {i} pos_q={pos_q} max_abs={err:.3e} "
+              f"cos={cos:.7f}", flush=True)
         assert err <= 2e-3 and cos >= 0.9999
 
 

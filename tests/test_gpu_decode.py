@@ -80,13 +80,18 @@ GQA_CASES = [
     (1, 4, 8, 192, 2000, 70),   # 8 query heads per kv head: two workgroups of 4 per head
     (3, 2, 8, 64, 333, 5),
     (1, 2, 16, 128, 700, 3),    # 16 query heads per kv head
+    (1, 8, 3, 192, 3000, 20),   # Llama-3.2-3B's 24 query heads over 8 kv heads: groups of 3
+    (2, 4, 6, 128, 800, 9),     # two groups of 3 per kv head
+    (1, 4, 5, 160, 640, 2),     # 5 per kv head: five single-head workgroups
+    (2, 2, 12, 192, 500, 4),    # three groups of 4
 ]
 
 
 @pytest.mark.parametrize("case", GQA_CASES, ids=[str(c) for c in GQA_CASES])
 def test_decode_other_gqa_groups(cuda, case):
-    """Query-head groups of 1, 2, 8 and 16 on the token-tiled kernel (the
-    reference's fused path takes any n_q / n_kv, attention.py:18-81)."""
+    """Query-head groups of 1, 2, 3, 5, 6, 8, 12 and 16 on the token-tiled
+    kernel (the reference's fused path takes any n_q / n_kv,
+    attention.py:18-81)."""
     B, nkv, gqa, rank, n_comp, n_stream = case
     gc, inv = random_layer(B=B, nkv=nkv, rank=rank, n_comp=n_comp, n_stream=n_stream,
                            seed=7 * gqa + n_comp)
@@ -108,6 +113,8 @@ HD64_CASES = [
     (1, 4, 16, 192, 700, 4, 64, 2100, 0),  # 32 query heads per pair, 2,168 extra tokens
     (16, 8, 4, 128, 300, 4, 16, 1, 0),     # batch 16
     (1, 2, 6, 96, 1, 4, 64, 0, 0),         # a single compressed token, groups of 6 (12 per pair)
+    (1, 4, 3, 128, 1500, 4, 64, 30, 0),    # 3 per kv head: groups of 3 over a pair's 6
+    (2, 2, 5, 64, 400, 4, 32, 7, 3),       # 5 per kv head: groups of 2 over a pair's 10
 ]
 
 
