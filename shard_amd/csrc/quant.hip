@@ -15,20 +15,23 @@ namespace shard {
 
 // Dequantized group value of one coefficient (quantize_group then
 // dequantize_group): y = code/L*rng + lo, code = clamp(rint(clamp((x-lo)/rng,0,1)*L),0,L).
-__device__ __forceinline__ float group_deq(float x, int bits, float lo, float rng,
-                                           uint8_t* code_out) {
-  if (bits <= 0) {
-    *code_out = 0;
-    return 0.f;
-  }
+__device__ __forceinline__ int group_code(float x, int bits, float lo, float rng) {
+  if (bits <= 0) return 0;
   const float L = (float)((1 << bits) - 1);
   float v = div_rn(sub_rn(x, lo), rng);
   v = fminf(fmaxf(v, 0.f), 1.f);
   v = mul_rn(v, L);
-  float code = rintf(v);  // round half to even, as torch.round
-  code = fminf(fmaxf(code, 0.f), L);
-  *code_out = (uint8_t)(int)code;
-  return add_rn(mul_rn(div_rn(code, L), rng), lo);
+  const float code = rintf(v);  // round half to even, as torch.round
+  return (int)fminf(fmaxf(code, 0.f), L);
+}
+
+__device__ __forceinline__ float group_deq(float x, int bits, float lo, float rng,
+                                           uint8_t* code_out) {
+  const int code = group_code(x, bits, lo, rng);
+  *code_out = (uint8_t)code;
+  if (bits <= 0) return 0.f;
+  const float L = (float)((1 << bits) - 1);
+  return add_rn(mul_rn(div_rn((float)code, L), rng), lo);
 }
 
 // The column reductions write one partial per (block, column) and a wave per
@@ -98,6 +101,108 @@ __global__ void k_int4_fold_minmax(const uint32_t* __restrict__ pmin,
     lo[c] = lv;
     rng[c] = fmaxf(sub_rn(ord2f(b), lv), 1e-6f);
   }
+}
+
+// One wave per column: the column's lo, rng, coefficient scale and int4
+// table from its min and max alone.  The group code, and with it the
+// dequantized value y, never decreases as x grows (every step of group_deq is
+// a monotone rounding of a monotone function of x for rng > 0), so the
+// column's largest |y| is |y| of its smallest or of its largest element, both
+// computed here with the arithmetic the element pass uses: cs = max(max |y|,
+// 1e-6) / 7 is the reference's (cache.py:417-418) without a pass over the
+// elements (finite projections; a non-finite element breaks the order).
+__global__ void k_int4_fold(const uint32_t* __restrict__ pmin, const uint32_t* __restrict__ pmax,
+                            int nblk, int keep, const int32_t* __restrict__ bits,
+                            float* __restrict__ clo, float* __restrict__ crng,
+                            int8_t* __restrict__ qtab, float* coeff_scale, float* lo_out,
+                            float* rng_out) {
+  const int c = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6), l = (int)lane_id();
+  if (c >= keep) return;  // whole waves
+  uint32_t a = 0xFFFFFFFFu, bmax = 0u;
+  for (int q = l; q < nblk; q += 64) {
+    a = u32min(a, pmin[(int64_t)q * keep + c]);
+    bmax = u32max(bmax, pmax[(int64_t)q * keep + c]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a = u32min(a, __shfl_xor(a, o));
+    bmax = u32max(bmax, __shfl_xor(bmax, o));
+  }
+  const float lv = ord2f(a), xmax = ord2f(bmax);
+  const float rv = fmaxf(sub_rn(xmax, lv), 1e-6f);
+  const int b = bits[c];
+  uint8_t k0, k1;
+  const float y0 = group_deq(lv, b, lv, rv, &k0), y1 = group_deq(xmax, b, lv, rv, &k1);
+  const float cs = div_rn(fmaxf(fmaxf(fabsf(y0), fabsf(y1)), 1e-6f), 7.0f);
+  for (int code = l; code < 256; code += 64) {
+    float y = 0.f;  // columns without bits have y = 0 (code 0)
+    if (b > 0 && code < (1 << b)) {
+      const float L = (float)((1 << b) - 1);
+      y = add_rn(mul_rn(div_rn((float)code, L), rv), lv);
+    }
+    qtab[c * 256 + code] = (int8_t)fminf(fmaxf(rintf(div_rn(y, cs)), -7.f), 7.f);
+  }
+  if (l == 0) {
+    clo[c] = lv;
+    crng[c] = rv;
+    coeff_scale[c] = cs;
+    if (lo_out) lo_out[c] = b > 0 ? lv : 0.f;
+    if (rng_out) rng_out[c] = b > 0 ? rv : 0.f;
+  }
+}
+
+// Group codes and packed int4 values of one slab of rows, straight from the
+// projection (keep even: an element's nibble pair lies in its row).  Thread
+// (c, g) takes column c of rows r0 + g, r0 + g + RG, ..., eight rows in
+// flight; q = qtab[c][code] (k_int4_fold's table).  The waves hold 64
+// consecutive columns of a row, so the nibbles of 8 columns meet in one lane
+// by three DPP moves and go out as one 32-bit word (words: keep % 8 == 0 and
+// a 4-byte aligned output; else each even column stores its byte).
+template <bool WORDS, bool CODES>
+__global__ __launch_bounds__(1024) void k_int4_pack_rows(const float* __restrict__ proj, int64_t n,
+                                                         int keep, int64_t rows_per_block,
+                                                         const int32_t* __restrict__ bits,
+                                                         const float* __restrict__ clo,
+                                                         const float* __restrict__ crng,
+                                                         const int8_t* __restrict__ qtab,
+                                                         uint8_t* __restrict__ codes,
+                                                         uint8_t* __restrict__ packed) {
+  const int c = threadIdx.x, rg = threadIdx.y, RG = blockDim.y;
+  const int l = (int)lane_id();
+  const bool col_ok = c < keep;
+  const int cc = col_ok ? c : keep - 1;  // lanes past the last column read a valid column
+  const int b = bits[cc];
+  const float lv = clo[cc], rv = crng[cc];
+  const int8_t* qt = qtab + cc * 256;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
+  const bool store = col_ok && (WORDS ? (l & 7) == 0 : (c & 1) == 0);
+  const int64_t step = (int64_t)RG * keep;
+  int64_t e = (r0 + rg) * keep + cc;  // element of this thread's next row
+  auto emit = [&](float x) {  // all lanes of the wave (DPP moves)
+    const int code = group_code(x, b, lv, rv);
+    const uint32_t nib = col_ok ? (uint32_t)((qt[code] + 8) & 15) : 8u;
+    if (CODES && col_ok) codes[e] = (uint8_t)code;
+    // DPP moves within rows of 16 lanes: lane c takes lane c ^ 1, c ^ 2, c + 4
+    uint32_t t = nib | ((uint32_t)__builtin_amdgcn_mov_dpp((int)nib, kDppXor1, 0xF, 0xF, false) << 4);
+    if (WORDS) {
+      t |= (uint32_t)__builtin_amdgcn_mov_dpp((int)t, kDppXor2, 0xF, 0xF, false) << 8;
+      t |= (uint32_t)__builtin_amdgcn_mov_dpp((int)t, kDppRor12, 0xF, 0xF, false) << 16;
+      if (store) *(uint32_t*)(packed + e / 2) = t;
+    } else if (store) {
+      packed[e / 2] = (uint8_t)t;  // even lanes: the byte of columns c, c + 1
+    }
+    e += step;
+  };
+  int64_t r = r0 + rg;
+  for (; r + 7 * RG < r1; r += 8 * RG) {  // uniform per wave (one row group)
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = proj[e + i * step];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) emit(x[i]);
+  }
+  for (; r < r1; r += RG) emit(proj[e]);
 }
 
 // Column max |y| of the dequantized values of one slab, and the group codes.
@@ -1180,9 +1285,10 @@ extern "C" {
 size_t shard_int4_quant_pack_workspace(int64_t n_rows, int32_t keep) {
   if (n_rows <= 0 || keep <= 0) return 0;
   // pmin, pmax, pamax partials (kI4Blocks x keep), lo, rng (keep), the int4
-  // table (keep x 256 bytes) and the group codes (n_rows x keep bytes)
+  // table (keep x 256 bytes) and, for an odd keep (whose nibble pairs cross
+  // rows: a separate packing pass), the group codes (n_rows x keep bytes)
   return (size_t)(3 * kI4Blocks + 2) * keep * sizeof(uint32_t) + (size_t)keep * 256 +
-         (size_t)n_rows * keep;
+         ((keep & 1) ? (size_t)n_rows * keep : 0);
 }
 
 int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const int32_t* bits,
@@ -1208,6 +1314,28 @@ int shard_int4_quant_pack(const float* proj, int64_t n_rows, int32_t keep, const
   const dim3 cgrid((unsigned)nblk), cblock(tpb, rg);
   const dim3 fgrid((unsigned)((keep + 3) / 4)), fblock(256);  // a wave per column
   hipLaunchKernelGGL(k_int4_minmax, cgrid, cblock, 0, s, proj, n_rows, keep, rpb, pmin, pmax);
+  if ((keep & 1) == 0) {
+    // two passes over the projection: column min/max, then codes + packing
+    hipLaunchKernelGGL(k_int4_fold, fgrid, fblock, 0, s, pmin, pmax, (int)nblk, keep, bits, clo,
+                       crng, qtab, coeff_scale, lo, rng);
+    // the element pass has no partials to bound its grid: slabs of 16 rows
+    // per thread (two rounds of eight loads in flight), about one round of
+    // workgroups at config 4's 32K rows
+    const int words = (keep & 7) == 0 && ((uintptr_t)packed & 3) == 0;
+    const int64_t pblk = grid_cap((n_rows + 16 * rg - 1) / (16 * rg), 1 << 20);
+    const int64_t prpb = (n_rows + pblk - 1) / pblk;  // rows per block
+#define SHARD_PACK(W, C)                                                                     \
+  hipLaunchKernelGGL((k_int4_pack_rows<W, C>), dim3((unsigned)pblk), cblock, 0, s, proj, n_rows, \
+                     keep, prpb, bits, clo, crng, qtab, codes, packed)
+    if (words) {
+      if (codes) SHARD_PACK(true, true); else SHARD_PACK(true, false);
+    } else {
+      if (codes) SHARD_PACK(false, true); else SHARD_PACK(false, false);
+    }
+#undef SHARD_PACK
+    SHARD_LAUNCH_CHECK("shard_int4_quant_pack");
+    return SHARD_OK;
+  }
   hipLaunchKernelGGL(k_int4_fold_minmax, fgrid, fblock, 0, s, pmin, pmax, (int)nblk, keep, clo, crng);
   hipLaunchKernelGGL(k_int4_absmax, cgrid, cblock, 0, s, proj, n_rows, keep, rpb, bits, clo, crng,
                      pamax, ccodes);

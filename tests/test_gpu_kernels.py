@@ -21,14 +21,24 @@ def _ops():
     (33, [8] * 10 + [4] * 6),
     (7, [3] * 20 + [0] * 5 + [5] * 10),  # odd element count: a padded last nibble
     (1, [2] * 32),
+    (300, [4] * 30 + [2] * 12),          # even keep, not a multiple of 8: byte stores
+    (2049, [1] * 8 + [7] * 56 + [4] * 64),  # constant, near-constant and one-sided columns
 ])
 def test_int4_quant_pack_bitexact(cuda, n, alloc, want_codes):
+    """Even keep takes two passes (column min/max, then codes and packing, the
+    coefficient scale from each column's extreme elements); odd keep the
+    three-pass chain.  Both bit-exact against the oracle's chain."""
     ops = _ops()
     keep = len(alloc)
     rng = np.random.default_rng(n)
     proj = (rng.standard_normal((n, keep)) * np.exp(-np.arange(keep) / 60.0)).astype(np.float32)
     if n > 2:
         proj[rng.integers(0, n, 3), rng.integers(0, keep, 3)] = 0.0
+    if n == 2049:
+        proj[:, 0] = 0.75                                            # constant: rng clamps to 1e-6
+        proj[:, 1] = -3.0 + rng.random(n).astype(np.float32) * 4e-7   # range below 1e-6
+        proj[:, 2] = np.abs(proj[:, 2]) + 5.0                        # all positive, lo far from 0
+        proj[:, 3] = -np.abs(proj[:, 3]) - 5.0                       # all negative
     want = ref.k_code_chain(proj, alloc)
     got = ops.int4_quant_pack(torch.from_numpy(proj).to(cuda),
                               torch.tensor(alloc, dtype=torch.int32), want_codes=want_codes)
