@@ -13,11 +13,11 @@ pytestmark = pytest.mark.gpu
 VOCAB = 512
 
 
-def _model(dev):
+def _model(dev, n_q=8, n_kv=2, hd=128):
     from transformers import LlamaConfig, LlamaForCausalLM
-    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=1024, intermediate_size=512,
-                      num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
-                      head_dim=128, max_position_embeddings=4096, rope_theta=500000.0)
+    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=n_q * hd, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=n_q, num_key_value_heads=n_kv,
+                      head_dim=hd, max_position_embeddings=4096, rope_theta=500000.0)
     torch.manual_seed(0)
     return LlamaForCausalLM(cfg).to(dev, torch.float16).eval()
 
@@ -43,11 +43,15 @@ def _compare(got, want, what):
     assert err <= 1e-2 * max(scale, 1.0) and cos >= 0.9999, (what, err, cos)
 
 
-@pytest.mark.parametrize("B,qjl,kernel", [(1, False, 0), (3, False, 0), (2, True, 0), (2, False, 2)])
-def test_decode_graph_matches_eager_steps(cuda, B, qjl, kernel):
+@pytest.mark.parametrize("B,qjl,kernel,shape", [(1, False, 0, (8, 2, 128)), (3, False, 0, (8, 2, 128)),
+                                                (2, True, 0, (8, 2, 128)), (2, False, 2, (8, 2, 128)),
+                                                (2, False, 0, (8, 2, 64)), (2, False, 0, (12, 4, 128))],
+                         ids=["b1", "b3", "b2-qjl", "b2-tok", "b2-hd64", "b2-gqa3"])
+def test_decode_graph_matches_eager_steps(cuda, B, qjl, kernel, shape):
+    """Also a head_dim-64 model (kv heads paired) and 3 query heads per kv head."""
     from shard import enable_llama_fused_attention
     from shard_amd.graph import DecodeGraph
-    model = _model(cuda)
+    model = _model(cuda, *shape)
     assert enable_llama_fused_attention(model)
     g = torch.Generator().manual_seed(B)
     ids = torch.randint(0, VOCAB, (B, 300), generator=g).to(cuda)
