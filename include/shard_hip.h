@@ -48,7 +48,8 @@ size_t shard_decode_args_size(void);
 
 /* PCA projection GEMM on MFMA: C[m, n] (fp32) = A[m, k] (fp16) . Bt[n, k]^T (fp16).
  * A row-major with row stride lda (elements), Bt row-major (n rows of k),
- * C row-major with row stride ldc.  k % 16 == 0, n % 32 == 0, n <= 256.
+ * C row-major with row stride ldc.  k % 16 == 0, n % 32 == 0 (one launch per
+ * 256 columns: ranks above 256 take several).
  * Replaces the projection GEMM of _compress_k, cache.py:392
  * ((flat - mean) @ (basis_q * scale)). */
 int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_t lda,
@@ -58,8 +59,8 @@ int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_t lda,
 /* The same projection with fp32 operands, as the reference computes it
  * (cache.py:389-392: (flat - mean) @ (basis_q.float() * scale.float()), fp32):
  * C[m, n] = A[m, k] (fp32) . Bt[n, k]^T (fp32) on v_mfma_f32_32x32x2_f32,
- * fp32 sums.  k % 8 == 0, n % 32 == 0, n <= 256, lda % 4 == 0, a and bt
- * 16-byte aligned.  The path Cache.compress takes. */
+ * fp32 sums.  k % 8 == 0, n % 32 == 0 (one launch per 256 columns),
+ * lda % 4 == 0, a and bt 16-byte aligned.  The path Cache.compress takes. */
 int shard_pca_project_f32(const float* a, int64_t m, int32_t k, int64_t lda,
                           const float* bt, int32_t n, float* c, int64_t ldc,
                           void* stream);
@@ -391,7 +392,10 @@ int shard_decode_attn_noalloc(const shard_decode_args* args, void* stream);
  *   K: fp16(fp16(sum_r fp16(nib*cs) * basis) + mean), then RoPE re-applied at
  *      positions compress_start + t with fp32 phases fl(pos*theta), fp16 out;
  *   V: fp16(hadamard(cb[idx] * ch)) (hadamard in fp32, bit-exact).
- * k_out / v_out: (B, G, n_comp, D) fp16 contiguous. */
+ * k_out / v_out: (B, G, n_comp, D) fp16 contiguous.  D = 64, 128 or 256; any
+ * even rank whose (32 + D) x rank fp16 staging fits 160 KB of LDS (rank <= 512
+ * at D = 128), so layers the fused call does not take (rank above 192) decode
+ * through it. */
 int shard_kv_reconstruct(const shard_decode_args* args, uint16_t* k_out,
                          uint16_t* v_out, void* stream);
 

@@ -11,6 +11,8 @@
 // (rows past m, k past the row end) are handled by an out-of-range offset that
 // the hardware answers with zeros: no load sits under a branch, so the
 // compiler's wait counters stay exact and a chunk waits only for its own data.
+#include <algorithm>
+
 #include "common.h"
 
 namespace shard {
@@ -447,29 +449,38 @@ __global__ void k_rope_phases(int start, int n, int hd2, const float* __restrict
 
 using namespace shard;
 
+static constexpr int32_t kPcaMaxCols = 256;  // output columns of one projection launch
+
 extern "C" int shard_pca_project(const uint16_t* a, int64_t m, int32_t k, int64_t lda,
                                  const uint16_t* bt, int32_t n, float* c, int64_t ldc,
                                  void* stream) {
   if (!a || !bt || !c || m <= 0 || k <= 0 || n <= 0) return SHARD_ERR_ARG;
-  if (k % 16 != 0 || n % 32 != 0 || n > 256 || lda < k || ldc < n || (lda % 8) != 0)
+  if (k % 16 != 0 || n % 32 != 0 || lda < k || ldc < n || (lda % 8) != 0)
     return SHARD_ERR_SHAPE;
-  // byte ranges of the buffer resources (one workgroup's A rows, all of Bt)
-  if ((int64_t)kPcaRows * lda * 2 >= (1ll << 31) - 256 || (int64_t)n * k * 2 >= (1ll << 31) - 256)
+  // byte ranges of the buffer resources (one workgroup's A rows, one launch's Bt)
+  if ((int64_t)kPcaRows * lda * 2 >= (1ll << 31) - 256 ||
+      (int64_t)std::min(n, kPcaMaxCols) * k * 2 >= (1ll << 31) - 256)
     return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)((m + kPcaRows - 1) / kPcaRows));
-  switch (n / 32) {
-    case 1: hipLaunchKernelGGL(k_pca_project<1>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 2: hipLaunchKernelGGL(k_pca_project<2>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 3: hipLaunchKernelGGL(k_pca_project<3>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 4: hipLaunchKernelGGL(k_pca_project<4>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 5: hipLaunchKernelGGL(k_pca_project<5>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 6: hipLaunchKernelGGL(k_pca_project<6>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 7: hipLaunchKernelGGL(k_pca_project<7>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 8: hipLaunchKernelGGL(k_pca_project<8>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    default: return SHARD_ERR_SHAPE;
+  // up to 256 columns per launch (the accumulators of a wave); wider
+  // projections (ranks above 256) take one launch per 256 columns
+  for (int32_t c0 = 0; c0 < n; c0 += kPcaMaxCols) {
+    const int32_t nc = std::min(n - c0, kPcaMaxCols);
+    const uint16_t* btc = bt + (int64_t)c0 * k;
+    float* cc = c + c0;
+    switch (nc / 32) {
+      case 1: hipLaunchKernelGGL(k_pca_project<1>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 2: hipLaunchKernelGGL(k_pca_project<2>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 3: hipLaunchKernelGGL(k_pca_project<3>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 4: hipLaunchKernelGGL(k_pca_project<4>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 5: hipLaunchKernelGGL(k_pca_project<5>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 6: hipLaunchKernelGGL(k_pca_project<6>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 7: hipLaunchKernelGGL(k_pca_project<7>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      default: hipLaunchKernelGGL(k_pca_project<8>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+    }
+    SHARD_LAUNCH_CHECK("shard_pca_project");
   }
-  SHARD_LAUNCH_CHECK("shard_pca_project");
   return SHARD_OK;
 }
 
@@ -477,25 +488,30 @@ extern "C" int shard_pca_project_f32(const float* a, int64_t m, int32_t k, int64
                                      const float* bt, int32_t n, float* c, int64_t ldc,
                                      void* stream) {
   if (!a || !bt || !c || m <= 0 || k <= 0 || n <= 0) return SHARD_ERR_ARG;
-  if (k % 8 != 0 || n % 32 != 0 || n > 256 || lda < k || ldc < n || (lda % 4) != 0)
+  if (k % 8 != 0 || n % 32 != 0 || lda < k || ldc < n || (lda % 4) != 0)
     return SHARD_ERR_SHAPE;
   if (((uintptr_t)a & 15) || ((uintptr_t)bt & 15)) return SHARD_ERR_SHAPE;  // 16-byte vectors
-  if ((int64_t)kPcaRows * lda * 4 >= (1ll << 31) - 256 || (int64_t)n * k * 4 >= (1ll << 31) - 256)
+  if ((int64_t)kPcaRows * lda * 4 >= (1ll << 31) - 256 ||
+      (int64_t)std::min(n, kPcaMaxCols) * k * 4 >= (1ll << 31) - 256)
     return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)((m + kPcaRows - 1) / kPcaRows));
-  switch (n / 32) {
-    case 1: hipLaunchKernelGGL(k_pca_project_f32<1>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 2: hipLaunchKernelGGL(k_pca_project_f32<2>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 3: hipLaunchKernelGGL(k_pca_project_f32<3>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 4: hipLaunchKernelGGL(k_pca_project_f32<4>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 5: hipLaunchKernelGGL(k_pca_project_f32<5>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 6: hipLaunchKernelGGL(k_pca_project_f32<6>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 7: hipLaunchKernelGGL(k_pca_project_f32<7>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    case 8: hipLaunchKernelGGL(k_pca_project_f32<8>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, bt, c, ldc); break;
-    default: return SHARD_ERR_SHAPE;
+  for (int32_t c0 = 0; c0 < n; c0 += kPcaMaxCols) {  // as shard_pca_project: 256 columns per launch
+    const int32_t nc = std::min(n - c0, kPcaMaxCols);
+    const float* btc = bt + (int64_t)c0 * k;
+    float* cc = c + c0;
+    switch (nc / 32) {
+      case 1: hipLaunchKernelGGL(k_pca_project_f32<1>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 2: hipLaunchKernelGGL(k_pca_project_f32<2>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 3: hipLaunchKernelGGL(k_pca_project_f32<3>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 4: hipLaunchKernelGGL(k_pca_project_f32<4>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 5: hipLaunchKernelGGL(k_pca_project_f32<5>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 6: hipLaunchKernelGGL(k_pca_project_f32<6>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      case 7: hipLaunchKernelGGL(k_pca_project_f32<7>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+      default: hipLaunchKernelGGL(k_pca_project_f32<8>, grid, dim3(kPcaThreads), 0, s, a, m, k, lda, btc, cc, ldc); break;
+    }
+    SHARD_LAUNCH_CHECK("shard_pca_project_f32");
   }
-  SHARD_LAUNCH_CHECK("shard_pca_project_f32");
   return SHARD_OK;
 }
 

@@ -140,10 +140,12 @@ int shard_kv_reconstruct(const shard_decode_args* a, uint16_t* k_out, uint16_t* 
     return SHARD_ERR_ARG;
   if (a->batch <= 0 || a->n_comp <= 0 || a->n_kv_heads <= 0) return SHARD_ERR_ARG;
   const int hd = a->head_dim;
-  if ((hd != 64 && hd != 128 && hd != 256) || a->rank <= 0 || (a->rank & 1) || a->rank > 192)
+  // the tile's fp16 coefficients and the head's basis rows in LDS: up to
+  // 160 KB (rank 512 at head_dim 128, 284 at 256)
+  const size_t lds = (size_t)(kRcTok + hd) * (a->rank > 0 ? a->rank : 0) * sizeof(uint16_t);
+  if ((hd != 64 && hd != 128 && hd != 256) || a->rank <= 0 || (a->rank & 1) || lds > 160 * 1024)
     return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  const size_t lds = (size_t)(kRcTok + hd) * a->rank * sizeof(uint16_t);  // <= 108 KB at hd 256, rank 192
   dim3 grid((unsigned)((a->n_comp + kRcTok - 1) / kRcTok), (unsigned)a->n_kv_heads,
             (unsigned)a->batch);
   auto launch_k = [&](auto kern) {
@@ -158,8 +160,10 @@ int shard_kv_reconstruct(const shard_decode_args* a, uint16_t* k_out, uint16_t* 
                        a->n_kv_heads, a->n_comp, v_out);
   };
   if (lds > 64 * 1024) {  // LDS beyond the default dynamic limit (160 KB per CU on gfx950)
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_reconstruct_k<256>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const void* kern = hd == 64 ? reinterpret_cast<const void*>(&k_reconstruct_k<64>)
+                     : hd == 128 ? reinterpret_cast<const void*>(&k_reconstruct_k<128>)
+                                 : reinterpret_cast<const void*>(&k_reconstruct_k<256>);
+    const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) {
       set_last_error("shard_kv_reconstruct LDS attribute", e);
       return SHARD_ERR_HIP;

@@ -212,3 +212,42 @@ def test_head_dim_64_odd_kv_heads_fall_back(cuda):
         LlamaAttention.forward = patched
     assert torch.isfinite(got).all()
     assert torch.equal(got, want)
+
+
+def test_rank_above_192_falls_back(cuda):
+    """A Cache with max_rank_k = 320 and a budget that keeps every component
+    (k_target_cr = 4; 4 kv heads of 128 dims): compression keeps 320
+    components (the fp32 projection in two launches), the fused call does not
+    take the layer, and decode steps run the original forward over
+    kv_reconstruct's K/V, counted, with the unpatched forward's logits."""
+    from transformers.models.llama.modeling_llama import LlamaAttention
+    from shard_amd import Cache, enable_llama_fused_attention
+    model = _llama(cuda, n_q=16, n_kv=4, hd=128, hidden=2048)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(6)
+    ids = torch.randint(0, VOCAB, (1, 600), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (1, 2), generator=g).to(cuda)
+
+    def run():
+        c = Cache.from_model(model, k_target_cr=4.0, max_rank_k=320)
+        c._streaming = True
+        out = []
+        with torch.no_grad():
+            model(ids, past_key_values=c, use_cache=True)
+            for s in range(steps.shape[1]):
+                out.append(model(steps[:, s:s + 1], past_key_values=c, use_cache=True).logits.float())
+        return torch.cat(out, 1), c
+
+    got, cache = run()
+    gc = cache.layers[0]._gpu_compressed
+    assert gc is not None and gc["rank"] == 320 and gc["decode_prep"] is None
+    assert cache._fused_fallbacks == 2 * steps.shape[1] - 1
+    assert "rank=320" in cache._last_fused_fallback
+    patched = LlamaAttention.forward
+    try:
+        LlamaAttention.forward = patched.__wrapped__
+        want, _ = run()
+    finally:
+        LlamaAttention.forward = patched
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want)

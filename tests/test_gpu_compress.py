@@ -273,3 +273,44 @@ def test_compress_rank_not_a_multiple_of_32(cuda):
     err, cos = compare(out, ref_out)
     print(f"[compress rank 100] decode max_abs={err:.3e} cos={cos:.7f}", flush=True)
     assert err <= 2e-3 and cos >= 0.9999
+
+
+def test_compress_rank_above_256(cuda):
+    """max_rank_k = 320 with a budget that keeps every component (k_target_cr =
+    4): the fp32 projection runs as two launches (256 + 64 columns), the codes
+    agree with the oracle's as above, the layer takes no fused operands (rank
+    above 192) and its unfused rebuild (shard_kv_reconstruct) matches the
+    oracle's _ensure_dequant on the stored layer."""
+    from shard_amd import bench_data, ops
+    from shard_amd.cache import Cache, compress_layer
+    k, v = bench_data.make_kv(1024, seed=4)
+    inv = bench_data.inv_freq()
+    x = _centred_rows(k, inv)
+    _, S, Vh = torch.linalg.svd(x.double(), full_matrices=False)
+    basis = Vh[:320].T.float().contiguous()
+    cache = Cache(head_dim=128, num_layers=1, n_kv_heads=8, device="cuda", rope_inv_freq=inv,
+                  max_rank_k=320, k_target_cr=4.0)
+    dbg = {}
+    got = compress_layer(cache, k.to(cuda), v.to(cuda), 0, basis=basis.to(cuda), debug=dbg)
+    torch.cuda.synchronize()
+    want = ref.compress_layer(k, v, 0, inv, k_target_cr=4.0, max_rank=320, basis=basis,
+                              assign=cref.vq_assign_direct_t)
+    n, keep = got["k_coeffs_shape"]
+    assert keep == 320 and got["rank_pad"] == 320 and got["decode_prep"] is None
+    assert dbg["alloc"] == list(want["alloc"])
+    assert_codes_agree(got["k_coeffs"].cpu().numpy(), want["chain"], want["proj"].numpy(), want["alloc"],
+                       n, keep, "compress rank 320")
+    k_got, v_got = ops.kv_reconstruct(got, 1)
+    # the oracle's view of the stored layer (its _ensure_dequant reads these)
+    stored = {kk: (vv.cpu() if torch.is_tensor(vv) else vv) for kk, vv in got.items()
+              if kk in ("k_coeffs", "k_coeff_scale", "k_basis_q", "k_basis_scale", "k_mean",
+                        "k_coeffs_shape", "n_compress", "batch", "compress_start")}
+    stored["v_qdata"] = {"centroids": got["v_centroids_f16"].cpu(),
+                         "idx": got["v_indices"].cpu().reshape(-1),
+                         "ch_maxabs": got["v_ch_f16"].cpu().reshape(8, 128),
+                         "shape": (8, n, 128), "group_size": 4}
+    k_want, v_want = ref.reconstruct_kv(stored, 8, 128, inv)
+    assert np.array_equal(v_got.cpu().numpy().view(np.uint16), v_want.numpy().view(np.uint16))
+    diff = (k_got.cpu().float() - k_want.float()).abs()
+    print(f"[compress rank 320] rebuilt K max |diff| {float(diff.max()):.3e}", flush=True)
+    assert float(diff.max()) <= 2 * 2.0 ** -10 * max(1.0, float(k_want.float().abs().max()))

@@ -353,13 +353,18 @@ def test_decode_config5_layer_full_size(cuda):
     assert err <= TOL_ABS and cos >= TOL_COS, (err, cos)
 
 
-def test_kv_reconstruct(cuda):
-    """Unfused fp16 reconstruction (_ensure_dequant): V bit-exact, K within fp16 rounding."""
+@pytest.mark.parametrize("rank,nkv,hd", [(160, 8, 128), (320, 8, 128), (512, 4, 128), (320, 8, 64)])
+def test_kv_reconstruct(cuda, rank, nkv, hd):
+    """Unfused fp16 reconstruction (_ensure_dequant): V bit-exact, K within fp16
+    rounding.  Ranks above 192 (a Cache with a larger max_rank_k: the fused call
+    does not take them, these layers decode through this path) up to the LDS
+    staging limit, 512 at head_dim 128."""
     from shard_amd import ops
-    gc, inv = random_layer(B=2, rank=160, n_comp=300, seed=12)
-    d = to_device(gc, cuda, inv)
+    gc, inv = random_layer(B=2, nkv=nkv, hd=hd, rank=rank, n_comp=300, seed=12)
+    d = to_device(gc, cuda, inv, nkv=nkv, hd=hd)
+    assert (d["decode_prep"] is None) == (rank > 192)
     k_got, v_got = ops.kv_reconstruct(d, 2)
-    k_want, v_want = ref.reconstruct_kv(gc, 8, 128, inv)
+    k_want, v_want = ref.reconstruct_kv(gc, nkv, hd, inv)
     assert np.array_equal(v_got.cpu().numpy().view(np.uint16), v_want.numpy().view(np.uint16))
     # the fp16 rounding of the rebuilt key depends on the fp32 accumulation order,
     # so a key may differ by an ulp of its pre-RoPE value (|k| < 2: ulp <= 2^-10)

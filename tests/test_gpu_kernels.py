@@ -271,7 +271,8 @@ def test_kmeans_matches_reference_golden(cuda, golden):
     assert np.array_equal(idx.cpu().numpy().astype(np.int64), gld["idx"])
 
 
-@pytest.mark.parametrize("m,k,n", [(1000, 1024, 192), (4099, 1024, 64), (257, 512, 256), (31, 64, 32)])
+@pytest.mark.parametrize("m,k,n", [(1000, 1024, 192), (4099, 1024, 64), (257, 512, 256), (31, 64, 32),
+                                   (700, 1024, 320), (129, 256, 544)])  # wider: one launch per 256 columns
 def test_pca_project_mfma(cuda, m, k, n):
     ops = _ops()
     g = torch.Generator().manual_seed(m)
@@ -284,7 +285,7 @@ def test_pca_project_mfma(cuda, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(1980, 1024, 192), (4099, 1024, 64), (257, 512, 256), (31, 40, 32),
-                                   (130, 1024, 96)])
+                                   (130, 1024, 96), (700, 1024, 320), (129, 256, 544)])
 def test_pca_project_f32_mfma(cuda, m, k, n):
     """The fp32 projection (Cache.compress's GEMM) within fp32 summation error
     of the float64 product, including row tails, k past the last 32-chunk and
