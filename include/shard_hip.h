@@ -290,7 +290,8 @@ int shard_stream_dequant_qjl(const uint8_t* idx, const uint16_t* norm, const uin
  * H / G (query heads per kv head) is at most 64 (128 / D up to 32 at D = 64):
  * the token-tiled kernel takes them in groups of 4, 3, 2 or 1 (the largest
  * that divides the count) per workgroup.  rank must be a multiple of 32
- * (<= 192); pad coefficients and basis with zeros otherwise.  head_dim 64
+ * (<= 256; the row-split kernel takes <= 192, larger ranks run token-tiled);
+ * pad coefficients and basis with zeros otherwise.  head_dim 64
  * needs an even G: the kernel runs kv heads 2j and 2j+1 as one 128-dim head
  * (the token-tiled kernel; `prep` from shard_decode_prepare with head_dim
  * 64), every layout above with D = 64 as it stands.  Any number of sink, window, decode and stream tokens (the
@@ -351,7 +352,12 @@ typedef struct shard_decode_args {
  * shard_decode_prepare_bytes(n_kv_heads, rank) bytes (head_dim 64:
  * shard_decode_prepare_bytes(n_kv_heads / 2, rank), one image per pair of kv
  * heads) and is passed to shard_decode_attn as args->prep.  head_dim 128, or
- * 64 with n_kv_heads even; rank % 32 == 0, rank <= 192. */
+ * 64 with n_kv_heads even; rank % 32 == 0, rank <= 256.  The mean and the
+ * nibble offsets fold into one constant k-step per key dim, C = 16 mean -
+ * 16512 sum_{even r} A'(r) - 1152 sum_{odd r} A'(r) with A' = fp16(basis *
+ * coeff_scale), held as 16 fp16 parts: |C| must stay below about 1.04e6
+ * (callers check; shard_amd computes it on the host and otherwise decodes the
+ * layer unfused). */
 size_t shard_decode_prepare_bytes(int32_t n_kv_heads, int32_t rank);
 int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
                          const uint16_t* k_mean, const float* inv_freq, int32_t n_kv_heads,
@@ -360,7 +366,7 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
 
 /* 1 when shard_decode_attn takes the shapes in `args` (head_dim 128 with up
  * to 64 query heads per kv head, or head_dim 64 with an even number of kv
- * heads and up to 32 query heads per kv head; rank a multiple of 32 up to 192),
+ * heads and up to 32 query heads per kv head; rank a multiple of 32 up to 256),
  * else 0: the caller then rebuilds fp16 K/V (shard_kv_reconstruct) and runs
  * plain attention, as the reference's unfused path does (attention.py:411). */
 int shard_decode_supported(const shard_decode_args* args);
@@ -394,7 +400,7 @@ int shard_decode_attn_noalloc(const shard_decode_args* args, void* stream);
  *   V: fp16(hadamard(cb[idx] * ch)) (hadamard in fp32, bit-exact).
  * k_out / v_out: (B, G, n_comp, D) fp16 contiguous.  D = 64, 128 or 256; any
  * even rank whose (32 + D) x rank fp16 staging fits 160 KB of LDS (rank <= 512
- * at D = 128), so layers the fused call does not take (rank above 192) decode
+ * at D = 128), so layers the fused call does not take (rank above 256) decode
  * through it. */
 int shard_kv_reconstruct(const shard_decode_args* args, uint16_t* k_out,
                          uint16_t* v_out, void* stream);

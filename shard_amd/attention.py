@@ -133,7 +133,8 @@ def enable_llama_fused_attention(model=None):
             past_key_values._fused_fallbacks = getattr(past_key_values, "_fused_fallbacks", 0) + 1
             past_key_values._last_fused_fallback = (
                 f"head_dim={gc.get('head_dim')} n_q={self.config.num_attention_heads} "
-                f"n_kv={gc.get('n_kv')} rank={gc.get('rank_pad')}")
+                f"n_kv={gc.get('n_kv')} rank={gc.get('rank_pad')}"
+                + (f" ({gc['decode_refusal']})" if gc.get("decode_refusal") else ""))
             fuse = False
         if not fuse:
             if cache_position is not None:

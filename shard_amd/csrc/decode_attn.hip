@@ -60,6 +60,7 @@ constexpr int kRopeEntries = 32 * 64 + 64 + 2 * 32 * 64;
 constexpr int kRopeT2 = 32 * 64 + 64;       // (cos, sin)(32 b theta), b < 32
 constexpr int kRopeT1 = kRopeT2 + 32 * 64;  // (cos, sin)(1024 a theta), a < 32
 constexpr int kTokMaxTiles = 32 * 32;       // tiles per token-tiled chunk the tables cover
+constexpr int kTokMaxRank = 256;            // the token-tiled kernel (the row-split one: 192)
 #ifndef SHARD_SPLIT_PER_XCD
 #define SHARD_SPLIT_PER_XCD 1
 #endif
@@ -1551,7 +1552,7 @@ inline bool tok_supported(const shard_decode_args* a) {
     return false;
   if (head_pairs(a) && (a->n_kv_heads & 1)) return false;
   const int g = a->n_q_heads / tok_g(a);
-  return g <= 64 && a->rank > 0 && a->rank % 32 == 0 && a->rank <= 192;
+  return g <= 64 && a->rank > 0 && a->rank % 32 == 0 && a->rank <= kTokMaxRank;
 }
 
 inline int tok_nq(const shard_decode_args* a) {
@@ -1677,6 +1678,8 @@ int decode_attn_tok(const shard_decode_args* a, float* ws, hipStream_t s) {
     case 8: launch_tok<8>(tp, nq, hp, grid, s); break;
     case 10: launch_tok<10>(tp, nq, hp, grid, s); break;
     case 12: launch_tok<12>(tp, nq, hp, grid, s); break;
+    case 14: launch_tok<14>(tp, nq, hp, grid, s); break;
+    case 16: launch_tok<16>(tp, nq, hp, grid, s); break;
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_decode_attn token-tiled kernel");
@@ -1704,7 +1707,7 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
                          void* stream) {
   if (!k_basis || !k_coeff_scale || !k_mean || !inv_freq || !out || n_kv_heads <= 0)
     return SHARD_ERR_ARG;
-  if ((head_dim != kHD && head_dim != 64) || rank <= 0 || rank % 32 != 0 || rank > 192)
+  if ((head_dim != kHD && head_dim != 64) || rank <= 0 || rank % 32 != 0 || rank > kTokMaxRank)
     return SHARD_ERR_SHAPE;
   const int hp = head_dim == 64;  // head pairs: one operand image per two kv heads
   if (hp && (n_kv_heads & 1)) return SHARD_ERR_SHAPE;

@@ -467,7 +467,7 @@ def decode_supported(head_dim: int, n_q_heads: int, n_kv_heads: int, rank_pad: i
     """The shapes shard_decode_attn takes (its shard_decode_supported): head_dim
     128 with up to 64 query heads per kv head, or head_dim 64 with an even
     number of kv heads (run in pairs as 128-dim heads) and up to 32 query heads
-    per kv head; rank a multiple of 32 up to 192.  Other layers run the
+    per kv head; rank a multiple of 32 up to 256.  Other layers run the
     reference's unfused path (fp16 K/V rebuilt by shard_kv_reconstruct,
     attention.py:411)."""
     if head_dim not in (64, 128) or n_kv_heads <= 0 or n_q_heads <= 0 or n_q_heads % n_kv_heads:
@@ -477,7 +477,24 @@ def decode_supported(head_dim: int, n_q_heads: int, n_kv_heads: int, rank_pad: i
         if n_kv_heads % 2:
             return False
         g *= 2  # query heads per pair
-    return g <= 64 and 0 < rank_pad <= 192 and rank_pad % 32 == 0
+    return g <= 64 and 0 < rank_pad <= 256 and rank_pad % 32 == 0
+
+
+# The decode kernels fold the mean and the offsets of their nibble decoding
+# into one constant k-step: C = 16 mean - 16512 sum_{even r} A'(r) - 1152
+# sum_{odd r} A'(r) per key dim, A' = fp16(basis * coeff_scale), held as 16
+# fp16 parts of at most 65504 (shard_decode_prepare).  A layer whose |C| would
+# not fit takes the unfused path.
+DECODE_CONSTANT_LIMIT = 16 * 65504 - 8192
+
+
+def decode_constant_max(basis: torch.Tensor, coeff_scale: torch.Tensor, mean: torch.Tensor) -> float:
+    """max |C| over the key dims of a layer (float64, as shard_decode_prepare
+    accumulates it): basis (G*D, rank) fp16, coeff_scale (rank) fp16, mean (G*D)."""
+    a = (basis.float() * coeff_scale.float()[None, :]).half().double()
+    w = torch.where(torch.arange(a.shape[1], device=a.device) % 2 == 0, 16512.0, 1152.0).double()
+    c = 16.0 * mean.double() - a @ w
+    return float(c.abs().max())
 
 
 def decode_prepare(fmt) -> torch.Tensor:

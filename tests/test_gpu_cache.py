@@ -214,11 +214,11 @@ def test_head_dim_64_odd_kv_heads_fall_back(cuda):
     assert torch.equal(got, want)
 
 
-def test_rank_above_192_falls_back(cuda):
+def test_rank_above_256_falls_back(cuda):
     """A Cache with max_rank_k = 320 and a budget that keeps every component
     (k_target_cr = 4; 4 kv heads of 128 dims): compression keeps 320
-    components (the fp32 projection in two launches), the fused call does not
-    take the layer, and decode steps run the original forward over
+    components (the fp32 projection in two launches), the fused call (ranks up
+    to 256) does not take the layer, and decode steps run the original forward over
     kv_reconstruct's K/V, counted, with the unpatched forward's logits."""
     from transformers.models.llama.modeling_llama import LlamaAttention
     from shard_amd import Cache, enable_llama_fused_attention

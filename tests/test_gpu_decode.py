@@ -208,6 +208,40 @@ def test_decode_with_qjl_and_narrow_stream(cuda, bits, qjl, kernel):
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
+def test_layer_beyond_the_rebuild_constant_decodes_unfused(cuda):
+    """A layer whose rebuild constant would not fit its 16 fp16 parts (coefficient
+    scales x 2000) gets no fused operands, says why, and is left to the unfused
+    path, whose rebuild matches the oracle's."""
+    from shard_amd import attention, ops
+    gc, inv = random_layer(B=1, rank=128, n_comp=200, seed=31)
+    gc["k_coeff_scale"] = (gc["k_coeff_scale"].float() * 2000).half()
+    d = to_device(gc, cuda, inv)
+    assert d["decode_prep"] is None and "rebuild constant" in d["decode_refusal"]
+    assert not attention.fused_supported(d, 32)
+    k_got, v_got = ops.kv_reconstruct(d, 1)
+    k_want, _ = ref.reconstruct_kv(gc, 8, 128, inv)
+    # fp16 keys of large magnitude: within fp16 rounding of the largest key
+    diff = float((k_got.cpu().float() - k_want.float()).abs().max())
+    assert diff <= 2.0 ** -9 * float(k_want.float().abs().max()), diff
+
+
+@pytest.mark.parametrize("rank", [224, 256])
+def test_decode_ranks_above_192(cuda, rank):
+    """Ranks 224 and 256 (a Cache with a larger max_rank_k): the token-tiled
+    kernel takes them (a forced row-split request routes there too), batch 2
+    with stream and decode tokens, the same bar."""
+    gc, inv = random_layer(B=2, rank=rank, n_comp=1500, n_stream=6, n_dec=3, seed=rank,
+                           basis_amp=0.02)
+    q = torch.randn(2, 32, 1, 128, generator=torch.Generator().manual_seed(3)).half()
+    pos_q = 4 + 1500 + 64 + 3 + 6 - 1
+    want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    for kernel in KERNELS:
+        got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
+        err, cos = compare(got, want)
+        print(f"rank={rank} kernel={kernel} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (kernel, err, cos)
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
 def test_decode_rank_padding_and_splits(cuda, kernel):
     """rank 100 (padded to 128 on the device) and several explicit split counts."""
@@ -356,13 +390,13 @@ def test_decode_config5_layer_full_size(cuda):
 @pytest.mark.parametrize("rank,nkv,hd", [(160, 8, 128), (320, 8, 128), (512, 4, 128), (320, 8, 64)])
 def test_kv_reconstruct(cuda, rank, nkv, hd):
     """Unfused fp16 reconstruction (_ensure_dequant): V bit-exact, K within fp16
-    rounding.  Ranks above 192 (a Cache with a larger max_rank_k: the fused call
+    rounding.  Ranks above 256 (a Cache with a larger max_rank_k: the fused call
     does not take them, these layers decode through this path) up to the LDS
     staging limit, 512 at head_dim 128."""
     from shard_amd import ops
     gc, inv = random_layer(B=2, nkv=nkv, hd=hd, rank=rank, n_comp=300, seed=12)
     d = to_device(gc, cuda, inv, nkv=nkv, hd=hd)
-    assert (d["decode_prep"] is None) == (rank > 192)
+    assert (d["decode_prep"] is None) == (rank > 256)
     k_got, v_got = ops.kv_reconstruct(d, 2)
     k_want, v_want = ref.reconstruct_kv(gc, nkv, hd, inv)
     assert np.array_equal(v_got.cpu().numpy().view(np.uint16), v_want.numpy().view(np.uint16))

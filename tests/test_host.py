@@ -187,12 +187,50 @@ def test_decode_supported_shapes():
     for hd in (64, 128, 256):
         for n_kv in (1, 2, 8):
             for g in (1, 2, 3, 4, 6, 8, 16, 64, 68):
-                for rank in (32, 96, 100, 192, 224):
+                for rank in (32, 96, 100, 192, 224, 256, 288):
                     a = _lib.DecodeArgs()
                     a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim = 1, g * n_kv, n_kv, hd
                     a.rank, a.n_comp = rank, 100
                     want = bool(lib.shard_decode_supported(ctypes.byref(a)))
                     assert ops.decode_supported(hd, g * n_kv, n_kv, rank) == want, (hd, n_kv, g, rank)
+
+
+def _greedy_parts(c):
+    """shard_decode_prepare's split of the rebuild constant into 16 fp16 parts,
+    largest first (each clamped to +-65504 and rounded to fp16)."""
+    parts = []
+    for _ in range(16):
+        h = float(np.float16(min(max(c, -65504.0), 65504.0)))
+        parts.append(h)
+        c -= h
+    return parts, c
+
+
+def test_decode_constant_limit_and_formula():
+    """The host bound on the decode kernels' rebuild constant: below
+    DECODE_CONSTANT_LIMIT the 16 fp16 parts hold C up to the last part's
+    rounding (below one fp16 ulp of 65504), and decode_constant_max equals a
+    direct float64 evaluation of 16 mean - 16512 sum_even A' - 1152 sum_odd A'
+    with A' = fp16(basis * cs)."""
+    from shard_amd import ops
+    for c in (0.0, 12345.678, -654321.5, float(ops.DECODE_CONSTANT_LIMIT),
+              -float(ops.DECODE_CONSTANT_LIMIT)):
+        parts, rest = _greedy_parts(c)
+        assert abs(rest) <= 32.0, (c, rest)
+    _, rest = _greedy_parts(16 * 65504.0 + 5e4)  # beyond the parts: a visible residual
+    assert abs(rest) > 1e4
+    g = torch.Generator().manual_seed(0)
+    basis = (torch.randn(256, 64, generator=g) * 0.1).half()
+    cs = (torch.rand(64, generator=g) * 3).half()
+    mean = torch.randn(256, generator=g).half()
+    want = 0.0
+    for row in range(256):
+        c = 16.0 * float(mean[row])
+        for r in range(64):
+            a = float(np.float16(np.float32(basis[row, r]) * np.float32(cs[r])))
+            c -= (16512.0 if r % 2 == 0 else 1152.0) * a
+        want = max(want, abs(c))
+    assert abs(ops.decode_constant_max(basis, cs, mean) - want) <= 1e-9 * want
 
 
 def test_decode_graph_refuses_other_caches():
