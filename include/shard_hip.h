@@ -355,9 +355,7 @@ typedef struct shard_decode_args {
  * 64 with n_kv_heads even; rank % 32 == 0, rank <= 256.  The mean and the
  * nibble offsets fold into one constant k-step per key dim, C = 16 mean -
  * 16512 sum_{even r} A'(r) - 1152 sum_{odd r} A'(r) with A' = fp16(basis *
- * coeff_scale), held as 16 fp16 parts: |C| must stay below about 1.04e6
- * (callers check; shard_amd computes it on the host and otherwise decodes the
- * layer unfused). */
+ * coeff_scale), held as 16 bf16 parts (a bf16 MFMA k-step): any finite C. */
 size_t shard_decode_prepare_bytes(int32_t n_kv_heads, int32_t rank);
 int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
                          const uint16_t* k_mean, const float* inv_freq, int32_t n_kv_heads,

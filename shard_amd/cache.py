@@ -777,15 +777,15 @@ def finalize_format(gc: dict, inv_freq, dev):
         inv_freq = torch.zeros(gc["head_dim"] // 2)
     gc["inv_freq_dev"] = inv_freq.to(dev, torch.float32).contiguous()
     # decode-kernel operands for the shapes the fused kernel takes (head_dim
-    # 128, or 64 with an even kv head count, rank up to 256, a rebuild
-    # constant within its fp16 parts); other layers decode through
-    # kv_reconstruct and the model's own attention
+    # 128, or 64 with an even kv head count, rank up to 256, a finite rebuild
+    # constant); other layers decode through kv_reconstruct and the model's
+    # own attention
     hd, G = gc["head_dim"], gc["n_kv"]
     gc["decode_prep"] = None
     gc.pop("decode_refusal", None)
     if (hd == 128 or (hd == 64 and G % 2 == 0)) and rank_pad <= 256:
         cmax = ops.decode_constant_max(gc["k_basis_pad"], gc["k_coeff_scale_pad"], gc["k_mean_f16"])
-        if cmax <= ops.DECODE_CONSTANT_LIMIT:
+        if cmax <= ops.DECODE_CONSTANT_LIMIT:  # False for NaN
             gc["decode_prep"] = ops.decode_prepare(gc)
         else:
-            gc["decode_refusal"] = f"rebuild constant {cmax:.4g} beyond the fp16 parts"
+            gc["decode_refusal"] = f"rebuild constant {cmax:.4g} not finite or beyond fp32"

@@ -181,11 +181,15 @@ __device__ __forceinline__ void load_coef(const uint8_t* rowp, bool valid, uint3
 //        k-steps 0..KS-1 = A'(r) = fp16(basis * coeff_scale) in the nibble order
 //        of the coefficient dwords, times 16 for even ranks r (see
 //        nib8_to_mfma); k-step KS = C = 16 mean - 16512 sum_{r even} A'(r)
-//        - 1152 sum_{r odd} A'(r) as 16 fp16 parts (paired with a constant-1
-//        operand), which cancels the 1024 offsets of the nibble encoding:
+//        - 1152 sum_{r odd} A'(r) as 16 bf16 parts (a bf16 MFMA against a
+//        constant-1 operand), which cancels the 1024 offsets of the nibble
+//        encoding:
 //          16 sum_r A'(r)(n_r - 8) + 16 mean = C + sum_{r even} 16 A'(r)(1024 + n_r)
 //                                              + sum_{r odd} A'(r)(1024 + 16 n_r)
-//        The parts hold |C| up to about 9.8e5 (greedy split, 15 x 65504 + rest).
+//        The greedy split (each part the bf16 rounding of what remains) holds
+//        C to fp32 precision at any magnitude the fp32 accumulators hold (fp16
+//        parts would stop at 16 x 65504); the relative rounding of the sums
+//        does not depend on the layer's scale.
 //   rope float2 [32][64] = (cos, sin)(col * theta_i) for the token column inside
 //        a tile, then float2 [64] = (cos, sin)(32 * theta_i), the per-tile step,
 //        then the tile-offset tables of the token-tiled kernel: float2 [32][64] =
@@ -215,6 +219,7 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
       const int col = lane & 31, hh = lane >> 5;
       const int row = hp ? pair_row(g, row_dim(P, col)) : g * kHD + row_dim(P, col);
       half8 v;
+      uint16_t cb[8];  // the constant k-step's bf16 parts
       if (s < KS) {
         const int r0 = 8 * (KS * hh + s);
 #pragma unroll
@@ -228,15 +233,14 @@ __global__ void k_decode_prepare(const uint16_t* __restrict__ basis, const uint1
         for (int r = 0; r < rank; ++r)
           c -= ((r & 1) ? 1152.0 : 16512.0) *
                (double)(float)(half_t)(h2f(basis[(int64_t)row * rank + r]) * h2f(cs[r]));
-        // greedy split into 16 fp16 parts (8 per lane half), largest first
+        // greedy split into 16 bf16 parts (8 per lane half), largest first
         for (int part = 0; part < 16; ++part) {
-          const double cl = c > 65504.0 ? 65504.0 : (c < -65504.0 ? -65504.0 : c);
-          const half_t h = (half_t)(float)cl;
-          if (part >> 3 == hh) v[part & 7] = h;
+          const __bf16 h = (__bf16)(float)c;
+          if (part >> 3 == hh) cb[part & 7] = __builtin_bit_cast(uint16_t, h);
           c -= (double)(float)h;
         }
       }
-      op[i] = __builtin_bit_cast(uint4, v);
+      op[i] = s < KS ? __builtin_bit_cast(uint4, v) : __builtin_bit_cast(uint4, cb);
     } else {
       const int k = (int)(i - n_op);
       const int fm = hp ? 31 : 63;  // pair -> inv_freq entry
@@ -677,9 +681,9 @@ void k_decode_split(const SplitParams p) {
     ph_s[i] = s * 0.0625f;
     rstep[i] = phs[pr[i]];
   }
-  half8 one8;  // the B operand of the mean k-step: 1 in all 16 k-elements
+  bf16x8 one8;  // the B operand of the constant k-step: 1 in all 16 k-elements
 #pragma unroll
-  for (int e = 0; e < 8; ++e) one8[e] = (half_t)1.f;
+  for (int e = 0; e < 8; ++e) one8[e] = (__bf16)1.f;
 
   // ---- softmax-stage state: thread tid < NQ * TT owns (head tid / TT, token tid % TT)
   float m_run = -INFINITY, l_part = 0.f;
@@ -695,7 +699,8 @@ void k_decode_split(const SplitParams p) {
     // 1. 16 x the no-RoPE keys of the wave's 32 rows for the group's 32 tokens
     //    (fp32): constant (k-step KS, times 1) + basis . coefficients
     const float16v zero16 = {};
-    float16v acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[KS], one8, zero16, 0, 0, 0);
+    float16v acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, Ab[KS]), one8,
+                                                          zero16, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ab[s], nib8_to_mfma(cw[s]), acc, 0, 0, 0);
 
@@ -1156,9 +1161,9 @@ void k_decode_tok(const TokParams p) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) pr[i] = 8 * (i >> 2) + 4 * hh + (i & 3);
   const int qrow = min(col, NQ);  // rows >= NQ of the score MFMA read the zero row
-  half8 one8;
+  bf16x8 one8;  // the B operand of the constant k-step (bf16 parts of the image)
 #pragma unroll
-  for (int e = 0; e < 8; ++e) one8[e] = (half_t)1.f;
+  for (int e = 0; e < 8; ++e) one8[e] = (__bf16)1.f;
   __syncthreads();
 
   const float sc = kLog2e * rsqrtf(HP ? 64.f : (float)kHD);
@@ -1271,13 +1276,16 @@ void k_decode_tok(const TokParams p) {
     float16v acc[4];
 #pragma unroll
     for (int s = 0; s <= KS; ++s) {
-      const half8 bs = s == 0 ? one8 : nib8_to_mfma(cw[s - 1]);
+      const half8 bs = s == 0 ? half8{} : nib8_to_mfma(cw[s - 1]);
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
         const int j = 4 * s + rb;
         const half8 a = ring[j % kRing];
         if (j + kRing < NA) ring[j % kRing] = a_at(j + kRing);
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bs, s == 0 ? zero16 : acc[rb], 0, 0, 0);
+        if (s == 0)  // the constant k-step: bf16 parts
+          acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), one8, zero16, 0, 0, 0);
+        else
+          acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bs, acc[rb], 0, 0, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (j + kRing < NA) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }

@@ -543,7 +543,6 @@ __global__ void k_vq_assign(const float* __restrict__ x, int64_t n,
 //     sequential strict-< scan does (an index-0 answer when no distance is
 //     finite).
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // the direct distance of the reference kernel's statement, uncontracted (this
 // library's rule: no FMA): fp32 sum of squared differences in dim order

@@ -483,9 +483,10 @@ def decode_supported(head_dim: int, n_q_heads: int, n_kv_heads: int, rank_pad: i
 # The decode kernels fold the mean and the offsets of their nibble decoding
 # into one constant k-step: C = 16 mean - 16512 sum_{even r} A'(r) - 1152
 # sum_{odd r} A'(r) per key dim, A' = fp16(basis * coeff_scale), held as 16
-# fp16 parts of at most 65504 (shard_decode_prepare).  A layer whose |C| would
-# not fit takes the unfused path.
-DECODE_CONSTANT_LIMIT = 16 * 65504 - 8192
+# bf16 parts (shard_decode_prepare): any finite magnitude the fp32
+# accumulators hold.  A layer whose C is not finite or beyond this bound
+# (non-finite basis or scales) takes the unfused path.
+DECODE_CONSTANT_LIMIT = 1e30
 
 
 def decode_constant_max(basis: torch.Tensor, coeff_scale: torch.Tensor, mean: torch.Tensor) -> float:

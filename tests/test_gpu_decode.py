@@ -208,21 +208,32 @@ def test_decode_with_qjl_and_narrow_stream(cuda, bits, qjl, kernel):
     assert err <= TOL_ABS and cos >= TOL_COS
 
 
-def test_layer_beyond_the_rebuild_constant_decodes_unfused(cuda):
-    """A layer whose rebuild constant would not fit its 16 fp16 parts (coefficient
-    scales x 2000) gets no fused operands, says why, and is left to the unfused
-    path, whose rebuild matches the oracle's."""
+def test_large_rebuild_constant_decodes_fused(cuda):
+    """Coefficient scales x 2000 (the rebuild constant C near 5e6, beyond what
+    16 fp16 parts hold; q scaled down alike so the scores keep their range): the
+    bf16 parts of the constant k-step carry it, both split kernels decode the
+    layer within the bar, and a non-finite constant leaves the layer unfused
+    with the reason given."""
     from shard_amd import attention, ops
-    gc, inv = random_layer(B=1, rank=128, n_comp=200, seed=31)
+    gc, inv = random_layer(B=1, rank=192, n_comp=1200, n_stream=3, seed=31)
     gc["k_coeff_scale"] = (gc["k_coeff_scale"].float() * 2000).half()
     d = to_device(gc, cuda, inv)
-    assert d["decode_prep"] is None and "rebuild constant" in d["decode_refusal"]
-    assert not attention.fused_supported(d, 32)
-    k_got, v_got = ops.kv_reconstruct(d, 1)
-    k_want, _ = ref.reconstruct_kv(gc, 8, 128, inv)
-    # fp16 keys of large magnitude: within fp16 rounding of the largest key
-    diff = float((k_got.cpu().float() - k_want.float()).abs().max())
-    assert diff <= 2.0 ** -9 * float(k_want.float().abs().max()), diff
+    cmax = ops.decode_constant_max(d["k_basis_pad"], d["k_coeff_scale_pad"], d["k_mean_f16"])
+    assert cmax > 16 * 65504 and d["decode_prep"] is not None
+    q = (torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(4)) / 2000).half()
+    pos_q = 4 + 1200 + 64 + 3 - 1
+    want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    for kernel in KERNELS:
+        got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
+        err, cos = compare(got, want)
+        print(f"[C={cmax:.3g}] kernel={kernel} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (kernel, err, cos)
+    bad = dict(gc)
+    bad["k_coeff_scale"] = gc["k_coeff_scale"].clone()
+    bad["k_coeff_scale"][3] = float("inf")
+    d2 = to_device(bad, cuda, inv)
+    assert d2["decode_prep"] is None and "rebuild constant" in d2["decode_refusal"]
+    assert not attention.fused_supported(d2, 32)
 
 
 @pytest.mark.parametrize("rank", [224, 256])

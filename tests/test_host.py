@@ -195,30 +195,13 @@ def test_decode_supported_shapes():
                     assert ops.decode_supported(hd, g * n_kv, n_kv, rank) == want, (hd, n_kv, g, rank)
 
 
-def _greedy_parts(c):
-    """shard_decode_prepare's split of the rebuild constant into 16 fp16 parts,
-    largest first (each clamped to +-65504 and rounded to fp16)."""
-    parts = []
-    for _ in range(16):
-        h = float(np.float16(min(max(c, -65504.0), 65504.0)))
-        parts.append(h)
-        c -= h
-    return parts, c
-
-
-def test_decode_constant_limit_and_formula():
-    """The host bound on the decode kernels' rebuild constant: below
-    DECODE_CONSTANT_LIMIT the 16 fp16 parts hold C up to the last part's
-    rounding (below one fp16 ulp of 65504), and decode_constant_max equals a
-    direct float64 evaluation of 16 mean - 16512 sum_even A' - 1152 sum_odd A'
-    with A' = fp16(basis * cs)."""
+def test_decode_constant_formula():
+    """decode_constant_max equals a direct float64 evaluation of the decode
+    kernels' constant k-step, 16 mean - 16512 sum_even A' - 1152 sum_odd A'
+    with A' = fp16(basis * cs); and 16 greedy bf16 parts (each the bf16
+    rounding of what remains, as shard_decode_prepare splits it) hold C far
+    beyond fp16's 16 x 65504 to below fp32 resolution."""
     from shard_amd import ops
-    for c in (0.0, 12345.678, -654321.5, float(ops.DECODE_CONSTANT_LIMIT),
-              -float(ops.DECODE_CONSTANT_LIMIT)):
-        parts, rest = _greedy_parts(c)
-        assert abs(rest) <= 32.0, (c, rest)
-    _, rest = _greedy_parts(16 * 65504.0 + 5e4)  # beyond the parts: a visible residual
-    assert abs(rest) > 1e4
     g = torch.Generator().manual_seed(0)
     basis = (torch.randn(256, 64, generator=g) * 0.1).half()
     cs = (torch.rand(64, generator=g) * 3).half()
@@ -231,6 +214,12 @@ def test_decode_constant_limit_and_formula():
             c -= (16512.0 if r % 2 == 0 else 1152.0) * a
         want = max(want, abs(c))
     assert abs(ops.decode_constant_max(basis, cs, mean) - want) <= 1e-9 * want
+    for c in (12345.678, -654321.5, 3.1e6, -7.77e8):
+        rest = c
+        for _ in range(16):
+            h = float(torch.tensor(np.float32(rest)).to(torch.bfloat16).float())
+            rest -= h
+        assert abs(rest) <= abs(c) * 2.0 ** -40, (c, rest)
 
 
 def test_decode_graph_refuses_other_caches():
