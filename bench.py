@@ -874,7 +874,9 @@ def e2e(dev, batch=16, prompt=16384, new_tokens=128, layers=32, seed=0):
                 progress(f"shard: graph decode failed: {e!r}")
         res[kind] = r
         del cache
-    return {"metric": "e2e decode tokens/s, shard cache vs fp16 cache (BASELINE config 5)",
+    which = ("BASELINE config 5" if (batch, prompt, new_tokens) == (16, 16384, 128)
+             else f"batch {batch}, {prompt}-token prompts, {new_tokens} new tokens")
+    return {"metric": f"e2e decode tokens/s, shard cache vs fp16 cache ({which})",
             "unit": "tokens/s", "value": res["shard"]["tokens_per_s"],
             "vs_fp16_cache": round(res["shard"]["tokens_per_s"] / res["fp16"]["tokens_per_s"], 3),
             "vs_fp16_splitk_cache": round(res["shard"]["tokens_per_s"]
