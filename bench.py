@@ -479,7 +479,8 @@ def prefill(dev, layers=32, batch=4, T=8192):
     fused into its operand loads (the RoPE phase table is computed once per
     pass: every layer has the same positions), per-column int4 quantization +
     packing, FWHT + channel normalization of V, nearest-centroid assignment to
-    a seeded codebook."""
+    a seeded codebook (through its candidate table, built once in the timed
+    region: every layer uses the same codebook)."""
     from shard_amd import ops, bench_data
     G, D, R = 8, 128, 192
     basis = bench_data.random_orthonormal_basis(G * D, R).to(dev)
@@ -496,7 +497,7 @@ def prefill(dev, layers=32, batch=4, T=8192):
     codebook = x0[torch.randperm(x0.shape[0], generator=gsel, device=dev)[:256]].contiguous()
     del x0
 
-    def layer_pass(k, v, ph, ev=None):
+    def layer_pass(k, v, ph, table, ev=None):
         if ev is not None:
             ev[0].record()
         proj = ops.pca_project_rope(k, 0, T, ph, btp)
@@ -504,18 +505,19 @@ def prefill(dev, layers=32, batch=4, T=8192):
             ev[1].record()
         chain = ops.int4_quant_pack(proj, bits)
         x, _, _ = ops.vq_prepare(v.reshape(batch * G, T, D))
-        idx = ops.vq_assign(x, codebook)
+        idx = ops.vq_assign_table(x, table)
         return chain, idx
 
-    layer_pass(*data[0], ops.rope_phases(0, T, invf))              # warm-up
+    layer_pass(*data[0], ops.rope_phases(0, T, invf), ops.VqTable(codebook))  # warm-up
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(layers)]
     e0.record()
     ph = ops.rope_phases(0, T, invf)
+    table = ops.VqTable(codebook)
     for li in range(layers):
-        layer_pass(*data[li], ph, evs[li])
+        layer_pass(*data[li], ph, table, evs[li])
     e1.record()
     torch.cuda.synchronize()
     total_s = e0.elapsed_time(e1) / 1000.0
@@ -535,21 +537,29 @@ def prefill(dev, layers=32, batch=4, T=8192):
 
 def kmeans_update_bench(dev, batch=16, T=16384, k=256, reps=5):
     """The k-means step of one config-5 layer's V compression at its full size:
-    B x 8 heads x (T - 68) tokens x 32 subvectors of 4 values, one assignment
-    (shard_vq_assign) and one update (shard_kmeans_update), each timed with
-    HIP events over `reps` calls.  Synthetic rows: N(0, 1), the first k rows as
-    centroids."""
-    from shard_amd import ops
-    n = batch * 8 * (T - 68) * 32
-    g = torch.Generator(device=dev).manual_seed(1)
-    x = torch.randn(n, 4, device=dev, generator=g)
+    B x 8 heads x (T - 68) tokens x 32 subvectors of 4 values (the layer's V
+    through shard_vq_prepare, so the rows are normalized to [-1, 1] as in
+    compression), the first k rows as centroids.  Times, with HIP events over
+    `reps` calls: the all-centroid assignment (shard_vq_assign), the candidate
+    table's build and its assignment (shard_vq_table_build,
+    shard_vq_assign_table) and one update (shard_kmeans_update)."""
+    from shard_amd import ops, bench_data
+    Tc = T - 68
+    _, v, _ = bench_data.make_kv_device(Tc, batch, 1, dev)
+    x, _, _ = ops.vq_prepare(v.reshape(batch * 8, Tc, 128))
+    del v
+    n = x.shape[0]
     cent = x[:k].clone()
     idx = ops.vq_assign(x, cent)
+    table = ops.VqTable(cent)
+    same = bool(torch.equal(ops.vq_assign_table(x, table), idx))
     ops.kmeans_update(x, idx, cent)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    out = {"rows": n, "k": k}
+    out = {"rows": n, "k": k, "table_equals_all_centroid": same}
     for name, fn in (("assign_ms", lambda: ops.vq_assign(x, cent)),
+                     ("table_build_ms", lambda: ops.VqTable(cent)),
+                     ("assign_table_ms", lambda: ops.vq_assign_table(x, table)),
                      ("update_ms", lambda: ops.kmeans_update(x, idx, cent))):
         e0.record()
         for _ in range(reps):

@@ -157,6 +157,32 @@ int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
 int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids,
                     int32_t k, int32_t* idx, void* stream);
 
+/* The same assignment for 4-dim rows and k = 32, 64, ..., 256 centroids
+ * through a candidate table built once per codebook (the same replacement of
+ * triton_kernels.py:689-746; the reference's k-means calls it every
+ * iteration, cache.py:26-27).  The table cuts the box [lo, hi]^4 into
+ * nbins^4 cells (nbins <= 32) and lists for each cell, in index order, the
+ * centroids that can be the answer for some row in it (a rigorous bound on
+ * the fp32 distance drops the others); a row in the box is decided by the
+ * direct distances to its cell's list.  Rows outside the box, non-finite rows
+ * and rows of cells with more than 32 candidates are finished by the
+ * all-centroid path, so every result equals shard_vq_assign's.  The box must
+ * satisfy hi > lo and max(|lo|, |hi|) <= 64 (hi - lo); normalized subvectors
+ * (shard_vq_prepare's x, in [-1, 1]) take lo = -1, hi = 1.
+ * table: shard_vq_table_bytes(k, nbins) bytes, 16-byte aligned.
+ * shard_vq_assign_table takes the build's k, nbins, lo and hi (a table built
+ * with other values decides nothing: every row takes the all-centroid path)
+ * and a workspace of shard_vq_assign_table_workspace(n) bytes (the undecided
+ * rows); n < 2^31. */
+size_t shard_vq_table_bytes(int32_t k, int32_t nbins);
+int shard_vq_table_build(const float* centroids, int32_t k, float lo, float hi,
+                         int32_t nbins, void* table, size_t table_bytes, void* stream);
+size_t shard_vq_assign_table_workspace(int64_t n);
+int shard_vq_assign_table(const float* x, int64_t n, const float* centroids, int32_t k,
+                          const void* table, size_t table_bytes, int32_t nbins, float lo,
+                          float hi, int32_t* idx, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* One k-means update (cache.py:28-38) given assignments idx: new_c[k] = mean of
  * the rows assigned to k (empty clusters keep c[k]); also writes
  * max |new_c - c| to *max_delta (device fp32).  Sums are accumulated per

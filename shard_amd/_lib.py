@@ -11,6 +11,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SHARD_HIP_LIB") or os.path.join(_HERE, "libshard_hip.so")
 
 c_int32, c_int64, c_size_t, c_void_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
+c_float = ctypes.c_float
 
 ERRORS = {-1: "bad argument", -2: "unsupported shape", -3: "HIP error", -4: "workspace too small"}
 
@@ -64,6 +65,11 @@ SIGNATURES = [
     ("shard_vq_prepare_workspace", c_size_t, [c_int64, c_int32]),
     ("shard_vq_prepare", c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("shard_vq_assign", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
+    ("shard_vq_table_bytes", c_size_t, [c_int32, c_int32]),
+    ("shard_vq_table_build", c_int32, [c_void_p, c_int32, c_float, c_float, c_int32, c_void_p, c_size_t, c_void_p]),
+    ("shard_vq_assign_table_workspace", c_size_t, [c_int64]),
+    ("shard_vq_assign_table", c_int32, [c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_size_t, c_int32, c_float,
+                                        c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("shard_kmeans_update_workspace", c_size_t, [c_int64, c_int32]),
     ("shard_kmeans_update_workspace_d", c_size_t, [c_int64, c_int32, c_int32]),
     ("shard_kmeans_update", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

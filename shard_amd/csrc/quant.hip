@@ -5,6 +5,9 @@
 //     deterministic k-means centroid update
 // This file is compiled with -ffp-contract=off and uses explicitly rounded
 // fp32 operations so every value follows the reference's per-op rounding.
+#include <algorithm>
+#include <cmath>
+
 #include "common.h"
 
 namespace shard {
@@ -581,12 +584,16 @@ __device__ __forceinline__ void split3(float v, __bf16& h, __bf16& m, __bf16& l)
   l = (__bf16)(r - (float)m);
 }
 
-// (256, 2): at most 256 registers per lane, so the MFMA results land in VGPRs
-template <int NB>
+// (256, 2): at most 256 registers per lane, so the MFMA results land in VGPRs.
+// LIST: the rows are x[list[i]] for i < *list_n (the rows another kernel left
+// undecided), each answer written to idx[list[i]]; n is ignored.
+template <int NB, bool LIST = false>
 __global__ __launch_bounds__(256, 2)
 void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __restrict__ c,
-                      int32_t* __restrict__ idx) {
+                      int32_t* __restrict__ idx, const int32_t* __restrict__ list = nullptr,
+                      const int32_t* __restrict__ list_n = nullptr) {
   constexpr int K = 32 * NB;
+  if constexpr (LIST) n = *list_n;
   __shared__ float4 cs[K];
   __shared__ bf16x8 atab[NB][2][64];  // the A operands again, for the rare rescans
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
@@ -637,8 +644,10 @@ void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __res
   const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
   const float16v zero = {};
   for (int64_t g = ((int64_t)blockIdx.x * blockDim.x + tid) >> 6; g < ngroups; g += nwaves) {
-    const int64_t row = g * 32 + col;
-    const bool valid = row < n;
+    const int64_t pos = g * 32 + col;
+    const bool valid = pos < n;
+    int64_t row = pos;
+    if constexpr (LIST) row = valid ? list[pos] : 0;
     const float4 x4 = ((const float4*)x)[valid ? row : 0];
     const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
     // B operands: lane (row col, half hh): first [xh, xh] (hh 0) | [xm, xh]
@@ -753,6 +762,336 @@ void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __res
       if (amb) best = bi;
     }
     if (hh == 0 && valid) idx[row] = best;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Nearest centroid of 4-dim rows through a candidate table (k = 32 NB <= 256):
+// the same result as k_vq_assign, with most rows decided by the reference's
+// direct distance to a few centroids.
+//
+// The box [lo, hi]^4 is cut into nbins^4 cells.  For each cell the table
+// lists, in increasing index order, every centroid that can be the answer for
+// (or tie with the answer for) some row of the cell.
+//
+// Why a centroid c may be left out of cell Q = prod_j [l_j, h_j]: the exact
+// D(x, c) - D(x, c') (squared distances) is a sum over dims of terms linear in
+// x_j, so its minimum over Q is
+//   L = sum_j min((l_j - c_j)^2 - (l_j - c'_j)^2, (h_j - c_j)^2 - (h_j - c'_j)^2)
+// and D(x, c) <= Dmax(c) = sum_j max((l_j - c_j)^2, (h_j - c_j)^2) on Q.  The
+// reference's fp32 distance is within 6.01 2^-24 D of D (six roundings of
+// non-negative terms) and L evaluated in fp32 is within 8 2^-24 (Dmax(c) +
+// Dmax(c')) of its exact value, so
+//   L > 2^-17 (Dmax(c) + Dmax(c')) + 2^-100
+// (nine times the 14.01 2^-24 needed, plus an absolute term for underflow)
+// means that at every row of Q the reference's distance to c exceeds its
+// distance to c': c is neither the strict-< argmin nor tied with it.  Every
+// left-out centroid is beaten at every row by some other centroid, so the
+// first-index argmin is always listed, and the sequential strict-< scan of
+// the ascending list returns it.  The build keeps c when no other centroid of
+// a first survivor set (those the centroid nearest the cell centre does not
+// beat) beats it.
+//
+// Cells: l_j = lo + i_j w - w/1024 and h_j = lo + (i_j + 1) w + w/1024 with
+// w = (hi - lo)/nbins.  A row whose cell coordinate t_j = (x_j - lo) nbins /
+// (hi - lo) (fp32) lies in [-2^-12, nbins + 2^-12] goes to cell
+// clamp(trunc(t_j)): its fp32 error is below 1e-5 cells (96 2^-24 nbins) and
+// the box corners are within 130 2^-24 (hi - lo) of their exact values when
+// max(|lo|, |hi|) <= 64 (hi - lo), which the build requires, so the row lies
+// in that cell's widened box.  Rows outside the box, non-finite rows and rows
+// of cells with more than kVqTabCap candidates are appended to a list that
+// the MFMA kernel (LIST) finishes.  A centroid set holding a non-finite value
+// or one above 2^32 in magnitude lists every cell out.
+//
+// Table: a 64-byte header (nbins, k, lo, hi, a tag), one count byte per cell
+// (kVqTabFull: listed out), then kVqTabCap candidate bytes per cell padded
+// with the last candidate (a repeated candidate changes nothing under <).
+// ---------------------------------------------------------------------------
+constexpr int kVqTabCap = 32;
+constexpr int kVqTabFull = 255;
+constexpr int kVqTabHeader = 64;
+constexpr int kVqTabMaxBins = 32;
+constexpr int kVqTabSurv = 128;  // first-test survivors a build thread can hold
+constexpr uint32_t kVqTabTag = 0x54715653u;
+
+struct VqTabHeader {
+  int32_t nbins, k;
+  float lo, hi;
+  uint32_t tag;
+  int32_t pad[11];
+};
+
+__host__ __device__ inline int64_t vq_tab_cells(int nbins) {
+  return (int64_t)nbins * nbins * nbins * nbins;
+}
+__host__ __device__ inline int64_t vq_tab_counts_bytes(int nbins) {
+  return (vq_tab_cells(nbins) + 15) & ~(int64_t)15;
+}
+
+// the cell's box, widened by w/1024 on every side
+__device__ __forceinline__ void vq_cell_box(int64_t cell, int nbins, float lo, float hi,
+                                            float (&l)[4], float (&h)[4]) {
+  const float w = (hi - lo) / (float)nbins, pad = w * 0x1p-10f;
+  int64_t r = cell;
+#pragma unroll
+  for (int j = 3; j >= 0; --j) {
+    const int i = (int)(r % nbins);
+    r /= nbins;
+    l[j] = lo + (float)i * w - pad;
+    h[j] = lo + (float)(i + 1) * w + pad;
+  }
+}
+
+// Four lanes per cell, 64 cells per 256-thread workgroup.  Lane q of a cell
+// scans centroids q, q + 4, ...: the centroid nearest the cell centre (a quad
+// reduction), then the first test against it, whose survivors set bits of
+// the cell's LDS bitmap; the quad's first lane lists them in index order; each
+// lane then tests every fourth survivor against all the others and marks the
+// ones no survivor beats in a second bitmap, which the first lane writes out.
+constexpr int kVqTabCells = 64;  // cells per build workgroup
+
+__global__ __launch_bounds__(256) void k_vq_table_build(const float* __restrict__ c, int k,
+                                                        float lo, float hi, int nbins,
+                                                        uint8_t* __restrict__ table) {
+  __shared__ float4 cs[256];
+  __shared__ uint32_t first[kVqTabCells][8], keep[kVqTabCells][8];
+  __shared__ __align__(4) uint8_t surv[kVqTabCells][kVqTabSurv];
+  __shared__ int nsurv[kVqTabCells];
+  const int tid = threadIdx.x, slot = tid >> 2, q = tid & 3;
+  int bad = 0;
+  for (int i = tid; i < k; i += 256) {
+    const float4 v = ((const float4*)c)[i];
+    cs[i] = v;
+    bad |= !(fabsf(v.x) <= 0x1p32f && fabsf(v.y) <= 0x1p32f && fabsf(v.z) <= 0x1p32f &&
+             fabsf(v.w) <= 0x1p32f);
+  }
+  for (int i = tid; i < kVqTabCells * 8; i += 256) {
+    (&first[0][0])[i] = 0u;
+    (&keep[0][0])[i] = 0u;
+  }
+  bad = __syncthreads_or(bad);
+  if (blockIdx.x == 0 && tid == 0) {
+    VqTabHeader hd = {};
+    hd.nbins = nbins;
+    hd.k = k;
+    hd.lo = lo;
+    hd.hi = hi;
+    hd.tag = kVqTabTag;
+    *(VqTabHeader*)table = hd;
+  }
+  const int64_t cell = (int64_t)blockIdx.x * kVqTabCells + slot;
+  const bool live = cell < vq_tab_cells(nbins) && !bad;
+  uint8_t* counts = table + kVqTabHeader;
+  uint4* lists = (uint4*)(counts + vq_tab_counts_bytes(nbins));
+  float l[4], h[4];
+  vq_cell_box(live ? cell : 0, nbins, lo, hi, l, h);
+  // corner terms of a centroid: (l_j - c_j)^2, (h_j - c_j)^2 and Dmax
+  auto corners = [&](const float4 v, float (&a)[4], float (&b)[4]) {
+    const float cc[4] = {v.x, v.y, v.z, v.w};
+    float dm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = l[j] - cc[j], r = h[j] - cc[j];
+      a[j] = p * p;
+      b[j] = r * r;
+      dm += fmaxf(a[j], b[j]);
+    }
+    return dm;
+  };
+  // does the centroid with corner terms (a2, b2, d2) beat the one with (a, b, d) on the cell?
+  auto beaten = [](const float (&a)[4], const float (&b)[4], float d, const float (&a2)[4],
+                   const float (&b2)[4], float d2) {
+    float L = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) L += fminf(a[j] - a2[j], b[j] - b2[j]);
+    return L > 0x1p-17f * (d + d2) + 0x1p-100f;
+  };
+  if (live) {
+    // the centroid nearest the centre (any one: it only orders the work)
+    float best = INFINITY;
+    int c0 = q;
+#pragma unroll 4
+    for (int i = q; i < k; i += 4) {
+      const float4 v = cs[i];
+      const float cc[4] = {v.x, v.y, v.z, v.w};
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = 0.5f * (l[j] + h[j]) - cc[j];
+        d += e * e;
+      }
+      if (d < best) {
+        best = d;
+        c0 = i;
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 4; o <<= 1) {
+      const float ob = __shfl_xor(best, o);
+      const int oc = __shfl_xor(c0, o);
+      if (ob < best || (ob == best && oc < c0)) {
+        best = ob;
+        c0 = oc;
+      }
+    }
+    float a0[4], b0[4];
+    const float d0 = corners(cs[c0], a0, b0);
+#pragma unroll 4
+    for (int i = q; i < k; i += 4) {
+      float a[4], b[4];
+      const float d = corners(cs[i], a, b);
+      if (!beaten(a, b, d, a0, b0, d0)) atomicOr(&first[slot][i >> 5], 1u << (i & 31));
+    }
+  }
+  __syncthreads();
+  if (live && q == 0) {  // the survivors in index order
+    int n = 0;
+    for (int w = 0; w < 8; ++w) {
+      uint32_t bits = first[slot][w];
+      while (bits) {
+        const int i = 32 * w + __builtin_ctz(bits);
+        bits &= bits - 1;
+        if (n < kVqTabSurv) surv[slot][n] = (uint8_t)i;
+        ++n;
+      }
+    }
+    nsurv[slot] = n;
+  }
+  __syncthreads();
+  const int n = live ? nsurv[slot] : 0;
+  if (live && n <= kVqTabSurv) {
+    // survivors q, q + 4, ... against all the others, four comparators per
+    // step (their indices in one LDS word; bytes past n are never used)
+    for (int s = q; s < n; s += 4) {
+      float a[4], b[4];
+      const int ci = surv[slot][s];
+      const float d = corners(cs[ci], a, b);
+      bool out = false;
+      for (int t0 = 0; t0 < n && !out; t0 += 4) {
+        const uint32_t w = *(const uint32_t*)&surv[slot][t0];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float a2[4], b2[4];
+          const float d2 = corners(cs[(w >> (8 * r)) & 255u], a2, b2);
+          const int t = t0 + r;
+          out = out || (t < n && t != s && beaten(a, b, d, a2, b2, d2));
+        }
+      }
+      if (!out) atomicOr(&keep[slot][ci >> 5], 1u << (ci & 31));
+    }
+  }
+  __syncthreads();
+  if (!(cell < vq_tab_cells(nbins)) || q != 0) return;
+  int m = 0;
+  if (live && n <= kVqTabSurv) {
+    int last = 0;
+    for (int w = 0; w < 8; ++w) {
+      uint32_t bits = keep[slot][w];
+      while (bits) {
+        const int i = 32 * w + __builtin_ctz(bits);
+        bits &= bits - 1;
+        if (m < kVqTabCap) surv[slot][m] = (uint8_t)i;  // the survivor list is done with
+        last = i;
+        ++m;
+      }
+    }
+    // (m >= 1 always: a beating chain cannot close)
+    if (m >= 1 && m <= kVqTabCap)
+      for (int s = m; s < kVqTabCap; ++s) surv[slot][s] = (uint8_t)last;
+  }
+  if (m < 1 || m > kVqTabCap) {  // listed out: its rows take the other path
+    counts[cell] = (uint8_t)kVqTabFull;
+    return;
+  }
+  counts[cell] = (uint8_t)m;
+  const uint32_t* sw = (const uint32_t*)&surv[slot][0];
+  lists[2 * cell] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+  lists[2 * cell + 1] = make_uint4(sw[4], sw[5], sw[6], sw[7]);
+}
+
+__global__ void k_vq_list_reset(int32_t* __restrict__ list_n) {
+  if (threadIdx.x == 0) *list_n = 0;
+}
+
+// wave = 64 rows, one per lane; the candidates of the lane's cell are scanned
+// in order up to the wave's largest count (a scalar loop bound)
+__global__ __launch_bounds__(256) void k_vq_assign_table(
+    const float* __restrict__ x, int64_t n, const float* __restrict__ c, int k,
+    const uint8_t* __restrict__ table, int nbins, float lo, float hi, int32_t* __restrict__ idx,
+    int32_t* __restrict__ list_n, int32_t* __restrict__ list) {
+  __shared__ float4 cs[256];
+  for (int i = threadIdx.x; i < k; i += 256) cs[i] = ((const float4*)c)[i];
+  __syncthreads();
+  const VqTabHeader* hd = (const VqTabHeader*)table;
+  const bool ok = hd->tag == kVqTabTag && hd->nbins == nbins && hd->k == k &&
+                  __float_as_uint(hd->lo) == __float_as_uint(lo) &&
+                  __float_as_uint(hd->hi) == __float_as_uint(hi);
+  const uint8_t* counts = table + kVqTabHeader;
+  const uint4* lists = (const uint4*)(counts + vq_tab_counts_bytes(nbins));
+  const float inv_w = (float)nbins / (hi - lo), tmax = (float)nbins + 0x1p-12f;
+  const int lane = threadIdx.x & 63;
+  const int64_t ngroups = (n + 63) / 64;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; g < ngroups;
+       g += nwaves) {
+    const int64_t row = g * 64 + lane;
+    const bool live = row < n;
+    const float4 x4 = ((const float4*)x)[live ? row : 0];
+    const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+    bool in = ok && live;
+    int cell = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = (xv[j] - lo) * inv_w;
+      in = in && t >= -0x1p-12f && t <= tmax;
+      const int i = (int)(in ? fmaxf(t, 0.f) : 0.f);
+      cell = cell * nbins + (i < nbins ? i : nbins - 1);
+    }
+    // the count and the list together (a listed-out cell's list bytes are
+    // never written; its rows use no candidate, and any byte indexes cs)
+    int cnt = kVqTabFull;
+    uint4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+    if (in) {
+      cnt = counts[cell];
+      c0 = lists[2 * cell];
+      c1 = lists[2 * cell + 1];
+    }
+    const bool fast = cnt != kVqTabFull;
+    // the wave's largest count, bit by bit from ballots (counts <= 32)
+    const int cv = fast ? cnt : 0;
+    int top = 0;
+#pragma unroll
+    for (int b = 5; b >= 0; --b)
+      if (__ballot(cv >= (top | (1 << b)))) top |= 1 << b;
+    const uint32_t wl[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    float bd = INFINITY;
+    int bi = 0;
+    // four candidates per list word; the bytes past a lane's count repeat its
+    // last candidate
+#pragma unroll
+    for (int w = 0; w < kVqTabCap / 4; ++w) {
+      if (4 * w < top) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int ci = (int)((wl[w] >> (8 * q)) & 255u);
+          const float d = vq_dist4(xv, cs[ci]);
+          if (d < bd) {
+            bd = d;
+            bi = ci;
+          }
+        }
+      }
+    }
+    if (fast && live) idx[row] = bi;
+    const bool rest = live && !fast;
+    const uint64_t mask = __ballot(rest);
+    if (mask) {
+      int base = 0;
+      if (lane == 0) base = atomicAdd(list_n, (int)__popcll(mask));
+      base = __shfl(base, 0);
+      const int below = (int)__popcll(mask & ((1ull << lane) - 1));
+      if (rest) list[base + below] = (int32_t)row;
+    }
   }
 }
 
@@ -1447,6 +1786,69 @@ int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_vq_assign");
+  return SHARD_OK;
+}
+
+size_t shard_vq_table_bytes(int32_t k, int32_t nbins) {
+  if (k <= 0 || k > 256 || nbins < 1 || nbins > kVqTabMaxBins) return 0;
+  return (size_t)(kVqTabHeader + vq_tab_counts_bytes(nbins) + vq_tab_cells(nbins) * kVqTabCap);
+}
+
+int shard_vq_table_build(const float* centroids, int32_t k, float lo, float hi, int32_t nbins,
+                         void* table, size_t table_bytes, void* stream) {
+  if (!centroids || !table) return SHARD_ERR_ARG;
+  if (k <= 0 || k > 256 || k % 32 || nbins < 1 || nbins > kVqTabMaxBins) return SHARD_ERR_SHAPE;
+  if (!(std::isfinite(lo) && std::isfinite(hi) && hi > lo)) return SHARD_ERR_ARG;
+  if (std::max(std::fabs(lo), std::fabs(hi)) > 64.f * (hi - lo)) return SHARD_ERR_ARG;
+  if (((uintptr_t)centroids & 15) || ((uintptr_t)table & 15)) return SHARD_ERR_SHAPE;
+  if (table_bytes < shard_vq_table_bytes(k, nbins)) return SHARD_ERR_WORKSPACE;
+  const int64_t cells = vq_tab_cells(nbins);
+  hipLaunchKernelGGL(k_vq_table_build, dim3((unsigned)((cells + kVqTabCells - 1) / kVqTabCells)),
+                     dim3(4 * kVqTabCells), 0,
+                     (hipStream_t)stream, centroids, k, lo, hi, nbins, (uint8_t*)table);
+  SHARD_LAUNCH_CHECK("shard_vq_table_build");
+  return SHARD_OK;
+}
+
+size_t shard_vq_assign_table_workspace(int64_t n) {
+  if (n <= 0 || n >= ((int64_t)1 << 31)) return 0;
+  return (size_t)(n + 4) * sizeof(int32_t);  // the undecided-row count, then their rows
+}
+
+int shard_vq_assign_table(const float* x, int64_t n, const float* centroids, int32_t k,
+                          const void* table, size_t table_bytes, int32_t nbins, float lo,
+                          float hi, int32_t* idx, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (!x || !centroids || !table || !idx || n <= 0) return SHARD_ERR_ARG;
+  if (n >= ((int64_t)1 << 31)) return SHARD_ERR_SHAPE;
+  if (k <= 0 || k > 256 || k % 32 || nbins < 1 || nbins > kVqTabMaxBins) return SHARD_ERR_SHAPE;
+  if (((uintptr_t)x & 15) || ((uintptr_t)centroids & 15) || ((uintptr_t)table & 15))
+    return SHARD_ERR_SHAPE;
+  if (table_bytes < shard_vq_table_bytes(k, nbins)) return SHARD_ERR_WORKSPACE;
+  if (!workspace || ((uintptr_t)workspace & 3) ||
+      workspace_bytes < shard_vq_assign_table_workspace(n))
+    return SHARD_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* list_n = (int32_t*)workspace;
+  int32_t* list = list_n + 4;
+  hipLaunchKernelGGL(k_vq_list_reset, dim3(1), dim3(64), 0, s, list_n);
+  const dim3 grid(grid_cap(((n + 63) / 64 + 3) / 4, 4096)), block(256);
+  hipLaunchKernelGGL(k_vq_assign_table, grid, block, 0, s, x, n, centroids, (int)k,
+                     (const uint8_t*)table, (int)nbins, lo, hi, idx, list_n, list);
+  // the rows the table left undecided: at most 512 workgroups, each wave
+  // looping over the list length it reads
+  const dim3 lgrid(512);
+  switch (k / 32) {
+#define SHARD_VQ_LIST(NB)                                                                    \
+  case NB:                                                                                   \
+    hipLaunchKernelGGL((k_vq_assign_mfma<NB, true>), lgrid, block, 0, s, x, n, centroids, idx, \
+                       (const int32_t*)list, (const int32_t*)list_n);                          \
+    break;
+    SHARD_VQ_LIST(1) SHARD_VQ_LIST(2) SHARD_VQ_LIST(3) SHARD_VQ_LIST(4)
+    SHARD_VQ_LIST(5) SHARD_VQ_LIST(6) SHARD_VQ_LIST(7) SHARD_VQ_LIST(8)
+#undef SHARD_VQ_LIST
+  }
+  SHARD_LAUNCH_CHECK("shard_vq_assign_table");
   return SHARD_OK;
 }
 

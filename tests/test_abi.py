@@ -52,6 +52,29 @@ def test_argument_errors_without_gpu_work():
     assert lib.shard_decode_attn_noalloc(ctypes.byref(args), None) == -1
 
 
+def test_vq_table_sizes_and_argument_checks():
+    """The candidate-table entry points size and check on the host: the table
+    is a 64-byte header, a count byte per cell (padded to 16) and 32 list
+    bytes per cell; unsupported k, an empty or far-off-centre box and a short
+    table are refused before any launch (placeholder pointers, never used)."""
+    from shard_amd import _lib
+    lib = _lib.load()
+    assert lib.shard_vq_table_bytes(256, 20) == 64 + 160000 + 32 * 160000
+    assert lib.shard_vq_table_bytes(32, 3) == 64 + 96 + 32 * 81
+    assert lib.shard_vq_table_bytes(257, 20) == 0 and lib.shard_vq_table_bytes(256, 33) == 0
+    big = 1 << 30
+    p = ctypes.c_void_p(4096)
+    assert lib.shard_vq_table_build(None, 256, -1.0, 1.0, 20, p, big, None) == -1
+    assert lib.shard_vq_table_build(p, 100, -1.0, 1.0, 20, p, big, None) == -2
+    assert lib.shard_vq_table_build(p, 256, 1.0, -1.0, 20, p, big, None) == -1
+    assert lib.shard_vq_table_build(p, 256, 1000.0, 1001.0, 20, p, big, None) == -1
+    assert lib.shard_vq_table_build(p, 256, -1.0, 1.0, 20, p, 100, None) == -4
+    assert lib.shard_vq_assign_table_workspace(1000) == 4 * 1004
+    assert lib.shard_vq_assign_table_workspace(1 << 31) == 0
+    assert lib.shard_vq_assign_table(p, 1000, p, 256, p, big, 20, -1.0, 1.0, p, p, 16, None) == -4
+    assert lib.shard_vq_assign_table(p, 1000, p, 64, p, 100, 20, -1.0, 1.0, p, p, big, None) == -4
+
+
 def test_noalloc_refuses_calls_beyond_its_scratch_before_any_launch():
     """The size check of shard_decode_attn_noalloc runs on the host: with
     placeholder pointers (never dereferenced) and 375 forced splits the call

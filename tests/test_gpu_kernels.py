@@ -230,6 +230,178 @@ def test_vq_assign_out_of_range_centroids_bitexact(cuda, case):
     assert np.array_equal(got, want)
 
 
+def _normalized_rows(n, g):
+    """Rows shaped like shard_vq_prepare's output: in [-1, 1], most mass near
+    0 (Gaussian / 4), the channel maxima at exactly +-1."""
+    x = (0.25 * torch.randn(n, 4, generator=g)).clamp(-1.0, 1.0)
+    x[:64] = torch.where(torch.rand(64, 4, generator=g) < 0.5, -1.0, 1.0)
+    return x
+
+
+def _table_rows(c, g):
+    """Rows for the candidate table: normalized rows, hard rows (midpoints and
+    near ties of centroid pairs, rows on centroids, zero rows) squeezed into
+    the box, rows on cell boundaries and box faces, just outside the box, far
+    outside it, and non-finite rows."""
+    k = c.shape[0]
+    a = torch.randint(0, k, (4000,), generator=g)
+    b = torch.randint(0, k, (4000,), generator=g)
+    mid = 0.5 * (c[a] + c[b])
+    edges = torch.linspace(-1.0, 1.0, 21)[torch.randint(0, 21, (4000, 4), generator=g)]
+    nan, inf = float("nan"), float("inf")
+    special = torch.tensor([[nan, 0, 0, 0], [inf, 0, 0, 0], [-inf, 0.5, 0, 0], [1e30, 0, 0, 0],
+                            [1.0000001, 0, 0, 0], [-1.0000001, 0.3, 0.2, 0.1], [1.001, 1, 1, 1],
+                            [0, 0, 0, 0], [1e-40, 0, 0, 0], [-0.0, 0, 0, 0], [1, 1, 1, 1],
+                            [-1, -1, -1, -1]])
+    return torch.cat([_normalized_rows(40000, g), mid,
+                      mid + 1e-7 * torch.randn(4000, 4, generator=g),
+                      c[a] + 1e-6 * torch.randn(4000, 4, generator=g), c[a[:300]],
+                      edges, edges + 1e-7 * torch.randn(4000, 4, generator=g),
+                      torch.zeros(50, 4), 3.0 * torch.randn(500, 4, generator=g), special])
+
+
+def _table_case(k, g):
+    """A codebook drawn from normalized rows with duplicate, zero and
+    nearly-equal centroids (exact ties: first index wins)."""
+    c = _normalized_rows(4 * k, g)[64 + torch.randperm(4 * k - 64, generator=g)[:k]].clone()
+    c[3] = c[5]
+    c[7] = 0.0
+    c[k - 1] = c[0] * (1 + 2 ** -20)
+    return c
+
+
+@pytest.mark.parametrize("k,nbins", [(256, 20), (256, 32), (96, 8), (32, 1), (256, 3)])
+def test_vq_assign_table_bitexact(cuda, k, nbins):
+    """Nearest centroid through the candidate table (most rows decided from
+    their cell's list, the rest by the all-centroid kernel) against the
+    sequential direct-distance oracle, on rows built to sit on cell boundaries,
+    box faces, near ties and outside the box."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(4000 + 7 * k + nbins)
+    c = _table_case(k, g)
+    x = _table_rows(c, g)
+    x = x[torch.randperm(x.shape[0], generator=g)][: x.shape[0] - 13]  # ragged tail
+    table = ops.VqTable(c.to(cuda), nbins=nbins)
+    got = ops.vq_assign_table(x.to(cuda), table).cpu().numpy()
+    with np.errstate(all="ignore"):
+        want = ref.vq_assign_direct(x.numpy(), c.numpy())
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} rows differ, first {bad[:5]}: got {got[bad[:5]]} want {want[bad[:5]]}"
+    # and the same as the all-centroid kernel
+    assert np.array_equal(got, ops.vq_assign(x.to(cuda), c.to(cuda)).cpu().numpy())
+
+
+def _read_table(table):
+    """(counts (cells,), lists (cells, 32)) of a built table."""
+    raw = table.table.cpu().numpy()
+    cells = table.nbins ** 4
+    counts = raw[64:64 + cells]
+    off = 64 + ((cells + 15) & ~15)
+    lists = raw[off:off + 32 * cells].reshape(cells, 32)
+    return counts, lists
+
+
+def test_vq_table_lists_every_nearest_centroid(cuda):
+    """The table's own contract, cell by cell: counts within 1..32 (255 marks a
+    cell whose rows take the other path), lists ascending and padded with
+    their last entry, and for sampled rows of each sampled cell (its corners,
+    its centre, random interior points) the oracle's nearest centroid is
+    listed."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(31)
+    k, nbins = 256, 12
+    c = _table_case(k, g)
+    table = ops.VqTable(c.to(cuda), nbins=nbins)
+    counts, lists = _read_table(table)
+    listed = counts != 255
+    assert listed.mean() > 0.99
+    assert counts[listed].min() >= 1 and counts[listed].max() <= 32
+    w = 2.0 / nbins
+    cells = torch.randperm(nbins ** 4, generator=g)[:3000].numpy()
+    rows, owner = [], []
+    for cell in cells:
+        ijk = np.array([(cell // nbins ** (3 - j)) % nbins for j in range(4)])
+        lo = -1.0 + ijk * w
+        corners = lo + w * np.array([[(m >> j) & 1 for j in range(4)] for m in range(16)])
+        inner = lo + w * torch.rand(8, 4, generator=g).numpy()
+        pts = np.concatenate([corners, inner, (lo + 0.5 * w)[None]]).astype(np.float32)
+        rows.append(pts)
+        owner += [cell] * len(pts)
+    rows = np.concatenate(rows)
+    owner = np.array(owner)
+    want = ref.vq_assign_direct(rows, c.numpy())
+    for cell in cells:
+        n = counts[cell]
+        if n == 255:
+            continue
+        lst = lists[cell]
+        assert np.all(np.diff(lst[:n].astype(int)) > 0), "list not ascending"
+        assert np.all(lst[n:] == lst[n - 1]), "padding is not the last candidate"
+        assert np.all(np.isin(want[owner == cell], lst[:n])), f"cell {cell} misses a nearest centroid"
+
+
+@pytest.mark.parametrize("case", ["nan_centroid", "huge_centroids", "other_box"])
+def test_vq_assign_table_undecidable_tables_bitexact(cuda, case):
+    """Tables that decide nothing (a non-finite centroid, centroids above 2^32,
+    or a call whose box differs from the build's): every row takes the
+    all-centroid path and the result is still the oracle's."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(78)
+    c = _table_case(256, g)
+    if case == "nan_centroid":
+        c[9] = float("nan")
+        c[10, 2] = float("inf")
+    elif case == "huge_centroids":
+        c[11] = 1e12
+    x = _normalized_rows(9000, g)
+    table = ops.VqTable(c.to(cuda))
+    if case == "other_box":
+        table.hi = 2.0  # a table built for [-1, 1] used as if for [-1, 2]
+    lib = __import__("shard_amd._lib", fromlist=["load"]).load()
+    ws = torch.zeros(lib.shard_vq_assign_table_workspace(x.shape[0]), dtype=torch.uint8, device=cuda)
+    got = ops.vq_assign_table(x.to(cuda), table, ws=ws).cpu().numpy()
+    with np.errstate(all="ignore"):
+        want = ref.vq_assign_direct(x.numpy(), c.numpy())
+    assert np.array_equal(got, want)
+    assert int(ws[:4].view(torch.int32).item()) == x.shape[0]  # every row took the other path
+
+
+def test_vq_assign_table_decides_normalized_rows_itself(cuda):
+    """On normalized rows (shard_vq_prepare's range) with a codebook drawn
+    from them, the table decides almost every row (the undecided count is
+    the workspace's first word)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(79)
+    c = _table_case(256, g)
+    x = _normalized_rows(200000, g)
+    table = ops.VqTable(c.to(cuda))
+    lib = __import__("shard_amd._lib", fromlist=["load"]).load()
+    ws = torch.zeros(lib.shard_vq_assign_table_workspace(x.shape[0]), dtype=torch.uint8, device=cuda)
+    got = ops.vq_assign_table(x.to(cuda), table, ws=ws).cpu().numpy()
+    assert np.array_equal(got, ref.vq_assign_direct(x.numpy(), c.numpy()))
+    undecided = int(ws[:4].view(torch.int32).item())
+    assert undecided < 0.001 * x.shape[0], undecided
+
+
+def test_kmeans_through_the_table_equals_the_all_centroid_path(cuda, monkeypatch):
+    """k-means with the per-iteration candidate table (taken from
+    VQ_TABLE_MIN_ROWS rows on) gives the same centroids and indices as with
+    the all-centroid assignment, on normalized rows from shard_vq_prepare."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(5)
+    v = torch.randn(2, 8, 700, 128, generator=g).half()
+    v[..., 3] *= 8
+    x, _, _ = ops.vq_prepare(v.to(cuda).reshape(16, 700, 128))
+    c1, i1 = ops.kmeans(x, 256, n_iter=6)
+    calls = []
+    real = ops.vq_assign_table
+    monkeypatch.setattr(ops, "VQ_TABLE_MIN_ROWS", 0)
+    monkeypatch.setattr(ops, "vq_assign_table", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    c2, i2 = ops.kmeans(x, 256, n_iter=6)
+    assert len(calls) == 6
+    assert torch.equal(c1, c2) and torch.equal(i1, i2)
+
+
 @pytest.mark.parametrize("n,k,d,assign", [(70000, 256, 4, "nearest"), (9000, 1000, 8, "random"),
                                           (4097, 3, 2, "random"), (130, 1, 1, "random"),
                                           (200000, 64, 4, "skewed")])
@@ -495,6 +667,9 @@ def test_prefill_kernels_at_config4_layer_size(cuda):
     idx = ops.vq_assign(x, codebook.to(cuda)).cpu().numpy().astype(np.int64)
     want_idx = cref.vq_assign_direct(xc.numpy(), codebook.numpy())
     assert np.array_equal(idx, want_idx), int((idx != want_idx).sum())
+    print(f"[config4 layer] vq_assign_table on {xc.shape[0]} subvectors", flush=True)
+    tidx = ops.vq_assign_table(x, ops.VqTable(codebook.to(cuda))).cpu().numpy().astype(np.int64)
+    assert np.array_equal(tidx, want_idx), int((tidx != want_idx).sum())
     del x, xc
 
     # the K front end at full size: undo RoPE and centring into the fp16 operand
