@@ -68,6 +68,16 @@ __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, 
 __device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+// a / b correctly rounded from y = div_rn(1, b) (Markstein's theorem: with y
+// within half an ulp of 1/b and q within one ulp of a/b, the exact residual
+// r = a - b q and RN(q + r y) give RN(a / b)), for quotients in the normal
+// range: three full-rate operations instead of the division sequence.  The
+// residual is formed as -(b q - a) so that a zero a keeps its sign.
+__device__ __forceinline__ float div_by_rcp(float a, float b, float y) {
+  const float q = a * y;
+  const float r = -__builtin_fmaf(b, q, -a);
+  return __builtin_fmaf(r, y, q);
+}
 
 // ---- cross-lane exchange without the LDS crossbar.
 // DPP moves inside rows of 16 lanes; v_permlane16_swap / v_permlane32_swap

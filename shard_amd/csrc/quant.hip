@@ -390,12 +390,24 @@ __global__ __launch_bounds__(256) void k_vq_rot(const uint16_t* __restrict__ v, 
     const uint16_t* src = v + b * bh_stride;
     float* dst = xo + b * seq * d;
     // lane l holds channels E l .. E l + E - 1 (contiguous-layout FWHT)
-    float m[E], cs[E];
+    // pass 2 divides by sqrt(d), then by the channel scale, each division
+    // through its divisor's correctly rounded reciprocal (div_by_rcp: the
+    // quotients of finite fp16 rows are normal, |FWHT| being >= 2^-24 or 0
+    // and the scales in [1e-8, 1e6]).  A head with an infinite value (so an
+    // infinite channel scale) divides with div_rn throughout.
+    float m[E], cs[E], rcs[E];
+    const float sd = (float)sqrt((double)d), rsd = div_rn(1.f, sd);
+    bool finite = true;
 #pragma unroll
     for (int k = 0; k < E; ++k) {
       m[k] = 0.f;
-      if constexpr (NORM) cs[k] = ch[b * d + E * l + k];
+      if constexpr (NORM) {
+        cs[k] = ch[b * d + E * l + k];
+        rcs[k] = div_rn(1.f, cs[k]);
+        finite = finite && fabsf(cs[k]) <= 0x1.fffffep127f;
+      }
     }
+    const bool by_rcp = __ballot(!finite) == 0;  // wave-uniform
     // raw rows (E halves per lane) of a step; the next step's loads are issued
     // before this step's transforms
     auto load_rows = [&](int64_t tt, uint32_t (&u)[RS][(E + 1) / 2]) {
@@ -427,16 +439,24 @@ __global__ __launch_bounds__(256) void k_vq_rot(const uint16_t* __restrict__ v, 
         if (t + q >= t1) break;  // wave-uniform
         // the statistics pass keeps max |y| of the unscaled transform: dividing
         // by sqrt(d) rounds monotonically, so max |RN(y / s)| = RN(max |y| / s)
-        wave_fwht_contig<E, NORM>(x[q], d);
+        wave_fwht_contig<E, false>(x[q], d);
         if constexpr (NORM) {
+          float y[E];
+          if (by_rcp) {
+#pragma unroll
+            for (int k = 0; k < E; ++k)
+              y[k] = div_by_rcp(div_by_rcp(x[q][k], sd, rsd), cs[k], rcs[k]);
+          } else {
+#pragma unroll
+            for (int k = 0; k < E; ++k) y[k] = div_rn(div_rn(x[q][k], sd), cs[k]);
+          }
           float* o = dst + (t + q) * d + E * l;
           if constexpr (E == 1) {
-            o[0] = div_rn(x[q][0], cs[0]);
+            o[0] = y[0];
           } else if constexpr (E == 2) {
-            *(float2*)o = make_float2(div_rn(x[q][0], cs[0]), div_rn(x[q][1], cs[1]));
+            *(float2*)o = make_float2(y[0], y[1]);
           } else {
-            *(float4*)o = make_float4(div_rn(x[q][0], cs[0]), div_rn(x[q][1], cs[1]),
-                                      div_rn(x[q][2], cs[2]), div_rn(x[q][3], cs[3]));
+            *(float4*)o = make_float4(y[0], y[1], y[2], y[3]);
           }
         } else {
 #pragma unroll

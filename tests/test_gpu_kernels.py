@@ -156,7 +156,39 @@ def test_vq_prepare_bitexact(cuda):
     x, ch32, ch16 = ops.vq_prepare(v.to(cuda)[:, :, start:end, :].reshape(B * G, end - start, D))
     assert np.array_equal(ch32.cpu().numpy(), ch.numpy())
     assert np.array_equal(ch16.cpu().numpy().view(np.uint16), ch.half().numpy().view(np.uint16))
-    assert np.array_equal(x.cpu().numpy(), want.numpy())
+    assert np.array_equal(x.cpu().numpy().view(np.uint32), want.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_vq_prepare_bits_at_the_edges(cuda, D):
+    """shard_vq_prepare's rows and channel scales bit for bit (signed zeros
+    included) against the reference's hadamard + division, per head size, on
+    heads built to reach the divisions' edges: an all-zero head (scales
+    clamped to 1e-8), a head of negative zeros, rows at +-65504, fp16
+    subnormals, and a head holding an infinity (infinite scales: that head
+    divides with the IEEE sequence)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(30 + D)
+    BG, T = 7, 257
+    v = torch.randn(BG, T, D, generator=g).half()
+    v[0, :, 5] *= 8
+    v[1] = 0.0
+    v[2] = -0.0
+    v[3, 0, :] = 65504.0
+    v[3, 1, :] = -65504.0
+    v[4] = (v[4].float() * 1e-6).half()
+    v[6, 3, 9] = float("inf")
+    rot = ref.hadamard(v.float())
+    ch = rot.abs().amax(dim=1).clamp(min=1e-8)
+    with np.errstate(all="ignore"):
+        want = (rot / ch.unsqueeze(1)).reshape(BG, -1).numpy()
+    x, ch32, _ = ops.vq_prepare(v.to(cuda))
+    assert np.array_equal(ch32.cpu().numpy().view(np.uint32), ch.numpy().view(np.uint32))
+    got = x.cpu().numpy().reshape(BG, -1)
+    assert np.array_equal(got[:6].view(np.uint32), want[:6].view(np.uint32))
+    nan = np.isnan(want[6])
+    assert np.array_equal(np.isnan(got[6]), nan)
+    assert np.array_equal(got[6][~nan].view(np.uint32), want[6][~nan].view(np.uint32))
 
 
 def test_vq_assign_bitexact(cuda):
@@ -653,7 +685,8 @@ def test_prefill_kernels_at_config4_layer_size(cuda):
     rot = ref.hadamard(v.float().reshape(B * G, T, D))
     ch = rot.abs().amax(dim=1).clamp(min=1e-8)
     assert np.array_equal(ch32.cpu().numpy(), ch.numpy())
-    assert np.array_equal(x.cpu().numpy(), (rot / ch.unsqueeze(1)).reshape(-1, 4).numpy())
+    assert np.array_equal(x.cpu().numpy().view(np.uint32),
+                          (rot / ch.unsqueeze(1)).reshape(-1, 4).numpy().view(np.uint32))
     del rot
     # the layer's nearest-centroid stage at full size: its 8.4M subvectors
     # against a seeded codebook drawn from them, bit-exact with the C oracle
