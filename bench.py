@@ -480,7 +480,8 @@ def prefill(dev, layers=32, batch=4, T=8192):
     pass: every layer has the same positions), per-column int4 quantization +
     packing, FWHT + channel normalization of V, nearest-centroid assignment to
     a seeded codebook (through its candidate table, built once in the timed
-    region: every layer uses the same codebook).  `value` runs each layer's K
+    region: every layer uses the same codebook; the normalized subvectors are
+    formed in the assigning kernel's registers).  `value` runs each layer's K
     and V chains on two streams; `one_stream` times the same work on one
     stream (where the projection's share is measured)."""
     from shard_amd import ops, bench_data
@@ -508,8 +509,11 @@ def prefill(dev, layers=32, batch=4, T=8192):
         return ops.int4_quant_pack(proj, bits)
 
     def v_pass(v, table):
-        x, _, _ = ops.vq_prepare(v.reshape(batch * G, T, D))
-        return ops.vq_assign_table(x, table)
+        # channel scales (FWHT pass 1 + fold), then the normalized subvectors
+        # formed in registers and assigned through the table (never written)
+        vr = v.reshape(batch * G, T, D)
+        ch, _, rcp = ops.vq_scales(vr)
+        return ops.vq_encode_table(vr, ch, rcp, table)
 
     def run(two_streams, evs=None):
         """All layers; with two_streams the K chain and the V chain of each

@@ -175,6 +175,28 @@ int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids
  * and a workspace of shard_vq_assign_table_workspace(n) bytes (the undecided
  * rows); n < 2^31. */
 size_t shard_vq_table_bytes(int32_t k, int32_t nbins);
+/* shard_vq_prepare's first half (cache.py:43-44: the FWHT's per-(bh,
+ * channel) max |.|, clamped): ch_f32 (bh, hd), optional ch_f16 and ch_rcp
+ * (the scales' correctly rounded reciprocals, for shard_vq_encode_table);
+ * the same workspace as shard_vq_prepare. */
+int shard_vq_scales(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
+                    int64_t v_bh_stride, float* ch_f32, uint16_t* ch_f16, float* ch_rcp,
+                    void* workspace, size_t workspace_bytes, void* stream);
+/* vq_encode against a given codebook (cache.py:41-52 with the k-means step
+ * replaced by one assignment, triton_kernels.py:689-746): the normalized
+ * subvectors of shard_vq_prepare are formed in registers from V (hd = 128,
+ * 8-byte aligned rows, v_bh_stride % 4 == 0) and assigned through a table
+ * of those centroids (built for the box [lo, hi]^4; lo = -1, hi = 1 holds
+ * every normalized row), without writing them out: idx (bh * seq * 32)
+ * equals shard_vq_assign_table(shard_vq_prepare(v).x).  ch_f32 / ch_rcp from
+ * shard_vq_scales; workspace shard_vq_encode_table_workspace(bh * seq * 32)
+ * bytes, 16-byte aligned (the undecided rows and their values). */
+size_t shard_vq_encode_table_workspace(int64_t n_rows);
+int shard_vq_encode_table(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
+                          int64_t v_bh_stride, const float* ch_f32, const float* ch_rcp,
+                          const float* centroids, int32_t k, const void* table,
+                          size_t table_bytes, int32_t nbins, float lo, float hi, int32_t* idx,
+                          void* workspace, size_t workspace_bytes, void* stream);
 int shard_vq_table_build(const float* centroids, int32_t k, float lo, float hi,
                          int32_t nbins, void* table, size_t table_bytes, void* stream);
 size_t shard_vq_assign_table_workspace(int64_t n);

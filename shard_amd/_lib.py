@@ -66,6 +66,12 @@ SIGNATURES = [
     ("shard_vq_prepare", c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("shard_vq_assign", c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     ("shard_vq_table_bytes", c_size_t, [c_int32, c_int32]),
+    ("shard_vq_scales", c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int64, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_size_t, c_void_p]),
+    ("shard_vq_encode_table_workspace", c_size_t, [c_int64]),
+    ("shard_vq_encode_table", c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int64, c_void_p, c_void_p, c_void_p,
+                                        c_int32, c_void_p, c_size_t, c_int32, c_float, c_float, c_void_p,
+                                        c_void_p, c_size_t, c_void_p]),
     ("shard_vq_table_build", c_int32, [c_void_p, c_int32, c_float, c_float, c_int32, c_void_p, c_size_t, c_void_p]),
     ("shard_vq_assign_table_workspace", c_size_t, [c_int64]),
     ("shard_vq_assign_table", c_int32, [c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_size_t, c_int32, c_float,

@@ -482,7 +482,7 @@ __global__ __launch_bounds__(256) void k_vq_rot(const uint16_t* __restrict__ v, 
 // the fp32 / fp16 copies the caller asked for.
 __global__ __launch_bounds__(256) void k_vq_fold(const float* __restrict__ part, int64_t bh, int d,
                                                  int nslots, float* __restrict__ ch, float* ch_f32,
-                                                 uint16_t* ch_f16) {
+                                                 uint16_t* ch_f16, float* ch_rcp = nullptr) {
   __shared__ float red[256];
   const int tid = threadIdx.x, c = tid & (d - 1), j0 = tid / d, nj = 256 / d;
   for (int64_t b = blockIdx.x; b < bh; b += gridDim.x) {
@@ -498,6 +498,7 @@ __global__ __launch_bounds__(256) void k_vq_fold(const float* __restrict__ part,
       ch[b * d + tid] = v;
       if (ch_f32) ch_f32[b * d + tid] = v;
       if (ch_f16) ch_f16[b * d + tid] = f2h(v);
+      if (ch_rcp) ch_rcp[b * d + tid] = div_rn(1.f, v);
     }
   }
 }
@@ -605,15 +606,20 @@ __device__ __forceinline__ void split3(float v, __bf16& h, __bf16& m, __bf16& l)
 }
 
 // (256, 2): at most 256 registers per lane, so the MFMA results land in VGPRs.
-// LIST: the rows are x[list[i]] for i < *list_n (the rows another kernel left
-// undecided), each answer written to idx[list[i]]; n is ignored.
-template <int NB, bool LIST = false>
+// LIST 1: the rows are x[list[i]] for i < *list_n (the rows another kernel
+// left undecided), each answer written to idx[list[i]]; n is ignored.
+// LIST 2: the same with the rows' values in list_x[i] (x is not read).
+template <int NB, int LIST = 0>
 __global__ __launch_bounds__(256, 2)
 void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __restrict__ c,
                       int32_t* __restrict__ idx, const int32_t* __restrict__ list = nullptr,
-                      const int32_t* __restrict__ list_n = nullptr) {
+                      const int32_t* __restrict__ list_n = nullptr,
+                      const float4* __restrict__ list_x = nullptr) {
   constexpr int K = 32 * NB;
-  if constexpr (LIST) n = *list_n;
+  if constexpr (LIST != 0) {
+    n = *list_n;
+    if (n == 0) return;  // the usual case: nothing left undecided
+  }
   __shared__ float4 cs[K];
   __shared__ bf16x8 atab[NB][2][64];  // the A operands again, for the rare rescans
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
@@ -667,8 +673,8 @@ void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __res
     const int64_t pos = g * 32 + col;
     const bool valid = pos < n;
     int64_t row = pos;
-    if constexpr (LIST) row = valid ? list[pos] : 0;
-    const float4 x4 = ((const float4*)x)[valid ? row : 0];
+    if constexpr (LIST != 0) row = valid ? list[pos] : 0;
+    const float4 x4 = LIST == 2 ? list_x[valid ? pos : 0] : ((const float4*)x)[valid ? row : 0];
     const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
     // B operands: lane (row col, half hh): first [xh, xh] (hh 0) | [xm, xh]
     // (hh 1), second [xl, xm] (hh 0) | [1, 1, 1, bias, 0, 0, 0, 0] (hh 1)
@@ -1033,12 +1039,28 @@ __global__ void k_vq_list_reset(int32_t* __restrict__ list_n) {
   if (threadIdx.x == 0) *list_n = 0;
 }
 
+// Rows for k_vq_assign_table<true>: computed from V (head_dim 128) as
+// shard_vq_prepare's pass 2 computes them, instead of read from x.
+struct VqFromV {
+  const uint16_t* v;
+  int64_t seq, bh_stride;
+  const float* ch;   // (bh, 128) channel scales
+  const float* rch;  // their correctly rounded reciprocals
+};
+
 // wave = 64 rows, one per lane; the candidates of the lane's cell are scanned
-// in order up to the wave's largest count (a scalar loop bound)
+// in order up to the wave's largest count (a scalar loop bound).  FROM_V: the
+// wave's rows are two tokens' 32 subvectors, lane l holding subvector l % 32
+// of token 2 g + l / 32: the lane loads its 4 values of V, the FWHT runs
+// within each half-wave (strides 1, 2 in the lane, then lanes 1..16 apart:
+// the reference's stage order), and the row is divided by sqrt(128) and its
+// channel scales; undecided rows go to the list with their values.
+template <bool FROM_V>
 __global__ __launch_bounds__(256) void k_vq_assign_table(
     const float* __restrict__ x, int64_t n, const float* __restrict__ c, int k,
     const uint8_t* __restrict__ table, int nbins, float lo, float hi, int32_t* __restrict__ idx,
-    int32_t* __restrict__ list_n, int32_t* __restrict__ list) {
+    int32_t* __restrict__ list_n, int32_t* __restrict__ list, float4* __restrict__ list_x,
+    const VqFromV fv) {
   __shared__ float4 cs[256];
   for (int i = threadIdx.x; i < k; i += 256) cs[i] = ((const float4*)c)[i];
   __syncthreads();
@@ -1052,12 +1074,77 @@ __global__ __launch_bounds__(256) void k_vq_assign_table(
   const int lane = threadIdx.x & 63;
   const int64_t ngroups = (n + 63) / 64;
   const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; g < ngroups;
-       g += nwaves) {
+  const float sd = (float)sqrt(128.0), rsd = div_rn(1.f, sd);
+  // a row's inputs (x, or its V values and channel scales) are loaded one
+  // group ahead
+  struct In {
+    uint4 a;       // x, or (V's 4 halves, -, -)
+    float4 c, r;   // FROM_V: the channel scales and their reciprocals
+  };
+  const int64_t g0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  auto load_in = [&](int64_t g) {
     const int64_t row = g * 64 + lane;
     const bool live = row < n;
-    const float4 x4 = ((const float4*)x)[live ? row : 0];
-    const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+    In in_;
+    if constexpr (FROM_V) {
+      const int64_t tok = live ? row >> 5 : 0;
+      const int64_t b = tok / fv.seq, t = tok - b * fv.seq;
+      const int j = lane & 31;
+      const uint2 raw = *(const uint2*)(fv.v + b * fv.bh_stride + t * 128 + 4 * j);
+      in_.a = make_uint4(raw.x, raw.y, 0u, 0u);
+      in_.c = *(const float4*)(fv.ch + b * 128 + 4 * j);
+      in_.r = *(const float4*)(fv.rch + b * 128 + 4 * j);
+    } else {
+      in_.a = __builtin_bit_cast(uint4, ((const float4*)x)[live ? row : 0]);
+    }
+    return in_;
+  };
+  In nxt = {};
+  if (g0 < ngroups) nxt = load_in(g0);
+  for (int64_t g = g0; g < ngroups; g += nwaves) {
+    const int64_t row = g * 64 + lane;
+    const bool live = row < n;
+    const In in_ = nxt;
+    if (g + nwaves < ngroups) nxt = load_in(g + nwaves);
+    float xv[4];
+    if constexpr (FROM_V) {
+      const uint2 raw = make_uint2(in_.a.x, in_.a.y);
+      float u[4] = {h2f((uint16_t)raw.x), h2f((uint16_t)(raw.x >> 16)), h2f((uint16_t)raw.y),
+                    h2f((uint16_t)(raw.y >> 16))};
+      // strides 1 and 2 inside the lane, then 4 .. 64 across lanes 1 .. 16 apart
+#pragma unroll
+      for (int h = 1; h < 4; h <<= 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((e & h) == 0) {
+            const float a0 = u[e], a1 = u[e | h];
+            u[e] = add_rn(a0, a1);
+            u[e | h] = sub_rn(a0, a1);
+          }
+      fwht_lane_stage<1>(u, lane);
+      fwht_lane_stage<2>(u, lane);
+      fwht_lane_stage<4>(u, lane);
+      fwht_lane_stage<8>(u, lane);
+      fwht_lane_stage<16>(u, lane);
+      const float cc[4] = {in_.c.x, in_.c.y, in_.c.z, in_.c.w};
+      const float rr[4] = {in_.r.x, in_.r.y, in_.r.z, in_.r.w};
+      bool finite = true;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) finite = finite && fabsf(cc[e]) <= 0x1.fffffep127f;
+      if (__ballot(!finite) == 0) {  // as shard_vq_prepare: reciprocals unless a scale is infinite
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = div_by_rcp(div_by_rcp(u[e], sd, rsd), cc[e], rr[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = div_rn(div_rn(u[e], sd), cc[e]);
+      }
+    } else {
+      const float4 x4 = __builtin_bit_cast(float4, in_.a);
+      xv[0] = x4.x;
+      xv[1] = x4.y;
+      xv[2] = x4.z;
+      xv[3] = x4.w;
+    }
     bool in = ok && live;
     int cell = 0;
 #pragma unroll
@@ -1110,7 +1197,10 @@ __global__ __launch_bounds__(256) void k_vq_assign_table(
       if (lane == 0) base = atomicAdd(list_n, (int)__popcll(mask));
       base = __shfl(base, 0);
       const int below = (int)__popcll(mask & ((1ull << lane) - 1));
-      if (rest) list[base + below] = (int32_t)row;
+      if (rest) {
+        list[base + below] = (int32_t)row;
+        if constexpr (FROM_V) list_x[base + below] = make_float4(xv[0], xv[1], xv[2], xv[3]);
+      }
     }
   }
 }
@@ -1774,6 +1864,84 @@ int shard_vq_prepare(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int
   return SHARD_OK;
 }
 
+int shard_vq_scales(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int64_t v_bh_stride,
+                    float* ch_f32, uint16_t* ch_f16, float* ch_rcp, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (!v || !ch_f32 || bh <= 0 || seq <= 0) return SHARD_ERR_ARG;
+  if (hd != 64 && hd != 128 && hd != 256) return SHARD_ERR_SHAPE;
+  const int E = hd / 64;
+  if (((uintptr_t)v & (2 * E - 1)) || (v_bh_stride % E)) return SHARD_ERR_SHAPE;
+  if (!workspace || workspace_bytes < shard_vq_prepare_workspace(bh, hd)) return SHARD_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  float* ch = part + (size_t)kVqSlots * bh * hd;
+  const int64_t nx = (seq + 63) / 64 < kVqSlots ? (seq + 63) / 64 : kVqSlots;
+  const dim3 rgrid((unsigned)nx, (unsigned)(bh < 65535 ? bh : 65535)), rblock(256);
+  const dim3 fgrid((unsigned)(bh < 65535 ? bh : 65535)), fblock(256);
+#define SHARD_VQ_PASS1(E)                                                                       \
+  hipLaunchKernelGGL((k_vq_rot<E, false>), rgrid, rblock, 0, s, v, bh, seq, v_bh_stride, part,  \
+                     (const float*)nullptr, (float*)nullptr)
+  switch (hd) {
+    case 64: SHARD_VQ_PASS1(1); break;
+    case 128: SHARD_VQ_PASS1(2); break;
+    default: SHARD_VQ_PASS1(4); break;
+  }
+#undef SHARD_VQ_PASS1
+  hipLaunchKernelGGL(k_vq_fold, fgrid, fblock, 0, s, part, bh, hd, (int)nx, ch, ch_f32, ch_f16,
+                     ch_rcp);
+  SHARD_LAUNCH_CHECK("shard_vq_scales");
+  return SHARD_OK;
+}
+
+size_t shard_vq_encode_table_workspace(int64_t n_rows) {
+  if (n_rows <= 0 || n_rows >= ((int64_t)1 << 31)) return 0;
+  // the undecided-row count, their rows, then their values (16-byte aligned)
+  return 16 + (size_t)((4 * n_rows + 15) & ~(int64_t)15) + (size_t)n_rows * 16;
+}
+
+int shard_vq_encode_table(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
+                          int64_t v_bh_stride, const float* ch_f32, const float* ch_rcp,
+                          const float* centroids, int32_t k, const void* table, size_t table_bytes,
+                          int32_t nbins, float lo, float hi, int32_t* idx, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (!v || !ch_f32 || !ch_rcp || !centroids || !table || !idx || bh <= 0 || seq <= 0)
+    return SHARD_ERR_ARG;
+  if (hd != 128) return SHARD_ERR_SHAPE;
+  const int64_t n = bh * seq * 32;  // 4-value subvectors
+  if (n >= ((int64_t)1 << 31)) return SHARD_ERR_SHAPE;
+  if (k <= 0 || k > 256 || k % 32 || nbins < 1 || nbins > kVqTabMaxBins) return SHARD_ERR_SHAPE;
+  if (((uintptr_t)v & 7) || (v_bh_stride % 4) || ((uintptr_t)ch_f32 & 15) ||
+      ((uintptr_t)ch_rcp & 15) || ((uintptr_t)centroids & 15) || ((uintptr_t)table & 15))
+    return SHARD_ERR_SHAPE;
+  if (table_bytes < shard_vq_table_bytes(k, nbins)) return SHARD_ERR_WORKSPACE;
+  if (!workspace || ((uintptr_t)workspace & 15) ||
+      workspace_bytes < shard_vq_encode_table_workspace(n))
+    return SHARD_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* list_n = (int32_t*)workspace;
+  int32_t* list = list_n + 4;
+  float4* list_x = (float4*)((char*)workspace + 16 + ((4 * n + 15) & ~(int64_t)15));
+  hipLaunchKernelGGL(k_vq_list_reset, dim3(1), dim3(64), 0, s, list_n);
+  const dim3 grid(grid_cap(((n + 63) / 64 + 3) / 4, 4096)), block(256);
+  hipLaunchKernelGGL(k_vq_assign_table<true>, grid, block, 0, s, (const float*)nullptr, n,
+                     centroids, (int)k, (const uint8_t*)table, (int)nbins, lo, hi, idx, list_n,
+                     list, list_x, VqFromV{v, seq, v_bh_stride, ch_f32, ch_rcp});
+  const dim3 lgrid(128);
+  switch (k / 32) {
+#define SHARD_VQ_LISTX(NB)                                                                   \
+  case NB:                                                                                   \
+    hipLaunchKernelGGL((k_vq_assign_mfma<NB, 2>), lgrid, block, 0, s, (const float*)nullptr, \
+                       n, centroids, idx, (const int32_t*)list, (const int32_t*)list_n,      \
+                       (const float4*)list_x);                                              \
+    break;
+    SHARD_VQ_LISTX(1) SHARD_VQ_LISTX(2) SHARD_VQ_LISTX(3) SHARD_VQ_LISTX(4)
+    SHARD_VQ_LISTX(5) SHARD_VQ_LISTX(6) SHARD_VQ_LISTX(7) SHARD_VQ_LISTX(8)
+#undef SHARD_VQ_LISTX
+  }
+  SHARD_LAUNCH_CHECK("shard_vq_encode_table");
+  return SHARD_OK;
+}
+
 int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids, int32_t k,
                     int32_t* idx, void* stream) {
   if (!x || !centroids || !idx || n <= 0 || k <= 0 || d <= 0) return SHARD_ERR_ARG;
@@ -1853,16 +2021,17 @@ int shard_vq_assign_table(const float* x, int64_t n, const float* centroids, int
   int32_t* list = list_n + 4;
   hipLaunchKernelGGL(k_vq_list_reset, dim3(1), dim3(64), 0, s, list_n);
   const dim3 grid(grid_cap(((n + 63) / 64 + 3) / 4, 4096)), block(256);
-  hipLaunchKernelGGL(k_vq_assign_table, grid, block, 0, s, x, n, centroids, (int)k,
-                     (const uint8_t*)table, (int)nbins, lo, hi, idx, list_n, list);
-  // the rows the table left undecided: at most 512 workgroups, each wave
-  // looping over the list length it reads
-  const dim3 lgrid(512);
+  hipLaunchKernelGGL(k_vq_assign_table<false>, grid, block, 0, s, x, n, centroids, (int)k,
+                     (const uint8_t*)table, (int)nbins, lo, hi, idx, list_n, list,
+                     (float4*)nullptr, VqFromV{});
+  // the rows the table left undecided: 128 workgroups, each wave looping
+  // over the list length it reads (all return at once when it is 0)
+  const dim3 lgrid(128);
   switch (k / 32) {
 #define SHARD_VQ_LIST(NB)                                                                    \
   case NB:                                                                                   \
-    hipLaunchKernelGGL((k_vq_assign_mfma<NB, true>), lgrid, block, 0, s, x, n, centroids, idx, \
-                       (const int32_t*)list, (const int32_t*)list_n);                          \
+    hipLaunchKernelGGL((k_vq_assign_mfma<NB, 1>), lgrid, block, 0, s, x, n, centroids, idx,    \
+                       (const int32_t*)list, (const int32_t*)list_n, (const float4*)nullptr);  \
     break;
     SHARD_VQ_LIST(1) SHARD_VQ_LIST(2) SHARD_VQ_LIST(3) SHARD_VQ_LIST(4)
     SHARD_VQ_LIST(5) SHARD_VQ_LIST(6) SHARD_VQ_LIST(7) SHARD_VQ_LIST(8)

@@ -308,6 +308,57 @@ def vq_assign_table(x: torch.Tensor, table: "VqTable", ws=None) -> torch.Tensor:
     return idx
 
 
+def _vq_rows(v: torch.Tensor):
+    """(bh, seq, D) view of V whose last two dims are contiguous."""
+    if v.dtype != torch.float16:
+        raise TypeError("V must be fp16")
+    D, seq = v.shape[-1], v.shape[-2]
+    v3 = v.reshape(-1, seq, D) if v.dim() != 3 else v
+    if v3.stride(-1) != 1 or v3.stride(-2) != D:
+        v3 = v3.contiguous()
+    return v3
+
+
+def vq_scales(v: torch.Tensor):
+    """shard_vq_prepare's channel scales alone: (ch fp32 (bh, D), ch fp16,
+    their reciprocals fp32)."""
+    _require_gpu(v)
+    lib = _lib.load()
+    v3 = _vq_rows(v)
+    bh, seq, D = v3.shape
+    dev = v.device
+    ch32 = torch.empty(bh, D, dtype=torch.float32, device=dev)
+    ch16 = torch.empty(bh, D, dtype=torch.float16, device=dev)
+    rcp = torch.empty(bh, D, dtype=torch.float32, device=dev)
+    ws = _workspace(lib.shard_vq_prepare_workspace(bh, D), dev)
+    _lib.check("shard_vq_scales", lib.shard_vq_scales(
+        _p(v3), bh, seq, D, v3.stride(0), _p(ch32), _p(ch16), _p(rcp), _p(ws), ws.numel(),
+        _stream(v)))
+    return ch32, ch16, rcp
+
+
+def vq_encode_table(v: torch.Tensor, ch32: torch.Tensor, rcp: torch.Tensor, table: "VqTable",
+                    ws=None) -> torch.Tensor:
+    """Indices of V's normalized subvectors (head_dim 128) through the table,
+    formed from V in registers: vq_assign_table(vq_prepare(v)[0], table)."""
+    _require_gpu(v, ch32, rcp)
+    lib = _lib.load()
+    v3 = _vq_rows(v)
+    bh, seq, D = v3.shape
+    n = bh * seq * (D // 4)
+    idx = torch.empty(n, dtype=torch.int32, device=v.device)
+    need = lib.shard_vq_encode_table_workspace(n)
+    if ws is None or ws.numel() < need:
+        ws = _workspace(need, v.device)
+    ch32 = _contig(ch32, torch.float32, "ch")
+    rcp = _contig(rcp, torch.float32, "rcp")
+    _lib.check("shard_vq_encode_table", lib.shard_vq_encode_table(
+        _p(v3), bh, seq, D, v3.stride(0), _p(ch32), _p(rcp), _p(table.centroids), table.k,
+        _p(table.table), table.table.numel(), table.nbins, table.lo, table.hi, _p(idx), _p(ws),
+        ws.numel(), _stream(v)))
+    return idx
+
+
 def kmeans_update(x: torch.Tensor, idx: torch.Tensor, centroids: torch.Tensor, ws=None):
     """One deterministic k-means update; returns (new_centroids, max_delta (1,) fp32)."""
     _require_gpu(x, idx, centroids)

@@ -323,6 +323,41 @@ def test_vq_assign_table_bitexact(cuda, k, nbins):
     assert np.array_equal(got, ops.vq_assign(x.to(cuda), c.to(cuda)).cpu().numpy())
 
 
+@pytest.mark.parametrize("B,G,T,nbins", [(2, 8, 772, 16), (1, 3, 325, 3)])
+def test_vq_encode_table_equals_prepare_then_assign(cuda, B, G, T, nbins):
+    """The fused V encoder (subvectors formed from V in registers, assigned
+    through the table, never written out) against shard_vq_prepare followed
+    by the table assignment, bit for bit, on a slice of the sequence (a row
+    stride past the slice), with outlier channels, a head at +-65504, an
+    all-zero head, a head holding an infinity (the IEEE division path), an odd
+    token count (a wave straddling the end) and, at 3 cells per dim, most
+    rows left to the all-centroid kernel (rows passed with their values)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    v = torch.randn(B, G, T, 128, generator=g).half()
+    v[..., 9] *= 8
+    v[0, 1, 7, :] = 65504.0
+    v[0, 1, 8, :] = -65504.0
+    v[0, 2] = 0.0
+    if G > 3:
+        v[0, 3, 11, 40] = float("inf")
+    start, end = 4, T - 64
+    vs = v.to(cuda)[:, :, start:end, :].reshape(B * G, end - start, 128)
+    x, ch32, ch16 = ops.vq_prepare(vs)
+    s32, s16, rcp = ops.vq_scales(vs)
+    assert np.array_equal(s32.cpu().numpy().view(np.uint32), ch32.cpu().numpy().view(np.uint32))
+    assert np.array_equal(s16.cpu().numpy().view(np.uint16), ch16.cpu().numpy().view(np.uint16))
+    assert torch.equal(rcp.cpu(), 1.0 / ch32.cpu())
+    gsel = torch.Generator().manual_seed(7)
+    finite = torch.isfinite(x).all(1)
+    pool = x[finite]
+    cb = pool[torch.randperm(pool.shape[0], generator=gsel)[:256].to(cuda)].contiguous()
+    table = ops.VqTable(cb, nbins=nbins)
+    want = ops.vq_assign_table(x, table)
+    got = ops.vq_encode_table(vs, s32, rcp, table)
+    assert torch.equal(got, want), int((got != want).sum())
+
+
 def _read_table(table):
     """(counts (cells,), lists (cells, 32)) of a built table."""
     raw = table.table.cpu().numpy()
@@ -701,8 +736,14 @@ def test_prefill_kernels_at_config4_layer_size(cuda):
     want_idx = cref.vq_assign_direct(xc.numpy(), codebook.numpy())
     assert np.array_equal(idx, want_idx), int((idx != want_idx).sum())
     print(f"[config4 layer] vq_assign_table on {xc.shape[0]} subvectors", flush=True)
-    tidx = ops.vq_assign_table(x, ops.VqTable(codebook.to(cuda))).cpu().numpy().astype(np.int64)
+    table = ops.VqTable(codebook.to(cuda))
+    tidx = ops.vq_assign_table(x, table).cpu().numpy().astype(np.int64)
     assert np.array_equal(tidx, want_idx), int((tidx != want_idx).sum())
+    print(f"[config4 layer] vq_encode_table on {xc.shape[0]} subvectors", flush=True)
+    vr = v.to(cuda).reshape(B * G, T, D)
+    s32, _, rcp = ops.vq_scales(vr)
+    eidx = ops.vq_encode_table(vr, s32, rcp, table).cpu().numpy().astype(np.int64)
+    assert np.array_equal(eidx, want_idx), int((eidx != want_idx).sum())
     del x, xc
 
     # the K front end at full size: undo RoPE and centring into the fp16 operand
