@@ -605,21 +605,12 @@ __device__ __forceinline__ void split3(float v, __bf16& h, __bf16& m, __bf16& l)
   l = (__bf16)(r - (float)m);
 }
 
-// (256, 2): at most 256 registers per lane, so the MFMA results land in VGPRs.
-// LIST 1: the rows are x[list[i]] for i < *list_n (the rows another kernel
-// left undecided), each answer written to idx[list[i]]; n is ignored.
-// LIST 2: the same with the rows' values in list_x[i] (x is not read).
-template <int NB, int LIST = 0>
+// (256, 2): at most 256 registers per lane, so the MFMA results land in VGPRs
+template <int NB>
 __global__ __launch_bounds__(256, 2)
 void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __restrict__ c,
-                      int32_t* __restrict__ idx, const int32_t* __restrict__ list = nullptr,
-                      const int32_t* __restrict__ list_n = nullptr,
-                      const float4* __restrict__ list_x = nullptr) {
+                      int32_t* __restrict__ idx) {
   constexpr int K = 32 * NB;
-  if constexpr (LIST != 0) {
-    n = *list_n;
-    if (n == 0) return;  // the usual case: nothing left undecided
-  }
   __shared__ float4 cs[K];
   __shared__ bf16x8 atab[NB][2][64];  // the A operands again, for the rare rescans
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hh = lane >> 5;
@@ -670,11 +661,9 @@ void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __res
   const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
   const float16v zero = {};
   for (int64_t g = ((int64_t)blockIdx.x * blockDim.x + tid) >> 6; g < ngroups; g += nwaves) {
-    const int64_t pos = g * 32 + col;
-    const bool valid = pos < n;
-    int64_t row = pos;
-    if constexpr (LIST != 0) row = valid ? list[pos] : 0;
-    const float4 x4 = LIST == 2 ? list_x[valid ? pos : 0] : ((const float4*)x)[valid ? row : 0];
+    const int64_t row = g * 32 + col;
+    const bool valid = row < n;
+    const float4 x4 = ((const float4*)x)[valid ? row : 0];
     const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
     // B operands: lane (row col, half hh): first [xh, xh] (hh 0) | [xm, xh]
     // (hh 1), second [xl, xm] (hh 0) | [1, 1, 1, bias, 0, 0, 0, 0] (hh 1)
@@ -826,8 +815,10 @@ void k_vq_assign_mfma(const float* __restrict__ x, int64_t n, const float* __res
 // max(|lo|, |hi|) <= 64 (hi - lo), which the build requires, so the row lies
 // in that cell's widened box.  Rows outside the box, non-finite rows and rows
 // of cells with more than kVqTabCap candidates are appended to a list that
-// the MFMA kernel (LIST) finishes.  A centroid set holding a non-finite value
-// or one above 2^32 in magnitude lists every cell out.
+// k_vq_list_direct finishes with the direct distance to every centroid (fine
+// for the few rows normalized data leaves there; rows not normalized to the
+// box belong with shard_vq_assign).  A centroid set holding a non-finite
+// value or one above 2^32 in magnitude lists every cell out.
 //
 // Table: a 64-byte header (nbins, k, lo, hi, a tag), one count byte per cell
 // (kVqTabFull: listed out), then kVqTabCap candidate bytes per cell padded
@@ -1035,8 +1026,60 @@ __global__ __launch_bounds__(256) void k_vq_table_build(const float* __restrict_
   lists[2 * cell + 1] = make_uint4(sw[4], sw[5], sw[6], sw[7]);
 }
 
-__global__ void k_vq_list_reset(int32_t* __restrict__ list_n) {
-  if (threadIdx.x == 0) *list_n = 0;
+// Undecided rows: wave w of a table assignment appends its rows (and, when
+// it formed them itself, their values) to region w of the workspace
+// (vq_list_per rows, the most it can meet) and stores their count in
+// counts[w], with no atomic; k_vq_list_direct reads every region.
+struct VqList {
+  int32_t* counts;  // one per wave of the launch
+  int32_t* rows;    // nwaves * per
+  float4* xs;       // nwaves * per values, or null
+  int64_t per;      // rows per region
+};
+inline void vq_list_geometry(int64_t n, int* grid, int64_t* per) {
+  const int64_t groups = (n + 63) / 64;  // 64 rows per wave
+  *grid = grid_cap((groups + 3) / 4, 4096);
+  const int64_t nwaves = (int64_t)*grid * 4;
+  *per = (groups + nwaves - 1) / nwaves * 64;
+}
+
+// The rows a table left undecided: the reference's direct distance to every
+// centroid in index order, strict < (k_vq_assign's rule).  A small kernel on
+// purpose: it follows every table assignment, usually to find every region
+// empty (then each workgroup returns after reading its share of the counts),
+// and must start at once beside other streams' kernels.
+template <bool WITH_X>
+__global__ __launch_bounds__(256) void k_vq_list_direct(const float* __restrict__ x,
+                                                        const float* __restrict__ c, int k,
+                                                        int32_t* __restrict__ idx,
+                                                        const VqList lst, int nregions) {
+  // thread t owns regions t, t + T, t + 2 T, ... (T threads in all)
+  const int t0 = blockIdx.x * 256 + threadIdx.x, nt = gridDim.x * 256;
+  int any = 0;
+  for (int r = t0; r < nregions; r += nt) any |= lst.counts[r] != 0;
+  if (!__syncthreads_or(any)) return;
+  __shared__ float4 cs[256];
+  for (int i = threadIdx.x; i < k; i += 256) cs[i] = ((const float4*)c)[i];
+  __syncthreads();
+  for (int r = t0; r < nregions; r += nt) {
+    const int cnt = lst.counts[r];
+    for (int i = 0; i < cnt; ++i) {
+      const int64_t slot = (int64_t)r * lst.per + i;
+      const int row = lst.rows[slot];
+      const float4 x4 = WITH_X ? lst.xs[slot] : ((const float4*)x)[row];
+      const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+      float bd = INFINITY;
+      int bi = 0;
+      for (int q = 0; q < k; ++q) {
+        const float d = vq_dist4(xv, cs[q]);
+        if (d < bd) {
+          bd = d;
+          bi = q;
+        }
+      }
+      idx[row] = bi;
+    }
+  }
 }
 
 // Rows for k_vq_assign_table<true>: computed from V (head_dim 128) as
@@ -1059,8 +1102,7 @@ template <bool FROM_V>
 __global__ __launch_bounds__(256) void k_vq_assign_table(
     const float* __restrict__ x, int64_t n, const float* __restrict__ c, int k,
     const uint8_t* __restrict__ table, int nbins, float lo, float hi, int32_t* __restrict__ idx,
-    int32_t* __restrict__ list_n, int32_t* __restrict__ list, float4* __restrict__ list_x,
-    const VqFromV fv) {
+    const VqList lst, const VqFromV fv) {
   __shared__ float4 cs[256];
   for (int i = threadIdx.x; i < k; i += 256) cs[i] = ((const float4*)c)[i];
   __syncthreads();
@@ -1101,6 +1143,8 @@ __global__ __launch_bounds__(256) void k_vq_assign_table(
   };
   In nxt = {};
   if (g0 < ngroups) nxt = load_in(g0);
+  const int64_t region = g0 * lst.per;  // this wave's undecided rows
+  int filled = 0;
   for (int64_t g = g0; g < ngroups; g += nwaves) {
     const int64_t row = g * 64 + lane;
     const bool live = row < n;
@@ -1193,16 +1237,15 @@ __global__ __launch_bounds__(256) void k_vq_assign_table(
     const bool rest = live && !fast;
     const uint64_t mask = __ballot(rest);
     if (mask) {
-      int base = 0;
-      if (lane == 0) base = atomicAdd(list_n, (int)__popcll(mask));
-      base = __shfl(base, 0);
-      const int below = (int)__popcll(mask & ((1ull << lane) - 1));
+      const int64_t slot = region + filled + (int)__popcll(mask & ((1ull << lane) - 1));
       if (rest) {
-        list[base + below] = (int32_t)row;
-        if constexpr (FROM_V) list_x[base + below] = make_float4(xv[0], xv[1], xv[2], xv[3]);
+        lst.rows[slot] = (int32_t)row;
+        if constexpr (FROM_V) lst.xs[slot] = make_float4(xv[0], xv[1], xv[2], xv[3]);
       }
+      filled += (int)__popcll(mask);
     }
   }
+  if (lane == 0) lst.counts[g0] = filled;  // every wave, 0 included
 }
 
 // ---------------------------------------------------------------------------
@@ -1893,10 +1936,28 @@ int shard_vq_scales(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd, int6
   return SHARD_OK;
 }
 
+// workspace of a table assignment: per wave of its launch an undecided-row
+// count, then the waves' row regions, then (with values) their values
+static size_t vq_list_bytes(int64_t n, bool with_x, VqList* lst, void* base) {
+  int grid;
+  int64_t per;
+  vq_list_geometry(n, &grid, &per);
+  const int64_t nwaves = (int64_t)grid * 4;
+  const size_t counts = (size_t)((4 * nwaves + 15) & ~(int64_t)15);
+  const size_t rows = (size_t)((4 * nwaves * per + 15) & ~(int64_t)15);
+  if (lst) {
+    char* b = (char*)base;
+    lst->counts = (int32_t*)b;
+    lst->rows = (int32_t*)(b + counts);
+    lst->xs = with_x ? (float4*)(b + counts + rows) : nullptr;
+    lst->per = per;
+  }
+  return counts + rows + (with_x ? (size_t)nwaves * per * 16 : 0);
+}
+
 size_t shard_vq_encode_table_workspace(int64_t n_rows) {
   if (n_rows <= 0 || n_rows >= ((int64_t)1 << 31)) return 0;
-  // the undecided-row count, their rows, then their values (16-byte aligned)
-  return 16 + (size_t)((4 * n_rows + 15) & ~(int64_t)15) + (size_t)n_rows * 16;
+  return vq_list_bytes(n_rows, true, nullptr, nullptr);
 }
 
 int shard_vq_encode_table(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd,
@@ -1918,26 +1979,16 @@ int shard_vq_encode_table(const uint16_t* v, int64_t bh, int64_t seq, int32_t hd
       workspace_bytes < shard_vq_encode_table_workspace(n))
     return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
-  int32_t* list_n = (int32_t*)workspace;
-  int32_t* list = list_n + 4;
-  float4* list_x = (float4*)((char*)workspace + 16 + ((4 * n + 15) & ~(int64_t)15));
-  hipLaunchKernelGGL(k_vq_list_reset, dim3(1), dim3(64), 0, s, list_n);
-  const dim3 grid(grid_cap(((n + 63) / 64 + 3) / 4, 4096)), block(256);
-  hipLaunchKernelGGL(k_vq_assign_table<true>, grid, block, 0, s, (const float*)nullptr, n,
-                     centroids, (int)k, (const uint8_t*)table, (int)nbins, lo, hi, idx, list_n,
-                     list, list_x, VqFromV{v, seq, v_bh_stride, ch_f32, ch_rcp});
-  const dim3 lgrid(128);
-  switch (k / 32) {
-#define SHARD_VQ_LISTX(NB)                                                                   \
-  case NB:                                                                                   \
-    hipLaunchKernelGGL((k_vq_assign_mfma<NB, 2>), lgrid, block, 0, s, (const float*)nullptr, \
-                       n, centroids, idx, (const int32_t*)list, (const int32_t*)list_n,      \
-                       (const float4*)list_x);                                              \
-    break;
-    SHARD_VQ_LISTX(1) SHARD_VQ_LISTX(2) SHARD_VQ_LISTX(3) SHARD_VQ_LISTX(4)
-    SHARD_VQ_LISTX(5) SHARD_VQ_LISTX(6) SHARD_VQ_LISTX(7) SHARD_VQ_LISTX(8)
-#undef SHARD_VQ_LISTX
-  }
+  VqList lst;
+  vq_list_bytes(n, true, &lst, workspace);
+  int grid;
+  int64_t per;
+  vq_list_geometry(n, &grid, &per);
+  hipLaunchKernelGGL(k_vq_assign_table<true>, dim3(grid), dim3(256), 0, s, (const float*)nullptr,
+                     n, centroids, (int)k, (const uint8_t*)table, (int)nbins, lo, hi, idx, lst,
+                     VqFromV{v, seq, v_bh_stride, ch_f32, ch_rcp});
+  hipLaunchKernelGGL(k_vq_list_direct<true>, dim3(64), dim3(256), 0, s, (const float*)nullptr,
+                     centroids, (int)k, idx, lst, 4 * grid);
   SHARD_LAUNCH_CHECK("shard_vq_encode_table");
   return SHARD_OK;
 }
@@ -2000,7 +2051,7 @@ int shard_vq_table_build(const float* centroids, int32_t k, float lo, float hi, 
 
 size_t shard_vq_assign_table_workspace(int64_t n) {
   if (n <= 0 || n >= ((int64_t)1 << 31)) return 0;
-  return (size_t)(n + 4) * sizeof(int32_t);  // the undecided-row count, then their rows
+  return vq_list_bytes(n, false, nullptr, nullptr);
 }
 
 int shard_vq_assign_table(const float* x, int64_t n, const float* centroids, int32_t k,
@@ -2013,30 +2064,20 @@ int shard_vq_assign_table(const float* x, int64_t n, const float* centroids, int
   if (((uintptr_t)x & 15) || ((uintptr_t)centroids & 15) || ((uintptr_t)table & 15))
     return SHARD_ERR_SHAPE;
   if (table_bytes < shard_vq_table_bytes(k, nbins)) return SHARD_ERR_WORKSPACE;
-  if (!workspace || ((uintptr_t)workspace & 3) ||
+  if (!workspace || ((uintptr_t)workspace & 15) ||
       workspace_bytes < shard_vq_assign_table_workspace(n))
     return SHARD_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
-  int32_t* list_n = (int32_t*)workspace;
-  int32_t* list = list_n + 4;
-  hipLaunchKernelGGL(k_vq_list_reset, dim3(1), dim3(64), 0, s, list_n);
-  const dim3 grid(grid_cap(((n + 63) / 64 + 3) / 4, 4096)), block(256);
-  hipLaunchKernelGGL(k_vq_assign_table<false>, grid, block, 0, s, x, n, centroids, (int)k,
-                     (const uint8_t*)table, (int)nbins, lo, hi, idx, list_n, list,
-                     (float4*)nullptr, VqFromV{});
-  // the rows the table left undecided: 128 workgroups, each wave looping
-  // over the list length it reads (all return at once when it is 0)
-  const dim3 lgrid(128);
-  switch (k / 32) {
-#define SHARD_VQ_LIST(NB)                                                                    \
-  case NB:                                                                                   \
-    hipLaunchKernelGGL((k_vq_assign_mfma<NB, 1>), lgrid, block, 0, s, x, n, centroids, idx,    \
-                       (const int32_t*)list, (const int32_t*)list_n, (const float4*)nullptr);  \
-    break;
-    SHARD_VQ_LIST(1) SHARD_VQ_LIST(2) SHARD_VQ_LIST(3) SHARD_VQ_LIST(4)
-    SHARD_VQ_LIST(5) SHARD_VQ_LIST(6) SHARD_VQ_LIST(7) SHARD_VQ_LIST(8)
-#undef SHARD_VQ_LIST
-  }
+  VqList lst;
+  vq_list_bytes(n, false, &lst, workspace);
+  int grid;
+  int64_t per;
+  vq_list_geometry(n, &grid, &per);
+  hipLaunchKernelGGL(k_vq_assign_table<false>, dim3(grid), dim3(256), 0, s, x, n, centroids,
+                     (int)k, (const uint8_t*)table, (int)nbins, lo, hi, idx, lst, VqFromV{});
+  // the rows the table left undecided (usually none)
+  hipLaunchKernelGGL(k_vq_list_direct<false>, dim3(64), dim3(256), 0, s, x, centroids, (int)k,
+                     idx, lst, 4 * grid);
   SHARD_LAUNCH_CHECK("shard_vq_assign_table");
   return SHARD_OK;
 }

@@ -290,6 +290,16 @@ class VqTable:
         return centroids.dim() == 2 and centroids.shape[1] == 4 and k % 32 == 0 and 0 < k <= 256
 
 
+def vq_undecided_rows(ws: torch.Tensor, n: int) -> int:
+    """Rows that the last table assignment of n rows into workspace ws left to
+    the all-centroid scan: the per-wave counts at the workspace's start (one
+    per wave of a launch of min(ceil(ceil(n / 64) / 4), 4096) workgroups of 4
+    waves)."""
+    groups = (n + 63) // 64
+    nwaves = 4 * min((groups + 3) // 4, 4096)
+    return int(ws[:4 * nwaves].view(torch.int32).sum().item())
+
+
 def vq_assign_table(x: torch.Tensor, table: "VqTable", ws=None) -> torch.Tensor:
     """vq_assign(x, table.centroids) through the table (same result)."""
     _require_gpu(x)

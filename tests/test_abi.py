@@ -69,7 +69,10 @@ def test_vq_table_sizes_and_argument_checks():
     assert lib.shard_vq_table_build(p, 256, 1.0, -1.0, 20, p, big, None) == -1
     assert lib.shard_vq_table_build(p, 256, 1000.0, 1001.0, 20, p, big, None) == -1
     assert lib.shard_vq_table_build(p, 256, -1.0, 1.0, 20, p, 100, None) == -4
-    assert lib.shard_vq_assign_table_workspace(1000) == 4 * 1004
+    # 1000 rows: 16 groups of 64, 4 workgroups of 4 waves; per wave a count and
+    # a region of 64 rows (with values: 16 more bytes per row)
+    assert lib.shard_vq_assign_table_workspace(1000) == 16 * 4 + 16 * 64 * 4
+    assert lib.shard_vq_encode_table_workspace(1000) == 16 * 4 + 16 * 64 * 4 + 16 * 64 * 16
     assert lib.shard_vq_assign_table_workspace(1 << 31) == 0
     assert lib.shard_vq_assign_table(p, 1000, p, 256, p, big, 20, -1.0, 1.0, p, p, 16, None) == -4
     assert lib.shard_vq_assign_table(p, 1000, p, 64, p, 100, 20, -1.0, 1.0, p, p, big, None) == -4

@@ -430,7 +430,7 @@ def test_vq_assign_table_undecidable_tables_bitexact(cuda, case):
     with np.errstate(all="ignore"):
         want = ref.vq_assign_direct(x.numpy(), c.numpy())
     assert np.array_equal(got, want)
-    assert int(ws[:4].view(torch.int32).item()) == x.shape[0]  # every row took the other path
+    assert ops.vq_undecided_rows(ws, x.shape[0]) == x.shape[0]  # every row took the other path
 
 
 def test_vq_assign_table_decides_normalized_rows_itself(cuda):
@@ -446,7 +446,7 @@ def test_vq_assign_table_decides_normalized_rows_itself(cuda):
     ws = torch.zeros(lib.shard_vq_assign_table_workspace(x.shape[0]), dtype=torch.uint8, device=cuda)
     got = ops.vq_assign_table(x.to(cuda), table, ws=ws).cpu().numpy()
     assert np.array_equal(got, ref.vq_assign_direct(x.numpy(), c.numpy()))
-    undecided = int(ws[:4].view(torch.int32).item())
+    undecided = ops.vq_undecided_rows(ws, x.shape[0])
     assert undecided < 0.001 * x.shape[0], undecided
 
 
