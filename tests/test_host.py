@@ -1,5 +1,7 @@
 """Host logic of shard_amd on the CPU: tables, HF Cache glue, the Llama patch
 and its fallbacks (forced from the host, no kernel launched)."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -282,3 +284,16 @@ def test_decode_graph_refuses_a_masked_cache_and_reorder_under_a_graph():
     cache._graph = object()
     with pytest.raises(RuntimeError, match="decode graph"):
         cache.reorder_cache(torch.tensor([0]))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits with a message (one GPU is built and
+    measured); nothing is launched."""
+    import json
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode != 0
+    assert "one GPU" in json.loads(out.stdout.strip().splitlines()[-1])["error"]
