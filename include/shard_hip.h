@@ -165,15 +165,18 @@ int shard_vq_assign(const float* x, int64_t n, int32_t d, const float* centroids
  * centroids that can be the answer for some row in it (a rigorous bound on
  * the fp32 distance drops the others); a row in the box is decided by the
  * direct distances to its cell's list.  Rows outside the box, non-finite rows
- * and rows of cells with more than 32 candidates are finished by the
- * all-centroid path, so every result equals shard_vq_assign's.  The box must
- * satisfy hi > lo and max(|lo|, |hi|) <= 64 (hi - lo); normalized subvectors
- * (shard_vq_prepare's x, in [-1, 1]) take lo = -1, hi = 1.
+ * and rows of cells with more than 32 candidates are finished by a direct
+ * scan of every centroid, so every result equals shard_vq_assign's (the scan
+ * suits the few rows normalized data leaves to it; rows not normalized to
+ * the box belong with shard_vq_assign).  The box must satisfy hi > lo and
+ * max(|lo|, |hi|) <= 64 (hi - lo); normalized subvectors (shard_vq_prepare's
+ * x, in [-1, 1]) take lo = -1, hi = 1.
  * table: shard_vq_table_bytes(k, nbins) bytes, 16-byte aligned.
  * shard_vq_assign_table takes the build's k, nbins, lo and hi (a table built
- * with other values decides nothing: every row takes the all-centroid path)
- * and a workspace of shard_vq_assign_table_workspace(n) bytes (the undecided
- * rows); n < 2^31. */
+ * with other values decides nothing: every row takes the direct scan) and a
+ * 16-byte aligned workspace of shard_vq_assign_table_workspace(n) bytes (per
+ * wave of the launch, a count and a region of the rows it left undecided);
+ * n < 2^31. */
 size_t shard_vq_table_bytes(int32_t k, int32_t nbins);
 /* shard_vq_prepare's first half (cache.py:43-44: the FWHT's per-(bh,
  * channel) max |.|, clamped): ch_f32 (bh, hd), optional ch_f16 and ch_rcp
