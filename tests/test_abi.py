@@ -76,6 +76,13 @@ def test_vq_table_sizes_and_argument_checks():
     assert lib.shard_vq_assign_table_workspace(1 << 31) == 0
     assert lib.shard_vq_assign_table(p, 1000, p, 256, p, big, 20, -1.0, 1.0, p, p, 16, None) == -4
     assert lib.shard_vq_assign_table(p, 1000, p, 64, p, 100, 20, -1.0, 1.0, p, p, big, None) == -4
+    # the V encoder: scales need V and an output; the fused encoder is head_dim 128 only
+    assert lib.shard_vq_scales(None, 4, 100, 128, 12800, p, None, None, p, big, None) == -1
+    assert lib.shard_vq_scales(p, 4, 100, 96, 9600, p, None, None, p, big, None) == -2
+    assert lib.shard_vq_encode_table(p, 4, 100, 64, 6400, p, p, p, 256, p, big, 16, -1.0, 1.0,
+                                     p, p, big, None) == -2
+    assert lib.shard_vq_encode_table(p, 4, 100, 128, 12800, p, p, p, 256, p, big, 16, -1.0, 1.0,
+                                     p, p, 16, None) == -4
 
 
 def test_noalloc_refuses_calls_beyond_its_scratch_before_any_launch():
