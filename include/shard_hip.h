@@ -394,6 +394,13 @@ typedef struct shard_decode_args {
    * every decode step while the stream grows.  No counterpart in the
    * reference (its counts are host integers).  Not together with `mask`. */
   const int32_t* n_stream_dev;
+  /* V codebook shape (v_codebook is v_codebook_n x v_group fp16, v_idx holds
+   * head_dim / v_group indices per token): 0 means the default 4 and 256.
+   * shard_decode_attn takes group 4 with a 256-row codebook (pad a smaller
+   * one with rows no index names); shard_kv_reconstruct takes groups 1, 2, 4
+   * and 8 and 1..256 rows (cache.py:41-61: any Cache(v_vq_group_size,
+   * v_vq_codebook_size) this build accepts). */
+  int32_t v_group, v_codebook_n;
 } shard_decode_args;
 
 /* Per-layer constant operands of shard_decode_attn, computed once after a
@@ -415,8 +422,9 @@ int shard_decode_prepare(const uint16_t* k_basis, const uint16_t* k_coeff_scale,
 
 /* 1 when shard_decode_attn takes the shapes in `args` (head_dim 128 with up
  * to 64 query heads per kv head, or head_dim 64 with an even number of kv
- * heads and up to 32 query heads per kv head; rank a multiple of 32 up to 256),
- * else 0: the caller then rebuilds fp16 K/V (shard_kv_reconstruct) and runs
+ * heads and up to 32 query heads per kv head; rank a multiple of 32 up to 256;
+ * V subvectors of 4 values from a 256-row codebook), else 0: the caller then
+ * rebuilds fp16 K/V (shard_kv_reconstruct) and runs
  * plain attention, as the reference's unfused path does (attention.py:411). */
 int shard_decode_supported(const shard_decode_args* args);
 
@@ -446,7 +454,9 @@ int shard_decode_attn_noalloc(const shard_decode_args* args, void* stream);
  * `args` (q, out and the fp16 segments are ignored):
  *   K: fp16(fp16(sum_r fp16(nib*cs) * basis) + mean), then RoPE re-applied at
  *      positions compress_start + t with fp32 phases fl(pos*theta), fp16 out;
- *   V: fp16(hadamard(cb[idx] * ch)) (hadamard in fp32, bit-exact).
+ *   V: fp16(hadamard(cb[idx] * ch)) (hadamard in fp32, bit-exact), for
+ *      subvectors of args->v_group values (1, 2, 4 or 8) from a codebook of
+ *      args->v_codebook_n rows (<= 256; 0 means 4 and 256).
  * k_out / v_out: (B, G, n_comp, D) fp16 contiguous.  D = 64, 128 or 256; any
  * even rank whose (32 + D) x rank fp16 staging fits 160 KB of LDS (rank <= 512
  * at D = 128), so layers the fused call does not take (rank above 256) decode

@@ -64,8 +64,8 @@ def keys_norope(gc, nkv, hd):
 def values_comp(gc, nkv, hd):
     """(B, nkv, n_comp, hd) fp64 compressed values FWHT(cb[idx]*ch)."""
     B, n_comp = gc["batch"], gc["n_compress"]
-    idx = _np(gc["v_idx_full"]).astype(np.int64).reshape(B, nkv, n_comp, hd // 4)
-    cb = _np(gc["v_centroids_f16"]).astype(F64)
+    cb = _np(gc["v_centroids_f16"]).astype(F64)   # (codebook rows, subvector size)
+    idx = _np(gc["v_idx_full"]).astype(np.int64).reshape(B, nkv, n_comp, hd // cb.shape[1])
     ch = _np(gc["v_ch_f16"]).astype(F64).reshape(B, nkv, hd)
     v_rot = cb[idx].reshape(B, nkv, n_comp, hd) * ch[:, :, None, :]
     return fwht64(v_rot)

@@ -45,6 +45,7 @@ class DecodeArgs(ctypes.Structure):
         ("out", c_void_p), ("n_splits", c_int32), ("kernel", c_int32),
         ("pos_q_dev", c_void_p),
         ("n_stream_dev", c_void_p),
+        ("v_group", c_int32), ("v_codebook_n", c_int32),
     ]
 
 

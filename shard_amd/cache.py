@@ -326,6 +326,16 @@ class Cache(HFCache):
                  k_target_cr=20.0, max_rank_k=192,
                  v_vq_group_size=4, v_vq_codebook_size=256,
                  sink_tokens=4, residual_window=64, rope_inv_freq=None):
+        # V subvectors of 1, 2, 4 or 8 values (the assignment and update kernels'
+        # widths) and at most 256 centroids (one byte per index, as the
+        # reference's v_indices_u8, cache.py:442): refused here rather than
+        # after a layer's compression
+        if v_vq_group_size not in (1, 2, 4, 8) or head_dim % v_vq_group_size:
+            raise ValueError(f"v_vq_group_size={v_vq_group_size}: this build takes 1, 2, 4 or 8 "
+                             f"dividing head_dim={head_dim}")
+        if not 1 <= v_vq_codebook_size <= 256:
+            raise ValueError(f"v_vq_codebook_size={v_vq_codebook_size}: indices are one byte "
+                             "(1..256 centroids)")
         self.head_dim = head_dim
         self._num_layers = num_layers
         self._n_kv_heads = n_kv_heads
@@ -783,7 +793,20 @@ def finalize_format(gc: dict, inv_freq, dev):
     hd, G = gc["head_dim"], gc["n_kv"]
     gc["decode_prep"] = None
     gc.pop("decode_refusal", None)
-    if (hd == 128 or (hd == 64 and G % 2 == 0)) and rank_pad <= 256:
+    # the fused value stage reads 4-value subvectors from a 256-row codebook:
+    # a smaller codebook is padded with rows no index names
+    cb = gc["v_centroids_f16"]
+    gc.pop("v_centroids_pad", None)
+    if cb.shape[1] == 4:
+        if cb.shape[0] == 256:
+            gc["v_centroids_pad"] = cb
+        else:
+            pad = torch.zeros(256, 4, dtype=torch.float16, device=cb.device)
+            pad[: cb.shape[0]] = cb
+            gc["v_centroids_pad"] = pad
+    if "v_centroids_pad" not in gc:
+        gc["decode_refusal"] = f"V subvectors of {cb.shape[1]} values (the fused kernel takes 4)"
+    elif (hd == 128 or (hd == 64 and G % 2 == 0)) and rank_pad <= 256:
         cmax = ops.decode_constant_max(gc["k_basis_pad"], gc["k_coeff_scale_pad"], gc["k_mean_f16"])
         if cmax <= ops.DECODE_CONSTANT_LIMIT:  # False for NaN
             gc["decode_prep"] = ops.decode_prepare(gc)

@@ -1558,6 +1558,9 @@ inline bool tok_supported(const shard_decode_args* a) {
   if ((a->head_dim != kHD && a->head_dim != 64) || a->n_kv_heads <= 0 || a->n_q_heads <= 0 ||
       a->n_q_heads % a->n_kv_heads)
     return false;
+  // the value stage reads 4-value subvectors from a 256-row codebook in LDS
+  if ((a->v_group != 0 && a->v_group != 4) || (a->v_codebook_n != 0 && a->v_codebook_n != 256))
+    return false;
   if (head_pairs(a) && (a->n_kv_heads & 1)) return false;
   const int g = a->n_q_heads / tok_g(a);
   return g <= 64 && a->rank > 0 && a->rank % 32 == 0 && a->rank <= kTokMaxRank;

@@ -70,25 +70,29 @@ void k_reconstruct_k(const uint8_t* __restrict__ coef, const uint16_t* __restric
   }
 }
 
-// V: one wave per (b, g, t): fp16(hadamard(cb[idx] * ch)), fp32 math; 4-dim
-// subvectors, head dim D = 64 E (element i = lane + 64 k).
+// V: one wave per (b, g, t): fp16(hadamard(cb[idx] * ch)), fp32 math;
+// subvectors of gs = 2^lg values (D / gs indices per token), a codebook of
+// cbn rows (an index past it reads its last row), head dim D = 64 E
+// (element i = lane + 64 k).
 template <int E>
 __global__ void k_reconstruct_v(const uint8_t* __restrict__ vidx, const uint16_t* __restrict__ vcb,
                                 const uint16_t* __restrict__ vch, int64_t rows, int G, int n_comp,
-                                uint16_t* __restrict__ v_out) {
+                                int lg, int cbn, uint16_t* __restrict__ v_out) {
   constexpr int D = 64 * E;
   const int l = (int)lane_id();
+  const int gs = 1 << lg;
   int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
   for (int64_t r = wave; r < rows; r += nw) {  // r = (b*G + g)*n_comp + t
     const int64_t bg = r / n_comp;
-    const uint8_t* ix = vidx + r * (D / 4);
+    const uint8_t* ix = vidx + r * (D >> lg);
     const uint16_t* ch = vch + bg * D;
     float x[E];
 #pragma unroll
     for (int k = 0; k < E; ++k) {
       const int d = l + 64 * k;
-      x[k] = __fmul_rn(h2f(vcb[4 * ix[d >> 2] + (d & 3)]), h2f(ch[d]));
+      const int e = min((int)ix[d >> lg], cbn - 1);
+      x[k] = __fmul_rn(h2f(vcb[gs * e + (d & (gs - 1))]), h2f(ch[d]));
     }
     wave_fwht<E>(x, D);
 #pragma unroll
@@ -145,6 +149,9 @@ int shard_kv_reconstruct(const shard_decode_args* a, uint16_t* k_out, uint16_t* 
   const size_t lds = (size_t)(kRcTok + hd) * (a->rank > 0 ? a->rank : 0) * sizeof(uint16_t);
   if ((hd != 64 && hd != 128 && hd != 256) || a->rank <= 0 || (a->rank & 1) || lds > 160 * 1024)
     return SHARD_ERR_SHAPE;
+  const int gs = a->v_group ? a->v_group : 4, cbn = a->v_codebook_n ? a->v_codebook_n : 256;
+  const int lg = gs == 1 ? 0 : gs == 2 ? 1 : gs == 4 ? 2 : gs == 8 ? 3 : -1;
+  if (lg < 0 || cbn < 1 || cbn > 256) return SHARD_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)((a->n_comp + kRcTok - 1) / kRcTok), (unsigned)a->n_kv_heads,
             (unsigned)a->batch);
@@ -157,7 +164,7 @@ int shard_kv_reconstruct(const shard_decode_args* a, uint16_t* k_out, uint16_t* 
   const dim3 vgrid(grid_cap((rows + 3) / 4, 16384));
   auto launch_v = [&](auto kern) {
     hipLaunchKernelGGL(kern, vgrid, dim3(256), 0, s, a->v_idx, a->v_codebook, a->v_ch, rows,
-                       a->n_kv_heads, a->n_comp, v_out);
+                       a->n_kv_heads, a->n_comp, lg, cbn, v_out);
   };
   if (lds > 64 * 1024) {  // LDS beyond the default dynamic limit (160 KB per CU on gfx950)
     const void* kern = hd == 64 ? reinterpret_cast<const void*>(&k_reconstruct_k<64>)

@@ -649,8 +649,11 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
     attends over its value's worth of stream rows, at most stream_n."""
     _require_gpu(q)
     B, H, D = q.shape
-    if tuple(fmt["v_centroids_f16"].shape) != (256, 4):
-        raise ValueError("decode kernel needs a (256, 4) VQ codebook")
+    # the fused kernel's codebook: 4-value subvectors, 256 rows (padded);
+    # other shapes only reach kv_reconstruct, which takes the codebook as is
+    cb = fmt.get("v_centroids_pad")
+    if cb is None:
+        cb = fmt["v_centroids_f16"]
     keep = []
     a = DecodeArgs()
     a.batch, a.n_q_heads, a.n_kv_heads, a.head_dim = B, H, fmt["n_kv"], D
@@ -660,7 +663,7 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
                     ("k_coeff_scale", fmt["k_coeff_scale_pad"]), ("k_basis", fmt["k_basis_pad"]),
                     ("k_mean", fmt["k_mean_f16"]), ("prep", fmt.get("decode_prep")),
                     ("v_idx", fmt["v_indices"]),
-                    ("v_codebook", fmt["v_centroids_f16"]), ("v_ch", fmt["v_ch_f16"]),
+                    ("v_codebook", cb), ("v_ch", fmt["v_ch_f16"]),
                     ("sink_k", fmt["sink_k"]), ("sink_v", fmt["sink_v"]),
                     ("win_k", fmt["win_k"]), ("win_v", fmt["win_v"])):
         if t is None:  # no decode operands: a layer shape only kv_reconstruct takes
@@ -670,6 +673,7 @@ def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
         keep.append(t)
     a.n_sink = fmt["sink_k"].shape[2]
     a.n_win = fmt["win_k"].shape[2]
+    a.v_codebook_n, a.v_group = cb.shape
     call = DecodeCall(a, keep)
     return call.refresh(q, fmt, pos_q, inv_freq, mask, n_splits, out, stream_n, decode_kv,
                         stream_n_dev)
@@ -832,6 +836,9 @@ def kv_reconstruct(fmt, batch: int):
     B, G, n, D = batch, fmt["n_kv"], fmt["n_compress"], fmt["head_dim"]
     q_dummy = torch.empty(B, G * 4, D, dtype=torch.float16, device=dev)
     call = make_decode_args(q_dummy, fmt, 0, None)
+    cb = fmt["v_centroids_f16"]  # its own shape: any group and codebook size the Cache takes
+    call.args.v_codebook = cb.data_ptr()
+    call.args.v_codebook_n, call.args.v_group = cb.shape
     call.args.k_coeffs = fmt["k_coeffs"].data_ptr()
     call.args.k_coeff_scale = fmt["k_coeff_scale"].data_ptr()
     call.args.k_basis = fmt["k_basis_f16"].data_ptr()

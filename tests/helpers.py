@@ -8,8 +8,10 @@ from oracle import ref
 
 
 def random_layer(B=1, nkv=8, hd=128, rank=192, n_comp=512, sink=4, win=64, n_stream=0,
-                 n_dec=0, seed=0, inv_freq=None, basis_amp=0.05, stream_bits=8, qjl=False):
-    """A random compressed layer in the oracle's gc format (CPU tensors)."""
+                 n_dec=0, seed=0, inv_freq=None, basis_amp=0.05, stream_bits=8, qjl=False,
+                 v_group=4, v_codebook=256):
+    """A random compressed layer in the oracle's gc format (CPU tensors); V
+    subvectors of v_group values from a codebook of v_codebook rows."""
     g = torch.Generator().manual_seed(seed)
     if inv_freq is None:
         inv_freq = ref.default_inv_freq(500000.0, hd)
@@ -21,8 +23,8 @@ def random_layer(B=1, nkv=8, hd=128, rank=192, n_comp=512, sink=4, win=64, n_str
     # spectrum-like decay of the coefficient scales
     coeff_scale = (torch.exp(-torch.arange(rank) / 80.0) * 0.4 + 0.01).half()
     mean = (torch.randn(nkv * hd, generator=g) * 0.2).half()
-    v_idx = torch.randint(0, 256, (B, nkv, n_comp, hd // 4), generator=g).to(torch.uint8)
-    cent = (torch.randn(256, 4, generator=g) * 0.5).half()
+    v_idx = torch.randint(0, v_codebook, (B, nkv, n_comp, hd // v_group), generator=g).to(torch.uint8)
+    cent = (torch.randn(v_codebook, v_group, generator=g) * 0.5).half()
     ch = (torch.rand(B, nkv, hd, generator=g) * 2 + 0.5).half()
     gc = {
         "k_coeffs": packed, "k_coeffs_shape": (B * n_comp, rank),
@@ -31,7 +33,7 @@ def random_layer(B=1, nkv=8, hd=128, rank=192, n_comp=512, sink=4, win=64, n_str
         "k_mean": mean, "k_mean_f16": mean,
         "v_idx_full": v_idx, "v_centroids_f16": cent, "v_ch_f16": ch,
         "v_qdata": {"centroids": cent, "idx": v_idx.reshape(-1), "ch_maxabs": ch.view(B * nkv, hd),
-                    "shape": (B * nkv, n_comp, hd), "group_size": 4},
+                    "shape": (B * nkv, n_comp, hd), "group_size": v_group},
         "sink_k": torch.randn(B, nkv, sink, hd, generator=g).half(),
         "sink_v": torch.randn(B, nkv, sink, hd, generator=g).half(),
         "win_k": torch.randn(B, nkv, win, hd, generator=g).half(),
@@ -69,7 +71,7 @@ def to_device(gc, device, inv_freq, nkv=8, hd=128):
         "k_coeffs_shape": (n_total, rank),
         "k_basis_f16": t(gc["k_basis_f16"]).contiguous(),
         "k_mean_f16": t(gc["k_mean_f16"]).contiguous(),
-        "v_indices": t(gc["v_idx_full"]).reshape(B, nkv, n_comp, hd // 4).contiguous(),
+        "v_indices": t(gc["v_idx_full"]).reshape(B, nkv, n_comp, hd // gc["v_qdata"]["group_size"]).contiguous(),
         "v_centroids_f16": t(gc["v_centroids_f16"]).contiguous(),
         "v_ch_f16": t(gc["v_ch_f16"]).reshape(B, nkv, hd).contiguous(),
         "sink_k": t(gc["sink_k"]).contiguous(), "sink_v": t(gc["sink_v"]).contiguous(),

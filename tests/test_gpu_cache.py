@@ -10,7 +10,9 @@
 * a head_dim-64 model with an even kv head count (kv heads paired) and
   Llama-3.2-3B's 3 query heads per kv head: every decode step is fused and
   checked against the oracle; head_dim 64 with one kv head: decode runs the
-  original forward on rebuilt K/V, every such layer-step counted.
+  original forward on rebuilt K/V, every such layer-step counted;
+* other V codebook shapes: 64 centroids (fused, oracle-checked) and
+  subvectors of 8 values (unfused, equal to the unpatched forward).
 """
 import pytest
 import torch
@@ -168,6 +170,86 @@ def test_other_shapes_decode_fused(cuda, monkeypatch, n_q, n_kv, hd):
         print(f"[{n_q}q/{n_kv}kv hd{hd} cache] step {i} pos_q={pos_q} max_abs={err:.3e} "
               f"cos={cos:.7f}", flush=True)
         assert err <= 2e-3 and cos >= 0.9999
+
+
+def test_small_codebook_decodes_fused(cuda, monkeypatch):
+    """Cache(v_vq_codebook_size=64): k-means trains 64 centroids, the fused
+    kernel takes the layer (its codebook padded to 256 rows no index names),
+    no step falls back, and every fused call matches the fp64 oracle over the
+    layer's own 64-row codebook."""
+    from shard_amd import Cache, attention, enable_llama_fused_attention
+    model = _llama(cuda)
+    assert enable_llama_fused_attention(model)
+    seen = []
+    inner = attention.fused_attention_compressed
+
+    def record(q, layer, pos_q, inv, mask=None):
+        out = inner(q, layer, pos_q, inv, mask)
+        if layer.layer_idx == 1:
+            p = int(pos_q.reshape(-1)[-1].item()) if torch.is_tensor(pos_q) else int(pos_q)
+            seen.append((q.detach().cpu(), p, out.detach().cpu(),
+                         _oracle_format(layer._gpu_compressed), inv.cpu()))
+        return out
+    monkeypatch.setattr(attention, "fused_attention_compressed", record)
+    g = torch.Generator().manual_seed(8)
+    B, T = 1, 400
+    ids = torch.randint(0, VOCAB, (B, T), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (B, 2), generator=g).to(cuda)
+    cache = Cache.from_model(model, v_vq_codebook_size=64)
+    cache._streaming = True
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        for s in range(steps.shape[1]):
+            model(steps[:, s:s + 1], past_key_values=cache, use_cache=True)
+    gc = cache.layers[1]._gpu_compressed
+    assert tuple(gc["v_centroids_f16"].shape) == (64, 4) and gc["decode_prep"] is not None
+    assert int(gc["v_indices"].max()) < 64
+    assert getattr(cache, "_fused_fallbacks", 0) == 0 and len(seen) == 2
+    n_q, n_kv, hd = 32, 8, 128
+    for i, (q, pos_q, out, ogc, inv) in enumerate(seen):
+        want = exact.decode_attention(q.float().numpy().reshape(B, n_q, 1, hd), ogc, n_kv, pos_q,
+                                      inv.numpy())
+        err, cos = compare(out.float().numpy().reshape(want.shape), want)
+        print(f"[64-row codebook] step {i} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= 2e-3 and cos >= 0.9999
+
+
+def test_vq_group_8_falls_back(cuda):
+    """Cache(v_vq_group_size=8): V subvectors of 8 values (k-means over 8-dim
+    rows), which the fused value stage does not take: every decode step of a
+    compressed layer runs the original forward over kv_reconstruct's K/V
+    (counted, with the reason), with the unpatched forward's logits."""
+    from transformers.models.llama.modeling_llama import LlamaAttention
+    from shard_amd import Cache, enable_llama_fused_attention
+    model = _llama(cuda)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, VOCAB, (1, 400), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (1, 2), generator=g).to(cuda)
+
+    def run():
+        c = Cache.from_model(model, v_vq_group_size=8)
+        c._streaming = True
+        out = []
+        with torch.no_grad():
+            model(ids, past_key_values=c, use_cache=True)
+            for s in range(steps.shape[1]):
+                out.append(model(steps[:, s:s + 1], past_key_values=c, use_cache=True).logits.float())
+        return torch.cat(out, 1), c
+
+    got, cache = run()
+    gc = cache.layers[0]._gpu_compressed
+    assert gc is not None and tuple(gc["v_centroids_f16"].shape) == (256, 8)
+    assert gc["decode_prep"] is None and "subvectors of 8" in gc["decode_refusal"]
+    assert cache._fused_fallbacks == 2 * steps.shape[1] - 1
+    patched = LlamaAttention.forward
+    try:
+        LlamaAttention.forward = patched.__wrapped__
+        want, _ = run()
+    finally:
+        LlamaAttention.forward = patched
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want)
 
 
 def test_head_dim_64_odd_kv_heads_fall_back(cuda):

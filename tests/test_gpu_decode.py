@@ -419,6 +419,38 @@ def test_kv_reconstruct(cuda, rank, nkv, hd):
     assert float((diff > 0).float().mean()) < 0.02
 
 
+@pytest.mark.parametrize("group,n_cent", [(2, 256), (8, 256), (1, 16), (4, 64)])
+def test_kv_reconstruct_vq_shapes(cuda, group, n_cent):
+    """V subvectors of 1, 2 or 8 values and codebooks below 256 rows (a Cache
+    built with another v_vq_group_size or v_vq_codebook_size): the unfused
+    reconstruction's V bit-exact with the oracle's vq_decode + hadamard; the
+    fused call takes only 4-value subvectors (a smaller codebook padded to 256
+    rows)."""
+    from shard_amd import ops
+    gc, inv = random_layer(B=2, nkv=4, hd=128, rank=64, n_comp=200, seed=21,
+                           v_group=group, v_codebook=n_cent)
+    d = to_device(gc, cuda, inv, nkv=4, hd=128)
+    assert (d["decode_prep"] is None) == (group != 4)
+    _, v_got = ops.kv_reconstruct(d, 2)
+    _, v_want = ref.reconstruct_kv(gc, 4, 128, inv)
+    assert np.array_equal(v_got.cpu().numpy().view(np.uint16), v_want.numpy().view(np.uint16))
+
+
+def test_decode_small_codebook_fused(cuda):
+    """A 64-row codebook of 4-value subvectors decodes on the fused kernels
+    (padded to 256 rows that no index names) within the fp64 oracle's
+    tolerance, on both split kernels."""
+    gc, inv = random_layer(B=1, n_comp=900, seed=22, v_codebook=64)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(23)).half()
+    pos_q = 4 + 900 + 64
+    want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    for kernel in KERNELS:
+        got = _run(cuda, gc, inv, q, pos_q, kernel=kernel)
+        err, cos = compare(got, want)
+        print(f"kernel {kernel}: max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
 def test_decode_device_position_matches_host_position(cuda, kernel):
     """pos_q read by the kernel from a device int64 (the patched forward passes

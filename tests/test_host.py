@@ -297,3 +297,17 @@ def test_bench_refuses_more_than_one_gpu():
                          capture_output=True, text=True, timeout=300)
     assert out.returncode != 0
     assert "one GPU" in json.loads(out.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_cache_refuses_vq_shapes_it_cannot_decode():
+    """V subvectors of 1, 2, 4 or 8 values and 1..256 centroids are taken;
+    other values are refused when the Cache is built, not after a layer's
+    compression."""
+    from shard_amd import Cache
+    for gs in (1, 2, 4, 8):
+        Cache(num_layers=1, v_vq_group_size=gs, device="cpu")
+    Cache(num_layers=1, v_vq_codebook_size=1, device="cpu")
+    for kw in ({"v_vq_group_size": 3}, {"v_vq_group_size": 16}, {"v_vq_codebook_size": 300},
+               {"v_vq_codebook_size": 0}, {"head_dim": 100, "v_vq_group_size": 8}):
+        with pytest.raises(ValueError):
+            Cache(num_layers=1, device="cpu", **kw)
