@@ -11,8 +11,9 @@
   Llama-3.2-3B's 3 query heads per kv head: every decode step is fused and
   checked against the oracle; head_dim 64 with one kv head: decode runs the
   original forward on rebuilt K/V, every such layer-step counted;
-* other V codebook shapes: 64 centroids (fused, oracle-checked) and
-  subvectors of 8 values (unfused, equal to the unpatched forward).
+* other Cache options: 64 centroids, no sink tokens, longer sinks and
+  windows (fused, oracle-checked); subvectors of 8 values (unfused, equal to
+  the unpatched forward).
 """
 import pytest
 import torch
@@ -172,11 +173,16 @@ def test_other_shapes_decode_fused(cuda, monkeypatch, n_q, n_kv, hd):
         assert err <= 2e-3 and cos >= 0.9999
 
 
-def test_small_codebook_decodes_fused(cuda, monkeypatch):
-    """Cache(v_vq_codebook_size=64): k-means trains 64 centroids, the fused
-    kernel takes the layer (its codebook padded to 256 rows no index names),
-    no step falls back, and every fused call matches the fp64 oracle over the
-    layer's own 64-row codebook."""
+@pytest.mark.parametrize("opts", [{"v_vq_codebook_size": 64},
+                                  {"sink_tokens": 0, "residual_window": 16},
+                                  {"sink_tokens": 8, "residual_window": 128}],
+                         ids=["codebook64", "no-sink-window16", "sink8-window128"])
+def test_cache_options_decode_fused(cuda, monkeypatch, opts):
+    """Cache options other than the defaults: a 64-centroid codebook (k-means
+    trains 64, the fused kernel takes the layer with its codebook padded to
+    256 rows no index names), no sink tokens with a 16-token window, 8 sink
+    tokens with a 128-token window: no step falls back, and every fused call
+    matches the fp64 oracle over the layer's own representation."""
     from shard_amd import Cache, attention, enable_llama_fused_attention
     model = _llama(cuda)
     assert enable_llama_fused_attention(model)
@@ -195,22 +201,25 @@ def test_small_codebook_decodes_fused(cuda, monkeypatch):
     B, T = 1, 400
     ids = torch.randint(0, VOCAB, (B, T), generator=g).to(cuda)
     steps = torch.randint(0, VOCAB, (B, 2), generator=g).to(cuda)
-    cache = Cache.from_model(model, v_vq_codebook_size=64)
+    cache = Cache.from_model(model, **opts)
     cache._streaming = True
     with torch.no_grad():
         model(ids, past_key_values=cache, use_cache=True)
         for s in range(steps.shape[1]):
             model(steps[:, s:s + 1], past_key_values=cache, use_cache=True)
     gc = cache.layers[1]._gpu_compressed
-    assert tuple(gc["v_centroids_f16"].shape) == (64, 4) and gc["decode_prep"] is not None
-    assert int(gc["v_indices"].max()) < 64
+    n_cent = opts.get("v_vq_codebook_size", 256)
+    assert tuple(gc["v_centroids_f16"].shape) == (n_cent, 4) and gc["decode_prep"] is not None
+    assert int(gc["v_indices"].max()) < n_cent
+    assert gc["sink_k"].shape[2] == opts.get("sink_tokens", 4)
+    assert gc["win_k"].shape[2] == opts.get("residual_window", 64)
     assert getattr(cache, "_fused_fallbacks", 0) == 0 and len(seen) == 2
     n_q, n_kv, hd = 32, 8, 128
     for i, (q, pos_q, out, ogc, inv) in enumerate(seen):
         want = exact.decode_attention(q.float().numpy().reshape(B, n_q, 1, hd), ogc, n_kv, pos_q,
                                       inv.numpy())
         err, cos = compare(out.float().numpy().reshape(want.shape), want)
-        print(f"[64-row codebook] step {i} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        print(f"[{opts}] step {i} max_abs={err:.3e} cos={cos:.7f}", flush=True)
         assert err <= 2e-3 and cos >= 0.9999
 
 

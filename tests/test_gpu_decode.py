@@ -46,6 +46,7 @@ CASES = [
     (16, 8, 128, 300, 4, 16, 1, 0),      # batch 16
     (1, 8, 192, 700, 4, 64, 3000, 0),    # 3,068 extra tokens: spread over many splits
     (2, 4, 160, 900, 4, 64, 700, 9),     # long stream and decode tokens together
+    (1, 8, 192, 600, 0, 0, 0, 0),        # no sink, window or stream: compressed tokens alone
 ]
 
 # split kernels: 0 = automatic, 1 = row-split, 2 = token-tiled
