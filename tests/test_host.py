@@ -311,3 +311,18 @@ def test_cache_refuses_vq_shapes_it_cannot_decode():
                {"v_vq_codebook_size": 0}, {"head_dim": 100, "v_vq_group_size": 8}):
         with pytest.raises(ValueError):
             Cache(num_layers=1, device="cpu", **kw)
+
+
+def test_reference_import_paths_resolve():
+    """The import paths the reference's scripts use (example.py:9,
+    benchmarks/benchmark.py:43-45) resolve to this build's objects."""
+    import shard
+    import shard_amd
+    from shard.attention import enable_llama_fused_attention, fused_attention_compressed
+    from shard.cache import Cache
+    from shard.rope import get_rope_inv_freq
+    assert shard.Cache is Cache is shard_amd.Cache
+    assert enable_llama_fused_attention is shard_amd.enable_llama_fused_attention
+    assert fused_attention_compressed is shard_amd.fused_attention_compressed
+    from shard_amd.host import get_rope_inv_freq as mine
+    assert get_rope_inv_freq is mine
