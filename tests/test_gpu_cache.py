@@ -1,5 +1,8 @@
 """The shard Cache driven by a real (random-init) Llama on the GPU:
 
+* transformers' generate() with the Cache, as the reference's example.py
+  drives it, against a hand-written greedy loop;
+
 * batch 16 (the end-to-end decode batch, shorter prompt): the fused
   decode call the patched forward makes, checked against the fp64 oracle over
   the layer's own compressed representation (attention.py:300-343,
@@ -88,6 +91,46 @@ def test_batch16_cache_decode_matches_oracle(cuda, monkeypatch):
         err, cos = compare(out.float().numpy().reshape(want.shape), want)
         print(f"[batch16 cache] step {i} pos_q={pos_q} max_abs={err:.3e} cos={cos:.7f}", flush=True)
         assert err <= 2e-3 and cos >= 0.9999
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_generate_with_the_cache(cuda, B):
+    """transformers' generate() with the Cache as past_key_values, as the
+    reference's example.py and benchmark drive it (greedy, an all-ones
+    attention mask): compression at the first decode step, fused decode after
+    it, the same tokens as a hand-written greedy loop over a fresh Cache, and
+    the accounting methods afterwards."""
+    from shard_amd import Cache, enable_llama_fused_attention
+    model = _llama(cuda)
+    assert enable_llama_fused_attention(model)
+    g = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, VOCAB, (B, 300), generator=g).to(cuda)
+    n_new = 6
+    cache = Cache.from_model(model)
+    cache._streaming = True
+    with torch.no_grad():
+        out = model.generate(input_ids=ids, attention_mask=torch.ones_like(ids), max_new_tokens=n_new,
+                             do_sample=False, past_key_values=cache, pad_token_id=0)
+    assert out.shape == (B, 300 + n_new)
+    assert cache.layers[0]._gpu_compressed is not None
+    assert getattr(cache, "_fused_fallbacks", 0) == 0
+    # the same greedy steps by hand
+    ref_cache = Cache.from_model(model)
+    ref_cache._streaming = True
+    toks = []
+    with torch.no_grad():
+        logits = model(ids, past_key_values=ref_cache, use_cache=True).logits[:, -1]
+        for _ in range(n_new):
+            nxt = logits.argmax(-1, keepdim=True)
+            toks.append(nxt)
+            logits = model(nxt, past_key_values=ref_cache, use_cache=True).logits[:, -1]
+    assert torch.equal(out[:, 300:], torch.cat(toks, 1))
+    # the reference's ratios count one batch row of fp16 (cache.py:511-539);
+    # over all rows the compressed cache is the smaller one at any batch
+    assert cache.memory_bytes() > 0 and cache.clean_compress_ratio_all_rows() > 1
+    if B == 1:
+        assert cache.compress_ratio() > 1
+        assert cache.fp16_equivalent_bytes() > cache.memory_bytes()
 
 
 def test_reorder_cache_selects_compressed_rows(cuda):
