@@ -55,9 +55,12 @@ def fused_attention_compressed(q_rope, layer, pos_q, inv_freq, attn_mask=None):
     dec = (gc["decode_k"], gc["decode_v"]) if "decode_k" in gc else None
     mask = None
     if attn_mask is not None:
-        mask = attn_mask.reshape(B, -1)[:, -(gc["sink_k"].shape[2] + gc["n_compress"] +
-                                          gc["win_k"].shape[2] + stream_n +
-                                          (dec[0].shape[2] if dec else 0)):]
+        # the reference adds the mask to the scores (attention.py:314); a
+        # boolean mask (transformers' sdpa masks: True = attend) is taken as
+        # the additive mask it stands for, not as 1.0 / 0.0 added to scores
+        mask = ops.additive_mask(attn_mask).reshape(B, -1)[
+            :, -(gc["sink_k"].shape[2] + gc["n_compress"] + gc["win_k"].shape[2] + stream_n +
+                 (dec[0].shape[2] if dec else 0)):]
     n_splits = getattr(c, "_n_splits", 0)
     stream_n_dev = None
     graph = getattr(c, "_graph", None)

@@ -637,6 +637,17 @@ def decode_prepare(fmt) -> torch.Tensor:
     return buf
 
 
+def additive_mask(mask: torch.Tensor) -> torch.Tensor:
+    """An attention mask as the fp32 additive form the decode kernel reads:
+    a boolean mask (True = attend, what transformers builds for its sdpa
+    attention) becomes 0 / the fp32 minimum, as transformers' own float masks
+    hold them; a float mask is taken as added to the scores."""
+    if mask.dtype == torch.bool:
+        return torch.zeros(mask.shape, dtype=torch.float32, device=mask.device).masked_fill_(
+            ~mask, torch.finfo(torch.float32).min)
+    return mask if mask.dtype == torch.float32 else mask.float()
+
+
 def make_decode_args(q, fmt, pos_q, inv_freq, mask=None, n_splits=0, out=None,
                      stream_n=0, decode_kv=None, stream_n_dev=None) -> DecodeCall:
     """Build shard_decode_args for one layer.
@@ -727,12 +738,10 @@ def _decode_refresh(self, q, fmt, pos_q, inv_freq=None, mask=None, n_splits=0, o
     else:
         a.n_stream_dev = None
     if mask is not None:
-        m = mask.reshape(B, -1)
+        m = additive_mask(mask).reshape(B, -1)
         n_total = (a.n_sink + a.n_comp + a.n_win + a.n_dec + a.n_stream)
         if m.shape[1] < n_total:
             raise ValueError(f"attention mask covers {m.shape[1]} keys, the cache holds {n_total}")
-        if m.dtype != torch.float32:
-            m = m.float()
         if m.stride(-1) != 1:
             m = m.contiguous()
         a.mask, a.mask_stride = m.data_ptr(), m.stride(0)

@@ -133,6 +133,55 @@ def test_generate_with_the_cache(cuda, B):
         assert cache.fp16_equivalent_bytes() > cache.memory_bytes()
 
 
+def test_left_padded_batch_decodes_fused(cuda, monkeypatch):
+    """generate() on a left-padded batch (rows of 300 and 260 prompt tokens):
+    the fused calls receive the padding mask, and each one matches the fp64
+    oracle with the same additive mask over the layer's own representation
+    (sink, compressed, window and stream keys in position order, as
+    attention.py:300-343 concatenates them)."""
+    from shard_amd import Cache, attention, enable_llama_fused_attention
+    model = _llama(cuda)
+    assert enable_llama_fused_attention(model)
+    seen, mask_bool = [], []
+    inner = attention.fused_attention_compressed
+
+    def record(q, layer, pos_q, inv, mask=None):
+        out = inner(q, layer, pos_q, inv, mask)
+        if layer.layer_idx == 1:
+            p = int(pos_q.reshape(-1)[-1].item()) if torch.is_tensor(pos_q) else int(pos_q)
+            seen.append((q.detach().cpu(), p, out.detach().cpu(), _oracle_format(layer._gpu_compressed),
+                         inv.cpu(), None if mask is None else mask.detach().float().cpu()))
+            mask_bool.append(mask is not None and mask.dtype == torch.bool)
+        return out
+    monkeypatch.setattr(attention, "fused_attention_compressed", record)
+    g = torch.Generator().manual_seed(13)
+    T, pad = 300, 40
+    ids = torch.randint(1, VOCAB, (2, T), generator=g)
+    ids[1, :pad] = 0
+    am = torch.ones_like(ids)
+    am[1, :pad] = 0
+    cache = Cache.from_model(model)
+    cache._streaming = True
+    with torch.no_grad():
+        model.generate(input_ids=ids.to(cuda), attention_mask=am.to(cuda), max_new_tokens=4,
+                       do_sample=False, past_key_values=cache, pad_token_id=0)
+    assert getattr(cache, "_fused_fallbacks", 0) == 0 and len(seen) == 3
+    for i, (q, pos_q, out, ogc, inv, mask) in enumerate(seen):
+        assert mask is not None
+        n_keys = (ogc["sink_k"].shape[2] + ogc["n_compress"] + ogc["win_k"].shape[2]
+                  + ogc.get("stream_n", 0) // 2)
+        # transformers' sdpa attention masks are boolean (True = attend)
+        m = torch.zeros(mask.shape).masked_fill_(mask == 0, torch.finfo(torch.float32).min) \
+            if mask_bool[i] else mask
+        m = m.reshape(2, -1)[:, -n_keys:]
+        assert bool((m[1, :pad] < -1e30).all()) and bool((m[0] == 0).all())
+        want = exact.decode_attention(q.float().numpy().reshape(2, 32, 1, 128), ogc, 8, pos_q,
+                                      inv.numpy(), attn_mask=m.numpy())
+        err, cos = compare(out.float().numpy().reshape(want.shape), want)
+        print(f"[left-padded] step {i} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= 2e-3 and cos >= 0.9999
+
+
 def test_reorder_cache_selects_compressed_rows(cuda):
     from shard_amd import Cache, attention, enable_llama_fused_attention
     model = _llama(cuda)

@@ -286,6 +286,21 @@ def test_decode_graph_refuses_a_masked_cache_and_reorder_under_a_graph():
         cache.reorder_cache(torch.tensor([0]))
 
 
+def test_boolean_attention_masks_become_additive():
+    """transformers' sdpa masks are boolean (True = attend): the decode path
+    takes them as the additive mask they stand for (0 / fp32 min), so padding
+    keys are masked rather than shifted by 1.0; float masks pass as added."""
+    from shard_amd.ops import additive_mask
+    b = torch.tensor([[[[True, False, True]]]])
+    m = additive_mask(b)
+    assert m.dtype == torch.float32 and m.shape == b.shape
+    assert m.reshape(-1).tolist() == [0.0, torch.finfo(torch.float32).min, 0.0]
+    f = torch.tensor([[0.0, -1e9, 0.0]], dtype=torch.float16)
+    assert additive_mask(f).dtype == torch.float32
+    f32 = torch.tensor([[0.0, float("-inf")]])
+    assert additive_mask(f32) is f32
+
+
 def test_bench_refuses_more_than_one_gpu():
     """bench.py --gpus N with N > 1 exits with a message (one GPU is built and
     measured); nothing is launched."""
