@@ -298,16 +298,20 @@ class CacheLayer(CacheLayerMixin):
         pass
 
     def reorder_cache(self, beam_idx):
-        """Beam reordering (cache.py:287-292): the dequantized K/V are rebuilt and
-        their batch rows selected, as the reference does.  The reference leaves
-        the compressed representation as it was, so the next decode step (which
-        reads it) sees the old row order; here its per-row tensors are selected
-        too, so every later step runs on the reordered beams."""
+        """Beam reordering (cache.py:287-292).  The reference rebuilds the
+        dequantized K/V and selects their batch rows, and leaves the compressed
+        representation as it was, so its next decode step (which reads it) sees
+        the old row order.  Here the compressed layer's per-row tensors are
+        selected, so every later step runs on the reordered beams; dequantized
+        K/V that are current are selected too, and stale ones are dropped and
+        rebuilt from the selected rows at their next access.  Each batch row is
+        rebuilt from its own rows only, so that equals the reference's
+        rebuild-then-select, without a full rebuild at every beam step."""
         if getattr(self._cache_ref, "_graph", None) is not None:
             # a captured decode step holds the addresses of the rows reordered here
             raise RuntimeError("reorder_cache while a decode graph is open: close() it first")
-        if self._needs_decompress:
-            _ = self.keys
+        if self._needs_decompress and self._gpu_compressed is not None:
+            self._keys = self._values = None
         if self._keys is not None:
             self._keys = self._keys.index_select(0, beam_idx.to(self._keys.device))
         if self._values is not None:

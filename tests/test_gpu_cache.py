@@ -182,6 +182,52 @@ def test_left_padded_batch_decodes_fused(cuda, monkeypatch):
         assert err <= 2e-3 and cos >= 0.9999
 
 
+def test_beam_search_decodes_fused(cuda, monkeypatch):
+    """generate(num_beams=2) with the Cache: transformers reorders the cache
+    between steps (Cache.reorder_cache -> CacheLayer.reorder_cache,
+    cache.py:287-292), and every fused call after a reorder matches the fp64
+    oracle over the reordered representation, with no fallback."""
+    from shard_amd import Cache, attention, enable_llama_fused_attention
+    from shard_amd import cache as cache_mod
+    model = _llama(cuda)
+    assert enable_llama_fused_attention(model)
+    seen, reorders = [], []
+    inner = attention.fused_attention_compressed
+
+    def record(q, layer, pos_q, inv, mask=None):
+        out = inner(q, layer, pos_q, inv, mask)
+        if layer.layer_idx == 1:
+            p = int(pos_q.reshape(-1)[-1].item()) if torch.is_tensor(pos_q) else int(pos_q)
+            seen.append((q.detach().cpu(), p, out.detach().cpu(), _oracle_format(layer._gpu_compressed),
+                         inv.cpu()))
+        return out
+    inner_reorder = cache_mod.CacheLayer.reorder_cache
+
+    def record_reorder(self, beam_idx):
+        if self.layer_idx == 1:
+            reorders.append(beam_idx.detach().cpu().clone())
+        return inner_reorder(self, beam_idx)
+    monkeypatch.setattr(attention, "fused_attention_compressed", record)
+    monkeypatch.setattr(cache_mod.CacheLayer, "reorder_cache", record_reorder)
+    g = torch.Generator().manual_seed(21)
+    ids = torch.randint(1, VOCAB, (1, 300), generator=g).to(cuda)
+    cache = Cache.from_model(model)
+    cache._streaming = True
+    with torch.no_grad():
+        out = model.generate(input_ids=ids, attention_mask=torch.ones_like(ids), max_new_tokens=5,
+                             num_beams=2, do_sample=False, past_key_values=cache, pad_token_id=0)
+    assert out.shape[0] == 1 and out.shape[1] > 300
+    assert getattr(cache, "_fused_fallbacks", 0) == 0
+    assert len(seen) >= 2 and len(reorders) >= 1
+    for i, (q, pos_q, o, ogc, inv) in enumerate(seen):
+        B = q.shape[0]
+        want = exact.decode_attention(q.float().numpy().reshape(B, 32, 1, 128), ogc, 8, pos_q,
+                                      inv.numpy())
+        err, cos = compare(o.float().numpy().reshape(want.shape), want)
+        print(f"[beam] step {i} B={B} max_abs={err:.3e} cos={cos:.7f}", flush=True)
+        assert err <= 2e-3 and cos >= 0.9999
+
+
 def test_reorder_cache_selects_compressed_rows(cuda):
     from shard_amd import Cache, attention, enable_llama_fused_attention
     model = _llama(cuda)
@@ -202,9 +248,12 @@ def test_reorder_cache_selects_compressed_rows(cuda):
     order = torch.tensor([2, 0, 3, 1])
     layer = beam.layers[1]
     want_keys = base.layers[1].keys.index_select(0, order.to(cuda))
+    want_values = base.layers[1].values.index_select(0, order.to(cuda))
     beam.reorder_cache(order)   # the HF Cache entry point: every layer
-    # the reference's semantics for the dequantized rows
-    assert torch.equal(layer._keys, want_keys)
+    # the reference's semantics for the dequantized rows (rebuilt lazily from
+    # the selected compressed rows: no full rebuild inside the reorder)
+    assert layer._keys is None and layer._needs_decompress
+    assert torch.equal(layer.keys, want_keys) and torch.equal(layer.values, want_values)
     # the next fused step reads the reordered compressed rows: row b of the
     # reordered cache equals row order[b] of the original, bit for bit
     q = torch.randn(B, 32, 1, 128, generator=g).half().to(cuda)
