@@ -391,6 +391,11 @@ class Cache(HFCache):
         sink, win = self._sink_tokens, self._residual_window
         if seq <= sink + win + 4:
             return
+        if k0.dtype != torch.float16:
+            # the compressed format keeps fp16 segments and fp16 operands, as
+            # the reference's does (cache.py:96-113, 430-449; its example and
+            # README load the model in float16)
+            raise TypeError(f"shard_amd.Cache compresses fp16 K/V (a float16 model); got {k0.dtype}")
         if not k0.is_cuda:
             raise ops.ShardHipUnavailable("shard_amd.Cache compresses on the GPU only")
         for li in range(self._num_layers):

@@ -67,6 +67,16 @@ def test_compress_on_cpu_fails_loudly():
         c.update(torch.randn(1, 8, 1, 128).half(), torch.randn(1, 8, 1, 128).half(), 0)
 
 
+def test_compress_refuses_non_fp16_models():
+    """The compressed format is fp16 (the reference's documented model dtype):
+    a bfloat16 prefill raises a clear TypeError at the compressing step."""
+    from shard_amd import Cache
+    c = Cache(num_layers=1)
+    c.update(torch.randn(1, 8, 200, 128).bfloat16(), torch.randn(1, 8, 200, 128).bfloat16(), 0)
+    with pytest.raises(TypeError, match="fp16"):
+        c.update(torch.randn(1, 8, 1, 128).bfloat16(), torch.randn(1, 8, 1, 128).bfloat16(), 0)
+
+
 def test_short_prompt_skips_compression():
     from shard_amd import Cache
     c = Cache(num_layers=1)
