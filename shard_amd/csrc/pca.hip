@@ -266,16 +266,19 @@ void k_pca_project_f32(const float* __restrict__ A, int64_t m, int k, int64_t ld
 // Workgroup shape as k_pca_project (8 waves, 128 rows, two column halves).
 // The k order is permuted so that one lane's 8-element MFMA fragment holds 4
 // dims of the low half of a head and their 4 RoPE partners of the high half:
-// chunk c (64 k) = head c % G, pairs 32 (c / G) .. + 31 (every head's first
-// pair half, then their second), k step s = 2 j + o and lane half hh: element
-// e is dim d0 + 4 o + e (e < 4) or 64 + d0 + 4 o + e - 4 (e >= 4),
-// d0 = 32 (c / G) + 16 j + 8 hh.  Btp holds the basis columns in that order
-// (the host permutes them once).  A lane meets 16 pairs per pair half, the
-// same in every head: their phases sit in registers (reloaded once, halfway).
+// chunk c (64 k) = head c / 2, pairs 32 (c % 2) .. + 31 (a head's first pair
+// half, then its second: the two chunks of a head read the two halves of the
+// same 128-byte lines of each key row, so every line is fetched from HBM
+// once), k step s = 2 j + o and lane half hh: element e is dim d0 + 4 o + e
+// (e < 4) or 64 + d0 + 4 o + e - 4 (e >= 4), d0 = 32 (c % 2) + 16 j + 8 hh.
+// Btp holds the basis columns in that order (the host permutes them once).
+// The phases of the workgroup's 128 rows sit in LDS (the same in every head);
+// a lane reads the 16 of its chunk's pair half before the chunk's undo.
 // C = fp16(undo(k)) . Btp^T - bias (bias: mean . basis, nullable).  Btp is
 // staged in LDS 64 k at a time, double-buffered; the keys and the Btp pieces
 // are loaded R - 1 chunks ahead into an R-slot register ring.
 constexpr int kRopePairs = 64;  // head_dim 128
+constexpr int kPhStride = kRopePairs + 2;  // float2 per staged row: rows 4 banks apart
 #ifndef SHARD_ROPE_RING
 #define SHARD_ROPE_RING 4
 #endif
@@ -292,8 +295,9 @@ void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int s
   constexpr int kPer = (kPieces + kPcaThreads - 1) / kPcaThreads;
   constexpr int R = SHARD_ROPE_RING;
   static_assert(kKc == 64, "a chunk is half a head: 32 RoPE pairs");
-  static_assert(R == 3 || R == 4, "ring of 3 or 4 slots");
+  static_assert(R == 4, "a ring of 4 slots: each step's pair half (c % 2) is static");
   __shared__ __align__(16) uint16_t bs[2][NB32 * 32 * kRowStride];
+  __shared__ __align__(16) float2 phs[kPcaRows * kPhStride];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rw = w & 3, half = w >> 2;
@@ -301,7 +305,8 @@ void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int s
   const int j0 = half * NH;
   const int nj = NB32 - j0 < NH ? NB32 - j0 : NH;
   const int k = n_kv * 128;
-  const int64_t row0 = (int64_t)blockIdx.x * kPcaRows + 32 * rw;
+  const int64_t blk0 = (int64_t)blockIdx.x * kPcaRows;
+  const int64_t row0 = blk0 + 32 * rw;
   // this lane's A row (clamped past m: its loads stay in bounds, never stored)
   const int64_t r = row0 + col < m ? row0 + col : m - 1;
   const int64_t bb = r / n_comp, t = r - bb * n_comp;
@@ -311,20 +316,17 @@ void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int s
       (void*)Btp, (short)0, NB32 * 32 * k * 2, kBufWord3);
   const int nc = k / kKc;
 
-  // the lane's phases of pair half ph: pairs 32 ph + 16 j + 8 hh + 0..7 -> ph_[j][0..7]
-  float2 ph_[2][8];
-  auto load_phases = [&](int ph) {
-    const float2* pt = phases + t * kRopePairs + 32 * ph + 8 * hh;
+  // the phases of the workgroup's rows (rows past m take row m - 1's) into
+  // LDS: 128 rows x 64 pairs, 8 float4 per thread
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float4 v = *(const float4*)(pt + 16 * q + e);
-        ph_[q][e] = make_float2(v.x, v.y);
-        ph_[q][e + 1] = make_float2(v.z, v.w);
-      }
-  };
-  load_phases(0);
+  for (int u = 0; u < kPcaRows * kRopePairs / 2 / kPcaThreads; ++u) {
+    const int pc = tid + kPcaThreads * u;
+    const int lr = pc / (kRopePairs / 2), pq = pc % (kRopePairs / 2);
+    const int64_t gr = blk0 + lr < m ? blk0 + lr : m - 1;
+    const int64_t tt = gr - gr / n_comp * n_comp;
+    *(float4*)&phs[lr * kPhStride + 2 * pq] = *(const float4*)(phases + tt * kRopePairs + 2 * pq);
+  }
+  const float2* myph = phs + (32 * rw + col) * kPhStride + 8 * hh;
 
   auto load_b = [&](int c, uint4 (&pb)[kPer]) {
 #pragma unroll
@@ -346,8 +348,8 @@ void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int s
   // by zero pieces): [2 j] = dims d0 .. d0 + 7, [2 j + 1] = dims 64 + d0 .. + 7
   auto load_a = [&](int c, uint4 (&ka)[4]) {
     const int cc = c < nc ? c : 0;
-    const int ph = cc >= n_kv ? 1 : 0;
-    const uint16_t* kh = krow + (cc - ph * n_kv) * head_stride + 32 * ph;
+    const int ph = cc & 1;
+    const uint16_t* kh = krow + (cc >> 1) * head_stride + 32 * ph;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       ka[2 * j] = *(const uint4*)(kh + 16 * j);
@@ -371,7 +373,16 @@ void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int s
 
   auto step = [&](const int c, const uint4 (&a)[4], uint4 (&an)[4],
                   const uint4 (&b1)[kPer], uint4 (&bn)[kPer]) {
-    if (c == n_kv) load_phases(1);
+    // the lane's 16 phases of this chunk's pair half: pairs 32 (c % 2) + 16 j + 8 hh + e
+    float2 phc[2][8];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float4 v = *(const float4*)(myph + 32 * (c & 1) + 16 * j + e);
+        phc[j][e] = make_float2(v.x, v.y);
+        phc[j][e + 1] = make_float2(v.z, v.w);
+      }
     const uint16_t* b = bs[c & 1];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -380,7 +391,7 @@ void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int s
       half8 f[2];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float2 cs = ph_[j][e];
+        const float2 cs = phc[j][e];
         const float l = h2f(lo[e]), h = h2f(hi[e]);
         // undo_rope: k cos - rotate_half(k) sin, rotate_half = [-hi, lo] (k_k_prepare's arithmetic)
         f[e >> 2][e & 3] = (half_t)__fadd_rn(__fmul_rn(l, cs.x), __fmul_rn(h, cs.y));
@@ -407,16 +418,10 @@ void k_pca_project_rope(const uint16_t* __restrict__ K, int n_kv, int seq, int s
   // Btp pieces (out-of-range reads) and add exact zeros
   const int ncr = (nc + R - 1) / R * R;
   for (int c0 = 0; c0 < ncr; c0 += R) {
-    if constexpr (R == 3) {
-      step(c0, ka[0], ka[2], pb[1], pb[2]);
-      step(c0 + 1, ka[1], ka[0], pb[2], pb[0]);
-      step(c0 + 2, ka[2], ka[1], pb[0], pb[1]);
-    } else {
-      step(c0, ka[0], ka[3], pb[1], pb[3]);
-      step(c0 + 1, ka[1], ka[0], pb[2], pb[0]);
-      step(c0 + 2, ka[2], ka[1], pb[3], pb[1]);
-      step(c0 + 3, ka[3], ka[2], pb[0], pb[2]);
-    }
+    step(c0, ka[0], ka[3], pb[1], pb[3]);
+    step(c0 + 1, ka[1], ka[0], pb[2], pb[0]);
+    step(c0 + 2, ka[2], ka[1], pb[3], pb[1]);
+    step(c0 + 3, ka[3], ka[2], pb[0], pb[2]);
   }
   // C layout of the 32x32 block: lane (col, hh), reg i -> row 8 (i / 4) + 4 hh + i % 4
 #pragma unroll

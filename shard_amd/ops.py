@@ -103,14 +103,14 @@ _ROPE_K_ORDER = {}
 
 def rope_k_order(n_kv: int) -> torch.Tensor:
     """Basis column of each k position of shard_pca_project_rope's permuted k
-    order (head_dim 128): k = 64 c + 16 s + 8 hh + e with chunk c = head c % G,
-    pair half c // G, step s = 2 j + o, element e -> dim d0 + 4 o + e (e < 4)
-    or 64 + d0 + 4 o + e - 4, d0 = 32 (c // G) + 16 j + 8 hh."""
+    order (head_dim 128): k = 64 c + 16 s + 8 hh + e with chunk c = head c // 2,
+    pair half c % 2, step s = 2 j + o, element e -> dim d0 + 4 o + e (e < 4)
+    or 64 + d0 + 4 o + e - 4, d0 = 32 (c % 2) + 16 j + 8 hh."""
     order = _ROPE_K_ORDER.get(n_kv)
     if order is None:
         cols = []
         for c in range(2 * n_kv):
-            ph, g = divmod(c, n_kv)
+            g, ph = divmod(c, 2)
             for s in range(4):
                 j, o = divmod(s, 2)
                 for hh in range(2):
