@@ -23,12 +23,13 @@ def _model(dev):
     return LlamaForCausalLM(cfg).to(dev, torch.float16).eval()
 
 
-def _run(model, ids, steps, streaming, bits=8, qjl=False):
+def _run(model, ids, steps, streaming, bits=8, qjl=False, lazy=True):
     from shard import Cache
     cache = Cache.from_model(model)
     cache._streaming = streaming
     cache._stream_bits = bits
     cache._stream_qjl = qjl
+    cache._lazy_per_layer = lazy
     logits = []
     with torch.no_grad():
         model(ids, past_key_values=cache, use_cache=True)
@@ -109,3 +110,24 @@ def test_multi_token_extend_after_compression(cuda, streaming):
     print(f"[extend streaming={streaming}] max|diff| {err:.3e} (scale {scale:.3f}) cos {cos:.6f}")
     assert err <= 2e-2 * max(scale, 1.0)
     assert cos >= 0.9999
+
+
+def test_lazy_per_layer_off_keeps_every_layers_kv(cuda):
+    """_lazy_per_layer (cache.py:74-85): on the original forward the cache hands
+    back dequantized K/V; with the knob on only the last layer read keeps them,
+    with it off every layer does.  The logits are the same bits either way."""
+    from transformers.models.llama.modeling_llama import LlamaAttention
+    model = _model(cuda)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, VOCAB, (1, 500), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (1, 3), generator=g).to(cuda)
+    fwd = LlamaAttention.forward
+    try:
+        LlamaAttention.forward = getattr(fwd, "__wrapped__", fwd)  # the original forward
+        lazy, c_lazy = _run(model, ids, steps, True, lazy=True)
+        keep, c_keep = _run(model, ids, steps, True, lazy=False)
+    finally:
+        LlamaAttention.forward = fwd
+    assert torch.equal(lazy, keep)
+    assert all(l._keys is not None for l in c_keep.layers)
+    assert [l._keys is not None for l in c_lazy.layers] == [False] * (len(c_lazy.layers) - 1) + [True]
