@@ -314,6 +314,52 @@ def test_other_shapes_decode_fused(cuda, monkeypatch, n_q, n_kv, hd):
         assert err <= 2e-3 and cos >= 0.9999
 
 
+@pytest.mark.parametrize("n_q,n_kv,hd", [(32, 8, 128), (8, 2, 64)], ids=["hd128", "hd64-2kv"])
+def test_shortest_compressible_prompt_decodes_fused(cuda, monkeypatch, n_q, n_kv, hd):
+    """The shortest prompt Cache.compress takes (sink + window + 5 tokens,
+    cache.py:343-344): 5 compressed tokens, so the PCA keeps at most 4
+    components (rank padded to 32) and, at head_dim 64 with 2 kv heads, k-means
+    has 160 subvectors for 256 centroids (cache.py:25 then draws only 160: the
+    codebook has 160 rows, padded for the kernel).  Decode stays fused and
+    matches the fp64 oracle."""
+    from shard_amd import Cache, attention, enable_llama_fused_attention
+    model = _llama(cuda, n_q=n_q, n_kv=n_kv, hd=hd, hidden=n_q * hd)
+    assert enable_llama_fused_attention(model)
+    seen = []
+    inner = attention.fused_attention_compressed
+
+    def record(q, layer, pos_q, inv, mask=None):
+        out = inner(q, layer, pos_q, inv, mask)
+        if layer.layer_idx == 1:
+            p = int(pos_q.reshape(-1)[-1].item()) if torch.is_tensor(pos_q) else int(pos_q)
+            seen.append((q.detach().cpu(), p, out.detach().cpu(),
+                         _oracle_format(layer._gpu_compressed), inv.cpu()))
+        return out
+    monkeypatch.setattr(attention, "fused_attention_compressed", record)
+    g = torch.Generator().manual_seed(8)
+    T = 4 + 64 + 5
+    ids = torch.randint(0, VOCAB, (1, T), generator=g).to(cuda)
+    steps = torch.randint(0, VOCAB, (1, 3), generator=g).to(cuda)
+    cache = Cache.from_model(model)
+    cache._streaming = True
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        for s in range(steps.shape[1]):
+            model(steps[:, s:s + 1], past_key_values=cache, use_cache=True)
+    gc = cache.layers[1]._gpu_compressed
+    assert gc is not None and gc["n_compress"] == 5 and gc["k_coeffs_shape"][1] <= 4
+    n_sub = 5 * n_kv * hd // 4
+    assert gc["v_centroids_f16"].shape[0] == min(256, n_sub)
+    assert getattr(cache, "_fused_fallbacks", 0) == 0 and len(seen) == 3
+    for i, (q, pos_q, out, ogc, inv) in enumerate(seen):
+        want = exact.decode_attention(q.float().numpy().reshape(1, n_q, 1, hd), ogc, n_kv, pos_q,
+                                      inv.numpy())
+        err, cos = compare(out.float().numpy().reshape(want.shape), want)
+        print(f"[shortest prompt {n_q}q/{n_kv}kv hd{hd}] step {i} max_abs={err:.3e} cos={cos:.7f}",
+              flush=True)
+        assert err <= 2e-3 and cos >= 0.9999
+
+
 @pytest.mark.parametrize("opts", [{"v_vq_codebook_size": 64},
                                   {"sink_tokens": 0, "residual_window": 16},
                                   {"sink_tokens": 8, "residual_window": 128}],
