@@ -507,6 +507,24 @@ def test_fused_attention_grows_a_small_workspace(cuda):
             attention._workspaces[key] = saved
 
 
+def test_decode_one_split_past_the_phase_tables(cuda):
+    """n_splits = 1 over 40,000 compressed tokens (1,250 tiles): the token-tiled
+    kernel's phase tables cover 1,024 tiles per split, so its plan splits the
+    range in two; the row-split kernel advances its phases per tile and takes
+    the whole range in one split."""
+    n_comp = 40000
+    gc, inv = random_layer(B=1, n_comp=n_comp, n_stream=3, seed=41)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(14)).half()
+    pos_q = 4 + n_comp + 64 + 3 - 1
+    want = exact.decode_attention(q.numpy(), gc, 8, pos_q, inv.numpy())
+    for kernel in KERNELS:
+        got = _run(cuda, gc, inv, q, pos_q, n_splits=1, kernel=kernel)
+        err, cos = compare(got, want)
+        print(f"one split over {n_comp} tokens, kernel={kernel}: max_abs={err:.3e} cos={cos:.7f}",
+              flush=True)
+        assert err <= TOL_ABS and cos >= TOL_COS, (kernel, err, cos)
+
+
 @pytest.mark.parametrize("case", [(1, 8, 1, 192, 2500), (1, 4, 8, 128, 2300), (2, 2, 2, 192, 2200)],
                          ids=["gqa1", "gqa8", "gqa2_b2"])
 def test_decode_long_split_other_groups(cuda, case):
