@@ -65,6 +65,14 @@ constexpr int kTokMaxRank = 256;            // the token-tiled kernel (the row-s
 #define SHARD_SPLIT_PER_XCD 1
 #endif
 constexpr bool kSplitPerXcd = SHARD_SPLIT_PER_XCD;
+// Row-split launches in two classes whose (batch row, kv head) groups fill
+// the 8 XCDs evenly put every split of a group on one XCD and run the group's
+// merge workgroups there too, so the merge reads the partial rows that XCD's
+// L2 wrote (8K, batch 1: 13.86 -> 13.51 us).  SHARD_KV_XCD=0 keeps the split
+// order of the other launches.
+#ifndef SHARD_KV_XCD
+#define SHARD_KV_XCD 1
+#endif
 
 // The fp16 segments around the compressed span, in attention-mask order:
 // sink [0, n_sink), window, decode tokens, then the 8-bit stream (dequantized
@@ -109,6 +117,9 @@ struct SplitParams {
   float* ws_m;
   float* ws_l;
   float* ws_acc;
+  // kv_xcd (two_class launches whose (batch row, kv head) groups fill the 8
+  // XCDs evenly): every split of a group on one XCD
+  int32_t kv_xcd;
 };
 
 // 2^x for the online softmax, where x <= 0 (a difference from the running
@@ -527,7 +538,17 @@ void k_decode_split(const SplitParams p) {
   const int HG = p.G;
   const int bid = blockIdx.x;
   int hg, split, b;
-  if (p.two_class) {
+  if (p.kv_xcd) {
+    // every workgroup of a (batch row, kv head) group on one XCD (block id
+    // mod 8): group x + 8 gi on XCD x, its splits of each class in one run
+    const int L = blockIdx.y * gridDim.x + bid;  // dispatch order
+    const int c = L >> 8, j = L & 255;
+    const int r = j >> 3;
+    const int grp_i = (j & 7) + 8 * (r / p.n_first);
+    split = c * p.n_first + r % p.n_first;
+    b = grp_i / HG;
+    hg = grp_i % HG;
+  } else if (p.two_class) {
     const int L = blockIdx.y * gridDim.x + bid;  // dispatch order
     const int c = L >> 8, j = L & 255;
     const int slot = j >> 3;
@@ -1646,10 +1667,12 @@ void launch_tok(const TokParams& tp, int nq, bool hp, dim3 grid, hipStream_t s) 
   }
 }
 
-int launch_merge(const shard_decode_args* a, const float* ws, int nsp, hipStream_t s) {
+int launch_merge(const shard_decode_args* a, const float* ws, int nsp, hipStream_t s,
+                 int kv_nq = 0) {
   const int64_t nm = (int64_t)a->batch * a->n_q_heads * nsp;
   MergeParams mp;
   mp.H = a->n_q_heads; mp.nsp = nsp; mp.hd = a->head_dim;
+  mp.kv_nq = kv_nq;
   mp.ws_m = ws; mp.ws_l = ws + nm; mp.ws_acc = ws + 2 * nm; mp.out = a->out;
   launch_partial_merge(mp, a->batch, s);
   SHARD_LAUNCH_CHECK("shard_decode_attn merge");
@@ -1796,7 +1819,8 @@ static int decode_attn_run(const shard_decode_args* a, void* workspace, hipStrea
   sp.n_first = ns;
   sp.two_class = 0;
   const int half = ns / 2;
-  if (kTG == 1 && kSplitBias && (int64_t)ns * a->n_kv_heads * a->batch == 2 * device_cus() &&
+  // the class split and both block orders assume 256 CUs (two classes of 256 workgroups)
+  if (kTG == 1 && kSplitBias && device_cus() == 256 && (int64_t)ns * a->n_kv_heads * a->batch == 512 &&
       ns % 2 == 0 && 32 % a->n_kv_heads == 0 && n_tiles >= 2 * ns) {
     // first class: ta tiles per split, second class: tb (the last split also
     // runs the extra tokens, counted as x_cost tiles)
@@ -1823,6 +1847,7 @@ static int decode_attn_run(const shard_decode_args* a, void* workspace, hipStrea
   sp.vidx = a->v_idx; sp.vcb = a->v_codebook; sp.vch = a->v_ch;
   sp.mask = a->mask; sp.mask_stride = a->mask_stride; sp.n_sink = a->n_sink;
   sp.ws_m = ws; sp.ws_l = ws + nm; sp.ws_acc = ws + 2 * nm;
+  sp.kv_xcd = SHARD_KV_XCD && sp.two_class && (a->batch * a->n_kv_heads) % 8 == 0;
 
   dim3 grid((unsigned)(ns * a->n_kv_heads), (unsigned)a->batch);
   switch (a->rank / 16) {
@@ -1835,7 +1860,7 @@ static int decode_attn_run(const shard_decode_args* a, void* workspace, hipStrea
     default: return SHARD_ERR_SHAPE;
   }
   SHARD_LAUNCH_CHECK("shard_decode_attn row-split kernel");
-  return launch_merge(a, ws, nsp, s);
+  return launch_merge(a, ws, nsp, s, sp.kv_xcd ? kGQA : 0);
 }
 
 // ---- scratch of shard_decode_attn_noalloc: the partial rows (m, l, acc) of

@@ -230,7 +230,7 @@ int shard_bench_fp16_decode_ld(const uint16_t* q, const uint16_t* k, const uint1
                      dim3(64 * kFdWaves), 0, s, p);
   SHARD_LAUNCH_CHECK("shard_bench_fp16_decode split");
   MergeParams mp;
-  mp.H = n_kv_heads * kFdGQA; mp.nsp = n_splits; mp.hd = kMergeHD;
+  mp.H = n_kv_heads * kFdGQA; mp.nsp = n_splits; mp.hd = kMergeHD; mp.kv_nq = 0;
   mp.ws_m = p.ws_m; mp.ws_l = p.ws_l; mp.ws_acc = p.ws_acc; mp.out = out;
   launch_partial_merge(mp, batch, s);
   SHARD_LAUNCH_CHECK("shard_bench_fp16_decode merge");

@@ -27,6 +27,9 @@ constexpr int kMergeHD = 128;
 struct MergeParams {
   int32_t H, nsp;   // query heads per batch row, partial rows per query head
   int32_t hd;       // output dims per query head: 128, or 64 (the first 64 of each row)
+  // kv_nq > 0: the partial rows of (batch row, kv head) group i were written
+  // on XCD i mod 8 (kv_nq query heads per kv head); the group's slices run there
+  int32_t kv_nq;
   const float* ws_m;
   const float* ws_l;
   const float* ws_acc;
@@ -47,10 +50,22 @@ void k_decode_merge(const MergeParams p) {
   const int dp = tid % DP, g = tid / DP;
   // the MS slices of a head share one XCD (workgroups go to XCD id mod 8), so
   // one L2 fetches each 128-byte line of the partial rows once
-  const int bx = blockIdx.x, slice = (bx >> 3) % MS;
+  const int bx = blockIdx.x;
+  int slice, head, brow;
+  if (p.kv_nq) {
+    const int L = blockIdx.y * gridDim.x + bx, r = L >> 3;
+    slice = r % MS;
+    const int grp_i = (L & 7) + 8 * (r / (MS * p.kv_nq));
+    const int G = p.H / p.kv_nq;
+    brow = grp_i / G;
+    head = (grp_i % G) * p.kv_nq + (r / MS) % p.kv_nq;
+  } else {
+    slice = (bx >> 3) % MS;
+    head = (bx & 7) + 8 * (bx / (8 * MS));
+    brow = blockIdx.y;
+  }
   if (slice * 2 * DP >= p.hd) return;  // a slice past the output's dims (whole workgroup)
-  const int head = (bx & 7) + 8 * (bx / (8 * MS));
-  const int64_t hrow = (int64_t)blockIdx.y * p.H + head;
+  const int64_t hrow = (int64_t)brow * p.H + head;
   const int nsp = p.nsp;
   const float* mrow = p.ws_m + hrow * nsp;
   const float* lrow = p.ws_l + hrow * nsp;

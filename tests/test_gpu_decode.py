@@ -47,6 +47,11 @@ CASES = [
     (1, 8, 192, 700, 4, 64, 3000, 0),    # 3,068 extra tokens: spread over many splits
     (2, 4, 160, 900, 4, 64, 700, 9),     # long stream and decode tokens together
     (1, 8, 192, 600, 0, 0, 0, 0),        # no sink, window or stream: compressed tokens alone
+    # row-split launches of 512 workgroups in two classes with every split of a
+    # (batch row, kv head) group on one XCD and its merge there too
+    (2, 4, 192, 4200, 4, 64, 0, 0),      # 8 groups, 64 splits each
+    (2, 8, 192, 2100, 4, 64, 2, 0),      # 16 groups, 32 splits each
+    (1, 16, 128, 2100, 4, 64, 0, 0),     # 16 kv heads, 32 splits each
 ]
 
 # split kernels: 0 = automatic, 1 = row-split, 2 = token-tiled
