@@ -561,7 +561,10 @@ def test_k_prepare_f32(cuda):
 
 
 @pytest.mark.parametrize("B,G,T,start,n_comp,n", [(2, 8, 300, 4, 232, 192), (1, 8, 700, 4, 632, 64),
-                                                    (3, 4, 200, 0, 200, 256)])
+                                                    (3, 4, 200, 0, 200, 256),
+                                                    # k chunk counts (2 per kv head) that are not
+                                                    # a multiple of the key ring
+                                                    (1, 2, 150, 4, 100, 96), (2, 6, 130, 0, 130, 128)])
 def test_pca_project_rope_equals_prepare_then_project(cuda, B, G, T, start, n_comp, n):
     """The fused front end (undo RoPE in the A loads, permuted k order) computes
     the same fp16 operand as shard_k_prepare with a zero mean, so it matches
